@@ -1,0 +1,219 @@
+"""Benchmark: YOLOv3-416 fp32 inference on one MI355X through libtensorium_hip.
+
+A step is one forward pass of YOLOv3-416 (75 convolutions, shortcuts,
+routes, upsamples, yolo heads) over a batch of synthetic images already
+resident in HBM.  Prints ONE JSON line (rank 0):
+
+  value          images/s at the configured batch (default 16)
+  roofline       the dominant kernel (most GPU time) from a separate pass that
+                 brackets every launch with HIP events on the library stream:
+                 achieved = its algorithmic conv FLOP (2*M*N*K) / its time,
+                 against the 157.3 TFLOP/s fp32 MFMA peak
+  cpu_baseline   the CPU oracle (C restatement of the reference's AVX2 path)
+                 on the host, a bounded sample of batch-1 images
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 16]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "conv im2col+SGEMM GFLOP/s (% fp32 MFMA peak); YOLOv3-416 img/s at batch 1/16"
+PEAK_FP32_MFMA = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_kind(L, batch):
+    """Name of the kernel family a conv layer launches (see conv.hip)."""
+    is1x1 = L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0
+    return "conv1x1_kernel" if is1x1 else f"conv_gather_kernel<{L['size']}x{L['size']}>"
+
+
+def time_forward(hip, net, x, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        net.forward(x)
+    torch.cuda.synchronize()
+    hip.finish()
+    e0, e1 = hip.eventCreate(), hip.eventCreate()
+    t0 = time.perf_counter()
+    hip.eventRecord(e0)
+    for _ in range(steps):
+        net.forward(x)
+    hip.eventRecord(e1)
+    hip.finish()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = hip.eventElapsed(e0, e1)
+    hip.eventDestroy(e0)
+    hip.eventDestroy(e1)
+    return ms, wall
+
+
+def profile_kernels(hip, net, layers, x, reps=3):
+    """Per-layer GPU durations from HIP events recorded on the library stream
+    around each layer's launches; conv layers are grouped by kernel family."""
+    evs = {L["index"]: (hip.eventCreate(), hip.eventCreate()) for L in layers}
+
+    def hook(i, begin):
+        hip.eventRecord(evs[i][0 if begin else 1])
+
+    stats = {}
+    try:
+        for _ in range(reps):
+            net.forward(x, on_layer=hook)
+            hip.finish()
+            for L in layers:
+                i = L["index"]
+                ms = hip.eventElapsed(*evs[i])
+                if L["type"] == "convolutional":
+                    kind = kernel_kind(L, net.batch)
+                    F, oh, ow = L["out"]
+                    flop = 2 * F * L["in"][0] * L["size"] ** 2 * oh * ow * net.batch
+                else:
+                    kind, flop = L["type"], 0
+                s = stats.setdefault(kind, {"ms": 0.0, "flop": 0.0, "launches": 0.0})
+                s["ms"] += ms / reps
+                s["flop"] += flop / reps
+                s["launches"] += 1.0 / reps
+    finally:
+        for a, b in evs.values():
+            hip.eventDestroy(a)
+            hip.eventDestroy(b)
+    return stats
+
+
+def cpu_baseline(layers, weights, budget_s=12.0):
+    """Oracle YOLOv3-416 forward at batch 1 on the host cores, repeated until
+    ~budget_s of work; returns (img/s, threads, images)."""
+    import numpy as np
+
+    from oracle import netref
+    from oracle import refcpu as R
+    from tensorium_amd import synth
+
+    threads = min(16, os.cpu_count() or 4)
+    R.set_threads(threads)
+    x = synth.uniform(7, (1, 3, 416, 416))
+    netref.forward(layers, weights, x)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        netref.forward(layers, weights, x)
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    del np
+    return n / dt, threads, n
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--size", type=int, default=416)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batch1", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the YOLOv3 inference path shards by image "
+              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from tensorium_amd import darknet, synth
+    from tensorium_amd.nnhip import TNNHip
+
+    hip = TNNHip(0)
+    hip.useTorchStream()  # one ordered stream for torch's buffers and the kernels
+    _, layers = darknet.load_cfg("yolov3.cfg", args.size, args.size)
+    weights = darknet.synthetic_weights(layers)
+    flop_img = darknet.conv_flops(layers)
+
+    def run(batch, steps, warmup):
+        net = darknet.Network(hip, layers, batch, weights)
+        x = torch.from_numpy(synth.uniform(7, (batch, 3, args.size, args.size))).cuda()
+        torch.cuda.synchronize()
+        ms, wall = time_forward(hip, net, x, steps, warmup)
+        return net, x, ms, wall
+
+    net, x, ms, wall = run(args.batch, args.steps, args.warmup)
+    ms_step = ms / args.steps
+    img_s = args.batch * args.steps / (ms / 1e3)
+    gflops = flop_img * args.batch / (ms_step / 1e3) / 1e9
+    log(f"batch {args.batch}: {ms_step:.3f} ms/step (event), wall {wall / args.steps * 1e3:.3f} ms/step, "
+        f"{img_s:.1f} img/s, {gflops:.0f} GFLOP/s")
+
+    stats = profile_kernels(hip, net, layers, x)
+    conv_kinds = [k for k in stats if k.startswith("conv")]
+    dom = max(conv_kinds, key=lambda k: stats[k]["ms"])
+    d = stats[dom]
+    achieved = d["flop"] / (d["ms"] / 1e3)
+    for k, s in sorted(stats.items(), key=lambda kv: -kv[1]["ms"]):
+        log(f"  {k}: {s['ms']:.3f} ms over {s['launches']:.0f} launches, "
+            f"{s['flop'] / (s['ms'] / 1e3) / 1e12:.1f} TFLOP/s")
+    conv_ms = sum(stats[k]["ms"] for k in conv_kinds)
+    del net, x
+    torch.cuda.empty_cache()
+
+    b1 = None
+    if not args.no_batch1 and args.batch != 1:
+        _, _, ms1, _ = run(1, max(args.steps, 20), args.warmup)
+        b1 = 1 * max(args.steps, 20) / (ms1 / 1e3)
+        log(f"batch 1: {ms1 / max(args.steps, 20):.3f} ms/img, {b1:.1f} img/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        v, threads, n = cpu_baseline(layers, weights, args.cpu_budget)
+        cpu = {"value": round(v, 4), "unit": "img/s", "cores": threads, "kind": "port",
+               "sample": f"YOLOv3-416 batch-1 forward x{n} on the CPU oracle (C AVX2+FMA restatement of the "
+                         f"reference path, {threads} threads, BN folded)"}
+        log(f"cpu baseline: {v:.3f} img/s on {threads} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(img_s, 2),
+        "unit": "img/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64 U[0,1) images, He-normal random weights, BN folded)",
+        "config": {"workload": f"YOLOv3-{args.size} fp32 inference, batch {args.batch}, 1 GPU",
+                   "global_batch": args.batch, "image": [3, args.size, args.size]},
+        "conv_gflops": round(gflops, 1),
+        "conv_frac_fp32_mfma_peak": round(gflops * 1e9 / PEAK_FP32_MFMA, 4),
+        "conv_kernel_ms_per_step": round(conv_ms, 4),
+        "img_s_batch1": None if b1 is None else round(b1, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
+                     "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "launches_per_step": round(d["launches"]),
+                     "flop_per_launch": round(d["flop"] / max(d["launches"], 1))},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    del np
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,244 @@
+/*
+ * tensorium_hip.h -- C ABI of libtensorium_hip.so, the MI355X (gfx950)
+ * backend for Tensorium's fp32 convolution hot path.
+ *
+ * Drop-in boundary: the GPU backend object TNNCuda<T> (source/nncuda.pas:
+ * 35-200, global singleton `cuda`, ntensors.pas:1055).  Every entry point
+ * below names the TNNCuda method (or CPU op-table pointer) it replaces.
+ *
+ * Conventions (mirroring TNNCuda):
+ *  - cdecl, plain C types only: int64_t for SizeInt, int32_t for longint /
+ *    boolean / enum ordinals, float for T = single, raw pointers.
+ *  - device buffers are (pointer, element offset) pairs; the library never
+ *    frees or retains caller buffers.
+ *  - all compute is enqueued in order on the context's single stream and is
+ *    asynchronous; tnh_h2d / tnh_d2h are blocking, tnh_synchronize waits
+ *    (TNNCuda.readBuffer/writeBuffer/finish, nncuda.pas:499-522, 1575).
+ *  - every call returns a status (TNH_OK = 0); on failure
+ *    tnh_last_error() returns a thread-local message.  This replaces the
+ *    reference's SAFE_CALL -> assert (nncuda.pas:237-275).
+ *  - matrices are row-major, as in cblas_sgemm with Order ignored
+ *    (ntensors.pas:2231).  Tensors are NCHW fp32.
+ */
+#ifndef TENSORIUM_HIP_H
+#define TENSORIUM_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  TNH_OK = 0,
+  TNH_ERR_NOT_INITIALIZED = 1,
+  TNH_ERR_INVALID_ARG = 2,
+  TNH_ERR_HIP = 3,
+  TNH_ERR_UNSUPPORTED = 4,
+  TNH_ERR_OUT_OF_MEMORY = 5
+};
+
+/* TActivationType ordinals (ntypes.pas:66) accepted by the kernels. */
+enum { TNH_AC_LOGISTIC = 0, TNH_AC_LINEAR = 4, TNH_AC_LEAKY = 9 };
+
+/* ---- context ---------------------------------------------------------- */
+/* TNNCuda.Create(deviceIndex) (nncuda.pas:448): selects the device, creates
+ * the context's stream. Calling it again re-targets the context. */
+int32_t tnh_init(int32_t device);
+/* TNNCuda.Destroy (nncuda.pas:469) */
+int32_t tnh_finalize(void);
+/* TNNCuda.deviceCount (nncuda.pas:443) */
+int32_t tnh_device_count(int32_t *count);
+/* TNNCuda.finish (nncuda.pas:1575): waits for the context stream */
+int32_t tnh_synchronize(void);
+/* message of the last failing call on this thread ("" if none) */
+const char *tnh_last_error(void);
+/* the hipStream_t kernels are enqueued on */
+int32_t tnh_get_stream(void **stream);
+/* enqueue on a caller-owned stream instead; NULL selects the HIP null
+ * (legacy default) stream, which orders with other blocking streams */
+int32_t tnh_set_stream(void *stream);
+/* go back to the context's own stream */
+int32_t tnh_reset_stream(void);
+/* number of compute units of the context device */
+int32_t tnh_cu_count(int32_t *count);
+
+/* ---- memory (TNNCuda.createDeviceBuffer/freeDeviceBuffer/writeBuffer/
+ *      readBuffer, nncuda.pas:488, 493, 512, 499) ----------------------- */
+int32_t tnh_malloc(int64_t bytes, void **ptr);
+int32_t tnh_free(void *ptr);
+int32_t tnh_h2d(void *dst, const void *src, int64_t bytes);
+int32_t tnh_d2h(void *dst, const void *src, int64_t bytes);
+
+/* ---- timing on the context stream (replaces the telemetry clock,
+ *      nopmetrics.pas:56-70, which had to synchronize the stream) ------- */
+int32_t tnh_event_create(void **ev);
+int32_t tnh_event_destroy(void *ev);
+int32_t tnh_event_record(void *ev);
+int32_t tnh_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* ---- GEMM ------------------------------------------------------------- */
+/* TNNCuda.gemm (nncuda.pas:624) / cblas_sgemm (ntensors.pas:2231):
+ * C = alpha*op(A)*op(B) + beta*C, all four NN/NT/TN/TT variants.
+ * beta = 0 overwrites C without reading it (BLAS semantics). */
+int32_t tnh_sgemm(int32_t transA, int32_t transB, int64_t M, int64_t N,
+                  int64_t K, float alpha, const float *A, int64_t aOff,
+                  int64_t lda, const float *B, int64_t bOff, int64_t ldb,
+                  float beta, float *C, int64_t cOff, int64_t ldc);
+/* TNNCuda.gemmStridedBatched (nncuda.pas:809) /
+ * cblas_sgemm_batch_strided (ntensors.pas:2288); strideA = 0 is legal. */
+int32_t tnh_sgemm_strided_batched(int32_t transA, int32_t transB, int64_t M,
+                                  int64_t N, int64_t K, float alpha,
+                                  const float *A, int64_t aOff, int64_t lda,
+                                  int64_t strideA, const float *B,
+                                  int64_t bOff, int64_t ldb, int64_t strideB,
+                                  float beta, float *C, int64_t cOff,
+                                  int64_t ldc, int64_t strideC,
+                                  int64_t batch);
+
+/* ---- im2col / col2im ---------------------------------------------------- */
+/* TNNCuda.im2col (nncuda.pas:1144) / sim2Col (ntensors.pas:11415):
+ * col[(c*kh+ky)*kw+kx][oy*OW+ox] = im[c][oy*sY-pH+ky*dY][ox*sX-pW+kx*dX] or 0 */
+int32_t tnh_im2col(int64_t C, int64_t H, int64_t W, int64_t kh, int64_t kw,
+                   int64_t pH, int64_t pW, int64_t sY, int64_t sX, int64_t dY,
+                   int64_t dX, const float *im, int64_t imOff, float *col,
+                   int64_t colOff);
+/* sim2colStridedBatched (ntensors.pas:11493) */
+int32_t tnh_im2col_batched(int64_t C, int64_t H, int64_t W, int64_t kh,
+                           int64_t kw, int64_t pH, int64_t pW, int64_t sY,
+                           int64_t sX, int64_t dY, int64_t dX, const float *im,
+                           int64_t imOff, int64_t imStride, float *col,
+                           int64_t colOff, int64_t colStride, int64_t batch);
+/* TNNCuda.col2im (nncuda.pas:1212) / scol2im (ntensors.pas:11717):
+ * ACCUMULATES into im, adding contributions per pixel in the reference CPU
+ * order (existing value first, then ky, kx ascending): bit-exact. */
+int32_t tnh_col2im(int64_t C, int64_t H, int64_t W, int64_t kh, int64_t kw,
+                   int64_t pH, int64_t pW, int64_t sY, int64_t sX, int64_t dY,
+                   int64_t dX, const float *col, int64_t colOff, float *im,
+                   int64_t imOff);
+/* scol2imStridedBatched (ntensors.pas:11833) */
+int32_t tnh_col2im_batched(int64_t C, int64_t H, int64_t W, int64_t kh,
+                           int64_t kw, int64_t pH, int64_t pW, int64_t sY,
+                           int64_t sX, int64_t dY, int64_t dX,
+                           const float *col, int64_t colOff, int64_t colStride,
+                           float *im, int64_t imOff, int64_t imStride,
+                           int64_t batch);
+
+/* ---- fused convolution ------------------------------------------------- */
+/* Replaces the sequence im2col -> gemmStridedBatched -> forwardBias ->
+ * ActivateArray of TConvolutionalLayer.forwardGPU
+ * (nConvolutionLayer.pas:1051-1118) and the CPU forward
+ * (nConvolutionLayer.pas:457-566, Conv2D ntensors.pas:8252) with one
+ * implicit-GEMM kernel (BN folded, dilation 1, groups 1):
+ *   out[b][f][p] = act(sum_k W[f][k]*col_b[k][p] + bias[f]) (+ residual[b][f][p])
+ * x image b starts at x + xOff + b*xBatchStride; out/residual likewise, so a
+ * route (concat) destination can be written in place.  bias and residual may
+ * be NULL.  The residual add (a following shortcut layer, naddlayer.pas:698)
+ * is applied after the activation, exactly as the separate layer would.
+ * workspace/workspaceBytes: scratch for split-K partial sums (may be NULL/0,
+ * then split-K is not used). */
+int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W,
+                       int64_t F, int64_t kh, int64_t kw, int64_t pH,
+                       int64_t pW, int64_t sY, int64_t sX, const float *x,
+                       int64_t xOff, int64_t xBatchStride,
+                       const float *weights, int64_t wOff, const float *bias,
+                       int64_t biasOff, int32_t act, const float *residual,
+                       int64_t rOff, int64_t rBatchStride, float *out,
+                       int64_t outOff, int64_t outBatchStride,
+                       float *workspace, int64_t workspaceBytes);
+/* output size of tnh_conv2d_fwd: (H + 2p - k)/s + 1 (standard formula) */
+int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw,
+                            int64_t pH, int64_t pW, int64_t sY, int64_t sX,
+                            int64_t *OH, int64_t *OW);
+
+/* ---- epilogue and element-wise ops ------------------------------------- */
+/* TNNCuda.forwardBias (nncuda.pas:582): blockSize = dstSize/(srcSize*batch);
+ * dst[offset+i] += src[((i/blockSize) % srcSize)*incb] */
+int32_t tnh_forward_bias(int64_t dstSize, float *dst, int64_t offset,
+                         int64_t srcSize, const float *src, int64_t incb,
+                         int64_t batch);
+/* TNNCuda.forwardScale (nncuda.pas:1468): dst *= scale[...] likewise */
+int32_t tnh_forward_scale(int64_t dstSize, float *dst, int64_t offset,
+                          int64_t scaleSize, const float *scale, int64_t incb,
+                          int64_t batch);
+/* TNNCuda.backwardBias (nncuda.pas:602): dst[f] += sum over batch and the
+ * blockSize = srcSize/(dstSize*batch) elements of channel f of src. */
+int32_t tnh_backward_bias(int64_t dstSize, float *dst, int64_t srcSize,
+                          const float *src, int64_t srcOffset, int64_t incb,
+                          int64_t batch);
+/* TNNCuda.ActivateArray (nncuda.pas:524): act = ord(TActivationType);
+ * acLINEAR launches nothing. Logistic is the IEEE 1/(1+exp(-x)) form. */
+int32_t tnh_activate(int64_t N, float *x, int64_t offset, int32_t act);
+/* TNNCuda.DeriveArray (nncuda.pas:562): delta[i] *= act'(x[offset+i]) */
+int32_t tnh_derive(int64_t N, const float *x, int64_t offset, int32_t act,
+                   float *delta);
+/* TNNCuda.addvv (nncuda.pas:897): dst[i*incc] = src1[i*inca] + src2[i*incb] */
+int32_t tnh_addvv(int64_t N, const float *src1, int64_t src1Offset,
+                  int64_t inca, const float *src2, int64_t src2Offset,
+                  int64_t incb, float *dst, int64_t dstOffset, int64_t incc);
+/* TNNCuda.axpy (nncuda.pas:945): y[i*incy] += a*x[i*incx] */
+int32_t tnh_axpy(int64_t N, float a, const float *x, int64_t xOffset,
+                 int64_t incx, float *y, int64_t yOffset, int64_t incy);
+/* TNNCuda.scale (nncuda.pas:986): x[i*stride] *= a */
+int32_t tnh_scale(int64_t N, float a, float *x, int64_t stride);
+/* TNNCuda.fill (nncuda.pas:1017): x[offset + i*stride] = val */
+int32_t tnh_fill(int64_t N, float *x, int64_t offset, float val,
+                 int64_t stride);
+/* TNNCuda.copy (nncuda.pas:1037): dst[i*incb] = src[i*inca] */
+int32_t tnh_copy(int64_t N, const float *src, int64_t srcOffset, int64_t inca,
+                 float *dst, int64_t dstOffset, int64_t incb);
+/* TTensor.concat of batched tensors (ntensors.pas:12045, used by
+ * TConcatLayer.forward nconcatlayer.pas:115) in per-image (darknet) order:
+ * dst[b] = [src0[b] | src1[b] | ...], each src_i holding sizes[i] floats per
+ * image.  n <= 8. */
+int32_t tnh_route(int64_t batch, int32_t n, const float *const *srcs,
+                  const int64_t *sizes, float *dst);
+
+/* ---- pooling / resampling --------------------------------------------- */
+/* TNNCuda.forwardMaxPool (nncuda.pas:1088) with the CPU semantics of
+ * TMaxPoolLayer.forwardMaxPool (nMaxPoolLayer.pas:363-455): window offset
+ * -pad div 2, strict '>', -MaxSingle init, global int64 indices.
+ * indexes may be NULL (inference). */
+int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH,
+                        int64_t outW, const float *input, int64_t c,
+                        int64_t h, int64_t w, int64_t strideX, int64_t strideY,
+                        int64_t padding, int64_t kernelSize, int64_t *indexes,
+                        float *output);
+/* TNNCuda.backwardMaxPool (nncuda.pas:1121) with the CPU order of
+ * backwardMaxPool (nMaxPoolLayer.pas:501-512): delta_in[idx[i]] += delta[i]
+ * summed per input element in ascending i (gather, no atomics).  Needs the
+ * forward geometry to enumerate each input's candidate windows. */
+int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH,
+                        int64_t outW, int64_t h, int64_t w, int64_t strideX,
+                        int64_t strideY, int64_t padding, int64_t kernelSize,
+                        const int64_t *indexes, const float *delta,
+                        float *deltaIn);
+/* TNNCuda.upSample (nncuda.pas:1267) / upsample (nupsamplelayer.pas:83):
+ * h,w are the small-side dims.  isForward=1: out = scale*in (nearest);
+ * isForward=0: in += scale*out summed per input pixel in raster order
+ * (gather, bit-exact); zeroIn=1 clears `in` first. */
+int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w,
+                     float *in, int64_t stride, int32_t isForward, float scale,
+                     float *out, int32_t zeroIn);
+
+/* ---- YOLO head ------------------------------------------------------- */
+/* TYoloLayer.forward inference part (nyololayer.pas:786-830): out = in, then
+ * the logistic on entries x, y (0, 1) and obj + classes (4 .. 4+classes) of
+ * each of the n anchors; w, h (2, 3) pass through.  The logistic restates
+ * logistic_array (nactivation.pas:36-127): exp(-x) = 2^floor(t) * p(frac(t))
+ * with t = -x*log2(e) clamped, p the reference's degree-2 polynomial, then
+ * 1/(1+e) by IEEE division (the reference's vrcpps is CPU-specific). */
+int32_t tnh_yolo_fwd(int64_t batch, int64_t n, int64_t classes, int64_t h,
+                     int64_t w, const float *in, float *out);
+
+/* ---- batch norm (inference, unfused) ----------------------------------- */
+/* TNNCuda.normalize (nncuda.pas:1371) with the CPU clamp of _snormblkvv
+ * (ntensors.pas:4357): x = (x - mean[f]) / max(sqrt(var[f]), 1e-6), IEEE
+ * division; blockSize = dstSize/(N*batch). */
+int32_t tnh_bn_normalize(int64_t dstSize, float *x, int64_t offset, int64_t N,
+                         const float *mean, const float *variance,
+                         int64_t batch);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,42 @@
+// Shared host-side plumbing of libtensorium_hip: status codes, the
+// thread-local last-error string, the per-process device context (one HIP
+// stream, like TNNCuda's single stream, nncuda.pas:455) and argument checks.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+
+#include "../../include/tensorium_hip.h"
+
+namespace tnh {
+
+// Records a formatted message for tnh_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+struct Context {
+  int device = -1;
+  hipStream_t own_stream = nullptr;  // created by tnh_init
+  hipStream_t stream = nullptr;      // stream kernels are launched on
+  int cu_count = 0;
+  int xcd_count = 8;
+};
+
+// Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).
+Context* ctx();
+
+// Checks a launch or runtime call; returns TNH_OK or TNH_ERR_HIP with text.
+int hip_status(hipError_t e, const char* what);
+
+inline int launch_status(const char* what) { return hip_status(hipGetLastError(), what); }
+
+}  // namespace tnh
+
+#define TNH_REQUIRE_CTX(c)                 \
+  tnh::Context* c = tnh::ctx();            \
+  if (!c) return TNH_ERR_NOT_INITIALIZED;
+
+#define TNH_ARG(cond, ...)                                   \
+  do {                                                       \
+    if (!(cond)) return tnh::fail(TNH_ERR_INVALID_ARG, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,188 @@
+// Context, memory, error and event entry points of libtensorium_hip.
+// Mirrors TNNCuda's lifecycle (Create/Destroy/finish, nncuda.pas:448-469,
+// 1575) with a status-code + last-error channel in place of SAFE_CALL's
+// assert (nncuda.pas:237-275).
+#include <cstdio>
+#include <mutex>
+
+#include "common.hpp"
+
+namespace tnh {
+
+namespace {
+thread_local char g_err[512] = "";
+Context g_ctx;
+bool g_live = false;
+std::mutex g_mu;
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return TNH_OK;
+  if (e == hipErrorOutOfMemory) return fail(TNH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  return fail(TNH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+Context* ctx() {
+  if (!g_live) {
+    fail(TNH_ERR_NOT_INITIALIZED, "tnh_init has not been called");
+    return nullptr;
+  }
+  return &g_ctx;
+}
+
+}  // namespace tnh
+
+using namespace tnh;
+
+extern "C" const char* tnh_last_error(void) { return g_err; }
+
+extern "C" int32_t tnh_device_count(int32_t* count) {
+  TNH_ARG(count != nullptr, "device_count: NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return hip_status(e, "hipGetDeviceCount");
+  }
+  *count = n;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_init(int32_t device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int n = 0;
+  if (int st = hip_status(hipGetDeviceCount(&n), "hipGetDeviceCount")) return st;
+  TNH_ARG(device >= 0 && device < n, "init: device %d out of range (%d devices)", device, n);
+  if (g_live) {
+    if (g_ctx.device == device) return TNH_OK;
+    (void)hipSetDevice(g_ctx.device);
+    (void)hipStreamDestroy(g_ctx.own_stream);
+    g_live = false;
+  }
+  if (int st = hip_status(hipSetDevice(device), "hipSetDevice")) return st;
+  hipStream_t s = nullptr;
+  if (int st = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return st;
+  int cus = 0;
+  (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  g_ctx.device = device;
+  g_ctx.own_stream = s;
+  g_ctx.stream = s;
+  g_ctx.cu_count = cus > 0 ? cus : 256;
+  g_live = true;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_finalize(void) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_live) return TNH_OK;
+  (void)hipSetDevice(g_ctx.device);
+  (void)hipStreamSynchronize(g_ctx.stream);
+  (void)hipStreamDestroy(g_ctx.own_stream);
+  g_ctx = Context{};
+  g_live = false;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_synchronize(void) {
+  TNH_REQUIRE_CTX(cx);
+  return hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize");
+}
+
+extern "C" int32_t tnh_get_stream(void** stream) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(stream != nullptr, "get_stream: NULL");
+  *stream = cx->stream;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_set_stream(void* stream) {
+  TNH_REQUIRE_CTX(cx);
+  cx->stream = static_cast<hipStream_t>(stream);  // NULL selects the HIP null stream
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_reset_stream(void) {
+  TNH_REQUIRE_CTX(cx);
+  cx->stream = cx->own_stream;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_cu_count(int32_t* count) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(count != nullptr, "cu_count: NULL");
+  *count = cx->cu_count;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_malloc(int64_t bytes, void** ptr) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(ptr != nullptr && bytes >= 0, "malloc: bad arguments");
+  *ptr = nullptr;
+  if (bytes == 0) return TNH_OK;
+  return hip_status(hipMalloc(ptr, static_cast<size_t>(bytes)), "hipMalloc");
+}
+
+extern "C" int32_t tnh_free(void* ptr) {
+  TNH_REQUIRE_CTX(cx);
+  if (!ptr) return TNH_OK;
+  return hip_status(hipFree(ptr), "hipFree");
+}
+
+extern "C" int32_t tnh_h2d(void* dst, const void* src, int64_t bytes) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(bytes >= 0, "h2d: negative size");
+  if (bytes == 0) return TNH_OK;
+  TNH_ARG(dst && src, "h2d: NULL pointer");
+  if (int st = hip_status(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyHostToDevice, cx->stream),
+                          "hipMemcpyAsync(H2D)"))
+    return st;
+  return hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize");
+}
+
+extern "C" int32_t tnh_d2h(void* dst, const void* src, int64_t bytes) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(bytes >= 0, "d2h: negative size");
+  if (bytes == 0) return TNH_OK;
+  TNH_ARG(dst && src, "d2h: NULL pointer");
+  if (int st = hip_status(hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToHost, cx->stream),
+                          "hipMemcpyAsync(D2H)"))
+    return st;
+  return hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize");
+}
+
+extern "C" int32_t tnh_event_create(void** ev) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(ev != nullptr, "event_create: NULL");
+  hipEvent_t e = nullptr;
+  if (int st = hip_status(hipEventCreate(&e), "hipEventCreate")) return st;
+  *ev = e;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_event_destroy(void* ev) {
+  TNH_REQUIRE_CTX(cx);
+  if (!ev) return TNH_OK;
+  return hip_status(hipEventDestroy(static_cast<hipEvent_t>(ev)), "hipEventDestroy");
+}
+
+extern "C" int32_t tnh_event_record(void* ev) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(ev != nullptr, "event_record: NULL");
+  return hip_status(hipEventRecord(static_cast<hipEvent_t>(ev), cx->stream), "hipEventRecord");
+}
+
+extern "C" int32_t tnh_event_elapsed_ms(void* start, void* stop, float* ms) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(start && stop && ms, "event_elapsed: NULL");
+  if (int st = hip_status(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize")) return st;
+  return hip_status(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+                    "hipEventElapsedTime");
+}

@@ -1,0 +1,214 @@
+// Max-pool forward/backward and nearest upsample forward/backward.
+//
+// Maxpool follows the CPU path of TMaxPoolLayer (nMaxPoolLayer.pas:265-455):
+// window origin (i*sY + off, j*sX + off) with off = -pad div 2, out-of-range
+// taps read as -MaxSingle, windows scanned n-major then m, strict '>' keeps
+// the first maximum, indices are global flat int64, -1 when no tap beats
+// -MaxSingle.  Backward is a gather: each input element sums, in ascending
+// output index (the order of the serial scatter at :501-512), the deltas of
+// the windows whose recorded index is that element.
+//
+// Upsample (nupsamplelayer.pas:83-113): forward out = scale*in per output
+// pixel; backward gathers the stride^2 output pixels of each input pixel in
+// raster order, in += scale*out each, bit-identical to the serial loop.
+#include <cfloat>
+
+#include "common.hpp"
+
+namespace tnh {
+namespace {
+
+constexpr int kThreads = 256;
+
+unsigned grid_for(int64_t n) {
+  const int64_t b = (n + kThreads - 1) / kThreads;
+  return static_cast<unsigned>(b < 65536 ? (b > 0 ? b : 1) : 65536);
+}
+
+#define GRID_STRIDE(i, n) \
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < (n); i += int64_t(gridDim.x) * blockDim.x)
+
+struct PoolGeom {
+  int64_t C, H, W, OH, OW, size, sX, sY, off;
+};
+
+__global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(PoolGeom g, int64_t total, const float* __restrict__ in,
+                                                               float* __restrict__ out, int64_t* __restrict__ idx) {
+  GRID_STRIDE(o, total) {
+    const int64_t j = o % g.OW;
+    const int64_t t = o / g.OW;
+    const int64_t i = t % g.OH;
+    const int64_t plane = t / g.OH;  // b*C + k
+    float mx = -FLT_MAX;
+    int64_t mi = -1;
+    for (int64_t n = 0; n < g.size; ++n) {
+      const int64_t ch = g.off + i * g.sY + n;
+      for (int64_t m = 0; m < g.size; ++m) {
+        const int64_t cw = g.off + j * g.sX + m;
+        const int64_t index = cw + g.W * (ch + g.H * plane);
+        const bool ok = ch >= 0 && ch < g.H && cw >= 0 && cw < g.W;
+        const float v = ok ? in[index] : -FLT_MAX;
+        if (v > mx) {
+          mi = index;
+          mx = v;
+        }
+      }
+    }
+    out[o] = mx;
+    if (idx) idx[o] = mi;
+  }
+}
+
+// first output row/col whose window can contain input coordinate p:
+// smallest i with off + i*s + size - 1 >= p
+__device__ inline int64_t first_win(int64_t p, int64_t off, int64_t s, int64_t size) {
+  const int64_t t = p - off - size + 1;
+  return t <= 0 ? 0 : (t + s - 1) / s;
+}
+
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(PoolGeom g, int64_t total,
+                                                               const int64_t* __restrict__ idx,
+                                                               const float* __restrict__ delta,
+                                                               float* __restrict__ dIn) {
+  GRID_STRIDE(e, total) {  // e = global input index
+    const int64_t x = e % g.W;
+    const int64_t t = e / g.W;
+    const int64_t y = t % g.H;
+    const int64_t plane = t / g.H;
+    const int64_t i0 = first_win(y, g.off, g.sY, g.size);
+    const int64_t j0 = first_win(x, g.off, g.sX, g.size);
+    int64_t i1 = y - g.off;  // last i with off + i*s <= y
+    int64_t j1 = x - g.off;
+    if (i1 < 0 || j1 < 0) continue;
+    i1 = min(i1 / g.sY, g.OH - 1);
+    j1 = min(j1 / g.sX, g.OW - 1);
+    float v = dIn[e];
+    bool hit = false;
+    for (int64_t i = i0; i <= i1; ++i)
+      for (int64_t j = j0; j <= j1; ++j) {
+        const int64_t o = (plane * g.OH + i) * g.OW + j;
+        if (idx[o] == e) {
+          v = v + delta[o];
+          hit = true;
+        }
+      }
+    if (hit) dIn[e] = v;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void upsample_fwd_kernel(int64_t total, int64_t h, int64_t w, int64_t s,
+                                                                float scale, const float* __restrict__ in,
+                                                                float* __restrict__ out) {
+  const int64_t OW = w * s, OH = h * s;
+  GRID_STRIDE(o, total) {
+    const int64_t x = o % OW;
+    const int64_t t = o / OW;
+    const int64_t y = t % OH;
+    const int64_t c = t / OH;
+    out[o] = scale * in[(c * h + y / s) * w + x / s];
+  }
+}
+
+// 2x nearest with scale 1 is a pure replication: each thread reads one input
+// float and writes a 2x2 output block with two 8-byte stores.
+__global__ __launch_bounds__(kThreads) void upsample2_fwd_kernel(int64_t total, int64_t h, int64_t w, float scale,
+                                                                 const float* __restrict__ in,
+                                                                 float* __restrict__ out) {
+  const int64_t OW = 2 * w;
+  GRID_STRIDE(e, total) {  // e = input index
+    const int64_t x = e % w;
+    const int64_t t = e / w;  // c*h + y
+    const float v = scale * in[e];
+    const int64_t o = (2 * t) * OW + 2 * x;
+    *reinterpret_cast<float2*>(out + o) = make_float2(v, v);
+    *reinterpret_cast<float2*>(out + o + OW) = make_float2(v, v);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void upsample_bwd_kernel(int64_t total, int64_t h, int64_t w, int64_t s,
+                                                                float scale, float* __restrict__ in,
+                                                                const float* __restrict__ out, int zeroIn) {
+  const int64_t OW = w * s;
+  GRID_STRIDE(e, total) {
+    const int64_t x = e % w;
+    const int64_t t = e / w;
+    const int64_t y = t % h;
+    const int64_t c = t / h;
+    float v = zeroIn ? 0.f : in[e];
+    for (int64_t dy = 0; dy < s; ++dy)
+      for (int64_t dx = 0; dx < s; ++dx) {
+        const float p = scale * out[((c * h) * s + y * s + dy) * OW + x * s + dx];
+        v = v + p;
+      }
+    in[e] = v;
+  }
+}
+
+bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+
+}  // namespace
+}  // namespace tnh
+
+using namespace tnh;
+
+extern "C" int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH, int64_t outW, const float* input,
+                                   int64_t c, int64_t h, int64_t w, int64_t strideX, int64_t strideY, int64_t padding,
+                                   int64_t kernelSize, int64_t* indexes, float* output) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && c > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 && padding >= 0,
+          "maxpool_fwd: bad geometry");
+  TNH_ARG(outC == c, "maxpool_fwd: outC %lld != c %lld (maxpool_depth is not supported)", (long long)outC,
+          (long long)c);
+  TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
+          "maxpool_fwd: output dims do not match (h + pad - size)/stride + 1");
+  TNH_ARG(outH > 0 && outW > 0, "maxpool_fwd: empty output");
+  TNH_ARG(input && output, "maxpool_fwd: NULL buffer");
+  const int64_t total = batch * outC * outH * outW;
+  if (total == 0) return TNH_OK;
+  PoolGeom g{c, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, g, total, input, output,
+                     indexes);
+  return launch_status("maxpool_fwd_kernel");
+}
+
+extern "C" int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH, int64_t outW, int64_t h, int64_t w,
+                                   int64_t strideX, int64_t strideY, int64_t padding, int64_t kernelSize,
+                                   const int64_t* indexes, const float* delta, float* deltaIn) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && outC > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 && padding >= 0,
+          "maxpool_bwd: bad geometry");
+  TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
+          "maxpool_bwd: output dims do not match the forward geometry");
+  TNH_ARG(indexes && delta && deltaIn, "maxpool_bwd: NULL buffer");
+  const int64_t total = batch * outC * h * w;
+  if (total == 0) return TNH_OK;
+  PoolGeom g{outC, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, g, total, indexes,
+                     delta, deltaIn);
+  return launch_status("maxpool_bwd_kernel");
+}
+
+extern "C" int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w, float* in, int64_t stride,
+                                int32_t isForward, float scale, float* out, int32_t zeroIn) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && channels > 0 && h > 0 && w > 0 && stride > 0, "upsample: bad geometry");
+  TNH_ARG(in && out, "upsample: NULL buffer");
+  const int64_t planes = batch * channels;
+  if (planes == 0) return TNH_OK;
+  if (isForward) {
+    if (stride == 2 && al8(out) && w > 0) {
+      const int64_t total = planes * h * w;
+      hipLaunchKernelGGL(upsample2_fwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, h, w,
+                         scale, in, out);
+      return launch_status("upsample2_fwd_kernel");
+    }
+    const int64_t total = planes * h * w * stride * stride;
+    hipLaunchKernelGGL(upsample_fwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, h, w, stride,
+                       scale, in, out);
+    return launch_status("upsample_fwd_kernel");
+  }
+  const int64_t total = planes * h * w;
+  hipLaunchKernelGGL(upsample_bwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, h, w, stride,
+                     scale, in, out, zeroIn);
+  return launch_status("upsample_bwd_kernel");
+}

@@ -1,0 +1,269 @@
+"""Darknet cfg parsing and a device-resident network runner.
+
+``parse_cfg`` reads a darknet .cfg (the format TDarknetParser consumes,
+nparser.pas:782-940; INI sections as in nconfig.pas:15-45) into layer specs
+with their shapes resolved.  ``Network`` plays the role of TNNet.forward
+(nnet.pas:275-317) for inference on one GPU: every layer's output lives in
+HBM and each layer is one or two launches through the C ABI.
+
+Fusions (results bit-identical to the unfused layer sequence):
+  * a convolution whose only consumer is the next layer, a ``[shortcut]``
+    with linear activation, writes ``act(conv + bias) + other`` straight into
+    the shortcut's buffer (the separate add of naddlayer.pas:698);
+  * a single-input ``[route]`` is an alias of its input (no copy).
+
+Route concat of several inputs is per image (darknet semantics).  The
+reference's TConcatLayer copies whole batched tensors back to back
+(nconcatlayer.pas:115 -> ntensors.pas:12045), which mixes images at batch > 1;
+``route_mode="reference"`` reproduces that layout for parity studies.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+
+from . import synth
+from .nnhip import acLEAKY, acLINEAR, acLOGISTIC
+
+CFG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cfg")
+_ACT = {"leaky": acLEAKY, "linear": acLINEAR, "logistic": acLOGISTIC}
+
+
+def read_sections(text):
+    """[name] key=value sections, '#'/';' comments (nconfig.pas:15-45)."""
+    secs = []
+    for raw in text.splitlines():
+        line = raw.split("#", 1)[0].split(";", 1)[0].strip()
+        if not line:
+            continue
+        if line.startswith("["):
+            secs.append((line.strip("[]").strip().lower(), {}))
+        elif "=" in line and secs:
+            k, v = line.split("=", 1)
+            secs[-1][1][k.strip()] = v.strip()
+    return secs
+
+
+def parse_cfg(text, height=None, width=None):
+    """Returns (net_options, layers); layers carry resolved in/out shapes (C, H, W)."""
+    secs = read_sections(text)
+    if not secs or secs[0][0] not in ("net", "network"):
+        raise ValueError("cfg must start with [net]")
+    net = secs[0][1]
+    H = int(height or net.get("height", 416))
+    W = int(width or net.get("width", 416))
+    Cin = int(net.get("channels", 3))
+    layers = []
+    shape = (Cin, H, W)
+    for idx, (name, o) in enumerate(secs[1:]):
+        L = {"type": name, "index": idx, "in": shape}
+        if name == "convolutional":
+            k = int(o.get("size", 1))
+            s = int(o.get("stride", 1))
+            pad = int(o.get("padding", 0))
+            if int(o.get("pad", 0)):  # parseConvolutional: pad=1 -> size div 2 (nparser.pas:154)
+                pad = k // 2
+            F = int(o["filters"])
+            C, h, w = shape
+            oh = (h + 2 * pad - k) // s + 1
+            ow = (w + 2 * pad - k) // s + 1
+            L.update(filters=F, size=k, stride=s, pad=pad, act=_ACT[o.get("activation", "logistic")],
+                     bn=int(o.get("batch_normalize", 0)), out=(F, oh, ow))
+        elif name == "shortcut":
+            frm = int(o["from"])
+            src = idx + frm if frm < 0 else frm
+            L.update(src=src, act=_ACT[o.get("activation", "linear")], out=shape)
+            if layers[src]["out"] != shape:
+                raise ValueError(f"shortcut {idx}: shape mismatch with layer {src}")
+        elif name == "route":
+            srcs = [int(v) for v in o["layers"].split(",")]
+            srcs = [idx + v if v < 0 else v for v in srcs]
+            shapes = [layers[v]["out"] for v in srcs]
+            if any(sh[1:] != shapes[0][1:] for sh in shapes):
+                raise ValueError(f"route {idx}: spatial size mismatch")
+            L.update(srcs=srcs, out=(sum(sh[0] for sh in shapes),) + shapes[0][1:])
+        elif name == "upsample":
+            s = int(o.get("stride", 2))
+            C, h, w = shape
+            L.update(stride=s, scale=float(o.get("scale", 1)), out=(C, h * s, w * s))
+        elif name == "maxpool":
+            k = int(o.get("size", 1))
+            s = int(o.get("stride", 1))
+            pad = int(o.get("padding", k - 1))  # parseMaxPool default (nparser.pas:257)
+            C, h, w = shape
+            L.update(size=k, stride=s, pad=pad, out=(C, (h + pad - k) // s + 1, (w + pad - k) // s + 1))
+        elif name == "yolo":
+            mask = [int(v) for v in o.get("mask", "0").split(",")]
+            classes = int(o.get("classes", 80))
+            if shape[0] != len(mask) * (classes + 5):
+                raise ValueError(f"yolo {idx}: {shape[0]} channels != {len(mask)}*(classes+5)")
+            L.update(n=len(mask), classes=classes, out=shape)
+        else:
+            raise ValueError(f"unsupported layer type [{name}]")
+        layers.append(L)
+        shape = L["out"]
+    return net, layers
+
+
+def load_cfg(name="yolov3.cfg", height=None, width=None):
+    path = name if os.path.isabs(name) else os.path.join(CFG_DIR, name)
+    with open(path) as f:
+        return parse_cfg(f.read(), height, width)
+
+
+def conv_flops(layers, batch=1):
+    """2*M*N*K summed over convolutions (the metric's algorithmic FLOP)."""
+    tot = 0
+    for L in layers:
+        if L["type"] == "convolutional":
+            F, oh, ow = L["out"]
+            tot += 2 * F * (L["in"][0] * L["size"] ** 2) * oh * ow * batch
+    return tot
+
+
+def synthetic_weights(layers, seed=0x5EED):
+    """He-normal weights N(0, sqrt(2/fan_in)), one splitmix64 seed per layer;
+    BN folded with its default init (scale 1, mean 0, var 1 -> /sqrt(1)) and
+    biases 0, as the benchmark configuration specifies."""
+    out = {}
+    for L in layers:
+        if L["type"] != "convolutional":
+            continue
+        F = L["filters"]
+        fan_in = L["in"][0] * L["size"] ** 2
+        w = synth.normal(seed + 1000 * L["index"] + 1, (F, fan_in), math.sqrt(2.0 / fan_in))
+        out[L["index"]] = (w, np.zeros(F, np.float32))
+    return out
+
+
+def consumers(layers):
+    use = {i: [] for i in range(len(layers))}
+    for L in layers:
+        i = L["index"]
+        if L["type"] == "shortcut":
+            use[i - 1].append(i)
+            use[L["src"]].append(i)
+        elif L["type"] == "route":
+            for s in L["srcs"]:
+                use[s].append(i)
+        elif i > 0:
+            use[i - 1].append(i)
+    return use
+
+
+class Network:
+    """Inference runner over the C ABI; buffers are device torch tensors."""
+
+    def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image"):
+        import torch
+
+        self.hip, self.layers, self.batch = hip, layers, batch
+        self.route_mode = route_mode
+        self.torch = torch
+        use = consumers(layers)
+        self.fused = set()  # conv indices whose shortcut is fused
+        if fuse:
+            for L in layers:
+                i = L["index"]
+                if (L["type"] == "convolutional" and i + 1 < len(layers) and layers[i + 1]["type"] == "shortcut"
+                        and layers[i + 1]["act"] == acLINEAR and use[i] == [i + 1] and layers[i + 1]["src"] != i):
+                    self.fused.add(i)
+        self.w = {}
+        for i, (w, b) in weights.items():
+            self.w[i] = (torch.from_numpy(np.ascontiguousarray(w)).to(device),
+                         torch.from_numpy(np.ascontiguousarray(b)).to(device))
+        self.out = [None] * len(layers)
+        for L in layers:
+            i = L["index"]
+            if L["type"] == "route" and len(L["srcs"]) == 1:
+                continue  # alias, resolved at run time
+            if i in self.fused:
+                continue  # writes into the shortcut's buffer
+            C, h, w = L["out"]
+            self.out[i] = torch.empty((batch, C, h, w), dtype=torch.float32, device=device)
+        self.input_shape = (batch,) + layers[0]["in"]
+
+    def buffer(self, i):
+        L = self.layers[i]
+        if L["type"] == "route" and len(L["srcs"]) == 1:
+            return self.buffer(L["srcs"][0])
+        if i in self.fused:
+            return self.out[i + 1]
+        return self.out[i]
+
+    def forward(self, x, on_layer=None):
+        """Runs every layer on the context stream; returns the yolo outputs.
+
+        on_layer(i, begin): optional hook called before (begin=True) and after
+        (begin=False) the launches of layer i (used to bracket them with
+        events)."""
+        hip, B = self.hip, self.batch
+        prev = x
+        heads = []
+        for L in self.layers:
+            i, t = L["index"], L["type"]
+            if on_layer:
+                on_layer(i, True)
+            prev = self._layer(L, prev, heads)
+            if on_layer:
+                on_layer(i, False)
+        return heads
+
+    def _layer(self, L, prev, heads):
+        hip, B = self.hip, self.batch
+        i, t = L["index"], L["type"]
+        if t == "convolutional":
+            w, b = self.w[i]
+            C, h, ww = L["in"]
+            res = None
+            if i in self.fused:
+                sc = self.layers[i + 1]
+                res = self.buffer(sc["src"])
+                dst = self.out[i + 1]
+            else:
+                dst = self.out[i]
+            hip.conv2dForward(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], prev, 0, w, b,
+                              L["act"], dst, 0, residual=res)
+            prev = dst
+        elif t == "shortcut":
+            if i - 1 not in self.fused:
+                n = B * int(np.prod(L["out"]))
+                hip.addvv(n, prev, 0, 1, self.buffer(L["src"]), 0, 1, self.out[i], 0, 1)
+                hip.ActivateArray(n, self.out[i], 0, L["act"])
+            prev = self.buffer(i)
+        elif t == "route":
+            if len(L["srcs"]) == 1:
+                prev = self.buffer(L["srcs"][0])
+            else:
+                srcs = [self.buffer(s) for s in L["srcs"]]
+                sizes = [int(np.prod(self.layers[s]["out"])) for s in L["srcs"]]
+                if self.route_mode == "image":
+                    hip.concat(B, srcs, sizes, self.out[i])
+                else:  # whole batched tensors back to back (ntensors.pas:12045)
+                    off = 0
+                    for s, n in zip(srcs, sizes):
+                        hip.copy(B * n, s, 0, 1, self.out[i], off, 1)
+                        off += B * n
+                prev = self.out[i]
+        elif t == "upsample":
+            C, h, ww = L["in"]
+            hip.upSample(B, C, h, ww, prev, L["stride"], 1, L["scale"], self.out[i])
+            prev = self.out[i]
+        elif t == "maxpool":
+            C, h, ww = L["in"]
+            _, oh, ow = L["out"]
+            hip.forwardMaxPool(B, C, oh, ow, prev, C, h, ww, L["stride"], L["stride"], L["pad"], L["size"],
+                               None, self.out[i])
+            prev = self.out[i]
+        elif t == "yolo":
+            C, h, ww = L["in"]
+            hip.yoloForward(B, L["n"], L["classes"], h, ww, prev, self.out[i])
+            heads.append(self.out[i])
+            prev = self.out[i]
+        return prev
+
+    def head_convs(self):
+        """Indices of the convolutions feeding the yolo layers (pre-logistic)."""
+        return [L["index"] - 1 for L in self.layers if L["type"] == "yolo"]

@@ -1,0 +1,359 @@
+"""Host-side mirror of Tensorium's GPU backend object over libtensorium_hip.
+
+``TNNHip`` has the method names, argument order and argument meaning of
+``TNNCuda<T>`` (source/nncuda.pas:35-200), so code written against the
+reference backend (``cuda.gemm(...)``, ``cuda.im2col(...)``, ...) reads the
+same against this one (``hip.gemm(...)``).  Buffers are ``(buffer, offset)``
+pairs exactly as in the reference; a buffer may be a ``DeviceBuffer`` from
+``createDeviceBuffer``, a device ``torch.Tensor`` or a raw device address.
+
+Errors: every C call returns a status; a non-zero status raises
+``TNHError`` carrying ``tnh_last_error()``.  This is the analogue of the
+reference's ``SAFE_CALL`` assertion (nncuda.pas:237-275).
+
+The library must be built (``python tensorium_amd/build.py``); importing this
+module fails loudly if ``libtensorium_hip.so`` is missing -- there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtensorium_hip.so")
+
+# TActivationType ordinals (ntypes.pas:66)
+acLOGISTIC, acLINEAR, acLEAKY = 0, 4, 9
+
+i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
+
+# name -> argtypes (restype is int32 status unless listed in _RESTYPES)
+_PROTOS = {
+    "tnh_init": [i32],
+    "tnh_finalize": [],
+    "tnh_device_count": [C.POINTER(i32)],
+    "tnh_synchronize": [],
+    "tnh_last_error": [],
+    "tnh_get_stream": [C.POINTER(vp)],
+    "tnh_set_stream": [vp],
+    "tnh_reset_stream": [],
+    "tnh_cu_count": [C.POINTER(i32)],
+    "tnh_malloc": [i64, C.POINTER(vp)],
+    "tnh_free": [vp],
+    "tnh_h2d": [vp, vp, i64],
+    "tnh_d2h": [vp, vp, i64],
+    "tnh_event_create": [C.POINTER(vp)],
+    "tnh_event_destroy": [vp],
+    "tnh_event_record": [vp],
+    "tnh_event_elapsed_ms": [vp, vp, C.POINTER(f32)],
+    "tnh_sgemm": [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64],
+    "tnh_sgemm_strided_batched": [i32, i32, i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64,
+                                  f32, vp, i64, i64, i64, i64],
+    "tnh_im2col": [i64] * 11 + [vp, i64, vp, i64],
+    "tnh_im2col_batched": [i64] * 11 + [vp, i64, i64, vp, i64, i64, i64],
+    "tnh_col2im": [i64] * 11 + [vp, i64, vp, i64],
+    "tnh_col2im_batched": [i64] * 11 + [vp, i64, i64, vp, i64, i64, i64],
+    "tnh_conv2d_fwd": [i64] * 11 + [vp, i64, i64, vp, i64, vp, i64, i32, vp, i64, i64, vp, i64, i64, vp, i64],
+    "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
+    "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
+    "tnh_forward_scale": [i64, vp, i64, i64, vp, i64, i64],
+    "tnh_backward_bias": [i64, vp, i64, vp, i64, i64, i64],
+    "tnh_activate": [i64, vp, i64, i32],
+    "tnh_derive": [i64, vp, i64, i32, vp],
+    "tnh_addvv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
+    "tnh_axpy": [i64, f32, vp, i64, i64, vp, i64, i64],
+    "tnh_scale": [i64, f32, vp, i64],
+    "tnh_fill": [i64, vp, i64, f32, i64],
+    "tnh_copy": [i64, vp, i64, i64, vp, i64, i64],
+    "tnh_route": [i64, i32, C.POINTER(vp), C.POINTER(i64), vp],
+    "tnh_maxpool_fwd": [i64] * 4 + [vp] + [i64] * 7 + [vp, vp],
+    "tnh_maxpool_bwd": [i64] * 10 + [vp, vp, vp],
+    "tnh_upsample": [i64, i64, i64, i64, vp, i64, i32, f32, vp, i32],
+    "tnh_bn_normalize": [i64, vp, i64, i64, vp, vp, i64],
+    "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
+}
+_RESTYPES = {"tnh_last_error": C.c_char_p}
+
+_lib = None
+
+
+class TNHError(RuntimeError):
+    """A libtensorium_hip call returned a non-zero status."""
+
+    def __init__(self, fn, status, message):
+        super().__init__(f"{fn} failed with status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+def lib():
+    """Loads libtensorium_hip.so once; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python tensorium_amd/build.py` "
+                              "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, args in _PROTOS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = _RESTYPES.get(name, i32)
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_PROTOS)
+
+
+def call(name, *args):
+    """Calls a tnh_* entry point and raises TNHError on a non-zero status."""
+    L = lib()
+    st = getattr(L, name)(*args)
+    if st != 0:
+        raise TNHError(name, st, L.tnh_last_error().decode(errors="replace"))
+    return st
+
+
+def last_error():
+    return lib().tnh_last_error().decode(errors="replace")
+
+
+class DeviceBuffer:
+    """A device allocation made through tnh_malloc (TCUMem of the reference)."""
+
+    __slots__ = ("ptr", "count", "itemsize")
+
+    def __init__(self, ptr, count, itemsize=4):
+        self.ptr, self.count, self.itemsize = ptr, count, itemsize
+
+    def __int__(self):
+        return self.ptr or 0
+
+
+def addr(buf):
+    """Device address of a buffer argument (None -> NULL)."""
+    if buf is None:
+        return None
+    if isinstance(buf, int):
+        return buf
+    if isinstance(buf, DeviceBuffer):
+        return buf.ptr
+    if hasattr(buf, "data_ptr"):
+        if getattr(buf, "is_cuda", False) is False:
+            raise TypeError("host torch.Tensor passed where a device buffer is required")
+        return buf.data_ptr()
+    raise TypeError(f"not a device buffer: {type(buf)!r}")
+
+
+def _b(flag):
+    return 1 if flag else 0
+
+
+class TNNHip:
+    """MI355X backend object; method surface of TNNCuda<single>."""
+
+    NUM_THREADS = 0x200
+
+    @staticmethod
+    def deviceCount():
+        n = i32(0)
+        st = lib().tnh_device_count(C.byref(n))
+        return n.value if st == 0 else 0
+
+    def __init__(self, deviceIndex=0):
+        call("tnh_init", deviceIndex)
+        self.deviceIndex = deviceIndex
+        self._pool_geom = {}
+
+    # -- lifecycle -------------------------------------------------------
+    def Destroy(self):
+        call("tnh_finalize")
+
+    def finish(self):
+        call("tnh_synchronize")
+
+    @property
+    def stream(self):
+        s = vp()
+        call("tnh_get_stream", C.byref(s))
+        return s.value
+
+    def setStream(self, stream):
+        """Enqueue on `stream` (a hipStream_t; 0/None = the null stream)."""
+        call("tnh_set_stream", stream or None)
+
+    def useTorchStream(self):
+        """Share torch's current stream so torch and library work stay ordered."""
+        import torch
+
+        self.setStream(torch.cuda.current_stream().cuda_stream)
+
+    def resetStream(self):
+        call("tnh_reset_stream")
+
+    def cuCount(self):
+        n = i32(0)
+        call("tnh_cu_count", C.byref(n))
+        return n.value
+
+    # -- memory ------------------------------------------------------------
+    def createDeviceBuffer(self, N):
+        p = vp()
+        call("tnh_malloc", 4 * N, C.byref(p))
+        return DeviceBuffer(p.value, N)
+
+    def freeDeviceBuffer(self, cudaMem):
+        call("tnh_free", addr(cudaMem))
+
+    def writeBuffer(self, cudaMem, bufferSize, buffer):
+        a = np.ascontiguousarray(buffer)
+        assert a.nbytes >= bufferSize
+        call("tnh_h2d", addr(cudaMem), a.ctypes.data, bufferSize)
+
+    def readBuffer(self, cudaMem, bufferSize, buffer):
+        assert isinstance(buffer, np.ndarray) and buffer.flags.c_contiguous and buffer.nbytes >= bufferSize
+        call("tnh_d2h", buffer.ctypes.data, addr(cudaMem), bufferSize)
+
+    # -- GEMM ----------------------------------------------------------------
+    def gemm(self, transA, transB, M, N, K, ALPHA, A, aOffset, lda, B, bOffset, ldb, BETA, C_, cOffset, ldc):
+        call("tnh_sgemm", _b(transA), _b(transB), M, N, K, ALPHA, addr(A), aOffset, lda, addr(B), bOffset, ldb,
+             BETA, addr(C_), cOffset, ldc)
+
+    def gemmStridedBatched(self, transA, transB, M, N, K, ALPHA, A, aOffset, lda, strideA, B, bOffset, ldb,
+                           strideB, BETA, C_, cOffset, ldc, strideC, batchCount):
+        call("tnh_sgemm_strided_batched", _b(transA), _b(transB), M, N, K, ALPHA, addr(A), aOffset, lda, strideA,
+             addr(B), bOffset, ldb, strideB, BETA, addr(C_), cOffset, ldc, strideC, batchCount)
+
+    # -- im2col / col2im -----------------------------------------------------
+    def im2col(self, aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth, strideY, strideX,
+               dilationY, dilationX, im, imOffset, col, colOffset):
+        call("tnh_im2col", aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth, strideY,
+             strideX, dilationY, dilationX, addr(im), imOffset, addr(col), colOffset)
+
+    def im2colStridedBatched(self, aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
+                             strideY, strideX, dilationY, dilationX, im, imStride, imOffset, col, colStride,
+                             colOffset, batchCount):
+        """sim2colStridedBatched (ntensors.pas:11493) argument order."""
+        call("tnh_im2col_batched", aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
+             strideY, strideX, dilationY, dilationX, addr(im), imOffset, imStride, addr(col), colOffset, colStride,
+             batchCount)
+
+    def col2im(self, aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth, strideY, strideX,
+               dilationY, dilationX, col, colOffset, im, imOffset):
+        call("tnh_col2im", aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth, strideY,
+             strideX, dilationY, dilationX, addr(col), colOffset, addr(im), imOffset)
+
+    def col2imStridedBatched(self, aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
+                             strideY, strideX, dilationY, dilationX, col, colStride, colOffset, im, imStride,
+                             imOffset, batchCount):
+        """scol2imStridedBatched (ntensors.pas:11833) argument order."""
+        call("tnh_col2im_batched", aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
+             strideY, strideX, dilationY, dilationX, addr(col), colOffset, colStride, addr(im), imOffset, imStride,
+             batchCount)
+
+    # -- fused convolution (new: replaces im2col+gemm+bias+activate) ---------
+    def conv2dForward(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
+                      biases, activation, output, outOffset, inBatchStride=None, outBatchStride=None,
+                      residual=None, resOffset=0, resBatchStride=None, workspace=None, workspaceBytes=0):
+        oh = (h + 2 * padding - kernelSize) // stride + 1
+        ow = (w + 2 * padding - kernelSize) // stride + 1
+        xs = c * h * w if inBatchStride is None else inBatchStride
+        os_ = filters * oh * ow if outBatchStride is None else outBatchStride
+        rs = filters * oh * ow if resBatchStride is None else resBatchStride
+        call("tnh_conv2d_fwd", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
+             addr(input), inOffset, xs, addr(weights), 0, addr(biases), 0, activation, addr(residual), resOffset,
+             rs, addr(output), outOffset, os_, addr(workspace), workspaceBytes)
+        return oh, ow
+
+    # -- epilogue / element-wise ---------------------------------------------
+    def forwardBias(self, dstSize, dst, offset, srcSize, src, incb, batch):
+        call("tnh_forward_bias", dstSize, addr(dst), offset, srcSize, addr(src), incb, batch)
+
+    def forwardScale(self, dstSize, dst, offset, scaleSize, scale, incb, batch):
+        call("tnh_forward_scale", dstSize, addr(dst), offset, scaleSize, addr(scale), incb, batch)
+
+    def backwardBias(self, dstSize, dst, srcSize, src, srcOffset, incb, batch):
+        call("tnh_backward_bias", dstSize, addr(dst), srcSize, addr(src), srcOffset, incb, batch)
+
+    def ActivateArray(self, N, x, offset, activation):
+        call("tnh_activate", N, addr(x), offset, activation)
+
+    def DeriveArray(self, N, x, offset, activation, delta):
+        call("tnh_derive", N, addr(x), offset, activation, addr(delta))
+
+    def addvv(self, N, src1, src1Offset, inca, src2, src2Offset, incb, dst, dstOffset, incc):
+        call("tnh_addvv", N, addr(src1), src1Offset, inca, addr(src2), src2Offset, incb, addr(dst), dstOffset, incc)
+
+    def axpy(self, N, a, x, xOffset, incx, y, yOffset, incy):
+        call("tnh_axpy", N, a, addr(x), xOffset, incx, addr(y), yOffset, incy)
+
+    def scale(self, N, a, x, stride):
+        call("tnh_scale", N, a, addr(x), stride)
+
+    def fill(self, N, x, offset, val, stride):
+        call("tnh_fill", N, addr(x), offset, val, stride)
+
+    def copy(self, N, src, srcOffset, inca, dst, dstOffset, incb):
+        call("tnh_copy", N, addr(src), srcOffset, inca, addr(dst), dstOffset, incb)
+
+    def concat(self, batch, srcs, sizes, dst):
+        """Per-image route concat: dst[b] = [src0[b] | src1[b] | ...]."""
+        n = len(srcs)
+        ptrs = (vp * n)(*[addr(s) for s in srcs])
+        szs = (i64 * n)(*sizes)
+        call("tnh_route", batch, n, ptrs, szs, addr(dst))
+
+    # -- pooling / resampling ------------------------------------------------
+    def forwardMaxPool(self, aBatch, outC, outH, outW, input, c, h, w, stride_x, stride_y, padding, kernelSize,
+                       indexes, output):
+        call("tnh_maxpool_fwd", aBatch, outC, outH, outW, addr(input), c, h, w, stride_x, stride_y, padding,
+             kernelSize, addr(indexes), addr(output))
+        if indexes is not None:
+            self._pool_geom[addr(indexes)] = (h, w, stride_x, stride_y, padding, kernelSize)
+
+    def backwardMaxPool(self, aBatch, outC, outH, outW, output, indexes, delta, geometry=None):
+        """output = delta of the layer input (accumulated), as in the reference.
+
+        The gather formulation needs the forward geometry; it is remembered
+        from the forwardMaxPool call that filled ``indexes`` unless given as
+        ``geometry=(h, w, stride_x, stride_y, padding, kernelSize)``.
+        """
+        g = geometry or self._pool_geom.get(addr(indexes))
+        if g is None:
+            raise TNHError("tnh_maxpool_bwd", 2, "unknown forward geometry for these indexes")
+        h, w, sx, sy, pad, k = g
+        call("tnh_maxpool_bwd", aBatch, outC, outH, outW, h, w, sx, sy, pad, k, addr(indexes), addr(delta),
+             addr(output))
+
+    def upSample(self, aBatch, aChannels, outHeight, outWidth, in_, stride, isForward, scale, out, zeroIn=0):
+        call("tnh_upsample", aBatch, aChannels, outHeight, outWidth, addr(in_), stride, isForward, scale, addr(out),
+             zeroIn)
+
+    def yoloForward(self, batch, n, classes, h, w, input, output):
+        """TYoloLayer.forward inference: copy + logistic on x, y, obj, classes."""
+        call("tnh_yolo_fwd", batch, n, classes, h, w, addr(input), addr(output))
+
+    # -- batch norm ------------------------------------------------------------
+    def blockNormalize(self, dstSize, dst, offset, N, mean, variance, batch):
+        call("tnh_bn_normalize", dstSize, addr(dst), offset, N, addr(mean), addr(variance), batch)
+
+    # -- events ----------------------------------------------------------------
+    def eventCreate(self):
+        e = vp()
+        call("tnh_event_create", C.byref(e))
+        return e.value
+
+    def eventRecord(self, ev):
+        call("tnh_event_record", ev)
+
+    def eventElapsed(self, start, stop):
+        ms = f32(0)
+        call("tnh_event_elapsed_ms", start, stop, C.byref(ms))
+        return ms.value
+
+    def eventDestroy(self, ev):
+        call("tnh_event_destroy", ev)

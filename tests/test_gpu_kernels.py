@@ -1,0 +1,340 @@
+"""GPU parity tests: every kernel through the C ABI against the CPU oracle on
+identical seeded inputs.  Bit-exact for im2col/col2im, maxpool (values and
+int64 indices), upsample, bias, activations, copies and the YOLO head;
+per-tensor max|g - r| / max|r| <= 1e-5 for GEMM and convolution, and exact
+equality for GEMMs on integer-valued data (every partial sum exact)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import refcpu as R
+from tensorium_amd import synth
+from tensorium_amd.nnhip import TNHError, acLEAKY, acLINEAR, acLOGISTIC
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def D(a):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    torch.cuda.synchronize()
+    return t
+
+
+def H(t, hip):
+    hip.finish()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def op(X, t):
+    return X.T if t else X
+
+
+# ---------------------------------------------------------------- SGEMM ----
+SHAPES = [(1, 1, 1), (7, 5, 3), (33, 65, 17), (64, 64, 16), (128, 128, 64), (129, 257, 100), (300, 200, 500),
+          (16, 5000, 27)]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_sgemm_exact_integer(hip, ta, tb, M, N, K):
+    case(f"sgemm int ta={ta} tb={tb} {M}x{N}x{K}")
+    rng = np.random.default_rng(M * 1000 + N + K)
+    A = rng.integers(-4, 5, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (N, K) if tb else (K, N)).astype(np.float32)
+    C0 = rng.integers(-9, 10, (M, N)).astype(np.float32)
+    dA, dB, dC = D(A), D(B), D(C0)
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, A.shape[1], dB, 0, B.shape[1], 1.0, dC, 0, N)
+    ref = op(A, ta).astype(np.int64) @ op(B, tb).astype(np.int64) + C0.astype(np.int64)
+    assert np.array_equal(H(dC, hip), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (512, 512, 512), (100, 300, 1000), (64, 10816, 288)])
+def test_sgemm_vs_oracle(hip, ta, tb, M, N, K):
+    case(f"sgemm rand ta={ta} tb={tb} {M}x{N}x{K}")
+    A = synth.uniform(11, (K, M) if ta else (M, K), -1, 1)
+    B = synth.uniform(12, (N, K) if tb else (K, N), -1, 1)
+    C = np.zeros((M, N), np.float32)
+    dA, dB, dC = D(A), D(B), D(C)
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, A.shape[1], dB, 0, B.shape[1], 0.0, dC, 0, N)
+    R.sgemm(ta, tb, M, N, K, 1.0, A, A.shape[1], B, B.shape[1], 0.0, C, N)
+    assert R.rel_err(H(dC, hip), C) <= TOL
+
+
+def test_sgemm_alpha_beta_offsets_ld(hip):
+    case("sgemm alpha/beta, offsets, padded ld")
+    rng = np.random.default_rng(5)
+    M, N, K, lda, ldb, ldc = 45, 70, 33, 40, 77, 81
+    A = rng.uniform(-1, 1, 3 + M * lda).astype(np.float32)
+    B = rng.uniform(-1, 1, 5 + K * ldb).astype(np.float32)
+    C = rng.uniform(-1, 1, 7 + M * ldc).astype(np.float32)
+    dA, dB, dC = D(A), D(B), D(C)
+    hip.gemm(0, 0, M, N, K, 0.5, dA, 3, lda, dB, 5, ldb, 2.0, dC, 7, ldc)
+    ref = C.copy()
+    Cv = ref[7:].reshape(M, ldc)
+    Cv2 = np.ascontiguousarray(Cv)
+    R.sgemm(0, 0, M, N, K, 0.5, A[3:].reshape(M, lda), lda, B[5:].reshape(K, ldb), ldb, 2.0, Cv2, ldc)
+    ref[7:] = Cv2.ravel()
+    got = H(dC, hip)
+    assert np.array_equal(got[:7], C[:7])                      # untouched prefix
+    g2, r2 = got[7:].reshape(M, ldc), ref[7:].reshape(M, ldc)
+    assert np.array_equal(g2[:, N:], r2[:, N:])                # untouched ld padding
+    assert R.rel_err(g2[:, :N], r2[:, :N]) <= TOL
+
+
+def test_sgemm_beta_zero_overwrites(hip):
+    case("sgemm beta=0 ignores NaN in C")
+    A = np.ones((8, 4), np.float32)
+    B = np.ones((4, 8), np.float32)
+    dC = D(np.full((8, 8), np.nan, np.float32))
+    hip.gemm(0, 0, 8, 8, 4, 1.0, D(A), 0, 4, D(B), 0, 8, 0.0, dC, 0, 8)
+    assert np.all(H(dC, hip) == 4.0)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_sgemm_strided_batched(hip, ta, tb):
+    case(f"sgemm strided batched ta={ta} tb={tb}")
+    M, N, K, batch = 40, 90, 50, 3
+    A = synth.uniform(21, (K, M) if ta else (M, K), -1, 1)  # shared: strideA = 0
+    B = synth.uniform(22, (batch,) + ((N, K) if tb else (K, N)), -1, 1)
+    C = np.zeros((batch, M, N), np.float32)
+    dC = D(C)
+    hip.gemmStridedBatched(ta, tb, M, N, K, 1.0, D(A), 0, A.shape[1], 0, D(B), 0, B.shape[2], N * K, 0.0, dC, 0, N,
+                           M * N, batch)
+    R.sgemm_strided_batched(ta, tb, M, N, K, 1.0, A, A.shape[1], 0, B, B.shape[2], N * K, 0.0, C, N, M * N, batch)
+    assert R.rel_err(H(dC, hip), C) <= TOL
+
+
+# ------------------------------------------------------- im2col/col2im ----
+GEOMS = [((1, 3, 416, 416), 3, 1, 1), ((2, 8, 33, 31), 3, 1, 2), ((2, 5, 20, 20), 1, 0, 1), ((1, 4, 13, 13), 3, 1, 1),
+         ((3, 2, 10, 12), 3, 2, 3)]
+
+
+@pytest.mark.parametrize("shape,k,p,s", GEOMS)
+def test_im2col_bit_exact(hip, shape, k, p, s):
+    case(f"im2col {shape} k{k} p{p} s{s}")
+    x = synth.uniform(31, shape)
+    B, Cc, Hh, W = shape
+    ref = R.im2col(x, k, k, p, p, s, s)
+    dcol = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.im2colStridedBatched(Cc, Hh, W, k, k, p, p, s, s, 1, 1, D(x), Cc * Hh * W, 0, dcol, ref[0].size, 0, B)
+    assert np.array_equal(H(dcol, hip), ref)
+
+
+def test_im2col_dilation(hip):
+    case("im2col dilation 2")
+    x = synth.uniform(32, (1, 3, 15, 14))
+    ref = R.im2col(x, 3, 3, 2, 2, 1, 1, 2, 2)
+    dcol = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.im2col(3, 15, 14, 3, 3, 2, 2, 1, 1, 2, 2, D(x), 0, dcol, 0)
+    assert np.array_equal(H(dcol, hip), ref)
+
+
+@pytest.mark.parametrize("shape,k,p,s", GEOMS[1:])
+def test_col2im_bit_exact_accumulates(hip, shape, k, p, s):
+    case(f"col2im {shape} k{k} p{p} s{s}")
+    B, Cc, Hh, W = shape
+    OH, OW = R.conv_out(Hh, k, p, s), R.conv_out(W, k, p, s)
+    col = synth.normal(33, (B, Cc * k * k, OH * OW))
+    im0 = synth.normal(34, shape)
+    ref = R.col2im(col, im0.copy(), k, k, p, p, s, s)
+    dim = D(im0)
+    hip.col2imStridedBatched(Cc, Hh, W, k, k, p, p, s, s, 1, 1, D(col), col[0].size, 0, dim, Cc * Hh * W, 0, B)
+    assert np.array_equal(H(dim, hip), ref)
+
+
+# ----------------------------------------------------------- convolution ----
+CONVS = [  # batch, C, H, F, k, s, p, act
+    (1, 3, 416, 16, 3, 1, 1, acLEAKY),    # config 1
+    (2, 32, 52, 64, 3, 2, 1, acLEAKY),
+    (2, 64, 26, 32, 1, 1, 0, acLEAKY),
+    (3, 128, 13, 255, 1, 1, 0, acLINEAR),  # odd HW (169): scalar 1x1 path
+    (2, 256, 13, 512, 3, 1, 1, acLEAKY),
+    (1, 27, 30, 130, 3, 1, 1, acLEAKY),    # K = 243, F not a tile multiple
+]
+
+
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", CONVS)
+def test_conv_forward_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act):
+    case(f"conv B{B} C{Cc} H{Hh} F{F} k{k} s{s} p{p} act{act}")
+    x = synth.uniform(41, (B, Cc, Hh, Hh))
+    Wt = synth.normal(42, (F, Cc * k * k), 0.05 if Cc == 3 else (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(43, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, k, s, p, act)
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, D(Wt), D(b), act, dout, 0)
+    assert R.rel_err(H(dout, hip), ref) <= TOL
+
+
+def test_conv_golden_fixture(hip):
+    case("conv golden fixture (torch fp64)")
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "conv_small.npz"))
+    dout = torch.empty(g["y64"].shape, dtype=torch.float32, device="cuda")
+    hip.conv2dForward(1, 3, 16, 16, 8, 3, 1, 1, D(g["x"]), 0, D(g["W"]), D(g["b"]), acLEAKY, dout, 0)
+    assert R.rel_err(H(dout, hip), g["y64"]) <= TOL
+
+
+def test_conv_fused_shortcut_and_strided_io(hip):
+    """residual fused after the activation (== conv then addvv) and output
+    written into a channel slice of a wider (route) buffer."""
+    case("conv + fused shortcut + strided output")
+    B, Cc, Hh, F = 2, 64, 26, 128
+    x = synth.uniform(51, (B, Cc, Hh, Hh))
+    Wt = synth.normal(52, (F, Cc * 9), (2.0 / (Cc * 9)) ** 0.5)
+    b = synth.normal(53, (F,), 0.1)
+    res = synth.normal(54, (B, F, Hh, Hh))
+    y = R.conv_forward(x, Wt, b, 3, 1, 1, acLEAKY)
+    ref = R.addvv(y, res)
+    wide = torch.zeros((B, F + 32, Hh, Hh), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, 1, 1, D(x), 0, D(Wt), D(b), acLEAKY, wide, 32 * Hh * Hh,
+                      outBatchStride=(F + 32) * Hh * Hh, residual=D(res))
+    got = H(wide, hip)
+    assert np.all(got[:, :32] == 0)
+    assert R.rel_err(got[:, 32:], ref) <= TOL
+    # the fused add itself is one fp32 add: exact w.r.t. the GPU conv result
+    plain = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, 1, 1, D(x), 0, D(Wt), D(b), acLEAKY, plain, 0)
+    assert np.array_equal(got[:, 32:], H(plain, hip) + res)
+
+
+# ------------------------------------------------------- pool / upsample ----
+@pytest.mark.parametrize("size,stride,pad", [(2, 2, 0), (3, 2, 0), (2, 1, 1), (3, 1, 2), (5, 1, 4)])
+def test_maxpool_forward_backward_bit_exact(hip, size, stride, pad):
+    case(f"maxpool size{size} stride{stride} pad{pad}")
+    B, Cc, Hh, W = 2, 5, 19, 16
+    x = synth.normal(61, (B, Cc, Hh, W))
+    x[0, 0, :4, :4] = 1.0  # ties
+    out, idx = R.maxpool_fwd(x, size, stride, stride, pad)
+    _, _, OH, OW = out.shape
+    dout = torch.empty(out.shape, dtype=torch.float32, device="cuda")
+    didx = torch.empty(out.shape, dtype=torch.int64, device="cuda")
+    hip.forwardMaxPool(B, Cc, OH, OW, D(x), Cc, Hh, W, stride, stride, pad, size, didx, dout)
+    assert np.array_equal(H(dout, hip), out)
+    assert np.array_equal(H(didx, hip), idx)
+    delta = synth.normal(62, out.shape)
+    dIn0 = synth.normal(63, x.shape)
+    ref = R.maxpool_bwd(idx, delta, dIn0.copy())
+    ddIn = D(dIn0)
+    hip.backwardMaxPool(B, Cc, OH, OW, ddIn, didx, D(delta))
+    assert np.array_equal(H(ddIn, hip), ref)
+
+
+def test_maxpool_inference_no_indexes(hip):
+    case("maxpool without indexes")
+    x = synth.normal(64, (2, 3, 8, 8))
+    out, _ = R.maxpool_fwd(x, 2, 2, 2, 0, with_idx=False)
+    dout = torch.empty(out.shape, dtype=torch.float32, device="cuda")
+    hip.forwardMaxPool(2, 3, 4, 4, D(x), 3, 8, 8, 2, 2, 0, 2, None, dout)
+    assert np.array_equal(H(dout, hip), out)
+
+
+@pytest.mark.parametrize("stride,scale", [(2, 1.0), (2, 0.5), (3, 1.0)])
+def test_upsample_bit_exact(hip, stride, scale):
+    case(f"upsample stride{stride} scale{scale}")
+    B, Cc, h, w = 2, 7, 13, 11
+    x = synth.normal(71, (B, Cc, h, w))
+    ref = R.upsample_fwd(x, stride, scale)
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.upSample(B, Cc, h, w, D(x), stride, 1, scale, dout)
+    assert np.array_equal(H(dout, hip), ref)
+    d = synth.normal(72, ref.shape)
+    dIn0 = synth.normal(73, x.shape)
+    refb = R.upsample_bwd(dIn0.copy(), d, stride, scale)
+    ddIn = D(dIn0)
+    hip.upSample(B, Cc, h, w, ddIn, stride, 0, scale, D(d))
+    assert np.array_equal(H(ddIn, hip), refb)
+
+
+# ------------------------------------------------------------ element-wise ----
+def test_bias_scale_activation_bit_exact(hip):
+    case("forward_bias / forward_scale / activate / derive")
+    B, F, P = 3, 17, 50
+    x = synth.normal(81, (B, F, P))
+    b = synth.normal(82, (F,))
+    dx = D(x)
+    hip.forwardBias(x.size, dx, 0, F, D(b), 1, B)
+    ref = R.forward_bias(x.copy(), b, B)
+    assert np.array_equal(H(dx, hip), ref)
+    hip.forwardScale(x.size, dx, 0, F, D(b), 1, B)
+    ref = R.forward_scale(ref, b, B)
+    assert np.array_equal(H(dx, hip), ref)
+    v = np.concatenate([x.ravel(), np.array([0.0, -0.0, np.nan, -np.inf, np.inf, -1e-40], np.float32)])
+    dv = D(v)
+    hip.ActivateArray(v.size, dv, 0, acLEAKY)
+    refv = R.activate(v.copy(), acLEAKY)
+    assert np.array_equal(H(dv, hip).view(np.uint32), refv.view(np.uint32))
+    delta = synth.normal(83, v.shape)
+    dd = D(delta)
+    hip.DeriveArray(v.size, D(refv), 0, acLEAKY, dd)
+    assert np.array_equal(H(dd, hip), R.derive(refv, acLEAKY, delta.copy()))
+
+
+def test_copy_fill_axpy_addvv_route(hip):
+    case("copy / fill / axpy / addvv / route")
+    a = synth.normal(91, (1000,))
+    b = synth.normal(92, (1000,))
+    da, db = D(a), D(b)
+    dc = torch.empty(1000, dtype=torch.float32, device="cuda")
+    hip.addvv(1000, da, 0, 1, db, 0, 1, dc, 0, 1)
+    assert np.array_equal(H(dc, hip), a + b)
+    hip.addvv(333, da, 1, 3, db, 0, 3, dc, 0, 3)  # strided
+    got = H(dc, hip)
+    assert np.array_equal(got[0:999:3], a[1::3][:333] + b[0:999:3])
+    hip.axpy(1000, 0.25, da, 0, 1, db, 0, 1)
+    assert np.array_equal(H(db, hip), b + np.float32(0.25) * a)
+    hip.fill(500, dc, 1, 7.0, 2)
+    got = H(dc, hip)
+    assert np.all(got[1:1000:2] == 7.0)
+    hip.copy(1000, da, 0, 1, dc, 0, 1)
+    assert np.array_equal(H(dc, hip), a)
+    hip.scale(1000, 3.0, dc, 1)
+    assert np.array_equal(H(dc, hip), np.float32(3.0) * a)
+    s0, s1 = synth.normal(93, (2, 3, 4)), synth.normal(94, (2, 5, 4))
+    dst = torch.empty((2, 8, 4), dtype=torch.float32, device="cuda")
+    hip.concat(2, [D(s0), D(s1)], [12, 20], dst)
+    assert np.array_equal(H(dst, hip), np.concatenate([s0, s1], axis=1))
+
+
+def test_yolo_head_bit_exact(hip):
+    case("yolo head logistic")
+    x = synth.normal(95, (2, 3 * 85, 13, 13), 3.0)
+    ref = R.yolo_fwd(x, 3, 80, exact=True)
+    dout = torch.empty(x.shape, dtype=torch.float32, device="cuda")
+    hip.yoloForward(2, 3, 80, 13, 13, D(x), dout)
+    assert np.array_equal(H(dout, hip), ref)
+
+
+def test_bn_normalize_vs_oracle_exact(hip):
+    case("bn normalize (exact division)")
+    B, F, P = 2, 6, 40
+    x = synth.normal(96, (B, F, P))
+    mean = synth.normal(97, (F,))
+    var = synth.uniform(98, (F,), 0.1, 3.0)
+    var[2] = 0.0
+    dx = D(x)
+    hip.blockNormalize(x.size, dx, 0, F, D(mean), D(var), B)
+    assert np.array_equal(H(dx, hip), R.bn_normalize(x.copy(), mean, var, B, exact=True))
+
+
+# --------------------------------------------------------------- errors ----
+def test_invalid_arguments_raise(hip):
+    case("argument checks")
+    dx = D(np.zeros(16, np.float32))
+    with pytest.raises(TNHError):
+        hip.gemm(0, 0, 4, 4, 4, 1.0, dx, 0, 2, dx, 0, 4, 0.0, dx, 0, 4)  # lda < K
+    with pytest.raises(TNHError):
+        hip.conv2dForward(1, 1, 4, 4, 1, 5, 1, 2, dx, 0, dx, None, acLEAKY, dx, 0)  # 5x5 unsupported
+    with pytest.raises(TNHError):
+        hip.ActivateArray(4, dx, 0, 123)
+    with pytest.raises(TNHError):
+        hip.forwardMaxPool(1, 1, 3, 3, dx, 1, 4, 4, 2, 2, 0, 2, None, dx)  # wrong out dims
+    hip.finish()  # the context stays usable after rejected calls

@@ -1,0 +1,74 @@
+"""YOLOv3-416 end to end on the GPU against the CPU oracle: the three
+pre-logistic head convolutions (darknet layers 81, 93, 105) within the
+per-tensor 1e-5 bound, every intermediate convolution too, and the yolo
+outputs.  Batch 2 checks that per-image results do not depend on the batch
+(per-image route concat)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import netref
+from oracle import refcpu as R
+from tensorium_amd import darknet, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def yolo():
+    net, layers = darknet.load_cfg("yolov3.cfg")
+    return layers, darknet.synthetic_weights(layers)
+
+
+def run_gpu(hip, layers, weights, x, fuse=True):
+    n = darknet.Network(hip, layers, x.shape[0], weights, fuse=fuse)
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    heads = n.forward(dx)
+    hip.finish()
+    return n, [h.cpu().numpy() for h in heads]
+
+
+def test_yolov3_416_batch1_heads(hip, yolo):
+    layers, W = yolo
+    print("[case] yolov3-416 batch 1 vs oracle", flush=True)
+    x = synth.uniform(7, (1, 3, 416, 416))
+    ref = netref.forward(layers, W, x)
+    n, heads = run_gpu(hip, layers, W, x)
+    worst = 0.0
+    for L in layers:
+        i = L["index"]
+        if L["type"] == "convolutional" and i not in n.fused:
+            e = R.rel_err(n.out[i].cpu().numpy(), ref[i])
+            worst = max(worst, e)
+            assert e <= TOL, (i, e)
+    for i in (81, 93, 105):
+        assert R.rel_err(n.out[i].cpu().numpy(), ref[i]) <= TOL
+    for h, i in zip(heads, (82, 94, 106)):
+        # logistic of values matching to ~1e-6 relative: compare loosely, the
+        # conv outputs above carry the parity bound
+        assert np.max(np.abs(h - ref[i])) < 1e-3
+    print(f"worst per-tensor conv error {worst:.3e}", flush=True)
+
+
+def test_yolov3_fusion_is_exact(hip, yolo):
+    """Shortcut fused into the conv epilogue == separate addvv, bit for bit."""
+    layers, W = yolo
+    print("[case] yolov3 fused vs unfused", flush=True)
+    x = synth.uniform(8, (1, 3, 416, 416))
+    _, a = run_gpu(hip, layers, W, x, fuse=True)
+    _, b = run_gpu(hip, layers, W, x, fuse=False)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+
+
+def test_yolov3_batch_independent(hip, yolo):
+    layers, W = yolo
+    print("[case] yolov3 batch 2 == two batch-1 runs", flush=True)
+    x = synth.uniform(9, (2, 3, 416, 416))
+    _, h2 = run_gpu(hip, layers, W, x)
+    for b in range(2):
+        _, h1 = run_gpu(hip, layers, W, x[b:b + 1].copy())
+        for u, v in zip(h2, h1):
+            assert R.rel_err(u[b:b + 1], v) <= TOL
