@@ -33,9 +33,12 @@ def log(*a):
 
 
 def kernel_kind(L, batch):
-    """Name of the kernel family a conv layer launches (see conv.hip)."""
-    is1x1 = L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0
-    return "conv1x1_kernel" if is1x1 else f"conv_gather_kernel<{L['size']}x{L['size']}>"
+    """Kernel family a conv layer launches (conv_kernel<cfg, MODE> in conv.hip)."""
+    if L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0:
+        return "conv_kernel<1x1>"
+    if L["size"] == 3 and L["in"][0] % 16 == 0:
+        return "conv_kernel<tap3x3>"
+    return f"conv_kernel<gather{L['size']}x{L['size']}>"
 
 
 def time_forward(hip, net, x, steps, warmup):

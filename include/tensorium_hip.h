@@ -124,6 +124,9 @@ int32_t tnh_col2im_batched(int64_t C, int64_t H, int64_t W, int64_t kh,
                            int64_t batch);
 
 /* ---- fused convolution ------------------------------------------------- */
+/* weight layouts accepted by tnh_conv2d_fwd */
+enum { TNH_WEIGHTS_REFERENCE = 0, TNH_WEIGHTS_TAP_MAJOR = 1 };
+
 /* Replaces the sequence im2col -> gemmStridedBatched -> forwardBias ->
  * ActivateArray of TConvolutionalLayer.forwardGPU
  * (nConvolutionLayer.pas:1051-1118) and the CPU forward
@@ -134,21 +137,32 @@ int32_t tnh_col2im_batched(int64_t C, int64_t H, int64_t W, int64_t kh,
  * route (concat) destination can be written in place.  bias and residual may
  * be NULL.  The residual add (a following shortcut layer, naddlayer.pas:698)
  * is applied after the activation, exactly as the separate layer would.
- * workspace/workspaceBytes: scratch for split-K partial sums (may be NULL/0,
- * then split-K is not used). */
+ * weightLayout: TNH_WEIGHTS_REFERENCE ([F][C][kh][kw], the reference's
+ * storage, nConvolutionLayer.pas:206) or TNH_WEIGHTS_TAP_MAJOR
+ * ([F][kh][kw][C], from tnh_conv2d_pack_weights; the fast path).
+ * Kernels: 1x1/3x3, any stride/padding.  The first call for a shape may
+ * time several tile shapes (see tnh_conv2d_set_autotune). */
 int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W,
                        int64_t F, int64_t kh, int64_t kw, int64_t pH,
                        int64_t pW, int64_t sY, int64_t sX, const float *x,
                        int64_t xOff, int64_t xBatchStride,
-                       const float *weights, int64_t wOff, const float *bias,
-                       int64_t biasOff, int32_t act, const float *residual,
-                       int64_t rOff, int64_t rBatchStride, float *out,
-                       int64_t outOff, int64_t outBatchStride,
-                       float *workspace, int64_t workspaceBytes);
+                       const float *weights, int64_t wOff, int32_t weightLayout,
+                       const float *bias, int64_t biasOff, int32_t act,
+                       const float *residual, int64_t rOff,
+                       int64_t rBatchStride, float *out, int64_t outOff,
+                       int64_t outBatchStride);
 /* output size of tnh_conv2d_fwd: (H + 2p - k)/s + 1 (standard formula) */
 int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw,
                             int64_t pH, int64_t pW, int64_t sY, int64_t sX,
                             int64_t *OH, int64_t *OW);
+/* No reference counterpart (layout helper): dst[f][ky][kx][c] =
+ * src[f][c][ky][kx] on the device; src and dst must not overlap. */
+int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
+                                const float *src, float *dst);
+/* No reference counterpart: enable (1, default) or disable per-shape
+ * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape
+ * (0..5), -1 lets the library choose. */
+int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig);
 
 /* ---- epilogue and element-wise ops ------------------------------------- */
 /* TNNCuda.forwardBias (nncuda.pas:582): blockSize = dstSize/(srcSize*batch);

@@ -1,13 +1,28 @@
-// Fused convolution forward: implicit-GEMM (im2col gathered straight into
+// Fused convolution forward: implicit GEMM (im2col gathered straight into
 // LDS) on MFMA with the bias + activation (+ shortcut) epilogue applied to
 // the accumulators before the single write of the output.
 //
 // GEMM view (Conv2D, ntensors.pas:8252-8345, batch merged into N):
 //   M = F filters, N = batch*OH*OW, K = C*kh*kw
-//   A = weights [F][K] row-major (filter-major, nConvolutionLayer.pas:206)
+//   A = weights [F][K] row-major
 //   B = im2col(x) gathered on the fly
 // Epilogue per element (reference order, nConvolutionLayer.pas:508-545 and
 // naddlayer.pas:698):  v = acc + bias[f];  v = act(v);  v = v + residual.
+//
+// Weight layouts: TNH_WEIGHTS_REFERENCE = [F][C][kh][kw] (the reference's
+// filter-major storage, nConvolutionLayer.pas:206), TNH_WEIGHTS_TAP_MAJOR =
+// [F][kh][kw][C] (tnh_conv2d_pack_weights).  With tap-major weights and
+// C % BK == 0 each K panel lies inside one (ky, kx) tap and the gather does
+// one bounds test per panel.
+//
+// Kernel choice: several tile shapes are compiled; the first call for a
+// shape times the valid candidates with HIP events (when autotuning is on
+// and the stream is not being captured) and caches the fastest; otherwise a
+// wave-quantization cost model picks one.
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
 #include "common.hpp"
 #include "gemm_core.hpp"
 
@@ -15,17 +30,15 @@ namespace tnh {
 namespace {
 
 struct ConvArgs {
-  const float* x;
-  int64_t xBatchStride;
+  ConvGeom g;
   const float* w;
+  int64_t wBytes;
   const float* bias;
   const float* res;
   int64_t rBatchStride;
   float* out;
   int64_t outBatchStride;
-  int64_t F, N, K;
-  int C, H, W, OW, OHW;
-  int sY, sX, pH, pW;
+  int64_t F;
   int act;
   int tilesM, tilesN;
 };
@@ -36,91 +49,79 @@ __device__ inline float apply_act(float v, int act) {
   return v;
 }
 
-template <class Cfg, int KH, int KW, bool VA>
-__global__ __launch_bounds__(Cfg::NT) void conv_gather_kernel(ConvArgs a) {
-  using AL = DenseLoader<true, VA, Cfg::BM, Cfg::NT>;
-  using BL = ConvGatherLoader<KH, KW, Cfg::BN, Cfg::NT>;
-  using Main = GemmMainloop<Cfg, AL, BL>;
-  __shared__ __attribute__((aligned(16))) float lds[Main::LDS_FLOATS];
+enum Mode { kGatherRef3 = 0, kGatherTap3 = 1, kGatherRef1 = 2, kTap3 = 3, k1x1 = 4 };
 
-  int tm, tn;
-  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
-
-  AL al;
-  al.base = a.w;
-  al.ld = a.K;
-  al.rows = a.F;
-  al.K = a.K;
-  BL bl;
-  bl.x = a.x;
-  bl.xBatchStride = a.xBatchStride;
-  bl.H = a.H; bl.W = a.W; bl.OW = a.OW; bl.OHW = a.OHW;
-  bl.sY = a.sY; bl.sX = a.sX; bl.pH = a.pH; bl.pW = a.pW;
-  bl.N = a.N; bl.K = a.K;
-  bl.init_col(n0, threadIdx.x);
-
-  f32x16 acc[Cfg::FM][Cfg::FN];
-  Main::run(al, bl, m0, n0, 0, a.K, lds, acc);
-
-  Main::for_each(acc, [&](int row, int col, float v) {
-    const int64_t f = m0 + row, n = n0 + col;
-    if (f < a.F && n < a.N) {
-      const int64_t b = n / a.OHW, p = n - b * a.OHW;
-      if (a.bias) v = v + a.bias[f];
-      v = apply_act(v, a.act);
-      if (a.res) v = v + a.res[b * a.rBatchStride + f * a.OHW + p];
-      a.out[b * a.outBatchStride + f * a.OHW + p] = v;
-    }
-  });
-}
+template <class Cfg, int MODE, bool VA, bool VB>
+struct KernelTraits;
 
 template <class Cfg, bool VA, bool VB>
-__global__ __launch_bounds__(Cfg::NT) void conv1x1_kernel(ConvArgs a) {
-  using AL = DenseLoader<true, VA, Cfg::BM, Cfg::NT>;
-  using BL = Conv1x1Loader<VB, Cfg::BN, Cfg::NT>;
+struct KernelTraits<Cfg, kGatherRef3, VA, VB> { using BL = ConvGatherLoader<3, 3, Cfg::BN, Cfg::BK, Cfg::NT>; };
+template <class Cfg, bool VA, bool VB>
+struct KernelTraits<Cfg, kGatherRef1, VA, VB> { using BL = ConvGatherLoader<1, 1, Cfg::BN, Cfg::BK, Cfg::NT>; };
+template <class Cfg, bool VA, bool VB>
+struct KernelTraits<Cfg, kTap3, VA, VB> { using BL = ConvTapLoader<3, Cfg::BN, Cfg::BK, Cfg::NT>; };
+template <class Cfg, bool VA, bool VB>
+struct KernelTraits<Cfg, k1x1, VA, VB> { using BL = Conv1x1Loader<VB, Cfg::BN, Cfg::BK, Cfg::NT>; };
+template <class Cfg, bool VA, bool VB>
+struct KernelTraits<Cfg, kGatherTap3, VA, VB> { using BL = ConvGatherTapLoader<3, 3, Cfg::BN, Cfg::BK, Cfg::NT>; };
+
+template <class Cfg, int MODE, bool VA, bool VB>
+__global__ __launch_bounds__(Cfg::NT) void conv_kernel(ConvArgs a) {
+  using AL = DenseLoader<true, VA, Cfg::BM, Cfg::BK, Cfg::NT>;
+  using BL = typename KernelTraits<Cfg, MODE, VA, VB>::BL;
   using Main = GemmMainloop<Cfg, AL, BL>;
-  __shared__ __attribute__((aligned(16))) float lds[Main::LDS_FLOATS];
+  __shared__ __attribute__((aligned(16))) float smem[Main::LDS_FLOATS];
+  lds_t* lds = (lds_t*)smem;
 
   int tm, tn;
   tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
 
   AL al;
-  al.base = a.w;
-  al.ld = a.K;
-  al.rows = a.F;
-  al.K = a.K;
+  al.init(a.w, a.wBytes, a.g.K, a.F, a.g.K);
   BL bl;
-  bl.x = a.x;
-  bl.xBatchStride = a.xBatchStride;
-  bl.HW = a.OHW;
-  bl.N = a.N;
-  bl.K = a.K;
-  bl.init_col(n0, threadIdx.x);
+  bl.init(a.g, n0, threadIdx.x);
 
   f32x16 acc[Cfg::FM][Cfg::FN];
-  Main::run(al, bl, m0, n0, 0, a.K, lds, acc);
+  Main::run(al, bl, m0, n0, 0, a.g.K, lds, acc);
 
+  const int64_t OHW = a.g.OHW;
   Main::for_each(acc, [&](int row, int col, float v) {
     const int64_t f = m0 + row, n = n0 + col;
-    if (f < a.F && n < a.N) {
-      const int64_t b = n / a.OHW, p = n - b * a.OHW;
+    if (f < a.F && n < a.g.N) {
+      const int64_t b = n / OHW, p = n - b * OHW;
       if (a.bias) v = v + a.bias[f];
       v = apply_act(v, a.act);
-      if (a.res) v = v + a.res[b * a.rBatchStride + f * a.OHW + p];
-      a.out[b * a.outBatchStride + f * a.OHW + p] = v;
+      if (a.res) v = v + a.res[b * a.rBatchStride + f * OHW + p];
+      a.out[b * a.outBatchStride + f * OHW + p] = v;
     }
   });
 }
 
-using Cfg128 = TileCfg<128, 128, 2, 2>;
-using Cfg64 = TileCfg<64, 64, 2, 2>;
-using Cfg64x128 = TileCfg<64, 128, 2, 2>;
+// ---------------------------------------------------------------------------
+// tile configurations
+// ---------------------------------------------------------------------------
+using C128k16 = TileCfg<128, 128, 16, 2, 2>;
+using C128k32 = TileCfg<128, 128, 32, 2, 2>;
+using C256k16 = TileCfg<256, 128, 16, 4, 2>;
+using C128x64 = TileCfg<128, 64, 32, 2, 2>;
+using C64x128 = TileCfg<64, 128, 32, 2, 2>;
+using C64x64 = TileCfg<64, 64, 32, 2, 2>;
+
+struct CfgInfo {
+  int BM, BN, BK;
+  float eff;  // relative per-CU throughput used by the cost model
+  int perCU;  // resident workgroups per CU assumed by the cost model
+};
+constexpr int kNumCfg = 6;
+const CfgInfo kCfgs[kNumCfg] = {
+    {128, 128, 16, 1.00f, 2}, {128, 128, 32, 1.00f, 2}, {256, 128, 16, 1.05f, 1},
+    {128, 64, 32, 0.90f, 3},  {64, 128, 32, 0.90f, 3},  {64, 64, 32, 0.70f, 4},
+};
 
 template <class Cfg>
 int grid_for(ConvArgs& a, dim3& grid) {
-  const int64_t tm = (a.F + Cfg::BM - 1) / Cfg::BM, tn = (a.N + Cfg::BN - 1) / Cfg::BN;
+  const int64_t tm = (a.F + Cfg::BM - 1) / Cfg::BM, tn = (a.g.N + Cfg::BN - 1) / Cfg::BN;
   if (tm * tn > INT32_MAX) return fail(TNH_ERR_UNSUPPORTED, "conv2d: grid too large");
   a.tilesM = static_cast<int>(tm);
   a.tilesN = static_cast<int>(tn);
@@ -128,44 +129,106 @@ int grid_for(ConvArgs& a, dim3& grid) {
   return TNH_OK;
 }
 
-template <class Cfg, int KH, int KW>
-int launch_gather(ConvArgs a, bool va, hipStream_t s) {
+template <class Cfg, int MODE>
+int launch_mode(ConvArgs a, bool va, bool vb, hipStream_t s) {
   dim3 grid;
   if (int st = grid_for<Cfg>(a, grid)) return st;
-  if (va)
-    hipLaunchKernelGGL((conv_gather_kernel<Cfg, KH, KW, true>), grid, dim3(Cfg::NT), 0, s, a);
-  else
-    hipLaunchKernelGGL((conv_gather_kernel<Cfg, KH, KW, false>), grid, dim3(Cfg::NT), 0, s, a);
-  return launch_status("conv_gather_kernel");
+  if constexpr (MODE == k1x1) {
+    if (va && vb)
+      hipLaunchKernelGGL((conv_kernel<Cfg, MODE, true, true>), grid, dim3(Cfg::NT), 0, s, a);
+    else if (va)
+      hipLaunchKernelGGL((conv_kernel<Cfg, MODE, true, false>), grid, dim3(Cfg::NT), 0, s, a);
+    else if (vb)
+      hipLaunchKernelGGL((conv_kernel<Cfg, MODE, false, true>), grid, dim3(Cfg::NT), 0, s, a);
+    else
+      hipLaunchKernelGGL((conv_kernel<Cfg, MODE, false, false>), grid, dim3(Cfg::NT), 0, s, a);
+  } else if constexpr (MODE == kTap3) {
+    hipLaunchKernelGGL((conv_kernel<Cfg, MODE, true, false>), grid, dim3(Cfg::NT), 0, s, a);
+  } else {
+    (void)va;
+    (void)vb;
+    hipLaunchKernelGGL((conv_kernel<Cfg, MODE, false, false>), grid, dim3(Cfg::NT), 0, s, a);
+  }
+  return launch_status("conv_kernel");
 }
 
 template <class Cfg>
-int launch_1x1(ConvArgs a, bool va, bool vb, hipStream_t s) {
-  dim3 grid;
-  if (int st = grid_for<Cfg>(a, grid)) return st;
-  if (va && vb)
-    hipLaunchKernelGGL((conv1x1_kernel<Cfg, true, true>), grid, dim3(Cfg::NT), 0, s, a);
-  else if (va)
-    hipLaunchKernelGGL((conv1x1_kernel<Cfg, true, false>), grid, dim3(Cfg::NT), 0, s, a);
-  else if (vb)
-    hipLaunchKernelGGL((conv1x1_kernel<Cfg, false, true>), grid, dim3(Cfg::NT), 0, s, a);
-  else
-    hipLaunchKernelGGL((conv1x1_kernel<Cfg, false, false>), grid, dim3(Cfg::NT), 0, s, a);
-  return launch_status("conv1x1_kernel");
+int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
+  switch (mode) {
+    case kGatherRef3: return launch_mode<Cfg, kGatherRef3>(a, va, vb, s);
+    case kGatherTap3: return launch_mode<Cfg, kGatherTap3>(a, va, vb, s);
+    case kGatherRef1: return launch_mode<Cfg, kGatherRef1>(a, va, vb, s);
+    case kTap3: return launch_mode<Cfg, kTap3>(a, va, vb, s);
+    default: return launch_mode<Cfg, k1x1>(a, va, vb, s);
+  }
 }
 
-template <class Cfg>
-int launch_any(const ConvArgs& a, int k, bool is1x1, bool va, bool vb, hipStream_t s) {
-  if (is1x1) return launch_1x1<Cfg>(a, va, vb, s);
-  if (k == 3) return launch_gather<Cfg, 3, 3>(a, va, s);
-  if (k == 1) return launch_gather<Cfg, 1, 1>(a, va, s);
-  return fail(TNH_ERR_UNSUPPORTED, "conv2d: kernel size %d not supported (1 or 3)", k);
+int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
+  switch (cfg) {
+    case 0: return launch_cfg<C128k16>(a, mode, va, vb, s);
+    case 1: return launch_cfg<C128k32>(a, mode, va, vb, s);
+    case 2: return launch_cfg<C256k16>(a, mode, va, vb, s);
+    case 3: return launch_cfg<C128x64>(a, mode, va, vb, s);
+    case 4: return launch_cfg<C64x128>(a, mode, va, vb, s);
+    default: return launch_cfg<C64x64>(a, mode, va, vb, s);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// [F][C][taps] -> [F][taps][C]
+__global__ void pack_weights_kernel(int64_t total, int64_t C, int64_t taps, const float* __restrict__ src,
+                                    float* __restrict__ dst) {
+  for (int64_t o = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; o < total; o += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t c = o % C;
+    const int64_t t = (o / C) % taps;
+    const int64_t f = o / (C * taps);
+    dst[o] = src[(f * C + c) * taps + t];
+  }
+}
+
+// Estimated time (arbitrary units): rounds of resident tiles times the work
+// of one tile, divided by the configuration's relative efficiency.
+float cost(const CfgInfo& c, int64_t F, int64_t N, int64_t K, int cus) {
+  const int64_t tiles = ((F + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN);
+  const int64_t slots = static_cast<int64_t>(cus) * c.perCU;
+  const int64_t rounds = (tiles + slots - 1) / slots;
+  const int64_t kp = (K + c.BK - 1) / c.BK * c.BK;
+  return static_cast<float>(rounds) * c.BM * c.BN * static_cast<float>(kp) / (c.eff * c.perCU);
+}
+
+struct TuneKey {
+  int64_t F, N, K, C, H, W;
+  int k, s, mode, va, vb;
+  bool operator==(const TuneKey& o) const {
+    return F == o.F && N == o.N && K == o.K && C == o.C && H == o.H && W == o.W && k == o.k && s == o.s &&
+           mode == o.mode && va == o.va && vb == o.vb;
+  }
+};
+struct TuneHash {
+  size_t operator()(const TuneKey& t) const {
+    size_t h = 1469598103934665603ull;
+    for (int64_t v : {t.F, t.N, t.K, t.C, t.H, t.W, (int64_t)t.k, (int64_t)t.s, (int64_t)t.mode, (int64_t)t.va,
+                      (int64_t)t.vb})
+      h = (h ^ static_cast<size_t>(v)) * 1099511628211ull;
+    return h;
+  }
+};
+
+std::mutex g_tune_mu;
+std::unordered_map<TuneKey, int, TuneHash> g_tuned;
+bool g_autotune = true;
+int g_forced_cfg = -1;
+
+bool cfg_valid(int c, int mode, int64_t C) {
+  if (mode == kTap3) return C % kCfgs[c].BK == 0;
+  return true;
+}
+
 }  // namespace
 }  // namespace tnh
+
+using namespace tnh;
 
 extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw, int64_t pH, int64_t pW,
                                        int64_t sY, int64_t sX, int64_t* OH, int64_t* OW) {
@@ -176,20 +239,39 @@ extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t
   return TNH_OK;
 }
 
+extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig) {
+  std::lock_guard<std::mutex> lk(g_tune_mu);
+  TNH_ARG(forcedConfig >= -1 && forcedConfig < kNumCfg, "conv2d_set_autotune: config %d", forcedConfig);
+  g_autotune = enable != 0;
+  g_forced_cfg = forcedConfig;
+  if (!g_autotune) g_tuned.clear();
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw, const float* src,
+                                           float* dst) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(F > 0 && C > 0 && kh > 0 && kw > 0 && src && dst && src != dst, "conv2d_pack_weights: bad arguments");
+  const int64_t total = F * C * kh * kw;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(pack_weights_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
+                     cx->stream, total, C, kh * kw, src, dst);
+  return launch_status("pack_weights_kernel");
+}
+
 extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
                                   int64_t kw, int64_t pH, int64_t pW, int64_t sY, int64_t sX, const float* x,
                                   int64_t xOff, int64_t xBatchStride, const float* weights, int64_t wOff,
-                                  const float* bias, int64_t biasOff, int32_t act, const float* residual,
-                                  int64_t rOff, int64_t rBatchStride, float* out, int64_t outOff,
-                                  int64_t outBatchStride, float* workspace, int64_t workspaceBytes) {
-  using namespace tnh;
-  (void)workspace;
-  (void)workspaceBytes;
+                                  int32_t weightLayout, const float* bias, int64_t biasOff, int32_t act,
+                                  const float* residual, int64_t rOff, int64_t rBatchStride, float* out,
+                                  int64_t outOff, int64_t outBatchStride) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0, "conv2d: bad sizes");
   TNH_ARG(kh == kw && (kh == 1 || kh == 3), "conv2d: only square 1x1 / 3x3 kernels are supported");
   TNH_ARG(sY > 0 && sX > 0 && pH >= 0 && pW >= 0, "conv2d: bad stride/pad");
   TNH_ARG(x && weights && out, "conv2d: NULL x/weights/out");
+  TNH_ARG(weightLayout == TNH_WEIGHTS_REFERENCE || weightLayout == TNH_WEIGHTS_TAP_MAJOR,
+          "conv2d: weight layout %d", weightLayout);
   TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "conv2d: activation %d", act);
   TNH_ARG(xOff >= 0 && wOff >= 0 && outOff >= 0 && biasOff >= 0 && rOff >= 0, "conv2d: negative offset");
   const int64_t OH = (H + 2 * pH - kh) / sY + 1, OW = (W + 2 * pW - kw) / sX + 1;
@@ -199,28 +281,88 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   TNH_ARG(!residual || rBatchStride >= F * OH * OW || batch <= 1, "conv2d: rBatchStride too small");
   if (batch == 0) return TNH_OK;
   const int64_t K = C * kh * kw, N = batch * OH * OW;
-  TNH_ARG(K < (int64_t(1) << 30) && H * W < (int64_t(1) << 31) && OH * OW < (int64_t(1) << 31),
-          "conv2d: tensor too large");
+  const int64_t xElems = (batch - 1) * xBatchStride + C * H * W;
+  TNH_ARG(xElems * 4 <= kMaxBufBytes, "conv2d: input spans more than 2 GiB (split the batch)");
+  TNH_ARG(F * K * 4 <= kMaxBufBytes && OH * OW < (int64_t(1) << 31), "conv2d: tensor too large");
 
   ConvArgs a{};
-  a.x = x + xOff;
-  a.xBatchStride = xBatchStride;
+  a.g.x = x + xOff;
+  a.g.xBytes = xElems * 4;
+  a.g.xBatchStride = xBatchStride;
+  a.g.C = (int)C; a.g.H = (int)H; a.g.W = (int)W; a.g.OW = (int)OW; a.g.OHW = (int)(OH * OW);
+  a.g.sY = (int)sY; a.g.sX = (int)sX; a.g.pH = (int)pH; a.g.pW = (int)pW;
+  a.g.N = N; a.g.K = K;
   a.w = weights + wOff;
+  a.wBytes = F * K * 4;
   a.bias = bias ? bias + biasOff : nullptr;
   a.res = residual ? residual + rOff : nullptr;
   a.rBatchStride = rBatchStride;
   a.out = out + outOff;
   a.outBatchStride = outBatchStride;
-  a.F = F; a.N = N; a.K = K;
-  a.C = (int)C; a.H = (int)H; a.W = (int)W; a.OW = (int)OW; a.OHW = (int)(OH * OW);
-  a.sY = (int)sY; a.sX = (int)sX; a.pH = (int)pH; a.pW = (int)pW;
+  a.F = F;
   a.act = act;
 
   const bool is1x1 = kh == 1 && sY == 1 && sX == 1 && pH == 0 && pW == 0;
+  int mode;
+  if (is1x1)
+    mode = k1x1;  // both layouts coincide for 1x1
+  else if (kh == 1)
+    mode = kGatherRef1;
+  else if (weightLayout == TNH_WEIGHTS_TAP_MAJOR)
+    mode = C % 16 == 0 ? kTap3 : kGatherTap3;
+  else
+    mode = kGatherRef3;
   const bool va = aligned16(a.w) && K % 4 == 0;
-  const bool vb = is1x1 && aligned16(a.x) && (OH * OW) % 4 == 0 && (batch == 1 || xBatchStride % 4 == 0);
-  const int64_t tiles128 = ((F + 127) / 128) * ((N + 127) / 128);
-  if (F <= 64) return launch_any<Cfg64x128>(a, (int)kh, is1x1, va, vb, cx->stream);
-  if (tiles128 >= 2 * cx->cu_count) return launch_any<Cfg128>(a, (int)kh, is1x1, va, vb, cx->stream);
-  return launch_any<Cfg64>(a, (int)kh, is1x1, va, vb, cx->stream);
+  const bool vb = is1x1 && aligned16(a.g.x) && (OH * OW) % 4 == 0 && (batch == 1 || xBatchStride % 4 == 0);
+  if (mode == kTap3 && !va) mode = kGatherTap3;
+
+  // pick a configuration
+  std::vector<int> cands;
+  for (int c = 0; c < kNumCfg; ++c)
+    if (cfg_valid(c, mode, C)) cands.push_back(c);
+  int best = cands[0];
+  {
+    float bc = 1e30f;
+    for (int c : cands) {
+      const float v = cost(kCfgs[c], F, N, K, cx->cu_count);
+      if (v < bc) bc = v, best = c;
+    }
+  }
+  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, vb};
+  bool tune = false;
+  const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg, mode, C)) return launch(g_forced_cfg, a, mode, va, vb, cx->stream);
+    auto it = g_tuned.find(key);
+    if (it != g_tuned.end()) return launch(it->second, a, mode, va, vb, cx->stream);
+    if (g_autotune && !aliased) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
+    }
+  }
+  if (tune && cands.size() > 1) {
+    // Time each candidate (the output is rewritten identically by each run:
+    // out never aliases x or residual).
+    hipEvent_t e0, e1;
+    if (int st = hip_status(hipEventCreate(&e0), "hipEventCreate")) return st;
+    if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) return st;
+    float bestMs = 1e30f;
+    for (int c : cands) {
+      if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;  // warm-up
+      (void)hipEventRecord(e0, cx->stream);
+      for (int r = 0; r < 3; ++r)
+        if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;
+      (void)hipEventRecord(e1, cx->stream);
+      (void)hipEventSynchronize(e1);
+      float ms = 0.f;
+      (void)hipEventElapsedTime(&ms, e0, e1);
+      if (ms < bestMs) bestMs = ms, best = c;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tuned[key] = best;
+  }
+  return launch(best, a, mode, va, vb, cx->stream);
 }

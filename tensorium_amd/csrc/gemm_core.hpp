@@ -1,29 +1,36 @@
 // fp32 GEMM core on CDNA4 matrix cores (gfx950), shared by the plain SGEMM
-// entry points and the implicit-GEMM convolution.
+// entry points and the implicit-GEMM convolutions.
 //
-// One workgroup computes a BM x BN tile of C with NWAVES = WM*WN wavefronts;
-// each wave owns a (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks, each
-// accumulated by v_mfma_f32_32x32x2_f32.  Operands stream through LDS in
-// BK = 16 deep panels, double buffered, one barrier per panel; the next
-// panel's global loads are issued before the current panel's MFMAs so that
-// their latency hides behind matrix work.
+// One workgroup computes a BM x BN tile of C with WM x WN wavefronts; each
+// wave owns a (BM/WM) x (BN/WN) sub-tile made of 32x32 blocks, each
+// accumulated by v_mfma_f32_32x32x2_f32.  Operands stream through LDS in BK
+// deep panels (BK a multiple of 16), double buffered with one barrier per
+// panel; the next panel's global loads are issued before the current panel's
+// MFMAs so that their latency hides behind matrix work.
+//
+// Global loads are raw buffer loads: an out-of-range offset (kOOB) reads as
+// 0.0 in hardware, so edge tiles, K tails and convolution padding need no
+// branches.  LDS is addressed through address_space(3) pointers so that the
+// compiler emits ds_read/ds_write (a generic pointer would become flat_*
+// accesses, which share the vector-memory counter with the prefetch and
+// serialize it).
 //
 // MFMA operand layout of v_mfma_f32_32x32x2_f32 (one 32x32x2 block):
 //   A: lane l supplies A[m = l%32][kk = l/32]
 //   B: lane l supplies B[kk = l/32][n = l%32]
 //   D: lane l, register r holds D[m = 8*(r/4) + 4*(l/32) + r%4][n = l%32]
-// Within a BK = 16 panel, MFMA step s (0..7) pairs k = s (lanes 0-31) with
-// k = 8 + s (lanes 32-63), so a lane's eight A values of the panel are 8
-// contiguous k and can be read from a k-contiguous LDS tile with two 16-byte
-// loads.  The sum over k is unchanged; only the fp32 accumulation order
-// differs from the reference's sequential chain (covered by the 1e-5
+// Within each 16-deep chunk of a panel, MFMA step s (0..7) pairs k = s
+// (lanes 0-31) with k = 8 + s (lanes 32-63), so a lane's eight A values of a
+// chunk are 8 contiguous k and come from a k-contiguous LDS tile with two
+// 16-byte reads.  The sum over k is unchanged; only the fp32 accumulation
+// order differs from the reference's sequential chain (covered by the 1e-5
 // per-tensor tolerance; exact for integer-valued data).
 //
 // Operand tiles live in LDS in one of two layouts, chosen so that the
 // global->LDS copy never transposes:
 //   KC ("k contiguous"):   tile[row][BK + 4]   (A normal, B transposed)
 //   MC ("row contiguous"): tile[BK][ROWS + 4]  (A transposed, B normal,
-//                                               implicit im2col gather)
+//                                               implicit im2col gathers)
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -34,69 +41,94 @@ namespace tnh {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) float lds_t;
+typedef __attribute__((address_space(3))) f32x4 lds_f4;
 
-constexpr int kBK = 16;   // panel depth
-constexpr int kPad = 4;   // LDS row padding (floats)
+constexpr int kPad = 4;                 // LDS row padding (floats)
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset beyond every range: reads 0
+constexpr int64_t kMaxBufBytes = 0x7FFFFFF0;  // largest operand a buffer resource spans
 
-template <int BM_, int BN_, int WM_, int WN_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct TileCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
   static constexpr int NWAVES = WM * WN;
   static constexpr int NT = NWAVES * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   static constexpr int FM = WTM / 32, FN = WTN / 32;  // 32x32 blocks per wave
-  static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
+  static constexpr int KCH = BK / 16;                 // 16-deep chunks per panel
+  static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0 && BK % 16 == 0, "tile");
 };
 
-// LDS footprint (floats) of one operand panel in a layout.
-template <bool KC, int ROWS>
+// ---------------------------------------------------------------------------
+// buffer resources
+// ---------------------------------------------------------------------------
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const float* p, int64_t bytes) {
+  const int n = static_cast<int>(bytes < kMaxBufBytes ? bytes : kMaxBufBytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, n, 0x00020000);
+}
+__device__ inline float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ inline f32x4 buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// ---------------------------------------------------------------------------
+// LDS panels
+// ---------------------------------------------------------------------------
+template <bool KC, int ROWS, int BK>
 struct PanelLayout {
-  static constexpr int PITCH = KC ? (kBK + kPad) : (ROWS + kPad);
-  static constexpr int SIZE = KC ? ROWS * PITCH : kBK * PITCH;
+  static constexpr int PITCH = KC ? (BK + kPad) : (ROWS + kPad);
+  static constexpr int SIZE = KC ? ROWS * PITCH : BK * PITCH;
   __device__ static inline int at(int row, int k) { return KC ? row * PITCH + k : k * PITCH + row; }
 };
 
-// Reads the eight per-step operand values of one 32-row block for this lane.
-template <bool KC, int ROWS>
-__device__ inline void read_frag(const float* __restrict__ lds, int row0, int lane, float (&v)[8]) {
-  using L = PanelLayout<KC, ROWS>;
+// The eight per-step operand values of chunk `ch` of one 32-row block.
+template <bool KC, int ROWS, int BK>
+__device__ inline void read_frag(const lds_t* lds, int row0, int ch, int lane, float (&v)[8]) {
+  using L = PanelLayout<KC, ROWS, BK>;
   const int r = lane & 31, h = lane >> 5;
   if constexpr (KC) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(lds + L::at(row0 + r, h * 8));
-    f32x4 a = p[0], b = p[1];
+    const lds_f4* p = reinterpret_cast<const lds_f4*>(lds + L::at(row0 + r, ch * 16 + h * 8));
+    const f32x4 a = p[0], b = p[1];
     v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
     v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
   } else {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) v[s] = lds[L::at(row0 + r, h * 8 + s)];
+    for (int s = 0; s < 8; ++s) v[s] = lds[L::at(row0 + r, ch * 16 + h * 8 + s)];
   }
 }
 
 // ---------------------------------------------------------------------------
-// Dense operand loaders.  Operand element (row, k) of op(X):
+// Dense operand loader.  Operand element (row, k) of op(X):
 //   KC (k contiguous in memory):   X[(row0+row)*ld + k0 + k]
 //   MC (row contiguous in memory): X[(k0+k)*ld + row0 + row]
-// VEC: 16-byte loads (caller guarantees alignment, ld % 4 == 0 and the
+// VEC: 16-byte loads (the host guarantees 16-byte alignment, ld % 4 == 0 and
 // contiguous extent % 4 == 0, so a vector is entirely in or out of range).
 // ---------------------------------------------------------------------------
-template <bool KC, bool VEC, int ROWS, int NT>
+template <bool KC, bool VEC, int ROWS, int BK, int NT>
 struct DenseLoader {
   static constexpr bool kKC = KC;
-  static constexpr int ELEMS = ROWS * kBK;
-  static constexpr int PER = VEC ? ELEMS / 4 / NT : ELEMS / NT;  // loads per thread
-  static_assert(PER >= 1 && (VEC ? ELEMS / 4 : ELEMS) % NT == 0, "loader split");
+  static constexpr int ELEMS = ROWS * BK;
+  static constexpr int UNITS = VEC ? ELEMS / 4 : ELEMS;
+  static constexpr int PER = (UNITS + NT - 1) / NT;  // loads per thread
+  static constexpr bool kPartial = UNITS % NT != 0;
   using Reg = typename std::conditional<VEC, f32x4, float>::type;
 
-  const float* __restrict__ base;  // already offset to the batch item
-  int64_t ld;
-  int64_t rows;  // M (or N) extent
-  int64_t K;
-
+  __amdgpu_buffer_rsrc_t rsrc;
+  int64_t ld, rows, K;
   Reg reg[PER];
+
+  __device__ inline void init(const float* base, int64_t bytes, int64_t ld_, int64_t rows_, int64_t K_) {
+    rsrc = make_rsrc(base, bytes);
+    ld = ld_;
+    rows = rows_;
+    K = K_;
+  }
 
   __device__ inline void coords(int idx, int& row, int& k) const {
     if constexpr (KC) {
-      constexpr int PR = VEC ? kBK / 4 : kBK;  // vectors per row
+      constexpr int PR = VEC ? BK / 4 : BK;
       row = idx / PR;
       k = (idx % PR) * (VEC ? 4 : 1);
     } else {
@@ -109,27 +141,29 @@ struct DenseLoader {
   __device__ inline void load(int64_t row0, int64_t k0, int tid) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
       int row, k;
-      coords(tid + v * NT, row, k);
+      coords(idx, row, k);
       const int64_t gr = row0 + row, gk = k0 + k;
-      const bool ok = gr < rows && gk < K;
-      const int64_t off = KC ? gr * ld + gk : gk * ld + gr;
-      if constexpr (VEC) {
-        reg[v] = ok ? *reinterpret_cast<const f32x4*>(base + off) : f32x4{0.f, 0.f, 0.f, 0.f};
-      } else {
-        reg[v] = ok ? base[off] : 0.f;
-      }
+      const bool ok = gr < rows && gk < K && (!kPartial || idx < UNITS);
+      const uint32_t off = ok ? static_cast<uint32_t>((KC ? gr * ld + gk : gk * ld + gr) * 4) : kOOB;
+      if constexpr (VEC)
+        reg[v] = buf_ld4(rsrc, off);
+      else
+        reg[v] = buf_ld1(rsrc, off);
     }
   }
 
-  __device__ inline void store(float* __restrict__ lds, int tid) const {
-    using L = PanelLayout<KC, ROWS>;
+  __device__ inline void store(lds_t* lds, int tid) const {
+    using L = PanelLayout<KC, ROWS, BK>;
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      if (kPartial && idx >= UNITS) break;
       int row, k;
-      coords(tid + v * NT, row, k);
+      coords(idx, row, k);
       if constexpr (VEC)
-        *reinterpret_cast<f32x4*>(lds + L::at(row, k)) = reg[v];
+        *reinterpret_cast<lds_f4*>(lds + L::at(row, k)) = reg[v];
       else
         lds[L::at(row, k)] = reg[v];
     }
@@ -137,119 +171,187 @@ struct DenseLoader {
 };
 
 // ---------------------------------------------------------------------------
-// Implicit im2col gather for the B operand of a convolution (MC layout).
-// Column n = b*OH*OW + oy*OW + ox (batch merged into N); row k = (c*KH + ky)*KW
-// + kx; value = x_b[c][oy*sY - pH + ky][ox*sX - pW + kx] or 0 (sim2Col's
-// formula, ntensors.pas:11440-11455, dilation 1).  Each thread owns one
-// column for the whole K loop and BK*BN/NT rows of each panel.
+// Convolution B operands (MC layout, batch merged into N):
+//   column n = b*OH*OW + oy*OW + ox
+// Each thread owns one column for the whole K loop and BK*BN/NT rows of each
+// panel (rows myRow0 + v*RSTEP).
 // ---------------------------------------------------------------------------
-template <int KH, int KW, int BN, int NT>
-struct ConvGatherLoader {
-  static constexpr bool kKC = false;
-  static constexpr int RSTEP = NT / BN;       // rows between a thread's loads
-  static constexpr int PER = kBK * BN / NT;   // loads per thread per panel
-  static_assert(NT % BN == 0 && PER >= 1, "gather split");
-
-  const float* __restrict__ x;
-  int64_t xBatchStride;
-  int H, W, OW, OHW;
+struct ConvGeom {
+  const float* x;
+  int64_t xBytes;        // extent of x addressed by the gathers
+  int64_t xBatchStride;  // floats
+  int C, H, W, OW, OHW;
   int sY, sX, pH, pW;
   int64_t N, K;
+};
 
-  // per-thread column state
-  int64_t colBase;  // x offset of image b, row iy0, col ix0 (may be "negative")
+template <int BN, int BK, int NT>
+struct ColumnState {
+  static constexpr int RSTEP = NT / BN;
+  static constexpr int PER = BK * BN / NT;
+  static_assert(NT % BN == 0 && PER >= 1 && BK % RSTEP == 0, "column split");
+  int64_t colOff;  // x offset (floats) of image b at (iy0, ix0); may be negative
   int iy0, ix0;
   bool colOk;
   int myCol, myRow0;
 
-  float reg[PER];
-
-  __device__ inline void init_col(int64_t n0, int tid) {
+  __device__ inline void init_col(const ConvGeom& g, int64_t n0, int tid) {
     myCol = tid % BN;
     myRow0 = tid / BN;
     const int64_t n = n0 + myCol;
-    colOk = n < N;
+    colOk = n < g.N;
     const int64_t nn = colOk ? n : 0;
-    const int64_t b = nn / OHW;
-    const int p = static_cast<int>(nn - b * OHW);
-    const int oy = p / OW, ox = p - (p / OW) * OW;
-    iy0 = oy * sY - pH;
-    ix0 = ox * sX - pW;
-    colBase = b * xBatchStride + static_cast<int64_t>(iy0) * W + ix0;
-  }
-
-  __device__ inline void load(int64_t /*row0*/, int64_t k0, int /*tid*/) {
-    const int64_t HW = static_cast<int64_t>(H) * W;
-#pragma unroll
-    for (int v = 0; v < PER; ++v) {
-      const int k = static_cast<int>(k0) + myRow0 + v * RSTEP;
-      const int c = k / (KH * KW);
-      const int r = k - c * (KH * KW);
-      const int ky = r / KW, kx = r - (r / KW) * KW;
-      const int iy = iy0 + ky, ix = ix0 + kx;
-      const bool ok = colOk && k < static_cast<int>(K) && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
-                      static_cast<unsigned>(ix) < static_cast<unsigned>(W);
-      reg[v] = ok ? x[colBase + c * HW + ky * W + kx] : 0.f;
-    }
-  }
-
-  __device__ inline void store(float* __restrict__ lds, int /*tid*/) const {
-    using L = PanelLayout<false, BN>;
-#pragma unroll
-    for (int v = 0; v < PER; ++v) lds[L::at(myCol, myRow0 + v * RSTEP)] = reg[v];
+    const int64_t b = nn / g.OHW;
+    const int p = static_cast<int>(nn - b * g.OHW);
+    const int oy = p / g.OW, ox = p - (p / g.OW) * g.OW;
+    iy0 = oy * g.sY - g.pH;
+    ix0 = ox * g.sX - g.pW;
+    colOff = b * g.xBatchStride + static_cast<int64_t>(iy0) * g.W + ix0;
   }
 };
 
-// 1x1 stride-1 convolution: B[k = c][n = b*HW + p] = x_b[c][p]; VEC loads 4
-// consecutive columns (requires HW % 4 == 0, xBatchStride % 4 == 0, aligned).
-template <bool VEC, int BN, int NT>
+// General gather, any C.  TAP = false: the reference K order
+// k = (c*KH + ky)*KW + kx (sim2Col, ntensors.pas:11425-11463) for weights as
+// the reference stores them ([F][C][kh][kw]); TAP = true: tap-major order
+// k = (ky*KW + kx)*C + c for packed weights.
+template <int KH, int KW, int BN, int BK, int NT, bool TAP = false>
+struct ConvGatherLoader : ColumnState<BN, BK, NT> {
+  using S = ColumnState<BN, BK, NT>;
+  static constexpr bool kKC = false;
+  __amdgpu_buffer_rsrc_t rsrc;
+  ConvGeom g;
+  float reg[S::PER];
+
+  __device__ inline void init(const ConvGeom& geom, int64_t n0, int tid) {
+    g = geom;
+    rsrc = make_rsrc(g.x, g.xBytes);
+    S::init_col(g, n0, tid);
+  }
+
+  __device__ inline void load(int64_t, int64_t k0, int) {
+    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) {
+      const int k = static_cast<int>(k0) + S::myRow0 + v * S::RSTEP;
+      int c, r;
+      if constexpr (TAP) {
+        r = k / g.C;
+        c = k - r * g.C;
+      } else {
+        c = k / (KH * KW);
+        r = k - c * (KH * KW);
+      }
+      const int ky = r / KW, kx = r - (r / KW) * KW;
+      const int iy = S::iy0 + ky, ix = S::ix0 + kx;
+      const bool ok = S::colOk && k < static_cast<int>(g.K) && static_cast<unsigned>(iy) < static_cast<unsigned>(g.H) &&
+                      static_cast<unsigned>(ix) < static_cast<unsigned>(g.W);
+      const uint32_t off = ok ? static_cast<uint32_t>((S::colOff + c * HW + ky * g.W + kx) * 4) : kOOB;
+      reg[v] = buf_ld1(rsrc, off);
+    }
+  }
+
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<false, BN, BK>;
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) lds[L::at(S::myCol, S::myRow0 + v * S::RSTEP)] = reg[v];
+  }
+};
+
+template <int KH, int KW, int BN, int BK, int NT>
+using ConvGatherTapLoader = ConvGatherLoader<KH, KW, BN, BK, NT, true>;
+
+// Tap-major K order k = (ky*KW + kx)*C + c, weights packed [F][kh][kw][C]
+// (tnh_conv2d_pack_weights).  With C % BK == 0 a panel lies inside one tap,
+// so the tap, its bounds test and the base offset are computed once per
+// panel and each element is one more multiply-add of HW.
+template <int KW, int BN, int BK, int NT>
+struct ConvTapLoader : ColumnState<BN, BK, NT> {
+  using S = ColumnState<BN, BK, NT>;
+  static constexpr bool kKC = false;
+  __amdgpu_buffer_rsrc_t rsrc;
+  ConvGeom g;
+  float reg[S::PER];
+
+  __device__ inline void init(const ConvGeom& geom, int64_t n0, int tid) {
+    g = geom;
+    rsrc = make_rsrc(g.x, g.xBytes);
+    S::init_col(g, n0, tid);
+  }
+
+  __device__ inline void load(int64_t, int64_t k0, int) {
+    const int kk = static_cast<int>(k0);
+    const int tap = kk / g.C;  // uniform over the workgroup
+    const int c0 = kk - tap * g.C;
+    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+    const int iy = S::iy0 + ky, ix = S::ix0 + kx;
+    const bool ok = S::colOk && static_cast<unsigned>(iy) < static_cast<unsigned>(g.H) &&
+                    static_cast<unsigned>(ix) < static_cast<unsigned>(g.W);
+    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
+    const int64_t base = S::colOff + (c0 + S::myRow0) * HW + ky * g.W + kx;
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) {
+      const uint32_t off = ok ? static_cast<uint32_t>((base + v * S::RSTEP * HW) * 4) : kOOB;
+      reg[v] = buf_ld1(rsrc, off);
+    }
+  }
+
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<false, BN, BK>;
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) lds[L::at(S::myCol, S::myRow0 + v * S::RSTEP)] = reg[v];
+  }
+};
+
+// 1x1 stride-1 convolution: B[k = c][n = b*HW + p] = x_b[c][p].  VEC loads 4
+// consecutive columns (HW % 4 == 0, xBatchStride % 4 == 0, x aligned).
+template <bool VEC, int BN, int BK, int NT>
 struct Conv1x1Loader {
   static constexpr bool kKC = false;
-  static constexpr int CPT = VEC ? 4 : 1;              // columns per load
-  static constexpr int TPR = BN / CPT;                 // threads per k row
+  static constexpr int CPT = VEC ? 4 : 1;  // columns per load
+  static constexpr int TPR = BN / CPT;     // threads per k row
   static constexpr int RSTEP = NT / TPR;
-  static constexpr int PER = kBK / RSTEP;
-  static_assert(NT % TPR == 0 && PER >= 1 && kBK % RSTEP == 0, "1x1 split");
+  static constexpr int PER = BK / RSTEP;
+  static_assert(NT % TPR == 0 && PER >= 1 && BK % RSTEP == 0, "1x1 split");
   using Reg = typename std::conditional<VEC, f32x4, float>::type;
 
-  const float* __restrict__ x;
-  int64_t xBatchStride;
-  int64_t HW;
-  int64_t N, K;
-
-  int64_t colBase;
+  __amdgpu_buffer_rsrc_t rsrc;
+  int64_t HW, K;
+  int64_t colOff;
   bool colOk;
   int myCol, myRow0;
   Reg reg[PER];
 
-  __device__ inline void init_col(int64_t n0, int tid) {
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    HW = g.OHW;
+    K = g.K;
     myCol = (tid % TPR) * CPT;
     myRow0 = tid / TPR;
     const int64_t n = n0 + myCol;
-    colOk = n < N;
+    colOk = n < g.N;
     const int64_t nn = colOk ? n : 0;
     const int64_t b = nn / HW;
-    colBase = b * xBatchStride + (nn - b * HW);
+    colOff = b * g.xBatchStride + (nn - b * HW);
   }
 
   __device__ inline void load(int64_t, int64_t k0, int) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int64_t k = k0 + myRow0 + v * RSTEP;
-      const bool ok = colOk && k < K;
+      const uint32_t off = (colOk && k < K) ? static_cast<uint32_t>((colOff + k * HW) * 4) : kOOB;
       if constexpr (VEC)
-        reg[v] = ok ? *reinterpret_cast<const f32x4*>(x + colBase + k * HW) : f32x4{0.f, 0.f, 0.f, 0.f};
+        reg[v] = buf_ld4(rsrc, off);
       else
-        reg[v] = ok ? x[colBase + k * HW] : 0.f;
+        reg[v] = buf_ld1(rsrc, off);
     }
   }
 
-  __device__ inline void store(float* __restrict__ lds, int) const {
-    using L = PanelLayout<false, BN>;
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<false, BN, BK>;
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       if constexpr (VEC)
-        *reinterpret_cast<f32x4*>(lds + L::at(myCol, myRow0 + v * RSTEP)) = reg[v];
+        *reinterpret_cast<lds_f4*>(lds + L::at(myCol, myRow0 + v * RSTEP)) = reg[v];
       else
         lds[L::at(myCol, myRow0 + v * RSTEP)] = reg[v];
     }
@@ -277,23 +379,20 @@ __device__ inline void tile_coords(int pid, int tilesM, int tilesN, int& tm, int
 }
 
 // ---------------------------------------------------------------------------
-// The main loop.  ALoader/BLoader fill LDS panels; Epi receives every
-// accumulated element with its (row, col) in C.
+// The main loop over K panels [kBegin, kEnd) (kBegin a multiple of BK).
 // ---------------------------------------------------------------------------
 template <class Cfg, class AL, class BL>
 struct GemmMainloop {
-  using LA = PanelLayout<AL::kKC, Cfg::BM>;
-  using LB = PanelLayout<BL::kKC, Cfg::BN>;
-  static constexpr int LDS_FLOATS = 2 * (LA::SIZE + LB::SIZE);
+  using LA = PanelLayout<AL::kKC, Cfg::BM, Cfg::BK>;
+  using LB = PanelLayout<BL::kKC, Cfg::BN, Cfg::BK>;
+  static constexpr int STAGE = LA::SIZE + LB::SIZE;
+  static constexpr int LDS_FLOATS = 2 * STAGE;
 
-  // acc[i][j] is the 32x32 block (i, j) of this wave's sub-tile.
-  __device__ static inline void run(AL& al, BL& bl, int64_t m0, int64_t n0, int64_t kBegin, int64_t kEnd,
-                                    float* lds, f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+  __device__ static inline void run(AL& al, BL& bl, int64_t m0, int64_t n0, int64_t kBegin, int64_t kEnd, lds_t* lds,
+                                    f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-    float* ldsA[2] = {lds, lds + LA::SIZE + LB::SIZE};
-    float* ldsB[2] = {lds + LA::SIZE, lds + 2 * LA::SIZE + LB::SIZE};
 
 #pragma unroll
     for (int i = 0; i < Cfg::FM; ++i)
@@ -302,38 +401,42 @@ struct GemmMainloop {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int64_t nk = (kEnd - kBegin + kBK - 1) / kBK;
+    const int64_t nk = (kEnd - kBegin + Cfg::BK - 1) / Cfg::BK;
     if (nk <= 0) return;
     al.load(m0, kBegin, tid);
     bl.load(n0, kBegin, tid);
-    al.store(ldsA[0], tid);
-    bl.store(ldsB[0], tid);
+    al.store(lds, tid);
+    bl.store(lds + LA::SIZE, tid);
     __syncthreads();
 
     for (int64_t kt = 0; kt < nk; ++kt) {
-      const int cur = static_cast<int>(kt & 1);
+      lds_t* cur = lds + (kt & 1) * STAGE;
+      lds_t* nxt = lds + ((kt + 1) & 1) * STAGE;
       const bool more = kt + 1 < nk;
       if (more) {
-        al.load(m0, kBegin + (kt + 1) * kBK, tid);
-        bl.load(n0, kBegin + (kt + 1) * kBK, tid);
+        al.load(m0, kBegin + (kt + 1) * Cfg::BK, tid);
+        bl.load(n0, kBegin + (kt + 1) * Cfg::BK, tid);
       }
-      float a[Cfg::FM][8], b[Cfg::FN][8];
 #pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-        read_frag<AL::kKC, Cfg::BM>(ldsA[cur], wm * Cfg::WTM + i * 32, lane, a[i]);
-#pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j)
-        read_frag<BL::kKC, Cfg::BN>(ldsB[cur], wn * Cfg::WTN + j * 32, lane, b[j]);
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
+      for (int ch = 0; ch < Cfg::KCH; ++ch) {
+        float a[Cfg::FM][8], b[Cfg::FN][8];
 #pragma unroll
         for (int i = 0; i < Cfg::FM; ++i)
+          read_frag<AL::kKC, Cfg::BM, Cfg::BK>(cur, wm * Cfg::WTM + i * 32, ch, lane, a[i]);
 #pragma unroll
-          for (int j = 0; j < Cfg::FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < Cfg::FN; ++j)
+          read_frag<BL::kKC, Cfg::BN, Cfg::BK>(cur + LA::SIZE, wn * Cfg::WTN + j * 32, ch, lane, b[j]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+      }
       if (more) {
-        al.store(ldsA[cur ^ 1], tid);
-        bl.store(ldsB[cur ^ 1], tid);
+        al.store(nxt, tid);
+        bl.store(nxt + LA::SIZE, tid);
       }
       __syncthreads();
     }

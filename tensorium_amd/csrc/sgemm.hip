@@ -14,16 +14,18 @@ struct SgemmArgs {
   float* C;
   int64_t M, N, K, lda, ldb, ldc;
   int64_t strideA, strideB, strideC;
+  int64_t aBytes, bBytes;  // extent of one batch item of A / B
   float alpha, beta;
   int tilesM, tilesN;
 };
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__(Cfg::NT) void sgemm_kernel(SgemmArgs a) {
-  using AL = DenseLoader<!TA, VA, Cfg::BM, Cfg::NT>;
-  using BL = DenseLoader<TB, VB, Cfg::BN, Cfg::NT>;
+  using AL = DenseLoader<!TA, VA, Cfg::BM, Cfg::BK, Cfg::NT>;
+  using BL = DenseLoader<TB, VB, Cfg::BN, Cfg::BK, Cfg::NT>;
   using Main = GemmMainloop<Cfg, AL, BL>;
-  __shared__ __attribute__((aligned(16))) float lds[Main::LDS_FLOATS];
+  __shared__ __attribute__((aligned(16))) float smem[Main::LDS_FLOATS];
+  lds_t* lds = (lds_t*)smem;
 
   const int64_t bz = blockIdx.y;
   int tm, tn;
@@ -31,15 +33,9 @@ __global__ __launch_bounds__(Cfg::NT) void sgemm_kernel(SgemmArgs a) {
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
 
   AL al;
-  al.base = a.A + bz * a.strideA;
-  al.ld = a.lda;
-  al.rows = a.M;
-  al.K = a.K;
+  al.init(a.A + bz * a.strideA, a.aBytes, a.lda, a.M, a.K);
   BL bl;
-  bl.base = a.B + bz * a.strideB;
-  bl.ld = a.ldb;
-  bl.rows = a.N;
-  bl.K = a.K;
+  bl.init(a.B + bz * a.strideB, a.bBytes, a.ldb, a.N, a.K);
 
   f32x16 acc[Cfg::FM][Cfg::FN];
   Main::run(al, bl, m0, n0, 0, a.K, lds, acc);
@@ -57,8 +53,8 @@ __global__ __launch_bounds__(Cfg::NT) void sgemm_kernel(SgemmArgs a) {
   });
 }
 
-using Cfg128 = TileCfg<128, 128, 2, 2>;
-using Cfg64 = TileCfg<64, 64, 2, 2>;
+using Cfg128 = TileCfg<128, 128, 16, 2, 2>;
+using Cfg64 = TileCfg<64, 64, 16, 2, 2>;
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 int launch_one(const SgemmArgs& a0, int64_t batch, hipStream_t s) {
@@ -115,6 +111,11 @@ int sgemm_impl(int32_t transA, int32_t transB, int64_t M, int64_t N, int64_t K, 
   TNH_ARG(aOff >= 0 && bOff >= 0 && cOff >= 0, "sgemm: negative offset");
   TNH_ARG(strideA >= 0 && strideB >= 0 && strideC >= 0, "sgemm: negative stride");
   TNH_ARG(K < (int64_t(1) << 31), "sgemm: K too large");
+  // operand extents as addressed by the kernel (one batch item)
+  const int64_t aElems = K == 0 ? 0 : (ta ? (K - 1) * lda + M : (M - 1) * lda + K);
+  const int64_t bElems = K == 0 ? 0 : (tb ? (N - 1) * ldb + K : (K - 1) * ldb + N);
+  TNH_ARG(aElems * 4 <= kMaxBufBytes && bElems * 4 <= kMaxBufBytes,
+          "sgemm: an operand spans more than 2 GiB (split the call)");
 
   SgemmArgs a{};
   a.A = A ? A + aOff : nullptr;
@@ -123,6 +124,8 @@ int sgemm_impl(int32_t transA, int32_t transB, int64_t M, int64_t N, int64_t K, 
   a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
   a.strideA = strideA; a.strideB = strideB; a.strideC = strideC;
   a.alpha = alpha; a.beta = beta;
+  a.aBytes = aElems * 4;
+  a.bBytes = bElems * 4;
   // A operand: contiguous along k when not transposed, along m when transposed.
   const bool va = K > 0 && vec_ok(a.A, lda, ta ? M : K, strideA, batch);
   const bool vb = K > 0 && vec_ok(a.B, ldb, tb ? K : N, strideB, batch);

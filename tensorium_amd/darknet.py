@@ -25,7 +25,7 @@ import os
 import numpy as np
 
 from . import synth
-from .nnhip import acLEAKY, acLINEAR, acLOGISTIC
+from .nnhip import WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR, acLOGISTIC
 
 CFG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cfg")
 _ACT = {"leaky": acLEAKY, "linear": acLINEAR, "logistic": acLOGISTIC}
@@ -156,7 +156,7 @@ def consumers(layers):
 class Network:
     """Inference runner over the C ABI; buffers are device torch tensors."""
 
-    def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image"):
+    def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True):
         import torch
 
         self.hip, self.layers, self.batch = hip, layers, batch
@@ -170,10 +170,20 @@ class Network:
                 if (L["type"] == "convolutional" and i + 1 < len(layers) and layers[i + 1]["type"] == "shortcut"
                         and layers[i + 1]["act"] == acLINEAR and use[i] == [i + 1] and layers[i + 1]["src"] != i):
                     self.fused.add(i)
+        # Weights go to HBM once; 3x3 filters are repacked tap-major
+        # ([F][ky][kx][C]) on the device, the layout of the fast conv path.
         self.w = {}
         for i, (w, b) in weights.items():
-            self.w[i] = (torch.from_numpy(np.ascontiguousarray(w)).to(device),
-                         torch.from_numpy(np.ascontiguousarray(b)).to(device))
+            L = layers[i]
+            dw = torch.from_numpy(np.ascontiguousarray(w)).to(device)
+            layout = WEIGHTS_REFERENCE
+            if pack and L["size"] > 1:
+                packed = torch.empty_like(dw)
+                torch.cuda.synchronize()
+                hip.packConvWeights(L["filters"], L["in"][0], L["size"], dw, packed)
+                hip.finish()
+                dw, layout = packed, WEIGHTS_TAP_MAJOR
+            self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), layout)
         self.out = [None] * len(layers)
         for L in layers:
             i = L["index"]
@@ -215,7 +225,7 @@ class Network:
         hip, B = self.hip, self.batch
         i, t = L["index"], L["type"]
         if t == "convolutional":
-            w, b = self.w[i]
+            w, b, layout = self.w[i]
             C, h, ww = L["in"]
             res = None
             if i in self.fused:
@@ -225,7 +235,7 @@ class Network:
             else:
                 dst = self.out[i]
             hip.conv2dForward(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], prev, 0, w, b,
-                              L["act"], dst, 0, residual=res)
+                              L["act"], dst, 0, residual=res, weightLayout=layout)
             prev = dst
         elif t == "shortcut":
             if i - 1 not in self.fused:

@@ -27,6 +27,8 @@ LIB_PATH = os.path.join(_HERE, "libtensorium_hip.so")
 
 # TActivationType ordinals (ntypes.pas:66)
 acLOGISTIC, acLINEAR, acLEAKY = 0, 4, 9
+# conv weight layouts
+WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -56,7 +58,9 @@ _PROTOS = {
     "tnh_im2col_batched": [i64] * 11 + [vp, i64, i64, vp, i64, i64, i64],
     "tnh_col2im": [i64] * 11 + [vp, i64, vp, i64],
     "tnh_col2im_batched": [i64] * 11 + [vp, i64, i64, vp, i64, i64, i64],
-    "tnh_conv2d_fwd": [i64] * 11 + [vp, i64, i64, vp, i64, vp, i64, i32, vp, i64, i64, vp, i64, i64, vp, i64],
+    "tnh_conv2d_fwd": [i64] * 11 + [vp, i64, i64, vp, i64, i32, vp, i64, i32, vp, i64, i64, vp, i64, i64],
+    "tnh_conv2d_pack_weights": [i64, i64, i64, i64, vp, vp],
+    "tnh_conv2d_set_autotune": [i32, i32],
     "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
     "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
     "tnh_forward_scale": [i64, vp, i64, i64, vp, i64, i64],
@@ -258,16 +262,24 @@ class TNNHip:
     # -- fused convolution (new: replaces im2col+gemm+bias+activate) ---------
     def conv2dForward(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
                       biases, activation, output, outOffset, inBatchStride=None, outBatchStride=None,
-                      residual=None, resOffset=0, resBatchStride=None, workspace=None, workspaceBytes=0):
+                      residual=None, resOffset=0, resBatchStride=None, weightLayout=WEIGHTS_REFERENCE):
+        """Fused conv + bias + activation (+ shortcut add); returns (outH, outW)."""
         oh = (h + 2 * padding - kernelSize) // stride + 1
         ow = (w + 2 * padding - kernelSize) // stride + 1
         xs = c * h * w if inBatchStride is None else inBatchStride
         os_ = filters * oh * ow if outBatchStride is None else outBatchStride
         rs = filters * oh * ow if resBatchStride is None else resBatchStride
         call("tnh_conv2d_fwd", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
-             addr(input), inOffset, xs, addr(weights), 0, addr(biases), 0, activation, addr(residual), resOffset,
-             rs, addr(output), outOffset, os_, addr(workspace), workspaceBytes)
+             addr(input), inOffset, xs, addr(weights), 0, weightLayout, addr(biases), 0, activation, addr(residual),
+             resOffset, rs, addr(output), outOffset, os_)
         return oh, ow
+
+    def packConvWeights(self, filters, c, kernelSize, src, dst):
+        """[F][C][k][k] -> tap-major [F][k][k][C] (device to device)."""
+        call("tnh_conv2d_pack_weights", filters, c, kernelSize, kernelSize, addr(src), addr(dst))
+
+    def setConvAutotune(self, enable=True, forcedConfig=-1):
+        call("tnh_conv2d_set_autotune", 1 if enable else 0, forcedConfig)
 
     # -- epilogue / element-wise ---------------------------------------------
     def forwardBias(self, dstSize, dst, offset, srcSize, src, incb, batch):

