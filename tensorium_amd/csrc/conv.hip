@@ -19,6 +19,8 @@
 // shape times the valid candidates with HIP events (when autotuning is on
 // and the stream is not being captured) and caches the fastest; otherwise a
 // wave-quantization cost model picks one.
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -363,6 +365,11 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     (void)hipEventDestroy(e1);
     std::lock_guard<std::mutex> lk(g_tune_mu);
     g_tuned[key] = best;
+    static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
+    if (verbose)
+      std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) %.4f ms\n",
+                   (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best,
+                   kCfgs[best].BM, kCfgs[best].BN, kCfgs[best].BK, bestMs / 3);
   }
   return launch(best, a, mode, va, vb, cx->stream);
 }
