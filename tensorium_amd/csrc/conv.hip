@@ -68,7 +68,7 @@ template <class Cfg, bool VA, bool VB>
 struct KernelTraits<Cfg, kGatherTap3, VA, VB> { using BL = ConvGatherTapLoader<3, 3, Cfg::BN, Cfg::BK, Cfg::NT>; };
 
 template <class Cfg, int MODE, bool VA, bool VB>
-__global__ __launch_bounds__(Cfg::NT) void conv_kernel(ConvArgs a) {
+__global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
   using AL = DenseLoader<true, VA, Cfg::BM, Cfg::BK, Cfg::NT>;
   using BL = typename KernelTraits<Cfg, MODE, VA, VB>::BL;
   using Main = GemmMainloop<Cfg, AL, BL>;
@@ -80,35 +80,52 @@ __global__ __launch_bounds__(Cfg::NT) void conv_kernel(ConvArgs a) {
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
 
   AL al;
-  al.init(a.w, a.wBytes, a.g.K, a.F, a.g.K);
+  al.init(a.w, a.wBytes, a.g.K, a.F, a.g.K, m0, threadIdx.x);
   BL bl;
   bl.init(a.g, n0, threadIdx.x);
 
   f32x16 acc[Cfg::FM][Cfg::FN];
-  Main::run(al, bl, m0, n0, 0, a.g.K, lds, acc);
+  Main::exec(al, bl, 0, a.g.K, lds, acc);
 
+  // Epilogue: each lane owns FN output columns; their image / pixel split is
+  // computed once per column.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int64_t OHW = a.g.OHW;
-  Main::for_each(acc, [&](int row, int col, float v) {
-    const int64_t f = m0 + row, n = n0 + col;
-    if (f < a.F && n < a.g.N) {
-      const int64_t b = n / OHW, p = n - b * OHW;
-      if (a.bias) v = v + a.bias[f];
-      v = apply_act(v, a.act);
-      if (a.res) v = v + a.res[b * a.rBatchStride + f * OHW + p];
-      a.out[b * a.outBatchStride + f * OHW + p] = v;
-    }
-  });
+#pragma unroll
+  for (int j = 0; j < Cfg::FN; ++j) {
+    const int64_t n = n0 + wn * Cfg::WTN + j * 32 + (lane & 31);
+    if (n >= a.g.N) continue;
+    const int64_t b = n / OHW, p = n - b * OHW;
+    float* out = a.out + b * a.outBatchStride + p;
+    const float* res = a.res ? a.res + b * a.rBatchStride + p : nullptr;
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t f = m0 + wm * Cfg::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (f >= a.F) continue;
+        float v = acc[i][j][r];
+        if (a.bias) v = v + a.bias[f];
+        v = apply_act(v, a.act);
+        if (res) v = v + res[f * OHW];
+        out[f * OHW] = v;
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
 // tile configurations
 // ---------------------------------------------------------------------------
-using C128k16 = TileCfg<128, 128, 16, 2, 2>;
-using C128k32 = TileCfg<128, 128, 32, 2, 2>;
-using C256k16 = TileCfg<256, 128, 16, 4, 2>;
-using C128x64 = TileCfg<128, 64, 32, 2, 2>;
-using C64x128 = TileCfg<64, 128, 32, 2, 2>;
-using C64x64 = TileCfg<64, 64, 32, 2, 2>;
+// (tile M x N x K depth, waves M x N, prefetch depth); chosen from sweeps of
+// the YOLOv3 layer shapes: small tiles with two panels of prefetch keep the
+// most waves resident and win on most shapes.
+using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2, 1>;
+using Cfg1 = TileCfg<64, 64, 16, 2, 2, 2, 8>;
+using Cfg2 = TileCfg<128, 64, 16, 2, 2, 2, 5>;
+using Cfg3 = TileCfg<128, 128, 16, 2, 2, 1, 1>;
+using Cfg4 = TileCfg<64, 128, 32, 2, 2, 2, 1>;
+using Cfg5 = TileCfg<64, 128, 16, 2, 2, 2, 5>;
 
 struct CfgInfo {
   int BM, BN, BK;
@@ -117,8 +134,8 @@ struct CfgInfo {
 };
 constexpr int kNumCfg = 6;
 const CfgInfo kCfgs[kNumCfg] = {
-    {128, 128, 16, 1.00f, 2}, {128, 128, 32, 1.00f, 2}, {256, 128, 16, 1.05f, 1},
-    {128, 64, 32, 0.90f, 3},  {64, 128, 32, 0.90f, 3},  {64, 64, 32, 0.70f, 4},
+    {64, 64, 32, 1.00f, 4},   {64, 64, 16, 1.00f, 8}, {128, 64, 16, 0.97f, 5},
+    {128, 128, 16, 0.95f, 2}, {64, 128, 32, 0.97f, 3}, {64, 128, 16, 0.95f, 5},
 };
 
 template <class Cfg>
@@ -167,12 +184,12 @@ int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
 
 int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
   switch (cfg) {
-    case 0: return launch_cfg<C128k16>(a, mode, va, vb, s);
-    case 1: return launch_cfg<C128k32>(a, mode, va, vb, s);
-    case 2: return launch_cfg<C256k16>(a, mode, va, vb, s);
-    case 3: return launch_cfg<C128x64>(a, mode, va, vb, s);
-    case 4: return launch_cfg<C64x128>(a, mode, va, vb, s);
-    default: return launch_cfg<C64x64>(a, mode, va, vb, s);
+    case 0: return launch_cfg<Cfg0>(a, mode, va, vb, s);
+    case 1: return launch_cfg<Cfg1>(a, mode, va, vb, s);
+    case 2: return launch_cfg<Cfg2>(a, mode, va, vb, s);
+    case 3: return launch_cfg<Cfg3>(a, mode, va, vb, s);
+    case 4: return launch_cfg<Cfg4>(a, mode, va, vb, s);
+    default: return launch_cfg<Cfg5>(a, mode, va, vb, s);
   }
 }
 
@@ -349,17 +366,23 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     hipEvent_t e0, e1;
     if (int st = hip_status(hipEventCreate(&e0), "hipEventCreate")) return st;
     if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) return st;
+    // warm the clocks with the model's choice, then time every candidate
+    // twice (two launches each) and keep its faster run
+    for (int r = 0; r < 3; ++r)
+      if (int st = launch(best, a, mode, va, vb, cx->stream)) return st;
     float bestMs = 1e30f;
     for (int c : cands) {
       if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;  // warm-up
-      (void)hipEventRecord(e0, cx->stream);
-      for (int r = 0; r < 3; ++r)
-        if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;
-      (void)hipEventRecord(e1, cx->stream);
-      (void)hipEventSynchronize(e1);
-      float ms = 0.f;
-      (void)hipEventElapsedTime(&ms, e0, e1);
-      if (ms < bestMs) bestMs = ms, best = c;
+      for (int t = 0; t < 2; ++t) {
+        (void)hipEventRecord(e0, cx->stream);
+        for (int r = 0; r < 2; ++r)
+          if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;
+        (void)hipEventRecord(e1, cx->stream);
+        (void)hipEventSynchronize(e1);
+        float ms = 0.f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        if (ms < bestMs) bestMs = ms, best = c;
+      }
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
@@ -369,7 +392,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     if (verbose)
       std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) %.4f ms\n",
                    (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best,
-                   kCfgs[best].BM, kCfgs[best].BN, kCfgs[best].BK, bestMs / 3);
+                   kCfgs[best].BM, kCfgs[best].BN, kCfgs[best].BK, bestMs / 2);
   }
   return launch(best, a, mode, va, vb, cx->stream);
 }

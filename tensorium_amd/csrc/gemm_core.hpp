@@ -48,9 +48,11 @@ constexpr int kPad = 4;                 // LDS row padding (floats)
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset beyond every range: reads 0
 constexpr int64_t kMaxBufBytes = 0x7FFFFFF0;  // largest operand a buffer resource spans
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int PF_ = 2, int OCC_ = 1>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int PF = PF_;    // prefetch depth in panels (1 or 2)
+  static constexpr int OCC = OCC_;  // minimum waves per SIMD asked of the register allocator
   static constexpr int NWAVES = WM * WN;
   static constexpr int NT = NWAVES * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
@@ -100,12 +102,18 @@ __device__ inline void read_frag(const lds_t* lds, int row0, int ch, int lane, f
 }
 
 // ---------------------------------------------------------------------------
-// Dense operand loader.  Operand element (row, k) of op(X):
-//   KC (k contiguous in memory):   X[(row0+row)*ld + k0 + k]
-//   MC (row contiguous in memory): X[(k0+k)*ld + row0 + row]
+// Operand loaders.  A loader is bound to one tile (init) and then fetches
+// K panels into registers (load(k0)) and writes them to an LDS panel
+// (store).  Offsets are 32-bit byte offsets into a buffer resource whose
+// range is at most 2 GiB; per-element work is one add and one select (an
+// invalid element gets kOOB, which the hardware returns as 0).
+// ---------------------------------------------------------------------------
+
+// Dense operand.  Element (row, k) of op(X):
+//   KC (k contiguous in memory):   X[(row0+row)*ld + k]
+//   MC (row contiguous in memory): X[k*ld + row0 + row]
 // VEC: 16-byte loads (the host guarantees 16-byte alignment, ld % 4 == 0 and
 // contiguous extent % 4 == 0, so a vector is entirely in or out of range).
-// ---------------------------------------------------------------------------
 template <bool KC, bool VEC, int ROWS, int BK, int NT>
 struct DenseLoader {
   static constexpr bool kKC = KC;
@@ -116,17 +124,14 @@ struct DenseLoader {
   using Reg = typename std::conditional<VEC, f32x4, float>::type;
 
   __amdgpu_buffer_rsrc_t rsrc;
-  int64_t ld, rows, K;
+  uint32_t off0[PER];   // byte offset of this thread's element v at k0 = 0
+  uint32_t kStep;       // byte offset per unit of k
+  int kIdx[PER];        // k of element v within the panel
+  bool rowOk[PER];
+  int K;
   Reg reg[PER];
 
-  __device__ inline void init(const float* base, int64_t bytes, int64_t ld_, int64_t rows_, int64_t K_) {
-    rsrc = make_rsrc(base, bytes);
-    ld = ld_;
-    rows = rows_;
-    K = K_;
-  }
-
-  __device__ inline void coords(int idx, int& row, int& k) const {
+  __device__ static inline void coords(int idx, int& row, int& k) {
     if constexpr (KC) {
       constexpr int PR = VEC ? BK / 4 : BK;
       row = idx / PR;
@@ -138,15 +143,29 @@ struct DenseLoader {
     }
   }
 
-  __device__ inline void load(int64_t row0, int64_t k0, int tid) {
+  __device__ inline void init(const float* base, int64_t bytes, int64_t ld, int64_t rows, int64_t K_, int64_t row0,
+                              int tid) {
+    rsrc = make_rsrc(base, bytes);
+    K = static_cast<int>(K_);
+    kStep = KC ? 4u : static_cast<uint32_t>(ld * 4);
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int idx = tid + v * NT;
       int row, k;
       coords(idx, row, k);
-      const int64_t gr = row0 + row, gk = k0 + k;
-      const bool ok = gr < rows && gk < K && (!kPartial || idx < UNITS);
-      const uint32_t off = ok ? static_cast<uint32_t>((KC ? gr * ld + gk : gk * ld + gr) * 4) : kOOB;
+      const int64_t gr = row0 + row;
+      rowOk[v] = gr < rows && (!kPartial || idx < UNITS);
+      kIdx[v] = k;
+      off0[v] = static_cast<uint32_t>(KC ? (gr * ld + k) * 4 : (k * ld + gr) * 4);
+    }
+  }
+
+  __device__ inline void load(int64_t k0) {
+    const uint32_t koff = static_cast<uint32_t>(k0) * kStep;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const bool ok = rowOk[v] && static_cast<int>(k0) + kIdx[v] < K;
+      const uint32_t off = ok ? off0[v] + koff : kOOB;
       if constexpr (VEC)
         reg[v] = buf_ld4(rsrc, off);
       else
@@ -190,7 +209,7 @@ struct ColumnState {
   static constexpr int RSTEP = NT / BN;
   static constexpr int PER = BK * BN / NT;
   static_assert(NT % BN == 0 && PER >= 1 && BK % RSTEP == 0, "column split");
-  int64_t colOff;  // x offset (floats) of image b at (iy0, ix0); may be negative
+  uint32_t colOff;  // byte offset of image b at (iy0, ix0), modulo 2^32 (may wrap)
   int iy0, ix0;
   bool colOk;
   int myCol, myRow0;
@@ -206,7 +225,7 @@ struct ColumnState {
     const int oy = p / g.OW, ox = p - (p / g.OW) * g.OW;
     iy0 = oy * g.sY - g.pH;
     ix0 = ox * g.sX - g.pW;
-    colOff = b * g.xBatchStride + static_cast<int64_t>(iy0) * g.W + ix0;
+    colOff = static_cast<uint32_t>((b * g.xBatchStride + static_cast<int64_t>(iy0) * g.W + ix0) * 4);
   }
 };
 
@@ -219,34 +238,38 @@ struct ConvGatherLoader : ColumnState<BN, BK, NT> {
   using S = ColumnState<BN, BK, NT>;
   static constexpr bool kKC = false;
   __amdgpu_buffer_rsrc_t rsrc;
-  ConvGeom g;
+  int C, H, W, K;
+  uint32_t HW4;
   float reg[S::PER];
 
-  __device__ inline void init(const ConvGeom& geom, int64_t n0, int tid) {
-    g = geom;
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
     rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    H = g.H;
+    W = g.W;
+    K = static_cast<int>(g.K);
+    HW4 = static_cast<uint32_t>(g.H) * static_cast<uint32_t>(g.W) * 4u;
     S::init_col(g, n0, tid);
   }
 
-  __device__ inline void load(int64_t, int64_t k0, int) {
-    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
+  __device__ inline void load(int64_t k0) {
 #pragma unroll
     for (int v = 0; v < S::PER; ++v) {
       const int k = static_cast<int>(k0) + S::myRow0 + v * S::RSTEP;
       int c, r;
       if constexpr (TAP) {
-        r = k / g.C;
-        c = k - r * g.C;
+        r = k / C;
+        c = k - r * C;
       } else {
         c = k / (KH * KW);
         r = k - c * (KH * KW);
       }
       const int ky = r / KW, kx = r - (r / KW) * KW;
       const int iy = S::iy0 + ky, ix = S::ix0 + kx;
-      const bool ok = S::colOk && k < static_cast<int>(g.K) && static_cast<unsigned>(iy) < static_cast<unsigned>(g.H) &&
-                      static_cast<unsigned>(ix) < static_cast<unsigned>(g.W);
-      const uint32_t off = ok ? static_cast<uint32_t>((S::colOff + c * HW + ky * g.W + kx) * 4) : kOOB;
-      reg[v] = buf_ld1(rsrc, off);
+      const bool ok = S::colOk && k < K && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                      static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+      const uint32_t o = S::colOff + static_cast<uint32_t>(c) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
+      reg[v] = buf_ld1(rsrc, ok ? o : kOOB);
     }
   }
 
@@ -263,42 +286,152 @@ using ConvGatherTapLoader = ConvGatherLoader<KH, KW, BN, BK, NT, true>;
 // Tap-major K order k = (ky*KW + kx)*C + c, weights packed [F][kh][kw][C]
 // (tnh_conv2d_pack_weights).  With C % BK == 0 a panel lies inside one tap,
 // so the tap, its bounds test and the base offset are computed once per
-// panel and each element is one more multiply-add of HW.
+// panel and each element is one add.
 template <int KW, int BN, int BK, int NT>
 struct ConvTapLoader : ColumnState<BN, BK, NT> {
   using S = ColumnState<BN, BK, NT>;
   static constexpr bool kKC = false;
   __amdgpu_buffer_rsrc_t rsrc;
-  ConvGeom g;
+  int C, H, W;
+  uint32_t HW4, rowOff, vStride;
   float reg[S::PER];
 
-  __device__ inline void init(const ConvGeom& geom, int64_t n0, int tid) {
-    g = geom;
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
     rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    H = g.H;
+    W = g.W;
+    HW4 = static_cast<uint32_t>(g.H) * static_cast<uint32_t>(g.W) * 4u;
     S::init_col(g, n0, tid);
+    rowOff = S::colOff + static_cast<uint32_t>(S::myRow0) * HW4;
+    vStride = static_cast<uint32_t>(S::RSTEP) * HW4;
   }
 
-  __device__ inline void load(int64_t, int64_t k0, int) {
+  __device__ inline void load(int64_t k0) {
     const int kk = static_cast<int>(k0);
-    const int tap = kk / g.C;  // uniform over the workgroup
-    const int c0 = kk - tap * g.C;
+    const int tap = kk / C;  // uniform over the workgroup
+    const int c0 = kk - tap * C;
     const int ky = tap / KW, kx = tap - (tap / KW) * KW;
     const int iy = S::iy0 + ky, ix = S::ix0 + kx;
-    const bool ok = S::colOk && static_cast<unsigned>(iy) < static_cast<unsigned>(g.H) &&
-                    static_cast<unsigned>(ix) < static_cast<unsigned>(g.W);
-    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
-    const int64_t base = S::colOff + (c0 + S::myRow0) * HW + ky * g.W + kx;
+    const bool ok = S::colOk && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                    static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+    const uint32_t base = rowOff + static_cast<uint32_t>(c0) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
 #pragma unroll
-    for (int v = 0; v < S::PER; ++v) {
-      const uint32_t off = ok ? static_cast<uint32_t>((base + v * S::RSTEP * HW) * 4) : kOOB;
-      reg[v] = buf_ld1(rsrc, off);
-    }
+    for (int v = 0; v < S::PER; ++v) reg[v] = buf_ld1(rsrc, ok ? base + v * vStride : kOOB);
   }
 
   __device__ inline void store(lds_t* lds, int) const {
     using L = PanelLayout<false, BN, BK>;
 #pragma unroll
     for (int v = 0; v < S::PER; ++v) lds[L::at(S::myCol, S::myRow0 + v * S::RSTEP)] = reg[v];
+  }
+};
+
+// Quad-vectorised variants: the B panel is stored k-contiguous (KC,
+// [BN][BK+4], the layout of A) and each thread gathers 4 consecutive k of
+// one column, written with one 16-byte LDS store; fragments are then read
+// with 16-byte LDS reads.  Thread t owns column t % BN and k-quads
+// t / BN + j*(NT/BN).
+template <int BN, int BK, int NT>
+struct QuadColumnState {
+  static constexpr int QSTEP = NT / BN;           // quads between a thread's quads
+  static constexpr int NQ = (BK / 4) / QSTEP;     // quads per thread per panel
+  static_assert(NT % BN == 0 && NQ >= 1 && (BK / 4) % QSTEP == 0, "quad split");
+  int myCol, myQ0;
+};
+
+// tap-major K (packed weights), C % BK == 0
+template <int KW, int BN, int BK, int NT>
+struct ConvTapQuadLoader : ColumnState<BN, BK, NT> {
+  using S = ColumnState<BN, BK, NT>;
+  using Q = QuadColumnState<BN, BK, NT>;
+  static constexpr bool kKC = true;
+  __amdgpu_buffer_rsrc_t rsrc;
+  int C, H, W;
+  uint32_t HW4, qOff, qStride;
+  int myQ0;
+  float reg[Q::NQ][4];
+
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    H = g.H;
+    W = g.W;
+    HW4 = static_cast<uint32_t>(g.H) * static_cast<uint32_t>(g.W) * 4u;
+    S::init_col(g, n0, tid);  // column tid % BN
+    myQ0 = tid / BN;
+    qOff = S::colOff + static_cast<uint32_t>(myQ0 * 4) * HW4;
+    qStride = static_cast<uint32_t>(Q::QSTEP * 4) * HW4;
+  }
+
+  __device__ inline void load(int64_t k0) {
+    const int kk = static_cast<int>(k0);
+    const int tap = kk / C;
+    const int c0 = kk - tap * C;
+    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+    const int iy = S::iy0 + ky, ix = S::ix0 + kx;
+    const bool ok = S::colOk && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                    static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+    const uint32_t base = qOff + static_cast<uint32_t>(c0) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
+#pragma unroll
+    for (int q = 0; q < Q::NQ; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) reg[q][e] = buf_ld1(rsrc, ok ? base + q * qStride + e * HW4 : kOOB);
+  }
+
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<true, BN, BK>;
+#pragma unroll
+    for (int q = 0; q < Q::NQ; ++q)
+      *reinterpret_cast<lds_f4*>(lds + L::at(S::myCol, (myQ0 + q * Q::QSTEP) * 4)) =
+          f32x4{reg[q][0], reg[q][1], reg[q][2], reg[q][3]};
+  }
+};
+
+// 1x1 stride-1: B[k = c][n] with 4 consecutive channels per thread
+template <int BN, int BK, int NT>
+struct Conv1x1QuadLoader {
+  using Q = QuadColumnState<BN, BK, NT>;
+  static constexpr bool kKC = true;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t qOff, HW4, qStride;
+  int K;
+  bool colOk;
+  int myCol, myQ0;
+  float reg[Q::NQ][4];
+
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    const int64_t HW = g.OHW;
+    HW4 = static_cast<uint32_t>(HW) * 4u;
+    K = static_cast<int>(g.K);
+    myCol = tid % BN;
+    myQ0 = tid / BN;
+    const int64_t n = n0 + myCol;
+    colOk = n < g.N;
+    const int64_t nn = colOk ? n : 0;
+    const int64_t b = nn / HW;
+    qOff = static_cast<uint32_t>((b * g.xBatchStride + (nn - b * HW) + static_cast<int64_t>(myQ0 * 4) * HW) * 4);
+    qStride = static_cast<uint32_t>(Q::QSTEP * 4) * HW4;
+  }
+
+  __device__ inline void load(int64_t k0) {
+    const uint32_t base = qOff + static_cast<uint32_t>(k0) * HW4;
+#pragma unroll
+    for (int q = 0; q < Q::NQ; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = colOk && static_cast<int>(k0) + (myQ0 + q * Q::QSTEP) * 4 + e < K;
+        reg[q][e] = buf_ld1(rsrc, ok ? base + q * qStride + e * HW4 : kOOB);
+      }
+  }
+
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<true, BN, BK>;
+#pragma unroll
+    for (int q = 0; q < Q::NQ; ++q)
+      *reinterpret_cast<lds_f4*>(lds + L::at(myCol, (myQ0 + q * Q::QSTEP) * 4)) =
+          f32x4{reg[q][0], reg[q][1], reg[q][2], reg[q][3]};
   }
 };
 
@@ -315,30 +448,32 @@ struct Conv1x1Loader {
   using Reg = typename std::conditional<VEC, f32x4, float>::type;
 
   __amdgpu_buffer_rsrc_t rsrc;
-  int64_t HW, K;
-  int64_t colOff;
+  uint32_t rowOff, HW4;
+  int K;
   bool colOk;
   int myCol, myRow0;
   Reg reg[PER];
 
   __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
     rsrc = make_rsrc(g.x, g.xBytes);
-    HW = g.OHW;
-    K = g.K;
+    const int64_t HW = g.OHW;
+    HW4 = static_cast<uint32_t>(HW) * 4u;
+    K = static_cast<int>(g.K);
     myCol = (tid % TPR) * CPT;
     myRow0 = tid / TPR;
     const int64_t n = n0 + myCol;
     colOk = n < g.N;
     const int64_t nn = colOk ? n : 0;
     const int64_t b = nn / HW;
-    colOff = b * g.xBatchStride + (nn - b * HW);
+    rowOff = static_cast<uint32_t>((b * g.xBatchStride + (nn - b * HW) + static_cast<int64_t>(myRow0) * HW) * 4);
   }
 
-  __device__ inline void load(int64_t, int64_t k0, int) {
+  __device__ inline void load(int64_t k0) {
+    const uint32_t base = rowOff + static_cast<uint32_t>(k0) * HW4;
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
-      const int64_t k = k0 + myRow0 + v * RSTEP;
-      const uint32_t off = (colOk && k < K) ? static_cast<uint32_t>((colOff + k * HW) * 4) : kOOB;
+      const bool ok = colOk && static_cast<int>(k0) + myRow0 + v * RSTEP < K;
+      const uint32_t off = ok ? base + static_cast<uint32_t>(v * RSTEP) * HW4 : kOOB;
       if constexpr (VEC)
         reg[v] = buf_ld4(rsrc, off);
       else
@@ -380,6 +515,7 @@ __device__ inline void tile_coords(int pid, int tilesM, int tilesN, int& tm, int
 
 // ---------------------------------------------------------------------------
 // The main loop over K panels [kBegin, kEnd) (kBegin a multiple of BK).
+// PF = 1: one panel of register prefetch; PF = 2: two (run2).
 // ---------------------------------------------------------------------------
 template <class Cfg, class AL, class BL>
 struct GemmMainloop {
@@ -388,7 +524,20 @@ struct GemmMainloop {
   static constexpr int STAGE = LA::SIZE + LB::SIZE;
   static constexpr int LDS_FLOATS = 2 * STAGE;
 
-  __device__ static inline void run(AL& al, BL& bl, int64_t m0, int64_t n0, int64_t kBegin, int64_t kEnd, lds_t* lds,
+  // Dispatches on the configuration's prefetch depth; al/bl are bound to the
+  // tile (init) already.
+  __device__ static inline void exec(AL& al, BL& bl, int64_t kBegin, int64_t kEnd, lds_t* lds,
+                                     f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+    if constexpr (Cfg::PF == 2) {
+      AL al1 = al;
+      BL bl1 = bl;
+      run2(al, bl, al1, bl1, kBegin, kEnd, lds, acc);
+    } else {
+      run(al, bl, kBegin, kEnd, lds, acc);
+    }
+  }
+
+  __device__ static inline void run(AL& al, BL& bl, int64_t kBegin, int64_t kEnd, lds_t* lds,
                                     f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -403,8 +552,8 @@ struct GemmMainloop {
 
     const int64_t nk = (kEnd - kBegin + Cfg::BK - 1) / Cfg::BK;
     if (nk <= 0) return;
-    al.load(m0, kBegin, tid);
-    bl.load(n0, kBegin, tid);
+    al.load(kBegin);
+    bl.load(kBegin);
     al.store(lds, tid);
     bl.store(lds + LA::SIZE, tid);
     __syncthreads();
@@ -414,8 +563,8 @@ struct GemmMainloop {
       lds_t* nxt = lds + ((kt + 1) & 1) * STAGE;
       const bool more = kt + 1 < nk;
       if (more) {
-        al.load(m0, kBegin + (kt + 1) * Cfg::BK, tid);
-        bl.load(n0, kBegin + (kt + 1) * Cfg::BK, tid);
+        al.load(kBegin + (kt + 1) * Cfg::BK);
+        bl.load(kBegin + (kt + 1) * Cfg::BK);
       }
 #pragma unroll
       for (int ch = 0; ch < Cfg::KCH; ++ch) {
@@ -439,6 +588,72 @@ struct GemmMainloop {
         bl.store(nxt + LA::SIZE, tid);
       }
       __syncthreads();
+    }
+  }
+
+  // Two-deep prefetch: panel kt+2 is loaded into registers while panel kt is
+  // multiplied and panel kt+1 (loaded one iteration earlier) is written to
+  // LDS, so a global load has two iterations of MFMA work to land.  The two
+  // loader copies hold the two register sets; all fragments of a chunk are
+  // read before its MFMAs.
+  __device__ static inline void run2(AL& al0, BL& bl0, AL& al1, BL& bl1, int64_t kBegin, int64_t kEnd, lds_t* lds,
+                                     f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int64_t nk = (kEnd - kBegin + Cfg::BK - 1) / Cfg::BK;
+    if (nk <= 0) return;
+    al0.load(kBegin);
+    bl0.load(kBegin);
+    if (nk > 1) {
+      al1.load(kBegin + Cfg::BK);
+      bl1.load(kBegin + Cfg::BK);
+    }
+    al0.store(lds, tid);
+    bl0.store(lds + LA::SIZE, tid);
+    __syncthreads();
+
+    auto step = [&](int64_t kt, AL& alNext, BL& blNext, AL& alFree, BL& blFree) {
+      lds_t* cur = lds + (kt & 1) * STAGE;
+      lds_t* nxt = lds + ((kt + 1) & 1) * STAGE;
+      if (kt + 2 < nk) {
+        alFree.load(kBegin + (kt + 2) * Cfg::BK);
+        blFree.load(kBegin + (kt + 2) * Cfg::BK);
+      }
+#pragma unroll
+      for (int ch = 0; ch < Cfg::KCH; ++ch) {
+        float a[Cfg::FM][8], b[Cfg::FN][8];
+#pragma unroll
+        for (int i = 0; i < Cfg::FM; ++i)
+          read_frag<AL::kKC, Cfg::BM, Cfg::BK>(cur, wm * Cfg::WTM + i * 32, ch, lane, a[i]);
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+          read_frag<BL::kKC, Cfg::BN, Cfg::BK>(cur + LA::SIZE, wn * Cfg::WTN + j * 32, ch, lane, b[j]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+      }
+      if (kt + 1 < nk) {
+        alNext.store(nxt, tid);
+        blNext.store(nxt + LA::SIZE, tid);
+      }
+      __syncthreads();
+    };
+    for (int64_t kt = 0; kt < nk; kt += 2) {
+      step(kt, al1, bl1, al0, bl0);          // panel kt+1 is in set 1; set 0 is free
+      if (kt + 1 < nk) step(kt + 1, al0, bl0, al1, bl1);
     }
   }
 

@@ -33,12 +33,12 @@ __global__ __launch_bounds__(Cfg::NT) void sgemm_kernel(SgemmArgs a) {
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
 
   AL al;
-  al.init(a.A + bz * a.strideA, a.aBytes, a.lda, a.M, a.K);
+  al.init(a.A + bz * a.strideA, a.aBytes, a.lda, a.M, a.K, m0, threadIdx.x);
   BL bl;
-  bl.init(a.B + bz * a.strideB, a.bBytes, a.ldb, a.N, a.K);
+  bl.init(a.B + bz * a.strideB, a.bBytes, a.ldb, a.N, a.K, n0, threadIdx.x);
 
   f32x16 acc[Cfg::FM][Cfg::FN];
-  Main::run(al, bl, m0, n0, 0, a.K, lds, acc);
+  Main::exec(al, bl, 0, a.K, lds, acc);
 
   float* C = a.C + bz * a.strideC;
   const float alpha = a.alpha, beta = a.beta;
@@ -53,8 +53,8 @@ __global__ __launch_bounds__(Cfg::NT) void sgemm_kernel(SgemmArgs a) {
   });
 }
 
-using Cfg128 = TileCfg<128, 128, 16, 2, 2>;
-using Cfg64 = TileCfg<64, 64, 16, 2, 2>;
+using Cfg128 = TileCfg<128, 128, 16, 2, 2, 1>;
+using Cfg64 = TileCfg<64, 64, 32, 2, 2, 2>;
 
 template <class Cfg, bool TA, bool TB, bool VA, bool VB>
 int launch_one(const SgemmArgs& a0, int64_t batch, hipStream_t s) {
