@@ -41,18 +41,28 @@ def kernel_kind(L, batch):
     return f"conv_kernel<gather{L['size']}x{L['size']}>"
 
 
-def time_forward(hip, net, x, steps, warmup):
+def time_forward(hip, net, x, steps, warmup, graph=True):
+    """Warm-up steps run eagerly (the first one autotunes every layer shape);
+    the forward is then captured into a HIP graph and the timed steps replay
+    it (graph=False times eager launches instead)."""
     import torch
 
     for _ in range(warmup):
         net.forward(x)
     torch.cuda.synchronize()
     hip.finish()
+    if graph:
+        net.capture(x)
+        net.replay()
+        hip.finish()
     e0, e1 = hip.eventCreate(), hip.eventCreate()
     t0 = time.perf_counter()
     hip.eventRecord(e0)
     for _ in range(steps):
-        net.forward(x)
+        if graph:
+            net.replay()
+        else:
+            net.forward(x)
     hip.eventRecord(e1)
     hip.finish()
     torch.cuda.synchronize()
@@ -60,6 +70,9 @@ def time_forward(hip, net, x, steps, warmup):
     ms = hip.eventElapsed(e0, e1)
     hip.eventDestroy(e0)
     hip.eventDestroy(e1)
+    if graph:
+        net.release_graph()
+        hip.useTorchStream()
     return ms, wall
 
 
@@ -130,6 +143,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the YOLOv3 inference path shards by image "
@@ -152,7 +166,7 @@ def main():
         net = darknet.Network(hip, layers, batch, weights)
         x = torch.from_numpy(synth.uniform(7, (batch, 3, args.size, args.size))).cuda()
         torch.cuda.synchronize()
-        ms, wall = time_forward(hip, net, x, steps, warmup)
+        ms, wall = time_forward(hip, net, x, steps, warmup, graph=not args.eager)
         return net, x, ms, wall
 
     net, x, ms, wall = run(args.batch, args.steps, args.warmup)
@@ -196,6 +210,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "launch": "eager" if args.eager else "hip_graph",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

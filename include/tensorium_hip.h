@@ -62,6 +62,15 @@ int32_t tnh_reset_stream(void);
 /* number of compute units of the context device */
 int32_t tnh_cu_count(int32_t *count);
 
+/* ---- HIP graphs (no reference counterpart: the reference launches every
+ *      kernel eagerly).  Capture the context's own stream into an executable
+ *      graph and replay it; kernels recorded this way skip autotuning, so run
+ *      one eager pass first.  The null stream cannot be captured. ---------- */
+int32_t tnh_graph_begin(void);
+int32_t tnh_graph_end(void **graphExec);
+int32_t tnh_graph_launch(void *graphExec);
+int32_t tnh_graph_destroy(void *graphExec);
+
 /* ---- memory (TNNCuda.createDeviceBuffer/freeDeviceBuffer/writeBuffer/
  *      readBuffer, nncuda.pas:488, 493, 512, 499) ----------------------- */
 int32_t tnh_malloc(int64_t bytes, void **ptr);
@@ -160,8 +169,9 @@ int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw,
 int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
                                 const float *src, float *dst);
 /* No reference counterpart: enable (1, default) or disable per-shape
- * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape
- * (0..5), -1 lets the library choose. */
+ * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape:
+ * forcedConfig % 16 is the tile shape (0..5) and forcedConfig / 16 the
+ * split-K factor (0 or 1: none); -1 lets the library choose. */
 int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig);
 
 /* ---- epilogue and element-wise ops ------------------------------------- */

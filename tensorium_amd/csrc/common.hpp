@@ -20,7 +20,14 @@ struct Context {
   hipStream_t stream = nullptr;      // stream kernels are launched on
   int cu_count = 0;
   int xcd_count = 8;
+  void* ws = nullptr;     // library scratch (split-K partial sums), grown on demand
+  size_t wsBytes = 0;
 };
+
+// Returns a scratch buffer of at least `bytes` on the context device, growing
+// it (hipMalloc) when needed; returns nullptr when growing is not possible
+// (allocation failure, or the stream is being captured into a graph).
+void* workspace(Context* c, size_t bytes);
 
 // Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).
 Context* ctx();

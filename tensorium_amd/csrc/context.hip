@@ -38,6 +38,26 @@ Context* ctx() {
   return &g_ctx;
 }
 
+void* workspace(Context* c, size_t bytes) {
+  if (bytes <= c->wsBytes) return c->ws;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  if (c->ws) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->ws);
+    c->ws = nullptr;
+    c->wsBytes = 0;
+  }
+  const size_t want = bytes + (bytes >> 2);
+  if (hipMalloc(&c->ws, want) != hipSuccess) {
+    (void)hipGetLastError();
+    c->ws = nullptr;
+    return nullptr;
+  }
+  c->wsBytes = want;
+  return c->ws;
+}
+
 }  // namespace tnh
 
 using namespace tnh;
@@ -64,7 +84,10 @@ extern "C" int32_t tnh_init(int32_t device) {
   if (g_live) {
     if (g_ctx.device == device) return TNH_OK;
     (void)hipSetDevice(g_ctx.device);
+    (void)hipStreamSynchronize(g_ctx.stream);
+    if (g_ctx.ws) (void)hipFree(g_ctx.ws);
     (void)hipStreamDestroy(g_ctx.own_stream);
+    g_ctx = Context{};
     g_live = false;
   }
   if (int st = hip_status(hipSetDevice(device), "hipSetDevice")) return st;
@@ -85,6 +108,7 @@ extern "C" int32_t tnh_finalize(void) {
   if (!g_live) return TNH_OK;
   (void)hipSetDevice(g_ctx.device);
   (void)hipStreamSynchronize(g_ctx.stream);
+  if (g_ctx.ws) (void)hipFree(g_ctx.ws);
   (void)hipStreamDestroy(g_ctx.own_stream);
   g_ctx = Context{};
   g_live = false;
@@ -185,4 +209,36 @@ extern "C" int32_t tnh_event_elapsed_ms(void* start, void* stop, float* ms) {
   if (int st = hip_status(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize")) return st;
   return hip_status(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
                     "hipEventElapsedTime");
+}
+
+extern "C" int32_t tnh_graph_begin(void) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(cx->stream != nullptr, "graph_begin: the null stream cannot be captured (tnh_reset_stream first)");
+  return hip_status(hipStreamBeginCapture(cx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+
+extern "C" int32_t tnh_graph_end(void** graphExec) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(graphExec != nullptr, "graph_end: NULL");
+  *graphExec = nullptr;
+  hipGraph_t g = nullptr;
+  if (int st = hip_status(hipStreamEndCapture(cx->stream, &g), "hipStreamEndCapture")) return st;
+  hipGraphExec_t ge = nullptr;
+  const int st = hip_status(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+  (void)hipGraphDestroy(g);
+  if (st) return st;
+  *graphExec = ge;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_graph_launch(void* graphExec) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(graphExec != nullptr, "graph_launch: NULL");
+  return hip_status(hipGraphLaunch(static_cast<hipGraphExec_t>(graphExec), cx->stream), "hipGraphLaunch");
+}
+
+extern "C" int32_t tnh_graph_destroy(void* graphExec) {
+  TNH_REQUIRE_CTX(cx);
+  if (!graphExec) return TNH_OK;
+  return hip_status(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graphExec)), "hipGraphExecDestroy");
 }

@@ -43,6 +43,9 @@ struct ConvArgs {
   int64_t F;
   int act;
   int tilesM, tilesN;
+  int splits;       // split-K factor (gridDim.y)
+  int64_t kChunk;   // K range per split (multiple of BK)
+  float* part;      // splits > 1: partial sums [splits][F][N]
 };
 
 __device__ inline float apply_act(float v, int act) {
@@ -85,12 +88,31 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
   bl.init(a.g, n0, threadIdx.x);
 
   f32x16 acc[Cfg::FM][Cfg::FN];
-  Main::exec(al, bl, 0, a.g.K, lds, acc);
+  const int64_t kBegin = blockIdx.y * a.kChunk;
+  const int64_t kEnd = min(a.g.K, kBegin + a.kChunk);
+  Main::exec(al, bl, kBegin, kEnd, lds, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  if (a.splits > 1) {  // raw partial sums; conv_splitk_reduce applies the epilogue
+    float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.F * a.g.N;
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j) {
+      const int64_t n = n0 + wn * Cfg::WTN + j * 32 + (lane & 31);
+      if (n >= a.g.N) continue;
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t f = m0 + wm * Cfg::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (f < a.F) part[f * a.g.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
 
   // Epilogue: each lane owns FN output columns; their image / pixel split is
   // computed once per column.
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int64_t OHW = a.g.OHW;
 #pragma unroll
   for (int j = 0; j < Cfg::FN; ++j) {
@@ -111,6 +133,22 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
         if (res) v = v + res[f * OHW];
         out[f * OHW] = v;
       }
+  }
+}
+
+// Sums the split-K partials in split order (deterministic) and applies the
+// epilogue: one thread per output element, consecutive threads along n.
+__global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
+  const int64_t total = a.F * a.g.N, OHW = a.g.OHW;
+  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t f = e / a.g.N, n = e - f * a.g.N;
+    float v = a.part[e];
+    for (int s = 1; s < a.splits; ++s) v = v + a.part[s * total + e];
+    const int64_t b = n / OHW, p = n - b * OHW;
+    if (a.bias) v = v + a.bias[f];
+    v = apply_act(v, a.act);
+    if (a.res) v = v + a.res[b * a.rBatchStride + f * OHW + p];
+    a.out[b * a.outBatchStride + f * OHW + p] = v;
   }
 }
 
@@ -144,7 +182,14 @@ int grid_for(ConvArgs& a, dim3& grid) {
   if (tm * tn > INT32_MAX) return fail(TNH_ERR_UNSUPPORTED, "conv2d: grid too large");
   a.tilesM = static_cast<int>(tm);
   a.tilesN = static_cast<int>(tn);
-  grid = dim3(static_cast<unsigned>(tm * tn));
+  if (a.splits > 1) {
+    const int64_t panels = (a.g.K + Cfg::BK - 1) / Cfg::BK;
+    a.kChunk = (panels + a.splits - 1) / a.splits * Cfg::BK;
+    a.splits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty split
+  } else {
+    a.kChunk = a.g.K;
+  }
+  grid = dim3(static_cast<unsigned>(tm * tn), static_cast<unsigned>(a.splits));
   return TNH_OK;
 }
 
@@ -168,7 +213,15 @@ int launch_mode(ConvArgs a, bool va, bool vb, hipStream_t s) {
     (void)vb;
     hipLaunchKernelGGL((conv_kernel<Cfg, MODE, false, false>), grid, dim3(Cfg::NT), 0, s, a);
   }
-  return launch_status("conv_kernel");
+  if (int st = launch_status("conv_kernel")) return st;
+  if (a.splits > 1) {
+    const int64_t total = a.F * a.g.N;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
+                       s, a);
+    return launch_status("conv_splitk_reduce");
+  }
+  return TNH_OK;
 }
 
 template <class Cfg>
@@ -206,14 +259,22 @@ __global__ void pack_weights_kernel(int64_t total, int64_t C, int64_t taps, cons
   }
 }
 
+struct Cand {
+  int cfg, splits;
+};
+
 // Estimated time (arbitrary units): rounds of resident tiles times the work
-// of one tile, divided by the configuration's relative efficiency.
-float cost(const CfgInfo& c, int64_t F, int64_t N, int64_t K, int cus) {
-  const int64_t tiles = ((F + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN);
+// of one tile, divided by the configuration's relative efficiency; split-K
+// adds the partial-sum traffic of the reduction.
+float cost(const CfgInfo& c, int64_t F, int64_t N, int64_t K, int cus, int splits) {
+  const int64_t tiles = ((F + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN) * splits;
   const int64_t slots = static_cast<int64_t>(cus) * c.perCU;
   const int64_t rounds = (tiles + slots - 1) / slots;
-  const int64_t kp = (K + c.BK - 1) / c.BK * c.BK;
-  return static_cast<float>(rounds) * c.BM * c.BN * static_cast<float>(kp) / (c.eff * c.perCU);
+  const int64_t kp = ((K + splits - 1) / splits + c.BK - 1) / c.BK * c.BK;
+  const float mm = static_cast<float>(rounds) * c.BM * c.BN * static_cast<float>(kp) / (c.eff * c.perCU);
+  // ~30 FLOP-units per partial float round trip at this model's scale
+  const float red = splits > 1 ? 30.f * static_cast<float>(splits) * F * N / (static_cast<float>(cus) * c.perCU) : 0.f;
+  return mm + red;
 }
 
 struct TuneKey {
@@ -235,7 +296,7 @@ struct TuneHash {
 };
 
 std::mutex g_tune_mu;
-std::unordered_map<TuneKey, int, TuneHash> g_tuned;
+std::unordered_map<TuneKey, Cand, TuneHash> g_tuned;
 bool g_autotune = true;
 int g_forced_cfg = -1;
 
@@ -260,7 +321,8 @@ extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t
 
 extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
-  TNH_ARG(forcedConfig >= -1 && forcedConfig < kNumCfg, "conv2d_set_autotune: config %d", forcedConfig);
+  TNH_ARG(forcedConfig >= -1 && forcedConfig % 16 < kNumCfg && forcedConfig / 16 <= 16,
+          "conv2d_set_autotune: config %d", forcedConfig);
   g_autotune = enable != 0;
   g_forced_cfg = forcedConfig;
   if (!g_autotune) g_tuned.clear();
@@ -335,15 +397,38 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool vb = is1x1 && aligned16(a.g.x) && (OH * OW) % 4 == 0 && (batch == 1 || xBatchStride % 4 == 0);
   if (mode == kTap3 && !va) mode = kGatherTap3;
 
-  // pick a configuration
-  std::vector<int> cands;
-  for (int c = 0; c < kNumCfg; ++c)
-    if (cfg_valid(c, mode, C)) cands.push_back(c);
-  int best = cands[0];
+  // Candidates: every valid tile shape, and for shapes that leave the CUs
+  // under-filled also split-K factors (partial sums in the context
+  // workspace, reduced in fixed order).
+  std::vector<Cand> cands;
+  for (int c = 0; c < kNumCfg; ++c) {
+    if (!cfg_valid(c, mode, C)) continue;
+    cands.push_back({c, 1});
+    const CfgInfo& ci = kCfgs[c];
+    const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
+    if (tiles >= 2 * cx->cu_count) continue;
+    for (int sp : {2, 4, 8, 16})
+      if (tiles * sp <= 8 * cx->cu_count && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp});
+  }
+  auto wsFor = [&](const Cand& c) -> float* {
+    if (c.splits <= 1) return nullptr;
+    return static_cast<float*>(workspace(cx, static_cast<size_t>(c.splits) * F * N * 4));
+  };
+  auto run = [&](const Cand& c) -> int {
+    ConvArgs b = a;
+    b.splits = 1;
+    b.part = nullptr;
+    if (c.splits > 1) {
+      b.part = wsFor(c);
+      if (b.part) b.splits = c.splits;
+    }
+    return launch(c.cfg, b, mode, va, vb, cx->stream);
+  };
+  Cand best = cands[0];
   {
     float bc = 1e30f;
-    for (int c : cands) {
-      const float v = cost(kCfgs[c], F, N, K, cx->cu_count);
+    for (const Cand& c : cands) {
+      const float v = cost(kCfgs[c.cfg], F, N, K, cx->cu_count, c.splits);
       if (v < bc) bc = v, best = c;
     }
   }
@@ -352,9 +437,10 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg, mode, C)) return launch(g_forced_cfg, a, mode, va, vb, cx->stream);
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 16, mode, C))
+      return run({g_forced_cfg % 16, g_forced_cfg / 16 > 1 ? g_forced_cfg / 16 : 1});
     auto it = g_tuned.find(key);
-    if (it != g_tuned.end()) return launch(it->second, a, mode, va, vb, cx->stream);
+    if (it != g_tuned.end()) return run(it->second);
     if (g_autotune && !aliased) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
       if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
@@ -362,21 +448,22 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   }
   if (tune && cands.size() > 1) {
     // Time each candidate (the output is rewritten identically by each run:
-    // out never aliases x or residual).
+    // out never aliases x or residual).  Warm the clocks with the model's
+    // choice, then time every candidate twice (two launches each) and keep
+    // its faster run.
     hipEvent_t e0, e1;
     if (int st = hip_status(hipEventCreate(&e0), "hipEventCreate")) return st;
     if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) return st;
-    // warm the clocks with the model's choice, then time every candidate
-    // twice (two launches each) and keep its faster run
     for (int r = 0; r < 3; ++r)
-      if (int st = launch(best, a, mode, va, vb, cx->stream)) return st;
+      if (int st = run(best)) return st;
     float bestMs = 1e30f;
-    for (int c : cands) {
-      if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;  // warm-up
+    for (const Cand& c : cands) {
+      if (c.splits > 1 && !wsFor(c)) continue;
+      if (int st = run(c)) return st;  // warm-up
       for (int t = 0; t < 2; ++t) {
         (void)hipEventRecord(e0, cx->stream);
         for (int r = 0; r < 2; ++r)
-          if (int st = launch(c, a, mode, va, vb, cx->stream)) return st;
+          if (int st = run(c)) return st;
         (void)hipEventRecord(e1, cx->stream);
         (void)hipEventSynchronize(e1);
         float ms = 0.f;
@@ -390,9 +477,9 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     g_tuned[key] = best;
     static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
     if (verbose)
-      std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) %.4f ms\n",
-                   (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best,
-                   kCfgs[best].BM, kCfgs[best].BN, kCfgs[best].BK, bestMs / 2);
+      std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d %.4f ms\n",
+                   (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
+                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, bestMs / 2);
   }
-  return launch(best, a, mode, va, vb, cx->stream);
+  return run(best);
 }

@@ -274,6 +274,31 @@ class Network:
             prev = self.out[i]
         return prev
 
+    def capture(self, x):
+        """Records one forward pass over the fixed input buffer `x` into a HIP
+        graph on the library's own stream (after an eager pass has tuned the
+        kernels); replay() then launches the whole network at once."""
+        hip = self.hip
+        self.torch.cuda.synchronize()
+        hip.resetStream()
+        hip.finish()
+        hip.graphBegin()
+        try:
+            heads = self.forward(x)
+        finally:
+            graph = hip.graphEnd()
+        self.graph, self.graph_heads = graph, heads
+        return heads
+
+    def replay(self):
+        self.hip.graphLaunch(self.graph)
+        return self.graph_heads
+
+    def release_graph(self):
+        if getattr(self, "graph", None):
+            self.hip.graphDestroy(self.graph)
+            self.graph = None
+
     def head_convs(self):
         """Indices of the convolutions feeding the yolo layers (pre-logistic)."""
         return [L["index"] - 1 for L in self.layers if L["type"] == "yolo"]

@@ -43,6 +43,10 @@ _PROTOS = {
     "tnh_set_stream": [vp],
     "tnh_reset_stream": [],
     "tnh_cu_count": [C.POINTER(i32)],
+    "tnh_graph_begin": [],
+    "tnh_graph_end": [C.POINTER(vp)],
+    "tnh_graph_launch": [vp],
+    "tnh_graph_destroy": [vp],
     "tnh_malloc": [i64, C.POINTER(vp)],
     "tnh_free": [vp],
     "tnh_h2d": [vp, vp, i64],
@@ -203,6 +207,22 @@ class TNNHip:
         n = i32(0)
         call("tnh_cu_count", C.byref(n))
         return n.value
+
+    # -- graphs --------------------------------------------------------------
+    def graphBegin(self):
+        """Start capturing the context's own stream (call resetStream first)."""
+        call("tnh_graph_begin")
+
+    def graphEnd(self):
+        g = vp()
+        call("tnh_graph_end", C.byref(g))
+        return g.value
+
+    def graphLaunch(self, graph):
+        call("tnh_graph_launch", graph)
+
+    def graphDestroy(self, graph):
+        call("tnh_graph_destroy", graph)
 
     # -- memory ------------------------------------------------------------
     def createDeviceBuffer(self, N):

@@ -199,6 +199,31 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("splits", [2, 4, 16])
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 512, 13, 1024, 3, 1), (1, 256, 13, 255, 1, 1), (2, 64, 9, 96, 3, 2)])
+def test_conv_splitk(hip, splits, B, Cc, Hh, F, k, s):
+    """Split-K partial sums reduced in fixed order, then the epilogue."""
+    case(f"conv split-K {splits} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
+    p = k // 2
+    x = synth.uniform(47, (B, Cc, Hh, Hh))
+    Wt = synth.normal(48, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(49, (F,), 0.1)
+    res = synth.normal(50, (B, F, (Hh + 2 * p - k) // s + 1, (Hh + 2 * p - k) // s + 1))
+    ref = R.addvv(R.conv_forward(x, Wt, b, k, s, p, acLEAKY), res)
+    dW = D(Wt)
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, k, dW, packed)
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, 16 * splits + 0)
+    try:
+        hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
+                          weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
+        got = H(dout, hip)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert R.rel_err(got, ref) <= TOL
+
+
 def test_conv_golden_fixture(hip):
     case("conv golden fixture (torch fp64)")
     import os
