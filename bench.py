@@ -26,6 +26,12 @@ sys.path.insert(0, ROOT)
 METRIC = "conv im2col+SGEMM GFLOP/s (% fp32 MFMA peak); YOLOv3-416 img/s at batch 1/16"
 PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
+# HBM bytes per launch of the dominant kernel family (tap-major 3x3 conv,
+# incl. its split-K reduction) from two rocprofv3 --pmc runs of
+# `bench.py --counter-pass` (FETCH_SIZE then WRITE_SIZE, KiB per dispatch,
+# scaled by a 64 MiB copy: read = 2.0 x FETCH_SIZE, write = 1.0 x WRITE_SIZE);
+# profiles/yolov3_416_b16_conv_tap3x3.md holds the figures and commands.
+TRAFFIC_TAP3X3_B16 = (2.0 * 90347.8 + 42229.1) * 1024
 
 
 def log(*a):
@@ -133,6 +139,36 @@ def cpu_baseline(layers, weights, budget_s=12.0):
     return n / dt, threads, n
 
 
+COPY_BYTES = 64 << 20
+
+
+def counter_pass(hip, net, args):
+    """Warm-up forwards (autotuning), a fence, then exactly one forward and one
+    copy of COPY_BYTES: the dispatches a counter run attributes.  The copy
+    calibrates FETCH_SIZE / WRITE_SIZE (KiB per dispatch) against a kernel whose
+    HBM traffic is known (COPY_BYTES read + COPY_BYTES written)."""
+    import torch
+
+    from tensorium_amd import synth
+
+    x = torch.from_numpy(synth.uniform(7, (args.batch, 3, args.size, args.size))).cuda()
+    src = torch.rand(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup)):
+        net.forward(x)
+    hip.finish()
+    torch.cuda.synchronize()
+    marker = torch.zeros(64, device="cuda")
+    hip.fill(1, marker, 0, 0.0, 1)  # fill_kernel: marks the start of the attributed region
+    log("counter pass: timed region starts")
+    net.forward(x)
+    hip.copy(COPY_BYTES // 4, src, 0, 1, dst, 0, 1)
+    hip.finish()
+    torch.cuda.synchronize()
+    log("counter pass: done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,10 +180,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="for rocprofv3 --pmc: tune, then run ONE eager forward and a 64 MiB copy "
+                         "(the calibration kernel), print nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the YOLOv3 inference path shards by image "
-              "with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "with no communication, one process per GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -161,6 +200,10 @@ def main():
     _, layers = darknet.load_cfg("yolov3.cfg", args.size, args.size)
     weights = darknet.synthetic_weights(layers)
     flop_img = darknet.conv_flops(layers)
+
+    if args.counter_pass:
+        counter_pass(hip, darknet.Network(hip, layers, args.batch, weights), args)
+        return
 
     def run(batch, steps, warmup):
         net = darknet.Network(hip, layers, batch, weights)
@@ -224,7 +267,10 @@ def main():
         "img_s_batch1": None if b1 is None else round(b1, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                     "traffic": (round(TRAFFIC_TAP3X3_B16) if dom == "conv_kernel<tap3x3>" and args.batch == 16
+                                 and args.size == 416 else None),
+                     "traffic_unit": "bytes/launch",
                      "launches_per_step": round(d["launches"]),
                      "flop_per_launch": round(d["flop"] / max(d["launches"], 1))},
         "cpu_baseline": cpu,

@@ -136,6 +136,205 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct variant: no LDS and no barriers.  Each wave owns a
+// (32*FM) x (32*FN) output tile and loads its own MFMA operands from global
+// memory (L1/L2) straight into registers, one 16-deep K chunk ahead of the
+// chunk it multiplies.  For v_mfma_f32_32x32x2_f32 with the chunk pairing
+// (step s uses k = s on lanes 0-31 and k = 8 + s on lanes 32-63) a lane
+// needs 8 consecutive k of one row of A (two 16-byte loads of the
+// k-contiguous weights) and 8 consecutive k of one column of B: with
+// tap-major weights and C % 16 == 0 those are 8 consecutive channels of one
+// input pixel, i.e. 8 loads HW floats apart.  Everything that varies along K
+// is uniform across the wave (tap, channel) and rides in the buffer
+// instruction's scalar offset, so the inner loop is loads and MFMAs only;
+// the per-lane offsets are recomputed once per tap.  The waves of a
+// workgroup cover adjacent tiles and share A rows / B columns through L1.
+// ---------------------------------------------------------------------------
+template <int FM_, int FN_, int WM_, int WN_, int OCC_, int PF_ = 1>
+struct DirectCfg {
+  static constexpr int FM = FM_, FN = FN_, WM = WM_, WN = WN_, OCC = OCC_;
+  static constexpr int PF = PF_;  // chunks loaded ahead of the one multiplied (1 or 2)
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int WTM = FM * 32, WTN = FN * 32;
+  static constexpr int BM = WM * WTM, BN = WN * WTN, BK = 16;
+};
+
+__device__ inline float buf_ld1s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ inline f32x4 buf_ld4s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+template <class D, int KH, int KW>
+__global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) {
+  constexpr int FM = D::FM, FN = D::FN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / D::WN, wn = wave % D::WN;
+  const int r = lane & 31, h = lane >> 5;
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * D::BM + wm * D::WTM;
+  const int64_t n0 = static_cast<int64_t>(tn) * D::BN + wn * D::WTN;
+
+  const int C = a.g.C, H = a.g.H, W = a.g.W;
+  const int64_t K = a.g.K;
+  const uint32_t HW4 = static_cast<uint32_t>(H) * static_cast<uint32_t>(W) * 4u;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.wBytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
+
+  // A: lane (r, h) of row block i reads W[m0 + 32i + r][k0 + 8h .. k0 + 8h + 7]
+  uint32_t aOff[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int64_t row = m0 + 32 * i + r;
+    aOff[i] = row < a.F ? static_cast<uint32_t>((row * K + 8 * h) * 4) : kOOB;
+  }
+  // B: lane (r, h) of column block j reads channels c0 + 8h .. c0 + 8h + 7
+  // of input pixel (iy0 + ky, ix0 + kx) of its column's image.  cOff is the
+  // byte offset of (iy0, ix0) modulo 2^32 (it may wrap; in-range taps add
+  // back to the exact offset).
+  int iy0[FN], ix0[FN];
+  uint32_t cOff[FN];
+  bool cOk[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0 + 32 * j + r;
+    cOk[j] = n < a.g.N;
+    const int64_t nn = cOk[j] ? n : 0;
+    const int64_t b = nn / a.g.OHW;
+    const int p = static_cast<int>(nn - b * a.g.OHW);
+    const int oy = p / a.g.OW, ox = p - (p / a.g.OW) * a.g.OW;
+    iy0[j] = oy * a.g.sY - a.g.pH;
+    ix0[j] = ox * a.g.sX - a.g.pW;
+    cOff[j] = static_cast<uint32_t>((b * a.g.xBatchStride + static_cast<int64_t>(iy0[j]) * W + ix0[j]) * 4) +
+              static_cast<uint32_t>(8 * h) * HW4;
+  }
+
+  // K is walked channel-chunk outer, tap inner: chunk q covers channels
+  // c0 = 16*(q / TAPS) .. c0 + 15 of tap q % TAPS (k = tap*C + c0 in the
+  // tap-major weights).  The nine taps of one channel chunk read nearly the
+  // same input lines back to back, so they hit in L1/L2 instead of
+  // re-streaming every channel of the input once per tap.
+  constexpr int TAPS = KH * KW;
+  const int qBegin = static_cast<int>(blockIdx.y * a.kChunk / 16);
+  const int qEnd = static_cast<int>(min(K, (blockIdx.y + 1) * a.kChunk) / 16);
+  const int nq = qEnd - qBegin;
+  int q = qBegin;
+  auto load = [&](f32x4 (&A)[FM][2], float (&B)[FN][8]) {
+    const int cc = q / TAPS, tap = q - cc * TAPS;
+    const int c0 = cc * 16;
+    const uint32_t ks = static_cast<uint32_t>(tap * C + c0) * 4u;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      A[i][0] = buf_ld4s(wr, aOff[i], ks);
+      A[i][1] = buf_ld4s(wr, aOff[i], ks + 16);
+    }
+    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+    const uint32_t tapOff = static_cast<uint32_t>(ky * W + kx) * 4u;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int iy = iy0[j] + ky, ix = ix0[j] + kx;
+      const bool ok = cOk[j] && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                      static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+      const uint32_t vo = ok ? cOff[j] + tapOff : kOOB;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) B[j][s] = buf_ld1s(xr, vo, static_cast<uint32_t>(c0 + s) * HW4);
+    }
+    ++q;
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  auto compute = [&](const f32x4 (&A)[FM][2], const float (&B)[FN][8]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[i][s >> 2][s & 3], B[j][s], acc[i][j], 0, 0, 0);
+  };
+
+  // Single-exit loop over chunk pairs (accumulators stay in place; a loop
+  // with an exit between the two halves makes the compiler shuttle them
+  // between register files every iteration).
+  if (nq > 0 && D::PF == 1) {
+    f32x4 A0[FM][2], A1[FM][2];
+    float B0[FN][8], B1[FN][8];
+    load(A0, B0);  // chunk 0
+    int i = 0;
+    for (; i + 1 < nq; i += 2) {
+      load(A1, B1);  // chunk i + 1
+      compute(A0, B0);
+      if (i + 2 < nq) load(A0, B0);  // chunk i + 2
+      compute(A1, B1);
+    }
+    if (i < nq) compute(A0, B0);  // odd count: the last chunk
+  } else if (nq > 0) {
+    // two chunks in flight: three register sets in rotation
+    f32x4 A0[FM][2], A1[FM][2], A2[FM][2];
+    float B0[FN][8], B1[FN][8], B2[FN][8];
+    load(A0, B0);  // chunk 0
+    if (nq > 1) load(A1, B1);  // chunk 1
+    int i = 0;
+    for (; i + 2 < nq; i += 3) {  // chunks i, i + 1 are in sets 0, 1
+      load(A2, B2);  // chunk i + 2
+      compute(A0, B0);
+      if (i + 3 < nq) load(A0, B0);  // chunk i + 3
+      compute(A1, B1);
+      if (i + 4 < nq) load(A1, B1);  // chunk i + 4
+      compute(A2, B2);
+    }
+    if (i < nq) compute(A0, B0);
+    if (i + 1 < nq) compute(A1, B1);
+  }
+
+  if (a.splits > 1) {  // raw partial sums; conv_splitk_reduce applies the epilogue
+    float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.F * a.g.N;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0 + 32 * j + r;
+      if (n >= a.g.N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t f = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (f < a.F) part[f * a.g.N + n] = acc[i][j][e];
+        }
+    }
+    return;
+  }
+  const int64_t OHW = a.g.OHW;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0 + 32 * j + r;
+    if (n >= a.g.N) continue;
+    const int64_t b = n / OHW, p = n - b * OHW;
+    float* out = a.out + b * a.outBatchStride + p;
+    const float* res = a.res ? a.res + b * a.rBatchStride + p : nullptr;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t f = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (f >= a.F) continue;
+        float v = acc[i][j][e];
+        if (a.bias) v = v + a.bias[f];
+        v = apply_act(v, a.act);
+        if (res) v = v + res[f * OHW];
+        out[f * OHW] = v;
+      }
+  }
+}
+
 // Sums the split-K partials in split order (deterministic) and applies the
 // epilogue: one thread per output element, consecutive threads along n.
 __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
@@ -155,25 +354,37 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
 // ---------------------------------------------------------------------------
 // tile configurations
 // ---------------------------------------------------------------------------
-// (tile M x N x K depth, waves M x N, prefetch depth); chosen from sweeps of
-// the YOLOv3 layer shapes: small tiles with two panels of prefetch keep the
-// most waves resident and win on most shapes.
+// LDS-staged tiles (tile M x N x K depth, waves M x N, prefetch depth,
+// occupancy), chosen from sweeps of the YOLOv3 layer shapes: small tiles
+// with two panels of prefetch keep the most waves resident and win on most
+// shapes.  The register-direct tiles win some large-M and 1x1 shapes; the
+// autotuner picks per layer shape.
 using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2, 1>;
 using Cfg1 = TileCfg<64, 64, 16, 2, 2, 2, 8>;
 using Cfg2 = TileCfg<128, 64, 16, 2, 2, 2, 5>;
 using Cfg3 = TileCfg<128, 128, 16, 2, 2, 1, 1>;
 using Cfg4 = TileCfg<64, 128, 32, 2, 2, 2, 1>;
 using Cfg5 = TileCfg<64, 128, 16, 2, 2, 2, 5>;
+// register-direct tiles (FM x FN 32x32 blocks per wave, WM x WN waves)
+using Dir6 = DirectCfg<2, 2, 4, 1, 3>;
+using Dir7 = DirectCfg<2, 1, 1, 4, 4>;
+using Dir8 = DirectCfg<2, 2, 2, 2, 3>;
+using Dir9 = DirectCfg<2, 2, 1, 4, 3>;
+using Dir10 = DirectCfg<1, 2, 4, 1, 4>;
 
 struct CfgInfo {
   int BM, BN, BK;
   float eff;  // relative per-CU throughput used by the cost model
   int perCU;  // resident workgroups per CU assumed by the cost model
+  bool direct;
 };
-constexpr int kNumCfg = 6;
+constexpr int kNumCfg = 11;
+constexpr int kFirstDirect = 6;
 const CfgInfo kCfgs[kNumCfg] = {
-    {64, 64, 32, 1.00f, 4},   {64, 64, 16, 1.00f, 8}, {128, 64, 16, 0.97f, 5},
-    {128, 128, 16, 0.95f, 2}, {64, 128, 32, 0.97f, 3}, {64, 128, 16, 0.95f, 5},
+    {64, 64, 32, 1.00f, 4, false},   {64, 64, 16, 1.00f, 8, false}, {128, 64, 16, 0.97f, 5, false},
+    {128, 128, 16, 0.95f, 2, false}, {64, 128, 32, 0.97f, 3, false}, {64, 128, 16, 0.95f, 5, false},
+    {256, 64, 16, 0.95f, 3, true},   {64, 128, 16, 0.95f, 4, true}, {128, 128, 16, 0.95f, 3, true},
+    {64, 256, 16, 0.95f, 3, true},   {128, 64, 16, 0.95f, 4, true},
 };
 
 template <class Cfg>
@@ -235,6 +446,25 @@ int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
   }
 }
 
+template <class D>
+int launch_direct(ConvArgs a, int mode, hipStream_t s) {
+  dim3 grid;
+  if (int st = grid_for<D>(a, grid)) return st;
+  if (mode == kTap3)
+    hipLaunchKernelGGL((conv_direct_kernel<D, 3, 3>), grid, dim3(D::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_direct_kernel<D, 1, 1>), grid, dim3(D::NT), 0, s, a);
+  if (int st = launch_status("conv_direct_kernel")) return st;
+  if (a.splits > 1) {
+    const int64_t total = a.F * a.g.N;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
+                       s, a);
+    return launch_status("conv_splitk_reduce");
+  }
+  return TNH_OK;
+}
+
 int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
   switch (cfg) {
     case 0: return launch_cfg<Cfg0>(a, mode, va, vb, s);
@@ -242,7 +472,12 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s
     case 2: return launch_cfg<Cfg2>(a, mode, va, vb, s);
     case 3: return launch_cfg<Cfg3>(a, mode, va, vb, s);
     case 4: return launch_cfg<Cfg4>(a, mode, va, vb, s);
-    default: return launch_cfg<Cfg5>(a, mode, va, vb, s);
+    case 5: return launch_cfg<Cfg5>(a, mode, va, vb, s);
+    case 6: return launch_direct<Dir6>(a, mode, s);
+    case 7: return launch_direct<Dir7>(a, mode, s);
+    case 8: return launch_direct<Dir8>(a, mode, s);
+    case 9: return launch_direct<Dir9>(a, mode, s);
+    default: return launch_direct<Dir10>(a, mode, s);
   }
 }
 
@@ -300,7 +535,10 @@ std::unordered_map<TuneKey, Cand, TuneHash> g_tuned;
 bool g_autotune = true;
 int g_forced_cfg = -1;
 
-bool cfg_valid(int c, int mode, int64_t C) {
+// The register-direct kernels need whole 16-channel chunks inside one tap
+// and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
+bool cfg_valid(int c, int mode, int64_t C, bool va) {
+  if (kCfgs[c].direct) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
   if (mode == kTap3) return C % kCfgs[c].BK == 0;
   return true;
 }
@@ -402,7 +640,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   // workspace, reduced in fixed order).
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
-    if (!cfg_valid(c, mode, C)) continue;
+    if (!cfg_valid(c, mode, C, va)) continue;
     cands.push_back({c, 1});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
@@ -437,7 +675,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 16, mode, C))
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 16, mode, C, va))
       return run({g_forced_cfg % 16, g_forced_cfg / 16 > 1 ? g_forced_cfg / 16 : 1});
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return run(it->second);

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -172,10 +172,11 @@ def test_conv_forward_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(H(dout, hip), ref) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("cfg", range(NUM_CONV_CFGS))
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", [(2, 32, 26, 64, 3, 1, 1, acLEAKY), (1, 64, 13, 96, 3, 2, 1, acLEAKY),
                                                  (2, 48, 11, 40, 3, 1, 1, acLINEAR), (1, 3, 20, 16, 3, 1, 1, acLEAKY),
-                                                 (2, 40, 9, 70, 1, 1, 0, acLEAKY)])
+                                                 (2, 40, 9, 70, 1, 1, 0, acLEAKY), (3, 64, 13, 300, 1, 1, 0, acLEAKY),
+                                                 (2, 16, 7, 33, 3, 2, 1, acLEAKY)])
 def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     """Tap-major packed weights through each tile configuration (pinned)."""
     case(f"conv packed cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
@@ -199,11 +200,12 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("cfg", [0, 6, 8])
 @pytest.mark.parametrize("splits", [2, 4, 16])
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 512, 13, 1024, 3, 1), (1, 256, 13, 255, 1, 1), (2, 64, 9, 96, 3, 2)])
-def test_conv_splitk(hip, splits, B, Cc, Hh, F, k, s):
+def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
     """Split-K partial sums reduced in fixed order, then the epilogue."""
-    case(f"conv split-K {splits} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
+    case(f"conv split-K {splits} cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
     p = k // 2
     x = synth.uniform(47, (B, Cc, Hh, Hh))
     Wt = synth.normal(48, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
@@ -214,7 +216,7 @@ def test_conv_splitk(hip, splits, B, Cc, Hh, F, k, s):
     packed = torch.empty_like(dW)
     hip.packConvWeights(F, Cc, k, dW, packed)
     dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
-    hip.setConvAutotune(True, 16 * splits + 0)
+    hip.setConvAutotune(True, 16 * splits + cfg)
     try:
         hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
                           weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
