@@ -264,6 +264,86 @@ int32_t tnh_bn_normalize(int64_t dstSize, float *x, int64_t offset, int64_t N,
                          const float *mean, const float *variance,
                          int64_t batch);
 
+/* ---- training direction (config-3 step: conv-BN-leaky, pooling,
+ *      connected, softmax cross-entropy, SGD) --------------------------- */
+/* TNNCuda.meansAndVars (nncuda.pas:1308) with the CPU semantics of
+ * TTensor.MeansAndVars (ntensors.pas:9102-9180): src (+offset) viewed as
+ * [groups][dstSize][block], block = srcSize/(dstSize*groups);
+ * means[i] = sum/(groups*block), vars[i] = sum (x-mean)^2/(groups*block-1). */
+int32_t tnh_means_vars(int64_t srcSize, int64_t dstSize, int64_t groups,
+                       const float *src, int64_t offset, float *means,
+                       float *vars);
+/* TNNCuda.meansAndVarsDelta (nncuda.pas:1398) / sMeanAndVarianceDelta
+ * (ntensors.pas:8831-8898): mean_delta[i] = sum(delta) * -1/sqrt(max(var,
+ * 1e-6)); variance_delta[i] = sum(delta*(x-mean)) * -0.5 *
+ * max(var, 1e-6)^-1.5.  delta and x share the offset. */
+int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_t groups,
+                             const float *delta, const float *x,
+                             int64_t offset, const float *mean,
+                             const float *variance, float *mean_delta,
+                             float *variance_delta);
+/* TNNCuda.normalizeDelta (nncuda.pas:1421) / sNormalizeDelta
+ * (ntensors.pas:8900-8960): delta = delta/sqrt(max(var,1e-6)) +
+ * ((x-mean)*(2*variance_delta/bs) + mean_delta/bs), bs = block*groups. */
+int32_t tnh_normalize_delta(int64_t deltaSize, int64_t meanSize,
+                            int64_t groups, float *delta, const float *x,
+                            int64_t offset, const float *mean,
+                            const float *variance, const float *mean_delta,
+                            const float *variance_delta);
+/* TNNCuda.addDots (nncuda.pas:1448) / TTensor.addDots (ntensors.pas:7783):
+ * dst[i] += sum over (group, block) of src1*src2. */
+int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups,
+                     const float *src1, const float *src2, int64_t srcOffset,
+                     float *dst);
+/* TNNCuda.softmaxBatch (nncuda.pas:1056) / softmax (nsoftmaxlayer.pas:81):
+ * per (batch, group) row of N values (stride apart): e = exp((x-max)/temp),
+ * out = e / sum(e). */
+int32_t tnh_softmax_batch(int64_t N, const float *input, int64_t iOffset,
+                          int64_t batch, int64_t batchSize, int64_t groups,
+                          int64_t groupSize, int64_t stride, float temp,
+                          float *output, int64_t oOffset);
+/* TNNCuda.crossEntropySoftmax (nncuda.pas:1075) / softmaxCrossEntropy
+ * (nsoftmaxlayer.pas:123): error = t != 0 ? -ln(max(p, 1e-6)) : 0;
+ * delta = t - p. */
+int32_t tnh_cross_entropy_softmax(int64_t N, const float *pred,
+                                  const float *truth, float *delta,
+                                  float *error);
+/* TNNCuda.clamp (nncuda.pas:1551): dst = max(min(src, alpha), -alpha) at
+ * offset + i*stride (TTensor.Clamp(-1, 1), nconnectedlayer.pas:255). */
+int32_t tnh_clamp(int64_t N, float alpha, const float *src, float *dst,
+                  int64_t stride, int64_t offset);
+/* TAvgPoolLayer.forward (navgpoollayer.pas:60-84; the reference has no GPU
+ * version): out[b][c] = sum(in[b][c]) / (h*w). */
+int32_t tnh_avgpool_fwd(int64_t batch, int64_t c, int64_t h, int64_t w,
+                        const float *input, float *output);
+/* TAvgPoolLayer.backward (navgpoollayer.pas:86-100):
+ * deltaIn[b][c][k] += delta[b][c] / (h*w). */
+int32_t tnh_avgpool_bwd(int64_t batch, int64_t c, int64_t h, int64_t w,
+                        const float *delta, float *deltaIn);
+/* T*Layer.update weight part (nConvolutionLayer.pas:684-691,
+ * nconnectedlayer.pas:344-353), fused: weightUpdates =
+ * fma(-decay*batch, weights, weightUpdates); weights = fma(lr/batch,
+ * weightUpdates, weights); weightUpdates *= momentum. */
+int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch,
+                       float momentum, float decay, float *weights,
+                       float *weightUpdates);
+/* bias / scale part of the same updates (nConvolutionLayer.pas:694-706):
+ * params = fma(lr/batch, paramUpdates, params); paramUpdates *= momentum. */
+int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch,
+                         float momentum, float *params, float *paramUpdates);
+/* Weight gradient of conv backward: replaces the per-image loop
+ * `for b: gemm(NoTrans, Trans, F, C*k*k, OH*OW, 1, delta_b, col_b, 1, dW)`
+ * (nConvolutionLayer.pas:644-650) with one launch:
+ *   C = beta*C + alpha * sum_b A_b * B_b^T,
+ *   A_b = A + aOff + b*strideA  ([M][L], row stride lda),
+ *   B_b = B + bOff + b*strideB  ([N][L], row stride ldb). */
+int32_t tnh_sgemm_nt_batch_reduce(int64_t M, int64_t N, int64_t L,
+                                  float alpha, const float *A, int64_t aOff,
+                                  int64_t lda, int64_t strideA, const float *B,
+                                  int64_t bOff, int64_t ldb, int64_t strideB,
+                                  float beta, float *C, int64_t cOff,
+                                  int64_t ldc, int64_t batch);
+
 #ifdef __cplusplus
 }
 #endif

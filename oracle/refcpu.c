@@ -249,6 +249,9 @@ static void sscal_row(int64_t n, float a, float *x) {
   for (int64_t j = 0; j < n; ++j) x[j] = a * x[j];
 }
 
+/* cblas_saxpy (bound at ntensors.pas:12691) -> saxpy_avx2: y = fma(a, x, y) */
+void ref_axpy(int64_t n, float a, const float *x, float *y) { saxpy8(n, a, x, y); }
+
 void ref_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
                float alpha, const float *A, int64_t lda, const float *B,
                int64_t ldb, float beta, float *C, int64_t ldc) {

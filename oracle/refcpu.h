@@ -24,6 +24,9 @@ extern "C" {
 void ref_set_threads(int p);
 int ref_get_threads(void);
 
+/* cblas_saxpy -> saxpy_avx2 (ntensors.pas:1308): y = fma(a, x, y) */
+void ref_axpy(int64_t n, float a, const float *x, float *y);
+
 /* cblas_sgemm (ntensors.pas:2231-2286); trans flags: 0 = no, 1 = yes */
 void ref_sgemm(int transA, int transB, int64_t M, int64_t N, int64_t K,
                float alpha, const float *A, int64_t lda, const float *B,

@@ -19,6 +19,7 @@ P = C.c_void_p
 _PROTOS = {
     "ref_set_threads": ([i32], None),
     "ref_get_threads": ([], i32),
+    "ref_axpy": ([i64, f32, P, P], None),
     "ref_sgemm": ([i32, i32, i64, i64, i64, f32, P, i64, P, i64, f32, P, i64], None),
     "ref_sgemm_strided_batched": ([i32, i32, i64, i64, i64, f32, P, i64, i64, P, i64, i64, f32, P, i64, i64,
                                    i64], None),
@@ -74,6 +75,14 @@ def set_threads(p):
 
 def get_threads():
     return lib().ref_get_threads()
+
+
+def axpy(y, a, x):
+    """Returns y + a*x with one fused multiply-add per element (saxpy_avx2)."""
+    y = _f32(y).copy()
+    x = _f32(x)
+    lib().ref_axpy(y.size, a, _p(x), _p(y))
+    return y
 
 
 def sgemm(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, Cm, ldc):

@@ -1,0 +1,357 @@
+"""CPU restatement of the reference's training-mode layer arithmetic (TEST
+INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg).
+
+Covers what the config-3 training step (conv-BN-leaky x3, maxpool, avgpool,
+connected, softmax cross-entropy, SGD with momentum and decay) needs beyond
+the forward path in refcpu.c:
+
+  means_vars          TTensor.MeansAndVars            ntensors.pas:9102-9180
+  means_vars_delta    sMeanAndVarianceDelta           ntensors.pas:8831-8898
+  normalize_delta     sNormalizeDelta(_pas)           ntensors.pas:8823-8829, 8900-8960
+  add_dots            TTensor.addDots                 ntensors.pas:7783-7830
+  add_sums            TTensor.addSums                 ntensors.pas:7729-7781
+  softmax_batch       softmax / softmaxBatch          nsoftmaxlayer.pas:81-121
+  cross_entropy       softmaxCrossEntropy             nsoftmaxlayer.pas:123-137
+  avgpool_fwd / _bwd  TAvgPoolLayer.forward/backward  navgpoollayer.pas:60-100
+  clamp               TTensor.Clamp                   ntensors.pas:10077
+  sgd_update          T*Layer.update                  nConvolutionLayer.pas:673-710,
+                                                      nconnectedlayer.pas:324-355
+
+Element-wise formulas are restated in the reference's fp32 operation order
+(bit-exact given identical inputs).  Channel reductions (sums, dots) use
+float64 accumulation rounded to fp32 once: the reference sums with 8-lane
+AVX partial sums whose order is host-specific, so these are compared under
+the per-tensor tolerance, not bit-for-bit.  sEPSILON = 1e-6
+(ntensors.pas:95).
+
+Parity pins (tests/test_oracle_train.py): closed forms in float64, torch
+autograd for the softmax cross-entropy, conv, pooling and connected
+gradients, and for the batch-norm backward the exact autograd gradient plus
+the closed-form correction the reference's formula differs by.
+"""
+import math
+
+import numpy as np
+
+from oracle import refcpu as R
+
+EPS = np.float32(1e-6)
+acLEAKY, acLINEAR = 9, 4
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- batch norm
+def means_vars(x, nch, groups):
+    """mean[i] = sum over (b, k) of x[b][i][k] / S and
+    var[i] = sum (x - mean[i])^2 / (S - 1), S = groups*block, on x viewed as
+    [groups][nch][block] (MeansAndVars: Division(m, S), rss / S2 with
+    S2 = Groups*blockSize - 1, ntensors.pas:9140-9170)."""
+    v = _f32(x).reshape(groups, nch, -1)
+    S = v.shape[0] * v.shape[2]
+    s = v.astype(np.float64).sum(axis=(0, 2))
+    mean = (s.astype(np.float32) / np.float32(S)).astype(np.float32)
+    d = (v - mean[None, :, None]).astype(np.float64)  # fp32 x - m, as rss does
+    rss = (d * d).sum(axis=(0, 2))
+    var = (rss.astype(np.float32) / np.float32(S - 1)).astype(np.float32)
+    return mean, var
+
+
+def bn_normalize(x, mean, var, groups):
+    """x <- (x - mean) / max(sqrt(var), 1e-6) per channel (exact mode of
+    _snormblkvv, ntensors.pas:4357; the AVX build's rcpss is host-specific)."""
+    return R.bn_normalize(_f32(x).copy(), mean, var, groups, exact=True)
+
+
+def means_vars_delta(delta, x, mean, var, groups):
+    """sMeanAndVarianceDelta (ntensors.pas:8831-8898):
+    mean_delta[i] = (sum delta) * (-1 / sqrt(max(var, eps)))            (fp32)
+    variance_delta[i] = (sum delta*(x - mean)) * -0.5 * max(var, eps)^-1.5
+    (Power() evaluates in double; the product is stored as fp32)."""
+    nch = mean.size
+    d = _f32(delta).reshape(groups, nch, -1)
+    xx = _f32(x).reshape(groups, nch, -1)
+    m = d.astype(np.float64).sum(axis=(0, 2)).astype(np.float32)
+    xm = (xx - mean[None, :, None]).astype(np.float32)
+    v = (d.astype(np.float64) * xm.astype(np.float32).astype(np.float64)).sum(axis=(0, 2)).astype(np.float32)
+    vc = np.maximum(var, EPS).astype(np.float32)
+    mean_delta = (m * (np.float32(-1.0) / np.sqrt(vc))).astype(np.float32)
+    variance_delta = (v.astype(np.float64) * -0.5 * np.power(vc.astype(np.float64), -1.5)).astype(np.float32)
+    return mean_delta, variance_delta
+
+
+def normalize_delta(delta, x, mean, var, mean_delta, variance_delta, groups):
+    """sNormalizeDelta (ntensors.pas:8900-8960) with the per-element order of
+    sNormalizeDelta_pas/_avx: d = d / std + ((x - mean) * vd + md), where
+    std = sqrt(max(var, eps)), md = mean_delta / batchSize,
+    vd = 2 * variance_delta / batchSize, batchSize = block * groups."""
+    nch = mean.size
+    d = _f32(delta).reshape(groups, nch, -1)
+    xx = _f32(x).reshape(groups, nch, -1)
+    bs = np.float32(d.shape[2] * groups)
+    md = (mean_delta / bs).astype(np.float32)
+    vd = ((np.float32(2) * variance_delta) / bs).astype(np.float32)
+    std = np.sqrt(np.maximum(var, EPS)).astype(np.float32)
+    t = ((xx - mean[None, :, None]) * vd[None, :, None]).astype(np.float32)
+    t = (t + md[None, :, None]).astype(np.float32)
+    out = ((d / std[None, :, None]).astype(np.float32) + t).astype(np.float32)
+    return out.reshape(delta.shape)
+
+
+def add_dots(dst, a, b, groups):
+    """dst[i] += sum over (b, k) of a*b (addDots, ntensors.pas:7783)."""
+    nch = dst.size
+    aa = _f32(a).reshape(groups, nch, -1).astype(np.float64)
+    bb = _f32(b).reshape(groups, nch, -1).astype(np.float64)
+    s = (aa * bb).sum(axis=(0, 2)).astype(np.float32)
+    return (dst + s).astype(np.float32)
+
+
+def add_sums(dst, src, groups):
+    """dst[i] += sum over (b, k) of src (addSums, ntensors.pas:7729)."""
+    nch = dst.size
+    s = _f32(src).reshape(groups, nch, -1).astype(np.float64).sum(axis=(0, 2)).astype(np.float32)
+    return (dst + s).astype(np.float32)
+
+
+# ---------------------------------------------------------- softmax / cost
+def softmax_batch(x, temp=1.0):
+    """Row-wise softmax (nsoftmaxlayer.pas:81-105): e = exp((x - max)/temp)
+    (exp evaluated in double, stored fp32), sum accumulated in row order in
+    fp32, out = e / sum."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    t = np.float32(temp)
+    for r in range(x.shape[0]):
+        row = x[r]
+        largest = row.max()
+        e = np.exp(((row - largest) / t).astype(np.float32).astype(np.float64)).astype(np.float32)
+        s = np.float32(0)
+        for v in e:
+            s = np.float32(s + v)
+        out[r] = (e / s).astype(np.float32)
+    return out
+
+
+def cross_entropy(pred, truth):
+    """softmaxCrossEntropy (nsoftmaxlayer.pas:123-137): error = t != 0 ?
+    -ln(max(p, eps)) : 0; delta = t - p."""
+    pred, truth = _f32(pred), _f32(truth)
+    err = np.where(truth != 0, (-np.log(np.maximum(pred, EPS).astype(np.float64))).astype(np.float32),
+                   np.float32(0)).astype(np.float32)
+    delta = (truth - pred).astype(np.float32)
+    return delta, err
+
+
+def clamp(x, lo, hi):
+    return np.minimum(np.maximum(_f32(x), np.float32(lo)), np.float32(hi)).astype(np.float32)
+
+
+# ------------------------------------------------------------------ avgpool
+def avgpool_fwd(x):
+    """out[b][c] = sum(x[b][c]) / (h*w) (navgpoollayer.pas:60-84)."""
+    x = _f32(x)
+    B, Cc = x.shape[:2]
+    hw = int(np.prod(x.shape[2:]))
+    s = x.reshape(B, Cc, hw).astype(np.float64).sum(axis=2).astype(np.float32)
+    return (s / np.float32(hw)).astype(np.float32)
+
+
+def avgpool_bwd(dIn, dOut):
+    """dIn[b][c][k] += dOut[b][c] / (h*w) (navgpoollayer.pas:86-100)."""
+    B, Cc = dOut.shape[:2]
+    hw = dIn.size // (B * Cc)
+    v = (_f32(dOut) / np.float32(hw)).astype(np.float32)
+    return (dIn.reshape(B, Cc, hw) + v[:, :, None]).astype(np.float32).reshape(dIn.shape)
+
+
+# --------------------------------------------------------------------- SGD
+def axpy(y, a, x):
+    """cblas_saxpy via saxpy_avx2 (ntensors.pas:1308): y = fma(a, x, y)."""
+    return R.axpy(y, np.float32(a), x)
+
+
+def sgd_update(w, wu, lr, batch, momentum, decay):
+    """weight_updates.axpy(-decay*batch, weights); weights.axpy(lr/batch,
+    weight_updates); weight_updates *= momentum (nConvolutionLayer.pas:684-691).
+    The fp32 coefficients are formed as the reference forms them."""
+    a1 = np.float32(-np.float32(decay)) * np.float32(batch)
+    a2 = np.float32(lr) / np.float32(batch)
+    wu = axpy(wu, a1, w)
+    w = axpy(w, a2, wu)
+    wu = (wu * np.float32(momentum)).astype(np.float32)
+    return w, wu
+
+
+def param_update(p, pu, lr, batch, momentum):
+    """biases/scales.axpy(lr/batch, updates); updates *= momentum."""
+    a2 = np.float32(lr) / np.float32(batch)
+    p = axpy(p, a2, pu)
+    pu = (pu * np.float32(momentum)).astype(np.float32)
+    return p, pu
+
+
+# ------------------------------------------------------------ conv pieces
+def conv_plain(x, Wt, k, stride, pad):
+    """Conv2D (ntensors.pas:8252): im2col + per-image NN SGEMM, no bias."""
+    F = Wt.shape[0]
+    return R.conv_forward(x, Wt, np.zeros(F, np.float32), k, stride, pad, acLINEAR)
+
+
+def conv_backward(x, Wt, delta, dW, k, stride, pad, need_dx=True):
+    """TConvolutionalLayer.backward after the activation / BN part
+    (nConvolutionLayer.pas:626-665): col = im2col(x); for each image b
+    dW += delta_b * col_b^T (NT SGEMM, beta 1, images in order); then
+    colDelta_b = W^T * delta_b (TN, strided batched) and
+    dX = col2im(colDelta) accumulated into a zeroed input delta."""
+    x = _f32(x)
+    B, Cc, H, W = x.shape
+    F = Wt.shape[0]
+    K = Cc * k * k
+    col = R.im2col(x, k, k, pad, pad, stride, stride)
+    OHW = col.shape[2]
+    d = _f32(delta).reshape(B, F, OHW)
+    for b in range(B):
+        R.sgemm(0, 1, F, K, OHW, 1.0, d[b], OHW, col[b], OHW, 1.0, dW, K)
+    dx = None
+    if need_dx:
+        cd = np.zeros((B, K, OHW), np.float32)
+        R.sgemm_strided_batched(1, 0, K, OHW, F, 1.0, _f32(Wt), K, 0, d, OHW, F * OHW, 0.0, cd, OHW, K * OHW, B)
+        dx = np.zeros((B, Cc, H, W), np.float32)
+        R.col2im(cd, dx, k, k, pad, pad, stride, stride)
+    return dW, dx
+
+
+# ---------------------------------------------------- config-3 network
+CIFAR_LAYERS = (  # (C_in, F) of the three conv-BN-leaky blocks
+    (3, 32), (32, 64), (64, 128))
+
+
+def cifar_init(seed=0xC1FA):
+    """Reference-style init: conv weights U(-sqrt(2/(9C)), +sqrt(2/(9C)))
+    (nConvolutionLayer.pas:216-220), connected U(-sqrt(2/128), +...)
+    (nconnectedlayer.pas:79-80), BN scales 1, biases 0, rolling stats 0
+    (nConvolutionLayer.pas:246-260); generator = splitmix64 (seeded)."""
+    from tensorium_amd import synth
+
+    p = {}
+    for i, (Cc, F) in enumerate(CIFAR_LAYERS):
+        r = math.sqrt(2.0 / (9 * Cc))
+        p[f"w{i}"] = synth.uniform(seed + 10 * i + 1, (F, Cc * 9), -r, r)
+        p[f"s{i}"] = np.ones(F, np.float32)
+        p[f"b{i}"] = np.zeros(F, np.float32)
+        p[f"rm{i}"] = np.zeros(F, np.float32)
+        p[f"rv{i}"] = np.zeros(F, np.float32)
+    r = math.sqrt(2.0 / 128)
+    p["fw"] = synth.uniform(seed + 100, (10, 128), -r, r)
+    p["fb"] = np.zeros(10, np.float32)
+    for k in list(p):
+        if k[0] in "wsbf":  # w*, s*, b*, fw, fb carry momentum buffers
+            p["u_" + k] = np.zeros_like(p[k])
+    return p
+
+
+class CifarStep:
+    """One TNNet.trainEpoch iteration of the config-3 network on the CPU:
+    forward (nnet.pas:275-317), backward (nnet.pas:319-369) and update
+    (nnet.pas:371-400).  lr 1e-3, momentum 0.9, decay 1e-4, bnMomentum 0.1.
+    Quirks kept: BN layers do not update their biases (batchNormBack leaves
+    bias_updates alone, nbaselayer.pas:372-392), the connected layer clamps
+    its delta to [-1, 1] (nconnectedlayer.pas:255), the first layer computes
+    no input delta (state.delta is nil for layer 0, nnet.pas:333-336)."""
+
+    def __init__(self, params, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1):
+        self.p = {k: v.copy() for k, v in params.items()}
+        self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
+        self.t = {}
+
+    def forward(self, x, truth):
+        p, t = self.p, self.t
+        B = x.shape[0]
+        h = _f32(x)
+        t["in0"] = h
+        for i in range(3):
+            y = conv_plain(h, p[f"w{i}"], 3, 1, 1)
+            F = y.shape[1]
+            mean, var = means_vars(y, F, B)
+            bm = np.float32(self.bnm)
+            p[f"rm{i}"] = axpy((p[f"rm{i}"] * np.float32(1 - bm)).astype(np.float32), bm, mean)
+            p[f"rv{i}"] = axpy((p[f"rv{i}"] * np.float32(1 - bm)).astype(np.float32), bm, var)
+            t[f"x{i}"] = y.copy()
+            yn = bn_normalize(y, mean, var, B)
+            t[f"xn{i}"] = yn.copy()
+            t[f"mean{i}"], t[f"var{i}"] = mean, var
+            o = R.forward_scale(yn.copy(), p[f"s{i}"], B)
+            o = R.forward_bias(o, p[f"b{i}"], B)
+            o = R.activate(o, acLEAKY)
+            t[f"out{i}"] = o
+            if i < 2:
+                pooled, idx = R.maxpool_fwd(o, 2, 2, 2, 0)
+                t[f"pidx{i}"] = idx
+                t[f"pool{i}"] = pooled
+                h = pooled
+                t[f"in{i + 1}"] = h
+            else:
+                h = o
+        a = avgpool_fwd(h)
+        t["avg"] = a
+        logits = np.zeros((B, 10), np.float32)
+        R.sgemm(0, 1, B, 10, 128, 1.0, a, 128, p["fw"], 128, 0.0, logits, 10)
+        logits = R.forward_bias(logits, p["fb"], B)
+        t["logits"] = logits
+        prob = softmax_batch(logits)
+        t["prob"] = prob
+        delta, err = cross_entropy(prob, truth)
+        t["sm_delta"] = delta
+        t["loss"] = np.float32(err.astype(np.float64).sum())
+        return t["loss"]
+
+    def backward(self):
+        p, t = self.p, self.t
+        B = t["prob"].shape[0]
+        # softmax backward: state.delta.add(delta) into the (zeroed) FC delta
+        d = (np.zeros_like(t["sm_delta"]) + t["sm_delta"]).astype(np.float32)
+        # connected backward (nconnectedlayer.pas:239-300)
+        d = clamp(d, -1.0, 1.0)
+        p["u_fb"] = add_sums(p["u_fb"], d, B)
+        R.sgemm(1, 0, 10, 128, B, 1.0, d, 10, t["avg"], 128, 1.0, p["u_fw"], 128)
+        dA = np.zeros((B, 128), np.float32)
+        R.sgemm(0, 0, B, 128, 10, 1.0, d, 10, p["fw"], 128, 1.0, dA, 128)
+        # avgpool backward into conv3's (zeroed) delta
+        d = avgpool_bwd(np.zeros_like(t["out2"]), dA)
+        for i in (2, 1, 0):
+            o = t[f"out{i}"]
+            d = R.derive(o, acLEAKY, _f32(d).copy())
+            # batchNormBack (nbaselayer.pas:372-392)
+            p[f"u_s{i}"] = add_dots(p[f"u_s{i}"], t[f"xn{i}"], d, B)
+            d = R.forward_scale(_f32(d).copy(), p[f"s{i}"], B)
+            md, vd = means_vars_delta(d, t[f"x{i}"], t[f"mean{i}"], t[f"var{i}"], B)
+            t[f"md{i}"], t[f"vd{i}"] = md, vd
+            d = normalize_delta(d, t[f"x{i}"], t[f"mean{i}"], t[f"var{i}"], md, vd, B)
+            t[f"bn_delta{i}"] = d
+            p[f"u_w{i}"], dx = conv_backward(t[f"in{i}"], p[f"w{i}"], d, p[f"u_w{i}"], 3, 1, 1, need_dx=i > 0)
+            if i > 0:
+                t[f"dx{i}"] = dx
+                # maxpool backward into the previous block's (zeroed) delta
+                dprev = np.zeros_like(t[f"out{i - 1}"])
+                R.maxpool_bwd(t[f"pidx{i - 1}"], dx, dprev)
+                d = dprev
+
+    def update(self, batch):
+        p = self.p
+        for i in range(3):
+            p[f"w{i}"], p[f"u_w{i}"] = sgd_update(p[f"w{i}"], p[f"u_w{i}"], self.lr, batch, self.momentum,
+                                                  self.decay)
+            p[f"b{i}"], p[f"u_b{i}"] = param_update(p[f"b{i}"], p[f"u_b{i}"], self.lr, batch, self.momentum)
+            p[f"s{i}"], p[f"u_s{i}"] = param_update(p[f"s{i}"], p[f"u_s{i}"], self.lr, batch, self.momentum)
+        p["fb"], p["u_fb"] = param_update(p["fb"], p["u_fb"], self.lr, batch, self.momentum)
+        p["fw"], p["u_fw"] = sgd_update(p["fw"], p["u_fw"], self.lr, batch, self.momentum, self.decay)
+
+    def step(self, x, truth):
+        loss = self.forward(x, truth)
+        self.backward()
+        self.update(x.shape[0])
+        return loss

@@ -85,11 +85,10 @@ __global__ void addvv4_kernel(int64_t n4, const float4* a, const float4* b, floa
   }
 }
 
+// cblas_saxpy -> saxpy_avx2 (ntensors.pas:1308-1436): one fused multiply-add
+// per element, y = fma(a, x, y)
 __global__ void axpy_kernel(int64_t n, float a, const float* x, int64_t ix, float* y, int64_t iy) {
-  GRID_STRIDE(i, n) {
-    const float t = a * x[i * ix];
-    y[i * iy] = y[i * iy] + t;
-  }
+  GRID_STRIDE(i, n) y[i * iy] = fmaf(a, x[i * ix], y[i * iy]);
 }
 
 __global__ void scale_kernel(int64_t n, float a, float* x, int64_t stride) {

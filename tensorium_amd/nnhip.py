@@ -85,6 +85,19 @@ _PROTOS = {
     "tnh_upsample": [i64, i64, i64, i64, vp, i64, i32, f32, vp, i32],
     "tnh_bn_normalize": [i64, vp, i64, i64, vp, vp, i64],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
+    "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
+    "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
+    "tnh_normalize_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
+    "tnh_add_dots": [i64, i64, i64, vp, vp, i64, vp],
+    "tnh_softmax_batch": [i64, vp, i64, i64, i64, i64, i64, i64, f32, vp, i64],
+    "tnh_cross_entropy_softmax": [i64, vp, vp, vp, vp],
+    "tnh_clamp": [i64, f32, vp, vp, i64, i64],
+    "tnh_avgpool_fwd": [i64, i64, i64, i64, vp, vp],
+    "tnh_avgpool_bwd": [i64, i64, i64, i64, vp, vp],
+    "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
+    "tnh_param_update": [i64, f32, i64, f32, vp, vp],
+    "tnh_sgemm_nt_batch_reduce": [i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64, f32, vp, i64, i64,
+                                  i64],
 }
 _RESTYPES = {"tnh_last_error": C.c_char_p}
 
@@ -375,6 +388,52 @@ class TNNHip:
     # -- batch norm ------------------------------------------------------------
     def blockNormalize(self, dstSize, dst, offset, N, mean, variance, batch):
         call("tnh_bn_normalize", dstSize, addr(dst), offset, N, addr(mean), addr(variance), batch)
+
+    # -- training direction ----------------------------------------------------
+    def meansAndVars(self, srcSize, dstSize, groups, src, offset, means, vars):
+        call("tnh_means_vars", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
+
+    def meansAndVarsDelta(self, srcSize, dstSize, groups, delta, x, offset, mean, variance, mean_delta,
+                          variance_delta):
+        call("tnh_means_vars_delta", srcSize, dstSize, groups, addr(delta), addr(x), offset, addr(mean),
+             addr(variance), addr(mean_delta), addr(variance_delta))
+
+    def normalizeDelta(self, deltaSize, meanSize, groups, delta, x, offset, mean, variance, mean_delta,
+                       variance_delta):
+        call("tnh_normalize_delta", deltaSize, meanSize, groups, addr(delta), addr(x), offset, addr(mean),
+             addr(variance), addr(mean_delta), addr(variance_delta))
+
+    def addDots(self, N, dstSize, groups, src1, src2, srcOffset, dst):
+        call("tnh_add_dots", N, dstSize, groups, addr(src1), addr(src2), srcOffset, addr(dst))
+
+    def softmaxBatch(self, N, input, iOffset, batch, batch_size, groups, group_size, stride, temp, output,
+                     oOffset):
+        call("tnh_softmax_batch", N, addr(input), iOffset, batch, batch_size, groups, group_size, stride, temp,
+             addr(output), oOffset)
+
+    def crossEntropySoftmax(self, N, pred, truth, delta, error):
+        call("tnh_cross_entropy_softmax", N, addr(pred), addr(truth), addr(delta), addr(error))
+
+    def clamp(self, N, alpha, src, dst, stride=1, offset=0):
+        call("tnh_clamp", N, alpha, addr(src), addr(dst), stride, offset)
+
+    def avgPoolForward(self, batch, c, h, w, input, output):
+        call("tnh_avgpool_fwd", batch, c, h, w, addr(input), addr(output))
+
+    def avgPoolBackward(self, batch, c, h, w, delta, deltaIn):
+        call("tnh_avgpool_bwd", batch, c, h, w, addr(delta), addr(deltaIn))
+
+    def sgdUpdate(self, N, learningRate, batch, momentum, decay, weights, weightUpdates):
+        call("tnh_sgd_update", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates))
+
+    def paramUpdate(self, N, learningRate, batch, momentum, params, paramUpdates):
+        call("tnh_param_update", N, learningRate, batch, momentum, addr(params), addr(paramUpdates))
+
+    def gemmNTBatchReduce(self, M, N, L, ALPHA, A, aOffset, lda, strideA, B, bOffset, ldb, strideB, BETA, C_,
+                          cOffset, ldc, batch):
+        """C = BETA*C + ALPHA * sum_b A_b * B_b^T (conv weight gradient)."""
+        call("tnh_sgemm_nt_batch_reduce", M, N, L, ALPHA, addr(A), aOffset, lda, strideA, addr(B), bOffset, ldb,
+             strideB, BETA, addr(C_), cOffset, ldc, batch)
 
     # -- events ----------------------------------------------------------------
     def eventCreate(self):

@@ -1,0 +1,225 @@
+"""Device-resident training step of the config-3 network through the C ABI.
+
+Plays TNNet.trainEpoch for one batch (nnet.pas:474-530: Propagate = forward
++ backward, then update) on the network
+
+    conv3x3(32)-BN-leaky, maxpool 2/2, conv3x3(64)-BN-leaky, maxpool 2/2,
+    conv3x3(128)-BN-leaky, avgpool, connected 128->10, softmax cross-entropy
+
+with the layer semantics of the reference CPU path:
+  * TConvolutionalLayer.forward with batch norm in training mode
+    (nConvolutionLayer.pas:457-566, TBaseLayer.batchNorm nbaselayer.pas:336-370):
+    conv, MeansAndVars, rolling statistics, normalize, scale, bias, leaky;
+  * TConvolutionalLayer.backward (nConvolutionLayer.pas:571-671): leaky
+    derivative, batchNormBack (nbaselayer.pas:372-392), im2col, weight
+    gradient, W^T * delta, col2im; the first layer computes no input delta;
+  * TMaxPoolLayer forward with int64 indexes / backward
+    (nMaxPoolLayer.pas:363-512), TAvgPoolLayer (navgpoollayer.pas:60-100),
+    TConnectedLayer (nconnectedlayer.pas:157-322, delta clamped to [-1, 1]),
+    TSoftmaxLayer with cross-entropy (nsoftmaxlayer.pas:123-182);
+  * updates (nConvolutionLayer.pas:673-710, nconnectedlayer.pas:324-355):
+    SGD with momentum and decay; BN biases receive no gradient (the
+    reference's batchNormBack leaves bias_updates alone).
+
+Every operation is one C-ABI call on the library stream; buffers are device
+torch tensors (memory only).  Conv weights are kept in the reference layout
+[F][C*9] for the backward GEMMs and repacked tap-major for the forward.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from .nnhip import WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR
+
+BLOCKS = ((3, 32), (32, 64), (64, 128))  # (C_in, F) of the conv-BN-leaky blocks
+CLASSES = 10
+
+
+def init_params(seed=0xC1FA):
+    """Reference-style initial parameters (host numpy): conv weights
+    U(-sqrt(2/(9C)), sqrt(2/(9C))) (nConvolutionLayer.pas:216-220), connected
+    U(-sqrt(2/128), sqrt(2/128)) (nconnectedlayer.pas:79-80), BN scales 1,
+    biases and rolling statistics 0; splitmix64 streams (synth)."""
+    from . import synth
+
+    p = {}
+    for i, (c, f) in enumerate(BLOCKS):
+        r = math.sqrt(2.0 / (9 * c))
+        p[f"w{i}"] = synth.uniform(seed + 10 * i + 1, (f, c * 9), -r, r)
+        p[f"s{i}"] = np.ones(f, np.float32)
+        p[f"b{i}"] = np.zeros(f, np.float32)
+        p[f"rm{i}"] = np.zeros(f, np.float32)
+        p[f"rv{i}"] = np.zeros(f, np.float32)
+    r = math.sqrt(2.0 / BLOCKS[-1][1])
+    p["fw"] = synth.uniform(seed + 100, (CLASSES, BLOCKS[-1][1]), -r, r)
+    p["fb"] = np.zeros(CLASSES, np.float32)
+    for k in list(p):
+        if k[0] in "wsbf":  # w*, s*, b*, fw, fb carry momentum buffers
+            p["u_" + k] = np.zeros_like(p[k])
+    return p
+
+
+class CifarTrainer:
+    """One trainer per (batch, image size); `step(x, truth)` runs forward,
+    backward and update on the device; `cost()` reads the loss back."""
+
+    def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1):
+        import torch
+
+        self.hip, self.B, self.torch = hip, batch, torch
+        self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
+        dev = "cuda"
+        self.p = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in params.items()}
+        self.packed = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
+        B = batch
+        t = {}
+        h = size
+        self.dims = []
+        for i, (c, f) in enumerate(BLOCKS):
+            self.dims.append((c, h, f))
+            for name in ("x", "xn", "out", "delta"):
+                t[f"{name}{i}"] = torch.empty((B, f, h, h), device=dev)
+            t[f"mean{i}"] = torch.empty(f, device=dev)
+            t[f"var{i}"] = torch.empty(f, device=dev)
+            t[f"md{i}"] = torch.empty(f, device=dev)
+            t[f"vd{i}"] = torch.empty(f, device=dev)
+            if i > 0:
+                t[f"dx{i}"] = torch.empty((B, c, h, h), device=dev)
+            if i < len(BLOCKS) - 1:
+                t[f"pool{i}"] = torch.empty((B, f, h // 2, h // 2), device=dev)
+                t[f"pidx{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.int64, device=dev)
+                h //= 2
+        self.final_hw = h
+        F = BLOCKS[-1][1]
+        t["avg"] = torch.empty((B, F), device=dev)
+        t["avg_delta"] = torch.empty((B, F), device=dev)
+        t["logits"] = torch.empty((B, CLASSES), device=dev)
+        t["prob"] = torch.empty((B, CLASSES), device=dev)
+        t["fc_delta"] = torch.empty((B, CLASSES), device=dev)
+        t["sm_delta"] = torch.empty((B, CLASSES), device=dev)
+        t["err"] = torch.empty((B, CLASSES), device=dev)
+        colmax = max(c * 9 * (hh * hh) for (c, hh, f) in self.dims)
+        t["col"] = torch.empty(B * colmax, device=dev)
+        self.t = t
+        torch.cuda.synchronize()
+        self._pack()
+
+    def _pack(self):
+        for i, (c, _, f) in enumerate(self.dims):
+            self.hip.packConvWeights(f, c, 3, self.p[f"w{i}"], self.packed[i])
+
+    # ------------------------------------------------------------- forward
+    def forward(self, x, truth):
+        hip, p, t, B = self.hip, self.p, self.t, self.B
+        self.input = x
+        h = x
+        for i, (c, hh, f) in enumerate(self.dims):
+            n = B * f * hh * hh
+            y = t[f"x{i}"]
+            hip.conv2dForward(B, c, hh, hh, f, 3, 1, 1, h, 0, self.packed[i], None, acLINEAR, y, 0,
+                              weightLayout=WEIGHTS_TAP_MAJOR)
+            hip.meansAndVars(n, f, B, y, 0, t[f"mean{i}"], t[f"var{i}"])
+            bm = float(np.float32(self.bnm))
+            keep = float(np.float32(1) - np.float32(self.bnm))
+            hip.scale(f, keep, p[f"rm{i}"], 1)
+            hip.axpy(f, bm, t[f"mean{i}"], 0, 1, p[f"rm{i}"], 0, 1)
+            hip.scale(f, keep, p[f"rv{i}"], 1)
+            hip.axpy(f, bm, t[f"var{i}"], 0, 1, p[f"rv{i}"], 0, 1)
+            xn, out = t[f"xn{i}"], t[f"out{i}"]
+            hip.copy(n, y, 0, 1, xn, 0, 1)
+            hip.blockNormalize(n, xn, 0, f, t[f"mean{i}"], t[f"var{i}"], B)
+            hip.copy(n, xn, 0, 1, out, 0, 1)
+            hip.forwardScale(n, out, 0, f, p[f"s{i}"], 1, B)
+            hip.forwardBias(n, out, 0, f, p[f"b{i}"], 1, B)
+            hip.ActivateArray(n, out, 0, acLEAKY)
+            if i < len(self.dims) - 1:
+                ph = hh // 2
+                hip.forwardMaxPool(B, f, ph, ph, out, f, hh, hh, 2, 2, 0, 2, t[f"pidx{i}"], t[f"pool{i}"])
+                h = t[f"pool{i}"]
+            else:
+                h = out
+        F, hw = BLOCKS[-1][1], self.final_hw
+        hip.avgPoolForward(B, F, hw, hw, h, t["avg"])
+        hip.gemm(False, True, B, CLASSES, F, 1.0, t["avg"], 0, F, p["fw"], 0, F, 0.0, t["logits"], 0, CLASSES)
+        hip.forwardBias(B * CLASSES, t["logits"], 0, CLASSES, p["fb"], 1, B)
+        hip.softmaxBatch(CLASSES, t["logits"], 0, B, CLASSES, 1, CLASSES, 1, 1.0, t["prob"], 0)
+        self.truth = truth
+        hip.crossEntropySoftmax(B * CLASSES, t["prob"], truth, t["sm_delta"], t["err"])
+
+    # ------------------------------------------------------------ backward
+    def backward(self):
+        hip, p, t, B = self.hip, self.p, self.t, self.B
+        F, hw = BLOCKS[-1][1], self.final_hw
+        nfc = B * CLASSES
+        # softmax backward: net.delta (zeroed each forward) += delta
+        hip.copy(nfc, t["sm_delta"], 0, 1, t["fc_delta"], 0, 1)
+        # connected backward
+        hip.clamp(nfc, 1.0, t["fc_delta"], t["fc_delta"])
+        hip.backwardBias(CLASSES, p["u_fb"], nfc, t["fc_delta"], 0, 1, B)
+        hip.gemm(True, False, CLASSES, F, B, 1.0, t["fc_delta"], 0, CLASSES, t["avg"], 0, F, 1.0, p["u_fw"], 0, F)
+        hip.gemm(False, False, B, F, CLASSES, 1.0, t["fc_delta"], 0, CLASSES, p["fw"], 0, F, 0.0, t["avg_delta"], 0, F)
+        # avgpool backward into the last block's zeroed delta
+        last = len(self.dims) - 1
+        d = t[f"delta{last}"]
+        hip.fill(B * F * hw * hw, d, 0, 0.0, 1)
+        hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
+        col = t["col"]
+        for i in range(last, -1, -1):
+            c, hh, f = self.dims[i]
+            n = B * f * hh * hh
+            d = t[f"delta{i}"]
+            hip.DeriveArray(n, t[f"out{i}"], 0, acLEAKY, d)
+            # batchNormBack
+            hip.addDots(n, f, B, t[f"xn{i}"], d, 0, p[f"u_s{i}"])
+            hip.forwardScale(n, d, 0, f, p[f"s{i}"], 1, B)
+            hip.meansAndVarsDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
+            hip.normalizeDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
+            # conv weight gradient: im2col of the layer input, then sum_b delta_b * col_b^T
+            src = self.input if i == 0 else t[f"pool{i - 1}"]
+            K, L = c * 9, hh * hh
+            hip.im2colStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, 0, col, K * L, 0, B)
+            hip.gemmNTBatchReduce(f, K, L, 1.0, d, 0, L, f * L, col, 0, L, K * L, 1.0, p[f"u_w{i}"], 0, K, B)
+            if i == 0:
+                break  # state.delta is nil for the first layer
+            # input delta: col_b = W^T * delta_b, then col2im into a zeroed delta
+            hip.gemmStridedBatched(True, False, K, L, f, 1.0, p[f"w{i}"], 0, K, 0, d, 0, L, f * L, 0.0, col, 0, L,
+                                   K * L, B)
+            dx = t[f"dx{i}"]
+            hip.fill(B * c * hh * hh, dx, 0, 0.0, 1)
+            hip.col2imStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx, c * hh * hh, 0, B)
+            # maxpool backward into the previous block's zeroed delta
+            pc, phh, pf = self.dims[i - 1]
+            prev = t[f"delta{i - 1}"]
+            hip.fill(B * pf * phh * phh, prev, 0, 0.0, 1)
+            hip.backwardMaxPool(B, pf, phh // 2, phh // 2, prev, t[f"pidx{i - 1}"], dx)
+
+    # -------------------------------------------------------------- update
+    def update(self):
+        hip, p, B = self.hip, self.p, self.B
+        lr, m, dec = self.lr, self.momentum, self.decay
+        for i in range(len(self.dims)):
+            hip.sgdUpdate(p[f"w{i}"].numel(), lr, B, m, dec, p[f"w{i}"], p[f"u_w{i}"])
+            hip.paramUpdate(p[f"b{i}"].numel(), lr, B, m, p[f"b{i}"], p[f"u_b{i}"])
+            hip.paramUpdate(p[f"s{i}"].numel(), lr, B, m, p[f"s{i}"], p[f"u_s{i}"])
+        hip.paramUpdate(CLASSES, lr, B, m, p["fb"], p["u_fb"])
+        hip.sgdUpdate(p["fw"].numel(), lr, B, m, dec, p["fw"], p["u_fw"])
+        self._pack()
+
+    def step(self, x, truth):
+        self.forward(x, truth)
+        self.backward()
+        self.update()
+
+    def cost(self):
+        """Sum of the softmax cross-entropy errors of the last forward
+        (TSoftmaxLayer cost[0] = loss.Sum(), read by TNNet.cost)."""
+        self.hip.finish()
+        err = self.t["err"].cpu().numpy()
+        return np.float32(err.astype(np.float64).sum())
+
+    def host(self, name):
+        self.hip.finish()
+        src = self.p if name in self.p else self.t
+        return src[name].cpu().numpy()

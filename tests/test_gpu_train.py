@@ -1,0 +1,206 @@
+"""GPU parity of the training-direction kernels and of the config-3 training
+step (conv-BN-leaky x3, maxpool, avgpool, connected, softmax cross-entropy,
+SGD) against the CPU oracle (oracle/trainref.py) on identical inputs.
+
+Bit-exact: element-wise kernels given identical inputs (normalize_delta,
+clamp, avgpool backward, cross-entropy delta, the fused SGD / parameter
+updates, which are the reference's fused multiply-adds) and integer-valued
+weight-gradient GEMMs.  Per-tensor max|g - r| / max|r| for reductions and
+GEMMs (accumulation order differs from the reference's AVX sums)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import refcpu as R
+from oracle import trainref as T
+from tensorium_amd import synth, trainnet
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def D(a):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    torch.cuda.synchronize()
+    return t
+
+
+def H(t, hip):
+    hip.finish()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("shape", [(128, 32, 32, 32), (4, 3, 5, 7), (2, 130, 1, 1)])
+def test_means_vars(hip, shape):
+    case(f"means_vars {shape}")
+    x = synth.normal(301, shape, 2.0) + np.float32(1)
+    B, Cc = shape[:2]
+    m_ref, v_ref = T.means_vars(x, Cc, B)
+    dm, dv = (torch.empty(Cc, device="cuda") for _ in range(2))
+    hip.meansAndVars(x.size, Cc, B, D(x), 0, dm, dv)
+    assert R.rel_err(H(dm, hip), m_ref) <= TOL
+    assert R.rel_err(H(dv, hip), v_ref) <= TOL
+
+
+def test_bn_backward_kernels(hip):
+    case("means_vars_delta / normalize_delta / add_dots")
+    B, Cc, Hh = 16, 24, 9
+    x = synth.normal(302, (B, Cc, Hh, Hh), 1.5) + np.float32(0.3)
+    d = synth.normal(303, (B, Cc, Hh, Hh))
+    mean, var = T.means_vars(x, Cc, B)
+    md_ref, vd_ref = T.means_vars_delta(d, x, mean, var, B)
+    dx, dd = D(x), D(d)
+    dmean, dvar = D(mean), D(var)
+    dmd, dvd = (torch.empty(Cc, device="cuda") for _ in range(2))
+    hip.meansAndVarsDelta(d.size, Cc, B, dd, dx, 0, dmean, dvar, dmd, dvd)
+    assert R.rel_err(H(dmd, hip), md_ref) <= TOL
+    assert R.rel_err(H(dvd, hip), vd_ref) <= TOL
+    # normalize_delta is element-wise: bit-exact given the oracle's md / vd
+    ref = T.normalize_delta(d, x, mean, var, md_ref, vd_ref, B)
+    hip.normalizeDelta(d.size, Cc, B, dd, dx, 0, dmean, dvar, D(md_ref), D(vd_ref))
+    assert np.array_equal(H(dd, hip), ref)
+    acc0 = synth.normal(304, (Cc,))
+    ref = T.add_dots(acc0, x, d, B)
+    dacc = D(acc0)
+    hip.addDots(x.size, Cc, B, dx, D(d), 0, dacc)
+    assert R.rel_err(H(dacc, hip), ref) <= TOL
+
+
+def test_softmax_cross_entropy_clamp(hip):
+    case("softmax / cross-entropy / clamp")
+    B = 300
+    logits = synth.normal(305, (B, 10), 4.0)
+    lab = (synth.splitmix64(306, B) % np.uint64(10)).astype(np.int64)
+    truth = np.zeros((B, 10), np.float32)
+    truth[np.arange(B), lab] = 1
+    p_ref = T.softmax_batch(logits)
+    dp = torch.empty((B, 10), device="cuda")
+    hip.softmaxBatch(10, D(logits), 0, B, 10, 1, 10, 1, 1.0, dp, 0)
+    p = H(dp, hip)
+    assert np.max(np.abs(p - p_ref) / np.maximum(p_ref, 1e-30)) <= 1e-6
+    delta_ref, err_ref = T.cross_entropy(p, truth)
+    dd, de = torch.empty_like(dp), torch.empty_like(dp)
+    hip.crossEntropySoftmax(B * 10, dp, D(truth), dd, de)
+    assert np.array_equal(H(dd, hip), delta_ref)
+    assert R.rel_err(H(de, hip), err_ref) <= 1e-6
+    big = synth.normal(307, (1000,), 3.0)
+    db = D(big)
+    hip.clamp(1000, 1.0, db, db)
+    assert np.array_equal(H(db, hip), T.clamp(big, -1, 1))
+
+
+def test_avgpool(hip):
+    case("avgpool fwd/bwd")
+    x = synth.normal(308, (7, 20, 8, 8))
+    ref = T.avgpool_fwd(x)
+    dy = torch.empty((7, 20), device="cuda")
+    hip.avgPoolForward(7, 20, 8, 8, D(x), dy)
+    assert R.rel_err(H(dy, hip), ref) <= TOL
+    g = synth.normal(309, (7, 20))
+    base = synth.normal(310, x.shape)
+    ref = T.avgpool_bwd(base.copy(), g)
+    db = D(base)
+    hip.avgPoolBackward(7, 20, 8, 8, D(g), db)
+    assert np.array_equal(H(db, hip), ref)
+
+
+def test_sgd_param_update_bit_exact(hip):
+    case("sgd / param update")
+    w = synth.normal(311, (4097,))
+    wu = synth.normal(312, (4097,), 0.1)
+    w_ref, wu_ref = T.sgd_update(w, wu, 1e-3, 128, 0.9, 1e-4)
+    dw, dwu = D(w), D(wu)
+    hip.sgdUpdate(4097, 1e-3, 128, 0.9, 1e-4, dw, dwu)
+    assert np.array_equal(H(dw, hip), w_ref) and np.array_equal(H(dwu, hip), wu_ref)
+    p_ref, pu_ref = T.param_update(w, wu, 1e-3, 128, 0.9)
+    dw, dwu = D(w), D(wu)
+    hip.paramUpdate(4097, 1e-3, 128, 0.9, dw, dwu)
+    assert np.array_equal(H(dw, hip), p_ref) and np.array_equal(H(dwu, hip), pu_ref)
+
+
+@pytest.mark.parametrize("B,F,K,L", [(128, 32, 27, 1024), (128, 64, 288, 256), (3, 40, 70, 48), (2, 5, 9, 30)])
+def test_wgrad_gemm(hip, B, F, K, L):
+    """sum_b delta_b * col_b^T accumulated into dW (beta 1), vs the
+    reference's per-image NT SGEMM loop; L = 30 takes the per-image path."""
+    case(f"wgrad B{B} F{F} K{K} L{L}")
+    A = synth.normal(313, (B, F, L))
+    Bm = synth.normal(314, (B, K, L))
+    C0 = synth.normal(315, (F, K))
+    ref = C0.copy()
+    for b in range(B):
+        R.sgemm(0, 1, F, K, L, 1.0, A[b], L, Bm[b], L, 1.0, ref, K)
+    dC = D(C0)
+    hip.gemmNTBatchReduce(F, K, L, 1.0, D(A), 0, L, F * L, D(Bm), 0, L, K * L, 1.0, dC, 0, K, B)
+    assert R.rel_err(H(dC, hip), ref) <= TOL
+    # integer-valued data: every partial sum is exact, so any order is bit-exact
+    Ai = np.floor(synth.uniform(316, (B, F, L), -4, 4)).astype(np.float32)
+    Bi = np.floor(synth.uniform(317, (B, K, L), -4, 4)).astype(np.float32)
+    ref = np.zeros((F, K), np.float32)
+    for b in range(B):
+        R.sgemm(0, 1, F, K, L, 1.0, Ai[b], L, Bi[b], L, 1.0, ref, K)
+    dC = torch.zeros((F, K), device="cuda")
+    hip.gemmNTBatchReduce(F, K, L, 1.0, D(Ai), 0, L, F * L, D(Bi), 0, L, K * L, 1.0, dC, 0, K, B)
+    assert np.array_equal(H(dC, hip), ref)
+
+
+def _batch(seed, B):
+    x = synth.uniform(seed, (B, 3, 32, 32))
+    lab = (synth.splitmix64(seed + 1, B) % np.uint64(10)).astype(np.int64)
+    truth = np.zeros((B, 10), np.float32)
+    truth[np.arange(B), lab] = 1
+    return x, truth
+
+
+@pytest.mark.parametrize("B", [128, 8])
+def test_cifar_train_step(hip, B):
+    """One full trainEpoch iteration (forward, backward, update) on the device
+    vs the oracle from identical parameters and inputs: loss, BN statistics,
+    every gradient accumulator, the conv2/conv3 input deltas and the updated
+    parameters, per tensor."""
+    case(f"cifar train step B{B}")
+    params = trainnet.init_params()
+    x, truth = _batch(320, B)
+    ref = T.CifarStep(params)
+    loss_ref = ref.forward(x, truth)
+    ref.backward()
+    gpu = trainnet.CifarTrainer(hip, params, B)
+    dx, dt = D(x), D(truth)
+    gpu.forward(dx, dt)
+    gpu.backward()
+    loss = gpu.cost()
+    assert abs(float(loss) - float(loss_ref)) <= TOL * abs(float(loss_ref))
+    for i in range(3):
+        assert R.rel_err(gpu.host(f"mean{i}"), ref.t[f"mean{i}"]) <= TOL, f"mean{i}"
+        assert R.rel_err(gpu.host(f"var{i}"), ref.t[f"var{i}"]) <= TOL, f"var{i}"
+        assert R.rel_err(gpu.host(f"rm{i}"), ref.p[f"rm{i}"]) <= TOL, f"rolling mean {i}"
+        assert R.rel_err(gpu.host(f"out{i}"), ref.t[f"out{i}"]) <= TOL, f"out{i}"
+        assert R.rel_err(gpu.host(f"u_w{i}"), ref.p[f"u_w{i}"]) <= TOL, f"dW{i}"
+        assert R.rel_err(gpu.host(f"u_s{i}"), ref.p[f"u_s{i}"]) <= TOL, f"dScale{i}"
+        assert np.all(gpu.host(f"u_b{i}") == 0)
+    for i in (1, 2):
+        assert R.rel_err(gpu.host(f"dx{i}"), ref.t[f"dx{i}"]) <= TOL, f"input delta of conv{i + 1}"
+    assert R.rel_err(gpu.host("u_fw"), ref.p["u_fw"]) <= TOL
+    assert R.rel_err(gpu.host("u_fb"), ref.p["u_fb"]) <= TOL
+    ref.update(B)
+    gpu.update()
+    for k in ("w0", "w1", "w2", "s0", "s1", "s2", "fw", "fb", "u_w1", "u_fw"):
+        assert R.rel_err(gpu.host(k), ref.p[k]) <= TOL, k
+
+
+def test_cifar_train_loss_falls(hip):
+    """Several device steps on one batch: the loss decreases (descent)."""
+    case("cifar train loss falls")
+    B = 32
+    x, truth = _batch(330, B)
+    gpu = trainnet.CifarTrainer(hip, trainnet.init_params(), B, lr=0.1)
+    dx, dt = D(x), D(truth)
+    losses = []
+    for _ in range(5):
+        gpu.step(dx, dt)
+        losses.append(float(gpu.cost()))
+    assert np.all(np.isfinite(losses)) and losses[-1] < losses[0]

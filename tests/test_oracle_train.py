@@ -1,0 +1,155 @@
+"""Pins of the training-mode oracle (oracle/trainref.py) on the CPU.
+
+Each restated routine is checked against something that does not retype its
+formula: float64 closed forms, torch autograd of the same layer (conv,
+pooling, connected, softmax cross-entropy), and for the batch-norm backward
+the autograd gradient of the reference's forward plus the closed-form term
+by which the reference's backward formula differs from it."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import refcpu as R
+from oracle import trainref as T
+from tensorium_amd import synth
+
+torch.set_default_dtype(torch.float64)
+
+
+def test_means_vars_closed_form():
+    x = synth.normal(201, (4, 6, 5, 7), 2.0) + np.float32(3)
+    m, v = T.means_vars(x, 6, 4)
+    x64 = x.astype(np.float64).transpose(1, 0, 2, 3).reshape(6, -1)
+    assert np.allclose(m, x64.mean(axis=1), rtol=1e-6, atol=0)
+    assert np.allclose(v, x64.var(axis=1, ddof=1), rtol=2e-6, atol=0)  # unbiased (S - 1)
+    # a biased-variance restatement would fail: the factor is S/(S-1) = 140/139
+    assert not np.allclose(v, x64.var(axis=1, ddof=0), rtol=1e-3, atol=0)
+
+
+def _bn_ref_backward(dy, x, groups):
+    """Oracle's BN backward on fp32 inputs (means_vars_delta + normalize_delta)."""
+    nch = x.shape[1]
+    mean, var = T.means_vars(x, nch, groups)
+    md, vd = T.means_vars_delta(dy, x, mean, var, groups)
+    return T.normalize_delta(dy, x, mean, var, md, vd, groups), mean, var, vd
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 2, 2), (3, 4, 5, 5)])
+def test_bn_backward_vs_autograd(shape):
+    """dx_ref = dx_exact - (x - mu) * 2*vd / (m*(m-1)) where dx_exact is the
+    autograd gradient of y = (x - mean)/sqrt(var_unbiased) (the reference's
+    forward) and vd the reference's variance_delta: its backward uses 2/m
+    where the exact gradient of an unbiased variance has 2/(m-1)."""
+    B, Cc = shape[:2]
+    x = synth.normal(202, shape, 1.5) + np.float32(0.5)
+    dy = synth.normal(203, shape)
+    got, mean, var, vd = _bn_ref_backward(dy, x, B)
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    mu = xt.mean(dim=(0, 2, 3), keepdim=True)
+    vu = ((xt - mu) ** 2).sum(dim=(0, 2, 3), keepdim=True) / (xt[:, 0].numel() - 1)
+    y = (xt - mu) / torch.sqrt(vu)
+    y.backward(torch.tensor(dy.astype(np.float64)))
+    m = B * int(np.prod(shape[2:]))
+    x64 = x.astype(np.float64)
+    mu64 = x64.mean(axis=(0, 2, 3), keepdims=True)
+    v64 = ((x64 - mu64) ** 2).sum(axis=(0, 2, 3), keepdims=True) / (m - 1)
+    vd64 = ((dy.astype(np.float64) * (x64 - mu64)).sum(axis=(0, 2, 3), keepdims=True) * -0.5 * v64 ** -1.5)
+    expect = xt.grad.numpy() - (x64 - mu64) * 2 * vd64 / (m * (m - 1))
+    assert R.rel_err(got, expect) < 1e-5
+    # the exact gradient itself differs by O(1/m): the correction term is pinned
+    assert R.rel_err(got, xt.grad.numpy()) > 1e-4
+
+
+def test_add_dots_and_sums():
+    a = synth.normal(204, (3, 4, 9))
+    b = synth.normal(205, (3, 4, 9))
+    d = T.add_dots(np.ones(4, np.float32), a, b, 3)
+    assert np.allclose(d, 1 + (a.astype(np.float64) * b).sum(axis=(0, 2)), rtol=1e-6)
+    s = T.add_sums(np.zeros(4, np.float32), a, 3)
+    assert np.allclose(s, a.astype(np.float64).sum(axis=(0, 2)), rtol=1e-6, atol=1e-6)
+
+
+def test_softmax_cross_entropy_vs_autograd():
+    logits = synth.normal(206, (5, 10), 3.0)
+    lab = np.array([1, 0, 9, 4, 4])
+    truth = np.zeros((5, 10), np.float32)
+    truth[np.arange(5), lab] = 1
+    p = T.softmax_batch(logits)
+    assert np.allclose(p, torch.softmax(torch.tensor(logits.astype(np.float64)), 1).numpy(), rtol=1e-6)
+    delta, err = T.cross_entropy(p, truth)
+    lt = torch.tensor(logits.astype(np.float64), requires_grad=True)
+    loss = -(torch.tensor(truth.astype(np.float64)) * torch.log_softmax(lt, 1)).sum()
+    loss.backward()
+    # darknet convention: delta = -dLoss/dlogits = t - p
+    assert np.allclose(delta, -lt.grad.numpy(), atol=1e-6)
+    assert abs(err.sum() - loss.item()) < 1e-5 * loss.item()
+    assert np.all(err[truth == 0] == 0)
+
+
+def test_softmax_row_sum_order():
+    """sum in row order: 1 + 2^-24 (x8) stays 1 in fp32, so every term is
+    divided by exactly the first element's exp."""
+    x = np.zeros((1, 9), np.float32)
+    x[0, 0] = 20.0  # e^0 = 1 for the max; the rest are e^-20 ~ 2.06e-9 < 2^-24
+    p = T.softmax_batch(x)
+    assert p[0, 0] == np.float32(1.0)
+
+
+def test_avgpool_vs_torch():
+    x = synth.normal(207, (3, 5, 4, 4))
+    y = T.avgpool_fwd(x)
+    assert np.allclose(y, x.astype(np.float64).mean(axis=(2, 3)), rtol=1e-6, atol=1e-7)
+    g = synth.normal(208, (3, 5))
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    (xt.mean(dim=(2, 3)) * torch.tensor(g.astype(np.float64))).sum().backward()
+    d = T.avgpool_bwd(np.zeros_like(x), g)
+    assert np.allclose(d, xt.grad.numpy(), rtol=1e-6)
+
+
+def test_conv_backward_vs_autograd():
+    B, Cc, H, F = 2, 3, 6, 4
+    x = synth.normal(209, (B, Cc, H, H))
+    Wt = synth.normal(210, (F, Cc * 9), 0.3)
+    g = synth.normal(211, (B, F, H, H))
+    dW, dx = T.conv_backward(x, Wt, g, np.zeros((F, Cc * 9), np.float32), 3, 1, 1)
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    wt = torch.tensor(Wt.astype(np.float64).reshape(F, Cc, 3, 3), requires_grad=True)
+    (torch.nn.functional.conv2d(xt, wt, padding=1) * torch.tensor(g.astype(np.float64))).sum().backward()
+    assert R.rel_err(dW, wt.grad.numpy().reshape(F, -1)) < 1e-6
+    assert R.rel_err(dx, xt.grad.numpy()) < 1e-6
+
+
+def test_axpy_is_fused():
+    """fma(a, x, y) with a*x + y exact only when fused: a = 1 + 2^-12,
+    x = 1 + 2^-12, y = -(1 + 2^-11): fused gives 2^-24, mul-then-add 0."""
+    a = np.float32(1 + 2 ** -12)
+    y = T.axpy(np.array([-(1 + 2 ** -11)], np.float32), a, np.array([1 + 2 ** -12], np.float32))
+    assert y[0] == np.float32(2 ** -24)
+
+
+def test_sgd_update_closed_form():
+    w = synth.normal(212, (50,))
+    wu = synth.normal(213, (50,), 0.1)
+    w2, wu2 = T.sgd_update(w, wu, 1e-3, 128, 0.9, 1e-4)
+    a1 = np.float64(np.float32(-np.float32(1e-4)) * np.float32(128))
+    a2 = np.float64(np.float32(1e-3) / np.float32(128))
+    u = wu.astype(np.float64) + a1 * w
+    assert np.allclose(w2, w.astype(np.float64) + a2 * u, rtol=1e-6, atol=1e-9)
+    assert np.allclose(wu2, 0.9 * u, rtol=1e-6)
+
+
+def test_cifar_step_learns():
+    """The oracle step is a descent step: on a fixed batch the loss falls,
+    and the first loss is close to B*ln(10) for small random logits."""
+    p = T.cifar_init()
+    B = 16
+    x = synth.uniform(214, (B, 3, 32, 32))
+    lab = (synth.splitmix64(215, B) % np.uint64(10)).astype(np.int64)
+    truth = np.zeros((B, 10), np.float32)
+    truth[np.arange(B), lab] = 1
+    net = T.CifarStep(p, lr=0.1)
+    losses = [float(net.step(x, truth)) for _ in range(4)]
+    assert abs(losses[0] / B - np.log(10)) < 0.5
+    assert losses[-1] < losses[0]
+    # BN biases never receive gradient (reference quirk), scales do
+    assert np.all(net.p["b0"] == 0) and np.any(net.p["s0"] != 1)
