@@ -142,6 +142,151 @@ def cpu_baseline(layers, weights, budget_s=12.0):
 COPY_BYTES = 64 << 20
 
 
+def time_events(hip, fn, reps):
+    """Average ms of fn() over reps calls, HIP events on the library stream."""
+    e0, e1 = hip.eventCreate(), hip.eventCreate()
+    hip.eventRecord(e0)
+    for _ in range(reps):
+        fn()
+    hip.eventRecord(e1)
+    ms = hip.eventElapsed(e0, e1) / reps
+    hip.eventDestroy(e0)
+    hip.eventDestroy(e1)
+    return ms
+
+
+def extra_single_conv(hip):
+    """Config 1: one conv layer forward, batch 1, 3x416x416 -> 16 filters 3x3
+    s1 p1, weights N(0, 0.05), bias 0, leaky 0.1 (GEMM M=16, N=173056, K=27)."""
+    import numpy as np
+    import torch
+
+    from tensorium_amd import synth
+    from tensorium_amd.nnhip import acLEAKY
+
+    x = torch.from_numpy(synth.uniform(1, (1, 3, 416, 416))).cuda()
+    w = torch.from_numpy(synth.normal(2, (16, 27), 0.05)).cuda()
+    b = torch.zeros(16, dtype=torch.float32, device="cuda")
+    out = torch.empty((1, 16, 416, 416), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def fn():
+        hip.conv2dForward(1, 3, 416, 416, 16, 3, 1, 1, x, 0, w, b, acLEAKY, out, 0)
+
+    for _ in range(3):
+        fn()
+    ms = time_events(hip, fn, 50)
+    flop = 2.0 * 16 * 27 * 416 * 416
+    byts = 4.0 * (3 * 416 * 416 + 16 * 416 * 416 + 16 * 27)
+    del np
+    return {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "us": round(ms * 1e3, 2),
+            "gflops": round(flop / ms / 1e6, 1), "gb_s": round(byts / ms / 1e6, 1),
+            "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4)}
+
+
+def extra_sgemm(hip):
+    """Config 2: C = op(A)*op(B) (beta 0), A and B ~ U[-1, 1), four variants
+    at 4096^3, NN at 8192^3 and the YOLOv3 conv-shaped skinny GEMMs."""
+    import torch
+
+    from tensorium_amd import synth
+
+    cases = [("NN", 4096, 4096, 4096), ("NT", 4096, 4096, 4096), ("TN", 4096, 4096, 4096),
+             ("TT", 4096, 4096, 4096), ("NN", 8192, 8192, 8192), ("NN", 64, 692224, 288),
+             ("NN", 256, 43264, 1152), ("NN", 1024, 2704, 4608)]
+    res = []
+    for var, M, N, K in cases:
+        ta, tb = var[0] == "T", var[1] == "T"
+        A = torch.from_numpy(synth.uniform(11, (M * K,), -1, 1)).cuda()
+        B = torch.from_numpy(synth.uniform(12, (K * N,), -1, 1)).cuda()
+        C = torch.empty(M * N, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        lda, ldb = (M if ta else K), (K if tb else N)
+
+        def fn():
+            hip.gemm(ta, tb, M, N, K, 1.0, A, 0, lda, B, 0, ldb, 0.0, C, 0, N)
+
+        fn()
+        reps = 3 if M * N * K >= 8192 ** 3 else 10
+        ms = time_events(hip, fn, reps)
+        res.append({"variant": var, "M": M, "N": N, "K": K, "ms": round(ms, 4),
+                    "tflops": round(2.0 * M * N * K / ms / 1e9, 2),
+                    "frac": round(2.0 * M * N * K / ms * 1e3 / PEAK_FP32_MFMA, 4)})
+        del A, B, C
+        torch.cuda.empty_cache()
+    return res
+
+
+def extra_train(hip, steps, warmup, cpu_steps):
+    """Config 3: one training step (forward + backward + SGD update) of the
+    conv-BN-leaky x3 / pool / connected / softmax-CE network on synthetic
+    3x32x32 U[0,1) images with one-hot labels, batch 128, replayed from a HIP
+    graph; the CPU oracle's step timed beside it."""
+    import numpy as np
+    import torch
+
+    from tensorium_amd import synth, trainnet
+
+    B = 128
+    x = synth.uniform(21, (B, 3, 32, 32))
+    lab = (synth.splitmix64(22, B) % np.uint64(10)).astype(np.int64)
+    truth = np.zeros((B, 10), np.float32)
+    truth[np.arange(B), lab] = 1
+    params = trainnet.init_params()
+    tr = trainnet.CifarTrainer(hip, params, B)
+    dx, dt = torch.from_numpy(x).cuda(), torch.from_numpy(truth).cuda()
+    torch.cuda.synchronize()
+    for _ in range(max(1, warmup)):
+        tr.step(dx, dt)
+    loss0 = float(tr.cost())
+    tr.capture(dx, dt)
+    tr.replay()
+    tr.hip.finish()
+    ms = time_events(hip, tr.replay, steps)
+    loss1 = float(tr.cost())
+    tr.release_graph()
+    hip.useTorchStream()
+    flop = 0
+    for (c, f), hw in zip(trainnet.BLOCKS, (32, 16, 8)):
+        flop += 2 * f * 9 * c * hw * hw * B * (2 if c == 3 else 3)  # fwd + dW (+ dX except layer 0)
+    out = {"workload": "config-3 CNN train step (fwd+bwd+SGD), batch 128, 3x32x32", "ms_per_step": round(ms, 4),
+           "img_s": round(B / ms * 1e3, 1), "gflop_per_step": round(flop / 1e9, 3),
+           "gflops": round(flop / ms / 1e6, 1), "launch": "hip_graph",
+           "loss_first": round(loss0, 3), "loss_after": round(loss1, 3)}
+    if cpu_steps:
+        from oracle import refcpu as R
+        from oracle import trainref as T
+
+        R.set_threads(min(16, os.cpu_count() or 4))
+        ref = T.CifarStep(params)
+        ref.step(x, truth)
+        t0 = time.perf_counter()
+        for _ in range(cpu_steps):
+            ref.step(x, truth)
+        cms = (time.perf_counter() - t0) / cpu_steps * 1e3
+        out["cpu_baseline"] = {"value": round(cms, 1), "unit": "ms/step", "cores": R.get_threads(), "kind": "port",
+                               "sample": f"{cpu_steps} oracle steps (C AVX2 GEMM/im2col/col2im + numpy BN/softmax)"}
+    return out
+
+
+def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
+    """Config 5: YOLOv3-608 inference at batch 32 (HIP graph replay)."""
+    import torch
+
+    from tensorium_amd import darknet, synth
+
+    net = darknet.Network(hip, layers608, batch, weights608)
+    x = torch.from_numpy(synth.uniform(9, (batch, 3, size, size))).cuda()
+    torch.cuda.synchronize()
+    ms, _ = time_forward(hip, net, x, steps, warmup, graph=True)
+    ms /= steps
+    flop = darknet.conv_flops(layers608) * batch
+    del net, x
+    torch.cuda.empty_cache()
+    return {"workload": f"YOLOv3-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
+            "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+
+
 def counter_pass(hip, net, args):
     """Warm-up forwards (autotuning), a fence, then exactly one forward and one
     copy of COPY_BYTES: the dispatches a counter run attributes.  The copy
@@ -152,14 +297,14 @@ def counter_pass(hip, net, args):
     from tensorium_amd import synth
 
     x = torch.from_numpy(synth.uniform(7, (args.batch, 3, args.size, args.size))).cuda()
-    src = torch.rand(COPY_BYTES // 4, device="cuda")
+    src = torch.rand(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     for _ in range(max(1, args.warmup)):
         net.forward(x)
     hip.finish()
     torch.cuda.synchronize()
-    marker = torch.zeros(64, device="cuda")
+    marker = torch.zeros(64, dtype=torch.float32, device="cuda")
     hip.fill(1, marker, 0, 0.0, 1)  # fill_kernel: marks the start of the attributed region
     log("counter pass: timed region starts")
     net.forward(x)
@@ -180,6 +325,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the other BASELINE configurations (single conv, SGEMM sweep, training step, "
+                         "YOLOv3-608 batch 32)")
     ap.add_argument("--counter-pass", action="store_true",
                     help="for rocprofv3 --pmc: tune, then run ONE eager forward and a 64 MiB copy "
                          "(the calibration kernel), print nothing else")
@@ -245,6 +393,26 @@ def main():
                          f"reference path, {threads} threads, BN folded)"}
         log(f"cpu baseline: {v:.3f} img/s on {threads} threads")
 
+    extras = None
+    if not args.no_extras:
+        extras = {}
+
+        def guarded(name, fn):
+            try:
+                extras[name] = fn()
+                log(f"{name}: {extras[name]}")
+            except Exception as e:  # an extra must not hide the headline figure
+                extras[name] = {"error": f"{type(e).__name__}: {e}"}
+                log(f"{name} failed: {e}")
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+
+        guarded("single_conv_416", lambda: extra_single_conv(hip))
+        guarded("sgemm", lambda: extra_sgemm(hip))
+        guarded("train_cifar_b128", lambda: extra_train(hip, 50, 2, 0 if args.no_cpu_baseline else 2))
+        _, l608 = darknet.load_cfg("yolov3.cfg", 608, 608)
+        guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2))
+
     out = {
         "metric": METRIC,
         "value": round(img_s, 2),
@@ -274,6 +442,7 @@ def main():
                      "launches_per_step": round(d["launches"]),
                      "flop_per_launch": round(d["flop"] / max(d["launches"], 1))},
         "cpu_baseline": cpu,
+        "other_configs": extras,
     }
     print(json.dumps(out), flush=True)
     del np

@@ -80,28 +80,28 @@ class CifarTrainer:
         for i, (c, f) in enumerate(BLOCKS):
             self.dims.append((c, h, f))
             for name in ("x", "xn", "out", "delta"):
-                t[f"{name}{i}"] = torch.empty((B, f, h, h), device=dev)
-            t[f"mean{i}"] = torch.empty(f, device=dev)
-            t[f"var{i}"] = torch.empty(f, device=dev)
-            t[f"md{i}"] = torch.empty(f, device=dev)
-            t[f"vd{i}"] = torch.empty(f, device=dev)
+                t[f"{name}{i}"] = torch.empty((B, f, h, h), dtype=torch.float32, device=dev)
+            t[f"mean{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
+            t[f"var{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
+            t[f"md{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
+            t[f"vd{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
             if i > 0:
-                t[f"dx{i}"] = torch.empty((B, c, h, h), device=dev)
+                t[f"dx{i}"] = torch.empty((B, c, h, h), dtype=torch.float32, device=dev)
             if i < len(BLOCKS) - 1:
-                t[f"pool{i}"] = torch.empty((B, f, h // 2, h // 2), device=dev)
+                t[f"pool{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.float32, device=dev)
                 t[f"pidx{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.int64, device=dev)
                 h //= 2
         self.final_hw = h
         F = BLOCKS[-1][1]
-        t["avg"] = torch.empty((B, F), device=dev)
-        t["avg_delta"] = torch.empty((B, F), device=dev)
-        t["logits"] = torch.empty((B, CLASSES), device=dev)
-        t["prob"] = torch.empty((B, CLASSES), device=dev)
-        t["fc_delta"] = torch.empty((B, CLASSES), device=dev)
-        t["sm_delta"] = torch.empty((B, CLASSES), device=dev)
-        t["err"] = torch.empty((B, CLASSES), device=dev)
+        t["avg"] = torch.empty((B, F), dtype=torch.float32, device=dev)
+        t["avg_delta"] = torch.empty((B, F), dtype=torch.float32, device=dev)
+        t["logits"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
+        t["prob"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
+        t["fc_delta"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
+        t["sm_delta"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
+        t["err"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
         colmax = max(c * 9 * (hh * hh) for (c, hh, f) in self.dims)
-        t["col"] = torch.empty(B * colmax, device=dev)
+        t["col"] = torch.empty(B * colmax, dtype=torch.float32, device=dev)
         self.t = t
         torch.cuda.synchronize()
         self._pack()
@@ -211,6 +211,29 @@ class CifarTrainer:
         self.forward(x, truth)
         self.backward()
         self.update()
+
+    def capture(self, x, truth):
+        """Records one step (forward, backward, update) over the fixed input
+        buffers into a HIP graph on the library's own stream; run one eager
+        step first so autotuning and scratch allocation are done.  Each
+        replay() then trains on the same buffers (contents may change)."""
+        hip = self.hip
+        self.torch.cuda.synchronize()
+        hip.resetStream()
+        hip.finish()
+        hip.graphBegin()
+        try:
+            self.step(x, truth)
+        finally:
+            self.graph = hip.graphEnd()
+
+    def replay(self):
+        self.hip.graphLaunch(self.graph)
+
+    def release_graph(self):
+        if getattr(self, "graph", None):
+            self.hip.graphDestroy(self.graph)
+            self.graph = None
 
     def cost(self):
         """Sum of the softmax cross-entropy errors of the last forward

@@ -13,8 +13,6 @@ from oracle import refcpu as R
 from oracle import trainref as T
 from tensorium_amd import synth
 
-torch.set_default_dtype(torch.float64)
-
 
 def test_means_vars_closed_form():
     x = synth.normal(201, (4, 6, 5, 7), 2.0) + np.float32(3)
