@@ -26,35 +26,14 @@
 #include <vector>
 
 #include "common.hpp"
+#include "conv_args.hpp"
+#include "conv_lean.hpp"
 #include "gemm_core.hpp"
 
 namespace tnh {
+namespace conv {
 namespace {
 
-struct ConvArgs {
-  ConvGeom g;
-  const float* w;
-  int64_t wBytes;
-  const float* bias;
-  const float* res;
-  int64_t rBatchStride;
-  float* out;
-  int64_t outBatchStride;
-  int64_t F;
-  int act;
-  int tilesM, tilesN;
-  int splits;       // split-K factor (gridDim.y)
-  int64_t kChunk;   // K range per split (multiple of BK)
-  float* part;      // splits > 1: partial sums [splits][F][N]
-};
-
-__device__ inline float apply_act(float v, int act) {
-  if (act == TNH_AC_LEAKY) return v < 0.f ? 0.1f * v : v;  // leaky_array (nactivation.pas:234)
-  if (act == TNH_AC_LOGISTIC) return 1.f / (1.f + expf(-v));
-  return v;
-}
-
-enum Mode { kGatherRef3 = 0, kGatherTap3 = 1, kGatherRef1 = 2, kTap3 = 3, k1x1 = 4 };
 
 template <class Cfg, int MODE, bool VA, bool VB>
 struct KernelTraits;
@@ -94,46 +73,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-  if (a.splits > 1) {  // raw partial sums; conv_splitk_reduce applies the epilogue
-    float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.F * a.g.N;
-#pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j) {
-      const int64_t n = n0 + wn * Cfg::WTN + j * 32 + (lane & 31);
-      if (n >= a.g.N) continue;
-#pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t f = m0 + wm * Cfg::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (f < a.F) part[f * a.g.N + n] = acc[i][j][r];
-        }
-    }
-    return;
-  }
-
-  // Epilogue: each lane owns FN output columns; their image / pixel split is
-  // computed once per column.
-  const int64_t OHW = a.g.OHW;
-#pragma unroll
-  for (int j = 0; j < Cfg::FN; ++j) {
-    const int64_t n = n0 + wn * Cfg::WTN + j * 32 + (lane & 31);
-    if (n >= a.g.N) continue;
-    const int64_t b = n / OHW, p = n - b * OHW;
-    float* out = a.out + b * a.outBatchStride + p;
-    const float* res = a.res ? a.res + b * a.rBatchStride + p : nullptr;
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t f = m0 + wm * Cfg::WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (f >= a.F) continue;
-        float v = acc[i][j][r];
-        if (a.bias) v = v + a.bias[f];
-        v = apply_act(v, a.act);
-        if (res) v = v + res[f * OHW];
-        out[f * OHW] = v;
-      }
-  }
+  conv_store<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -160,12 +100,6 @@ struct DirectCfg {
   static constexpr int BM = WM * WTM, BN = WN * WTN, BK = 16;
 };
 
-__device__ inline float buf_ld1s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-}
-__device__ inline f32x4 buf_ld4s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
 
 template <class D, int KH, int KW>
 __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) {
@@ -189,7 +123,7 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int64_t row = m0 + 32 * i + r;
-    aOff[i] = row < a.F ? static_cast<uint32_t>((row * K + 8 * h) * 4) : kOOB;
+    aOff[i] = sel_off(row < a.F, static_cast<uint32_t>((row * K + 8 * h) * 4));
   }
   // B: lane (r, h) of column block j reads channels c0 + 8h .. c0 + 8h + 7
   // of input pixel (iy0 + ky, ix0 + kx) of its column's image.  cOff is the
@@ -238,7 +172,7 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
       const int iy = iy0[j] + ky, ix = ix0[j] + kx;
       const bool ok = cOk[j] && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
                       static_cast<unsigned>(ix) < static_cast<unsigned>(W);
-      const uint32_t vo = ok ? cOff[j] + tapOff : kOOB;
+      const uint32_t vo = sel_off(ok, cOff[j] + tapOff);
 #pragma unroll
       for (int s = 0; s < 8; ++s) B[j][s] = buf_ld1s(xr, vo, static_cast<uint32_t>(c0 + s) * HW4);
     }
@@ -296,43 +230,7 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
     if (i + 1 < nq) compute(A1, B1);
   }
 
-  if (a.splits > 1) {  // raw partial sums; conv_splitk_reduce applies the epilogue
-    float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.F * a.g.N;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t n = n0 + 32 * j + r;
-      if (n >= a.g.N) continue;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int64_t f = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-          if (f < a.F) part[f * a.g.N + n] = acc[i][j][e];
-        }
-    }
-    return;
-  }
-  const int64_t OHW = a.g.OHW;
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int64_t n = n0 + 32 * j + r;
-    if (n >= a.g.N) continue;
-    const int64_t b = n / OHW, p = n - b * OHW;
-    float* out = a.out + b * a.outBatchStride + p;
-    const float* res = a.res ? a.res + b * a.rBatchStride + p : nullptr;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t f = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (f >= a.F) continue;
-        float v = acc[i][j][e];
-        if (a.bias) v = v + a.bias[f];
-        v = apply_act(v, a.act);
-        if (res) v = v + res[f * OHW];
-        out[f * OHW] = v;
-      }
-  }
+  conv_store<FM, FN>(a, acc, m0, n0, lane);
 }
 
 // Sums the split-K partials in split order (deterministic) and applies the
@@ -371,20 +269,33 @@ using Dir7 = DirectCfg<2, 1, 1, 4, 4>;
 using Dir8 = DirectCfg<2, 2, 2, 2, 3>;
 using Dir9 = DirectCfg<2, 2, 1, 4, 3>;
 using Dir10 = DirectCfg<1, 2, 4, 1, 4>;
+// lean tiles (conv_lean.hpp: tile M x N x K depth, waves M x N, occupancy)
+using Lean11 = LeanCfg<64, 64, 32, 2, 2, 4>;
+using Lean12 = LeanCfg<64, 128, 32, 2, 2, 3>;
+using Lean13 = LeanCfg<128, 64, 32, 2, 2, 3>;
+using Lean14 = LeanCfg<128, 128, 32, 2, 2, 2>;
+using Lean15 = LeanCfg<64, 64, 64, 2, 2, 2>;
+using Lean16 = LeanCfg<64, 32, 32, 2, 1, 6>;
+using Lean17 = LeanCfg<128, 64, 32, 4, 2, 2>;
+using Lean18 = LeanCfg<64, 128, 32, 2, 4, 2>;
+using Lean19 = LeanCfg<128, 128, 32, 4, 2, 2>;
 
+enum CfgKind { kLds = 0, kDirect = 1, kLean = 2 };
 struct CfgInfo {
   int BM, BN, BK;
   float eff;  // relative per-CU throughput used by the cost model
   int perCU;  // resident workgroups per CU assumed by the cost model
-  bool direct;
+  int kind;
 };
-constexpr int kNumCfg = 11;
-constexpr int kFirstDirect = 6;
+constexpr int kNumCfg = 20;
 const CfgInfo kCfgs[kNumCfg] = {
-    {64, 64, 32, 1.00f, 4, false},   {64, 64, 16, 1.00f, 8, false}, {128, 64, 16, 0.97f, 5, false},
-    {128, 128, 16, 0.95f, 2, false}, {64, 128, 32, 0.97f, 3, false}, {64, 128, 16, 0.95f, 5, false},
-    {256, 64, 16, 0.95f, 3, true},   {64, 128, 16, 0.95f, 4, true}, {128, 128, 16, 0.95f, 3, true},
-    {64, 256, 16, 0.95f, 3, true},   {128, 64, 16, 0.95f, 4, true},
+    {64, 64, 32, 1.00f, 4, kLds},     {64, 64, 16, 1.00f, 8, kLds},     {128, 64, 16, 0.97f, 5, kLds},
+    {128, 128, 16, 0.95f, 2, kLds},   {64, 128, 32, 0.97f, 3, kLds},    {64, 128, 16, 0.95f, 5, kLds},
+    {256, 64, 16, 0.95f, 3, kDirect}, {64, 128, 16, 0.95f, 4, kDirect}, {128, 128, 16, 0.95f, 3, kDirect},
+    {64, 256, 16, 0.95f, 3, kDirect}, {128, 64, 16, 0.95f, 4, kDirect}, {64, 64, 32, 1.15f, 4, kLean},
+    {64, 128, 32, 1.10f, 3, kLean},   {128, 64, 32, 1.10f, 3, kLean},   {128, 128, 32, 1.05f, 2, kLean},
+    {64, 64, 64, 1.10f, 2, kLean},    {64, 32, 32, 1.10f, 6, kLean},    {128, 64, 32, 1.10f, 2, kLean},
+    {64, 128, 32, 1.10f, 2, kLean},   {128, 128, 32, 1.05f, 2, kLean},
 };
 
 template <class Cfg>
@@ -402,6 +313,17 @@ int grid_for(ConvArgs& a, dim3& grid) {
   }
   grid = dim3(static_cast<unsigned>(tm * tn), static_cast<unsigned>(a.splits));
   return TNH_OK;
+}
+
+// Second launch of a split-K convolution: sums the partials and applies the
+// epilogue (nothing to do without split-K).
+int launch_reduce(const ConvArgs& a, hipStream_t s) {
+  if (a.splits <= 1) return TNH_OK;
+  const int64_t total = a.F * a.g.N;
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s,
+                     a);
+  return launch_status("conv_splitk_reduce");
 }
 
 template <class Cfg, int MODE>
@@ -425,14 +347,7 @@ int launch_mode(ConvArgs a, bool va, bool vb, hipStream_t s) {
     hipLaunchKernelGGL((conv_kernel<Cfg, MODE, false, false>), grid, dim3(Cfg::NT), 0, s, a);
   }
   if (int st = launch_status("conv_kernel")) return st;
-  if (a.splits > 1) {
-    const int64_t total = a.F * a.g.N;
-    const int64_t blocks = (total + 255) / 256;
-    hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
-                       s, a);
-    return launch_status("conv_splitk_reduce");
-  }
-  return TNH_OK;
+  return launch_reduce(a, s);
 }
 
 template <class Cfg>
@@ -446,6 +361,20 @@ int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
   }
 }
 
+template <class Cfg>
+int launch_lean(ConvArgs a, int mode, bool vb, hipStream_t s) {
+  dim3 grid;
+  if (int st = grid_for<Cfg>(a, grid)) return st;
+  if (mode == kTap3)
+    hipLaunchKernelGGL((conv_lean_kernel<Cfg, kTap3, false>), grid, dim3(Cfg::NT), 0, s, a);
+  else if (vb)
+    hipLaunchKernelGGL((conv_lean_kernel<Cfg, k1x1, true>), grid, dim3(Cfg::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_lean_kernel<Cfg, k1x1, false>), grid, dim3(Cfg::NT), 0, s, a);
+  if (int st = launch_status("conv_lean_kernel")) return st;
+  return launch_reduce(a, s);
+}
+
 template <class D>
 int launch_direct(ConvArgs a, int mode, hipStream_t s) {
   dim3 grid;
@@ -455,14 +384,7 @@ int launch_direct(ConvArgs a, int mode, hipStream_t s) {
   else
     hipLaunchKernelGGL((conv_direct_kernel<D, 1, 1>), grid, dim3(D::NT), 0, s, a);
   if (int st = launch_status("conv_direct_kernel")) return st;
-  if (a.splits > 1) {
-    const int64_t total = a.F * a.g.N;
-    const int64_t blocks = (total + 255) / 256;
-    hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
-                       s, a);
-    return launch_status("conv_splitk_reduce");
-  }
-  return TNH_OK;
+  return launch_reduce(a, s);
 }
 
 int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
@@ -477,7 +399,16 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s
     case 7: return launch_direct<Dir7>(a, mode, s);
     case 8: return launch_direct<Dir8>(a, mode, s);
     case 9: return launch_direct<Dir9>(a, mode, s);
-    default: return launch_direct<Dir10>(a, mode, s);
+    case 10: return launch_direct<Dir10>(a, mode, s);
+    case 11: return launch_lean<Lean11>(a, mode, vb, s);
+    case 12: return launch_lean<Lean12>(a, mode, vb, s);
+    case 13: return launch_lean<Lean13>(a, mode, vb, s);
+    case 14: return launch_lean<Lean14>(a, mode, vb, s);
+    case 15: return launch_lean<Lean15>(a, mode, vb, s);
+    case 16: return launch_lean<Lean16>(a, mode, vb, s);
+    case 17: return launch_lean<Lean17>(a, mode, vb, s);
+    case 18: return launch_lean<Lean18>(a, mode, vb, s);
+    default: return launch_lean<Lean19>(a, mode, vb, s);
   }
 }
 
@@ -538,15 +469,18 @@ int g_forced_cfg = -1;
 // The register-direct kernels need whole 16-channel chunks inside one tap
 // and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
 bool cfg_valid(int c, int mode, int64_t C, bool va) {
-  if (kCfgs[c].direct) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
+  if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
+  if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;
   if (mode == kTap3) return C % kCfgs[c].BK == 0;
   return true;
 }
 
 }  // namespace
+}  // namespace conv
 }  // namespace tnh
 
 using namespace tnh;
+using namespace tnh::conv;
 
 extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw, int64_t pH, int64_t pW,
                                        int64_t sY, int64_t sX, int64_t* OH, int64_t* OW) {
@@ -559,7 +493,7 @@ extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t
 
 extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
-  TNH_ARG(forcedConfig >= -1 && forcedConfig % 16 < kNumCfg && forcedConfig / 16 <= 16,
+  TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 16,
           "conv2d_set_autotune: config %d", forcedConfig);
   g_autotune = enable != 0;
   g_forced_cfg = forcedConfig;
@@ -675,8 +609,8 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 16, mode, C, va))
-      return run({g_forced_cfg % 16, g_forced_cfg / 16 > 1 ? g_forced_cfg / 16 : 1});
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va))
+      return run({g_forced_cfg % 64, g_forced_cfg / 64 > 1 ? g_forced_cfg / 64 : 1});
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return run(it->second);
     if (g_autotune && !aliased) {

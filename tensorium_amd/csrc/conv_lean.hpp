@@ -1,0 +1,387 @@
+// Lean implicit-GEMM convolution on fp32 MFMA (gfx950).
+//
+// The fastest conv kernel family of the library.  What makes it lean:
+//   * Both operand panels are k-contiguous in LDS with their 16-byte chunks
+//     XOR-swizzled by row % 8: every LDS access is a conflict-free 16-byte
+//     ds_read/ds_write_b128 and no padding is needed.  The B gather writes 4
+//     consecutive k of one output column per 16-byte store.
+//   * Per-lane global offsets are fixed for the whole K loop; what varies
+//     along K is wave-uniform and rides in the buffer instruction's scalar
+//     offset.  The 3x3 padding test is a per-lane 9-bit tap mask computed
+//     once, so a K panel costs a few vector ALU operations instead of two per
+//     load.
+//   * Schedule of panel p (two LDS stages; the loaders' registers hold panel
+//     p+1; the fragments of chunk 0 of panel p are in registers):
+//       chunks 0 .. KCH-2: read the fragments of chunk c+1, then the MFMAs of
+//         chunk c; during chunk 0 the registers of panel p+1 go to the other
+//         stage and the global loads of panel p+2 are issued;
+//       barrier (every wave stored panel p+1 and read all of panel p);
+//       read the fragments of chunk 0 of panel p+1, then the MFMAs of chunk
+//       KCH-1 of panel p.
+//     The other stage held panel p-1, whose last reads precede the previous
+//     barrier, so overwriting it during panel p is safe; panel p+1 is read
+//     only after this panel's barrier.  A wave reaches the barrier with the
+//     last chunk's MFMAs still to issue, and the first fragment reads of the
+//     next panel hide behind them.  The panel loop is unrolled over the two
+//     stages (LDS addresses are per-lane constants plus immediates) and the
+//     last panels are peeled, so the steady-state body is one basic block.
+//
+// Requirements (checked by the host): K % BK == 0 (tap-major 3x3 with
+// C % BK == 0, or 1x1 stride 1 with C % BK == 0) and 16-byte weight rows.
+#pragma once
+#include "conv_args.hpp"
+
+namespace tnh {
+namespace conv {
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int OCC_>
+struct LeanCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, OCC = OCC_;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int KCH = BK / 16;
+  static_assert(FM >= 1 && FN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
+  static_assert(BK % 32 == 0 && KCH % 2 == 0, "BK: 32 or 64");
+};
+
+// k-contiguous panel [ROWS][BK] (floats) whose 16-byte chunks are
+// XOR-swizzled by row % 8.  Eight consecutive rows at one chunk index, or
+// one row's chunks, touch distinct banks.
+template <int ROWS, int BK>
+struct SwzPanel {
+  static constexpr int SIZE = ROWS * BK;
+  __device__ static inline int chunk(int row, int q) { return row * BK + 4 * (q ^ (row & 7)); }
+};
+
+// Weights [F][K] row-major, 16-byte loads.  Thread t owns chunk t % (BK/4)
+// of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 8 == 0, so every row of a
+// thread has the same swizzle).
+template <class Cfg>
+struct LeanA {
+  static constexpr int BK = Cfg::BK, NT = Cfg::NT;
+  static constexpr int QPR = BK / 4;
+  static constexpr int ROWSTEP = NT / QPR;
+  static constexpr int PER = Cfg::BM / ROWSTEP;
+  using L = SwzPanel<Cfg::BM, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % QPR == 0 && Cfg::BM % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0, "LeanA split");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t voff[PER];
+  int ldsOff;
+  f32x4 reg[PER];
+
+  __device__ inline void init(const float* w, int64_t wBytes, int64_t K, int64_t F, int64_t m0, int tid) {
+    rsrc = make_rsrc(w, wBytes);
+    const int row = tid / QPR, kq = tid % QPR;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int64_t gr = m0 + row + v * ROWSTEP;
+      voff[v] = sel_off(gr < F, static_cast<uint32_t>((gr * K + kq * 4) * 4));
+    }
+    ldsOff = L::chunk(row, kq);
+  }
+  __device__ inline void load(int64_t k0) {
+    const uint32_t so = static_cast<uint32_t>(k0) * 4u;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) reg[v] = buf_ld4s(rsrc, voff[v], so);
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) *reinterpret_cast<lds_f4*>(stage + ldsOff + v * ROWSTEP * BK) = reg[v];
+  }
+};
+
+// Tap-major 3x3 gather (k = tap*C + c, a panel inside one tap): thread t
+// owns output column t % BN and the k-quads t / BN + j * QSTEP; a quad is 4
+// consecutive channels of one input pixel (4 loads HW floats apart), stored
+// with one 16-byte LDS write.
+template <class Cfg, int KH, int KW>
+struct LeanTapB {
+  static constexpr int BK = Cfg::BK, BN = Cfg::BN, NT = Cfg::NT;
+  static constexpr int QSTEP = NT / BN, NQ = (BK / 4) / QSTEP;
+  using L = SwzPanel<BN, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % BN == 0 && (BK / 4) % QSTEP == 0 && NQ >= 1 && KH * KW <= 32, "LeanTapB split");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t colOff;   // byte offset of (image, iy0, ix0, channel 4 * first quad), modulo 2^32
+  uint32_t tapMask;  // bit ky*KW + kx: that tap reads inside the image
+  uint32_t HW4;
+  int C, W;
+  int ldsOff[NQ];
+  float reg[NQ][4];
+
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    W = g.W;
+    HW4 = static_cast<uint32_t>(g.H) * static_cast<uint32_t>(g.W) * 4u;
+    const int col = tid % BN, q0 = tid / BN;
+    const int64_t n = n0 + col;
+    const bool colOk = n < g.N;
+    const int64_t nn = colOk ? n : 0;
+    const int64_t b = nn / g.OHW;
+    const int p = static_cast<int>(nn - b * g.OHW);
+    const int oy = p / g.OW, ox = p - (p / g.OW) * g.OW;
+    const int iy0 = oy * g.sY - g.pH, ix0 = ox * g.sX - g.pW;
+    colOff = static_cast<uint32_t>((b * g.xBatchStride + static_cast<int64_t>(iy0) * g.W + ix0) * 4) +
+             static_cast<uint32_t>(4 * q0) * HW4;
+    uint32_t m = 0;
+#pragma unroll
+    for (int ky = 0; ky < KH; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < KW; ++kx) {
+        const bool in = static_cast<unsigned>(iy0 + ky) < static_cast<unsigned>(g.H) &&
+                        static_cast<unsigned>(ix0 + kx) < static_cast<unsigned>(g.W);
+        m |= (colOk && in ? 1u : 0u) << (ky * KW + kx);
+      }
+    tapMask = m;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) ldsOff[j] = L::chunk(col, q0 + j * QSTEP);
+  }
+  __device__ inline void load(int64_t k0) {
+    const int kk = static_cast<int>(k0);
+    const int tap = kk / C;  // uniform
+    const int c0 = kk - tap * C;
+    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+    const uint32_t vo = sel_off((tapMask >> tap) & 1u, colOff + static_cast<uint32_t>(ky * W + kx) * 4u);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        reg[j][e] = buf_ld1s(rsrc, vo, static_cast<uint32_t>(c0 + 4 * j * QSTEP + e) * HW4);
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+      *reinterpret_cast<lds_f4*>(stage + ldsOff[j]) = f32x4{reg[j][0], reg[j][1], reg[j][2], reg[j][3]};
+  }
+};
+
+// 1x1 stride 1: B[k = c][n = b*HW + p] = x_b[c][p].  Scalar: as LeanTapB
+// without the tap (4 loads HW apart per quad).  VEC (HW % 4 == 0, batch
+// stride % 4 == 0, x aligned): thread t owns columns 4 * (t % (BN/4)) .. +3
+// and k-quads t / (BN/4) + j * QSTEP; it loads a 4 (k) x 4 (column) block
+// with four 16-byte loads and stores its transpose, one 16-byte LDS write
+// per column.
+template <class Cfg, bool VEC>
+struct Lean1x1B {
+  static constexpr int BK = Cfg::BK, BN = Cfg::BN, NT = Cfg::NT;
+  static constexpr int CPT = VEC ? 4 : 1;
+  static constexpr int TPR = BN / CPT;
+  static constexpr int QSTEP = NT / TPR, NQ = (BK / 4) / QSTEP;
+  using L = SwzPanel<BN, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % TPR == 0 && (BK / 4) % QSTEP == 0 && NQ >= 1, "Lean1x1B split");
+  using Reg = typename std::conditional<VEC, f32x4, float>::type;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t voff, HW4;
+  int ldsOff[NQ][CPT];
+  Reg reg[NQ][4];
+
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    const int64_t HW = g.OHW;
+    HW4 = static_cast<uint32_t>(HW) * 4u;
+    const int col = (tid % TPR) * CPT, q0 = tid / TPR;
+    const int64_t n = n0 + col;
+    const bool colOk = n < g.N;
+    const int64_t nn = colOk ? n : 0;
+    const int64_t b = nn / HW;
+    voff = sel_off(colOk, static_cast<uint32_t>((b * g.xBatchStride + (nn - b * HW) + 4 * q0 * HW) * 4));
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) ldsOff[j][c] = L::chunk(col + c, q0 + j * QSTEP);
+  }
+  __device__ inline void load(int64_t k0) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t so = static_cast<uint32_t>(static_cast<int>(k0) + 4 * j * QSTEP + e) * HW4;
+        if constexpr (VEC)
+          reg[j][e] = buf_ld4s(rsrc, voff, so);
+        else
+          reg[j][e] = buf_ld1s(rsrc, voff, so);
+      }
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<lds_f4*>(stage + ldsOff[j][c]) =
+              f32x4{reg[j][0][c], reg[j][1][c], reg[j][2][c], reg[j][3][c]};
+      } else {
+        *reinterpret_cast<lds_f4*>(stage + ldsOff[j][0]) = f32x4{reg[j][0], reg[j][1], reg[j][2], reg[j][3]};
+      }
+    }
+  }
+};
+
+template <class Cfg, class AL, class BL>
+struct LeanLoop {
+  static constexpr int FM = Cfg::FM, FN = Cfg::FN, KCH = Cfg::KCH, BK = Cfg::BK;
+  static constexpr int STAGE = AL::SIZE + BL::SIZE;
+  static constexpr int LDS_FLOATS = 2 * STAGE;
+
+  // Eight k per lane and 32x32 block as two 16-byte halves: step s uses
+  // element s % 4 of half s / 4 (k = 16*chunk + 8*(lane/32) + s).
+  struct Frag {
+    f32x4 a[FM][2];
+    f32x4 b[FN][2];
+  };
+
+  // Per-lane float offsets inside a 32-row block of either panel (rows are a
+  // multiple of 32 apart, so row % 8 is lane % 8): lo[c][e] addresses half e
+  // of chunk c.
+  struct Lanes {
+    int lo[KCH][2];
+    int aRow, bRow;  // first row of the wave's blocks, times BK
+  };
+
+  __device__ static inline void read(const lds_t* stage, int c, const Lanes& L, Frag& f) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        f.a[i][e] = *reinterpret_cast<const lds_f4*>(stage + L.aRow + i * 32 * BK + L.lo[c][e]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        f.b[j][e] = *reinterpret_cast<const lds_f4*>(stage + AL::SIZE + L.bRow + j * 32 * BK + L.lo[c][e]);
+  }
+
+  __device__ static inline void mma(const Frag& f, f32x16 (&acc)[FM][FN]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[i][s >> 2][s & 3], f.b[j][s >> 2][s & 3], acc[i][j], 0,
+                                                           0, 0);
+  }
+
+  // Panel p in stage S, fragments of its chunk 0 in f0.  MORE: panel p+1
+  // exists (its registers are stored to the other stage); MORE2: panel p+2
+  // exists (its loads are issued).
+  template <int S, bool MORE, bool MORE2>
+  __device__ static inline void panel(AL& al, BL& bl, int64_t kNext2, lds_t* lds, Frag& f0, Frag& f1, const Lanes& L,
+                                      f32x16 (&acc)[FM][FN]) {
+    const lds_t* cur = lds + S * STAGE;
+    lds_t* nxt = lds + (1 - S) * STAGE;
+#pragma unroll
+    for (int c = 0; c < KCH - 1; ++c) {
+      Frag& fc = (c & 1) ? f1 : f0;
+      Frag& fn = (c & 1) ? f0 : f1;
+      read(cur, c + 1, L, fn);
+      if (c == 0 && MORE) {
+        al.store(nxt);
+        bl.store(nxt + AL::SIZE);
+        if (MORE2) {
+          al.load(kNext2);
+          bl.load(kNext2);
+        }
+      }
+      mma(fc, acc);
+    }
+    if (MORE) {
+      __syncthreads();
+      read(nxt, 0, L, f0);
+    }
+    mma(f1, acc);  // chunk KCH-1 (KCH is even)
+  }
+
+  __device__ static inline void exec(AL& al, BL& bl, int64_t kBegin, int64_t nk, lds_t* lds,
+                                     f32x16 (&acc)[FM][FN]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+    const int r = lane & 31, h = lane >> 5;
+    Lanes L;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) L.lo[c][e] = r * BK + 4 * ((4 * c + 2 * h + e) ^ (r & 7));
+    L.aRow = wm * Cfg::WTM * BK;
+    L.bRow = wn * Cfg::WTN * BK;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    if (nk <= 0) return;
+    al.load(kBegin);
+    bl.load(kBegin);
+    al.store(lds);
+    bl.store(lds + AL::SIZE);
+    if (nk > 1) {
+      al.load(kBegin + BK);
+      bl.load(kBegin + BK);
+    }
+    __syncthreads();
+    Frag f0, f1;
+    read(lds, 0, L, f0);
+    int64_t p = 0;
+    for (; p + 3 < nk; p += 2) {
+      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, acc);
+      panel<1, true, true>(al, bl, kBegin + (p + 3) * BK, lds, f0, f1, L, acc);
+    }
+    const int64_t rest = nk - p;  // 1, 2 or 3 panels left; p is even (stage 0)
+    if (rest == 3) {
+      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, acc);
+      panel<1, true, false>(al, bl, 0, lds, f0, f1, L, acc);
+      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+    } else if (rest == 2) {
+      panel<0, true, false>(al, bl, 0, lds, f0, f1, L, acc);
+      panel<1, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+    } else {
+      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+    }
+  }
+};
+
+template <class Cfg, int MODE, bool VB>
+struct LeanTraits;
+template <class Cfg, bool VB>
+struct LeanTraits<Cfg, kTap3, VB> {
+  using BL = LeanTapB<Cfg, 3, 3>;
+};
+template <class Cfg, bool VB>
+struct LeanTraits<Cfg, k1x1, VB> {
+  // the 4x4 blocks of the vector loader must tile the panel exactly
+  static constexpr bool kVec = VB && (Cfg::BK / 4) % (Cfg::NT / (Cfg::BN / 4)) == 0;
+  using BL = Lean1x1B<Cfg, kVec>;
+};
+
+template <class Cfg, int MODE, bool VB>
+__global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a) {
+  using AL = LeanA<Cfg>;
+  using BL = typename LeanTraits<Cfg, MODE, VB>::BL;
+  using Loop = LeanLoop<Cfg, AL, BL>;
+  __shared__ __attribute__((aligned(16))) float smem[Loop::LDS_FLOATS];
+  lds_t* lds = (lds_t*)smem;
+
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+  AL al;
+  al.init(a.w, a.wBytes, a.g.K, a.F, m0, threadIdx.x);
+  BL bl;
+  bl.init(a.g, n0, threadIdx.x);
+  f32x16 acc[Cfg::FM][Cfg::FN];
+  const int64_t kBegin = blockIdx.y * a.kChunk;
+  const int64_t kEnd = min(a.g.K, kBegin + a.kChunk);
+  Loop::exec(al, bl, kBegin, (kEnd - kBegin) / Cfg::BK, lds, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  conv_store<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+}
+
+}  // namespace conv
+}  // namespace tnh

@@ -68,11 +68,32 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const float* p, int64_t bytes
   const int n = static_cast<int>(bytes < kMaxBufBytes ? bytes : kMaxBufBytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, n, 0x00020000);
 }
+// `off` when `ok`, else kOOB (the load reads 0).  The selected offset passes
+// through an empty asm statement: without it the compiler pushes the select
+// into the buffer load and splits the load into two divergent branches, whose
+// join then waits for every outstanding load (s_waitcnt vmcnt(0)) in the
+// middle of the prefetch.
+__device__ inline uint32_t sel_off(bool ok, uint32_t off) {
+  uint32_t r = ok ? off : kOOB;
+  asm("" : "+v"(r));
+  return r;
+}
+
 __device__ inline float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 __device__ inline f32x4 buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+// Loads with a per-lane offset `voff` plus a wave-uniform offset `soff` (an
+// SGPR operand of the instruction).  Callers keep every valid voff + soff
+// inside the buffer and give invalid lanes voff = kOOB, so the result does
+// not depend on whether the hardware range check includes soff.
+__device__ inline float buf_ld1s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ inline f32x4 buf_ld4s(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
 // ---------------------------------------------------------------------------
@@ -106,7 +127,8 @@ __device__ inline void read_frag(const lds_t* lds, int row0, int ch, int lane, f
 // K panels into registers (load(k0)) and writes them to an LDS panel
 // (store).  Offsets are 32-bit byte offsets into a buffer resource whose
 // range is at most 2 GiB; per-element work is one add and one select (an
-// invalid element gets kOOB, which the hardware returns as 0).
+// invalid element gets kOOB through sel_off, which the hardware returns as
+// 0).
 // ---------------------------------------------------------------------------
 
 // Dense operand.  Element (row, k) of op(X):
@@ -165,7 +187,7 @@ struct DenseLoader {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const bool ok = rowOk[v] && static_cast<int>(k0) + kIdx[v] < K;
-      const uint32_t off = ok ? off0[v] + koff : kOOB;
+      const uint32_t off = sel_off(ok, off0[v] + koff);
       if constexpr (VEC)
         reg[v] = buf_ld4(rsrc, off);
       else
@@ -269,7 +291,7 @@ struct ConvGatherLoader : ColumnState<BN, BK, NT> {
       const bool ok = S::colOk && k < K && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
                       static_cast<unsigned>(ix) < static_cast<unsigned>(W);
       const uint32_t o = S::colOff + static_cast<uint32_t>(c) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
-      reg[v] = buf_ld1(rsrc, ok ? o : kOOB);
+      reg[v] = buf_ld1(rsrc, sel_off(ok, o));
     }
   }
 
@@ -317,7 +339,7 @@ struct ConvTapLoader : ColumnState<BN, BK, NT> {
                     static_cast<unsigned>(ix) < static_cast<unsigned>(W);
     const uint32_t base = rowOff + static_cast<uint32_t>(c0) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
 #pragma unroll
-    for (int v = 0; v < S::PER; ++v) reg[v] = buf_ld1(rsrc, ok ? base + v * vStride : kOOB);
+    for (int v = 0; v < S::PER; ++v) reg[v] = buf_ld1(rsrc, sel_off(ok, base + v * vStride));
   }
 
   __device__ inline void store(lds_t* lds, int) const {
@@ -376,7 +398,7 @@ struct ConvTapQuadLoader : ColumnState<BN, BK, NT> {
 #pragma unroll
     for (int q = 0; q < Q::NQ; ++q)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) reg[q][e] = buf_ld1(rsrc, ok ? base + q * qStride + e * HW4 : kOOB);
+      for (int e = 0; e < 4; ++e) reg[q][e] = buf_ld1(rsrc, sel_off(ok, base + q * qStride + e * HW4));
   }
 
   __device__ inline void store(lds_t* lds, int) const {
@@ -422,7 +444,7 @@ struct Conv1x1QuadLoader {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const bool ok = colOk && static_cast<int>(k0) + (myQ0 + q * Q::QSTEP) * 4 + e < K;
-        reg[q][e] = buf_ld1(rsrc, ok ? base + q * qStride + e * HW4 : kOOB);
+        reg[q][e] = buf_ld1(rsrc, sel_off(ok, base + q * qStride + e * HW4));
       }
   }
 
@@ -473,7 +495,7 @@ struct Conv1x1Loader {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const bool ok = colOk && static_cast<int>(k0) + myRow0 + v * RSTEP < K;
-      const uint32_t off = ok ? base + static_cast<uint32_t>(v * RSTEP) * HW4 : kOOB;
+      const uint32_t off = sel_off(ok, base + static_cast<uint32_t>(v * RSTEP) * HW4);
       if constexpr (VEC)
         reg[v] = buf_ld4(rsrc, off);
       else

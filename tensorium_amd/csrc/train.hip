@@ -213,7 +213,7 @@ struct SegLoader : DenseLoader<true, VEC, ROWS, BK, NT> {
 #pragma unroll
     for (int v = 0; v < Base::PER; ++v) {
       const bool ok = Base::rowOk[v] && static_cast<int>(k0) + Base::kIdx[v] < Base::K;
-      const uint32_t off = ok ? Base::off0[v] + koff : kOOB;
+      const uint32_t off = sel_off(ok, Base::off0[v] + koff);
       if constexpr (VEC)
         Base::reg[v] = buf_ld4(Base::rsrc, off);
       else

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -200,7 +200,7 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("cfg", [0, 6, 8])
+@pytest.mark.parametrize("cfg", [0, 6, 8, 11])
 @pytest.mark.parametrize("splits", [2, 4, 16])
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 512, 13, 1024, 3, 1), (1, 256, 13, 255, 1, 1), (2, 64, 9, 96, 3, 2)])
 def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
@@ -216,7 +216,7 @@ def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
     packed = torch.empty_like(dW)
     hip.packConvWeights(F, Cc, k, dW, packed)
     dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
-    hip.setConvAutotune(True, 16 * splits + cfg)
+    hip.setConvAutotune(True, CONV_SPLIT_UNIT * splits + cfg)
     try:
         hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
                           weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
