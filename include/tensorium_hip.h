@@ -171,8 +171,8 @@ int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
 /* No reference counterpart: enable (1, default) or disable per-shape
  * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape:
  * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 6..10
- * register-direct, 11..19 lean software-pipelined; a shape invalid for the call
- * falls back to the library's choice) and forcedConfig / 64 the split-K
+ * register-direct, 11..19 lean software-pipelined; a shape invalid for the
+ * call falls back to the library's choice) and forcedConfig / 64 the split-K
  * factor (0 or 1: none); -1 lets the library choose. */
 int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig);
 

@@ -233,6 +233,83 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
   conv_store<FM, FN>(a, acc, m0, n0, lane);
 }
 
+// Few-channel 3x3 convolution (C <= 4, e.g. the RGB input layer): the
+// output is store-bound (F outputs per pixel against 9*C inputs), so instead
+// of a GEMM each thread owns one output pixel, keeps its 9*C window inputs
+// in registers and walks the filters four at a time.  The weights are
+// wave-uniform: they are read through the scalar cache into SGPRs and feed
+// the fused multiply-adds directly.  Every store is coalesced along the
+// pixel row.  Each output is a sequential fused multiply-add chain over k in
+// the reference order k = (c*3 + ky)*3 + kx from 0, padding taps included as
+// zeros: exactly the arithmetic of the reference CPU path (im2col, then the
+// saxpy chain of ntensors.pas:1308-1436), then bias, activation, residual.
+template <int C, bool TAP>
+__global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w) {
+  constexpr int K = 9 * C;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (n >= a.g.N) return;
+  const int F = static_cast<int>(a.F);
+  const int OHW = a.g.OHW, OW = a.g.OW, H = a.g.H, W = a.g.W;
+  const int b = static_cast<int>(n / OHW);
+  const int p = static_cast<int>(n - static_cast<int64_t>(b) * OHW);
+  const int oy = p / OW, ox = p - (p / OW) * OW;
+  const int iy0 = oy * a.g.sY - a.g.pH, ix0 = ox * a.g.sX - a.g.pW;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
+  const uint32_t base = static_cast<uint32_t>(static_cast<int64_t>(b) * a.g.xBatchStride * 4);
+  float in[K];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const int iy = iy0 + ky, ix = ix0 + kx;
+        const bool ok = static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                        static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+        in[(c * 3 + ky) * 3 + kx] =
+            buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
+      }
+  float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
+  const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
+  auto finish = [&](int f, float acc) {
+    float v = acc;
+    if (a.bias) v = v + a.bias[f];
+    v = apply_act(v, a.act);
+    if (res) v = v + res[static_cast<int64_t>(f) * OHW];
+    out[static_cast<int64_t>(f) * OHW] = v;
+  };
+  // weight of filter f at reference index k = c*9 + t
+  auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
+  int f = 0;
+  for (; f + 4 <= F; f += 4) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt(f + q, k), in[k], acc[q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) finish(f + q, acc[q]);
+  }
+  for (; f < F; ++f) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc = fmaf(wt(f, k), in[k], acc);
+    finish(f, acc);
+  }
+}
+
+template <bool TAP>
+int launch_smallc(const ConvArgs& a, hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
+  switch (a.g.C) {
+    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+  }
+  return launch_status("conv_smallc_kernel");
+}
+
 // Sums the split-K partials in split order (deterministic) and applies the
 // epilogue: one thread per output element, consecutive threads along n.
 __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
@@ -468,7 +545,8 @@ int g_forced_cfg = -1;
 
 // The register-direct kernels need whole 16-channel chunks inside one tap
 // and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
-bool cfg_valid(int c, int mode, int64_t C, bool va) {
+bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO) {
+  if (kCfgs[c].kind == kLean && !smallIO) return false;
   if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
   if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;
   if (mode == kTap3) return C % kCfgs[c].BK == 0;
@@ -552,6 +630,8 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   a.rBatchStride = rBatchStride;
   a.out = out + outOff;
   a.outBatchStride = outBatchStride;
+  a.outBytes = ((batch - 1) * outBatchStride + F * OH * OW) * 4;
+  a.resBytes = residual ? ((batch - 1) * rBatchStride + F * OH * OW) * 4 : 0;
   a.F = F;
   a.act = act;
 
@@ -566,15 +646,30 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   else
     mode = kGatherRef3;
   const bool va = aligned16(a.w) && K % 4 == 0;
+  // the buffer-store epilogue of the lean kernels addresses out, residual and
+  // one split's partial sums through 2 GiB buffer resources
+  const bool smallIO = a.outBytes <= kMaxBufBytes && a.resBytes <= kMaxBufBytes && F * N * 4 <= kMaxBufBytes;
   const bool vb = is1x1 && aligned16(a.g.x) && (OH * OW) % 4 == 0 && (batch == 1 || xBatchStride % 4 == 0);
   if (mode == kTap3 && !va) mode = kGatherTap3;
+  if (kh == 3 && C <= 4 && N / 256 < INT32_MAX) {
+    // few input channels: per-pixel kernel (no tile choice to tune); a forced
+    // tile configuration still selects the GEMM path (tests of every tile)
+    bool forced;
+    {
+      std::lock_guard<std::mutex> lk(g_tune_mu);
+      forced = g_forced_cfg >= 0;
+    }
+    if (!forced)
+      return weightLayout == TNH_WEIGHTS_TAP_MAJOR ? launch_smallc<true>(a, cx->stream)
+                                                   : launch_smallc<false>(a, cx->stream);
+  }
 
   // Candidates: every valid tile shape, and for shapes that leave the CUs
   // under-filled also split-K factors (partial sums in the context
   // workspace, reduced in fixed order).
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
-    if (!cfg_valid(c, mode, C, va)) continue;
+    if (!cfg_valid(c, mode, C, va, smallIO)) continue;
     cands.push_back({c, 1});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
@@ -609,7 +704,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va))
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO))
       return run({g_forced_cfg % 64, g_forced_cfg / 64 > 1 ? g_forced_cfg / 64 : 1});
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return run(it->second);

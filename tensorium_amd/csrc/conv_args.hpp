@@ -26,6 +26,8 @@ struct ConvArgs {
   int splits;       // split-K factor (gridDim.y)
   int64_t kChunk;   // K range per split (multiple of BK)
   float* part;      // splits > 1: partial sums [splits][F][N]
+  int64_t outBytes; // extent of out addressed by the kernel
+  int64_t resBytes; // extent of res addressed by the kernel (0 without residual)
 };
 
 // K walk / B operand of a convolution kernel
@@ -81,6 +83,79 @@ __device__ inline void conv_store(const ConvArgs& a, const f32x16 (&acc)[FM][FN]
         v = apply_act(v, a.act);
         if (res) v = v + res[f * OHW];
         out[f * OHW] = v;
+      }
+  }
+}
+
+__device__ inline void buf_st1s(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
+}
+
+// conv_store through buffer instructions (same results): each lane's
+// column part of an offset is a 32-bit per-lane value, the row part
+// (block i, register r) is wave-uniform and rides in the scalar offset, and
+// an element outside [0, F) x [0, N) gets the lane offset kOOB, whose store
+// the hardware drops, so there are no per-element branches.  The host
+// guarantees that out, res and the split-K partials each span at most 2 GiB.
+template <int FM, int FN>
+__device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM][FN], int64_t m0w, int64_t n0w,
+                                      int lane) {
+  const int h = lane >> 5;
+  const int F = static_cast<int>(a.F);
+  const int rowBase = static_cast<int>(m0w) + 4 * h;  // row of element (i = 0, r = 0)
+  const bool allRows = m0w + FM * 32 <= a.F;          // wave-uniform
+  auto rowOk = [&](int c) { return allRows || rowBase + c < F; };
+  if (a.splits > 1) {
+    const uint32_t N = static_cast<uint32_t>(a.g.N);
+    const int64_t slice = a.F * a.g.N;
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part + static_cast<int64_t>(blockIdx.y) * slice, slice * 4);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int64_t n = n0w + j * 32 + (lane & 31);
+      const uint32_t vo = sel_off(n < a.g.N, (static_cast<uint32_t>(rowBase) * N + static_cast<uint32_t>(n)) * 4u);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = i * 32 + 8 * (r >> 2) + (r & 3);
+          buf_st1s(pr, acc[i][j][r], rowOk(c) ? vo : kOOB, static_cast<uint32_t>(c) * N * 4u);
+        }
+    }
+    return;
+  }
+  const uint32_t OHW = static_cast<uint32_t>(a.g.OHW);
+  const __amdgpu_buffer_rsrc_t outR = make_rsrc(a.out, a.outBytes);
+  const __amdgpu_buffer_rsrc_t resR = make_rsrc(a.res, a.resBytes);
+  float bias[FM][16];
+  if (a.bias) {
+    const __amdgpu_buffer_rsrc_t bR = make_rsrc(a.bias, a.F * 4);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        bias[i][r] = buf_ld1s(bR, static_cast<uint32_t>(rowBase) * 4u,
+                              static_cast<uint32_t>(i * 32 + 8 * (r >> 2) + (r & 3)) * 4u);
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0w + j * 32 + (lane & 31);
+    const bool okN = n < a.g.N;
+    const uint32_t nn = okN ? static_cast<uint32_t>(n) : 0u;
+    const uint32_t b = nn / OHW, p = nn - b * OHW;
+    const uint32_t rowOff = static_cast<uint32_t>(rowBase) * OHW + p;
+    const uint32_t vOut = sel_off(okN, (b * static_cast<uint32_t>(a.outBatchStride) + rowOff) * 4u);
+    const uint32_t vRes = sel_off(okN, (b * static_cast<uint32_t>(a.rBatchStride) + rowOff) * 4u);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = i * 32 + 8 * (r >> 2) + (r & 3);
+        const uint32_t so = static_cast<uint32_t>(c) * OHW * 4u;
+        float v = acc[i][j][r];
+        if (a.bias) v = v + bias[i][r];
+        v = apply_act(v, a.act);
+        if (a.res) v = v + buf_ld1s(resR, vRes, so);
+        buf_st1s(outR, v, rowOk(c) ? vOut : kOOB, so);
       }
   }
 }

@@ -27,7 +27,8 @@
 //     last panels are peeled, so the steady-state body is one basic block.
 //
 // Requirements (checked by the host): K % BK == 0 (tap-major 3x3 with
-// C % BK == 0, or 1x1 stride 1 with C % BK == 0) and 16-byte weight rows.
+// C % BK == 0, or 1x1 stride 1 with C % BK == 0), 16-byte weight rows, and
+// output / residual / split-K partials within 2 GiB each (conv_store_buf).
 #pragma once
 #include "conv_args.hpp"
 
@@ -268,7 +269,7 @@ struct LeanLoop {
 
   // Panel p in stage S, fragments of its chunk 0 in f0.  MORE: panel p+1
   // exists (its registers are stored to the other stage); MORE2: panel p+2
-  // exists (its loads are issued).
+  // exists (its loads are issued, at K offset kNext2).
   template <int S, bool MORE, bool MORE2>
   __device__ static inline void panel(AL& al, BL& bl, int64_t kNext2, lds_t* lds, Frag& f0, Frag& f1, const Lanes& L,
                                       f32x16 (&acc)[FM][FN]) {
@@ -296,8 +297,7 @@ struct LeanLoop {
     mma(f1, acc);  // chunk KCH-1 (KCH is even)
   }
 
-  __device__ static inline void exec(AL& al, BL& bl, int64_t kBegin, int64_t nk, lds_t* lds,
-                                     f32x16 (&acc)[FM][FN]) {
+  __device__ static inline Lanes lanes() {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     const int r = lane & 31, h = lane >> 5;
@@ -308,13 +308,22 @@ struct LeanLoop {
       for (int e = 0; e < 2; ++e) L.lo[c][e] = r * BK + 4 * ((4 * c + 2 * h + e) ^ (r & 7));
     L.aRow = wm * Cfg::WTM * BK;
     L.bRow = wn * Cfg::WTN * BK;
+    return L;
+  }
+
+  __device__ static inline void zero(f32x16 (&acc)[FM][FN]) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-    if (nk <= 0) return;
+  }
+
+  // Loads panel 0 into stage 0 and panel 1 into the registers, then reads
+  // the fragments of chunk 0 of panel 0 (nk panels from kBegin).
+  __device__ static inline void prologue(AL& al, BL& bl, int64_t kBegin, int64_t nk, lds_t* lds, const Lanes& L,
+                                         Frag& f0) {
     al.load(kBegin);
     bl.load(kBegin);
     al.store(lds);
@@ -324,8 +333,16 @@ struct LeanLoop {
       bl.load(kBegin + BK);
     }
     __syncthreads();
-    Frag f0, f1;
     read(lds, 0, L, f0);
+  }
+
+  __device__ static inline void exec(AL& al, BL& bl, int64_t kBegin, int64_t nk, lds_t* lds,
+                                     f32x16 (&acc)[FM][FN]) {
+    const Lanes L = lanes();
+    zero(acc);
+    if (nk <= 0) return;
+    Frag f0, f1;
+    prologue(al, bl, kBegin, nk, lds, L, f0);
     int64_t p = 0;
     for (; p + 3 < nk; p += 2) {
       panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, acc);
@@ -380,7 +397,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-  conv_store<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+  conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
 
 }  // namespace conv

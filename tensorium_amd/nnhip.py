@@ -31,7 +31,8 @@ acLOGISTIC, acLINEAR, acLEAKY = 0, 4, 9
 WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 # number of compiled conv tile configurations (tnh_conv2d_set_autotune ids
 # 0..NUM_CONV_CFGS-1: 0-5 LDS-staged, 6-10 register-direct, 11-19 lean
-# software-pipelined); a forced id is tile + CONV_SPLIT_UNIT * splits
+# software-pipelined); a forced id is
+# tile + CONV_SPLIT_UNIT * splits
 NUM_CONV_CFGS = 20
 CONV_SPLIT_UNIT = 64
 

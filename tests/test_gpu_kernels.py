@@ -200,6 +200,34 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("B,Cc,Hh,F,s,tap,act,resid", [(1, 3, 416, 16, 1, False, acLEAKY, False),
+                                                       (2, 3, 37, 32, 1, True, acLEAKY, True),
+                                                       (1, 1, 9, 5, 2, False, acLINEAR, False),
+                                                       (3, 4, 20, 7, 1, True, acLEAKY, False),
+                                                       (2, 2, 15, 9, 2, True, acLINEAR, True)])
+def test_conv_few_channels_bit_exact(hip, B, Cc, Hh, F, s, tap, act, resid):
+    """C <= 4 3x3 layers (the RGB input layer; config 1 at full size) run the
+    per-pixel kernel, whose sequential FMA chain in the reference k order is
+    the reference CPU arithmetic: equal bit for bit to the oracle."""
+    case(f"conv few-channel B{B} C{Cc} H{Hh} F{F} s{s} tap{tap} act{act} res{resid}")
+    x = synth.uniform(51, (B, Cc, Hh, Hh))
+    Wt = synth.normal(52, (F, Cc * 9), 0.05)
+    b = synth.normal(53, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, 3, s, 1, act)
+    res = synth.normal(54, ref.shape) if resid else None
+    if resid:
+        ref = R.addvv(ref, res)
+    dW = D(Wt)
+    if tap:
+        packed = torch.empty_like(dW)
+        hip.packConvWeights(F, Cc, 3, dW, packed)
+        dW = packed
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, s, 1, D(x), 0, dW, D(b), act, dout, 0,
+                      residual=D(res) if resid else None, weightLayout=WEIGHTS_TAP_MAJOR if tap else 0)
+    assert np.array_equal(H(dout, hip), ref)
+
+
 @pytest.mark.parametrize("cfg", [0, 6, 8, 11])
 @pytest.mark.parametrize("splits", [2, 4, 16])
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 512, 13, 1024, 3, 1), (1, 256, 13, 255, 1, 1), (2, 64, 9, 96, 3, 2)])
