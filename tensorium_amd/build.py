@@ -34,7 +34,8 @@ def sources():
 
 def _compile(src):
     obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    extra = os.environ.get("TNH_HIPCC_FLAGS", "").split()  # e.g. -D switches for kernel variants
+    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
