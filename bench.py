@@ -27,11 +27,11 @@ METRIC = "conv im2col+SGEMM GFLOP/s (% fp32 MFMA peak); YOLOv3-416 img/s at batc
 PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
 # HBM bytes per launch of the dominant kernel family (tap-major 3x3 conv,
-# incl. its split-K reduction) from two rocprofv3 --pmc runs of
-# `bench.py --counter-pass` (FETCH_SIZE then WRITE_SIZE, KiB per dispatch,
+# conv_lean_kernel, incl. its split-K reduction) from two rocprofv3 --pmc runs
+# of `bench.py --counter-pass` (FETCH_SIZE then WRITE_SIZE, KiB per dispatch,
 # scaled by a 64 MiB copy: read = 2.0 x FETCH_SIZE, write = 1.0 x WRITE_SIZE);
-# profiles/yolov3_416_b16_conv_tap3x3.md holds the figures and commands.
-TRAFFIC_TAP3X3_B16 = (2.0 * 90347.8 + 42229.1) * 1024
+# profiles/yolov3_416_b16_conv_lean_kernel.md holds the figures and commands.
+TRAFFIC_TAP3X3_B16 = (2.0 * 103367.8 + 40967.5) * 1024
 
 
 def log(*a):
@@ -39,11 +39,15 @@ def log(*a):
 
 
 def kernel_kind(L, batch):
-    """Kernel family a conv layer launches (conv_kernel<cfg, MODE> in conv.hip)."""
+    """Kernel family a conv layer launches: the lean implicit GEMM
+    (conv_lean_kernel, conv_lean.hpp) over tap-major 3x3 or 1x1 operands, or
+    the per-pixel kernel for few input channels (conv_smallc_kernel)."""
     if L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0:
-        return "conv_kernel<1x1>"
+        return "conv_lean_kernel<1x1>"
+    if L["size"] == 3 and L["in"][0] <= 4:
+        return "conv_smallc_kernel<3x3>"
     if L["size"] == 3 and L["in"][0] % 16 == 0:
-        return "conv_kernel<tap3x3>"
+        return "conv_lean_kernel<tap3x3>"
     return f"conv_kernel<gather{L['size']}x{L['size']}>"
 
 
@@ -436,7 +440,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4),
-                     "traffic": (round(TRAFFIC_TAP3X3_B16) if dom == "conv_kernel<tap3x3>" and args.batch == 16
+                     "traffic": (round(TRAFFIC_TAP3X3_B16) if dom == "conv_lean_kernel<tap3x3>" and args.batch == 16
                                  and args.size == 416 else None),
                      "traffic_unit": "bytes/launch",
                      "launches_per_step": round(d["launches"]),
