@@ -326,6 +326,9 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--size", type=int, default=416)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--weights", default=None,
+                    help="darknet .weights file for the YOLOv3 network (batch norm folded on the host); default: "
+                         "the seeded He-normal random weights of the benchmark configuration")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
@@ -350,7 +353,12 @@ def main():
     hip = TNNHip(0)
     hip.useTorchStream()  # one ordered stream for torch's buffers and the kernels
     _, layers = darknet.load_cfg("yolov3.cfg", args.size, args.size)
-    weights = darknet.synthetic_weights(layers)
+    if args.weights:
+        from tensorium_amd import weights as WT
+
+        weights = WT.load_weights(args.weights, layers)
+    else:
+        weights = darknet.synthetic_weights(layers)
     flop_img = darknet.conv_flops(layers)
 
     if args.counter_pass:
@@ -430,7 +438,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded splitmix64 U[0,1) images, He-normal random weights, BN folded)",
+        "data": ("synthetic (seeded splitmix64 U[0,1) images, He-normal random weights, BN folded)" if not args.weights
+                 else f"synthetic images, weights from {os.path.basename(args.weights)} (BN folded)"),
         "config": {"workload": f"YOLOv3-{args.size} fp32 inference, batch {args.batch}, 1 GPU",
                    "global_batch": args.batch, "image": [3, args.size, args.size]},
         "conv_gflops": round(gflops, 1),
