@@ -291,6 +291,39 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
             "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
 
 
+def extra_detect(hip, layers, weights, batch=16, thresh=0.5, nms=0.45):
+    """YOLO detection list + per-class NMS on the device
+    after a YOLOv3-416 forward at batch 16 (tnh_yolo_detections +
+    tnh_yolo_nms_sort, device time; the list stays in HBM)."""
+    import torch
+
+    from tensorium_amd import darknet, synth
+
+    net = darknet.Network(hip, layers, batch, weights)
+    x = torch.from_numpy(synth.uniform(7, (batch, 3, 416, 416))).cuda()
+    torch.cuda.synchronize()
+    net.forward(x)
+    dets = net.detect(thresh=thresh, nms=nms)  # allocates the buffers, checks capacity
+    yl = [L for L in layers if L["type"] == "yolo"]
+    _, boxes, obj, prob, counts = net._det_bufs
+    cap = boxes.shape[1]
+
+    def fn():
+        hip.yoloDetections(batch, [net.out[L["index"]] for L in yl], [L["out"][1:] for L in yl], yl[0]["n"],
+                           yl[0]["classes"], [L["anchors"] for L in yl], 416, 416, 416, 416, thresh, False, False,
+                           cap, boxes, obj, prob, counts)
+        hip.yoloNmsSort(batch, yl[0]["classes"], cap, boxes, prob, counts, nms)
+
+    for _ in range(2):
+        fn()
+    ms = time_events(hip, fn, 10)
+    nd = sum(len(d[1]) for d in dets)
+    kept = sum(int((d[2] > 0).sum()) for d in dets)
+    del net, x
+    return {"workload": f"YOLOv3-416 detections + per-class NMS on device, batch {batch}, thresh {thresh}, nms {nms}",
+            "us": round(ms * 1e3, 1), "detections": nd, "kept_class_scores": kept}
+
+
 def counter_pass(hip, net, args):
     """Warm-up forwards (autotuning), a fence, then exactly one forward and one
     copy of COPY_BYTES: the dispatches a counter run attributes.  The copy
@@ -424,6 +457,7 @@ def main():
         guarded("train_cifar_b128", lambda: extra_train(hip, 50, 2, 0 if args.no_cpu_baseline else 2))
         _, l608 = darknet.load_cfg("yolov3.cfg", 608, 608)
         guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2))
+        guarded("yolo_detect_nms_b16", lambda: extra_detect(hip, layers, weights))
 
     out = {
         "metric": METRIC,

@@ -255,6 +255,35 @@ int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w,
  * 1/(1+e) by IEEE division (the reference's vrcpps is CPU-specific). */
 int32_t tnh_yolo_fwd(int64_t batch, int64_t n, int64_t classes, int64_t h,
                      int64_t w, const float *in, float *out);
+/* TNNet.Detections (nnet.pas:584-680) on the device: for every yolo head
+ * (heads[i]: a device tensor [batch][n][classes+5][h][w] after tnh_yolo_fwd,
+ * hw[2i], hw[2i+1] = h, w; anchors[(i*n + a)*2 + {0,1}] = the mask's anchor
+ * width and height in network pixels) TYoloLayer.getDetections
+ * (nyololayer.pas:399-450, getBox :105-122, correctBoxes :452-498): every
+ * (location, anchor) whose objectness exceeds thresh, in the reference's
+ * order (head, then location row-major, then anchor), gets box x, y, w, h
+ * (image pixels unless relative; letterbox correction when letter),
+ * objectness, and prob[j] = objectness*class_j if that exceeds thresh, else
+ * 0.  Device outputs: boxes [batch][capacity][4], objectness
+ * [batch][capacity], prob [batch][capacity][classes], counts [batch]
+ * (int32, the number of detections; entries beyond capacity are not
+ * written).  At most 8 heads and 16 anchors per head. */
+int32_t tnh_yolo_detections(int64_t batch, int32_t nHeads,
+                            const float *const *heads, const int64_t *hw,
+                            int64_t n, int64_t classes, const float *anchors,
+                            int64_t netW, int64_t netH, int64_t imgW,
+                            int64_t imgH, float thresh, int32_t relative,
+                            int32_t letter, int64_t capacity, float *boxes,
+                            float *objectness, float *prob, int32_t *counts);
+/* TDetectionsHelper.doNMSSort (ntypes.pas:1612-1649) on the device, in place
+ * on prob: per class, the detections with a non-zero probability in
+ * descending order of it (equal probabilities: detection order; the
+ * reference's quicksort leaves that order unspecified), and every later one
+ * whose box_iou with a kept one exceeds thresh gets probability 0.  Uses
+ * the buffers and counts of tnh_yolo_detections; capacity <= 8192. */
+int32_t tnh_yolo_nms_sort(int64_t batch, int64_t classes, int64_t capacity,
+                          const float *boxes, float *prob,
+                          const int32_t *counts, float thresh);
 
 /* ---- batch norm (inference, unfused) ----------------------------------- */
 /* TNNCuda.normalize (nncuda.pas:1371) with the CPU clamp of _snormblkvv

@@ -99,7 +99,14 @@ def parse_cfg(text, height=None, width=None):
             classes = int(o.get("classes", 80))
             if shape[0] != len(mask) * (classes + 5):
                 raise ValueError(f"yolo {idx}: {shape[0]} channels != {len(mask)}*(classes+5)")
-            L.update(n=len(mask), classes=classes, out=shape)
+            # anchors (w, h pairs in network pixels; parseYolo, nparser.pas): default 0.5 as TYoloLayer's biases
+            a = [float(v) for v in o["anchors"].split(",")] if "anchors" in o else [0.5] * (2 * (max(mask) + 1))
+            if len(a) % 2 or max(mask) >= len(a) // 2:
+                raise ValueError(f"yolo {idx}: mask {mask} needs {max(mask) + 1} anchors, cfg has {len(a) // 2}")
+            if float(o.get("scale_x_y", 1)) != 1 or int(o.get("new_coords", 0)) != 0:
+                raise ValueError(f"yolo {idx}: scale_x_y != 1 / new_coords are not supported")
+            L.update(n=len(mask), classes=classes, mask=mask,
+                     anchors=[(a[2 * m], a[2 * m + 1]) for m in mask], out=shape)
         else:
             raise ValueError(f"unsupported layer type [{name}]")
         layers.append(L)
@@ -298,6 +305,44 @@ class Network:
         if getattr(self, "graph", None):
             self.hip.graphDestroy(self.graph)
             self.graph = None
+
+    def detect(self, thresh=0.5, nms=0.45, img_w=None, img_h=None, relative=False, letter=False, capacity=8192):
+        """TNNet.Detections and doNMSSort on the device after forward():
+        decodes the yolo heads into boxes / objectness / class probabilities
+        (tnh_yolo_detections), suppresses overlaps per class
+        (tnh_yolo_nms_sort, skipped when nms is None) and returns per image
+        (boxes [D, 4] in image pixels (or relative), objectness [D],
+        prob [D, classes]) as numpy arrays: only the detection list leaves
+        the GPU."""
+        torch = self.torch
+        yl = [L for L in self.layers if L["type"] == "yolo"]
+        if not yl:
+            raise ValueError("network has no yolo layer")
+        classes, n = yl[0]["classes"], yl[0]["n"]
+        if any(L["classes"] != classes or L["n"] != n for L in yl):
+            raise ValueError("yolo heads differ in classes or anchors per cell")
+        _, H, W = self.layers[0]["in"]
+        img_w, img_h = img_w or W, img_h or H
+        B = self.batch
+        key = (capacity, classes)
+        if getattr(self, "_det_bufs", (None,))[0] != key:
+            dev = self.out[yl[0]["index"]].device
+            self._det_bufs = (key, torch.empty((B, capacity, 4), dtype=torch.float32, device=dev),
+                              torch.empty((B, capacity), dtype=torch.float32, device=dev),
+                              torch.empty((B, capacity, classes), dtype=torch.float32, device=dev),
+                              torch.empty(B, dtype=torch.int32, device=dev))
+        _, boxes, obj, prob, counts = self._det_bufs
+        self.hip.yoloDetections(B, [self.out[L["index"]] for L in yl], [L["out"][1:] for L in yl], n, classes,
+                                [L["anchors"] for L in yl], W, H, img_w, img_h, thresh, relative, letter, capacity,
+                                boxes, obj, prob, counts)
+        if nms is not None:
+            self.hip.yoloNmsSort(B, classes, capacity, boxes, prob, counts, nms)
+        self.hip.finish()
+        cnt = counts.cpu().numpy()
+        if (cnt > capacity).any():
+            raise ValueError(f"{int(cnt.max())} detections exceed the capacity {capacity}")
+        return [(boxes[b, :c].cpu().numpy(), obj[b, :c].cpu().numpy(), prob[b, :c].cpu().numpy())
+                for b, c in enumerate(cnt)]
 
     def head_convs(self):
         """Indices of the convolutions feeding the yolo layers (pre-logistic)."""

@@ -88,6 +88,9 @@ _PROTOS = {
     "tnh_upsample": [i64, i64, i64, i64, vp, i64, i32, f32, vp, i32],
     "tnh_bn_normalize": [i64, vp, i64, i64, vp, vp, i64],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
+    "tnh_yolo_detections": [i64, i32, C.POINTER(vp), C.POINTER(i64), i64, i64, C.POINTER(f32), i64, i64, i64, i64,
+                            f32, i32, i32, i64, vp, vp, vp, vp],
+    "tnh_yolo_nms_sort": [i64, i64, i64, vp, vp, vp, f32],
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
     "tnh_normalize_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -387,6 +390,26 @@ class TNNHip:
     def yoloForward(self, batch, n, classes, h, w, input, output):
         """TYoloLayer.forward inference: copy + logistic on x, y, obj, classes."""
         call("tnh_yolo_fwd", batch, n, classes, h, w, addr(input), addr(output))
+
+    def yoloDetections(self, batch, heads, hw, n, classes, anchors, netW, netH, imgW, imgH, thresh, relative,
+                       letter, capacity, boxes, objectness, prob, counts):
+        """TNNet.Detections over yolo heads on the device: heads = device
+        tensors (after yoloForward), hw = [(h, w)] per head, anchors =
+        [[(w, h)] * n] per head (the mask's anchors); fills boxes
+        [batch][capacity][4], objectness [batch][capacity], prob
+        [batch][capacity][classes] and counts [batch] (int32; a count above
+        capacity means the buffers were too small)."""
+        nh = len(heads)
+        hp = (vp * nh)(*[addr(h) for h in heads])
+        hwa = (i64 * (2 * nh))(*[v for p in hw for v in p])
+        flat = [float(v) for head in anchors for pair in head for v in pair]
+        an = (f32 * len(flat))(*flat)
+        call("tnh_yolo_detections", batch, nh, hp, hwa, n, classes, an, netW, netH, imgW, imgH, thresh,
+             _b(relative), _b(letter), capacity, addr(boxes), addr(objectness), addr(prob), addr(counts))
+
+    def yoloNmsSort(self, batch, classes, capacity, boxes, prob, counts, thresh):
+        """TDetectionsHelper.doNMSSort on the device, in place on prob."""
+        call("tnh_yolo_nms_sort", batch, classes, capacity, addr(boxes), addr(prob), addr(counts), thresh)
 
     # -- batch norm ------------------------------------------------------------
     def blockNormalize(self, dstSize, dst, offset, N, mean, variance, batch):
