@@ -18,6 +18,7 @@ struct Context {
   int device = -1;
   hipStream_t own_stream = nullptr;  // created by tnh_init
   hipStream_t stream = nullptr;      // stream kernels are launched on
+  hipStream_t tune_stream = nullptr; // private stream the autotuner captures its timing graphs on
   int cu_count = 0;
   int xcd_count = 8;
   void* ws = nullptr;     // library scratch (split-K partial sums), grown on demand

@@ -42,6 +42,9 @@ void* workspace(Context* c, size_t bytes) {
   if (bytes <= c->wsBytes) return c->ws;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  if (c->tune_stream &&
+      (hipStreamIsCapturing(c->tune_stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone))
+    return nullptr;
   if (c->ws) {
     (void)hipStreamSynchronize(c->stream);
     (void)hipFree(c->ws);
@@ -87,17 +90,23 @@ extern "C" int32_t tnh_init(int32_t device) {
     (void)hipStreamSynchronize(g_ctx.stream);
     if (g_ctx.ws) (void)hipFree(g_ctx.ws);
     (void)hipStreamDestroy(g_ctx.own_stream);
+    (void)hipStreamDestroy(g_ctx.tune_stream);
     g_ctx = Context{};
     g_live = false;
   }
   if (int st = hip_status(hipSetDevice(device), "hipSetDevice")) return st;
-  hipStream_t s = nullptr;
+  hipStream_t s = nullptr, ts = nullptr;
   if (int st = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return st;
+  if (int st = hip_status(hipStreamCreateWithFlags(&ts, hipStreamNonBlocking), "hipStreamCreate")) {
+    (void)hipStreamDestroy(s);
+    return st;
+  }
   int cus = 0;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
   g_ctx.device = device;
   g_ctx.own_stream = s;
   g_ctx.stream = s;
+  g_ctx.tune_stream = ts;
   g_ctx.cu_count = cus > 0 ? cus : 256;
   g_live = true;
   return TNH_OK;
@@ -110,6 +119,7 @@ extern "C" int32_t tnh_finalize(void) {
   (void)hipStreamSynchronize(g_ctx.stream);
   if (g_ctx.ws) (void)hipFree(g_ctx.ws);
   (void)hipStreamDestroy(g_ctx.own_stream);
+  (void)hipStreamDestroy(g_ctx.tune_stream);
   g_ctx = Context{};
   g_live = false;
   return TNH_OK;

@@ -311,18 +311,26 @@ int launch_smallc(const ConvArgs& a, hipStream_t s) {
 }
 
 // Sums the split-K partials in split order (deterministic) and applies the
-// epilogue: one thread per output element, consecutive threads along n.
+// epilogue: one thread per output element, consecutive threads along n.  S
+// is the split count: the S partial loads of an element are issued together
+// and summed afterwards, so a thread waits for one memory round trip rather
+// than S.
+template <int S>
 __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
   const int64_t total = a.F * a.g.N, OHW = a.g.OHW;
   for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x) {
     const int64_t f = e / a.g.N, n = e - f * a.g.N;
-    float v = a.part[e];
-    for (int s = 1; s < a.splits; ++s) v = v + a.part[s * total + e];
-    const int64_t b = n / OHW, p = n - b * OHW;
+    float p[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) p[s] = a.part[s * total + e];
+    float v = p[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) v = v + p[s];
+    const int64_t b = n / OHW, q = n - b * OHW;
     if (a.bias) v = v + a.bias[f];
     v = apply_act(v, a.act);
-    if (a.res) v = v + a.res[b * a.rBatchStride + f * OHW + p];
-    a.out[b * a.outBatchStride + f * OHW + p] = v;
+    if (a.res) v = v + a.res[b * a.rBatchStride + f * OHW + q];
+    a.out[b * a.outBatchStride + f * OHW + q] = v;
   }
 }
 
@@ -398,8 +406,16 @@ int launch_reduce(const ConvArgs& a, hipStream_t s) {
   if (a.splits <= 1) return TNH_OK;
   const int64_t total = a.F * a.g.N;
   const int64_t blocks = (total + 255) / 256;
-  hipLaunchKernelGGL(conv_splitk_reduce, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s,
-                     a);
+  const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+  switch (a.splits) {
+#define TNH_REDUCE_CASE(S) \
+  case S: hipLaunchKernelGGL(conv_splitk_reduce<S>, grid, dim3(256), 0, s, a); break;
+    TNH_REDUCE_CASE(2) TNH_REDUCE_CASE(3) TNH_REDUCE_CASE(4) TNH_REDUCE_CASE(5) TNH_REDUCE_CASE(6)
+    TNH_REDUCE_CASE(7) TNH_REDUCE_CASE(8) TNH_REDUCE_CASE(9) TNH_REDUCE_CASE(10) TNH_REDUCE_CASE(11)
+    TNH_REDUCE_CASE(12) TNH_REDUCE_CASE(13) TNH_REDUCE_CASE(14) TNH_REDUCE_CASE(15) TNH_REDUCE_CASE(16)
+#undef TNH_REDUCE_CASE
+    default: return fail(TNH_ERR_UNSUPPORTED, "conv2d: %d split-K partitions (at most 16)", a.splits);
+  }
   return launch_status("conv_splitk_reduce");
 }
 
@@ -681,7 +697,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     if (c.splits <= 1) return nullptr;
     return static_cast<float*>(workspace(cx, static_cast<size_t>(c.splits) * F * N * 4));
   };
-  auto run = [&](const Cand& c) -> int {
+  auto runOn = [&](const Cand& c, hipStream_t s) -> int {
     ConvArgs b = a;
     b.splits = 1;
     b.part = nullptr;
@@ -689,8 +705,9 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
       b.part = wsFor(c);
       if (b.part) b.splits = c.splits;
     }
-    return launch(c.cfg, b, mode, va, vb, cx->stream);
+    return launch(c.cfg, b, mode, va, vb, s);
   };
+  auto run = [&](const Cand& c) -> int { return runOn(c, cx->stream); };
   Cand best = cands[0];
   {
     float bc = 1e30f;
@@ -714,39 +731,67 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     }
   }
   if (tune && cands.size() > 1) {
-    // Time each candidate (the output is rewritten identically by each run:
-    // out never aliases x or residual).  Warm the clocks with the model's
-    // choice, then time every candidate twice (two launches each) and keep
-    // its faster run.
+    // Time each candidate as it runs in a graph replay: kReps launches
+    // captured into a graph on the context's private tuning stream, replayed
+    // twice after a warm-up replay; the faster replay counts.  Eager timing
+    // would charge a candidate the host's launch cost, which at small sizes
+    // exceeds the kernels' own time and penalises split-K's second launch.
+    // The output is rewritten identically by every run (out never aliases x
+    // or residual).  Workspaces are grown before any capture.
+    constexpr int kReps = 4;
+    int maxSplit = 1;
+    for (const Cand& c : cands) maxSplit = c.splits > maxSplit ? c.splits : maxSplit;
+    if (maxSplit > 1) (void)wsFor({0, maxSplit});
+    const hipStream_t ts = cx->tune_stream;
+    if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
     hipEvent_t e0, e1;
     if (int st = hip_status(hipEventCreate(&e0), "hipEventCreate")) return st;
-    if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) return st;
-    for (int r = 0; r < 3; ++r)
-      if (int st = run(best)) return st;
+    if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) {
+      (void)hipEventDestroy(e0);
+      return st;
+    }
+    auto timeCand = [&](const Cand& c, float& ms) -> int {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      int st = hip_status(hipStreamBeginCapture(ts, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+      if (st) return st;
+      for (int r = 0; r < kReps && !st; ++r) st = runOn(c, ts);
+      const hipError_t ee = hipStreamEndCapture(ts, &g);
+      if (!st) st = hip_status(ee, "hipStreamEndCapture");
+      if (!st) st = hip_status(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+      if (!st) st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
+      ms = 1e30f;
+      for (int t = 0; t < 2 && !st; ++t) {
+        (void)hipEventRecord(e0, ts);
+        st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
+        (void)hipEventRecord(e1, ts);
+        if (!st) st = hip_status(hipEventSynchronize(e1), "hipEventSynchronize");
+        float v = 0.f;
+        if (!st && hipEventElapsedTime(&v, e0, e1) == hipSuccess && v / kReps < ms) ms = v / kReps;
+      }
+      if (ge) (void)hipGraphExecDestroy(ge);
+      if (g) (void)hipGraphDestroy(g);
+      return st;
+    };
     float bestMs = 1e30f;
+    int st = TNH_OK;
     for (const Cand& c : cands) {
       if (c.splits > 1 && !wsFor(c)) continue;
-      if (int st = run(c)) return st;  // warm-up
-      for (int t = 0; t < 2; ++t) {
-        (void)hipEventRecord(e0, cx->stream);
-        for (int r = 0; r < 2; ++r)
-          if (int st = run(c)) return st;
-        (void)hipEventRecord(e1, cx->stream);
-        (void)hipEventSynchronize(e1);
-        float ms = 0.f;
-        (void)hipEventElapsedTime(&ms, e0, e1);
-        if (ms < bestMs) bestMs = ms, best = c;
-      }
+      float ms = 0.f;
+      if ((st = timeCand(c, ms))) break;
+      if (ms < bestMs) bestMs = ms, best = c;
     }
+    (void)hipStreamSynchronize(ts);
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    if (st) return st;
     std::lock_guard<std::mutex> lk(g_tune_mu);
     g_tuned[key] = best;
     static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
     if (verbose)
       std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d %.4f ms\n",
                    (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
-                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, bestMs / 2);
+                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, bestMs);
   }
   return run(best);
 }
