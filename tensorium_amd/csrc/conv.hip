@@ -455,9 +455,27 @@ int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
 }
 
 template <class Cfg>
-int launch_lean(ConvArgs a, int mode, bool vb, hipStream_t s) {
+int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
   dim3 grid;
   if (int st = grid_for<Cfg>(a, grid)) return st;
+  const int64_t tiles = static_cast<int64_t>(a.tilesM) * a.tilesN;
+  if (a.tailSplits > 0 && a.splits <= 1) {
+    // whole rounds of tiles over the CUs stay whole; the remainder is cut
+    // along K so that every CU gets about the same work
+    const int64_t full = tiles / cus * cus;
+    const int64_t panels = a.g.K / Cfg::BK;
+    a.kChunk = (panels + a.tailSplits - 1) / a.tailSplits * Cfg::BK;
+    a.tailSplits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty piece
+    if (full == tiles || full == 0 || a.tailSplits < 2) {
+      a.tailSplits = 0;
+      a.kChunk = a.g.K;
+    } else {
+      a.nFull = static_cast<int>(full);
+      grid = dim3(static_cast<unsigned>(full + (tiles - full) * a.tailSplits), 1);
+    }
+  } else {
+    a.tailSplits = 0;
+  }
   if (mode == kTap3)
     hipLaunchKernelGGL((conv_lean_kernel<Cfg, kTap3, false>), grid, dim3(Cfg::NT), 0, s, a);
   else if (vb)
@@ -465,7 +483,22 @@ int launch_lean(ConvArgs a, int mode, bool vb, hipStream_t s) {
   else
     hipLaunchKernelGGL((conv_lean_kernel<Cfg, k1x1, false>), grid, dim3(Cfg::NT), 0, s, a);
   if (int st = launch_status("conv_lean_kernel")) return st;
+  if (a.tailSplits > 0) {
+    hipLaunchKernelGGL((conv_tail_reduce<Cfg>), dim3(static_cast<unsigned>(tiles - a.nFull)), dim3(Cfg::NT), 0, s, a);
+    return launch_status("conv_tail_reduce");
+  }
   return launch_reduce(a, s);
+}
+
+// Floats of tail-split pieces a lean configuration writes (0 when the tiles
+// divide evenly over the CUs).
+int64_t tail_floats(int BM, int BN, int BK, int64_t F, int64_t N, int64_t K, int cus, int tailSplits) {
+  const int64_t tiles = ((F + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int64_t rest = tiles % cus;
+  const int64_t panels = K / BK;
+  const int64_t chunk = (panels + tailSplits - 1) / tailSplits;
+  const int64_t pieces = (panels + chunk - 1) / chunk;
+  return tiles < cus ? 0 : rest * pieces * BM * BN;
 }
 
 template <class D>
@@ -480,7 +513,7 @@ int launch_direct(ConvArgs a, int mode, hipStream_t s) {
   return launch_reduce(a, s);
 }
 
-int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
+int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, int cus, hipStream_t s) {
   switch (cfg) {
     case 0: return launch_cfg<Cfg0>(a, mode, va, vb, s);
     case 1: return launch_cfg<Cfg1>(a, mode, va, vb, s);
@@ -493,15 +526,15 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s
     case 8: return launch_direct<Dir8>(a, mode, s);
     case 9: return launch_direct<Dir9>(a, mode, s);
     case 10: return launch_direct<Dir10>(a, mode, s);
-    case 11: return launch_lean<Lean11>(a, mode, vb, s);
-    case 12: return launch_lean<Lean12>(a, mode, vb, s);
-    case 13: return launch_lean<Lean13>(a, mode, vb, s);
-    case 14: return launch_lean<Lean14>(a, mode, vb, s);
-    case 15: return launch_lean<Lean15>(a, mode, vb, s);
-    case 16: return launch_lean<Lean16>(a, mode, vb, s);
-    case 17: return launch_lean<Lean17>(a, mode, vb, s);
-    case 18: return launch_lean<Lean18>(a, mode, vb, s);
-    default: return launch_lean<Lean19>(a, mode, vb, s);
+    case 11: return launch_lean<Lean11>(a, mode, vb, cus, s);
+    case 12: return launch_lean<Lean12>(a, mode, vb, cus, s);
+    case 13: return launch_lean<Lean13>(a, mode, vb, cus, s);
+    case 14: return launch_lean<Lean14>(a, mode, vb, cus, s);
+    case 15: return launch_lean<Lean15>(a, mode, vb, cus, s);
+    case 16: return launch_lean<Lean16>(a, mode, vb, cus, s);
+    case 17: return launch_lean<Lean17>(a, mode, vb, cus, s);
+    case 18: return launch_lean<Lean18>(a, mode, vb, cus, s);
+    default: return launch_lean<Lean19>(a, mode, vb, cus, s);
   }
 }
 
@@ -520,6 +553,7 @@ __global__ void pack_weights_kernel(int64_t total, int64_t C, int64_t taps, cons
 
 struct Cand {
   int cfg, splits;
+  int tail;  // tail-split pieces per remainder tile (lean configurations), 0: none
 };
 
 // Estimated time (arbitrary units): rounds of resident tiles times the work
@@ -587,7 +621,8 @@ extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t
 
 extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
-  TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 16,
+  TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 31 &&
+              forcedConfig / 64 != 17,
           "conv2d_set_autotune: config %d", forcedConfig);
   g_autotune = enable != 0;
   g_forced_cfg = forcedConfig;
@@ -683,29 +718,46 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   // Candidates: every valid tile shape, and for shapes that leave the CUs
   // under-filled also split-K factors (partial sums in the context
   // workspace, reduced in fixed order).
+  // Lean configurations whose tile count is not a multiple of the CU count
+  // also try tail splits (the last partial round of tiles cut along K).
+  const int cus = cx->cu_count;
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
     if (!cfg_valid(c, mode, C, va, smallIO)) continue;
-    cands.push_back({c, 1});
+    cands.push_back({c, 1, 0});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
-    if (tiles >= 2 * cx->cu_count) continue;
+    if (ci.kind == kLean && tiles > cus && tiles % cus != 0)
+      for (int tp : {2, 3, 4, 6, 8})
+        if (K >= static_cast<int64_t>(tp) * ci.BK * 2) cands.push_back({c, 1, tp});
+    if (tiles >= 2 * cus) continue;
     for (int sp : {2, 4, 8, 16})
-      if (tiles * sp <= 8 * cx->cu_count && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp});
+      if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp, 0});
   }
+  auto wsFloats = [&](const Cand& c) -> int64_t {
+    if (c.tail > 0) {
+      const CfgInfo& ci = kCfgs[c.cfg];
+      return tail_floats(ci.BM, ci.BN, ci.BK, F, N, K, cus, c.tail);
+    }
+    return c.splits > 1 ? c.splits * F * N : 0;
+  };
   auto wsFor = [&](const Cand& c) -> float* {
-    if (c.splits <= 1) return nullptr;
-    return static_cast<float*>(workspace(cx, static_cast<size_t>(c.splits) * F * N * 4));
+    const int64_t n = wsFloats(c);
+    return n > 0 ? static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4)) : nullptr;
   };
   auto runOn = [&](const Cand& c, hipStream_t s) -> int {
     ConvArgs b = a;
     b.splits = 1;
+    b.tailSplits = 0;
     b.part = nullptr;
-    if (c.splits > 1) {
+    if (c.splits > 1 || c.tail > 0) {
       b.part = wsFor(c);
-      if (b.part) b.splits = c.splits;
+      if (b.part) {
+        b.splits = c.splits;
+        b.tailSplits = c.tail;
+      }
     }
-    return launch(c.cfg, b, mode, va, vb, s);
+    return launch(c.cfg, b, mode, va, vb, cus, s);
   };
   auto run = [&](const Cand& c) -> int { return runOn(c, cx->stream); };
   Cand best = cands[0];
@@ -721,8 +773,13 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO))
-      return run({g_forced_cfg % 64, g_forced_cfg / 64 > 1 ? g_forced_cfg / 64 : 1});
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO)) {
+      const int hi = g_forced_cfg / 64;
+      if (hi > 17)
+        return kCfgs[g_forced_cfg % 64].kind == kLean ? run({g_forced_cfg % 64, 1, hi - 16})
+                                                      : fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
+      return run({g_forced_cfg % 64, hi > 1 ? hi : 1, 0});
+    }
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return run(it->second);
     if (g_autotune && !aliased) {
@@ -739,9 +796,11 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     // The output is rewritten identically by every run (out never aliases x
     // or residual).  Workspaces are grown before any capture.
     constexpr int kReps = 4;
-    int maxSplit = 1;
-    for (const Cand& c : cands) maxSplit = c.splits > maxSplit ? c.splits : maxSplit;
-    if (maxSplit > 1) (void)wsFor({0, maxSplit});
+    int64_t maxWs = 0;
+    Cand maxC{0, 1, 0};
+    for (const Cand& c : cands)
+      if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
+    if (maxWs > 0) (void)wsFor(maxC);
     const hipStream_t ts = cx->tune_stream;
     if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
     hipEvent_t e0, e1;
@@ -776,7 +835,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     float bestMs = 1e30f;
     int st = TNH_OK;
     for (const Cand& c : cands) {
-      if (c.splits > 1 && !wsFor(c)) continue;
+      if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
       float ms = 0.f;
       if ((st = timeCand(c, ms))) break;
       if (ms < bestMs) bestMs = ms, best = c;
@@ -789,9 +848,11 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     g_tuned[key] = best;
     static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
     if (verbose)
-      std::fprintf(stderr, "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d %.4f ms\n",
+      std::fprintf(stderr,
+                   "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d tail %d "
+                   "%.4f ms\n",
                    (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
-                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, bestMs);
+                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, best.tail, bestMs);
   }
   return run(best);
 }

@@ -28,6 +28,13 @@ struct ConvArgs {
   float* part;      // splits > 1: partial sums [splits][F][N]
   int64_t outBytes; // extent of out addressed by the kernel
   int64_t resBytes; // extent of res addressed by the kernel (0 without residual)
+  // Tail split (lean kernels; splits == 1): workgroups [0, nFull) own the
+  // whole K range of tiles [0, nFull); the remaining tiles are cut into
+  // tailSplits K pieces of kChunk each, one workgroup per piece, whose raw
+  // accumulators go to part (one BM x BN block per piece, tile-major) for
+  // conv_tail_reduce.  tailSplits == 0: off.
+  int tailSplits;
+  int nFull;
 };
 
 // K walk / B operand of a convolution kernel

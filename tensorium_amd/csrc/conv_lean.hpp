@@ -375,6 +375,14 @@ struct LeanTraits<Cfg, k1x1, VB> {
   using BL = Lean1x1B<Cfg, kVec>;
 };
 
+// Offset of accumulator register (i, j, r) of a lane inside a tail piece's
+// BM x BN block: register order, so that 64 consecutive lanes store 64
+// consecutive floats.
+template <class Cfg>
+__device__ inline int piece_off(int wave, int lane, int i, int j, int r) {
+  return ((wave * Cfg::FM * Cfg::FN + i * Cfg::FN + j) * 16 + r) * 64 + lane;
+}
+
 template <class Cfg, int MODE, bool VB>
 __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a) {
   using AL = LeanA<Cfg>;
@@ -383,19 +391,70 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
   __shared__ __attribute__((aligned(16))) float smem[Loop::LDS_FLOATS];
   lds_t* lds = (lds_t*)smem;
 
+  int tile = blockIdx.x;
+  int64_t kBegin = blockIdx.y * a.kChunk;
+  int piece = -1;
+  if (a.tailSplits > 0 && tile >= a.nFull) {  // a K piece of a tail tile
+    const int u = tile - a.nFull;
+    tile = a.nFull + u / a.tailSplits;
+    kBegin = static_cast<int64_t>(u % a.tailSplits) * a.kChunk;
+    piece = u;
+  }
+  const int64_t kEnd = a.tailSplits > 0 && piece < 0 ? a.g.K : min(a.g.K, kBegin + a.kChunk);
   int tm, tn;
-  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  tile_coords(tile, a.tilesM, a.tilesN, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
   AL al;
   al.init(a.w, a.wBytes, a.g.K, a.F, m0, threadIdx.x);
   BL bl;
   bl.init(a.g, n0, threadIdx.x);
   f32x16 acc[Cfg::FM][Cfg::FN];
-  const int64_t kBegin = blockIdx.y * a.kChunk;
-  const int64_t kEnd = min(a.g.K, kBegin + a.kChunk);
   Loop::exec(al, bl, kBegin, (kEnd - kBegin) / Cfg::BK, lds, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (piece >= 0) {
+    float* dst = a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN);
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[piece_off<Cfg>(wave, lane, i, j, r)] = acc[i][j][r];
+    return;
+  }
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+}
+
+// Second launch of a tail split: one workgroup per tail tile sums the tile's
+// pieces in K order (piece 0 first, as conv_splitk_reduce does) into the
+// accumulator registers the conv kernel would have held, then applies the
+// conv kernel's own epilogue.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) void conv_tail_reduce(ConvArgs a) {
+  const int t = blockIdx.x;
+  int tm, tn;
+  tile_coords(a.nFull + t, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int TILE = Cfg::BM * Cfg::BN;
+  const float* src = a.part + static_cast<int64_t>(t) * a.tailSplits * TILE;
+  f32x16 acc[Cfg::FM][Cfg::FN];
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = src[piece_off<Cfg>(wave, lane, i, j, r)];
+  for (int s = 1; s < a.tailSplits; ++s) {
+    const float* ps = src + static_cast<int64_t>(s) * TILE;
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + ps[piece_off<Cfg>(wave, lane, i, j, r)];
+  }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -245,6 +245,43 @@ def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
     hip.packConvWeights(F, Cc, k, dW, packed)
     dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
     hip.setConvAutotune(True, CONV_SPLIT_UNIT * splits + cfg)
+    try:
+        hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
+                          weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
+        got = H(dout, hip)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert R.rel_err(got, ref) <= TOL
+
+
+_TAIL_REFS = {}
+
+
+@pytest.mark.parametrize("cfg", [11, 13, 17])
+@pytest.mark.parametrize("pieces", [2, 3, 8])
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 32, 136, 128, 3, 1), (1, 64, 136, 128, 1, 1), (1, 32, 272, 128, 3, 2)])
+def test_conv_tail_split(hip, cfg, pieces, B, Cc, Hh, F, k, s):
+    """Tail split: whole rounds of tiles over the CUs, the remainder cut into
+    K pieces summed in K order by a second kernel, then the epilogue."""
+    case(f"conv tail split {pieces} cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
+    p = k // 2
+    OH = (Hh + 2 * p - k) // s + 1
+    bm, bn = {11: (64, 64), 13: (128, 64), 17: (128, 64)}[cfg]
+    tiles = -(-F // bm) * -(-(B * OH * OH) // bn)
+    assert tiles > hip.cuCount() and tiles % hip.cuCount() != 0, "shape must leave a partial round"
+    key = (B, Cc, Hh, F, k, s)
+    if key not in _TAIL_REFS:
+        x = synth.uniform(61, (B, Cc, Hh, Hh))
+        Wt = synth.normal(62, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+        b = synth.normal(63, (F,), 0.1)
+        res = synth.normal(64, (B, F, OH, OH))
+        _TAIL_REFS[key] = (x, Wt, b, res, R.addvv(R.conv_forward(x, Wt, b, k, s, p, acLEAKY), res))
+    x, Wt, b, res, ref = _TAIL_REFS[key]
+    dW = D(Wt)
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, k, dW, packed)
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, cfg + CONV_SPLIT_UNIT * (CONV_TAIL_BASE + pieces))
     try:
         hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
                           weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
