@@ -133,6 +133,8 @@ __device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM]
   const uint32_t OHW = static_cast<uint32_t>(a.g.OHW);
   const __amdgpu_buffer_rsrc_t outR = make_rsrc(a.out, a.outBytes);
   const __amdgpu_buffer_rsrc_t resR = make_rsrc(a.res, a.resBytes);
+  // without bias the add uses -0.0, the exact additive identity (x + -0.0
+  // == x for every x, signed zeros included), so it needs no branch
   float bias[FM][16];
   if (a.bias) {
     const __amdgpu_buffer_rsrc_t bR = make_rsrc(a.bias, a.F * 4);
@@ -142,7 +144,13 @@ __device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM]
       for (int r = 0; r < 16; ++r)
         bias[i][r] = buf_ld1s(bR, static_cast<uint32_t>(rowBase) * 4u,
                               static_cast<uint32_t>(i * 32 + 8 * (r >> 2) + (r & 3)) * 4u);
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bias[i][r] = -0.f;
   }
+  uint32_t vOut[FN], vRes[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int64_t n = n0w + j * 32 + (lane & 31);
@@ -150,20 +158,55 @@ __device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM]
     const uint32_t nn = okN ? static_cast<uint32_t>(n) : 0u;
     const uint32_t b = nn / OHW, p = nn - b * OHW;
     const uint32_t rowOff = static_cast<uint32_t>(rowBase) * OHW + p;
-    const uint32_t vOut = sel_off(okN, (b * static_cast<uint32_t>(a.outBatchStride) + rowOff) * 4u);
-    const uint32_t vRes = sel_off(okN, (b * static_cast<uint32_t>(a.rBatchStride) + rowOff) * 4u);
+    vOut[j] = sel_off(okN, (b * static_cast<uint32_t>(a.outBatchStride) + rowOff) * 4u);
+    vRes[j] = sel_off(okN, (b * static_cast<uint32_t>(a.rBatchStride) + rowOff) * 4u);
+  }
+  auto so = [&](int i, int r) { return static_cast<uint32_t>(i * 32 + 8 * (r >> 2) + (r & 3)) * OHW * 4u; };
+  // The activation and the residual are wave-uniform: each combination gets
+  // its own straight-line code, and every residual load is issued before the
+  // first store (a store may alias a later residual element, so interleaved
+  // loads would each wait for a full memory round trip).
+  auto finish = [&](auto actTag, auto resTag) {
+    constexpr int ACT = decltype(actTag)::value;
+    constexpr bool RES = decltype(resTag)::value;
+    float rv[FN][FM][16];
+    if constexpr (RES) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int c = i * 32 + 8 * (r >> 2) + (r & 3);
-        const uint32_t so = static_cast<uint32_t>(c) * OHW * 4u;
-        float v = acc[i][j][r];
-        if (a.bias) v = v + bias[i][r];
-        v = apply_act(v, a.act);
-        if (a.res) v = v + buf_ld1s(resR, vRes, so);
-        buf_st1s(outR, v, rowOk(c) ? vOut : kOOB, so);
-      }
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) rv[j][i][r] = buf_ld1s(resR, vRes[j], so(i, r));
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = i * 32 + 8 * (r >> 2) + (r & 3);
+          float v = apply_act(acc[i][j][r] + bias[i][r], ACT);
+          if constexpr (RES) v = v + rv[j][i][r];
+          buf_st1s(outR, v, rowOk(c) ? vOut[j] : kOOB, so(i, r));
+        }
+  };
+  using Leaky = std::integral_constant<int, TNH_AC_LEAKY>;
+  using Logistic = std::integral_constant<int, TNH_AC_LOGISTIC>;
+  using Linear = std::integral_constant<int, TNH_AC_LINEAR>;
+  if (a.res) {
+    if (a.act == TNH_AC_LEAKY)
+      finish(Leaky{}, std::true_type{});
+    else if (a.act == TNH_AC_LOGISTIC)
+      finish(Logistic{}, std::true_type{});
+    else
+      finish(Linear{}, std::true_type{});
+  } else {
+    if (a.act == TNH_AC_LEAKY)
+      finish(Leaky{}, std::false_type{});
+    else if (a.act == TNH_AC_LOGISTIC)
+      finish(Logistic{}, std::false_type{});
+    else
+      finish(Linear{}, std::false_type{});
   }
 }
 
