@@ -173,11 +173,13 @@ int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
  * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 6..10
  * register-direct, 11..19 lean software-pipelined; a shape invalid for the
  * call falls back to the library's choice) and forcedConfig / 64 either the
- * split-K factor (0 or 1: none; up to 16) or, from 18 to 31, a tail split of
- * forcedConfig / 64 - 16 pieces (lean shapes only: the tiles beyond the last
- * whole round over the CUs are cut into that many K pieces, summed in K order
- * by a second kernel); -1 lets the library choose.  Autotuning times each
- * candidate as a graph replay of a few launches on a private stream. */
+ * split-K factor (0 or 1: none; up to 16) or a tail split (lean shapes only:
+ * the tiles beyond the last whole round are cut into K pieces, summed in K
+ * order by a second kernel): 18..31 = forcedConfig / 64 - 16 pieces with
+ * rounds of one tile per CU, 34..47 = forcedConfig / 64 - 32 pieces with
+ * rounds of one tile per resident workgroup slot; -1 lets the library
+ * choose.  Autotuning times each candidate as a graph replay of a few
+ * launches on a private stream. */
 int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig);
 
 /* ---- epilogue and element-wise ops ------------------------------------- */

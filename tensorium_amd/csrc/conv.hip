@@ -19,6 +19,7 @@
 // shape times the valid candidates with HIP events (when autotuning is on
 // and the stream is not being captured) and caches the fastest; otherwise a
 // wave-quantization cost model picks one.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
@@ -460,9 +461,11 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
   if (int st = grid_for<Cfg>(a, grid)) return st;
   const int64_t tiles = static_cast<int64_t>(a.tilesM) * a.tilesN;
   if (a.tailSplits > 0 && a.splits <= 1) {
-    // whole rounds of tiles over the CUs stay whole; the remainder is cut
-    // along K so that every CU gets about the same work
-    const int64_t full = tiles / cus * cus;
+    // whole rounds of tiles (over the CUs, or over every resident workgroup
+    // slot) stay whole; the remainder is cut along K so that every CU gets
+    // about the same work
+    const int64_t unit = a.tailUnit > 0 ? a.tailUnit : cus;
+    const int64_t full = tiles / unit * unit;
     const int64_t panels = a.g.K / Cfg::BK;
     a.kChunk = (panels + a.tailSplits - 1) / a.tailSplits * Cfg::BK;
     a.tailSplits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty piece
@@ -491,14 +494,46 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
 }
 
 // Floats of tail-split pieces a lean configuration writes (0 when the tiles
-// divide evenly over the CUs).
-int64_t tail_floats(int BM, int BN, int BK, int64_t F, int64_t N, int64_t K, int cus, int tailSplits) {
+// divide evenly into rounds of `unit`).
+int64_t tail_floats(int BM, int BN, int BK, int64_t F, int64_t N, int64_t K, int64_t unit, int tailSplits) {
   const int64_t tiles = ((F + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int64_t rest = tiles % cus;
+  const int64_t rest = tiles % unit;
   const int64_t panels = K / BK;
   const int64_t chunk = (panels + tailSplits - 1) / tailSplits;
   const int64_t pieces = (panels + chunk - 1) / chunk;
-  return tiles < cus ? 0 : rest * pieces * BM * BN;
+  return tiles < unit ? 0 : rest * pieces * BM * BN;
+}
+
+// Workgroups of a lean configuration resident per CU (register and LDS
+// limits), queried once per kernel.
+template <class Cfg>
+int lean_occ(int mode, bool vb) {
+  auto q = [](const void* k) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, Cfg::NT, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    return n > 0 ? n : 1;
+  };
+  static const int occTap = q(reinterpret_cast<const void*>(&conv_lean_kernel<Cfg, kTap3, false>));
+  static const int occ1 = q(reinterpret_cast<const void*>(&conv_lean_kernel<Cfg, k1x1, false>));
+  static const int occ1v = q(reinterpret_cast<const void*>(&conv_lean_kernel<Cfg, k1x1, true>));
+  return mode == kTap3 ? occTap : (vb ? occ1v : occ1);
+}
+
+int lean_occupancy(int cfg, int mode, bool vb) {
+  switch (cfg) {
+    case 11: return lean_occ<Lean11>(mode, vb);
+    case 12: return lean_occ<Lean12>(mode, vb);
+    case 13: return lean_occ<Lean13>(mode, vb);
+    case 14: return lean_occ<Lean14>(mode, vb);
+    case 15: return lean_occ<Lean15>(mode, vb);
+    case 16: return lean_occ<Lean16>(mode, vb);
+    case 17: return lean_occ<Lean17>(mode, vb);
+    case 18: return lean_occ<Lean18>(mode, vb);
+    default: return lean_occ<Lean19>(mode, vb);
+  }
 }
 
 template <class D>
@@ -553,7 +588,8 @@ __global__ void pack_weights_kernel(int64_t total, int64_t C, int64_t taps, cons
 
 struct Cand {
   int cfg, splits;
-  int tail;  // tail-split pieces per remainder tile (lean configurations), 0: none
+  int tail;   // tail-split pieces per remainder tile (lean configurations), 0: none
+  int slots;  // tail split: rounds of every resident workgroup slot (1) or of the CUs (0)
 };
 
 // Estimated time (arbitrary units): rounds of resident tiles times the work
@@ -621,8 +657,8 @@ extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t
 
 extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
-  TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 31 &&
-              forcedConfig / 64 != 17,
+  TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 47 &&
+              forcedConfig / 64 != 17 && forcedConfig / 64 != 32 && forcedConfig / 64 != 33,
           "conv2d_set_autotune: config %d", forcedConfig);
   g_autotune = enable != 0;
   g_forced_cfg = forcedConfig;
@@ -718,26 +754,38 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   // Candidates: every valid tile shape, and for shapes that leave the CUs
   // under-filled also split-K factors (partial sums in the context
   // workspace, reduced in fixed order).
-  // Lean configurations whose tile count is not a multiple of the CU count
-  // also try tail splits (the last partial round of tiles cut along K).
+  // Candidates, first round: every valid tile shape, and for shapes that
+  // leave the CUs under-filled also uniform split-K factors.  Second round
+  // (timed tuning only): tail splits of the fastest lean shapes whose tiles
+  // do not divide into whole rounds.
   const int cus = cx->cu_count;
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
     if (!cfg_valid(c, mode, C, va, smallIO)) continue;
-    cands.push_back({c, 1, 0});
+    cands.push_back({c, 1, 0, 0});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
-    if (ci.kind == kLean && tiles > cus && tiles % cus != 0)
-      for (int tp : {2, 3, 4, 6, 8})
-        if (K >= static_cast<int64_t>(tp) * ci.BK * 2) cands.push_back({c, 1, tp});
     if (tiles >= 2 * cus) continue;
     for (int sp : {2, 4, 8, 16})
-      if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp, 0});
+      if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp, 0, 0});
   }
+  auto unitOf = [&](const Cand& c) -> int64_t {
+    return c.slots ? static_cast<int64_t>(cus) * lean_occupancy(c.cfg, mode, vb) : cus;
+  };
+  auto tailCands = [&](int c, std::vector<Cand>& out) {
+    const CfgInfo& ci = kCfgs[c];
+    const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
+    for (int sl = 0; sl < 2; ++sl) {
+      const int64_t unit = unitOf({c, 1, 2, sl});
+      if (tiles <= unit || tiles % unit == 0 || (sl == 1 && unit == cus)) continue;
+      for (int tp : {2, 3, 4, 6, 8})
+        if (K >= static_cast<int64_t>(tp) * ci.BK * 2) out.push_back({c, 1, tp, sl});
+    }
+  };
   auto wsFloats = [&](const Cand& c) -> int64_t {
     if (c.tail > 0) {
       const CfgInfo& ci = kCfgs[c.cfg];
-      return tail_floats(ci.BM, ci.BN, ci.BK, F, N, K, cus, c.tail);
+      return tail_floats(ci.BM, ci.BN, ci.BK, F, N, K, unitOf(c), c.tail);
     }
     return c.splits > 1 ? c.splits * F * N : 0;
   };
@@ -749,12 +797,14 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     ConvArgs b = a;
     b.splits = 1;
     b.tailSplits = 0;
+    b.tailUnit = 0;
     b.part = nullptr;
     if (c.splits > 1 || c.tail > 0) {
       b.part = wsFor(c);
       if (b.part) {
         b.splits = c.splits;
         b.tailSplits = c.tail;
+        b.tailUnit = c.tail > 0 ? static_cast<int>(unitOf(c)) : 0;
       }
     }
     return launch(c.cfg, b, mode, va, vb, cus, s);
@@ -774,11 +824,11 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   {
     std::lock_guard<std::mutex> lk(g_tune_mu);
     if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO)) {
-      const int hi = g_forced_cfg / 64;
-      if (hi > 17)
-        return kCfgs[g_forced_cfg % 64].kind == kLean ? run({g_forced_cfg % 64, 1, hi - 16})
-                                                      : fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
-      return run({g_forced_cfg % 64, hi > 1 ? hi : 1, 0});
+      const int c = g_forced_cfg % 64, hi = g_forced_cfg / 64;
+      if (hi > 16 && kCfgs[c].kind != kLean) return fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
+      if (hi >= 34) return run({c, 1, hi - 32, 1});
+      if (hi >= 18) return run({c, 1, hi - 16, 0});
+      return run({c, hi > 1 ? hi : 1, 0, 0});
     }
     auto it = g_tuned.find(key);
     if (it != g_tuned.end()) return run(it->second);
@@ -787,7 +837,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
       if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
     }
   }
-  if (tune && cands.size() > 1) {
+  if (tune) {
     // Time each candidate as it runs in a graph replay: kReps launches
     // captured into a graph on the context's private tuning stream, replayed
     // twice after a warm-up replay; the faster replay counts.  Eager timing
@@ -796,11 +846,6 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     // The output is rewritten identically by every run (out never aliases x
     // or residual).  Workspaces are grown before any capture.
     constexpr int kReps = 4;
-    int64_t maxWs = 0;
-    Cand maxC{0, 1, 0};
-    for (const Cand& c : cands)
-      if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
-    if (maxWs > 0) (void)wsFor(maxC);
     const hipStream_t ts = cx->tune_stream;
     if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
     hipEvent_t e0, e1;
@@ -832,13 +877,35 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
       if (g) (void)hipGraphDestroy(g);
       return st;
     };
+    // times a list of candidates; returns the per-candidate times
     float bestMs = 1e30f;
-    int st = TNH_OK;
-    for (const Cand& c : cands) {
-      if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
-      float ms = 0.f;
-      if ((st = timeCand(c, ms))) break;
-      if (ms < bestMs) bestMs = ms, best = c;
+    auto timeAll = [&](const std::vector<Cand>& list, std::vector<float>& times) -> int {
+      int64_t maxWs = 0;
+      Cand maxC{0, 1, 0, 0};
+      for (const Cand& c : list)
+        if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
+      if (maxWs > 0) (void)wsFor(maxC);
+      times.assign(list.size(), 1e30f);
+      for (size_t i = 0; i < list.size(); ++i) {
+        const Cand& c = list[i];
+        if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
+        if (int st = timeCand(c, times[i])) return st;
+        if (times[i] < bestMs) bestMs = times[i], best = c;
+      }
+      return TNH_OK;
+    };
+    std::vector<float> times;
+    int st = timeAll(cands, times);
+    if (!st) {
+      // tail splits of the three fastest whole-K lean candidates
+      std::vector<size_t> order;
+      for (size_t i = 0; i < cands.size(); ++i)
+        if (kCfgs[cands[i].cfg].kind == kLean && cands[i].splits == 1) order.push_back(i);
+      std::sort(order.begin(), order.end(), [&](size_t x, size_t y) { return times[x] < times[y]; });
+      std::vector<Cand> second;
+      for (size_t r = 0; r < order.size() && r < 3; ++r) tailCands(cands[order[r]].cfg, second);
+      std::vector<float> t2;
+      st = timeAll(second, t2);
     }
     (void)hipStreamSynchronize(ts);
     (void)hipEventDestroy(e0);
@@ -849,10 +916,11 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
     if (verbose)
       std::fprintf(stderr,
-                   "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d tail %d "
+                   "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d tail %d%s "
                    "%.4f ms\n",
                    (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
-                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, best.tail, bestMs);
+                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, best.tail,
+                   best.slots ? "/slots" : "", bestMs);
   }
   return run(best);
 }

@@ -35,6 +35,7 @@ struct ConvArgs {
   // conv_tail_reduce.  tailSplits == 0: off.
   int tailSplits;
   int nFull;
+  int tailUnit;  // host only: tiles per whole round (the CU count, or CUs x resident workgroups)
 };
 
 // K walk / B operand of a convolution kernel
@@ -72,13 +73,26 @@ __device__ inline void conv_store(const ConvArgs& a, const f32x16 (&acc)[FM][FN]
     return;
   }
   const int64_t OHW = a.g.OHW;
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
+  // Per column: the residual values are all loaded before the first store
+  // (a store may alias a later residual element), and the wave-uniform
+  // activation selects straight-line code.
+  auto column = [&](auto actTag, int j) {
+    constexpr int ACT = decltype(actTag)::value;
     const int64_t n = n0w + j * 32 + (lane & 31);
-    if (n >= a.g.N) continue;
+    if (n >= a.g.N) return;
     const int64_t b = n / OHW, p = n - b * OHW;
     float* out = a.out + b * a.outBatchStride + p;
-    const float* res = a.res ? a.res + b * a.rBatchStride + p : nullptr;
+    float rv[FM][16];
+    if (a.res) {
+      const float* res = a.res + b * a.rBatchStride + p;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t f = m0w + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          rv[i][r] = f < a.F ? res[f * OHW] : 0.f;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -87,10 +101,19 @@ __device__ inline void conv_store(const ConvArgs& a, const f32x16 (&acc)[FM][FN]
         if (f >= a.F) continue;
         float v = acc[i][j][r];
         if (a.bias) v = v + a.bias[f];
-        v = apply_act(v, a.act);
-        if (res) v = v + res[f * OHW];
+        v = apply_act(v, ACT);
+        if (a.res) v = v + rv[i][r];
         out[f * OHW] = v;
       }
+  };
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    if (a.act == TNH_AC_LEAKY)
+      column(std::integral_constant<int, TNH_AC_LEAKY>{}, j);
+    else if (a.act == TNH_AC_LOGISTIC)
+      column(std::integral_constant<int, TNH_AC_LOGISTIC>{}, j);
+    else
+      column(std::integral_constant<int, TNH_AC_LINEAR>{}, j);
   }
 }
 

@@ -33,10 +33,13 @@ WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 # 0..NUM_CONV_CFGS-1: 0-5 LDS-staged, 6-10 register-direct, 11-19 lean
 # software-pipelined); a forced id is
 # tile + CONV_SPLIT_UNIT * splits (uniform split-K, up to 16), or, for a lean
-# tile, tile + CONV_SPLIT_UNIT * (CONV_TAIL_BASE + pieces) (tail split)
+# tile, tile + CONV_SPLIT_UNIT * (base + pieces) (tail split; base
+# CONV_TAIL_BASE: rounds of one tile per CU, CONV_TAIL_SLOT_BASE: rounds of
+# one tile per resident workgroup slot)
 NUM_CONV_CFGS = 20
 CONV_SPLIT_UNIT = 64
 CONV_TAIL_BASE = 16
+CONV_TAIL_SLOT_BASE = 32
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -257,18 +257,22 @@ def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
 _TAIL_REFS = {}
 
 
+@pytest.mark.parametrize("base", [CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE])
 @pytest.mark.parametrize("cfg", [11, 13, 17])
 @pytest.mark.parametrize("pieces", [2, 3, 8])
-@pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 32, 136, 128, 3, 1), (1, 64, 136, 128, 1, 1), (1, 32, 272, 128, 3, 2)])
-def test_conv_tail_split(hip, cfg, pieces, B, Cc, Hh, F, k, s):
-    """Tail split: whole rounds of tiles over the CUs, the remainder cut into
-    K pieces summed in K order by a second kernel, then the epilogue."""
-    case(f"conv tail split {pieces} cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(4, 32, 184, 128, 3, 1), (4, 64, 184, 128, 1, 1), (4, 32, 368, 128, 3, 2)])
+def test_conv_tail_split(hip, base, cfg, pieces, B, Cc, Hh, F, k, s):
+    """Tail split: whole rounds of tiles (one per CU, or one per resident
+    workgroup slot), the remainder cut into K pieces summed in K order by a
+    second kernel, then the epilogue."""
+    case(f"conv tail split {pieces} base {base} cfg{cfg} B{B} C{Cc} H{Hh} F{F} k{k} s{s}")
     p = k // 2
     OH = (Hh + 2 * p - k) // s + 1
     bm, bn = {11: (64, 64), 13: (128, 64), 17: (128, 64)}[cfg]
     tiles = -(-F // bm) * -(-(B * OH * OH) // bn)
-    assert tiles > hip.cuCount() and tiles % hip.cuCount() != 0, "shape must leave a partial round"
+    # more tiles than 8 workgroup slots per CU, and a partial last round for
+    # every round size up to that, so the tail is cut in both modes
+    assert tiles > 8 * hip.cuCount() and all(tiles % (o * hip.cuCount()) != 0 for o in range(1, 9))
     key = (B, Cc, Hh, F, k, s)
     if key not in _TAIL_REFS:
         x = synth.uniform(61, (B, Cc, Hh, Hh))
@@ -281,7 +285,7 @@ def test_conv_tail_split(hip, cfg, pieces, B, Cc, Hh, F, k, s):
     packed = torch.empty_like(dW)
     hip.packConvWeights(F, Cc, k, dW, packed)
     dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
-    hip.setConvAutotune(True, cfg + CONV_SPLIT_UNIT * (CONV_TAIL_BASE + pieces))
+    hip.setConvAutotune(True, cfg + CONV_SPLIT_UNIT * (base + pieces))
     try:
         hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(x), 0, packed, D(b), acLEAKY, dout, 0, residual=D(res),
                           weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
