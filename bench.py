@@ -31,7 +31,7 @@ PEAK_HBM = 8.0e12
 # of `bench.py --counter-pass` (FETCH_SIZE then WRITE_SIZE, KiB per dispatch,
 # scaled by a 64 MiB copy: read = 2.0 x FETCH_SIZE, write = 1.0 x WRITE_SIZE);
 # profiles/yolov3_416_b16_conv_lean_kernel.md holds the figures and commands.
-TRAFFIC_TAP3X3_B16 = (2.0 * 103367.8 + 40967.5) * 1024
+TRAFFIC_TAP3X3_B16 = (2.0 * 103199.1 + 40665.2) * 1024
 
 
 def log(*a):
