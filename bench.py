@@ -159,6 +159,34 @@ def time_events(hip, fn, reps):
     return ms
 
 
+def time_graph(hip, fn, reps):
+    """Average ms of fn() as replayed from a HIP graph of `reps` calls (no
+    host launch cost in the timed region: small kernels are not launch-bound).
+    The capture runs on the library's own stream (the null stream that bench
+    shares with torch cannot be captured); the caller has synchronized."""
+    hip.finish()
+    hip.resetStream()
+    hip.graphBegin()
+    for _ in range(reps):
+        fn()
+    g = hip.graphEnd()
+    hip.graphLaunch(g)
+    hip.finish()
+    e0, e1 = hip.eventCreate(), hip.eventCreate()
+    best = 1e30
+    for _ in range(2):
+        hip.eventRecord(e0)
+        hip.graphLaunch(g)
+        hip.eventRecord(e1)
+        best = min(best, hip.eventElapsed(e0, e1) / reps)
+    hip.eventDestroy(e0)
+    hip.eventDestroy(e1)
+    hip.graphDestroy(g)
+    hip.finish()
+    hip.useTorchStream()
+    return best
+
+
 def extra_single_conv(hip):
     """Config 1: one conv layer forward, batch 1, 3x416x416 -> 16 filters 3x3
     s1 p1, weights N(0, 0.05), bias 0, leaky 0.1 (GEMM M=16, N=173056, K=27)."""
@@ -189,13 +217,15 @@ def extra_single_conv(hip):
 
 
 def extra_sgemm(hip):
-    """Config 2: C = op(A)*op(B) (beta 0), A and B ~ U[-1, 1), four variants
-    at 4096^3, NN at 8192^3 and the YOLOv3 conv-shaped skinny GEMMs."""
+    """Config 2: C = op(A)*op(B) (beta 0), A and B ~ U[-1, 1): NN at 512^3 ..
+    8192^3, the four variants at 4096^3 and the YOLOv3 conv-shaped skinny
+    GEMMs, each timed as a graph replay after the first (tuning) call."""
     import torch
 
     from tensorium_amd import synth
 
-    cases = [("NN", 4096, 4096, 4096), ("NT", 4096, 4096, 4096), ("TN", 4096, 4096, 4096),
+    cases = [("NN", 512, 512, 512), ("NN", 1024, 1024, 1024), ("NN", 2048, 2048, 2048),
+             ("NN", 4096, 4096, 4096), ("NT", 4096, 4096, 4096), ("TN", 4096, 4096, 4096),
              ("TT", 4096, 4096, 4096), ("NN", 8192, 8192, 8192), ("NN", 64, 692224, 288),
              ("NN", 256, 43264, 1152), ("NN", 1024, 2704, 4608)]
     res = []
@@ -211,8 +241,8 @@ def extra_sgemm(hip):
             hip.gemm(ta, tb, M, N, K, 1.0, A, 0, lda, B, 0, ldb, 0.0, C, 0, N)
 
         fn()
-        reps = 3 if M * N * K >= 8192 ** 3 else 10
-        ms = time_events(hip, fn, reps)
+        reps = 3 if M * N * K >= 8192 ** 3 else (10 if M * N * K >= 1024 ** 3 else 50)
+        ms = time_graph(hip, fn, reps)
         res.append({"variant": var, "M": M, "N": N, "K": K, "ms": round(ms, 4),
                     "tflops": round(2.0 * M * N * K / ms / 1e9, 2),
                     "frac": round(2.0 * M * N * K / ms * 1e3 / PEAK_FP32_MFMA, 4)})

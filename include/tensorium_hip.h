@@ -103,6 +103,17 @@ int32_t tnh_sgemm_strided_batched(int32_t transA, int32_t transB, int64_t M,
                                   float beta, float *C, int64_t cOff,
                                   int64_t ldc, int64_t strideC,
                                   int64_t batch);
+/* No reference counterpart: enable (1, default) or disable per-shape timing
+ * of the SGEMM tile configuration; forcedConfig >= 0 pins one: 0, 1 the
+ * general 128x128 / 64x64 tiles (any K, alignment, size), 2..5 the lean
+ * 128x128 / 128x64 / 64x128 / 64x64 tiles (need K % 32 == 0, 16-byte
+ * aligned operands with ld % 4 == 0, M and N multiples of 4 where that
+ * operand is row-contiguous, C within 2 GiB; other calls fall back to the
+ * general tiles); -1 lets the library choose.  Every non-split
+ * configuration sums k in the same order, so the choice does not change the
+ * results.  The first call for a shape times the candidates as graph
+ * replays into a scratch C. */
+int32_t tnh_sgemm_set_autotune(int32_t enable, int32_t forcedConfig);
 
 /* ---- im2col / col2im ---------------------------------------------------- */
 /* TNNCuda.im2col (nncuda.pas:1144) / sim2Col (ntensors.pas:11415):

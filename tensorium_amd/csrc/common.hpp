@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <functional>
 
 #include "../../include/tensorium_hip.h"
 
@@ -32,6 +33,13 @@ void* workspace(Context* c, size_t bytes);
 
 // Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).
 Context* ctx();
+
+// Times launch(stream) the way a captured network runs it: `reps` launches
+// captured into a graph on the context's tuning stream, replayed twice after a
+// warm-up replay; ms = the faster replay's time per launch.  The caller
+// synchronizes its own stream first and keeps every buffer the launches touch
+// allocated (nothing may be allocated during the capture).
+int time_graph(Context* cx, const std::function<int(hipStream_t)>& launch, int reps, float& ms);
 
 // Checks a launch or runtime call; returns TNH_OK or TNH_ERR_HIP with text.
 int hip_status(hipError_t e, const char* what);

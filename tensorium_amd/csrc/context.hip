@@ -38,6 +38,40 @@ Context* ctx() {
   return &g_ctx;
 }
 
+int time_graph(Context* cx, const std::function<int(hipStream_t)>& launch, int reps, float& ms) {
+  const hipStream_t ts = cx->tune_stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  ms = 1e30f;
+  int st = hip_status(hipEventCreate(&e0), "hipEventCreate");
+  if (!st) st = hip_status(hipEventCreate(&e1), "hipEventCreate");
+  if (!st) {
+    st = hip_status(hipStreamBeginCapture(ts, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    if (!st) {
+      for (int r = 0; r < reps && !st; ++r) st = launch(ts);
+      const hipError_t ee = hipStreamEndCapture(ts, &g);
+      if (!st) st = hip_status(ee, "hipStreamEndCapture");
+    }
+  }
+  if (!st) st = hip_status(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+  if (!st) st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
+  for (int t = 0; t < 2 && !st; ++t) {
+    (void)hipEventRecord(e0, ts);
+    st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
+    (void)hipEventRecord(e1, ts);
+    if (!st) st = hip_status(hipEventSynchronize(e1), "hipEventSynchronize");
+    float v = 0.f;
+    if (!st && hipEventElapsedTime(&v, e0, e1) == hipSuccess && v / reps < ms) ms = v / reps;
+  }
+  (void)hipStreamSynchronize(ts);
+  if (ge) (void)hipGraphExecDestroy(ge);
+  if (g) (void)hipGraphDestroy(g);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  return st;
+}
+
 void* workspace(Context* c, size_t bytes) {
   if (bytes <= c->wsBytes) return c->ws;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;

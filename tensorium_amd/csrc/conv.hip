@@ -838,44 +838,15 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     }
   }
   if (tune) {
-    // Time each candidate as it runs in a graph replay: kReps launches
-    // captured into a graph on the context's private tuning stream, replayed
-    // twice after a warm-up replay; the faster replay counts.  Eager timing
-    // would charge a candidate the host's launch cost, which at small sizes
-    // exceeds the kernels' own time and penalises split-K's second launch.
-    // The output is rewritten identically by every run (out never aliases x
-    // or residual).  Workspaces are grown before any capture.
+    // Time each candidate as it runs in a graph replay (time_graph).  Eager
+    // timing would charge a candidate the host's launch cost, which at small
+    // sizes exceeds the kernels' own time and penalises split-K's second
+    // launch.  The output is rewritten identically by every run (out never
+    // aliases x or residual).  Workspaces are grown before any capture.
     constexpr int kReps = 4;
-    const hipStream_t ts = cx->tune_stream;
     if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
-    hipEvent_t e0, e1;
-    if (int st = hip_status(hipEventCreate(&e0), "hipEventCreate")) return st;
-    if (int st = hip_status(hipEventCreate(&e1), "hipEventCreate")) {
-      (void)hipEventDestroy(e0);
-      return st;
-    }
     auto timeCand = [&](const Cand& c, float& ms) -> int {
-      hipGraph_t g = nullptr;
-      hipGraphExec_t ge = nullptr;
-      int st = hip_status(hipStreamBeginCapture(ts, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
-      if (st) return st;
-      for (int r = 0; r < kReps && !st; ++r) st = runOn(c, ts);
-      const hipError_t ee = hipStreamEndCapture(ts, &g);
-      if (!st) st = hip_status(ee, "hipStreamEndCapture");
-      if (!st) st = hip_status(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-      if (!st) st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
-      ms = 1e30f;
-      for (int t = 0; t < 2 && !st; ++t) {
-        (void)hipEventRecord(e0, ts);
-        st = hip_status(hipGraphLaunch(ge, ts), "hipGraphLaunch");
-        (void)hipEventRecord(e1, ts);
-        if (!st) st = hip_status(hipEventSynchronize(e1), "hipEventSynchronize");
-        float v = 0.f;
-        if (!st && hipEventElapsedTime(&v, e0, e1) == hipSuccess && v / kReps < ms) ms = v / kReps;
-      }
-      if (ge) (void)hipGraphExecDestroy(ge);
-      if (g) (void)hipGraphDestroy(g);
-      return st;
+      return time_graph(cx, [&](hipStream_t s) { return runOn(c, s); }, kReps, ms);
     };
     // times a list of candidates; returns the per-candidate times
     float bestMs = 1e30f;
@@ -907,9 +878,6 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
       std::vector<float> t2;
       st = timeAll(second, t2);
     }
-    (void)hipStreamSynchronize(ts);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
     if (st) return st;
     std::lock_guard<std::mutex> lk(g_tune_mu);
     g_tuned[key] = best;

@@ -55,30 +55,32 @@ struct SwzPanel {
   __device__ static inline int chunk(int row, int q) { return row * BK + 4 * (q ^ (row & 7)); }
 };
 
-// Weights [F][K] row-major, 16-byte loads.  Thread t owns chunk t % (BK/4)
-// of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 8 == 0, so every row of a
-// thread has the same swizzle).
-template <class Cfg>
-struct LeanA {
-  static constexpr int BK = Cfg::BK, NT = Cfg::NT;
+// k-contiguous operand: row r of the panel is memory row r0 + r (row stride
+// ld floats, rows >= `rows` read 0), 16-byte loads.  Thread t owns chunk
+// t % (BK/4) of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 8 == 0, so every row
+// of a thread has the same swizzle).  The conv weights [F][K] (ld = K), and
+// the GEMM operands A (not transposed) and B (transposed).
+template <int ROWS, int BK_, int NT_>
+struct LeanRowsK {
+  static constexpr int BK = BK_, NT = NT_;
   static constexpr int QPR = BK / 4;
   static constexpr int ROWSTEP = NT / QPR;
-  static constexpr int PER = Cfg::BM / ROWSTEP;
-  using L = SwzPanel<Cfg::BM, BK>;
+  static constexpr int PER = ROWS / ROWSTEP;
+  using L = SwzPanel<ROWS, BK>;
   static constexpr int SIZE = L::SIZE;
-  static_assert(NT % QPR == 0 && Cfg::BM % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0, "LeanA split");
+  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0, "LeanRowsK split");
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t voff[PER];
   int ldsOff;
   f32x4 reg[PER];
 
-  __device__ inline void init(const float* w, int64_t wBytes, int64_t K, int64_t F, int64_t m0, int tid) {
-    rsrc = make_rsrc(w, wBytes);
+  __device__ inline void init(const float* p, int64_t bytes, int64_t ld, int64_t rows, int64_t r0, int tid) {
+    rsrc = make_rsrc(p, bytes);
     const int row = tid / QPR, kq = tid % QPR;
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
-      const int64_t gr = m0 + row + v * ROWSTEP;
-      voff[v] = sel_off(gr < F, static_cast<uint32_t>((gr * K + kq * 4) * 4));
+      const int64_t gr = r0 + row + v * ROWSTEP;
+      voff[v] = sel_off(gr < rows, static_cast<uint32_t>((gr * ld + kq * 4) * 4));
     }
     ldsOff = L::chunk(row, kq);
   }
@@ -90,6 +92,69 @@ struct LeanA {
   __device__ inline void store(lds_t* stage) const {
 #pragma unroll
     for (int v = 0; v < PER; ++v) *reinterpret_cast<lds_f4*>(stage + ldsOff + v * ROWSTEP * BK) = reg[v];
+  }
+};
+
+template <class Cfg>
+using LeanA = LeanRowsK<Cfg::BM, Cfg::BK, Cfg::NT>;
+
+// Row-contiguous operand: element (row r, k) at (r0 + r) + k * ld floats
+// (rows >= `rows` read 0): the GEMM operands A (transposed) and B (not
+// transposed).  VEC (ld % 4 == 0, rows % 4 == 0, 16-byte aligned base):
+// thread t owns rows 4 * (t % (ROWS/4)) .. +3 and k-quads t / (ROWS/4) + j *
+// QSTEP; it loads a 4 (k) x 4 (row) block with four 16-byte loads and stores
+// its transpose, one 16-byte LDS write per row.  Scalar: one row per thread,
+// 4 loads ld floats apart per k-quad.
+template <int ROWS, int BK_, int NT_, bool VEC>
+struct LeanRowsMN {
+  static constexpr int BK = BK_, NT = NT_;
+  static constexpr int CPT = VEC ? 4 : 1;
+  static constexpr int TPR = ROWS / CPT;
+  static constexpr int QSTEP = NT / TPR, NQ = (BK / 4) / QSTEP;
+  using L = SwzPanel<ROWS, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % TPR == 0 && (BK / 4) % QSTEP == 0 && NQ >= 1, "LeanRowsMN split");
+  using Reg = typename std::conditional<VEC, f32x4, float>::type;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t voff, ld4;
+  int ldsOff[NQ][CPT];
+  Reg reg[NQ][4];
+
+  __device__ inline void init(const float* p, int64_t bytes, int64_t ld, int64_t rows, int64_t r0, int tid) {
+    rsrc = make_rsrc(p, bytes);
+    ld4 = static_cast<uint32_t>(ld) * 4u;
+    const int row = (tid % TPR) * CPT, q0 = tid / TPR;
+    const int64_t gr = r0 + row;
+    voff = sel_off(gr < rows, static_cast<uint32_t>((gr + 4 * q0 * ld) * 4));
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) ldsOff[j][c] = L::chunk(row + c, q0 + j * QSTEP);
+  }
+  __device__ inline void load(int64_t k0) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t so = static_cast<uint32_t>(static_cast<int>(k0) + 4 * j * QSTEP + e) * ld4;
+        if constexpr (VEC)
+          reg[j][e] = buf_ld4s(rsrc, voff, so);
+        else
+          reg[j][e] = buf_ld1s(rsrc, voff, so);
+      }
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *reinterpret_cast<lds_f4*>(stage + ldsOff[j][c]) =
+              f32x4{reg[j][0][c], reg[j][1][c], reg[j][2][c], reg[j][3][c]};
+      } else {
+        *reinterpret_cast<lds_f4*>(stage + ldsOff[j][0]) = f32x4{reg[j][0], reg[j][1], reg[j][2], reg[j][3]};
+      }
+    }
   }
 };
 

@@ -40,6 +40,8 @@ NUM_CONV_CFGS = 20
 CONV_SPLIT_UNIT = 64
 CONV_TAIL_BASE = 16
 CONV_TAIL_SLOT_BASE = 32
+# SGEMM tile configurations (tnh_sgemm_set_autotune): 0, 1 general, 2..5 lean
+NUM_SGEMM_CFGS = 6
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
@@ -76,6 +78,7 @@ _PROTOS = {
     "tnh_conv2d_fwd": [i64] * 11 + [vp, i64, i64, vp, i64, i32, vp, i64, i32, vp, i64, i64, vp, i64, i64],
     "tnh_conv2d_pack_weights": [i64, i64, i64, i64, vp, vp],
     "tnh_conv2d_set_autotune": [i32, i32],
+    "tnh_sgemm_set_autotune": [i32, i32],
     "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
     "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
     "tnh_forward_scale": [i64, vp, i64, i64, vp, i64, i64],
@@ -327,6 +330,10 @@ class TNNHip:
 
     def setConvAutotune(self, enable=True, forcedConfig=-1):
         call("tnh_conv2d_set_autotune", 1 if enable else 0, forcedConfig)
+
+    def setSgemmAutotune(self, enable=True, forcedConfig=-1):
+        """Pins an SGEMM tile configuration (0..NUM_SGEMM_CFGS-1, -1: the library's choice)."""
+        call("tnh_sgemm_set_autotune", 1 if enable else 0, forcedConfig)
 
     # -- epilogue / element-wise ---------------------------------------------
     def forwardBias(self, dstSize, dst, offset, srcSize, src, incb, batch):

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -86,6 +86,52 @@ def test_sgemm_alpha_beta_offsets_ld(hip):
     g2, r2 = got[7:].reshape(M, ldc), ref[7:].reshape(M, ldc)
     assert np.array_equal(g2[:, N:], r2[:, N:])                # untouched ld padding
     assert R.rel_err(g2[:, :N], r2[:, :N]) <= TOL
+
+
+@pytest.mark.parametrize("cfg", range(NUM_SGEMM_CFGS))
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(100, 300, 96), (36, 68, 32), (260, 132, 320)])
+def test_sgemm_forced_configs(hip, cfg, ta, tb, M, N, K):
+    """Every SGEMM tile configuration on shapes with edge tiles, padded leading
+    dimensions and beta = 1 (integer data: the sums are exact)."""
+    case(f"sgemm cfg{cfg} ta={ta} tb={tb} {M}x{N}x{K}")
+    rng = np.random.default_rng(cfg * 7919 + M + N + K + 2 * ta + tb)
+    lda, ldb, ldc = (M if ta else K) + 4, (K if tb else N) + 8, N + 4
+    A = rng.integers(-4, 5, (K if ta else M, lda)).astype(np.float32)
+    B = rng.integers(-4, 5, (N if tb else K, ldb)).astype(np.float32)
+    C0 = rng.integers(-9, 10, (M, ldc)).astype(np.float32)
+    dA, dB, dC = D(A), D(B), D(C0)
+    hip.setSgemmAutotune(True, cfg)
+    try:
+        hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, lda, dB, 0, ldb, 1.0, dC, 0, ldc)
+    finally:
+        hip.setSgemmAutotune(True, -1)
+    a = A[:, :M].T if ta else A[:, :K]
+    b = B[:, :K].T if tb else B[:, :N]
+    ref = C0.astype(np.int64)
+    ref[:, :N] += a.astype(np.int64) @ b.astype(np.int64)
+    assert np.array_equal(H(dC, hip), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("cfg", range(2, NUM_SGEMM_CFGS))
+def test_sgemm_lean_batched_alpha_beta(hip, cfg):
+    """Lean tiles through gemmStridedBatched with alpha, beta and a shared A."""
+    case(f"sgemm lean batched cfg{cfg}")
+    M, N, K, batch = 72, 200, 64, 3
+    A = synth.uniform(31, (M, K), -1, 1)
+    B = synth.uniform(32, (batch, K, N), -1, 1)
+    C = synth.uniform(33, (batch, M, N), -1, 1)
+    dA, dB, dC = D(A), D(B), D(C)
+    hip.setSgemmAutotune(True, cfg)
+    try:
+        hip.gemmStridedBatched(0, 0, M, N, K, 0.5, dA, 0, K, 0, dB, 0, N, K * N, 2.0, dC, 0, N, M * N, batch)
+    finally:
+        hip.setSgemmAutotune(True, -1)
+    got = H(dC, hip)
+    for i in range(batch):
+        ref = C[i].copy()
+        R.sgemm(0, 0, M, N, K, 0.5, A, K, np.ascontiguousarray(B[i]), N, 2.0, ref, N)
+        assert R.rel_err(got[i], ref) <= TOL
 
 
 def test_sgemm_beta_zero_overwrites(hip):
