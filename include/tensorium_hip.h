@@ -175,6 +175,26 @@ int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W,
 int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw,
                             int64_t pH, int64_t pW, int64_t sY, int64_t sX,
                             int64_t *OH, int64_t *OW);
+/* No reference counterpart: the convolution of tnh_conv2d_fwd on
+ * channels-last (NHWC) tensors, the layout a network keeps between its
+ * layers on this device (the input image stays NCHW).  Pixel (b, y, x) of x
+ * starts at x + xOff + ((b*H + y)*W + x)*xPix (xPix >= C: a tensor may be a
+ * channel slice of a wider buffer, e.g. a route/concat destination); out
+ * and residual likewise with outPix / rPix and the output geometry.
+ * Weights are tap-major [F][kh][kw][C] (tnh_conv2d_pack_weights).  Supports
+ * 3x3 (any stride/padding) and 1x1 stride 1; C % 32 == 0, x and weights
+ * 16-byte aligned with xPix % 4 == 0, out and residual within 2 GiB each.
+ * xPix == 0 with C <= 4 and a 3x3 kernel reads x as NCHW [batch][C][H][W]
+ * (the network's first layer).  The results equal tnh_conv2d_fwd's on the
+ * same data up to the fp32 summation order (the few-channel path: exactly). */
+int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W,
+                            int64_t F, int64_t kh, int64_t kw, int64_t pH,
+                            int64_t pW, int64_t sY, int64_t sX,
+                            const float *x, int64_t xOff, int64_t xPix,
+                            const float *weights, int64_t wOff,
+                            const float *bias, int64_t biasOff, int32_t act,
+                            const float *residual, int64_t rOff, int64_t rPix,
+                            float *out, int64_t outOff, int64_t outPix);
 /* No reference counterpart (layout helper): dst[f][ky][kx][c] =
  * src[f][c][ky][kx] on the device; src and dst must not overlap. */
 int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,

@@ -244,7 +244,9 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
 // the reference order k = (c*3 + ky)*3 + kx from 0, padding taps included as
 // zeros: exactly the arithmetic of the reference CPU path (im2col, then the
 // saxpy chain of ntensors.pas:1308-1436), then bias, activation, residual.
-template <int C, bool TAP>
+// The input is always NCHW (the network's image); NHWC writes the output
+// channels-last (pixel stride a.outPix, residual a.resPix).
+template <int C, bool TAP, bool NHWC>
 __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w) {
   constexpr int K = 9 * C;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -270,14 +272,16 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
         in[(c * 3 + ky) * 3 + kx] =
             buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
       }
-  float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
-  const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
+  // element f of this pixel: NCHW f*OHW floats apart, NHWC adjacent
+  float* out = NHWC ? a.out + n * a.outPix : a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
+  const float* res = !a.res ? nullptr : NHWC ? a.res + n * a.resPix : a.res + static_cast<int64_t>(b) * a.rBatchStride + p;
+  const int64_t fStride = NHWC ? 1 : OHW;
   auto finish = [&](int f, float acc) {
     float v = acc;
     if (a.bias) v = v + a.bias[f];
     v = apply_act(v, a.act);
-    if (res) v = v + res[static_cast<int64_t>(f) * OHW];
-    out[static_cast<int64_t>(f) * OHW] = v;
+    if (res) v = v + res[f * fStride];
+    out[f * fStride] = v;
   };
   // weight of filter f at reference index k = c*9 + t
   auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
@@ -299,14 +303,14 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
   }
 }
 
-template <bool TAP>
+template <bool TAP, bool NHWC>
 int launch_smallc(const ConvArgs& a, hipStream_t s) {
   const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
   switch (a.g.C) {
-    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
   }
   return launch_status("conv_smallc_kernel");
 }
@@ -493,10 +497,9 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
   return launch_reduce(a, s);
 }
 
-// Floats of tail-split pieces a lean configuration writes (0 when the tiles
-// divide evenly into rounds of `unit`).
-int64_t tail_floats(int BM, int BN, int BK, int64_t F, int64_t N, int64_t K, int64_t unit, int tailSplits) {
-  const int64_t tiles = ((F + BM - 1) / BM) * ((N + BN - 1) / BN);
+// Floats of tail-split pieces a lean configuration writes for `tiles` tiles
+// (0 when they divide evenly into rounds of `unit`).
+int64_t tail_floats(int64_t tiles, int BM, int BN, int BK, int64_t K, int64_t unit, int tailSplits) {
   const int64_t rest = tiles % unit;
   const int64_t panels = K / BK;
   const int64_t chunk = (panels + tailSplits - 1) / tailSplits;
@@ -522,17 +525,92 @@ int lean_occ(int mode, bool vb) {
   return mode == kTap3 ? occTap : (vb ? occ1v : occ1);
 }
 
-int lean_occupancy(int cfg, int mode, bool vb) {
+template <class Cfg>
+int nhwc_occ(int mode) {
+  auto q = [](const void* k) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, Cfg::NT, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    return n > 0 ? n : 1;
+  };
+  static const int occTap = q(reinterpret_cast<const void*>(&conv_nhwc_kernel<Cfg, kTap3>));
+  static const int occ1 = q(reinterpret_cast<const void*>(&conv_nhwc_kernel<Cfg, k1x1>));
+  return mode == kTap3 ? occTap : occ1;
+}
+
+// Resident workgroups per CU of a lean configuration's kernel for this
+// layout and mode.
+int lean_occupancy(int cfg, int mode, bool vb, bool nhwc) {
   switch (cfg) {
-    case 11: return lean_occ<Lean11>(mode, vb);
-    case 12: return lean_occ<Lean12>(mode, vb);
-    case 13: return lean_occ<Lean13>(mode, vb);
-    case 14: return lean_occ<Lean14>(mode, vb);
-    case 15: return lean_occ<Lean15>(mode, vb);
-    case 16: return lean_occ<Lean16>(mode, vb);
-    case 17: return lean_occ<Lean17>(mode, vb);
-    case 18: return lean_occ<Lean18>(mode, vb);
-    default: return lean_occ<Lean19>(mode, vb);
+    case 11: return nhwc ? nhwc_occ<Lean11>(mode) : lean_occ<Lean11>(mode, vb);
+    case 12: return nhwc ? nhwc_occ<Lean12>(mode) : lean_occ<Lean12>(mode, vb);
+    case 13: return nhwc ? nhwc_occ<Lean13>(mode) : lean_occ<Lean13>(mode, vb);
+    case 14: return nhwc ? nhwc_occ<Lean14>(mode) : lean_occ<Lean14>(mode, vb);
+    case 15: return nhwc ? nhwc_occ<Lean15>(mode) : lean_occ<Lean15>(mode, vb);
+    case 16: return nhwc ? nhwc_occ<Lean16>(mode) : lean_occ<Lean16>(mode, vb);
+    case 17: return nhwc ? nhwc_occ<Lean17>(mode) : lean_occ<Lean17>(mode, vb);
+    case 18: return nhwc ? nhwc_occ<Lean18>(mode) : lean_occ<Lean18>(mode, vb);
+    default: return nhwc ? nhwc_occ<Lean19>(mode) : lean_occ<Lean19>(mode, vb);
+  }
+}
+
+// Channels-last launch of a lean configuration: rows are output pixels
+// (tiles of BM), columns filters (tiles of BN).  a.tailSplits > 0 cuts the
+// tiles beyond the last whole round of a.tailUnit tiles (the CU count when
+// 0; every tile when negative) into K pieces.
+template <class Cfg>
+int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
+  const int64_t tm = (a.g.N + Cfg::BM - 1) / Cfg::BM, tn = (a.F + Cfg::BN - 1) / Cfg::BN;
+  if (tm * tn > INT32_MAX) return fail(TNH_ERR_UNSUPPORTED, "conv2d: grid too large");
+  a.tilesM = static_cast<int>(tm);
+  a.tilesN = static_cast<int>(tn);
+  a.splits = 1;
+  a.kChunk = a.g.K;
+  const int64_t tiles = tm * tn;
+  int64_t grid = tiles;
+  if (a.tailSplits > 0) {
+    const int64_t unit = a.tailUnit > 0 ? a.tailUnit : cus;
+    const int64_t full = a.tailUnit < 0 ? 0 : tiles / unit * unit;
+    const int64_t panels = a.g.K / Cfg::BK;
+    a.kChunk = (panels + a.tailSplits - 1) / a.tailSplits * Cfg::BK;
+    a.tailSplits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty piece
+    if (full == tiles || a.tailSplits < 2 || (tiles - full) * a.tailSplits + full > INT32_MAX) {
+      a.tailSplits = 0;
+      a.kChunk = a.g.K;
+    } else {
+      a.nFull = static_cast<int>(full);
+      grid = full + (tiles - full) * a.tailSplits;
+    }
+  } else {
+    a.tailSplits = 0;
+  }
+  if (mode == kTap3)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3>), dim3(static_cast<unsigned>(grid)), dim3(Cfg::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1>), dim3(static_cast<unsigned>(grid)), dim3(Cfg::NT), 0, s, a);
+  if (int st = launch_status("conv_nhwc_kernel")) return st;
+  if (a.tailSplits > 0) {
+    hipLaunchKernelGGL((conv_tail_reduce<Cfg, true>), dim3(static_cast<unsigned>(tiles - a.nFull)), dim3(Cfg::NT), 0,
+                       s, a);
+    return launch_status("conv_tail_reduce");
+  }
+  return TNH_OK;
+}
+
+int launch_nhwc_cfg(int cfg, const ConvArgs& a, int mode, int cus, hipStream_t s) {
+  switch (cfg) {
+    case 11: return launch_nhwc<Lean11>(a, mode, cus, s);
+    case 12: return launch_nhwc<Lean12>(a, mode, cus, s);
+    case 13: return launch_nhwc<Lean13>(a, mode, cus, s);
+    case 14: return launch_nhwc<Lean14>(a, mode, cus, s);
+    case 15: return launch_nhwc<Lean15>(a, mode, cus, s);
+    case 16: return launch_nhwc<Lean16>(a, mode, cus, s);
+    case 17: return launch_nhwc<Lean17>(a, mode, cus, s);
+    case 18: return launch_nhwc<Lean18>(a, mode, cus, s);
+    case 19: return launch_nhwc<Lean19>(a, mode, cus, s);
+    default: return fail(TNH_ERR_UNSUPPORTED, "conv2d: channels-last convolution needs a lean tile (11..19)");
   }
 }
 
@@ -609,16 +687,18 @@ float cost(const CfgInfo& c, int64_t F, int64_t N, int64_t K, int cus, int split
 struct TuneKey {
   int64_t F, N, K, C, H, W;
   int k, s, mode, va, vb;
+  int nhwc, xPix, outPix, resPix;
   bool operator==(const TuneKey& o) const {
     return F == o.F && N == o.N && K == o.K && C == o.C && H == o.H && W == o.W && k == o.k && s == o.s &&
-           mode == o.mode && va == o.va && vb == o.vb;
+           mode == o.mode && va == o.va && vb == o.vb && nhwc == o.nhwc && xPix == o.xPix && outPix == o.outPix &&
+           resPix == o.resPix;
   }
 };
 struct TuneHash {
   size_t operator()(const TuneKey& t) const {
     size_t h = 1469598103934665603ull;
     for (int64_t v : {t.F, t.N, t.K, t.C, t.H, t.W, (int64_t)t.k, (int64_t)t.s, (int64_t)t.mode, (int64_t)t.va,
-                      (int64_t)t.vb})
+                      (int64_t)t.vb, (int64_t)t.nhwc, (int64_t)t.xPix, (int64_t)t.outPix, (int64_t)t.resPix})
       h = (h ^ static_cast<size_t>(v)) * 1099511628211ull;
     return h;
   }
@@ -631,12 +711,166 @@ int g_forced_cfg = -1;
 
 // The register-direct kernels need whole 16-channel chunks inside one tap
 // and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
-bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO) {
+bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = false) {
+  if (nhwc) return kCfgs[c].kind == kLean && smallIO && va && C % kCfgs[c].BK == 0;
   if (kCfgs[c].kind == kLean && !smallIO) return false;
   if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
   if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;
   if (mode == kTap3) return C % kCfgs[c].BK == 0;
   return true;
+}
+
+// Candidate tile configurations for one convolution call, timed on the
+// first call for its shape (and layout), then launched.
+int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool smallIO, bool nhwc, const TuneKey& key) {
+  const int64_t F = a.F, N = a.g.N, K = a.g.K, C = a.g.C;
+  const int kh = key.k, sY = key.s;
+  auto tilesOf = [&](const CfgInfo& ci) -> int64_t {
+    return nhwc ? ((N + ci.BM - 1) / ci.BM) * ((F + ci.BN - 1) / ci.BN)
+                : ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
+  };
+  // Candidates, first round: every valid tile shape, and for shapes that
+  // leave the CUs under-filled also uniform split-K factors.  Second round
+  // (timed tuning only): tail splits of the fastest lean shapes whose tiles
+  // do not divide into whole rounds.
+  const int cus = cx->cu_count;
+  std::vector<Cand> cands;
+  for (int c = 0; c < kNumCfg; ++c) {
+    if (!cfg_valid(c, mode, C, va, smallIO, nhwc)) continue;
+    cands.push_back({c, 1, 0, 0});
+    const CfgInfo& ci = kCfgs[c];
+    const int64_t tiles = tilesOf(ci);
+    if (tiles >= 2 * cus) continue;
+    for (int sp : {2, 4, 8, 16})
+      if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4)
+        cands.push_back(nhwc ? Cand{c, 1, sp, 2} : Cand{c, sp, 0, 0});
+  }
+  auto unitOf = [&](const Cand& c) -> int64_t {
+    if (c.slots == 2) return -1;  // every tile cut
+    return c.slots ? static_cast<int64_t>(cus) * lean_occupancy(c.cfg, mode, vb, nhwc) : cus;
+  };
+  auto tailCands = [&](int c, std::vector<Cand>& out) {
+    const CfgInfo& ci = kCfgs[c];
+    const int64_t tiles = tilesOf(ci);
+    for (int sl = 0; sl < 2; ++sl) {
+      const int64_t unit = unitOf({c, 1, 2, sl});
+      if (tiles <= unit || tiles % unit == 0 || (sl == 1 && unit == cus)) continue;
+      for (int tp : {2, 3, 4, 6, 8})
+        if (K >= static_cast<int64_t>(tp) * ci.BK * 2) out.push_back({c, 1, tp, sl});
+    }
+  };
+  auto wsFloats = [&](const Cand& c) -> int64_t {
+    if (c.tail > 0) {
+      const CfgInfo& ci = kCfgs[c.cfg];
+      const int64_t unit = unitOf(c);
+      const int64_t panels = K / ci.BK, chunk = (panels + c.tail - 1) / c.tail;
+      return unit < 0 ? tilesOf(ci) * ((panels + chunk - 1) / chunk) * ci.BM * ci.BN
+                      : tail_floats(tilesOf(ci), ci.BM, ci.BN, ci.BK, K, unit, c.tail);
+    }
+    return c.splits > 1 ? c.splits * F * N : 0;
+  };
+  auto wsFor = [&](const Cand& c) -> float* {
+    const int64_t n = wsFloats(c);
+    return n > 0 ? static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4)) : nullptr;
+  };
+  auto runOn = [&](const Cand& c, hipStream_t s) -> int {
+    ConvArgs b = a;
+    b.splits = 1;
+    b.tailSplits = 0;
+    b.tailUnit = 0;
+    b.part = nullptr;
+    if (c.splits > 1 || c.tail > 0) {
+      b.part = wsFor(c);
+      if (b.part) {
+        b.splits = c.splits;
+        b.tailSplits = c.tail;
+        b.tailUnit = c.tail > 0 ? static_cast<int>(unitOf(c)) : 0;  // -1: every tile
+      }
+    }
+    return nhwc ? launch_nhwc_cfg(c.cfg, b, mode, cus, s) : launch(c.cfg, b, mode, va, vb, cus, s);
+  };
+  auto run = [&](const Cand& c) -> int { return runOn(c, cx->stream); };
+  Cand best = cands[0];
+  {
+    float bc = 1e30f;
+    for (const Cand& c : cands) {
+      const float v = cost(kCfgs[c.cfg], F, N, K, cx->cu_count, c.splits);
+      if (v < bc) bc = v, best = c;
+    }
+  }
+  bool tune = false;
+  const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO, nhwc)) {
+      const int c = g_forced_cfg % 64, hi = g_forced_cfg / 64;
+      if (hi > 16 && kCfgs[c].kind != kLean) return fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
+      if (nhwc && hi >= 2 && hi <= 16) return run({c, 1, hi, 2});  // split-K: every tile cut
+      if (hi >= 34) return run({c, 1, hi - 32, 1});
+      if (hi >= 18) return run({c, 1, hi - 16, 0});
+      return run({c, hi > 1 ? hi : 1, 0, 0});
+    }
+    auto it = g_tuned.find(key);
+    if (it != g_tuned.end()) return run(it->second);
+    if (g_autotune && !aliased) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
+    }
+  }
+  if (tune) {
+    // Time each candidate as it runs in a graph replay (time_graph).  Eager
+    // timing would charge a candidate the host's launch cost, which at small
+    // sizes exceeds the kernels' own time and penalises split-K's second
+    // launch.  The output is rewritten identically by every run (out never
+    // aliases x or residual).  Workspaces are grown before any capture.
+    constexpr int kReps = 4;
+    if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
+    auto timeCand = [&](const Cand& c, float& ms) -> int {
+      return time_graph(cx, [&](hipStream_t s) { return runOn(c, s); }, kReps, ms);
+    };
+    // times a list of candidates; returns the per-candidate times
+    float bestMs = 1e30f;
+    auto timeAll = [&](const std::vector<Cand>& list, std::vector<float>& times) -> int {
+      int64_t maxWs = 0;
+      Cand maxC{0, 1, 0, 0};
+      for (const Cand& c : list)
+        if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
+      if (maxWs > 0) (void)wsFor(maxC);
+      times.assign(list.size(), 1e30f);
+      for (size_t i = 0; i < list.size(); ++i) {
+        const Cand& c = list[i];
+        if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
+        if (int st = timeCand(c, times[i])) return st;
+        if (times[i] < bestMs) bestMs = times[i], best = c;
+      }
+      return TNH_OK;
+    };
+    std::vector<float> times;
+    int st = timeAll(cands, times);
+    if (!st) {
+      // tail splits of the three fastest whole-K lean candidates
+      std::vector<size_t> order;
+      for (size_t i = 0; i < cands.size(); ++i)
+        if (kCfgs[cands[i].cfg].kind == kLean && cands[i].splits == 1 && cands[i].tail == 0) order.push_back(i);
+      std::sort(order.begin(), order.end(), [&](size_t x, size_t y) { return times[x] < times[y]; });
+      std::vector<Cand> second;
+      for (size_t r = 0; r < order.size() && r < 3; ++r) tailCands(cands[order[r]].cfg, second);
+      std::vector<float> t2;
+      st = timeAll(second, t2);
+    }
+    if (st) return st;
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tuned[key] = best;
+    static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
+    if (verbose)
+      std::fprintf(stderr,
+                   "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d tail %d%s "
+                   "%.4f ms\n",
+                   (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
+                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, best.tail,
+                   best.slots ? "/slots" : "", bestMs);
+  }
+  return run(best);
 }
 
 }  // namespace
@@ -645,6 +879,64 @@ bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO) {
 
 using namespace tnh;
 using namespace tnh::conv;
+
+extern "C" int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                       int64_t kw, int64_t pH, int64_t pW, int64_t sY, int64_t sX, const float* x,
+                                       int64_t xOff, int64_t xPix, const float* weights, int64_t wOff,
+                                       const float* bias, int64_t biasOff, int32_t act, const float* residual,
+                                       int64_t rOff, int64_t rPix, float* out, int64_t outOff, int64_t outPix) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0, "conv2d_nhwc: bad sizes");
+  TNH_ARG(kh == kw && (kh == 1 || kh == 3), "conv2d_nhwc: only square 1x1 / 3x3 kernels are supported");
+  TNH_ARG(sY > 0 && sX > 0 && pH >= 0 && pW >= 0, "conv2d_nhwc: bad stride/pad");
+  TNH_ARG(x && weights && out, "conv2d_nhwc: NULL x/weights/out");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "conv2d_nhwc: activation %d", act);
+  TNH_ARG(xOff >= 0 && wOff >= 0 && outOff >= 0 && biasOff >= 0 && rOff >= 0, "conv2d_nhwc: negative offset");
+  const bool xNchw = xPix == 0;  // the network's NCHW image, few-channel 3x3 only
+  TNH_ARG(xNchw ? (kh == 3 && C <= 4) : xPix >= C, "conv2d_nhwc: xPix %lld (C %lld)", (long long)xPix,
+          (long long)C);
+  TNH_ARG(outPix >= F && (!residual || rPix >= F), "conv2d_nhwc: pixel stride below the filter count");
+  const int64_t OH = (H + 2 * pH - kh) / sY + 1, OW = (W + 2 * pW - kw) / sX + 1;
+  TNH_ARG(OH > 0 && OW > 0, "conv2d_nhwc: empty output");
+  TNH_ARG(kh == 3 || (sY == 1 && sX == 1 && pH == 0 && pW == 0), "conv2d_nhwc: 1x1 needs stride 1, no padding");
+  if (batch == 0) return TNH_OK;
+  const int64_t K = C * kh * kw, N = batch * OH * OW;
+  const int64_t xElems = xNchw ? batch * C * H * W : (batch * H * W - 1) * xPix + C;
+  TNH_ARG(xElems * 4 <= kMaxBufBytes, "conv2d_nhwc: input spans more than 2 GiB (split the batch)");
+  TNH_ARG(F * K * 4 <= kMaxBufBytes && OH * OW < (int64_t(1) << 31), "conv2d_nhwc: tensor too large");
+
+  ConvArgs a{};
+  a.g.x = x + xOff;
+  a.g.xBytes = xElems * 4;
+  a.g.xBatchStride = xNchw ? C * H * W : H * W * xPix;
+  a.g.C = (int)C; a.g.H = (int)H; a.g.W = (int)W; a.g.OW = (int)OW; a.g.OHW = (int)(OH * OW);
+  a.g.sY = (int)sY; a.g.sX = (int)sX; a.g.pH = (int)pH; a.g.pW = (int)pW;
+  a.g.N = N; a.g.K = K;
+  a.w = weights + wOff;
+  a.wBytes = F * K * 4;
+  a.bias = bias ? bias + biasOff : nullptr;
+  a.res = residual ? residual + rOff : nullptr;
+  a.out = out + outOff;
+  a.F = F;
+  a.act = act;
+  a.xPix = (int)xPix;
+  a.outPix = (int)outPix;
+  a.resPix = residual ? (int)rPix : 0;
+  a.outBatchStride = OH * OW * outPix;
+  a.rBatchStride = residual ? OH * OW * rPix : 0;
+  a.outBytes = ((N - 1) * outPix + F) * 4;
+  a.resBytes = residual ? ((N - 1) * rPix + F) * 4 : 0;
+  if (xNchw) return launch_smallc<true, true>(a, cx->stream);
+
+  const int mode = kh == 3 ? kTap3 : k1x1;
+  const bool va = aligned16(a.w) && K % 4 == 0 && aligned16(a.g.x) && xPix % 4 == 0;
+  const bool smallIO = a.outBytes <= kMaxBufBytes && a.resBytes <= kMaxBufBytes;
+  TNH_ARG(va && smallIO && C % 32 == 0,
+          "conv2d_nhwc: needs C %% 32 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
+  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, false, 1, (int)xPix, (int)outPix,
+                    residual ? (int)rPix : 0};
+  return conv_dispatch(cx, a, mode, va, false, smallIO, true, key);
+}
 
 extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw, int64_t pH, int64_t pW,
                                        int64_t sY, int64_t sX, int64_t* OH, int64_t* OW) {
@@ -747,148 +1039,10 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
       forced = g_forced_cfg >= 0;
     }
     if (!forced)
-      return weightLayout == TNH_WEIGHTS_TAP_MAJOR ? launch_smallc<true>(a, cx->stream)
-                                                   : launch_smallc<false>(a, cx->stream);
+      return weightLayout == TNH_WEIGHTS_TAP_MAJOR ? launch_smallc<true, false>(a, cx->stream)
+                                                   : launch_smallc<false, false>(a, cx->stream);
   }
 
-  // Candidates: every valid tile shape, and for shapes that leave the CUs
-  // under-filled also split-K factors (partial sums in the context
-  // workspace, reduced in fixed order).
-  // Candidates, first round: every valid tile shape, and for shapes that
-  // leave the CUs under-filled also uniform split-K factors.  Second round
-  // (timed tuning only): tail splits of the fastest lean shapes whose tiles
-  // do not divide into whole rounds.
-  const int cus = cx->cu_count;
-  std::vector<Cand> cands;
-  for (int c = 0; c < kNumCfg; ++c) {
-    if (!cfg_valid(c, mode, C, va, smallIO)) continue;
-    cands.push_back({c, 1, 0, 0});
-    const CfgInfo& ci = kCfgs[c];
-    const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
-    if (tiles >= 2 * cus) continue;
-    for (int sp : {2, 4, 8, 16})
-      if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4) cands.push_back({c, sp, 0, 0});
-  }
-  auto unitOf = [&](const Cand& c) -> int64_t {
-    return c.slots ? static_cast<int64_t>(cus) * lean_occupancy(c.cfg, mode, vb) : cus;
-  };
-  auto tailCands = [&](int c, std::vector<Cand>& out) {
-    const CfgInfo& ci = kCfgs[c];
-    const int64_t tiles = ((F + ci.BM - 1) / ci.BM) * ((N + ci.BN - 1) / ci.BN);
-    for (int sl = 0; sl < 2; ++sl) {
-      const int64_t unit = unitOf({c, 1, 2, sl});
-      if (tiles <= unit || tiles % unit == 0 || (sl == 1 && unit == cus)) continue;
-      for (int tp : {2, 3, 4, 6, 8})
-        if (K >= static_cast<int64_t>(tp) * ci.BK * 2) out.push_back({c, 1, tp, sl});
-    }
-  };
-  auto wsFloats = [&](const Cand& c) -> int64_t {
-    if (c.tail > 0) {
-      const CfgInfo& ci = kCfgs[c.cfg];
-      return tail_floats(ci.BM, ci.BN, ci.BK, F, N, K, unitOf(c), c.tail);
-    }
-    return c.splits > 1 ? c.splits * F * N : 0;
-  };
-  auto wsFor = [&](const Cand& c) -> float* {
-    const int64_t n = wsFloats(c);
-    return n > 0 ? static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4)) : nullptr;
-  };
-  auto runOn = [&](const Cand& c, hipStream_t s) -> int {
-    ConvArgs b = a;
-    b.splits = 1;
-    b.tailSplits = 0;
-    b.tailUnit = 0;
-    b.part = nullptr;
-    if (c.splits > 1 || c.tail > 0) {
-      b.part = wsFor(c);
-      if (b.part) {
-        b.splits = c.splits;
-        b.tailSplits = c.tail;
-        b.tailUnit = c.tail > 0 ? static_cast<int>(unitOf(c)) : 0;
-      }
-    }
-    return launch(c.cfg, b, mode, va, vb, cus, s);
-  };
-  auto run = [&](const Cand& c) -> int { return runOn(c, cx->stream); };
-  Cand best = cands[0];
-  {
-    float bc = 1e30f;
-    for (const Cand& c : cands) {
-      const float v = cost(kCfgs[c.cfg], F, N, K, cx->cu_count, c.splits);
-      if (v < bc) bc = v, best = c;
-    }
-  }
-  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, vb};
-  bool tune = false;
-  const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
-  {
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO)) {
-      const int c = g_forced_cfg % 64, hi = g_forced_cfg / 64;
-      if (hi > 16 && kCfgs[c].kind != kLean) return fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
-      if (hi >= 34) return run({c, 1, hi - 32, 1});
-      if (hi >= 18) return run({c, 1, hi - 16, 0});
-      return run({c, hi > 1 ? hi : 1, 0, 0});
-    }
-    auto it = g_tuned.find(key);
-    if (it != g_tuned.end()) return run(it->second);
-    if (g_autotune && !aliased) {
-      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-      if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
-    }
-  }
-  if (tune) {
-    // Time each candidate as it runs in a graph replay (time_graph).  Eager
-    // timing would charge a candidate the host's launch cost, which at small
-    // sizes exceeds the kernels' own time and penalises split-K's second
-    // launch.  The output is rewritten identically by every run (out never
-    // aliases x or residual).  Workspaces are grown before any capture.
-    constexpr int kReps = 4;
-    if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
-    auto timeCand = [&](const Cand& c, float& ms) -> int {
-      return time_graph(cx, [&](hipStream_t s) { return runOn(c, s); }, kReps, ms);
-    };
-    // times a list of candidates; returns the per-candidate times
-    float bestMs = 1e30f;
-    auto timeAll = [&](const std::vector<Cand>& list, std::vector<float>& times) -> int {
-      int64_t maxWs = 0;
-      Cand maxC{0, 1, 0, 0};
-      for (const Cand& c : list)
-        if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
-      if (maxWs > 0) (void)wsFor(maxC);
-      times.assign(list.size(), 1e30f);
-      for (size_t i = 0; i < list.size(); ++i) {
-        const Cand& c = list[i];
-        if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
-        if (int st = timeCand(c, times[i])) return st;
-        if (times[i] < bestMs) bestMs = times[i], best = c;
-      }
-      return TNH_OK;
-    };
-    std::vector<float> times;
-    int st = timeAll(cands, times);
-    if (!st) {
-      // tail splits of the three fastest whole-K lean candidates
-      std::vector<size_t> order;
-      for (size_t i = 0; i < cands.size(); ++i)
-        if (kCfgs[cands[i].cfg].kind == kLean && cands[i].splits == 1) order.push_back(i);
-      std::sort(order.begin(), order.end(), [&](size_t x, size_t y) { return times[x] < times[y]; });
-      std::vector<Cand> second;
-      for (size_t r = 0; r < order.size() && r < 3; ++r) tailCands(cands[order[r]].cfg, second);
-      std::vector<float> t2;
-      st = timeAll(second, t2);
-    }
-    if (st) return st;
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    g_tuned[key] = best;
-    static const bool verbose = std::getenv("TNH_VERBOSE") != nullptr;
-    if (verbose)
-      std::fprintf(stderr,
-                   "[tnh] conv F=%lld N=%lld K=%lld k=%lld s=%lld mode=%d -> cfg %d (%dx%dx%d) split %d tail %d%s "
-                   "%.4f ms\n",
-                   (long long)F, (long long)N, (long long)K, (long long)kh, (long long)sY, mode, best.cfg,
-                   kCfgs[best.cfg].BM, kCfgs[best.cfg].BN, kCfgs[best.cfg].BK, best.splits, best.tail,
-                   best.slots ? "/slots" : "", bestMs);
-  }
-  return run(best);
+  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, vb, 0, 0, 0, 0};
+  return conv_dispatch(cx, a, mode, va, vb, smallIO, false, key);
 }

@@ -36,6 +36,10 @@ struct ConvArgs {
   int tailSplits;
   int nFull;
   int tailUnit;  // host only: tiles per whole round (the CU count, or CUs x resident workgroups)
+  // Channels-last (NHWC) tensors: floats between consecutive pixels of x, out
+  // and res (the channel count of the buffer a tensor lives in, so a tensor
+  // can be a channel slice of a wider one); images are H*W*pixel-stride apart.
+  int xPix, outPix, resPix;
 };
 
 // K walk / B operand of a convolution kernel
@@ -211,6 +215,77 @@ __device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM]
           float v = apply_act(acc[i][j][r] + bias[i][r], ACT);
           if constexpr (RES) v = v + rv[j][i][r];
           buf_st1s(outR, v, rowOk(c) ? vOut[j] : kOOB, so(i, r));
+        }
+  };
+  using Leaky = std::integral_constant<int, TNH_AC_LEAKY>;
+  using Logistic = std::integral_constant<int, TNH_AC_LOGISTIC>;
+  using Linear = std::integral_constant<int, TNH_AC_LINEAR>;
+  if (a.res) {
+    if (a.act == TNH_AC_LEAKY)
+      finish(Leaky{}, std::true_type{});
+    else if (a.act == TNH_AC_LOGISTIC)
+      finish(Logistic{}, std::true_type{});
+    else
+      finish(Linear{}, std::true_type{});
+  } else {
+    if (a.act == TNH_AC_LEAKY)
+      finish(Leaky{}, std::false_type{});
+    else if (a.act == TNH_AC_LOGISTIC)
+      finish(Logistic{}, std::false_type{});
+    else
+      finish(Linear{}, std::false_type{});
+  }
+}
+
+// Channels-last epilogue (rows m = output pixels, columns = filters): the
+// result of pixel m, filter f goes to out[m * outPix + f] (residual likewise
+// with resPix).  Each lane owns FN filter columns (bias per lane); the pixel
+// part of an offset is wave-uniform (scalar operand).  Residual loads are all
+// issued before the first store; out-of-range elements get kOOB.
+template <int FM, int FN>
+__device__ inline void conv_store_nhwc(const ConvArgs& a, const f32x16 (&acc)[FM][FN], int64_t m0w, int64_t n0w,
+                                       int lane) {
+  const int h = lane >> 5;
+  const int64_t M = a.g.N;
+  const int rowBase = static_cast<int>(m0w) + 4 * h;  // pixel of element (i = 0, r = 0)
+  const bool allRows = m0w + FM * 32 <= M;
+  auto rowOk = [&](int c) { return allRows || rowBase + c < M; };
+  const uint32_t op4 = static_cast<uint32_t>(a.outPix) * 4u, rp4 = static_cast<uint32_t>(a.resPix) * 4u;
+  const __amdgpu_buffer_rsrc_t outR = make_rsrc(a.out, a.outBytes);
+  const __amdgpu_buffer_rsrc_t resR = make_rsrc(a.res, a.resBytes);
+  float bias[FN];
+  uint32_t vOut[FN], vRes[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t f = n0w + j * 32 + (lane & 31);
+    const bool okF = f < a.F;
+    bias[j] = a.bias && okF ? a.bias[f] : -0.f;  // -0.0: the exact additive identity
+    vOut[j] = sel_off(okF, static_cast<uint32_t>(rowBase) * op4 + static_cast<uint32_t>(f) * 4u);
+    vRes[j] = sel_off(okF, static_cast<uint32_t>(rowBase) * rp4 + static_cast<uint32_t>(f) * 4u);
+  }
+  auto rc = [](int i, int r) { return i * 32 + 8 * (r >> 2) + (r & 3); };
+  auto finish = [&](auto actTag, auto resTag) {
+    constexpr int ACT = decltype(actTag)::value;
+    constexpr bool RES = decltype(resTag)::value;
+    float rv[FM][FN][16];
+    if constexpr (RES) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            rv[i][j][r] = buf_ld1s(resR, rowOk(rc(i, r)) ? vRes[j] : kOOB, static_cast<uint32_t>(rc(i, r)) * rp4);
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = apply_act(acc[i][j][r] + bias[j], ACT);
+          if constexpr (RES) v = v + rv[i][j][r];
+          buf_st1s(outR, v, rowOk(rc(i, r)) ? vOut[j] : kOOB, static_cast<uint32_t>(rc(i, r)) * op4);
         }
   };
   using Leaky = std::integral_constant<int, TNH_AC_LEAKY>;

@@ -158,6 +158,77 @@ struct LeanRowsMN {
   }
 };
 
+// Channels-last tap gather as the A operand (row r of the panel = output
+// pixel m0 + r, k = tap*C + c with a panel inside one tap): a row's BK
+// channels are contiguous, so each thread issues PER 16-byte loads per panel.
+// Thread t owns chunk t % (BK/4) of rows t / (BK/4) + v * ROWSTEP.  A row's
+// pixel offset at tap (0, 0) is fixed for the K loop (modulo 2^32: it may
+// point before the image at the border); the uniform tap offset is added per
+// panel, the channel offset rides in the scalar operand, and a per-row tap
+// mask (computed once) sends taps in the padding to kOOB.
+template <int ROWS, int BK_, int NT_, int KH, int KW>
+struct NhwcTapRows {
+  static constexpr int BK = BK_, NT = NT_;
+  static constexpr int QPR = BK / 4;
+  static constexpr int ROWSTEP = NT / QPR;
+  static constexpr int PER = ROWS / ROWSTEP;
+  using L = SwzPanel<ROWS, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0 && KH * KW <= 32,
+                "NhwcTapRows split");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t rowOff[PER];
+  uint32_t tapMask[PER];
+  uint32_t pix4, rowPix4;  // bytes per pixel step, per image row
+  int C;
+  int ldsOff;
+  f32x4 reg[PER];
+
+  __device__ inline void init(const ConvGeom& g, int xPix, int64_t m0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    pix4 = static_cast<uint32_t>(xPix) * 4u;
+    rowPix4 = static_cast<uint32_t>(g.W) * pix4;
+    const int row = tid / QPR, kq = tid % QPR;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int64_t n = m0 + row + v * ROWSTEP;
+      const bool ok = n < g.N;
+      const int64_t nn = ok ? n : 0;
+      const int64_t b = nn / g.OHW;
+      const int p = static_cast<int>(nn - b * g.OHW);
+      const int oy = p / g.OW, ox = p - (p / g.OW) * g.OW;
+      const int iy0 = oy * g.sY - g.pH, ix0 = ox * g.sX - g.pW;
+      rowOff[v] = static_cast<uint32_t>(((b * g.H + iy0) * g.W + ix0) * xPix * 4 + kq * 16);
+      uint32_t m = 0;
+#pragma unroll
+      for (int ky = 0; ky < KH; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < KW; ++kx) {
+          const bool in = static_cast<unsigned>(iy0 + ky) < static_cast<unsigned>(g.H) &&
+                          static_cast<unsigned>(ix0 + kx) < static_cast<unsigned>(g.W);
+          m |= (ok && in ? 1u : 0u) << (ky * KW + kx);
+        }
+      tapMask[v] = m;
+    }
+    ldsOff = L::chunk(row, kq);
+  }
+  __device__ inline void load(int64_t k0) {
+    const int kk = static_cast<int>(k0);
+    const int tap = kk / C;  // uniform
+    const int c0 = kk - tap * C;
+    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
+    const uint32_t tapOff = static_cast<uint32_t>(ky) * rowPix4 + static_cast<uint32_t>(kx) * pix4;
+#pragma unroll
+    for (int v = 0; v < PER; ++v)
+      reg[v] = buf_ld4s(rsrc, sel_off((tapMask[v] >> tap) & 1u, rowOff[v] + tapOff), static_cast<uint32_t>(c0) * 4u);
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) *reinterpret_cast<lds_f4*>(stage + ldsOff + v * ROWSTEP * BK) = reg[v];
+  }
+};
+
 // Tap-major 3x3 gather (k = tap*C + c, a panel inside one tap): thread t
 // owns output column t % BN and the k-quads t / BN + j * QSTEP; a quad is 4
 // consecutive channels of one input pixel (4 loads HW floats apart), stored
@@ -495,7 +566,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
 // pieces in K order (piece 0 first, as conv_splitk_reduce does) into the
 // accumulator registers the conv kernel would have held, then applies the
 // conv kernel's own epilogue.
-template <class Cfg>
+template <class Cfg, bool NHWC = false>
 __global__ __launch_bounds__(Cfg::NT) void conv_tail_reduce(ConvArgs a) {
   const int t = blockIdx.x;
   int tm, tn;
@@ -521,7 +592,63 @@ __global__ __launch_bounds__(Cfg::NT) void conv_tail_reduce(ConvArgs a) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + ps[piece_off<Cfg>(wave, lane, i, j, r)];
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-  conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+  if constexpr (NHWC)
+    conv_store_nhwc<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+  else
+    conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+}
+
+// Channels-last convolution: rows of the GEMM are output pixels (A: the
+// input gathered per tap, or for a 1x1 stride-1 conv the input rows
+// themselves), columns are filters (B: the tap-major weights [F][K], k
+// contiguous), so both operands load 16 bytes along k and the epilogue
+// writes 32 consecutive channels of a pixel per half-wave.  Tail split as in
+// conv_lean_kernel (nFull may be 0: every tile cut into K pieces).
+template <class Cfg, int MODE>
+__global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a) {
+  using AL = typename std::conditional<MODE == kTap3, NhwcTapRows<Cfg::BM, Cfg::BK, Cfg::NT, 3, 3>,
+                                       LeanRowsK<Cfg::BM, Cfg::BK, Cfg::NT>>::type;
+  using BL = LeanRowsK<Cfg::BN, Cfg::BK, Cfg::NT>;
+  using Loop = LeanLoop<Cfg, AL, BL>;
+  __shared__ __attribute__((aligned(16))) float smem[Loop::LDS_FLOATS];
+  lds_t* lds = (lds_t*)smem;
+
+  int tile = blockIdx.x;
+  int64_t kBegin = 0;
+  int piece = -1;
+  if (a.tailSplits > 0 && tile >= a.nFull) {  // a K piece of a tail tile
+    const int u = tile - a.nFull;
+    tile = a.nFull + u / a.tailSplits;
+    kBegin = static_cast<int64_t>(u % a.tailSplits) * a.kChunk;
+    piece = u;
+  }
+  const int64_t kEnd = piece < 0 ? a.g.K : min(a.g.K, kBegin + a.kChunk);
+  int tm, tn;
+  tile_coords(tile, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+  AL al;
+  if constexpr (MODE == kTap3)
+    al.init(a.g, a.xPix, m0, threadIdx.x);
+  else
+    al.init(a.g.x, a.g.xBytes, a.xPix, a.g.N, m0, threadIdx.x);
+  BL bl;
+  bl.init(a.w, a.wBytes, a.g.K, a.F, n0, threadIdx.x);
+  f32x16 acc[Cfg::FM][Cfg::FN];
+  Loop::exec(al, bl, kBegin, (kEnd - kBegin) / Cfg::BK, lds, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (piece >= 0) {
+    float* dst = a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN);
+#pragma unroll
+    for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[piece_off<Cfg>(wave, lane, i, j, r)] = acc[i][j][r];
+    return;
+  }
+  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  conv_store_nhwc<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
 
 }  // namespace conv

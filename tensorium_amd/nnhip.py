@@ -78,6 +78,8 @@ _PROTOS = {
     "tnh_conv2d_fwd": [i64] * 11 + [vp, i64, i64, vp, i64, i32, vp, i64, i32, vp, i64, i64, vp, i64, i64],
     "tnh_conv2d_pack_weights": [i64, i64, i64, i64, vp, vp],
     "tnh_conv2d_set_autotune": [i32, i32],
+    "tnh_conv2d_fwd_nhwc": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, vp, i64,
+                            i32, vp, i64, i64, vp, i64, i64],
     "tnh_sgemm_set_autotune": [i32, i32],
     "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
     "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
@@ -322,6 +324,22 @@ class TNNHip:
         call("tnh_conv2d_fwd", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
              addr(input), inOffset, xs, addr(weights), 0, weightLayout, addr(biases), 0, activation, addr(residual),
              resOffset, rs, addr(output), outOffset, os_)
+        return oh, ow
+
+    def conv2dForwardNHWC(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
+                          biases, activation, output, outOffset, inPix=None, outPix=None, residual=None, resOffset=0,
+                          resPix=None, nchwInput=False):
+        """Channels-last fused conv (tap-major weights); pixel strides default
+        to the channel counts; nchwInput reads a C <= 4 image as NCHW.
+        Returns (outH, outW)."""
+        oh = (h + 2 * padding - kernelSize) // stride + 1
+        ow = (w + 2 * padding - kernelSize) // stride + 1
+        xp = 0 if nchwInput else (c if inPix is None else inPix)
+        op_ = filters if outPix is None else outPix
+        rp = filters if resPix is None else resPix
+        call("tnh_conv2d_fwd_nhwc", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
+             addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, addr(residual), resOffset, rp,
+             addr(output), outOffset, op_)
         return oh, ow
 
     def packConvWeights(self, filters, c, kernelSize, src, dst):

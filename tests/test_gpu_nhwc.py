@@ -1,0 +1,150 @@
+"""Channels-last (NHWC) convolution through the C ABI against the CPU oracle
+(NCHW) on identical seeded inputs: the oracle's tensors are transposed to
+channels-last on the host.  Per-tensor max|g - r| / max|r| <= 1e-5 (fp32
+summation order), exact for the few-channel first layer, and exact
+equality on integer-valued data; pixel strides that make a tensor a channel
+slice of a wider buffer leave the rest of the buffer untouched."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import refcpu as R
+from tensorium_amd import synth
+from tensorium_amd.nnhip import (CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, TNHError,
+                                  acLEAKY, acLINEAR, acLOGISTIC)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def D(a):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    torch.cuda.synchronize()
+    return t
+
+
+def H(t, hip):
+    hip.finish()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def nhwc(x):
+    return np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+
+
+def tap_major(Wt, F, C, k):
+    return np.ascontiguousarray(Wt.reshape(F, C, k, k).transpose(0, 2, 3, 1).reshape(F, k * k * C))
+
+
+CONVS = [  # batch, C, H, F, k, s, p, act, residual
+    (2, 32, 52, 64, 3, 2, 1, acLEAKY, False),
+    (2, 64, 26, 32, 1, 1, 0, acLEAKY, True),
+    (3, 128, 13, 255, 1, 1, 0, acLINEAR, False),
+    (2, 256, 13, 512, 3, 1, 1, acLEAKY, True),
+    (1, 64, 30, 130, 3, 1, 1, acLOGISTIC, False),
+    (2, 32, 17, 96, 3, 2, 1, acLEAKY, False),
+]
+
+
+@pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act,resid", CONVS)
+def test_conv_nhwc_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act, resid):
+    case(f"conv nhwc B{B} C{Cc} H{Hh} F{F} k{k} s{s} p{p} act{act} res{resid}")
+    x = synth.uniform(71, (B, Cc, Hh, Hh))
+    Wt = synth.normal(72, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(73, (F,), 0.1)
+    OH = (Hh + 2 * p - k) // s + 1
+    if act == acLOGISTIC:
+        # the oracle's logistic is the reference's approximation (within 2e-3);
+        # the device computes 1 / (1 + exp(-x)): compare against the exact one
+        lin = R.conv_forward(x, Wt, b, k, s, p, acLINEAR).astype(np.float64)
+        ref = (1.0 / (1.0 + np.exp(-lin))).astype(np.float32)
+    else:
+        ref = R.conv_forward(x, Wt, b, k, s, p, act)
+    res = None
+    if resid:
+        res = synth.normal(74, ref.shape)
+        ref = R.addvv(ref, res)
+    dout = torch.empty((B, OH, OH, F), dtype=torch.float32, device="cuda")
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, s, p, D(nhwc(x)), 0, D(tap_major(Wt, F, Cc, k)), D(b), act, dout, 0,
+                          residual=None if res is None else D(nhwc(res)))
+    got = H(dout, hip).transpose(0, 3, 1, 2)
+    assert R.rel_err(got, ref) <= TOL
+
+
+def test_conv_nhwc_first_layer_bit_exact(hip):
+    """C = 3 image read as NCHW, output channels-last: the few-channel kernel's
+    sequential FMA chain, bit-exact against the oracle."""
+    case("conv nhwc first layer C3 416")
+    B, Cc, Hh, F = 2, 3, 416, 32
+    x = synth.uniform(75, (B, Cc, Hh, Hh))
+    Wt = synth.normal(76, (F, Cc * 9), (2.0 / 27) ** 0.5)
+    b = synth.normal(77, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, 3, 1, 1, acLEAKY)
+    dout = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 3, 1, 1, D(x), 0, D(tap_major(Wt, F, Cc, 3)), D(b), acLEAKY, dout, 0,
+                          nchwInput=True)
+    assert np.array_equal(H(dout, hip).transpose(0, 3, 1, 2), ref)
+
+
+@pytest.mark.parametrize("k,s", [(3, 1), (3, 2), (1, 1)])
+def test_conv_nhwc_channel_slices(hip, k, s):
+    """Input, residual and output as channel slices of wider buffers (the
+    route/concat case): only the slice is written."""
+    case(f"conv nhwc slices k{k} s{s}")
+    B, Cc, Hh, F = 2, 64, 26, 96
+    p = k // 2
+    OH = (Hh + 2 * p - k) // s + 1
+    rng = np.random.default_rng(k * 10 + s)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    res = rng.integers(-5, 6, (B, F, OH, OH)).astype(np.float32)
+    ref = R.addvv(R.conv_forward(x, Wt, b, k, s, p, acLINEAR), res)
+    xin = np.zeros((B, Hh, Hh, Cc + 32), np.float32)
+    xin[..., 16:16 + Cc] = nhwc(x)
+    rin = np.zeros((B, OH, OH, F + 8), np.float32)
+    rin[..., 4:4 + F] = nhwc(res)
+    outbuf = np.full((B, OH, OH, F + 64), 7.0, np.float32)
+    dout = D(outbuf)
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, s, p, D(xin), 16, D(tap_major(Wt, F, Cc, k)), D(b), acLINEAR, dout, 32,
+                          inPix=Cc + 32, outPix=F + 64, residual=D(rin), resOffset=4, resPix=F + 8)
+    got = H(dout, hip)
+    assert np.array_equal(got[..., 32:32 + F].transpose(0, 3, 1, 2), ref)
+    assert np.all(got[..., :32] == 7.0) and np.all(got[..., 32 + F:] == 7.0)
+
+
+@pytest.mark.parametrize("cfg", range(11, NUM_CONV_CFGS))
+@pytest.mark.parametrize("hi", [0, 4, CONV_TAIL_BASE + 3, CONV_TAIL_SLOT_BASE + 2])
+def test_conv_nhwc_forced_configs(hip, cfg, hi):
+    """Every lean tile, plain, split-K (every tile cut), and tail splits per
+    CU and per workgroup slot, on integer data (exact sums)."""
+    B, Cc, Hh, F, k = 4, 64, 104, 96, 3
+    case(f"conv nhwc cfg{cfg} hi{hi}")
+    rng = np.random.default_rng(cfg * 100 + hi)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    ref = R.conv_forward(x, Wt, b, k, 1, 1, acLEAKY)
+    dout = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, cfg + CONV_SPLIT_UNIT * hi)
+    try:
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, 1, 1, D(nhwc(x)), 0, D(tap_major(Wt, F, Cc, k)), D(b), acLEAKY,
+                              dout, 0)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert np.array_equal(H(dout, hip).transpose(0, 3, 1, 2), ref)
+
+
+def test_conv_nhwc_rejects_unsupported(hip):
+    x = torch.zeros(1, 8, 8, 48, device="cuda")
+    w = torch.zeros(32, 9 * 48, device="cuda")
+    out = torch.zeros(1, 8, 8, 32, device="cuda")
+    with pytest.raises(TNHError):  # C % 32 != 0
+        hip.conv2dForwardNHWC(1, 48, 8, 8, 32, 3, 1, 1, x, 0, w, None, acLEAKY, out, 0)
+    with pytest.raises(TNHError):  # 1x1 with stride 2
+        hip.conv2dForwardNHWC(1, 32, 8, 8, 32, 1, 2, 0, x, 0, w, None, acLEAKY, out, 0, inPix=48)
