@@ -25,29 +25,42 @@ sys.path.insert(0, ROOT)
 
 METRIC = "conv im2col+SGEMM GFLOP/s (% fp32 MFMA peak); YOLOv3-416 img/s at batch 1/16"
 PEAK_FP32_MFMA = 157.3e12
+LAYOUT = ["auto"]  # activation layout of the networks bench.py builds (--layout)
+
+
+def layout_for(batch):
+    """--layout auto: channels-last between layers from batch 2 up (measured
+    faster at batch 4 and 16), NCHW at batch 1 (faster there)."""
+    if LAYOUT[0] != "auto":
+        return LAYOUT[0]
+    return "nhwc" if batch > 1 else "nchw"
 PEAK_HBM = 8.0e12
 # HBM bytes per launch of the dominant kernel family (tap-major 3x3 conv,
-# conv_lean_kernel, incl. its split-K reduction) from two rocprofv3 --pmc runs
+# channels-last conv_nhwc_kernel or NCHW conv_lean_kernel, incl. its
+# reductions) from two rocprofv3 --pmc runs
 # of `bench.py --counter-pass` (FETCH_SIZE then WRITE_SIZE, KiB per dispatch,
 # scaled by a 64 MiB copy: read = 2.0 x FETCH_SIZE, write = 1.0 x WRITE_SIZE);
-# profiles/yolov3_416_b16_conv_lean_kernel.md holds the figures and commands.
-TRAFFIC_TAP3X3_B16 = (2.0 * 103199.1 + 40665.2) * 1024
+# profiles/yolov3_416_b16_conv_{nhwc,lean}_kernel.md hold the figures and commands.
+TRAFFIC_TAP3X3_B16 = {"conv_lean_kernel<tap3x3>": (2.0 * 103199.1 + 40665.2) * 1024,
+                      "conv_nhwc_kernel<tap3x3>": (2.0 * 65605.6 + 40194.6) * 1024}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_kind(L, batch):
-    """Kernel family a conv layer launches: the lean implicit GEMM
-    (conv_lean_kernel, conv_lean.hpp) over tap-major 3x3 or 1x1 operands, or
-    the per-pixel kernel for few input channels (conv_smallc_kernel)."""
+def kernel_kind(L, batch, layout):
+    """Kernel family a conv layer launches: the lean implicit GEMM over
+    tap-major 3x3 or 1x1 operands (conv_nhwc_kernel for channels-last
+    activations, conv_lean_kernel for NCHW; conv_lean.hpp), or the per-pixel
+    kernel for few input channels (conv_smallc_kernel)."""
+    lean = "conv_nhwc_kernel" if layout == "nhwc" else "conv_lean_kernel"
     if L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0:
-        return "conv_lean_kernel<1x1>"
+        return f"{lean}<1x1>"
     if L["size"] == 3 and L["in"][0] <= 4:
         return "conv_smallc_kernel<3x3>"
     if L["size"] == 3 and L["in"][0] % 16 == 0:
-        return "conv_lean_kernel<tap3x3>"
+        return f"{lean}<tap3x3>"
     return f"conv_kernel<gather{L['size']}x{L['size']}>"
 
 
@@ -103,7 +116,7 @@ def profile_kernels(hip, net, layers, x, reps=3):
                 i = L["index"]
                 ms = hip.eventElapsed(*evs[i])
                 if L["type"] == "convolutional":
-                    kind = kernel_kind(L, net.batch)
+                    kind = kernel_kind(L, net.batch, net.layout)
                     F, oh, ow = L["out"]
                     flop = 2 * F * L["in"][0] * L["size"] ** 2 * oh * ow * net.batch
                 else:
@@ -309,7 +322,7 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
 
     from tensorium_amd import darknet, synth
 
-    net = darknet.Network(hip, layers608, batch, weights608)
+    net = darknet.Network(hip, layers608, batch, weights608, layout=layout_for(batch))
     x = torch.from_numpy(synth.uniform(9, (batch, 3, size, size))).cuda()
     torch.cuda.synchronize()
     ms, _ = time_forward(hip, net, x, steps, warmup, graph=True)
@@ -329,7 +342,7 @@ def extra_detect(hip, layers, weights, batch=16, thresh=0.5, nms=0.45):
 
     from tensorium_amd import darknet, synth
 
-    net = darknet.Network(hip, layers, batch, weights)
+    net = darknet.Network(hip, layers, batch, weights, layout=layout_for(batch))
     x = torch.from_numpy(synth.uniform(7, (batch, 3, 416, 416))).cuda()
     torch.cuda.synchronize()
     net.forward(x)
@@ -395,6 +408,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--layout", choices=("auto", "nhwc", "nchw"), default="auto",
+                    help="activation layout between layers (the image and the yolo heads stay NCHW); auto: "
+                         "channels-last from batch 2 up, NCHW at batch 1")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the other BASELINE configurations (single conv, SGEMM sweep, training step, "
                          "YOLOv3-608 batch 32)")
@@ -402,6 +418,7 @@ def main():
                     help="for rocprofv3 --pmc: tune, then run ONE eager forward and a 64 MiB copy "
                          "(the calibration kernel), print nothing else")
     args = ap.parse_args()
+    LAYOUT[0] = args.layout
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the YOLOv3 inference path shards by image "
               "with no communication, one process per GPU). Run with --gpus 1.", file=sys.stderr)
@@ -425,11 +442,11 @@ def main():
     flop_img = darknet.conv_flops(layers)
 
     if args.counter_pass:
-        counter_pass(hip, darknet.Network(hip, layers, args.batch, weights), args)
+        counter_pass(hip, darknet.Network(hip, layers, args.batch, weights, layout=layout_for(args.batch)), args)
         return
 
     def run(batch, steps, warmup):
-        net = darknet.Network(hip, layers, batch, weights)
+        net = darknet.Network(hip, layers, batch, weights, layout=layout_for(batch))
         x = torch.from_numpy(synth.uniform(7, (batch, 3, args.size, args.size))).cuda()
         torch.cuda.synchronize()
         ms, wall = time_forward(hip, net, x, steps, warmup, graph=not args.eager)
@@ -505,7 +522,8 @@ def main():
         "data": ("synthetic (seeded splitmix64 U[0,1) images, He-normal random weights, BN folded)" if not args.weights
                  else f"synthetic images, weights from {os.path.basename(args.weights)} (BN folded)"),
         "config": {"workload": f"YOLOv3-{args.size} fp32 inference, batch {args.batch}, 1 GPU",
-                   "global_batch": args.batch, "image": [3, args.size, args.size]},
+                   "global_batch": args.batch, "image": [3, args.size, args.size],
+                   "activation_layout": layout_for(args.batch)},
         "conv_gflops": round(gflops, 1),
         "conv_frac_fp32_mfma_peak": round(gflops * 1e9 / PEAK_FP32_MFMA, 4),
         "conv_kernel_ms_per_step": round(conv_ms, 4),
@@ -513,7 +531,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4),
-                     "traffic": (round(TRAFFIC_TAP3X3_B16) if dom == "conv_lean_kernel<tap3x3>" and args.batch == 16
+                     "traffic": (round(TRAFFIC_TAP3X3_B16[dom]) if dom in TRAFFIC_TAP3X3_B16 and args.batch == 16
                                  and args.size == 416 else None),
                      "traffic_unit": "bytes/launch",
                      "launches_per_step": round(d["launches"]),

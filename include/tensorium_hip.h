@@ -282,6 +282,14 @@ int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH,
 int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w,
                      float *in, int64_t stride, int32_t isForward, float scale,
                      float *out, int32_t zeroIn);
+/* The forward of tnh_upsample on channels-last tensors (bit-identical
+ * values): pixel (b, y, x) of in at in + inOff + ((b*h + y)*w + x)*inPix,
+ * of out at out + outOff + ((b*h*stride + y)*w*stride + x)*outPix, so the
+ * output can be a channel slice of a route (concat) buffer. */
+int32_t tnh_upsample_nhwc(int64_t batch, int64_t channels, int64_t h, int64_t w,
+                          int64_t stride, float scale, const float *in,
+                          int64_t inOff, int64_t inPix, float *out,
+                          int64_t outOff, int64_t outPix);
 
 /* ---- YOLO head ------------------------------------------------------- */
 /* TYoloLayer.forward inference part (nyololayer.pas:786-830): out = in, then
@@ -292,6 +300,20 @@ int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w,
  * 1/(1+e) by IEEE division (the reference's vrcpps is CPU-specific). */
 int32_t tnh_yolo_fwd(int64_t batch, int64_t n, int64_t classes, int64_t h,
                      int64_t w, const float *in, float *out);
+/* TYoloLayer.forward (nyololayer.pas:786-830) as tnh_yolo_fwd, reading a
+ * channels-last head (pixel (b, y, x) at in + inOff + ((b*h + y)*w + x)*inPix,
+ * inPix >= n*(classes+5)) and writing the NCHW head layout
+ * [batch][n*(classes+5)][h][w] that tnh_yolo_detections reads; bit-identical
+ * values. */
+int32_t tnh_yolo_fwd_nhwc(int64_t batch, int64_t n, int64_t classes, int64_t h,
+                          int64_t w, const float *in, int64_t inOff,
+                          int64_t inPix, float *out);
+/* No reference counterpart (the channels-last form of TConcatLayer's copy,
+ * nconcatlayer.pas:93-120): dst[dstOff + p*dstPix + c] =
+ * src[srcOff + p*srcPix + c] for pixels p and channels c < C. */
+int32_t tnh_copy_channels(int64_t pixels, int64_t C, const float *src,
+                          int64_t srcOff, int64_t srcPix, float *dst,
+                          int64_t dstOff, int64_t dstPix);
 /* TNNet.Detections (nnet.pas:584-680) on the device: for every yolo head
  * (heads[i]: a device tensor [batch][n][classes+5][h][w] after tnh_yolo_fwd,
  * hw[2i], hw[2i+1] = h, w; anchors[(i*n + a)*2 + {0,1}] = the mask's anchor

@@ -244,9 +244,7 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
 // the reference order k = (c*3 + ky)*3 + kx from 0, padding taps included as
 // zeros: exactly the arithmetic of the reference CPU path (im2col, then the
 // saxpy chain of ntensors.pas:1308-1436), then bias, activation, residual.
-// The input is always NCHW (the network's image); NHWC writes the output
-// channels-last (pixel stride a.outPix, residual a.resPix).
-template <int C, bool TAP, bool NHWC>
+template <int C, bool TAP>
 __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w) {
   constexpr int K = 9 * C;
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -272,16 +270,14 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
         in[(c * 3 + ky) * 3 + kx] =
             buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
       }
-  // element f of this pixel: NCHW f*OHW floats apart, NHWC adjacent
-  float* out = NHWC ? a.out + n * a.outPix : a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
-  const float* res = !a.res ? nullptr : NHWC ? a.res + n * a.resPix : a.res + static_cast<int64_t>(b) * a.rBatchStride + p;
-  const int64_t fStride = NHWC ? 1 : OHW;
+  float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
+  const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
   auto finish = [&](int f, float acc) {
     float v = acc;
     if (a.bias) v = v + a.bias[f];
     v = apply_act(v, a.act);
-    if (res) v = v + res[f * fStride];
-    out[f * fStride] = v;
+    if (res) v = v + res[static_cast<int64_t>(f) * OHW];
+    out[static_cast<int64_t>(f) * OHW] = v;
   };
   // weight of filter f at reference index k = c*9 + t
   auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
@@ -303,14 +299,115 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
   }
 }
 
+// Channels-last output of the few-channel kernel: the same per-pixel
+// sequential FMA chains (bit-exact), FC filters at a time, then each wave
+// passes its 64 pixels x FC results through LDS so that FC/4 consecutive
+// lanes store one pixel's FC channels (contiguous bytes) with 16-byte
+// stores.
+template <int C, bool TAP>
+__global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const float* __restrict__ w) {
+  constexpr int K = 9 * C, FC = 32;
+  __shared__ float tile[4][64 * (FC + 1)];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nWave = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;  // first pixel of this wave
+  const int64_t n = nWave + lane;
+  const bool valid = n < a.g.N;
+  const int F = static_cast<int>(a.F);
+  const int OHW = a.g.OHW, OW = a.g.OW, H = a.g.H, W = a.g.W;
+  const int64_t nn = valid ? n : 0;
+  const int b = static_cast<int>(nn / OHW);
+  const int p = static_cast<int>(nn - static_cast<int64_t>(b) * OHW);
+  const int oy = p / OW, ox = p - (p / OW) * OW;
+  const int iy0 = oy * a.g.sY - a.g.pH, ix0 = ox * a.g.sX - a.g.pW;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
+  const uint32_t base = static_cast<uint32_t>(static_cast<int64_t>(b) * a.g.xBatchStride * 4);
+  float in[K];
+#pragma unroll
+  for (int c = 0; c < C; ++c)
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+      for (int kx = 0; kx < 3; ++kx) {
+        const int iy = iy0 + ky, ix = ix0 + kx;
+        const bool ok = valid && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                        static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+        in[(c * 3 + ky) * 3 + kx] =
+            buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
+      }
+  auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
+  float* t = tile[wave];
+  const bool vec = a.outPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
+  for (int f0 = 0; f0 < F; f0 += FC) {
+    const int fc = F - f0 < FC ? F - f0 : FC;
+    auto put = [&](int q, float acc) {
+      float v = acc;
+      if (a.bias) v = v + a.bias[f0 + q];
+      t[lane * (FC + 1) + q] = apply_act(v, a.act);
+    };
+    int q0 = 0;
+    for (; q0 + 4 <= fc; q0 += 4) {  // four independent chains at a time
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = fmaf(wt(f0 + q0 + u, k), in[k], acc[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) put(q0 + u, acc[u]);
+    }
+    for (; q0 < fc; ++q0) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < K; ++k) acc = fmaf(wt(f0 + q0, k), in[k], acc);
+      put(q0, acc);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // element e = pixel * fc + channel of this wave's 64 x fc block
+    for (int e0 = 0; e0 < 64 * fc; e0 += 256) {
+      const int e = e0 + lane * 4;
+      if (e >= 64 * fc) break;
+      const int px = e / fc, q = e - px * fc;
+      const int64_t np = nWave + px;
+      if (np >= a.g.N) continue;
+      float* dst = a.out + np * a.outPix + f0 + q;
+      const float* res = a.res ? a.res + np * a.resPix + f0 + q : nullptr;
+      float v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = t[px * (FC + 1) + q + u];
+      if (res) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (q + u < fc) v[u] = v[u] + res[u];
+      }
+      if (vec && q + 4 <= fc) {
+        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (q + u < fc) dst[u] = v[u];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 template <bool TAP, bool NHWC>
 int launch_smallc(const ConvArgs& a, hipStream_t s) {
+  if constexpr (NHWC) {
+    const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
+    switch (a.g.C) {
+      case 1: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+      case 2: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+      case 3: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+      default: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    }
+    return launch_status("conv_smallc_nhwc_kernel");
+  }
   const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
   switch (a.g.C) {
-    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP, NHWC>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
   }
   return launch_status("conv_smallc_kernel");
 }

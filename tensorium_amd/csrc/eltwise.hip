@@ -166,6 +166,41 @@ __global__ void yolo_kernel(int64_t total, int64_t HW, int64_t entries, const fl
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// TYoloLayer.forward on a channels-last head (pixel stride inPix) into the
+// NCHW head layout [b][ch][y][x] the detection decoder reads: 32 pixels x 32
+// channels per tile through LDS, so the reads run along channels and the
+// writes along pixels; per element the same operation as yolo_kernel.
+__global__ __launch_bounds__(256) void yolo_nhwc_kernel(int64_t HW, int64_t CH, int64_t entries, const float* in,
+                                                        int64_t inPix, float* out) {
+  __shared__ float tile[32][33];
+  const int64_t b = blockIdx.z;
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 32, c0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 8 rows of 32
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t p = p0 + r, c = c0 + tx;
+    tile[r][tx] = p < HW && c < CH ? in[(b * HW + p) * inPix + c] : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 32; r += 8) {
+    const int64_t c = c0 + r, p = p0 + tx;
+    if (c < CH && p < HW) {
+      const float v = tile[tx][r];
+      const int64_t entry = c % entries;
+      out[(b * CH + c) * HW + p] = (entry == 2 || entry == 3) ? v : logistic_poly(v);
+    }
+  }
+}
+
+// dst[p*dstPix + c] = src[p*srcPix + c] for c < C: a channel slice copied
+// between channels-last tensors (a route input that cannot live in place).
+__global__ void copy_channels_kernel(int64_t total, int64_t C, const float* src, int64_t srcPix, float* dst,
+                                     int64_t dstPix) {
+  GRID_STRIDE(e, total) {
+    const int64_t p = e / C, c = e - p * C;
+    dst[p * dstPix + c] = src[p * srcPix + c];
+  }
+}
+
 }  // namespace
 }  // namespace tnh
 
@@ -327,6 +362,34 @@ extern "C" int32_t tnh_yolo_fwd(int64_t batch, int64_t n, int64_t classes, int64
   hipLaunchKernelGGL(yolo_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, h * w, classes + 5, in,
                      out);
   return launch_status("yolo_kernel");
+}
+
+extern "C" int32_t tnh_yolo_fwd_nhwc(int64_t batch, int64_t n, int64_t classes, int64_t h, int64_t w,
+                                     const float* in, int64_t inOff, int64_t inPix, float* out) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && n > 0 && classes >= 0 && h > 0 && w > 0, "yolo_fwd_nhwc: bad sizes");
+  TNH_ARG(in && out && inOff >= 0, "yolo_fwd_nhwc: NULL buffer or negative offset");
+  const int64_t CH = n * (classes + 5), HW = h * w;
+  TNH_ARG(inPix >= CH, "yolo_fwd_nhwc: inPix %lld < %lld channels", (long long)inPix, (long long)CH);
+  TNH_ARG(batch < 65536 && (HW + 31) / 32 < INT32_MAX && (CH + 31) / 32 < 65536, "yolo_fwd_nhwc: grid too large");
+  if (batch == 0) return TNH_OK;
+  const dim3 grid(static_cast<unsigned>((HW + 31) / 32), static_cast<unsigned>((CH + 31) / 32),
+                  static_cast<unsigned>(batch));
+  hipLaunchKernelGGL(yolo_nhwc_kernel, grid, dim3(256), 0, cx->stream, HW, CH, classes + 5, in + inOff, inPix, out);
+  return launch_status("yolo_nhwc_kernel");
+}
+
+extern "C" int32_t tnh_copy_channels(int64_t pixels, int64_t C, const float* src, int64_t srcOff, int64_t srcPix,
+                                     float* dst, int64_t dstOff, int64_t dstPix) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(pixels >= 0 && C >= 0 && srcPix >= C && dstPix >= C && srcOff >= 0 && dstOff >= 0,
+          "copy_channels: bad sizes");
+  const int64_t total = pixels * C;
+  if (total == 0) return TNH_OK;
+  TNH_ARG(src && dst, "copy_channels: NULL buffer");
+  hipLaunchKernelGGL(copy_channels_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, C,
+                     src + srcOff, srcPix, dst + dstOff, dstPix);
+  return launch_status("copy_channels_kernel");
 }
 
 extern "C" int32_t tnh_bn_normalize(int64_t dstSize, float* x, int64_t offset, int64_t N, const float* mean,

@@ -125,6 +125,33 @@ __global__ __launch_bounds__(kThreads) void upsample2_fwd_kernel(int64_t total, 
   }
 }
 
+// Channels-last nearest upsample, forward: out pixel (b, y, x) channel c =
+// scale * in pixel (b, y / s, x / s) channel c; four channels per thread
+// (16-byte loads and stores) when C, both pixel strides and both bases allow.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void upsample_nhwc_kernel(int64_t total, int64_t C, int64_t h, int64_t w,
+                                                                 int64_t s, float scale, const float* __restrict__ in,
+                                                                 int64_t inPix, float* __restrict__ out,
+                                                                 int64_t outPix) {
+  constexpr int V = VEC ? 4 : 1;
+  const int64_t CV = C / V, OW = w * s, OH = h * s;
+  GRID_STRIDE(e, total) {  // e = (output pixel, channel group)
+    const int64_t cg = e % CV;
+    const int64_t pix = e / CV;
+    const int64_t x = pix % OW;
+    const int64_t t = pix / OW;
+    const int64_t y = t % OH, b = t / OH;
+    const float* src = in + ((b * h + y / s) * w + x / s) * inPix + cg * V;
+    float* dst = out + pix * outPix + cg * V;
+    if constexpr (VEC) {
+      const float4 v = *reinterpret_cast<const float4*>(src);
+      *reinterpret_cast<float4*>(dst) = make_float4(scale * v.x, scale * v.y, scale * v.z, scale * v.w);
+    } else {
+      *dst = scale * *src;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void upsample_bwd_kernel(int64_t total, int64_t h, int64_t w, int64_t s,
                                                                 float scale, float* __restrict__ in,
                                                                 const float* __restrict__ out, int zeroIn) {
@@ -211,4 +238,27 @@ extern "C" int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int6
   hipLaunchKernelGGL(upsample_bwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, h, w, stride,
                      scale, in, out, zeroIn);
   return launch_status("upsample_bwd_kernel");
+}
+
+extern "C" int32_t tnh_upsample_nhwc(int64_t batch, int64_t channels, int64_t h, int64_t w, int64_t stride,
+                                     float scale, const float* in, int64_t inOff, int64_t inPix, float* out,
+                                     int64_t outOff, int64_t outPix) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && channels > 0 && h > 0 && w > 0 && stride > 0, "upsample_nhwc: bad geometry");
+  TNH_ARG(in && out && inOff >= 0 && outOff >= 0, "upsample_nhwc: NULL buffer or negative offset");
+  TNH_ARG(inPix >= channels && outPix >= channels, "upsample_nhwc: pixel stride below the channel count");
+  const float* src = in + inOff;
+  float* dst = out + outOff;
+  const int64_t pixels = batch * h * w * stride * stride;
+  if (pixels == 0) return TNH_OK;
+  const bool vec = channels % 4 == 0 && inPix % 4 == 0 && outPix % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+  const int64_t total = pixels * (vec ? channels / 4 : channels);
+  if (vec)
+    hipLaunchKernelGGL(upsample_nhwc_kernel<true>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
+                       channels, h, w, stride, scale, src, inPix, dst, outPix);
+  else
+    hipLaunchKernelGGL(upsample_nhwc_kernel<false>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
+                       channels, h, w, stride, scale, src, inPix, dst, outPix);
+  return launch_status("upsample_nhwc_kernel");
 }

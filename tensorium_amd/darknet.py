@@ -16,6 +16,12 @@ Route concat of several inputs is per image (darknet semantics).  The
 reference's TConcatLayer copies whole batched tensors back to back
 (nconcatlayer.pas:115 -> ntensors.pas:12045), which mixes images at batch > 1;
 ``route_mode="reference"`` reproduces that layout for parity studies.
+
+``layout="nhwc"`` keeps every activation channels-last between layers (the
+input image stays NCHW and the yolo heads are written NCHW, so the
+network's interface does not change): both GEMM operands of a convolution
+then load 16 bytes along K, and a route's inputs are written straight into
+their channel slice of the route buffer (no concat copy).
 """
 from __future__ import annotations
 
@@ -163,11 +169,17 @@ def consumers(layers):
 class Network:
     """Inference runner over the C ABI; buffers are device torch tensors."""
 
-    def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True):
+    def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True,
+                 layout="nchw"):
         import torch
 
+        if layout not in ("nchw", "nhwc"):
+            raise ValueError(f"layout {layout!r}")
         self.hip, self.layers, self.batch = hip, layers, batch
         self.route_mode = route_mode
+        self.layout = layout
+        if layout == "nhwc":
+            pack = True  # the channels-last kernels read tap-major weights
         self.torch = torch
         use = consumers(layers)
         self.fused = set()  # conv indices whose shortcut is fused
@@ -183,15 +195,19 @@ class Network:
         for i, (w, b) in weights.items():
             L = layers[i]
             dw = torch.from_numpy(np.ascontiguousarray(w)).to(device)
-            layout = WEIGHTS_REFERENCE
+            wl = WEIGHTS_REFERENCE
             if pack and L["size"] > 1:
                 packed = torch.empty_like(dw)
                 torch.cuda.synchronize()
                 hip.packConvWeights(L["filters"], L["in"][0], L["size"], dw, packed)
                 hip.finish()
-                dw, layout = packed, WEIGHTS_TAP_MAJOR
-            self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), layout)
+                dw, wl = packed, WEIGHTS_TAP_MAJOR
+            self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), wl)
         self.out = [None] * len(layers)
+        self.input_shape = (batch,) + layers[0]["in"]
+        if layout == "nhwc":
+            self._plan_nhwc(device)
+            return
         for L in layers:
             i = L["index"]
             if L["type"] == "route" and len(L["srcs"]) == 1:
@@ -200,7 +216,76 @@ class Network:
                 continue  # writes into the shortcut's buffer
             C, h, w = L["out"]
             self.out[i] = torch.empty((batch, C, h, w), dtype=torch.float32, device=device)
-        self.input_shape = (batch,) + layers[0]["in"]
+
+    # -- channels-last storage plan --------------------------------------------
+    def _owner(self, i):
+        """The layer whose storage holds layer i's output."""
+        L = self.layers[i]
+        if L["type"] == "route" and len(L["srcs"]) == 1:
+            return self._owner(L["srcs"][0])
+        if i in self.fused:
+            return i + 1
+        return i
+
+    def _plan_nhwc(self, device):
+        """store[i] = (tensor, channel offset, pixel stride) for every storage
+        owner.  A multi-input route gets a [B, h, w, sum C] buffer and each
+        input owner that is a convolution, shortcut or upsample not placed
+        elsewhere writes straight into its channel slice; other inputs are
+        copied (tnh_copy_channels).  Yolo outputs are NCHW head tensors."""
+        torch, layers, B = self.torch, self.layers, self.batch
+        L0 = layers[0]
+        if L0["type"] != "convolutional" or L0["size"] != 3 or L0["in"][0] > 4:
+            raise NotImplementedError("channels-last networks start with a 3x3 convolution on <= 4 channels")
+        self.store = {}
+        self.copy_srcs = {}
+        for L in layers:
+            if L["type"] == "route" and len(L["srcs"]) > 1:
+                C, h, w = L["out"]
+                buf = torch.empty((B, h, w, C), dtype=torch.float32, device=device)
+                self.store[L["index"]] = (buf, 0, C)
+                off, copies = 0, []
+                for s_ in L["srcs"]:
+                    o = self._owner(s_)
+                    cs = layers[s_]["out"][0]
+                    if o not in self.store and layers[o]["type"] in ("convolutional", "shortcut", "upsample"):
+                        self.store[o] = (buf, off, C)
+                    else:
+                        copies.append((s_, off))
+                    off += cs
+                self.copy_srcs[L["index"]] = copies
+        for L in layers:
+            i, t = L["index"], L["type"]
+            if t == "maxpool":
+                raise NotImplementedError("maxpool has no channels-last kernel")
+            if t == "yolo":
+                C, h, w = L["out"]
+                self.out[i] = torch.empty((B, C, h, w), dtype=torch.float32, device=device)
+                continue
+            if (t == "route" and len(L["srcs"]) == 1) or i in self.fused or i in self.store:
+                continue
+            C, h, w = L["out"]
+            self.store[i] = (torch.empty((B, h, w, C), dtype=torch.float32, device=device), 0, C)
+        for L in layers:  # nothing may read a yolo head as an activation
+            srcs = L.get("srcs", []) + ([L["src"]] if "src" in L else [])
+            if L["index"] > 0 and L["type"] != "route":
+                srcs = srcs + [L["index"] - 1]
+            for s_ in srcs:
+                if layers[self._owner(s_)]["type"] == "yolo" and L["type"] != "route":
+                    raise NotImplementedError(f"layer {L['index']} reads yolo layer {s_}")
+
+    def nhwc_store(self, i):
+        """(tensor, channel offset, pixel stride) of layer i's output."""
+        return self.store[self._owner(i)]
+
+    def output(self, i):
+        """Layer i's output as a [B, C, h, w] tensor (a view in NCHW mode, a
+        permuted view of the channel slice in NHWC mode)."""
+        if self.layout == "nchw" or self.layers[i]["type"] == "yolo":
+            return self.buffer(i)
+        t, off, pix = self.nhwc_store(i)
+        C = self.layers[i]["out"][0]
+        return t.view(self.batch, t.shape[1], t.shape[2], pix)[..., off:off + C].permute(0, 3, 1, 2)
 
     def buffer(self, i):
         L = self.layers[i]
@@ -228,7 +313,54 @@ class Network:
                 on_layer(i, False)
         return heads
 
+    def _layer_nhwc(self, L, x, heads):
+        hip, B = self.hip, self.batch
+        i, t = L["index"], L["type"]
+        if t == "convolutional":
+            w, b, _ = self.w[i]
+            C, h, ww = L["in"]
+            if i == 0:
+                src, soff, spix, nchw = x, 0, 0, True
+            else:
+                (src, soff, spix), nchw = self.nhwc_store(i - 1), False
+            res, roff, rpix = None, 0, None
+            if i in self.fused:
+                res, roff, rpix = self.nhwc_store(self.layers[i + 1]["src"])
+            dst, doff, dpix = self.nhwc_store(i)
+            hip.conv2dForwardNHWC(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], src, soff, w, b,
+                                  L["act"], dst, doff, inPix=spix, outPix=dpix, residual=res, resOffset=roff,
+                                  resPix=rpix, nchwInput=nchw)
+        elif t == "shortcut":
+            if i - 1 not in self.fused:
+                a_, b_, o_ = self.nhwc_store(i - 1), self.nhwc_store(L["src"]), self.nhwc_store(i)
+                C = L["out"][0]
+                if any(st[1] != 0 or st[2] != C for st in (a_, b_, o_)):
+                    raise NotImplementedError("unfused shortcut on a channel slice")
+                n = B * int(np.prod(L["out"]))
+                hip.addvv(n, a_[0], 0, 1, b_[0], 0, 1, o_[0], 0, 1)
+                hip.ActivateArray(n, o_[0], 0, L["act"])
+        elif t == "route":
+            if len(L["srcs"]) > 1:
+                dst, doff, dpix = self.nhwc_store(i)
+                _, h, ww = L["out"]
+                for s_, off in self.copy_srcs[i]:
+                    src, soff, spix = self.nhwc_store(s_)
+                    hip.copyChannels(B * h * ww, self.layers[s_]["out"][0], src, soff, spix, dst, doff + off, dpix)
+        elif t == "upsample":
+            C, h, ww = L["in"]
+            src, soff, spix = self.nhwc_store(i - 1)
+            dst, doff, dpix = self.nhwc_store(i)
+            hip.upSampleNHWC(B, C, h, ww, L["stride"], L["scale"], src, soff, spix, dst, doff, dpix)
+        elif t == "yolo":
+            C, h, ww = L["in"]
+            src, soff, spix = self.nhwc_store(i - 1)
+            hip.yoloForwardNHWC(B, L["n"], L["classes"], h, ww, src, soff, spix, self.out[i])
+            heads.append(self.out[i])
+        return x
+
     def _layer(self, L, prev, heads):
+        if self.layout == "nhwc":
+            return self._layer_nhwc(L, prev, heads)
         hip, B = self.hip, self.batch
         i, t = L["index"], L["type"]
         if t == "convolutional":

@@ -81,6 +81,9 @@ _PROTOS = {
     "tnh_conv2d_fwd_nhwc": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, vp, i64,
                             i32, vp, i64, i64, vp, i64, i64],
     "tnh_sgemm_set_autotune": [i32, i32],
+    "tnh_yolo_fwd_nhwc": [i64, i64, i64, i64, i64, vp, i64, i64, vp],
+    "tnh_copy_channels": [i64, i64, vp, i64, i64, vp, i64, i64],
+    "tnh_upsample_nhwc": [i64, i64, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64],
     "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
     "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
     "tnh_forward_scale": [i64, vp, i64, i64, vp, i64, i64],
@@ -341,6 +344,17 @@ class TNNHip:
              addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, addr(residual), resOffset, rp,
              addr(output), outOffset, op_)
         return oh, ow
+
+    def yoloForwardNHWC(self, batch, n, classes, h, w, input, inOffset, inPix, output):
+        """YOLO head on a channels-last input, NCHW head output."""
+        call("tnh_yolo_fwd_nhwc", batch, n, classes, h, w, addr(input), inOffset, inPix, addr(output))
+
+    def copyChannels(self, pixels, channels, src, srcOffset, srcPix, dst, dstOffset, dstPix):
+        call("tnh_copy_channels", pixels, channels, addr(src), srcOffset, srcPix, addr(dst), dstOffset, dstPix)
+
+    def upSampleNHWC(self, batch, channels, h, w, stride, scale, input, inOffset, inPix, output, outOffset, outPix):
+        call("tnh_upsample_nhwc", batch, channels, h, w, stride, scale, addr(input), inOffset, inPix, addr(output),
+             outOffset, outPix)
 
     def packConvWeights(self, filters, c, kernelSize, src, dst):
         """[F][C][k][k] -> tap-major [F][k][k][C] (device to device)."""

@@ -137,3 +137,63 @@ def test_yolov3_graph_replay(hip, yolo):
     finally:
         n.release_graph()
         hip.useTorchStream()
+
+
+def test_yolov3_nhwc_heads(hip, yolo):
+    """The channels-last network end to end: the three pre-logistic head
+    convolutions within 1e-5 of the oracle, every other unfused convolution
+    within 5e-5, and the yolo kernel bit-exact on the device's own head-conv
+    output (written NCHW)."""
+    layers, W = yolo
+    print("[case] yolov3-416 batch 1 channels-last end-to-end vs oracle", flush=True)
+    x = synth.uniform(7, (1, 3, 416, 416))
+    ref = netref.forward(layers, W, x)
+    n = darknet.Network(hip, layers, 1, W, layout="nhwc")
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    heads = [h.cpu().numpy() for h in n.forward(dx)]
+    hip.finish()
+    errs = {}
+    for L in layers:
+        i = L["index"]
+        if L["type"] == "convolutional" and i not in n.fused:
+            errs[i] = R.rel_err(n.output(i).cpu().numpy(), ref[i])
+    worst = max(errs, key=errs.get)
+    print(f"worst intermediate conv error {errs[worst]:.3e} at layer {worst}", flush=True)
+    for i in (81, 93, 105):
+        assert errs[i] <= TOL, (i, errs[i])
+    assert max(errs.values()) <= 5 * TOL
+    for h, i in zip(heads, (82, 94, 106)):
+        own = R.yolo_fwd(np.ascontiguousarray(n.output(i - 1).cpu().numpy()), 3, 80, exact=True)
+        assert np.array_equal(h, own)
+
+
+def test_yolov3_nhwc_matches_nchw_and_replays(hip, yolo):
+    """Batch 2: the channels-last network's head convolutions equal the NCHW
+    network's within the per-tensor bound, the route inputs written in place
+    equal a concat, and graph replays of the channels-last forward equal its
+    eager result bit for bit."""
+    layers, W = yolo
+    print("[case] yolov3 batch 2 nhwc vs nchw, graph replay", flush=True)
+    x = synth.uniform(11, (2, 3, 416, 416))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    a = darknet.Network(hip, layers, 2, W)
+    a.forward(dx)
+    hip.finish()
+    b = darknet.Network(hip, layers, 2, W, layout="nhwc")
+    eager = [h.cpu().numpy() for h in b.forward(dx)]
+    hip.finish()
+    for i in (81, 93, 105, 86, 98):  # head convs and the two multi-input routes
+        assert R.rel_err(b.output(i).cpu().numpy(), a.output(i).cpu().numpy()) <= 2 * TOL, i
+    try:
+        b.capture(dx)
+        for rep in range(3):
+            heads = b.replay()
+            hip.finish()
+            for u, v in zip([h.cpu().numpy() for h in heads], eager):
+                assert np.array_equal(u, v), rep
+            torch.cuda.synchronize()
+    finally:
+        b.release_graph()
+        hip.useTorchStream()
