@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <functional>
+#include <vector>
 
 #include "../../include/tensorium_hip.h"
 
@@ -24,11 +25,15 @@ struct Context {
   int xcd_count = 8;
   void* ws = nullptr;     // library scratch (split-K partial sums), grown on demand
   size_t wsBytes = 0;
+  // Outgrown scratch buffers: a graph captured earlier may still launch
+  // kernels that address them, so they are freed only by tnh_finalize.
+  std::vector<void*> wsRetired;
 };
 
 // Returns a scratch buffer of at least `bytes` on the context device, growing
-// it (hipMalloc) when needed; returns nullptr when growing is not possible
-// (allocation failure, or the stream is being captured into a graph).
+// it (a new hipMalloc; the outgrown buffer stays allocated until
+// tnh_finalize) when needed; returns nullptr when growing is not possible
+// (allocation failure, or a stream of the context is being captured).
 void* workspace(Context* c, size_t bytes);
 
 // Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).

@@ -80,8 +80,7 @@ void* workspace(Context* c, size_t bytes) {
       (hipStreamIsCapturing(c->tune_stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone))
     return nullptr;
   if (c->ws) {
-    (void)hipStreamSynchronize(c->stream);
-    (void)hipFree(c->ws);
+    c->wsRetired.push_back(c->ws);
     c->ws = nullptr;
     c->wsBytes = 0;
   }
@@ -123,6 +122,7 @@ extern "C" int32_t tnh_init(int32_t device) {
     (void)hipSetDevice(g_ctx.device);
     (void)hipStreamSynchronize(g_ctx.stream);
     if (g_ctx.ws) (void)hipFree(g_ctx.ws);
+    for (void* p : g_ctx.wsRetired) (void)hipFree(p);
     (void)hipStreamDestroy(g_ctx.own_stream);
     (void)hipStreamDestroy(g_ctx.tune_stream);
     g_ctx = Context{};
@@ -152,6 +152,7 @@ extern "C" int32_t tnh_finalize(void) {
   (void)hipSetDevice(g_ctx.device);
   (void)hipStreamSynchronize(g_ctx.stream);
   if (g_ctx.ws) (void)hipFree(g_ctx.ws);
+  for (void* p : g_ctx.wsRetired) (void)hipFree(p);
   (void)hipStreamDestroy(g_ctx.own_stream);
   (void)hipStreamDestroy(g_ctx.tune_stream);
   g_ctx = Context{};

@@ -143,22 +143,14 @@ __device__ inline float box_iou(float ax, float ay, float aw, float ah, float bx
 // One workgroup per (class, image): gather the detections with a non-zero
 // probability for the class, bitonic-sort them by (probability descending,
 // detection index ascending) in LDS, then greedy suppression in that order.
-__global__ __launch_bounds__(kNmsThreads) void yolo_nms_sort_kernel(int64_t capacity, int classes,
-                                                                  const float* __restrict__ boxes, float* prob,
-                                                                  const int32_t* counts, float thresh) {
-  __shared__ float score[kNmsMax];
-  __shared__ int idx[kNmsMax];
-  __shared__ unsigned char alive[kNmsMax];
-  __shared__ int waveSum[kNmsThreads / 64];
-  __shared__ int q;
-  constexpr int PER = kNmsMax / kNmsThreads;
-  const int k = blockIdx.x, b = blockIdx.y;
+// Compacts the candidates of class k of image b (non-zero probability, in
+// detection order) into score/idx and sorts them: higher score first, then
+// lower detection index.  Returns the candidate count (every thread).
+__device__ inline int nms_collect_sort(int64_t capacity, int classes, const float* pr, int64_t m, float* score,
+                                       int* idx, int* waveSum, int& q) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t m = min(static_cast<int64_t>(counts[b]), capacity);
-  float* pr = prob + static_cast<int64_t>(b) * capacity * classes + k;
   if (threadIdx.x == 0) q = 0;
   __syncthreads();
-  // compact the candidates of class k in detection order
   for (int64_t d0 = 0; d0 < m; d0 += kNmsThreads) {
     const int64_t d = d0 + threadIdx.x;
     const float p = d < m ? pr[d * classes] : 0.f;
@@ -182,7 +174,7 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_sort_kernel(int64_t capa
     __syncthreads();
   }
   const int n = q;
-  if (n <= 1) return;
+  if (n <= 1) return n;
   int P = 2;
   while (P < n) P <<= 1;
   for (int i = n + threadIdx.x; i < P; i += kNmsThreads) {
@@ -210,6 +202,24 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_sort_kernel(int64_t capa
       }
       __syncthreads();
     }
+  return n;
+}
+
+__global__ __launch_bounds__(kNmsThreads) void yolo_nms_sort_kernel(int64_t capacity, int classes,
+                                                                  const float* __restrict__ boxes, float* prob,
+                                                                  const int32_t* counts, float thresh) {
+  __shared__ float score[kNmsMax];
+  __shared__ int idx[kNmsMax];
+  __shared__ unsigned char alive[kNmsMax];
+  __shared__ int waveSum[kNmsThreads / 64];
+  __shared__ int q;
+  constexpr int PER = kNmsMax / kNmsThreads;
+  const int k = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = min(static_cast<int64_t>(counts[b]), capacity);
+  float* pr = prob + static_cast<int64_t>(b) * capacity * classes + k;
+  const int n = nms_collect_sort(capacity, classes, pr, m, score, idx, waveSum, q);
+  if (n <= 1) return;
   // Greedy suppression in chunks of 64 sorted candidates (thread t owns
   // sorted positions t + r * kNmsThreads and keeps their boxes in
   // registers).  Per chunk: wave 0 resolves the chunk by itself -- lane l
@@ -291,6 +301,134 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_sort_kernel(int64_t capa
     if (!alive[j]) pr[static_cast<int64_t>(idx[j]) * classes] = 0.f;
 }
 
+// Overlap bits of one image's detections (D = min(count, capacity)): bit t
+// of word w of row i is box_iou(box i, box j) > thresh for j = 64w + t < D,
+// j != i.  box_iou is symmetric bit for bit (max, min, products and the sum
+// of the two areas commute), so row i also answers "does i suppress j".
+// One thread per (row, word); the word's 64 column boxes are staged in LDS.
+__global__ __launch_bounds__(256) void nms_overlap_bits_kernel(int64_t capacity, int64_t words,
+                                                               const float* __restrict__ boxes,
+                                                               const int32_t* counts, float thresh, uint64_t* bits) {
+  __shared__ float cb[64][4];
+  const int64_t b = blockIdx.z, w = blockIdx.y;
+  const int64_t D = min(static_cast<int64_t>(counts[b]), capacity);
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 256;
+  if (i0 >= D || 64 * w >= D) return;  // uniform
+  const float* bb = boxes + b * capacity * 4;
+  const int64_t jn = min(static_cast<int64_t>(64), D - 64 * w);
+  if (threadIdx.x < jn) {
+    const float* p = bb + (64 * w + threadIdx.x) * 4;
+    cb[threadIdx.x][0] = p[0];
+    cb[threadIdx.x][1] = p[1];
+    cb[threadIdx.x][2] = p[2];
+    cb[threadIdx.x][3] = p[3];
+  }
+  __syncthreads();
+  const int64_t i = i0 + threadIdx.x;
+  if (i >= D) return;
+  const float ax = bb[i * 4], ay = bb[i * 4 + 1], aw = bb[i * 4 + 2], ah = bb[i * 4 + 3];
+  uint64_t m = 0;
+  for (int t = 0; t < jn; ++t)
+    if (64 * w + t != i && box_iou(ax, ay, aw, ah, cb[t][0], cb[t][1], cb[t][2], cb[t][3]) > thresh)
+      m |= uint64_t(1) << t;
+  bits[(b * capacity + i) * words + w] = m;
+}
+
+// doNMSSort of class k of image b over the overlap bits: the sorted
+// candidates go in chunks of 64.  Wave 0 resolves a chunk (a member is alive
+// unless an earlier kept candidate removed it; lane l reads the bits of the
+// later chunk members it suppresses; a 64-step scan keeps l if no kept
+// earlier member suppresses it), then the kept members' bit rows are OR-ed
+// into `removed` (a bitset over detection indices).  A kept candidate's bit
+// is never set (an earlier kept box overlapping it would have removed it),
+// so at the end a candidate survives iff its bit is clear: the greedy
+// result, without recomputing an overlap per class.
+__global__ __launch_bounds__(kNmsThreads) void yolo_nms_bits_kernel(int64_t capacity, int64_t words, int classes,
+                                                                  float* prob, const int32_t* counts,
+                                                                  const uint64_t* __restrict__ bits) {
+  __shared__ float score[kNmsMax];
+  __shared__ int idx[kNmsMax + 64];
+  __shared__ uint64_t removed[kNmsMax / 64];
+  __shared__ int waveSum[kNmsThreads / 64];
+  __shared__ int q;
+  __shared__ uint64_t keptBits;
+  const int k = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m = min(static_cast<int64_t>(counts[b]), capacity);
+  float* pr = prob + static_cast<int64_t>(b) * capacity * classes + k;
+  const int n = nms_collect_sort(capacity, classes, pr, m, score, idx, waveSum, q);
+  if (n <= 1) return;
+  const int W = static_cast<int>((m + 63) / 64);
+  for (int w = threadIdx.x; w < W; w += kNmsThreads) removed[w] = 0;
+  // positions past the last candidate name candidate 0, so every lookup
+  // below reads a valid row and word and needs no condition
+  for (int j = n + threadIdx.x; j < n + 64; j += kNmsThreads) idx[j] = idx[0];
+  __syncthreads();
+  const uint64_t* rows = bits + static_cast<int64_t>(b) * capacity * words;
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    if (wave == 0) {
+      const int l = lane;
+      const bool in = c0 + l < n;
+      const int di = idx[c0 + l];
+      const bool alive = in && !((removed[di >> 6] >> (di & 63)) & 1);
+      // the later chunk members l suppresses: 64 independent loads with no
+      // condition around them (a load inside a lane-dependent branch waits
+      // for every outstanding load at the branch's join), masked afterwards
+      uint64_t mask = 0;
+      const uint64_t* row = rows + static_cast<int64_t>(idx[c0 + l]) * words;
+#pragma unroll
+      for (int g = 0; g < 64; g += 16) {  // 16 loads in flight, then their bits
+        int dt[16];
+        uint64_t wv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) dt[u] = idx[c0 + g + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) wv[u] = row[dt[u] >> 6];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) mask |= ((wv[u] >> (dt[u] & 63)) & 1) << (g + u);
+      }
+      const int rest = n - c0;  // chunk members present
+      const uint64_t present = rest >= 64 ? ~uint64_t(0) : (uint64_t(1) << rest) - 1;
+      mask &= present & (l == 63 ? 0 : ~uint64_t(0) << (l + 1));
+      uint64_t keep = __ballot(alive);
+      const uint32_t mlo = static_cast<uint32_t>(mask), mhi = static_cast<uint32_t>(mask >> 32);
+      for (int i = 0; i < 64; ++i)
+        if ((keep >> i) & 1) {
+          // readlane returns a signed int: widen through uint32_t so the low
+          // word does not sign-extend into the high one
+          const uint64_t mi = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(mhi, i))) << 32) |
+                              static_cast<uint32_t>(__builtin_amdgcn_readlane(mlo, i));
+          keep &= ~mi;
+        }
+      if (lane == 0) keptBits = keep;
+    }
+    __syncthreads();
+    const uint64_t kept = keptBits;
+    // removed |= row of every kept member: (member, word) pairs spread over
+    // the threads, each thread's loads issued before its first LDS update
+    constexpr int kPairs = 64 * (kNmsMax / 64) / kNmsThreads;  // pairs per thread at most
+    uint64_t r[kPairs];
+#pragma unroll
+    for (int u = 0; u < kPairs; ++u) {
+      const int p = threadIdx.x + u * kNmsThreads;
+      const int l = p / W, w = p - (p / W) * W;
+      const bool use = p < 64 * W && ((kept >> l) & 1);  // kept members are < n
+      const uint64_t v = rows[static_cast<int64_t>(idx[c0 + (l & 63)]) * words + w];
+      r[u] = use ? v : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kPairs; ++u) {
+      const int p = threadIdx.x + u * kNmsThreads;
+      if (r[u]) atomicOr(reinterpret_cast<unsigned long long*>(&removed[p % W]), static_cast<unsigned long long>(r[u]));
+    }
+    __syncthreads();
+  }
+  for (int j = threadIdx.x; j < n; j += kNmsThreads) {
+    const int dj = idx[j];
+    if ((removed[dj >> 6] >> (dj & 63)) & 1) pr[static_cast<int64_t>(dj) * classes] = 0.f;
+  }
+}
+
 }  // namespace
 }  // namespace tnh
 
@@ -365,8 +503,25 @@ extern "C" int32_t tnh_yolo_nms_sort(int64_t batch, int64_t classes, int64_t cap
   TNH_ARG(capacity > 0 && capacity <= kNmsMax, "yolo_nms_sort: capacity %lld (1..%d detections per image)",
           (long long)capacity, kNmsMax);
   TNH_ARG(boxes && prob && counts, "yolo_nms_sort: NULL argument");
-  hipLaunchKernelGGL(yolo_nms_sort_kernel, dim3(static_cast<unsigned>(classes), static_cast<unsigned>(batch)),
-                     dim3(kNmsThreads), 0, cx->stream, capacity, static_cast<int>(classes), boxes, prob, counts,
-                     thresh);
-  return launch_status("yolo_nms_sort_kernel");
+  // Overlap bits of every image in the context scratch (batch x capacity x
+  // capacity/64 words), computed once and shared by the classes; without the
+  // scratch (no memory, or a stream under capture that would need it grown)
+  // each class computes its overlaps itself.
+  const int64_t words = (capacity + 63) / 64;
+  uint64_t* bits =
+      static_cast<uint64_t*>(workspace(cx, static_cast<size_t>(batch * capacity * words) * sizeof(uint64_t)));
+  const dim3 grid(static_cast<unsigned>(classes), static_cast<unsigned>(batch));
+  if (!bits) {
+    hipLaunchKernelGGL(yolo_nms_sort_kernel, grid, dim3(kNmsThreads), 0, cx->stream, capacity,
+                       static_cast<int>(classes), boxes, prob, counts, thresh);
+    return launch_status("yolo_nms_sort_kernel");
+  }
+  hipLaunchKernelGGL(nms_overlap_bits_kernel,
+                     dim3(static_cast<unsigned>((capacity + 255) / 256), static_cast<unsigned>(words),
+                          static_cast<unsigned>(batch)),
+                     dim3(256), 0, cx->stream, capacity, words, boxes, counts, thresh, bits);
+  if (int st = launch_status("nms_overlap_bits_kernel")) return st;
+  hipLaunchKernelGGL(yolo_nms_bits_kernel, grid, dim3(kNmsThreads), 0, cx->stream, capacity, words,
+                     static_cast<int>(classes), prob, counts, bits);
+  return launch_status("yolo_nms_bits_kernel");
 }
