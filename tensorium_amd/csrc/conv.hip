@@ -237,91 +237,23 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
 // Few-channel 3x3 convolution (C <= 4, e.g. the RGB input layer): the
 // output is store-bound (F outputs per pixel against 9*C inputs), so instead
 // of a GEMM each thread owns one output pixel, keeps its 9*C window inputs
-// in registers and walks the filters four at a time.  The weights are
-// wave-uniform: they are read through the scalar cache into SGPRs and feed
-// the fused multiply-adds directly.  Every store is coalesced along the
-// pixel row.  Each output is a sequential fused multiply-add chain over k in
-// the reference order k = (c*3 + ky)*3 + kx from 0, padding taps included as
-// zeros: exactly the arithmetic of the reference CPU path (im2col, then the
-// saxpy chain of ntensors.pas:1308-1436), then bias, activation, residual.
+// in registers and walks the filters four at a time.  The weights and the
+// bias are wave-uniform: they are read through the scalar cache into SGPRs
+// and feed the fused multiply-adds directly, and the activation is a template
+// argument, so the filter loop holds no vector load and no branch (a vector
+// load there would make every filter wait for the stores already issued).
+// Every store is coalesced along the pixel row.  Each output is a sequential
+// fused multiply-add chain over k in the reference order k = (c*3 + ky)*3 +
+// kx from 0, padding taps included as zeros: exactly the arithmetic of the
+// reference CPU path (im2col, then the saxpy chain of ntensors.pas:1308-1436),
+// then bias, activation, residual.
 template <int C, bool TAP>
-__global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w) {
-  constexpr int K = 9 * C;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (n >= a.g.N) return;
-  const int F = static_cast<int>(a.F);
-  const int OHW = a.g.OHW, OW = a.g.OW, H = a.g.H, W = a.g.W;
-  const int b = static_cast<int>(n / OHW);
-  const int p = static_cast<int>(n - static_cast<int64_t>(b) * OHW);
+__device__ inline void smallc_window(const ConvArgs& a, bool valid, int b, int p, float (&in)[9 * C]) {
+  const int OW = a.g.OW, H = a.g.H, W = a.g.W;
   const int oy = p / OW, ox = p - (p / OW) * OW;
   const int iy0 = oy * a.g.sY - a.g.pH, ix0 = ox * a.g.sX - a.g.pW;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
   const uint32_t base = static_cast<uint32_t>(static_cast<int64_t>(b) * a.g.xBatchStride * 4);
-  float in[K];
-#pragma unroll
-  for (int c = 0; c < C; ++c)
-#pragma unroll
-    for (int ky = 0; ky < 3; ++ky)
-#pragma unroll
-      for (int kx = 0; kx < 3; ++kx) {
-        const int iy = iy0 + ky, ix = ix0 + kx;
-        const bool ok = static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
-                        static_cast<unsigned>(ix) < static_cast<unsigned>(W);
-        in[(c * 3 + ky) * 3 + kx] =
-            buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
-      }
-  float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
-  const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
-  auto finish = [&](int f, float acc) {
-    float v = acc;
-    if (a.bias) v = v + a.bias[f];
-    v = apply_act(v, a.act);
-    if (res) v = v + res[static_cast<int64_t>(f) * OHW];
-    out[static_cast<int64_t>(f) * OHW] = v;
-  };
-  // weight of filter f at reference index k = c*9 + t
-  auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
-  int f = 0;
-  for (; f + 4 <= F; f += 4) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < K; ++k)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt(f + q, k), in[k], acc[q]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) finish(f + q, acc[q]);
-  }
-  for (; f < F; ++f) {
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < K; ++k) acc = fmaf(wt(f, k), in[k], acc);
-    finish(f, acc);
-  }
-}
-
-// Channels-last output of the few-channel kernel: the same per-pixel
-// sequential FMA chains (bit-exact), FC filters at a time, then each wave
-// passes its 64 pixels x FC results through LDS so that FC/4 consecutive
-// lanes store one pixel's FC channels (contiguous bytes) with 16-byte
-// stores.
-template <int C, bool TAP>
-__global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const float* __restrict__ w) {
-  constexpr int K = 9 * C, FC = 32;
-  __shared__ float tile[4][64 * (FC + 1)];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t nWave = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;  // first pixel of this wave
-  const int64_t n = nWave + lane;
-  const bool valid = n < a.g.N;
-  const int F = static_cast<int>(a.F);
-  const int OHW = a.g.OHW, OW = a.g.OW, H = a.g.H, W = a.g.W;
-  const int64_t nn = valid ? n : 0;
-  const int b = static_cast<int>(nn / OHW);
-  const int p = static_cast<int>(nn - static_cast<int64_t>(b) * OHW);
-  const int oy = p / OW, ox = p - (p / OW) * OW;
-  const int iy0 = oy * a.g.sY - a.g.pH, ix0 = ox * a.g.sX - a.g.pW;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
-  const uint32_t base = static_cast<uint32_t>(static_cast<int64_t>(b) * a.g.xBatchStride * 4);
-  float in[K];
 #pragma unroll
   for (int c = 0; c < C; ++c)
 #pragma unroll
@@ -334,82 +266,215 @@ __global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const
         in[(c * 3 + ky) * 3 + kx] =
             buf_ld1(xr, sel_off(ok, base + static_cast<uint32_t>((c * H + iy) * W + ix) * 4u));
       }
-  auto wt = [&](int f, int k) { return w[f * K + (TAP ? (k % 9) * C + k / 9 : k)]; };
-  float* t = tile[wave];
-  const bool vec = a.outPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
-  for (int f0 = 0; f0 < F; f0 += FC) {
-    const int fc = F - f0 < FC ? F - f0 : FC;
-    auto put = [&](int q, float acc) {
-      float v = acc;
-      if (a.bias) v = v + a.bias[f0 + q];
-      t[lane * (FC + 1) + q] = apply_act(v, a.act);
-    };
-    int q0 = 0;
-    for (; q0 + 4 <= fc; q0 += 4) {  // four independent chains at a time
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+}
+
+// weight of filter f at reference index k = c*9 + t (tap-major storage: t*C + c)
+template <int C, bool TAP>
+__device__ inline float smallc_wt(const float* __restrict__ w, int f, int k) {
+  return w[f * 9 * C + (TAP ? (k % 9) * C + k / 9 : k)];
+}
+
+// Four filters' sequential chains over one pixel's window, then bias and
+// activation.  HB: a bias is given (without one, -0.0 is added: the exact
+// additive identity).
+template <int C, bool TAP, int ACT, bool HB>
+__device__ inline void smallc_quad(const float* __restrict__ w, const float* __restrict__ bias, int f,
+                                   const float (&in)[9 * C], float (&v)[4]) {
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < K; ++k)
+  for (int k = 0; k < 9 * C; ++k)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] = fmaf(wt(f0 + q0 + u, k), in[k], acc[u]);
+    for (int q = 0; q < 4; ++q) acc[q] = fmaf(smallc_wt<C, TAP>(w, f + q, k), in[k], acc[q]);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) put(q0 + u, acc[u]);
-    }
-    for (; q0 < fc; ++q0) {
-      float acc = 0.f;
+  for (int q = 0; q < 4; ++q) v[q] = apply_act(acc[q] + (HB ? bias[f + q] : -0.f), ACT);
+}
+
+template <int C, bool TAP, int ACT, bool HB>
+__device__ inline float smallc_one(const float* __restrict__ w, const float* __restrict__ bias, int f,
+                                   const float (&in)[9 * C]) {
+  float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < K; ++k) acc = fmaf(wt(f0 + q0, k), in[k], acc);
-      put(q0, acc);
-    }
-    __builtin_amdgcn_wave_barrier();
-    // element e = pixel * fc + channel of this wave's 64 x fc block
-    for (int e0 = 0; e0 < 64 * fc; e0 += 256) {
-      const int e = e0 + lane * 4;
-      if (e >= 64 * fc) break;
-      const int px = e / fc, q = e - px * fc;
-      const int64_t np = nWave + px;
-      if (np >= a.g.N) continue;
-      float* dst = a.out + np * a.outPix + f0 + q;
-      const float* res = a.res ? a.res + np * a.resPix + f0 + q : nullptr;
+  for (int k = 0; k < 9 * C; ++k) acc = fmaf(smallc_wt<C, TAP>(w, f, k), in[k], acc);
+  return apply_act(acc + (HB ? bias[f] : -0.f), ACT);
+}
+
+// The bias and residual cases are compile-time branches of the kernels
+// below: a run-time test inside the filter loop costs about a third of the
+// layer's time (the loop's loads and stores can no longer be scheduled
+// across it).
+template <int C, bool TAP, int ACT>
+__global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w,
+                                                          const float* __restrict__ bias) {
+  constexpr int K = 9 * C;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (n >= a.g.N) return;
+  const int F = static_cast<int>(a.F);
+  const int OHW = a.g.OHW;
+  const int b = static_cast<int>(n / OHW);
+  const int p = static_cast<int>(n - static_cast<int64_t>(b) * OHW);
+  float in[K];
+  smallc_window<C, TAP>(a, true, b, p, in);
+  float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
+  const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
+  auto run = [&](auto hbTag, auto resTag) {
+    constexpr bool HB = decltype(hbTag)::value, RES = decltype(resTag)::value;
+    int f = 0;
+    for (; f + 4 <= F; f += 4) {
+      float rv[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (RES) {  // issued before the chains, used after them
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rv[q] = res[static_cast<int64_t>(f + q) * OHW];
+      }
       float v[4];
+      smallc_quad<C, TAP, ACT, HB>(w, bias, f, in, v);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = t[px * (FC + 1) + q + u];
-      if (res) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (q + u < fc) v[u] = v[u] + res[u];
-      }
-      if (vec && q + 4 <= fc) {
-        *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-      } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          if (q + u < fc) dst[u] = v[u];
-      }
+      for (int q = 0; q < 4; ++q) out[static_cast<int64_t>(f + q) * OHW] = RES ? v[q] + rv[q] : v[q];
     }
-    __builtin_amdgcn_wave_barrier();
+    for (; f < F; ++f) {
+      const float v = smallc_one<C, TAP, ACT, HB>(w, bias, f, in);
+      out[static_cast<int64_t>(f) * OHW] = RES ? v + res[static_cast<int64_t>(f) * OHW] : v;
+    }
+  };
+  if (bias) {
+    if (res)
+      run(std::true_type{}, std::true_type{});
+    else
+      run(std::true_type{}, std::false_type{});
+  } else {
+    if (res)
+      run(std::false_type{}, std::true_type{});
+    else
+      run(std::false_type{}, std::false_type{});
   }
+}
+
+// Channels-last output of the few-channel kernel: the same per-pixel
+// sequential FMA chains (bit-exact), 32 filters at a time.  Each wave then
+// passes its 64 pixels x 32 results through LDS so that 8 consecutive lanes
+// store one pixel's 32 channels (128 contiguous bytes) with 16-byte stores.
+// The LDS block is 64 rows of eight 16-byte chunks; chunk c of row r sits at
+// r*8 + (c ^ (r & 7)), so both the row-wise writes (a lane writes its own
+// pixel's chunk) and the pixel-wise reads (8 lanes read one row) touch eight
+// different 16-byte bank groups.  The common case (no residual, whole
+// 32-filter chunks, 16-byte aligned pixel rows) is a compile-time path of
+// its own.
+template <int C, bool TAP, int ACT>
+__global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const float* __restrict__ w,
+                                                               const float* __restrict__ bias) {
+  constexpr int K = 9 * C, FC = 32;
+  __shared__ f32x4 tile[4][64 * FC / 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nWave = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;  // first pixel of this wave
+  const int64_t n = nWave + lane;
+  const bool valid = n < a.g.N;
+  const int F = static_cast<int>(a.F);
+  const int OHW = a.g.OHW;
+  const int64_t nn = valid ? n : 0;
+  const int b = static_cast<int>(nn / OHW);
+  const int p = static_cast<int>(nn - static_cast<int64_t>(b) * OHW);
+  float in[K];
+  smallc_window<C, TAP>(a, valid, b, p, in);
+  f32x4* t = tile[wave];
+  float* tf = reinterpret_cast<float*>(t);
+  const bool vecOut = a.outPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
+  const bool vecRes = a.resPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.res) & 15) == 0;
+  const int sw = lane & 7;
+  auto run = [&](auto hbTag, auto fastTag) {
+    constexpr bool HB = decltype(hbTag)::value, FAST = decltype(fastTag)::value;
+    for (int f0 = 0; f0 < F; f0 += FC) {
+      const int fc = FAST ? FC : (F - f0 < FC ? F - f0 : FC);
+      int q0 = 0;
+      for (; q0 + 4 <= fc; q0 += 4) {  // four independent chains at a time
+        float v[4];
+        smallc_quad<C, TAP, ACT, HB>(w, bias, f0 + q0, in, v);
+        t[lane * 8 + ((q0 >> 2) ^ sw)] = f32x4{v[0], v[1], v[2], v[3]};
+      }
+      if constexpr (!FAST) {
+        for (; q0 < fc; ++q0)
+          tf[(lane * 8 + ((q0 >> 2) ^ sw)) * 4 + (q0 & 3)] = smallc_one<C, TAP, ACT, HB>(w, bias, f0 + q0, in);
+      }
+      __builtin_amdgcn_wave_barrier();
+      // pass it: lanes 8j .. 8j+7 store pixel 8*it + j, lane chunk (lane & 7) = channels 4*(lane & 7) .. +3
+      const int q = 4 * sw;
+#pragma unroll 2
+      for (int it = 0; it < 8; ++it) {
+        const int px = it * 8 + (lane >> 3);
+        const int64_t np = nWave + px;
+        const f32x4 v = t[px * 8 + (sw ^ (px & 7))];
+        float* dst = a.out + np * a.outPix + f0 + q;
+        if constexpr (FAST) {
+          if (np < a.g.N) *reinterpret_cast<f32x4*>(dst) = v;
+          continue;
+        }
+        if (np >= a.g.N || q >= fc) continue;
+        float o[4] = {v[0], v[1], v[2], v[3]};
+        if (a.res) {
+          const float* res = a.res + np * a.resPix + f0 + q;
+          if (vecRes && q + 4 <= fc) {
+            const float4 r = *reinterpret_cast<const float4*>(res);
+            o[0] = o[0] + r.x, o[1] = o[1] + r.y, o[2] = o[2] + r.z, o[3] = o[3] + r.w;
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              if (q + u < fc) o[u] = o[u] + res[u];
+          }
+        }
+        if (vecOut && q + 4 <= fc) {
+          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (q + u < fc) dst[u] = o[u];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+  const bool fast = !a.res && vecOut && F % FC == 0;
+  if (bias) {
+    if (fast)
+      run(std::true_type{}, std::true_type{});
+    else
+      run(std::true_type{}, std::false_type{});
+  } else {
+    if (fast)
+      run(std::false_type{}, std::true_type{});
+    else
+      run(std::false_type{}, std::false_type{});
+  }
+}
+
+template <int C, bool TAP, bool NHWC>
+void launch_smallc_act(const ConvArgs& a, unsigned blocks, hipStream_t s) {
+  auto go = [&](auto actTag) {
+    constexpr int ACT = decltype(actTag)::value;
+    if constexpr (NHWC)
+      hipLaunchKernelGGL((conv_smallc_nhwc_kernel<C, TAP, ACT>), dim3(blocks), dim3(256), 0, s, a, a.w, a.bias);
+    else
+      hipLaunchKernelGGL((conv_smallc_kernel<C, TAP, ACT>), dim3(blocks), dim3(256), 0, s, a, a.w, a.bias);
+  };
+  if (a.act == TNH_AC_LEAKY)
+    go(std::integral_constant<int, TNH_AC_LEAKY>{});
+  else if (a.act == TNH_AC_LOGISTIC)
+    go(std::integral_constant<int, TNH_AC_LOGISTIC>{});
+  else
+    go(std::integral_constant<int, TNH_AC_LINEAR>{});
 }
 
 template <bool TAP, bool NHWC>
 int launch_smallc(const ConvArgs& a, hipStream_t s) {
-  if constexpr (NHWC) {
-    const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
-    switch (a.g.C) {
-      case 1: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-      case 2: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-      case 3: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-      default: hipLaunchKernelGGL((conv_smallc_nhwc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    }
-    return launch_status("conv_smallc_nhwc_kernel");
-  }
   const unsigned blocks = static_cast<unsigned>((a.g.N + 255) / 256);
+  auto go = [&](auto cTag) {
+    constexpr int C = decltype(cTag)::value;
+    launch_smallc_act<C, TAP, NHWC>(a, blocks, s);
+  };
   switch (a.g.C) {
-    case 1: hipLaunchKernelGGL((conv_smallc_kernel<1, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 2: hipLaunchKernelGGL((conv_smallc_kernel<2, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    case 3: hipLaunchKernelGGL((conv_smallc_kernel<3, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
-    default: hipLaunchKernelGGL((conv_smallc_kernel<4, TAP>), dim3(blocks), dim3(256), 0, s, a, a.w); break;
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
   }
-  return launch_status("conv_smallc_kernel");
+  return launch_status(NHWC ? "conv_smallc_nhwc_kernel" : "conv_smallc_kernel");
 }
 
 // Sums the split-K partials in split order (deterministic) and applies the

@@ -76,19 +76,36 @@ def test_conv_nhwc_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act, resid):
     assert R.rel_err(got, ref) <= TOL
 
 
-def test_conv_nhwc_first_layer_bit_exact(hip):
-    """C = 3 image read as NCHW, output channels-last: the few-channel kernel's
-    sequential FMA chain, bit-exact against the oracle."""
-    case("conv nhwc first layer C3 416")
-    B, Cc, Hh, F = 2, 3, 416, 32
+@pytest.mark.parametrize("B,Cc,Hh,F,s,act,resid,bias,pad", [
+    (2, 3, 416, 32, 1, acLEAKY, False, True, 0),   # YOLOv3 layer 0
+    (2, 3, 37, 45, 1, acLEAKY, True, True, 4),     # ragged last chunk (13 filters), residual, channel slice
+    (2, 3, 21, 45, 1, acLEAKY, False, True, 3),    # unaligned channel slice: scalar stores
+    (1, 1, 9, 5, 2, acLINEAR, False, False, 0),    # no bias, fewer filters than one store quad
+    (3, 4, 20, 7, 1, acLEAKY, False, True, 1),     # unaligned slice, one ragged quad
+    (2, 2, 15, 64, 2, acLINEAR, True, True, 0),    # two whole chunks, stride 2
+])
+def test_conv_nhwc_first_layer_bit_exact(hip, B, Cc, Hh, F, s, act, resid, bias, pad):
+    """C <= 4 image read as NCHW, output channels-last: the few-channel
+    kernel's sequential FMA chain, bit-exact against the oracle; a channel
+    slice of a wider output leaves the other channels untouched."""
+    case(f"conv nhwc few-channel B{B} C{Cc} H{Hh} F{F} s{s} act{act} res{resid} bias{bias} pad{pad}")
     x = synth.uniform(75, (B, Cc, Hh, Hh))
-    Wt = synth.normal(76, (F, Cc * 9), (2.0 / 27) ** 0.5)
-    b = synth.normal(77, (F,), 0.1)
-    ref = R.conv_forward(x, Wt, b, 3, 1, 1, acLEAKY)
-    dout = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
-    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 3, 1, 1, D(x), 0, D(tap_major(Wt, F, Cc, 3)), D(b), acLEAKY, dout, 0,
-                          nchwInput=True)
-    assert np.array_equal(H(dout, hip).transpose(0, 3, 1, 2), ref)
+    Wt = synth.normal(76, (F, Cc * 9), (2.0 / (9 * Cc)) ** 0.5)
+    b = synth.normal(77, (F,), 0.1) if bias else np.zeros(F, np.float32)
+    ref = R.conv_forward(x, Wt, b, 3, s, 1, act)
+    OH = ref.shape[2]
+    res = None
+    if resid:
+        res = synth.normal(78, ref.shape)
+        ref = R.addvv(ref, res)
+    outPix = (F + pad + 3) // 4 * 4
+    dout = D(np.full((B, OH, OH, outPix), 7.0, np.float32))
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 3, s, 1, D(x), 0, D(tap_major(Wt, F, Cc, 3)), D(b) if bias else None,
+                          act, dout, pad, outPix=outPix, nchwInput=True,
+                          residual=None if res is None else D(nhwc(res)))
+    got = H(dout, hip)
+    assert np.array_equal(got[..., pad:pad + F].transpose(0, 3, 1, 2), ref)
+    assert np.all(got[..., :pad] == 7.0) and np.all(got[..., pad + F:] == 7.0)
 
 
 @pytest.mark.parametrize("k,s", [(3, 1), (3, 2), (1, 1)])
