@@ -353,9 +353,10 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
 // passes its 64 pixels x 32 results through LDS so that 8 consecutive lanes
 // store one pixel's 32 channels (128 contiguous bytes) with 16-byte stores.
 // The LDS block is 64 rows of eight 16-byte chunks; chunk c of row r sits at
-// r*8 + (c ^ (r & 7)), so both the row-wise writes (a lane writes its own
-// pixel's chunk) and the pixel-wise reads (8 lanes read one row) touch eight
-// different 16-byte bank groups.  The common case (no residual, whole
+// r*8 + (c ^ ((r / 2) % 8)) (the panel swizzle of the conv kernels), so both
+// the row-wise writes (16 lanes write 16 pixels' chunk c) and the pixel-wise
+// reads (16 lanes read two rows) touch 16 different 16-byte bank groups of
+// the 64-bank LDS.  The common case (no residual, whole
 // 32-filter chunks, 16-byte aligned pixel rows) is a compile-time path of
 // its own.
 template <int C, bool TAP, int ACT>
@@ -378,7 +379,7 @@ __global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const
   float* tf = reinterpret_cast<float*>(t);
   const bool vecOut = a.outPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
   const bool vecRes = a.resPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.res) & 15) == 0;
-  const int sw = lane & 7;
+  const int sw = (lane >> 1) & 7, qc = lane & 7;
   auto run = [&](auto hbTag, auto fastTag) {
     constexpr bool HB = decltype(hbTag)::value, FAST = decltype(fastTag)::value;
     for (int f0 = 0; f0 < F; f0 += FC) {
@@ -395,12 +396,12 @@ __global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const
       }
       __builtin_amdgcn_wave_barrier();
       // pass it: lanes 8j .. 8j+7 store pixel 8*it + j, lane chunk (lane & 7) = channels 4*(lane & 7) .. +3
-      const int q = 4 * sw;
+      const int q = 4 * qc;
 #pragma unroll 2
       for (int it = 0; it < 8; ++it) {
         const int px = it * 8 + (lane >> 3);
         const int64_t np = nWave + px;
-        const f32x4 v = t[px * 8 + (sw ^ (px & 7))];
+        const f32x4 v = t[px * 8 + (qc ^ ((px >> 1) & 7))];
         float* dst = a.out + np * a.outPix + f0 + q;
         if constexpr (FAST) {
           if (np < a.g.N) *reinterpret_cast<f32x4*>(dst) = v;

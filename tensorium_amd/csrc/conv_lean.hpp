@@ -47,17 +47,25 @@ struct LeanCfg {
 };
 
 // k-contiguous panel [ROWS][BK] (floats) whose 16-byte chunks are
-// XOR-swizzled by row % 8.  Eight consecutive rows at one chunk index, or
-// one row's chunks, touch distinct banks.
+// XOR-swizzled: logical chunk q of row r sits at physical chunk q ^ swz(r).
+// The LDS has 64 four-byte banks (256 bytes) and serves a 16-byte access 16
+// lanes at a time, so 16 consecutive rows at one logical chunk must land in
+// 16 different 16-byte bank groups.  A 32-float row is half a bank line: the
+// row parity picks the half and swz(r) = (r / 2) % 8 spreads each half's 8
+// rows over its 8 groups.  A 64-float row spans all 64 banks: swz(r) =
+// r % 16.  One row's chunks, and two consecutive rows' chunks, are always
+// distinct groups too (the row-wise stores of the loaders).
 template <int ROWS, int BK>
 struct SwzPanel {
   static constexpr int SIZE = ROWS * BK;
-  __device__ static inline int chunk(int row, int q) { return row * BK + 4 * (q ^ (row & 7)); }
+  static_assert(BK == 32 || BK == 64, "panel depth");
+  __device__ static inline int swz(int row) { return BK == 32 ? (row >> 1) & 7 : row & 15; }
+  __device__ static inline int chunk(int row, int q) { return row * BK + 4 * (q ^ swz(row)); }
 };
 
 // k-contiguous operand: row r of the panel is memory row r0 + r (row stride
 // ld floats, rows >= `rows` read 0), 16-byte loads.  Thread t owns chunk
-// t % (BK/4) of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 8 == 0, so every row
+// t % (BK/4) of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 16 == 0, so every row
 // of a thread has the same swizzle).  The conv weights [F][K] (ld = K), and
 // the GEMM operands A (not transposed) and B (transposed).
 template <int ROWS, int BK_, int NT_>
@@ -68,7 +76,7 @@ struct LeanRowsK {
   static constexpr int PER = ROWS / ROWSTEP;
   using L = SwzPanel<ROWS, BK>;
   static constexpr int SIZE = L::SIZE;
-  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0, "LeanRowsK split");
+  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 16 == 0, "LeanRowsK split");
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t voff[PER];
   int ldsOff;
@@ -174,7 +182,7 @@ struct NhwcTapRows {
   static constexpr int PER = ROWS / ROWSTEP;
   using L = SwzPanel<ROWS, BK>;
   static constexpr int SIZE = L::SIZE;
-  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 8 == 0 && KH * KW <= 32,
+  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 16 == 0 && KH * KW <= 32,
                 "NhwcTapRows split");
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t rowOff[PER];
@@ -371,9 +379,9 @@ struct LeanLoop {
     f32x4 b[FN][2];
   };
 
-  // Per-lane float offsets inside a 32-row block of either panel (rows are a
-  // multiple of 32 apart, so row % 8 is lane % 8): lo[c][e] addresses half e
-  // of chunk c.
+  // Per-lane float offsets inside a 32-row block of either panel (blocks
+  // start at multiples of 32 rows, so a row's swizzle is that of lane % 32):
+  // lo[c][e] addresses half e of chunk c.
   struct Lanes {
     int lo[KCH][2];
     int aRow, bRow;  // first row of the wave's blocks, times BK
@@ -441,7 +449,7 @@ struct LeanLoop {
 #pragma unroll
     for (int c = 0; c < KCH; ++c)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) L.lo[c][e] = r * BK + 4 * ((4 * c + 2 * h + e) ^ (r & 7));
+      for (int e = 0; e < 2; ++e) L.lo[c][e] = SwzPanel<32, BK>::chunk(r, 4 * c + 2 * h + e);
     L.aRow = wm * Cfg::WTM * BK;
     L.bRow = wn * Cfg::WTN * BK;
     return L;
