@@ -247,7 +247,7 @@ __global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) 
 // kx from 0, padding taps included as zeros: exactly the arithmetic of the
 // reference CPU path (im2col, then the saxpy chain of ntensors.pas:1308-1436),
 // then bias, activation, residual.
-template <int C, bool TAP>
+template <int C>
 __device__ inline void smallc_window(const ConvArgs& a, bool valid, int b, int p, float (&in)[9 * C]) {
   const int OW = a.g.OW, H = a.g.H, W = a.g.W;
   const int oy = p / OW, ox = p - (p / OW) * OW;
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const floa
   const int b = static_cast<int>(n / OHW);
   const int p = static_cast<int>(n - static_cast<int64_t>(b) * OHW);
   float in[K];
-  smallc_window<C, TAP>(a, true, b, p, in);
+  smallc_window<C>(a, true, b, p, in);
   float* out = a.out + static_cast<int64_t>(b) * a.outBatchStride + p;
   const float* res = a.res ? a.res + static_cast<int64_t>(b) * a.rBatchStride + p : nullptr;
   auto run = [&](auto hbTag, auto resTag) {
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const
   const int b = static_cast<int>(nn / OHW);
   const int p = static_cast<int>(nn - static_cast<int64_t>(b) * OHW);
   float in[K];
-  smallc_window<C, TAP>(a, valid, b, p, in);
+  smallc_window<C>(a, valid, b, p, in);
   f32x4* t = tile[wave];
   float* tf = reinterpret_cast<float*>(t);
   const bool vecOut = a.outPix % 4 == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
