@@ -335,8 +335,9 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
 
 
 def extra_detect(hip, layers, weights, batch=16, thresh=0.5, nms=0.45):
-    """YOLO detection list + per-class NMS on the device
-    after a YOLOv3-416 forward at batch 16 (tnh_yolo_detections +
+    """YOLO detection list + per-class NMS on the device (the reference's
+    TNNet.Detections, nnet.pas:584, and doNMSSort, ntypes.pas:1612) after a YOLOv3-416
+    forward at batch 16 (tnh_yolo_detections +
     tnh_yolo_nms_sort, device time; the list stays in HBM)."""
     import torch
 
