@@ -67,6 +67,24 @@ def test_sgemm_vs_oracle(hip, ta, tb, M, N, K):
     assert R.rel_err(H(dC, hip), C) <= TOL
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_full_size_exact(hip, ta, tb):
+    """BASELINE config 2 at 4096^3 (the tuned lean kernels at their benchmark
+    size): integer operands in [-4, 4] make every partial sum exact in fp32,
+    so the result equals a float64 product bit for bit."""
+    M = N = K = 4096
+    case(f"sgemm full size int ta={ta} tb={tb} {M}x{N}x{K}")
+    rng = np.random.default_rng(4096 + 2 * ta + tb)
+    A = rng.integers(-4, 5, (K, M) if ta else (M, K)).astype(np.float32)
+    B = rng.integers(-4, 5, (N, K) if tb else (K, N)).astype(np.float32)
+    dA, dB = D(A), D(B)
+    dC = torch.full((M, N), 3.0, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, A.shape[1], dB, 0, B.shape[1], 0.0, dC, 0, N)
+    ref = op(A, ta).astype(np.float64) @ op(B, tb).astype(np.float64)
+    assert np.array_equal(H(dC, hip), ref.astype(np.float32))
+
+
 def test_sgemm_alpha_beta_offsets_ld(hip):
     case("sgemm alpha/beta, offsets, padded ld")
     rng = np.random.default_rng(5)

@@ -2,7 +2,9 @@
 pre-logistic head convolutions (darknet layers 81, 93, 105) within the
 per-tensor 1e-5 bound, every intermediate convolution too, and the yolo
 outputs.  Batch 2 checks that per-image results do not depend on the batch
-(per-image route concat)."""
+(per-image route concat).  The benchmark configurations at their full sizes
+(416 at batch 16, 608 at batch 32, channels-last, tuned for those shapes)
+are tied to the oracle-checked batch-1 network image by image."""
 import numpy as np
 import pytest
 import torch
@@ -197,3 +199,67 @@ def test_yolov3_nhwc_matches_nchw_and_replays(hip, yolo):
     finally:
         b.release_graph()
         hip.useTorchStream()
+
+
+def test_yolov3_416_b16_bench_config(hip, yolo):
+    """The benchmark's own configuration: YOLOv3-416 at batch 16,
+    channels-last, autotuned for batch-16 shapes (tail splits included).
+    Images 0, 7 and 15 of the batch equal batch-1 NCHW runs of the same
+    images (checked against the oracle layer by layer above) at the three
+    head convolutions within the per-tensor bound, and two graph replays of
+    the batch-16 forward equal its eager result bit for bit."""
+    layers, W = yolo
+    print("[case] yolov3-416 batch 16 nhwc (bench configuration) vs batch-1 nchw, graph replay", flush=True)
+    x = synth.uniform(13, (16, 3, 416, 416))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    big = darknet.Network(hip, layers, 16, W, layout="nhwc")
+    eager = [h.cpu().numpy() for h in big.forward(dx)]
+    hip.finish()
+    heads16 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
+    one = darknet.Network(hip, layers, 1, W)
+    for img in (0, 7, 15):
+        xi = torch.from_numpy(np.ascontiguousarray(x[img:img + 1])).cuda()
+        torch.cuda.synchronize()
+        one.forward(xi)
+        hip.finish()
+        for i in (81, 93, 105):
+            e = R.rel_err(heads16[i][img:img + 1], one.output(i).cpu().numpy())
+            assert e <= 2 * TOL, (img, i, e)
+    try:
+        big.capture(dx)
+        for rep in range(2):
+            heads = big.replay()
+            hip.finish()
+            for u, v in zip([h.cpu().numpy() for h in heads], eager):
+                assert np.array_equal(u, v), rep
+            torch.cuda.synchronize()
+    finally:
+        big.release_graph()
+        hip.useTorchStream()
+
+
+def test_yolov3_608_b32_bench_config(hip):
+    """BASELINE config 5 at its size: YOLOv3-608 at batch 32, channels-last
+    and autotuned for those shapes; images 0 and 31 equal batch-1 NCHW runs
+    of the same images at the three head convolutions within the bound."""
+    _, layers = darknet.load_cfg("yolov3.cfg", 608, 608)
+    W = darknet.synthetic_weights(layers)
+    print("[case] yolov3-608 batch 32 nhwc vs batch-1 nchw", flush=True)
+    x = synth.uniform(17, (32, 3, 608, 608))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    big = darknet.Network(hip, layers, 32, W, layout="nhwc")
+    big.forward(dx)
+    hip.finish()
+    heads32 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
+    del big
+    one = darknet.Network(hip, layers, 1, W)
+    for img in (0, 31):
+        xi = torch.from_numpy(np.ascontiguousarray(x[img:img + 1])).cuda()
+        torch.cuda.synchronize()
+        one.forward(xi)
+        hip.finish()
+        for i in (81, 93, 105):
+            e = R.rel_err(heads32[i][img:img + 1], one.output(i).cpu().numpy())
+            assert e <= 2 * TOL, (img, i, e)
