@@ -10,7 +10,9 @@ Fusions (results bit-identical to the unfused layer sequence):
   * a convolution whose only consumer is the next layer, a ``[shortcut]``
     with linear activation, writes ``act(conv + bias) + other`` straight into
     the shortcut's buffer (the separate add of naddlayer.pas:698);
-  * a single-input ``[route]`` is an alias of its input (no copy).
+  * a single-input ``[route]`` is an alias of its input (no copy);
+  * at batch 1 (NCHW) a multi-input route's inputs are written by their
+    producers straight into their channel slices of the route buffer.
 
 Route concat of several inputs is per image (darknet semantics).  The
 reference's TConcatLayer copies whole batched tensors back to back
@@ -208,14 +210,36 @@ class Network:
         if layout == "nhwc":
             self._plan_nhwc(device)
             return
+        # At batch 1 a channel slice of an NCHW route buffer is contiguous, so
+        # a route input's producer (convolution, shortcut or upsample) writes
+        # straight into its slice and the route copies only the other inputs.
+        placed = {}
+        self.route_copies = {}
+        if batch == 1 and route_mode == "image":
+            for L in layers:
+                if L["type"] == "route" and len(L["srcs"]) > 1:
+                    C, h, w = L["out"]
+                    buf = torch.empty((1, C, h, w), dtype=torch.float32, device=device)
+                    self.out[L["index"]] = buf
+                    off, copies = 0, []
+                    for s_ in L["srcs"]:
+                        o = self._owner(s_)
+                        cs = layers[s_]["out"][0]
+                        if o not in placed and layers[o]["type"] in ("convolutional", "shortcut", "upsample"):
+                            placed[o] = buf[:, off:off + cs]
+                        else:
+                            copies.append((s_, off))
+                        off += cs
+                    self.route_copies[L["index"]] = copies
         for L in layers:
             i = L["index"]
             if L["type"] == "route" and len(L["srcs"]) == 1:
                 continue  # alias, resolved at run time
-            if i in self.fused:
-                continue  # writes into the shortcut's buffer
+            if i in self.fused or self.out[i] is not None:
+                continue  # writes into the shortcut's buffer / a route buffer
             C, h, w = L["out"]
-            self.out[i] = torch.empty((batch, C, h, w), dtype=torch.float32, device=device)
+            self.out[i] = placed[i] if i in placed else torch.empty((batch, C, h, w), dtype=torch.float32,
+                                                                     device=device)
 
     # -- channels-last storage plan --------------------------------------------
     def _owner(self, i):
@@ -385,6 +409,12 @@ class Network:
         elif t == "route":
             if len(L["srcs"]) == 1:
                 prev = self.buffer(L["srcs"][0])
+            elif i in self.route_copies:  # batch 1: producers wrote their slices in place
+                _, h, ww = L["out"]
+                for s_, off in self.route_copies[i]:
+                    n = int(np.prod(self.layers[s_]["out"]))
+                    hip.copy(n, self.buffer(s_), 0, 1, self.out[i], off * h * ww, 1)
+                prev = self.out[i]
             else:
                 srcs = [self.buffer(s) for s in L["srcs"]]
                 sizes = [int(np.prod(self.layers[s]["out"])) for s in L["srcs"]]
