@@ -636,7 +636,8 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
     const int64_t panels = a.g.K / Cfg::BK;
     a.kChunk = (panels + a.tailSplits - 1) / a.tailSplits * Cfg::BK;
     a.tailSplits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty piece
-    if (full == tiles || full == 0 || a.tailSplits < 2) {
+    if (full == tiles || full == 0 || a.tailSplits < 2 ||
+        (tiles - full) * std::max<int64_t>(a.tailSplits, Cfg::NT / 64) + full > INT32_MAX) {
       a.tailSplits = 0;
       a.kChunk = a.g.K;
     } else {
@@ -654,7 +655,8 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
     hipLaunchKernelGGL((conv_lean_kernel<Cfg, k1x1, false>), grid, dim3(Cfg::NT), 0, s, a);
   if (int st = launch_status("conv_lean_kernel")) return st;
   if (a.tailSplits > 0) {
-    hipLaunchKernelGGL((conv_tail_reduce<Cfg>), dim3(static_cast<unsigned>(tiles - a.nFull)), dim3(Cfg::NT), 0, s, a);
+    hipLaunchKernelGGL((conv_tail_reduce<Cfg>), dim3(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64))),
+                       dim3(64), 0, s, a);
     return launch_status("conv_tail_reduce");
   }
   return launch_reduce(a, s);
@@ -739,7 +741,8 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
     const int64_t panels = a.g.K / Cfg::BK;
     a.kChunk = (panels + a.tailSplits - 1) / a.tailSplits * Cfg::BK;
     a.tailSplits = static_cast<int>((a.g.K + a.kChunk - 1) / a.kChunk);  // no empty piece
-    if (full == tiles || a.tailSplits < 2 || (tiles - full) * a.tailSplits + full > INT32_MAX) {
+    if (full == tiles || a.tailSplits < 2 ||
+        (tiles - full) * std::max<int64_t>(a.tailSplits, Cfg::NT / 64) + full > INT32_MAX) {
       a.tailSplits = 0;
       a.kChunk = a.g.K;
     } else {
@@ -755,8 +758,8 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
     hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1>), dim3(static_cast<unsigned>(grid)), dim3(Cfg::NT), 0, s, a);
   if (int st = launch_status("conv_nhwc_kernel")) return st;
   if (a.tailSplits > 0) {
-    hipLaunchKernelGGL((conv_tail_reduce<Cfg, true>), dim3(static_cast<unsigned>(tiles - a.nFull)), dim3(Cfg::NT), 0,
-                       s, a);
+    hipLaunchKernelGGL((conv_tail_reduce<Cfg, true>), dim3(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64))),
+                       dim3(64), 0, s, a);
     return launch_status("conv_tail_reduce");
   }
   return TNH_OK;

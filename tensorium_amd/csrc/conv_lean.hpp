@@ -519,12 +519,25 @@ struct LeanTraits<Cfg, k1x1, VB> {
   using BL = Lean1x1B<Cfg, kVec>;
 };
 
-// Offset of accumulator register (i, j, r) of a lane inside a tail piece's
-// BM x BN block: register order, so that 64 consecutive lanes store 64
-// consecutive floats.
+// A tail piece is one workgroup's raw accumulators (a BM x BN block) in
+// register order, in 16-byte quads: quad q (registers 4q .. 4q+3) of
+// accumulator block (i, j) of a wave is 64 lanes x 16 consecutive bytes, so
+// every piece store and load is one coalesced 1 KB access per wave.
 template <class Cfg>
-__device__ inline int piece_off(int wave, int lane, int i, int j, int r) {
-  return ((wave * Cfg::FM * Cfg::FN + i * Cfg::FN + j) * 16 + r) * 64 + lane;
+__device__ inline int piece_quad(int wave, int lane, int i, int j, int q) {
+  return (((wave * Cfg::FM * Cfg::FN + i * Cfg::FN + j) * 4 + q) * 64 + lane) * 4;
+}
+
+template <class Cfg>
+__device__ inline void store_piece(float* dst, int wave, int lane, const f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+#pragma unroll
+  for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(dst + piece_quad<Cfg>(wave, lane, i, j, q)) =
+            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
 }
 
 template <class Cfg, int MODE, bool VB>
@@ -557,13 +570,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (piece >= 0) {
-    float* dst = a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN);
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dst[piece_off<Cfg>(wave, lane, i, j, r)] = acc[i][j][r];
+    store_piece<Cfg>(a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN), wave, lane, acc);
     return;
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
@@ -575,29 +582,48 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
 // accumulator registers the conv kernel would have held, then applies the
 // conv kernel's own epilogue.
 template <class Cfg, bool NHWC = false>
-__global__ __launch_bounds__(Cfg::NT) void conv_tail_reduce(ConvArgs a) {
-  const int t = blockIdx.x;
+__global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
+  // one single-wave workgroup per wave of a tail tile: the reduction of a
+  // few tail tiles still spreads over every CU
+  constexpr int NW = Cfg::NT / 64;
+  const int t = blockIdx.x / NW;
   int tm, tn;
   tile_coords(a.nFull + t, a.tilesM, a.tilesN, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x, wave = blockIdx.x - t * NW;
   constexpr int TILE = Cfg::BM * Cfg::BN;
-  const float* src = a.part + static_cast<int64_t>(t) * a.tailSplits * TILE;
+  const int P = a.tailSplits;
+  const float* src = a.part + static_cast<int64_t>(t) * P * TILE;
+  // The loads of G pieces are issued together (one memory round trip per G
+  // pieces instead of per piece); the sum still runs in piece order.
+  constexpr int G = Cfg::FM * Cfg::FN <= 2 ? 4 : 2;
   f32x16 acc[Cfg::FM][Cfg::FN];
+  for (int s0 = 0; s0 < P; s0 += G) {
+    f32x4 part[G][Cfg::FM][Cfg::FN][4];
 #pragma unroll
-  for (int i = 0; i < Cfg::FM; ++i)
+    for (int g = 0; g < G; ++g) {
+      const float* ps = src + static_cast<int64_t>(s0 + g < P ? s0 + g : P - 1) * TILE;
 #pragma unroll
-    for (int j = 0; j < Cfg::FN; ++j)
+      for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = src[piece_off<Cfg>(wave, lane, i, j, r)];
-  for (int s = 1; s < a.tailSplits; ++s) {
-    const float* ps = src + static_cast<int64_t>(s) * TILE;
+        for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
+          for (int q = 0; q < 4; ++q)
+            part[g][i][j][q] = *reinterpret_cast<const f32x4*>(ps + piece_quad<Cfg>(wave, lane, i, j, q));
+    }
 #pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j)
+    for (int g = 0; g < G; ++g) {
+      if (s0 + g >= P) break;  // uniform
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + ps[piece_off<Cfg>(wave, lane, i, j, r)];
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = part[g][i][j][r >> 2][r & 3];
+            acc[i][j][r] = s0 + g == 0 ? v : acc[i][j][r] + v;
+          }
+    }
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   if constexpr (NHWC)
@@ -646,13 +672,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (piece >= 0) {
-    float* dst = a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN);
-#pragma unroll
-    for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dst[piece_off<Cfg>(wave, lane, i, j, r)] = acc[i][j][r];
+    store_piece<Cfg>(a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN), wave, lane, acc);
     return;
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
