@@ -170,23 +170,33 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // NCHW head layout [b][ch][y][x] the detection decoder reads: 32 pixels x 32
 // channels per tile through LDS, so the reads run along channels and the
 // writes along pixels; per element the same operation as yolo_kernel.
-__global__ __launch_bounds__(256) void yolo_nhwc_kernel(int64_t HW, int64_t CH, int64_t entries, const float* in,
-                                                        int64_t inPix, float* out) {
+// The four loads of a thread are issued unconditionally (clamped to the
+// tensor) before any is used, and the entry index is 32-bit arithmetic
+// (HW, CH < 2^31 checked by the host).
+__global__ __launch_bounds__(256) void yolo_nhwc_kernel(int HW, int CH, int entries, const float* __restrict__ in,
+                                                        int64_t inPix, float* __restrict__ out) {
   __shared__ float tile[32][33];
   const int64_t b = blockIdx.z;
-  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 32, c0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int p0 = blockIdx.x * 32, c0 = blockIdx.y * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 8 rows of 32
-  for (int r = ty; r < 32; r += 8) {
-    const int64_t p = p0 + r, c = c0 + tx;
-    tile[r][tx] = p < HW && c < CH ? in[(b * HW + p) * inPix + c] : 0.f;
+  const float* src = in + b * HW * inPix;
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = min(p0 + ty + 8 * k, HW - 1), c = min(c0 + tx, CH - 1);
+    v[k] = src[static_cast<int64_t>(p) * inPix + c];
   }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) tile[ty + 8 * k][tx] = v[k];
   __syncthreads();
-  for (int r = ty; r < 32; r += 8) {
-    const int64_t c = c0 + r, p = p0 + tx;
+  float* dst = out + b * CH * HW;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = c0 + ty + 8 * k, p = p0 + tx;
     if (c < CH && p < HW) {
-      const float v = tile[tx][r];
-      const int64_t entry = c % entries;
-      out[(b * CH + c) * HW + p] = (entry == 2 || entry == 3) ? v : logistic_poly(v);
+      const float x = tile[tx][ty + 8 * k];
+      const int entry = c % entries;
+      dst[static_cast<int64_t>(c) * HW + p] = (entry == 2 || entry == 3) ? x : logistic_poly(x);
     }
   }
 }
@@ -371,11 +381,12 @@ extern "C" int32_t tnh_yolo_fwd_nhwc(int64_t batch, int64_t n, int64_t classes, 
   TNH_ARG(in && out && inOff >= 0, "yolo_fwd_nhwc: NULL buffer or negative offset");
   const int64_t CH = n * (classes + 5), HW = h * w;
   TNH_ARG(inPix >= CH, "yolo_fwd_nhwc: inPix %lld < %lld channels", (long long)inPix, (long long)CH);
-  TNH_ARG(batch < 65536 && (HW + 31) / 32 < INT32_MAX && (CH + 31) / 32 < 65536, "yolo_fwd_nhwc: grid too large");
+  TNH_ARG(batch < 65536 && HW <= INT32_MAX - 32 && (CH + 31) / 32 < 65536, "yolo_fwd_nhwc: grid too large");
   if (batch == 0) return TNH_OK;
   const dim3 grid(static_cast<unsigned>((HW + 31) / 32), static_cast<unsigned>((CH + 31) / 32),
                   static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(yolo_nhwc_kernel, grid, dim3(256), 0, cx->stream, HW, CH, classes + 5, in + inOff, inPix, out);
+  hipLaunchKernelGGL(yolo_nhwc_kernel, grid, dim3(256), 0, cx->stream, static_cast<int>(HW), static_cast<int>(CH),
+                     static_cast<int>(classes + 5), in + inOff, inPix, out);
   return launch_status("yolo_nhwc_kernel");
 }
 
