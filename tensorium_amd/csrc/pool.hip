@@ -126,28 +126,34 @@ __global__ __launch_bounds__(kThreads) void upsample2_fwd_kernel(int64_t total, 
 }
 
 // Channels-last nearest upsample, forward: out pixel (b, y, x) channel c =
-// scale * in pixel (b, y / s, x / s) channel c; four channels per thread
-// (16-byte loads and stores) when C, both pixel strides and both bases allow.
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void upsample_nhwc_kernel(int64_t total, int64_t C, int64_t h, int64_t w,
-                                                                 int64_t s, float scale, const float* __restrict__ in,
-                                                                 int64_t inPix, float* __restrict__ out,
-                                                                 int64_t outPix) {
+// scale * in pixel (b, y / s, x / s) channel c.  One thread per input pixel
+// and channel group: one load, s*s stores, so the index arithmetic (32-bit
+// when the sizes allow: I = int) is paid once per input element.  Four
+// channels per thread (16-byte loads and stores) when C, both pixel strides
+// and both bases allow.
+template <bool VEC, class I>
+__global__ __launch_bounds__(kThreads) void upsample_nhwc_kernel(I total, I C, I h, I w, int s, float scale,
+                                                                 const float* __restrict__ in, int64_t inPix,
+                                                                 float* __restrict__ out, int64_t outPix) {
   constexpr int V = VEC ? 4 : 1;
-  const int64_t CV = C / V, OW = w * s, OH = h * s;
-  GRID_STRIDE(e, total) {  // e = (output pixel, channel group)
-    const int64_t cg = e % CV;
-    const int64_t pix = e / CV;
-    const int64_t x = pix % OW;
-    const int64_t t = pix / OW;
-    const int64_t y = t % OH, b = t / OH;
-    const float* src = in + ((b * h + y / s) * w + x / s) * inPix + cg * V;
-    float* dst = out + pix * outPix + cg * V;
+  const I CV = C / V, OW = w * s;
+  for (I e = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; e < total;
+       e += static_cast<I>(gridDim.x) * kThreads) {  // e = (input pixel, channel group)
+    const I cg = e % CV, ip = e / CV;
+    const I x = ip % w, t = ip / w;
+    const I y = t % h, b = t / h;
+    const float* src = in + static_cast<int64_t>(ip) * inPix + cg * V;
+    const int64_t o0 = (static_cast<int64_t>(b) * h + y) * s * OW + static_cast<int64_t>(x) * s;
     if constexpr (VEC) {
       const float4 v = *reinterpret_cast<const float4*>(src);
-      *reinterpret_cast<float4*>(dst) = make_float4(scale * v.x, scale * v.y, scale * v.z, scale * v.w);
+      const float4 sv = make_float4(scale * v.x, scale * v.y, scale * v.z, scale * v.w);
+      for (int dy = 0; dy < s; ++dy)
+        for (int dx = 0; dx < s; ++dx)
+          *reinterpret_cast<float4*>(out + (o0 + static_cast<int64_t>(dy) * OW + dx) * outPix + cg * V) = sv;
     } else {
-      *dst = scale * *src;
+      const float sv = scale * *src;
+      for (int dy = 0; dy < s; ++dy)
+        for (int dx = 0; dx < s; ++dx) out[(o0 + static_cast<int64_t>(dy) * OW + dx) * outPix + cg] = sv;
     }
   }
 }
@@ -249,16 +255,26 @@ extern "C" int32_t tnh_upsample_nhwc(int64_t batch, int64_t channels, int64_t h,
   TNH_ARG(inPix >= channels && outPix >= channels, "upsample_nhwc: pixel stride below the channel count");
   const float* src = in + inOff;
   float* dst = out + outOff;
-  const int64_t pixels = batch * h * w * stride * stride;
+  TNH_ARG(stride <= 64, "upsample_nhwc: stride %lld above 64", (long long)stride);
+  const int64_t pixels = batch * h * w;  // input pixels
   if (pixels == 0) return TNH_OK;
   const bool vec = channels % 4 == 0 && inPix % 4 == 0 && outPix % 4 == 0 &&
                    (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
   const int64_t total = pixels * (vec ? channels / 4 : channels);
+  // 32-bit indices when every index the kernel forms (input elements, rows
+  // of output pixels) stays below 2^31
+  const bool small = total + kThreads * 65536LL < INT32_MAX && batch * h * stride < INT32_MAX &&
+                     w * stride < INT32_MAX;
+  auto go = [&](auto vecTag, auto idx) {
+    constexpr bool VEC = decltype(vecTag)::value;
+    using I = decltype(idx);
+    hipLaunchKernelGGL((upsample_nhwc_kernel<VEC, I>), dim3(grid_for(total)), dim3(kThreads), 0, cx->stream,
+                       static_cast<I>(total), static_cast<I>(channels), static_cast<I>(h), static_cast<I>(w),
+                       static_cast<int>(stride), scale, src, inPix, dst, outPix);
+  };
   if (vec)
-    hipLaunchKernelGGL(upsample_nhwc_kernel<true>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
-                       channels, h, w, stride, scale, src, inPix, dst, outPix);
+    small ? go(std::true_type{}, int{}) : go(std::true_type{}, int64_t{});
   else
-    hipLaunchKernelGGL(upsample_nhwc_kernel<false>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
-                       channels, h, w, stride, scale, src, inPix, dst, outPix);
+    small ? go(std::false_type{}, int{}) : go(std::false_type{}, int64_t{});
   return launch_status("upsample_nhwc_kernel");
 }

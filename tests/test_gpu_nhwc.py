@@ -165,3 +165,26 @@ def test_conv_nhwc_rejects_unsupported(hip):
         hip.conv2dForwardNHWC(1, 48, 8, 8, 32, 3, 1, 1, x, 0, w, None, acLEAKY, out, 0)
     with pytest.raises(TNHError):  # 1x1 with stride 2
         hip.conv2dForwardNHWC(1, 32, 8, 8, 32, 1, 2, 0, x, 0, w, None, acLEAKY, out, 0, inPix=48)
+
+
+@pytest.mark.parametrize("B,Cc,Hh,Ww,s,scale,inPad,outPad,outOff", [
+    (2, 256, 13, 13, 2, 1.0, 0, 0, 0),      # YOLOv3 upsample (16-byte path)
+    (3, 128, 7, 9, 2, 0.5, 4, 384, 128),    # into a channel slice of a route buffer
+    (1, 6, 5, 4, 3, 2.0, 1, 3, 1),          # odd channels and strides: scalar path, stride 3
+])
+def test_upsample_nhwc_vs_oracle(hip, B, Cc, Hh, Ww, s, scale, inPad, outPad, outOff):
+    """Channels-last nearest upsample (a channel slice in and out): bit-exact
+    against the oracle's NCHW upsample; the rest of the output buffer is
+    untouched."""
+    case(f"upsample nhwc B{B} C{Cc} {Hh}x{Ww} s{s} scale{scale} pads {inPad},{outPad} off{outOff}")
+    x = synth.normal(81, (B, Cc, Hh, Ww))
+    ref = R.upsample_fwd(x, s, scale)
+    inPix, outPix = Cc + inPad, Cc + outPad
+    xin = np.zeros((B, Hh, Ww, inPix), np.float32)
+    xin[..., :Cc] = nhwc(x)
+    dout = D(np.full((B, Hh * s, Ww * s, outPix), 7.0, np.float32))
+    hip.upSampleNHWC(B, Cc, Hh, Ww, s, scale, D(xin), 0, inPix, dout, outOff, outPix)
+    got = H(dout, hip)
+    assert np.array_equal(got[..., outOff:outOff + Cc].transpose(0, 3, 1, 2), ref)
+    rest = np.concatenate([got[..., :outOff], got[..., outOff + Cc:]], axis=-1)
+    assert np.all(rest == 7.0)
