@@ -42,7 +42,7 @@ PEAK_HBM = 8.0e12
 # scaled by a 64 MiB copy: read = 2.0 x FETCH_SIZE, write = 1.0 x WRITE_SIZE);
 # profiles/yolov3_416_b16_conv_{nhwc,lean}_kernel.md hold the figures and commands.
 TRAFFIC_TAP3X3_B16 = {"conv_lean_kernel<tap3x3>": (2.0 * 168517.7 + 40664.9) * 1024,
-                      "conv_nhwc_kernel<tap3x3>": (2.0 * 69021.7 + 40194.6) * 1024}
+                      "conv_nhwc_kernel<tap3x3>": (2.0 * 68422.7 + 39756.1) * 1024}
 
 
 def log(*a):
