@@ -132,16 +132,54 @@ def profile_kernels(hip, net, layers, x, reps=3):
     return stats
 
 
+CPU_SHARE = 16  # host CPUs the GPU pool grants one GPU's jobs (worker pools are sized to it)
+
+
+def host_cpus():
+    """What the host offers the CPU baseline: nproc (online CPUs), the CPUs
+    this process may run on (affinity, cut by a cgroup CPU quota), and the
+    CPU model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = nproc
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            avail = min(avail, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return nproc, avail, model
+
+
+def baseline_threads():
+    """P of the reference's worker pool: GetSystemThreadCount =
+    max(TThread.ProcessorCount, 4) (steroids.pas:281-296), with the processor
+    count taken as the CPUs this process may use, bounded by the pool's
+    per-GPU share (threads beyond the CPUs available only time-slice)."""
+    nproc, avail, model = host_cpus()
+    return max(min(avail, CPU_SHARE), 4), nproc, avail, model
+
+
 def cpu_baseline(layers, weights, budget_s=12.0):
     """Oracle YOLOv3-416 forward at batch 1 on the host cores, repeated until
-    ~budget_s of work; returns (img/s, threads, images)."""
+    ~budget_s of work; returns (img/s, threads, images, host description)."""
     import numpy as np
 
     from oracle import netref
     from oracle import refcpu as R
     from tensorium_amd import synth
 
-    threads = min(16, os.cpu_count() or 4)
+    threads, nproc, avail, model = baseline_threads()
     R.set_threads(threads)
     x = synth.uniform(7, (1, 3, 416, 416))
     netref.forward(layers, weights, x)  # warm-up
@@ -153,7 +191,7 @@ def cpu_baseline(layers, weights, budget_s=12.0):
             break
     dt = time.perf_counter() - t0
     del np
-    return n / dt, threads, n
+    return n / dt, threads, n, {"nproc": nproc, "cpus_available": avail, "cpu_model": model, "P": threads}
 
 
 COPY_BYTES = 64 << 20
@@ -220,47 +258,74 @@ def extra_single_conv(hip):
 
     for _ in range(3):
         fn()
-    ms = time_events(hip, fn, 50)
+    eager = time_events(hip, fn, 50)
+    ms = time_graph(hip, fn, 50)
     flop = 2.0 * 16 * 27 * 416 * 416
     byts = 4.0 * (3 * 416 * 416 + 16 * 416 * 416 + 16 * 27)
     del np
-    return {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "us": round(ms * 1e3, 2),
+    return {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "launch": "hip_graph",
+            "us": round(ms * 1e3, 2), "us_eager": round(eager * 1e3, 2),
             "gflops": round(flop / ms / 1e6, 1), "gb_s": round(byts / ms / 1e6, 1),
             "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4)}
 
 
+SGEMM_SQUARES = (512, 1024, 2048, 4096, 8192)
+# the conv-shaped skinny GEMMs of config 2: M = F, N = OH*OW*16, K = 9*C
+SGEMM_SKINNY = ((64, 692224, 288), (128, 173056, 576), (256, 43264, 1152), (512, 10816, 2304),
+                (1024, 2704, 4608))
+
+
 def extra_sgemm(hip):
-    """Config 2: C = op(A)*op(B) (beta 0), A and B ~ U[-1, 1): NN at 512^3 ..
-    8192^3, the four variants at 4096^3 and the YOLOv3 conv-shaped skinny
-    GEMMs, each timed as a graph replay after the first (tuning) call."""
+    """Config 2: C = alpha*op(A)*op(B) + beta*C with A and B ~ U[-1, 1):
+    the four NN/NT/TN/TT variants at M = N = K in 512 .. 8192 (beta 0), the
+    conv-shaped skinny GEMMs (NN, beta 0) and one alpha = 0.5 / beta = 1 run
+    at 4096^3, each timed as a graph replay after the first (tuning) call.
+    Operands are cut from one seeded U[-1, 1) pool of 2^26 floats (copied
+    on the device where a matrix is larger)."""
     import torch
 
     from tensorium_amd import synth
 
-    cases = [("NN", 512, 512, 512), ("NN", 1024, 1024, 1024), ("NN", 2048, 2048, 2048),
-             ("NN", 4096, 4096, 4096), ("NT", 4096, 4096, 4096), ("TN", 4096, 4096, 4096),
-             ("TT", 4096, 4096, 4096), ("NN", 8192, 8192, 8192), ("NN", 64, 692224, 288),
-             ("NN", 256, 43264, 1152), ("NN", 1024, 2704, 4608)]
+    pool = torch.from_numpy(synth.uniform(11, (1 << 26,), -1, 1)).cuda()
+
+    def operand(n):
+        t = torch.empty(n, dtype=torch.float32, device="cuda")
+        for o in range(0, n, pool.numel()):
+            k = min(pool.numel(), n - o)
+            t[o:o + k].copy_(pool[:k])
+        return t
+
+    cases = [(v, n, n, n, 1.0, 0.0) for n in SGEMM_SQUARES for v in ("NN", "NT", "TN", "TT")]
+    cases += [("NN", M, N, K, 1.0, 0.0) for M, N, K in SGEMM_SKINNY]
+    cases += [("NN", 4096, 4096, 4096, 0.5, 1.0)]
     res = []
-    for var, M, N, K in cases:
+    bufs = {}
+    for var, M, N, K, alpha, beta in cases:
         ta, tb = var[0] == "T", var[1] == "T"
-        A = torch.from_numpy(synth.uniform(11, (M * K,), -1, 1)).cuda()
-        B = torch.from_numpy(synth.uniform(12, (K * N,), -1, 1)).cuda()
-        C = torch.empty(M * N, dtype=torch.float32, device="cuda")
+        key = (M, N, K)
+        if key not in bufs:
+            bufs.clear()
+            torch.cuda.empty_cache()
+            bufs[key] = (operand(M * K), operand(K * N), operand(M * N))
+        A, B, C = bufs[key]
         torch.cuda.synchronize()
         lda, ldb = (M if ta else K), (K if tb else N)
 
         def fn():
-            hip.gemm(ta, tb, M, N, K, 1.0, A, 0, lda, B, 0, ldb, 0.0, C, 0, N)
+            hip.gemm(ta, tb, M, N, K, alpha, A, 0, lda, B, 0, ldb, beta, C, 0, N)
 
         fn()
         reps = 3 if M * N * K >= 8192 ** 3 else (10 if M * N * K >= 1024 ** 3 else 50)
         ms = time_graph(hip, fn, reps)
-        res.append({"variant": var, "M": M, "N": N, "K": K, "ms": round(ms, 4),
-                    "tflops": round(2.0 * M * N * K / ms / 1e9, 2),
-                    "frac": round(2.0 * M * N * K / ms * 1e3 / PEAK_FP32_MFMA, 4)})
-        del A, B, C
-        torch.cuda.empty_cache()
+        r = {"variant": var, "M": M, "N": N, "K": K, "ms": round(ms, 4),
+             "tflops": round(2.0 * M * N * K / ms / 1e9, 2),
+             "frac": round(2.0 * M * N * K / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+        if alpha != 1.0 or beta != 0.0:
+            r.update(alpha=alpha, beta=beta)
+        res.append(r)
+    bufs.clear()
+    del pool
+    torch.cuda.empty_cache()
     return res
 
 
@@ -304,7 +369,8 @@ def extra_train(hip, steps, warmup, cpu_steps):
         from oracle import refcpu as R
         from oracle import trainref as T
 
-        R.set_threads(min(16, os.cpu_count() or 4))
+        threads, nproc, avail, model = baseline_threads()
+        R.set_threads(threads)
         ref = T.CifarStep(params)
         ref.step(x, truth)
         t0 = time.perf_counter()
@@ -312,7 +378,8 @@ def extra_train(hip, steps, warmup, cpu_steps):
             ref.step(x, truth)
         cms = (time.perf_counter() - t0) / cpu_steps * 1e3
         out["cpu_baseline"] = {"value": round(cms, 1), "unit": "ms/step", "cores": R.get_threads(), "kind": "port",
-                               "sample": f"{cpu_steps} oracle steps (C AVX2 GEMM/im2col/col2im + numpy BN/softmax)"}
+                               "sample": f"{cpu_steps} oracle steps (C AVX2 GEMM/im2col/col2im + numpy BN/softmax)",
+                               "nproc": nproc, "cpus_available": avail, "cpu_model": model, "P": threads}
     return out
 
 
@@ -332,6 +399,117 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
     torch.cuda.empty_cache()
     return {"workload": f"YOLOv3-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
             "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+
+
+def extra_batch1(hip, layers, weights, steps, warmup):
+    """YOLOv3-416 at batch 1 (the other half of the metric), HIP graph replay."""
+    import torch
+
+    from tensorium_amd import darknet, synth
+
+    net = darknet.Network(hip, layers, 1, weights, layout=layout_for(1))
+    x = torch.from_numpy(synth.uniform(7, (1, 3, 416, 416))).cuda()
+    torch.cuda.synchronize()
+    ms, _ = time_forward(hip, net, x, steps, warmup, graph=True)
+    ms /= steps
+    flop = darknet.conv_flops(layers)
+    del net, x
+    torch.cuda.empty_cache()
+    return {"workload": "YOLOv3-416 fp32 inference, batch 1", "ms_per_step": round(ms, 4),
+            "img_s": round(1e3 / ms, 2), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+
+
+def _bw_entry(name, ms, byts, copy_gbs):
+    gbs = byts / ms / 1e6
+    return {"kernel": name, "us": round(ms * 1e3, 2), "bytes": int(byts), "gb_s": round(gbs, 1),
+            "hbm_frac": round(gbs * 1e9 / PEAK_HBM, 4),
+            "copy_frac": None if copy_gbs is None else round(gbs / copy_gbs, 4)}
+
+
+def extra_bandwidth(hip):
+    """The memory-bound kernels of the path at config-3 and YOLOv3 sizes, each
+    timed as a graph replay: achieved GB/s of the algorithmic bytes
+    (compulsory fp32 reads + writes, 8-byte indices) against the 8 TB/s
+    datasheet peak and against a plain device copy measured in the same run."""
+    import torch
+
+    from tensorium_amd import synth
+    from tensorium_amd.nnhip import acLEAKY
+
+    def dev(shape, seed, dtype=torch.float32):
+        t = torch.from_numpy(synth.uniform(seed, shape, -1, 1)).cuda()
+        return t if dtype == torch.float32 else t.to(dtype)
+
+    out = []
+    n = 64 << 20  # floats: a 256 MiB copy
+    src, dst = dev((n,), 1), torch.empty(n, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ms = time_graph(hip, lambda: hip.copy(n, src, 0, 1, dst, 0, 1), 20)
+    copy_gbs = 8.0 * n / ms / 1e6
+    out.append(_bw_entry("copy 256 MiB", ms, 8.0 * n, None))
+    del src, dst
+
+    def im2col_case(label, B, C, H, k, p, s):
+        OH = (H + 2 * p - k) // s + 1
+        x = dev((B, C, H, H), 2)
+        col = torch.empty(B * C * k * k * OH * OH, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        t = time_graph(hip, lambda: hip.im2colStridedBatched(C, H, H, k, k, p, p, s, s, 1, 1, x, C * H * H, 0, col,
+                                                             C * k * k * OH * OH, 0, B), 20)
+        out.append(_bw_entry(f"im2col {label} B{B} C{C} {H}x{H} k{k}", t,
+                             4.0 * B * (C * H * H + C * k * k * OH * OH), copy_gbs))
+        t = time_graph(hip, lambda: hip.col2imStridedBatched(C, H, H, k, k, p, p, s, s, 1, 1, col,
+                                                             C * k * k * OH * OH, 0, x, C * H * H, 0, B), 20)
+        out.append(_bw_entry(f"col2im {label} B{B} C{C} {H}x{H} k{k}", t,
+                             4.0 * B * (C * k * k * OH * OH + 2 * C * H * H), copy_gbs))
+
+    im2col_case("config-3 conv2", 128, 32, 16, 3, 1, 1)
+    im2col_case("config-3 conv3", 128, 64, 8, 3, 1, 1)
+    im2col_case("yolov3 52x52", 16, 128, 52, 3, 1, 1)
+
+    def pool_case(label, B, C, H):
+        OH = H // 2
+        x = dev((B, C, H, H), 3)
+        y = torch.empty((B, C, OH, OH), dtype=torch.float32, device="cuda")
+        idx = torch.empty((B, C, OH, OH), dtype=torch.int64, device="cuda")
+        dIn = torch.zeros((B, C, H, H), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        t = time_graph(hip, lambda: hip.forwardMaxPool(B, C, OH, OH, x, C, H, H, 2, 2, 0, 2, idx, y), 20)
+        out.append(_bw_entry(f"maxpool fwd {label} B{B} C{C} {H}x{H} 2/2 +idx", t,
+                             4.0 * B * C * (H * H + OH * OH) + 8.0 * B * C * OH * OH, copy_gbs))
+        t = time_graph(hip, lambda: hip.backwardMaxPool(B, C, OH, OH, dIn, idx, y), 20)
+        # dOut + indices read, and the touched (one per window) dIn elements read and written
+        out.append(_bw_entry(f"maxpool bwd {label} B{B} C{C} {H}x{H} 2/2", t,
+                             (4.0 + 8.0 + 8.0) * B * C * OH * OH, copy_gbs))
+
+    pool_case("config-3 pool1", 128, 32, 32)
+    pool_case("config-3 pool2", 128, 64, 16)
+
+    def up_case(label, B, C, H):
+        x = dev((B, C, H, H), 4)
+        y = torch.empty((B, C, 2 * H, 2 * H), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        t = time_graph(hip, lambda: hip.upSample(B, C, H, H, x, 2, 1, 1.0, y), 20)
+        out.append(_bw_entry(f"upsample fwd {label} B{B} C{C} {H}->{2 * H}", t, 4.0 * B * C * H * H * 5, copy_gbs))
+
+    up_case("yolov3-416 first", 16, 256, 13)
+    up_case("yolov3-416 second", 16, 128, 26)
+
+    B, F, Hh = 128, 32, 32
+    nel = B * F * Hh * Hh
+    y = dev((B, F, Hh, Hh), 5)
+    b = dev((F,), 6)
+    torch.cuda.synchronize()
+
+    def bias_leaky():
+        hip.forwardBias(nel, y, 0, F, b, 1, B)
+        hip.ActivateArray(nel, y, 0, acLEAKY)
+
+    t = time_graph(hip, bias_leaky, 20)
+    out.append(_bw_entry(f"bias + leaky (unfused, 2 passes) B{B} C{F} {Hh}x{Hh}", t, 2 * 8.0 * nel, copy_gbs))
+    del y, b
+    torch.cuda.empty_cache()
+    return {"copy_gb_s": round(copy_gbs, 1), "kernels": out}
 
 
 def extra_detect(hip, layers, weights, batch=16, thresh=0.5, nms=0.45):
@@ -415,6 +593,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the other BASELINE configurations (single conv, SGEMM sweep, training step, "
                          "YOLOv3-608 batch 32)")
+    ap.add_argument("--only", choices=("single_conv_416", "sgemm", "train_cifar_b128", "yolov3_608_b32",
+                                       "yolo_detect_nms_b16", "bandwidth", "batch1"), default=None,
+                    help="run one secondary configuration alone and print its figures (for profiling runs)")
     ap.add_argument("--counter-pass", action="store_true",
                     help="for rocprofv3 --pmc: tune, then run ONE eager forward and a 64 MiB copy "
                          "(the calibration kernel), print nothing else")
@@ -444,6 +625,19 @@ def main():
 
     if args.counter_pass:
         counter_pass(hip, darknet.Network(hip, layers, args.batch, weights, layout=layout_for(args.batch)), args)
+        return
+    if args.only:
+        only = {
+            "single_conv_416": lambda: extra_single_conv(hip),
+            "sgemm": lambda: extra_sgemm(hip),
+            "train_cifar_b128": lambda: extra_train(hip, args.steps, args.warmup, 0),
+            "yolov3_608_b32": lambda: extra_yolo(hip, darknet.load_cfg("yolov3.cfg", 608, 608)[1], weights,
+                                                 args.steps, args.warmup),
+            "yolo_detect_nms_b16": lambda: extra_detect(hip, layers, weights),
+            "bandwidth": lambda: extra_bandwidth(hip),
+            "batch1": lambda: extra_batch1(hip, layers, weights, args.steps, args.warmup),
+        }[args.only]
+        print(json.dumps({args.only: only()}), flush=True)
         return
 
     def run(batch, steps, warmup):
@@ -480,11 +674,13 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        v, threads, n = cpu_baseline(layers, weights, args.cpu_budget)
+        v, threads, n, hostd = cpu_baseline(layers, weights, args.cpu_budget)
         cpu = {"value": round(v, 4), "unit": "img/s", "cores": threads, "kind": "port",
                "sample": f"YOLOv3-416 batch-1 forward x{n} on the CPU oracle (C AVX2+FMA restatement of the "
-                         f"reference path, {threads} threads, BN folded)"}
-        log(f"cpu baseline: {v:.3f} img/s on {threads} threads")
+                         f"reference path, P = {threads} worker threads, BN folded); measured at batch 1, "
+                         f"not extrapolated",
+               **hostd}
+        log(f"cpu baseline: {v:.3f} img/s on {threads} threads ({hostd})")
 
     extras = None
     if not args.no_extras:
@@ -506,6 +702,7 @@ def main():
         _, l608 = darknet.load_cfg("yolov3.cfg", 608, 608)
         guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2))
         guarded("yolo_detect_nms_b16", lambda: extra_detect(hip, layers, weights))
+        guarded("bandwidth", lambda: extra_bandwidth(hip))
 
     out = {
         "metric": METRIC,

@@ -344,13 +344,46 @@ int32_t tnh_yolo_nms_sort(int64_t batch, int64_t classes, int64_t capacity,
                           const float *boxes, float *prob,
                           const int32_t *counts, float thresh);
 
-/* ---- batch norm (inference, unfused) ----------------------------------- */
-/* TNNCuda.normalize (nncuda.pas:1371) with the CPU clamp of _snormblkvv
- * (ntensors.pas:4357): x = (x - mean[f]) / max(sqrt(var[f]), 1e-6), IEEE
- * division; blockSize = dstSize/(N*batch). */
+/* ---- batch norm --------------------------------------------------------- */
+/* TNNCuda.normalize (nncuda.pas:1371, called by TBaseLayer.batchNormGPU
+ * nbaselayer.pas:620, 632): dst[dstOffset ..] viewed as [groups][srcSize]
+ * [blockSize], blockSize = dstSize/(srcSize*groups), normalized per channel
+ * i with the CPU semantics of TTensor.blockNormalize (ntensors.pas:8693):
+ * x = (x - means[i*meansStride]) / d, IEEE division, with
+ * d = max(sqrt(v), 1e-6) (_snormblkvv :4357) when blockSize > 1 and
+ * d = sqrt(max(v, 1e-6)) (_snormvv :4338) when blockSize == 1,
+ * v = vars[i*varsStride].  (The reference CUDA kernel clamps the variance
+ * in both cases; the CPU path is the parity target.) */
+int32_t tnh_normalize(int64_t srcSize, int64_t dstSize, int64_t groups,
+                      const float *means, int64_t meansStride,
+                      const float *vars, int64_t varsStride, float *dst,
+                      int64_t dstOffset);
+/* TTensor.blockNormalize (ntensors.pas:8693-8718) in the argument order of
+ * tnh_forward_bias: the same normalize over dst[offset ..] viewed as
+ * [batch][N][dstSize/(N*batch)], unit-stride statistics. */
 int32_t tnh_bn_normalize(int64_t dstSize, float *x, int64_t offset, int64_t N,
                          const float *mean, const float *variance,
                          int64_t batch);
+/* TNNCuda.forwardScaleAdd (nncuda.pas:1490): dst[offset+i] =
+ * fl(scales[f*incb] * dst[offset+i]) + biases[f*incb], f = (i/blockSize) %
+ * scaleSize, blockSize = dstSize/(scaleSize*batch): the two roundings of the
+ * CPU sequence forwardScale then forwardBias (nbaselayer.pas:366-367). */
+int32_t tnh_forward_scale_add(int64_t dstSize, float *dst, int64_t offset,
+                              int64_t scaleSize, const float *scales,
+                              const float *biases, int64_t incb,
+                              int64_t batch);
+/* No reference counterpart: the batch-norm forward of TBaseLayer.batchNorm
+ * (nbaselayer.pas:335-368) after the statistics, and the layer's
+ * activation, in one pass over x [batch][N][block]:
+ *   xNorm = (x - mean[f]) / d          (tnh_bn_normalize's arithmetic)
+ *   out   = act(fl(scales[f] * xNorm) + biases[f])
+ * xNorm may be NULL (inference with rolling statistics).  Bit-identical to
+ * the reference's copy / blockNormalize / copy / forwardScale /
+ * forwardBias / activate sequence; x, xNorm and out must not overlap. */
+int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch,
+                       const float *x, float *xNorm, float *out,
+                       const float *mean, const float *variance,
+                       const float *scales, const float *biases, int32_t act);
 
 /* ---- training direction (config-3 step: conv-BN-leaky, pooling,
  *      connected, softmax cross-entropy, SGD) --------------------------- */
@@ -361,6 +394,16 @@ int32_t tnh_bn_normalize(int64_t dstSize, float *x, int64_t offset, int64_t N,
 int32_t tnh_means_vars(int64_t srcSize, int64_t dstSize, int64_t groups,
                        const float *src, int64_t offset, float *means,
                        float *vars);
+/* No reference counterpart: tnh_means_vars followed by the rolling-statistics
+ * update of TBaseLayer.batchNorm in training (nbaselayer.pas:351-355:
+ * rolling.Multiply(1 - momentum), then rolling.axpy(momentum, stat)), in
+ * one call: rollingMeans[i] = fma(momentum, means[i], (1 - momentum) *
+ * rollingMeans[i]), likewise the variances; bit-identical to tnh_means_vars,
+ * tnh_scale and tnh_axpy in sequence.  The rolling buffers may both be NULL. */
+int32_t tnh_bn_statistics(int64_t srcSize, int64_t dstSize, int64_t groups,
+                          const float *src, int64_t offset, float *means,
+                          float *vars, float *rollingMeans, float *rollingVars,
+                          float momentum);
 /* TNNCuda.meansAndVarsDelta (nncuda.pas:1398) / sMeanAndVarianceDelta
  * (ntensors.pas:8831-8898): mean_delta[i] = sum(delta) * -1/sqrt(max(var,
  * 1e-6)); variance_delta[i] = sum(delta*(x-mean)) * -0.5 *

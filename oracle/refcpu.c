@@ -513,6 +513,10 @@ void ref_maxpool_fwd(int64_t batch, int64_t C, int64_t H, int64_t W,
 void ref_maxpool_bwd(int64_t nOut, const int64_t *idx, const float *dOut, float *dIn) {
   for (int64_t i = 0; i < nOut; ++i) {
     int64_t index = idx[i];
+    /* index -1 marks a window with no tap above -MaxSingle (all -inf or
+     * outside the image); the reference's serial loop would add into
+     * dIn[-1], outside the tensor.  Skipped here, as on the device. */
+    if (index < 0) continue;
     dIn[index] = dIn[index] + dOut[i];
   }
 }
@@ -546,11 +550,26 @@ void ref_addvv(int64_t n, const float *a, const float *b, float *out) {
 void ref_bn_normalize(float *x, int64_t nb, int64_t blockSize,
                       const float *mean, const float *var, int64_t batch,
                       int exact) {
+  /* TTensor.blockNormalize (ntensors.pas:8693-8718): one element per channel
+   * goes through normvv = _snormvv (:4338), which clamps the variance,
+   * (x - m) / sqrt(max(v, 1e-6)), exact division; longer blocks through
+   * normblkvv = _snormblkvv (:4357), which clamps the standard deviation,
+   * max(sqrt(v), 1e-6), and on AVX2 hosts multiplies by rcpss of it. */
+  if (blockSize == 1) {
+    for (int64_t g = 0; g < batch; ++g)
+      for (int64_t i = 0; i < nb; ++i) {
+        float v = var[i] > 1e-6f ? var[i] : 1e-6f; /* Max(v, sEPSILON) */
+        float d = sqrtf(v);
+        float t = x[g * nb + i] - mean[i];
+        x[g * nb + i] = t / d;
+      }
+    return;
+  }
   for (int64_t g = 0; g < batch; ++g)
     for (int64_t i = 0; i < nb; ++i) {
       float *o = x + (g * nb + i) * blockSize;
       float d = sqrtf(var[i]);
-      if (d < 1e-6f) d = 1e-6f; /* math.Max(d, sEPSILON), sEPSILON = 1e-6 */
+      if (!(d > 1e-6f)) d = 1e-6f; /* math.Max(d, sEPSILON) = d > eps ? d : eps, sEPSILON = 1e-6 */
       float m = mean[i];
       if (exact) {
         for (int64_t j = 0; j < blockSize; ++j) o[j] = (o[j] - m) / d;

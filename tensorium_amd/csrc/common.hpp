@@ -28,7 +28,14 @@ struct Context {
   // Outgrown scratch buffers: a graph captured earlier may still launch
   // kernels that address them, so they are freed only by tnh_finalize.
   std::vector<void*> wsRetired;
+  // Partial sums of the multi-workgroup channel reductions (batch-norm
+  // statistics and their deltas, weight-gradient split sums): allocated by
+  // tnh_init, so calls made under graph capture find it.
+  float* red = nullptr;
+  int64_t redFloats = 0;
 };
+
+constexpr int64_t kRedFloats = int64_t(1) << 20;  // 4 MiB of reduction partials
 
 // Returns a scratch buffer of at least `bytes` on the context device, growing
 // it (a new hipMalloc; the outgrown buffer stays allocated until

@@ -123,6 +123,7 @@ extern "C" int32_t tnh_init(int32_t device) {
     (void)hipStreamSynchronize(g_ctx.stream);
     if (g_ctx.ws) (void)hipFree(g_ctx.ws);
     for (void* p : g_ctx.wsRetired) (void)hipFree(p);
+    if (g_ctx.red) (void)hipFree(g_ctx.red);
     (void)hipStreamDestroy(g_ctx.own_stream);
     (void)hipStreamDestroy(g_ctx.tune_stream);
     g_ctx = Context{};
@@ -135,6 +136,12 @@ extern "C" int32_t tnh_init(int32_t device) {
     (void)hipStreamDestroy(s);
     return st;
   }
+  float* red = nullptr;
+  if (int st = hip_status(hipMalloc(&red, kRedFloats * 4), "hipMalloc(reduction partials)")) {
+    (void)hipStreamDestroy(s);
+    (void)hipStreamDestroy(ts);
+    return st;
+  }
   int cus = 0;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
   g_ctx.device = device;
@@ -142,6 +149,8 @@ extern "C" int32_t tnh_init(int32_t device) {
   g_ctx.stream = s;
   g_ctx.tune_stream = ts;
   g_ctx.cu_count = cus > 0 ? cus : 256;
+  g_ctx.red = red;
+  g_ctx.redFloats = kRedFloats;
   g_live = true;
   return TNH_OK;
 }
@@ -153,6 +162,7 @@ extern "C" int32_t tnh_finalize(void) {
   (void)hipStreamSynchronize(g_ctx.stream);
   if (g_ctx.ws) (void)hipFree(g_ctx.ws);
   for (void* p : g_ctx.wsRetired) (void)hipFree(p);
+  if (g_ctx.red) (void)hipFree(g_ctx.red);
   (void)hipStreamDestroy(g_ctx.own_stream);
   (void)hipStreamDestroy(g_ctx.tune_stream);
   g_ctx = Context{};

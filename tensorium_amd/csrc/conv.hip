@@ -850,21 +850,27 @@ float cost(const CfgInfo& c, int64_t F, int64_t N, int64_t K, int cus, int split
   return mm + red;
 }
 
+// Everything a cached choice depends on: the GEMM shape, the layout, the
+// operand alignment, whether a residual is read, and whether out, residual
+// and one split's partial sums lie within 2 GiB (smallIO: the lean kernels
+// address them through 2 GiB buffer resources).
 struct TuneKey {
   int64_t F, N, K, C, H, W;
   int k, s, mode, va, vb;
   int nhwc, xPix, outPix, resPix;
+  int hasRes, smallIO;
   bool operator==(const TuneKey& o) const {
     return F == o.F && N == o.N && K == o.K && C == o.C && H == o.H && W == o.W && k == o.k && s == o.s &&
            mode == o.mode && va == o.va && vb == o.vb && nhwc == o.nhwc && xPix == o.xPix && outPix == o.outPix &&
-           resPix == o.resPix;
+           resPix == o.resPix && hasRes == o.hasRes && smallIO == o.smallIO;
   }
 };
 struct TuneHash {
   size_t operator()(const TuneKey& t) const {
     size_t h = 1469598103934665603ull;
     for (int64_t v : {t.F, t.N, t.K, t.C, t.H, t.W, (int64_t)t.k, (int64_t)t.s, (int64_t)t.mode, (int64_t)t.va,
-                      (int64_t)t.vb, (int64_t)t.nhwc, (int64_t)t.xPix, (int64_t)t.outPix, (int64_t)t.resPix})
+                      (int64_t)t.vb, (int64_t)t.nhwc, (int64_t)t.xPix, (int64_t)t.outPix, (int64_t)t.resPix,
+                      (int64_t)t.hasRes, (int64_t)t.smallIO})
       h = (h ^ static_cast<size_t>(v)) * 1099511628211ull;
     return h;
   }
@@ -977,7 +983,7 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
       return run({c, hi > 1 ? hi : 1, 0, 0});
     }
     auto it = g_tuned.find(key);
-    if (it != g_tuned.end()) return run(it->second);
+    if (it != g_tuned.end() && cfg_valid(it->second.cfg, mode, C, va, smallIO, nhwc)) return run(it->second);
     if (g_autotune && !aliased) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
       if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
@@ -1100,7 +1106,7 @@ extern "C" int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int6
   TNH_ARG(va && smallIO && C % 32 == 0,
           "conv2d_nhwc: needs C %% 32 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
   const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, false, 1, (int)xPix, (int)outPix,
-                    residual ? (int)rPix : 0};
+                    residual ? (int)rPix : 0, residual != nullptr, smallIO};
   return conv_dispatch(cx, a, mode, va, false, smallIO, true, key);
 }
 
@@ -1209,6 +1215,6 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
                                                    : launch_smallc<false, false>(a, cx->stream);
   }
 
-  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, vb, 0, 0, 0, 0};
+  const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, vb, 0, 0, 0, 0, residual != nullptr, smallIO};
   return conv_dispatch(cx, a, mode, va, vb, smallIO, false, key);
 }

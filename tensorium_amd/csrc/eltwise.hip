@@ -17,19 +17,176 @@ unsigned grid_for(int64_t n) {
 #define GRID_STRIDE(i, n) \
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < (n); i += int64_t(gridDim.x) * blockDim.x)
 
-// vsAddB (ntensors.pas:4066) / forward_bias: x += bias[(i / block) % nb]
-__global__ void bias_kernel(float* x, int64_t n, int64_t block, int64_t nb, const float* b, int64_t incb) {
-  GRID_STRIDE(i, n) {
-    const int64_t f = (i / block) % nb;
-    x[i] = b[f * incb] + x[i];
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---------------------------------------------------------------------------
+// Per-channel passes.  A tensor [groups][nb][block] is walked as rows of
+// `block` contiguous floats; row r belongs to channel r % nb.  The channel's
+// constants are loaded once per row, so the element loop holds no index
+// division, and a row is read and written 16 bytes at a time when block % 4
+// == 0 and the base is 16-byte aligned.  A workgroup pass covers rpw rows of
+// cpt threads each (short rows share a workgroup; long rows loop over their
+// chunks).
+struct Rows {
+  int64_t rows, block, nb;
+  int64_t cpr;  // VW-wide chunks per row
+  int cpt;      // threads per row in one pass
+  int rpw;      // rows per workgroup pass
+};
+
+Rows make_rows(int64_t n, int64_t block, int64_t nb, int vw) {
+  Rows g;
+  g.rows = n / block;
+  g.block = block;
+  g.nb = nb;
+  g.cpr = block / vw;
+  g.cpt = static_cast<int>(g.cpr < kThreads ? g.cpr : kThreads);
+  g.rpw = kThreads / g.cpt;
+  return g;
+}
+
+unsigned grid_rows(const Rows& g) {
+  const int64_t b = (g.rows + g.rpw - 1) / g.rpw;
+  return static_cast<unsigned>(b < 16384 ? (b > 0 ? b : 1) : 16384);
+}
+
+template <class Op>
+__device__ inline float4 map4(const Op& op, const typename Op::Ch& c, float4 v) {
+  return make_float4(op(c, v.x), op(c, v.y), op(c, v.z), op(c, v.w));
+}
+
+// x = op(channel constants, x) in place
+template <int VW, class Op>
+__global__ __launch_bounds__(kThreads) void rows_kernel(Op op, float* __restrict__ x, Rows g) {
+  const int t = threadIdx.x, lr = t / g.cpt, lc = t - lr * g.cpt;
+  if (lr >= g.rpw) return;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * g.rpw + lr; r < g.rows;
+       r += static_cast<int64_t>(gridDim.x) * g.rpw) {
+    const typename Op::Ch c = op.chan(r % g.nb);
+    float* row = x + r * g.block;
+    for (int64_t k = lc; k < g.cpr; k += g.cpt) {
+      if constexpr (VW == 4) {
+        float4* p = reinterpret_cast<float4*>(row) + k;
+        *p = map4(op, c, *p);
+      } else {
+        row[k] = op(c, row[k]);
+      }
+    }
   }
 }
 
-__global__ void scale_blk_kernel(float* x, int64_t n, int64_t block, int64_t nb, const float* s, int64_t incb) {
-  GRID_STRIDE(i, n) {
-    const int64_t f = (i / block) % nb;
-    x[i] = s[f * incb] * x[i];
+// vsAddB (ntensors.pas:4066) / forward_bias: x = bias[f] + x
+struct BiasOp {
+  const float* b;
+  int64_t inc;
+  struct Ch { float b; };
+  __device__ Ch chan(int64_t f) const { return {b[f * inc]}; }
+  __device__ float operator()(const Ch& c, float x) const { return c.b + x; }
+};
+
+// vsMulB (ntensors.pas:4112) / forward_scale: x = scale[f] * x
+struct ScaleOp {
+  const float* s;
+  int64_t inc;
+  struct Ch { float s; };
+  __device__ Ch chan(int64_t f) const { return {s[f * inc]}; }
+  __device__ float operator()(const Ch& c, float x) const { return c.s * x; }
+};
+
+// forwardScale then forwardBias (nbaselayer.pas:366-367), two roundings:
+// x = fl(scale[f] * x) + bias[f]
+struct ScaleAddOp {
+  const float* s;
+  const float* b;
+  int64_t inc;
+  struct Ch { float s, b; };
+  __device__ Ch chan(int64_t f) const { return {s[f * inc], b[f * inc]}; }
+  __device__ float operator()(const Ch& c, float x) const {
+    const float u = c.s * x;
+    return c.b + u;
   }
+};
+
+// The CPU normalize of TTensor.blockNormalize (ntensors.pas:8693-8718) with
+// IEEE division: x = (x - mean[f]) / d with d = max(sqrt(var[f]), 1e-6)
+// (_snormblkvv, :4357, blocks of more than one element) or d =
+// sqrt(max(var[f], 1e-6)) (_snormvv, :4338, one element per channel).
+// Pascal's Max(a, b) = a > b ? a : b, so a NaN variance gives d = 1e-6.
+struct NormOp {
+  const float* m;
+  int64_t ms;
+  const float* v;
+  int64_t vs;
+  int clampVar;
+  struct Ch { float m, d; };
+  __device__ Ch chan(int64_t f) const {
+    const float var = v[f * vs];
+    float d;
+    if (clampVar) {
+      d = sqrtf(var > 1e-6f ? var : 1e-6f);
+    } else {
+      d = sqrtf(var);
+      d = d > 1e-6f ? d : 1e-6f;
+    }
+    return {m[f * ms], d};
+  }
+  __device__ float operator()(const Ch& c, float x) const {
+    const float t = x - c.m;
+    return t / c.d;
+  }
+};
+
+__device__ inline float act_fwd(float v, int act) {
+  if (act == TNH_AC_LEAKY) return 0.f > v ? 0.1f * v : v;  // leaky_array (nactivation.pas:234-268)
+  if (act == TNH_AC_LOGISTIC) return 1.f / (1.f + expf(-v));
+  return v;
+}
+
+
+// Batch norm forward of TBaseLayer.batchNorm (nbaselayer.pas:335-368) and
+// the layer's activation in one pass: xn = (x - mean) / d (NormOp), out =
+// act(fl(scale * xn) + bias); xNorm may be NULL (inference statistics).
+// Bit-identical to the reference's separate copy / normalize / copy / scale /
+// bias / activate passes.
+template <int VW, int ACT>
+__global__ __launch_bounds__(kThreads) void bn_fwd_kernel(NormOp norm, ScaleAddOp sa, const float* __restrict__ x,
+                                                          float* __restrict__ xNorm, float* __restrict__ out,
+                                                          Rows g) {
+  const int t = threadIdx.x, lr = t / g.cpt, lc = t - lr * g.cpt;
+  if (lr >= g.rpw) return;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * g.rpw + lr; r < g.rows;
+       r += static_cast<int64_t>(gridDim.x) * g.rpw) {
+    const int64_t f = r % g.nb;
+    const NormOp::Ch cn = norm.chan(f);
+    const ScaleAddOp::Ch cs = sa.chan(f);
+    const int64_t base = r * g.block;
+    for (int64_t k = lc; k < g.cpr; k += g.cpt) {
+      if constexpr (VW == 4) {
+        const float4 n = map4(norm, cn, reinterpret_cast<const float4*>(x + base)[k]);
+        if (xNorm) reinterpret_cast<float4*>(xNorm + base)[k] = n;
+        const float4 o = map4(sa, cs, n);
+        reinterpret_cast<float4*>(out + base)[k] =
+            make_float4(act_fwd(o.x, ACT), act_fwd(o.y, ACT), act_fwd(o.z, ACT), act_fwd(o.w, ACT));
+      } else {
+        const float n = norm(cn, x[base + k]);
+        if (xNorm) xNorm[base + k] = n;
+        out[base + k] = act_fwd(sa(cs, n), ACT);
+      }
+    }
+  }
+}
+
+// Launches op over [groups][nb][block] at dst (n floats).
+template <class Op>
+int launch_rows(Op op, float* dst, int64_t n, int64_t block, int64_t nb, hipStream_t s, const char* name) {
+  if (block % 4 == 0 && al16(dst)) {
+    const Rows g = make_rows(n, block, nb, 4);
+    hipLaunchKernelGGL((rows_kernel<4, Op>), dim3(grid_rows(g)), dim3(kThreads), 0, s, op, dst, g);
+  } else {
+    const Rows g = make_rows(n, block, nb, 1);
+    hipLaunchKernelGGL((rows_kernel<1, Op>), dim3(grid_rows(g)), dim3(kThreads), 0, s, op, dst, g);
+  }
+  return launch_status(name);
 }
 
 // backward_bias: dst[f] += sum over (b, j) of src[(b*nb + f)*block + j];
@@ -52,25 +209,38 @@ __global__ __launch_bounds__(256) void backward_bias_kernel(float* dst, int64_t 
   if (threadIdx.x == 0) dst[f] = dst[f] + part[0];
 }
 
-__device__ inline float act_fwd(float v, int act) {
-  if (act == TNH_AC_LEAKY) return 0.f > v ? 0.1f * v : v;  // leaky_array (nactivation.pas:234-268)
-  if (act == TNH_AC_LOGISTIC) return 1.f / (1.f + expf(-v));
-  return v;
-}
-
 __global__ void activate_kernel(float* x, int64_t n, int act) {
   GRID_STRIDE(i, n) x[i] = act_fwd(x[i], act);
 }
 
+// 16 bytes per thread (n4 float4s at a 16-byte aligned base)
+template <int ACT>
+__global__ void activate4_kernel(float4* x, int64_t n4) {
+  GRID_STRIDE(i, n4) {
+    const float4 v = x[i];
+    x[i] = make_float4(act_fwd(v.x, ACT), act_fwd(v.y, ACT), act_fwd(v.z, ACT), act_fwd(v.w, ACT));
+  }
+}
+
+__device__ inline float act_grad(float v, int act) {
+  if (act == TNH_AC_LEAKY) return v > 0.f ? 1.f : 0.1f;
+  if (act == TNH_AC_LOGISTIC) return (1.f - v) * v;
+  return 1.f;
+}
+
+template <int ACT>
+__global__ void derive4_kernel(const float4* x, int64_t n4, float4* delta) {
+  GRID_STRIDE(i, n4) {
+    const float4 v = x[i];
+    const float4 d = delta[i];
+    delta[i] = make_float4(d.x * act_grad(v.x, ACT), d.y * act_grad(v.y, ACT), d.z * act_grad(v.z, ACT),
+                           d.w * act_grad(v.w, ACT));
+  }
+}
+
 // gradient_array: leaky_gradient (nactivation.pas:472-476); logistic y(1-y)
 __global__ void derive_kernel(const float* x, int64_t n, int act, float* delta) {
-  GRID_STRIDE(i, n) {
-    const float v = x[i];
-    float g = 1.f;
-    if (act == TNH_AC_LEAKY) g = v > 0.f ? 1.f : 0.1f;
-    if (act == TNH_AC_LOGISTIC) g = (1.f - v) * v;
-    delta[i] = delta[i] * g;
-  }
+  GRID_STRIDE(i, n) delta[i] = delta[i] * act_grad(x[i], act);
 }
 
 __global__ void addvv_kernel(int64_t n, const float* a, int64_t ia, const float* b, int64_t ib, float* c, int64_t ic) {
@@ -126,18 +296,6 @@ __global__ void route_kernel(RouteArgs r, float* dst, int64_t perImage) {
   }
 }
 
-// _snormblkvv with IEEE division (ntensors.pas:4357, snormvss :4315):
-// x = (x - m) / max(sqrt(v), 1e-6)
-__global__ void bn_norm_kernel(float* x, int64_t n, int64_t block, int64_t nb, const float* mean, const float* var) {
-  GRID_STRIDE(i, n) {
-    const int64_t f = (i / block) % nb;
-    float d = sqrtf(var[f]);
-    d = d > 1e-6f ? d : 1e-6f;
-    const float t = x[i] - mean[f];
-    x[i] = t / d;
-  }
-}
-
 // logistic_array's exp approximation (nactivation.pas:36-127), IEEE reciprocal
 __device__ inline float logistic_poly(float x) {
   const float l2e = 1.442695041f, c0 = 1.00172476f, c1 = 0.657636276f, c2 = 0.3371894346f;
@@ -163,8 +321,6 @@ __global__ void yolo_kernel(int64_t total, int64_t HW, int64_t entries, const fl
     out[e] = (entry == 2 || entry == 3) ? v : logistic_poly(v);
   }
 }
-
-bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // TYoloLayer.forward on a channels-last head (pixel stride inPix) into the
 // NCHW head layout [b][ch][y][x] the detection decoder reads: 32 pixels x 32
@@ -224,9 +380,7 @@ extern "C" int32_t tnh_forward_bias(int64_t dstSize, float* dst, int64_t offset,
   TNH_ARG(dst && src, "forward_bias: NULL buffer");
   const int64_t block = dstSize / (srcSize * batch);
   TNH_ARG(block * srcSize * batch == dstSize, "forward_bias: sizes do not align");
-  hipLaunchKernelGGL(bias_kernel, dim3(grid_for(dstSize)), dim3(kThreads), 0, cx->stream, dst + offset, dstSize, block,
-                     srcSize, src, incb);
-  return launch_status("bias_kernel");
+  return launch_rows(BiasOp{src, incb}, dst + offset, dstSize, block, srcSize, cx->stream, "rows_kernel<bias>");
 }
 
 extern "C" int32_t tnh_forward_scale(int64_t dstSize, float* dst, int64_t offset, int64_t scaleSize,
@@ -237,9 +391,8 @@ extern "C" int32_t tnh_forward_scale(int64_t dstSize, float* dst, int64_t offset
   TNH_ARG(dst && scale, "forward_scale: NULL buffer");
   const int64_t block = dstSize / (scaleSize * batch);
   TNH_ARG(block * scaleSize * batch == dstSize, "forward_scale: sizes do not align");
-  hipLaunchKernelGGL(scale_blk_kernel, dim3(grid_for(dstSize)), dim3(kThreads), 0, cx->stream, dst + offset, dstSize,
-                     block, scaleSize, scale, incb);
-  return launch_status("scale_blk_kernel");
+  return launch_rows(ScaleOp{scale, incb}, dst + offset, dstSize, block, scaleSize, cx->stream,
+                     "rows_kernel<scale>");
 }
 
 extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSize, const float* src, int64_t srcOffset,
@@ -263,7 +416,18 @@ extern "C" int32_t tnh_activate(int64_t N, float* x, int64_t offset, int32_t act
           "activate: unsupported activation %d", act);
   if (N == 0 || act == TNH_AC_LINEAR) return TNH_OK;  // acLINEAR: no launch (nncuda.pas:533)
   TNH_ARG(x != nullptr, "activate: NULL buffer");
-  hipLaunchKernelGGL(activate_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, x + offset, N, act);
+  float* p = x + offset;
+  if (N % 4 == 0 && al16(p)) {
+    float4* p4 = reinterpret_cast<float4*>(p);
+    if (act == TNH_AC_LEAKY)
+      hipLaunchKernelGGL(activate4_kernel<TNH_AC_LEAKY>, dim3(grid_for(N / 4)), dim3(kThreads), 0, cx->stream, p4,
+                         N / 4);
+    else
+      hipLaunchKernelGGL(activate4_kernel<TNH_AC_LOGISTIC>, dim3(grid_for(N / 4)), dim3(kThreads), 0, cx->stream, p4,
+                         N / 4);
+    return launch_status("activate4_kernel");
+  }
+  hipLaunchKernelGGL(activate_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, p, N, act);
   return launch_status("activate_kernel");
 }
 
@@ -274,7 +438,19 @@ extern "C" int32_t tnh_derive(int64_t N, const float* x, int64_t offset, int32_t
           act);
   if (N == 0 || act == TNH_AC_LINEAR) return TNH_OK;
   TNH_ARG(x && delta, "derive: NULL buffer");
-  hipLaunchKernelGGL(derive_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, x + offset, N, act, delta);
+  const float* xp = x + offset;
+  if (N % 4 == 0 && al16(xp) && al16(delta)) {
+    const float4* x4 = reinterpret_cast<const float4*>(xp);
+    float4* d4 = reinterpret_cast<float4*>(delta);
+    if (act == TNH_AC_LEAKY)
+      hipLaunchKernelGGL(derive4_kernel<TNH_AC_LEAKY>, dim3(grid_for(N / 4)), dim3(kThreads), 0, cx->stream, x4, N / 4,
+                         d4);
+    else
+      hipLaunchKernelGGL(derive4_kernel<TNH_AC_LOGISTIC>, dim3(grid_for(N / 4)), dim3(kThreads), 0, cx->stream, x4,
+                         N / 4, d4);
+    return launch_status("derive4_kernel");
+  }
+  hipLaunchKernelGGL(derive_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, xp, N, act, delta);
   return launch_status("derive_kernel");
 }
 
@@ -411,7 +587,64 @@ extern "C" int32_t tnh_bn_normalize(int64_t dstSize, float* x, int64_t offset, i
   TNH_ARG(x && mean && variance, "bn_normalize: NULL buffer");
   const int64_t block = dstSize / (N * batch);
   TNH_ARG(block * N * batch == dstSize, "bn_normalize: sizes do not align");
-  hipLaunchKernelGGL(bn_norm_kernel, dim3(grid_for(dstSize)), dim3(kThreads), 0, cx->stream, x + offset, dstSize,
-                     block, N, mean, variance);
-  return launch_status("bn_norm_kernel");
+  return launch_rows(NormOp{mean, 1, variance, 1, block == 1}, x + offset, dstSize, block, N, cx->stream,
+                     "rows_kernel<normalize>");
+}
+
+extern "C" int32_t tnh_normalize(int64_t srcSize, int64_t dstSize, int64_t groups, const float* means,
+                                 int64_t meansStride, const float* vars, int64_t varsStride, float* dst,
+                                 int64_t dstOffset) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(srcSize > 0 && dstSize >= 0 && groups > 0 && dstOffset >= 0 && meansStride >= 0 && varsStride >= 0,
+          "normalize: bad sizes");
+  if (dstSize == 0) return TNH_OK;
+  TNH_ARG(means && vars && dst, "normalize: NULL buffer");
+  const int64_t block = dstSize / (srcSize * groups);
+  TNH_ARG(block > 0 && block * srcSize * groups == dstSize, "normalize: sizes do not align");
+  return launch_rows(NormOp{means, meansStride, vars, varsStride, block == 1}, dst + dstOffset, dstSize, block,
+                     srcSize, cx->stream, "rows_kernel<normalize>");
+}
+
+extern "C" int32_t tnh_forward_scale_add(int64_t dstSize, float* dst, int64_t offset, int64_t scaleSize,
+                                         const float* scales, const float* biases, int64_t incb, int64_t batch) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize >= 0 && scaleSize > 0 && batch > 0 && offset >= 0, "forward_scale_add: bad sizes");
+  if (dstSize == 0) return TNH_OK;
+  TNH_ARG(dst && scales && biases, "forward_scale_add: NULL buffer");
+  const int64_t block = dstSize / (scaleSize * batch);
+  TNH_ARG(block > 0 && block * scaleSize * batch == dstSize, "forward_scale_add: sizes do not align");
+  return launch_rows(ScaleAddOp{scales, biases, incb}, dst + offset, dstSize, block, scaleSize, cx->stream,
+                     "rows_kernel<scale_add>");
+}
+
+extern "C" int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch, const float* x, float* xNorm,
+                                  float* out, const float* mean, const float* variance, const float* scales,
+                                  const float* biases, int32_t act) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize >= 0 && N > 0 && batch > 0, "bn_forward: bad sizes");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_forward: activation %d", act);
+  if (dstSize == 0) return TNH_OK;
+  TNH_ARG(x && out && mean && variance && scales && biases, "bn_forward: NULL buffer");
+  const int64_t block = dstSize / (N * batch);
+  TNH_ARG(block > 0 && block * N * batch == dstSize, "bn_forward: sizes do not align");
+  const NormOp norm{mean, 1, variance, 1, block == 1};
+  const ScaleAddOp sa{scales, biases, 1};
+  const bool v4 = block % 4 == 0 && al16(x) && al16(out) && (!xNorm || al16(xNorm));
+  const Rows g = make_rows(dstSize, block, N, v4 ? 4 : 1);
+  auto go = [&](auto vw, auto ac) {
+    constexpr int VW = decltype(vw)::value, ACT = decltype(ac)::value;
+    hipLaunchKernelGGL((bn_fwd_kernel<VW, ACT>), dim3(grid_rows(g)), dim3(kThreads), 0, cx->stream, norm, sa, x,
+                       xNorm, out, g);
+  };
+  using L = std::integral_constant<int, TNH_AC_LEAKY>;
+  using G = std::integral_constant<int, TNH_AC_LOGISTIC>;
+  using I = std::integral_constant<int, TNH_AC_LINEAR>;
+  using V4 = std::integral_constant<int, 4>;
+  using V1 = std::integral_constant<int, 1>;
+  if (v4) {
+    if (act == TNH_AC_LEAKY) go(V4{}, L{}); else if (act == TNH_AC_LOGISTIC) go(V4{}, G{}); else go(V4{}, I{});
+  } else {
+    if (act == TNH_AC_LEAKY) go(V1{}, L{}); else if (act == TNH_AC_LOGISTIC) go(V1{}, G{}); else go(V1{}, I{});
+  }
+  return launch_status("bn_fwd_kernel");
 }

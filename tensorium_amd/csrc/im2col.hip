@@ -1,7 +1,8 @@
 // Standalone im2col / col2im (bit-exact data movement).
 //
-// im2col: one thread per column element, writes fully coalesced rows of col;
-//   formula of sim2Col (ntensors.pas:11425-11463).
+// im2col: one thread per (channel, output pixel), writing the kh*kw rows of
+//   its channel (coalesced along each row); formula of sim2Col
+//   (ntensors.pas:11425-11463).
 // col2im: a gather, one thread per image pixel.  The reference scatters
 //   (c2i, ntensors.pas:11650-11715: rows i = (c*kh + ky)*kw + kx ascending,
 //   each adding its value into im).  For a fixed pixel every row contributes
@@ -17,48 +18,66 @@ struct Geom {
   int64_t C, H, W, kh, kw, pH, pW, sY, sX, dY, dX, OH, OW;
 };
 
+// One thread per (channel, output pixel): it reads the kh*kw window taps of
+// its pixel and writes them to the kh*kw rows of the channel, so the stores
+// of a wave are consecutive along each row and the index arithmetic is paid
+// once per thread, not per element.  I is the index type (32-bit when every
+// index fits).
+template <class I>
 __global__ __launch_bounds__(256) void im2col_kernel(Geom g, const float* __restrict__ im, int64_t imStride,
-                                                     float* __restrict__ col, int64_t colStride, int64_t total) {
+                                                     float* __restrict__ col, int64_t colStride, I total) {
   const int64_t b = blockIdx.y;
   const float* src = im + b * imStride;
   float* dst = col + b * colStride;
-  const int64_t OHW = g.OH * g.OW;
-  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t row = e / OHW, p = e - row * OHW;
-    const int64_t oy = p / g.OW, ox = p - oy * g.OW;
-    const int64_t c = row / (g.kh * g.kw), r = row - c * (g.kh * g.kw);
-    const int64_t ky = r / g.kw, kx = r - ky * g.kw;
-    const int64_t iy = -g.pH + ky * g.dY + oy * g.sY;
-    const int64_t ix = -g.pW + kx * g.dX + ox * g.sX;
-    float v = 0.f;
-    if (static_cast<uint64_t>(iy) < static_cast<uint64_t>(g.H) && static_cast<uint64_t>(ix) < static_cast<uint64_t>(g.W))
-      v = src[(c * g.H + iy) * g.W + ix];
-    dst[e] = v;
+  const I OW = static_cast<I>(g.OW), OHW = static_cast<I>(g.OH * g.OW), H = static_cast<I>(g.H),
+          W = static_cast<I>(g.W);
+  const I kh = static_cast<I>(g.kh), kw = static_cast<I>(g.kw);
+  for (I e = static_cast<I>(blockIdx.x) * 256 + threadIdx.x; e < total; e += static_cast<I>(gridDim.x) * 256) {
+    const I c = e / OHW, p = e - c * OHW;
+    const I oy = p / OW, ox = p - oy * OW;
+    const I y0 = oy * static_cast<I>(g.sY) - static_cast<I>(g.pH);
+    const I x0 = ox * static_cast<I>(g.sX) - static_cast<I>(g.pW);
+    const float* plane = src + static_cast<int64_t>(c) * H * W;
+    float* out = dst + static_cast<int64_t>(c) * kh * kw * OHW + p;
+    for (I ky = 0; ky < kh; ++ky) {
+      const I iy = y0 + ky * static_cast<I>(g.dY);
+      const bool rowOk = iy >= 0 && iy < H;
+      for (I kx = 0; kx < kw; ++kx) {
+        const I ix = x0 + kx * static_cast<I>(g.dX);
+        float v = 0.f;
+        if (rowOk && ix >= 0 && ix < W) v = plane[static_cast<int64_t>(iy) * W + ix];
+        out[static_cast<int64_t>(ky * kw + kx) * OHW] = v;
+      }
+    }
   }
 }
 
+template <class I>
 __global__ __launch_bounds__(256) void col2im_kernel(Geom g, const float* __restrict__ col, int64_t colStride,
-                                                     float* __restrict__ im, int64_t imStride, int64_t total) {
+                                                     float* __restrict__ im, int64_t imStride, I total) {
   const int64_t b = blockIdx.y;
   const float* src = col + b * colStride;
   float* dst = im + b * imStride;
-  const int64_t HW = g.H * g.W, OHW = g.OH * g.OW;
-  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t c = e / HW, p = e - c * HW;
-    const int64_t y = p / g.W, x = p - y * g.W;
+  const I HW = static_cast<I>(g.H * g.W), W = static_cast<I>(g.W), OHW = static_cast<I>(g.OH * g.OW);
+  const I OW = static_cast<I>(g.OW), OH = static_cast<I>(g.OH), sY = static_cast<I>(g.sY), sX = static_cast<I>(g.sX);
+  const I kh = static_cast<I>(g.kh), kw = static_cast<I>(g.kw);
+  for (I e = static_cast<I>(blockIdx.x) * 256 + threadIdx.x; e < total; e += static_cast<I>(gridDim.x) * 256) {
+    const I c = e / HW, p = e - c * HW;
+    const I y = p / W, x = p - y * W;
     float v = dst[e];
-    for (int64_t ky = 0; ky < g.kh; ++ky) {
+    const float* rows = src + static_cast<int64_t>(c) * kh * kw * OHW;
+    for (I ky = 0; ky < kh; ++ky) {
       // c2i: iy = (ky - pH)*dY + oy*sY  ->  oy = (y - (ky - pH)*dY) / sY
-      const int64_t ty = y - (ky - g.pH) * g.dY;
-      if (ty < 0 || ty % g.sY) continue;
-      const int64_t oy = ty / g.sY;
-      if (oy >= g.OH) continue;
-      for (int64_t kx = 0; kx < g.kw; ++kx) {
-        const int64_t tx = x - (kx - g.pW) * g.dX;
-        if (tx < 0 || tx % g.sX) continue;
-        const int64_t ox = tx / g.sX;
-        if (ox >= g.OW) continue;
-        v = v + src[((c * g.kh + ky) * g.kw + kx) * OHW + oy * g.OW + ox];
+      const I ty = y - (ky - static_cast<I>(g.pH)) * static_cast<I>(g.dY);
+      if (ty < 0) continue;
+      const I oy = sY == 1 ? ty : ty / sY;
+      if (oy * sY != ty || oy >= OH) continue;
+      for (I kx = 0; kx < kw; ++kx) {
+        const I tx = x - (kx - static_cast<I>(g.pW)) * static_cast<I>(g.dX);
+        if (tx < 0) continue;
+        const I ox = sX == 1 ? tx : tx / sX;
+        if (ox * sX != tx || ox >= OW) continue;
+        v = v + rows[static_cast<int64_t>(ky * kw + kx) * OHW + oy * OW + ox];
       }
     }
     dst[e] = v;
@@ -94,9 +113,14 @@ extern "C" int32_t tnh_im2col_batched(int64_t C, int64_t H, int64_t W, int64_t k
   TNH_ARG(batch >= 0 && batch <= 65535, "im2col: batch %lld", (long long)batch);
   TNH_ARG(im && col && imOff >= 0 && colOff >= 0, "im2col: bad buffers");
   if (batch == 0) return TNH_OK;
-  const int64_t total = C * kh * kw * g.OH * g.OW;
-  hipLaunchKernelGGL(im2col_kernel, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
-                     im + imOff, imStride, col + colOff, colStride, total);
+  const int64_t total = C * g.OH * g.OW;  // (channel, output pixel) pairs
+  const bool small = C * kh * kw * g.OH * g.OW + 256LL * 65536 < INT32_MAX && C * H * W < INT32_MAX;
+  if (small)
+    hipLaunchKernelGGL(im2col_kernel<int>, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
+                       im + imOff, imStride, col + colOff, colStride, static_cast<int>(total));
+  else
+    hipLaunchKernelGGL(im2col_kernel<int64_t>, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
+                       im + imOff, imStride, col + colOff, colStride, total);
   return launch_status("im2col_kernel");
 }
 
@@ -118,8 +142,13 @@ extern "C" int32_t tnh_col2im_batched(int64_t C, int64_t H, int64_t W, int64_t k
   TNH_ARG(im && col && imOff >= 0 && colOff >= 0, "col2im: bad buffers");
   if (batch == 0) return TNH_OK;
   const int64_t total = C * H * W;
-  hipLaunchKernelGGL(col2im_kernel, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
-                     col + colOff, colStride, im + imOff, imStride, total);
+  const bool small = C * kh * kw * g.OH * g.OW < INT32_MAX && total + 256LL * 65536 < INT32_MAX;
+  if (small)
+    hipLaunchKernelGGL(col2im_kernel<int>, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
+                       col + colOff, colStride, im + imOff, imStride, static_cast<int>(total));
+  else
+    hipLaunchKernelGGL(col2im_kernel<int64_t>, dim3(blocks_for(total), (unsigned)batch), dim3(256), 0, cx->stream, g,
+                       col + colOff, colStride, im + imOff, imStride, total);
   return launch_status("col2im_kernel");
 }
 

@@ -59,6 +59,92 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(PoolGeom g, int64
   }
 }
 
+// 2x2 windows with stride 2 and no padding offset, every tap inside the
+// image (2*OH <= H, 2*OW <= W, W even): one thread per two adjacent outputs
+// of a row reads a 4-float span of the two input rows (16-byte loads when W
+// % 4 == 0, else two 8-byte loads each), scans the taps in the reference
+// order (row-major, strict '>', -MaxSingle start) and writes the two values
+// (8 bytes) and the two int64 indices (16 bytes).  32-bit index arithmetic;
+// the recorded indices are 64-bit.
+template <bool V4>
+__global__ __launch_bounds__(kThreads) void maxpool2_fwd_kernel(int total, int OH, int OW2, int H, int W,
+                                                                const float* __restrict__ in, float* __restrict__ out,
+                                                                int64_t* __restrict__ idx) {
+  for (int t = blockIdx.x * kThreads + threadIdx.x; t < total; t += gridDim.x * kThreads) {
+    const int jp = t % OW2, r = t / OW2;  // r = plane*OH + i
+    const int i = r % OH, plane = r / OH;
+    const int x0 = 4 * jp;
+    const int64_t row0 = (static_cast<int64_t>(plane) * H + 2 * i) * W;
+    float a[8];
+    if constexpr (V4) {
+      const float4 u = *reinterpret_cast<const float4*>(in + row0 + x0);
+      const float4 v = *reinterpret_cast<const float4*>(in + row0 + W + x0);
+      a[0] = u.x; a[1] = u.y; a[2] = u.z; a[3] = u.w; a[4] = v.x; a[5] = v.y; a[6] = v.z; a[7] = v.w;
+    } else {
+      const float2 u0 = *reinterpret_cast<const float2*>(in + row0 + x0);
+      const float2 u1 = *reinterpret_cast<const float2*>(in + row0 + x0 + 2);
+      const float2 v0 = *reinterpret_cast<const float2*>(in + row0 + W + x0);
+      const float2 v1 = *reinterpret_cast<const float2*>(in + row0 + W + x0 + 2);
+      a[0] = u0.x; a[1] = u0.y; a[2] = u1.x; a[3] = u1.y; a[4] = v0.x; a[5] = v0.y; a[6] = v1.x; a[7] = v1.y;
+    }
+    float m[2];
+    int64_t k[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float mx = -FLT_MAX;
+      int64_t mi = -1;
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float v = a[4 * n + 2 * h + c];
+          if (v > mx) {
+            mx = v;
+            mi = row0 + static_cast<int64_t>(n) * W + x0 + 2 * h + c;
+          }
+        }
+      m[h] = mx;
+      k[h] = mi;
+    }
+    const int64_t o = static_cast<int64_t>(r) * (2 * OW2) + 2 * jp;
+    *reinterpret_cast<float2*>(out + o) = make_float2(m[0], m[1]);
+    if (idx) {
+      idx[o] = k[0];
+      idx[o + 1] = k[1];
+    }
+  }
+}
+
+// Backward of the 2x2 / stride-2 case above: input pixel (y, x) lies in
+// exactly one window (y/2, x/2) (when inside the output), so each thread
+// takes four consecutive pixels of a row (two windows), adds a window's
+// delta to the pixel its index names (dIn += delta, the serial scatter's one
+// contribution) and rewrites the four pixels with one 16-byte store.
+__global__ __launch_bounds__(kThreads) void maxpool2_bwd_kernel(int total, int H, int W4, int OH, int OW,
+                                                                const int64_t* __restrict__ idx,
+                                                                const float* __restrict__ delta,
+                                                                float* __restrict__ dIn) {
+  for (int t = blockIdx.x * kThreads + threadIdx.x; t < total; t += gridDim.x * kThreads) {
+    const int q = t % W4, r = t / W4;  // r = plane*H + y
+    const int y = r % H, plane = r / H;
+    const int i = y >> 1;
+    if (i >= OH) continue;
+    const int64_t e0 = static_cast<int64_t>(r) * (4 * W4) + 4 * q;
+    float4 v = *reinterpret_cast<const float4*>(dIn + e0);
+    float w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * q + h;
+      if (j >= OW) break;
+      const int64_t o = (static_cast<int64_t>(plane) * OH + i) * OW + j;
+      const int64_t k = idx[o];
+      const int64_t d = k - (e0 + 2 * h);
+      if (d == 0 || d == 1) w[2 * h + d] = w[2 * h + d] + delta[o];
+    }
+    *reinterpret_cast<float4*>(dIn + e0) = make_float4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // first output row/col whose window can contain input coordinate p:
 // smallest i with off + i*s + size - 1 >= p
 __device__ inline int64_t first_win(int64_t p, int64_t off, int64_t s, int64_t size) {
@@ -178,6 +264,16 @@ __global__ __launch_bounds__(kThreads) void upsample_bwd_kernel(int64_t total, i
 }
 
 bool al8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The 2x2 / stride-2 kernels apply: window origin 0, every tap inside the
+// image, even output rows (pairs of outputs), 8-byte aligned input and
+// output, 16-byte aligned indices, and 32-bit element counts.
+bool pool2_fast(const PoolGeom& g, int64_t batch, const float* in, const float* out, const int64_t* idx) {
+  return g.size == 2 && g.sX == 2 && g.sY == 2 && g.off == 0 && 2 * g.OH <= g.H && 2 * g.OW <= g.W && g.W % 2 == 0 &&
+         g.OW % 2 == 0 && al8(in) && al8(out) && (!idx || al16(idx)) &&
+         batch * g.C * g.H * g.W + 65536LL * kThreads < INT32_MAX;
+}
 
 }  // namespace
 }  // namespace tnh
@@ -199,6 +295,18 @@ extern "C" int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH, in
   const int64_t total = batch * outC * outH * outW;
   if (total == 0) return TNH_OK;
   PoolGeom g{c, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  if (pool2_fast(g, batch, input, output, indexes)) {
+    const int tot = static_cast<int>(total / 2);
+    if (w % 4 == 0 && al16(input))
+      hipLaunchKernelGGL(maxpool2_fwd_kernel<true>, dim3(grid_for(tot)), dim3(kThreads), 0, cx->stream, tot,
+                         static_cast<int>(outH), static_cast<int>(outW / 2), static_cast<int>(h), static_cast<int>(w),
+                         input, output, indexes);
+    else
+      hipLaunchKernelGGL(maxpool2_fwd_kernel<false>, dim3(grid_for(tot)), dim3(kThreads), 0, cx->stream, tot,
+                         static_cast<int>(outH), static_cast<int>(outW / 2), static_cast<int>(h), static_cast<int>(w),
+                         input, output, indexes);
+    return launch_status("maxpool2_fwd_kernel");
+  }
   hipLaunchKernelGGL(maxpool_fwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, g, total, input, output,
                      indexes);
   return launch_status("maxpool_fwd_kernel");
@@ -216,6 +324,13 @@ extern "C" int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH, in
   const int64_t total = batch * outC * h * w;
   if (total == 0) return TNH_OK;
   PoolGeom g{outC, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  if (pool2_fast(g, batch, deltaIn, delta, indexes) && w % 4 == 0 && al16(deltaIn)) {
+    const int tot = static_cast<int>(total / 4);
+    hipLaunchKernelGGL(maxpool2_bwd_kernel, dim3(grid_for(tot)), dim3(kThreads), 0, cx->stream, tot,
+                       static_cast<int>(h), static_cast<int>(w / 4), static_cast<int>(outH), static_cast<int>(outW),
+                       indexes, delta, deltaIn);
+    return launch_status("maxpool2_bwd_kernel");
+  }
   hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, g, total, indexes,
                      delta, deltaIn);
   return launch_status("maxpool_bwd_kernel");

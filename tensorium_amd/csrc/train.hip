@@ -2,12 +2,14 @@
 // and their deltas, softmax cross-entropy, average pooling, delta clamping,
 // the fused SGD update and the weight-gradient GEMM of conv backward.
 //
-// Channel reductions run one workgroup per channel with a fixed-order tree
-// (deterministic run to run); element-wise formulas follow the reference
+// Channel reductions run several workgroups per channel and add their
+// partials in a fixed order (deterministic run to run); element-wise
+// formulas follow the reference
 // CPU operation order exactly (no contraction: the build uses
 // -ffp-contract=off, FMAs are explicit where the reference fuses).
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
 
 #include "common.hpp"
 #include "gemm_core.hpp"
@@ -39,60 +41,263 @@ __device__ inline float block_sum(float v, float* sh) {
   return r;
 }
 
-// Element (b, i, k) of a [groups][nch][block] view lives at (b*nch + i)*block + k.
-// MeansAndVars (ntensors.pas:9102-9180): mean over groups*block values, then
-// the residual sum of squares about the fp32 mean divided by (S - 1).
-__global__ __launch_bounds__(kRed) void means_vars_kernel(const float* src, int64_t nch, int64_t block,
-                                                          int64_t groups, float* means, float* vars) {
-  __shared__ float sh[kRed];
-  const int64_t i = blockIdx.x;
-  float s = 0.f;
-  for (int64_t b = 0; b < groups; ++b) {
-    const float* p = src + (b * nch + i) * block;
-    for (int64_t k = threadIdx.x; k < block; k += kRed) s = s + p[k];
+// ---------------------------------------------------------------------------
+// Channel reductions over a [groups][nch][block] view (element (b, i, k) at
+// (b*nch + i)*block + k), spread over P workgroups per channel.  A
+// channel's groups*block elements are cut into units (one row b, or a chunk
+// of cs elements of a long row); workgroup (p, i) takes units
+// [p*U/P, (p+1)*U/P) of channel i, each thread adds its elements in order
+// (16 bytes at a time when the rows allow) and a fixed tree over the
+// workgroup leaves one partial per workgroup in the context's reduction
+// buffer.  A second kernel adds a channel's P partials in a fixed order
+// (fixed_total).  Every order is fixed, so results do not vary run to run.
+// ---------------------------------------------------------------------------
+struct ChanSplit {
+  int64_t nch, block, groups;
+  int64_t cs;     // elements per unit
+  int64_t kc;     // units per row
+  int64_t units;  // groups * kc
+  int P;          // workgroups per channel
+};
+
+// nq partial sums per workgroup; about four workgroups per CU over all
+// channels, at least ~1024 elements each.
+int chan_split(ChanSplit& s, int64_t nch, int64_t block, int64_t groups, int nq, const Context* cx) {
+  TNH_ARG(nch <= 65535, "channel reduction: %lld channels (at most 65535)", (long long)nch);
+  TNH_ARG(nch * nq <= cx->redFloats, "channel reduction: %lld channels do not fit the partial-sum buffer",
+          (long long)nch);
+  s.nch = nch;
+  s.block = block;
+  s.groups = groups;
+  s.cs = block <= 4096 ? block : 4096;
+  s.kc = (block + s.cs - 1) / s.cs;
+  s.units = groups * s.kc;
+  int64_t P = (4 * static_cast<int64_t>(cx->cu_count) + nch - 1) / nch;
+  P = std::min<int64_t>(P, std::max<int64_t>(1, groups * block / 1024));
+  P = std::min<int64_t>({P, s.units, cx->redFloats / (nq * nch), 4096});
+  s.P = static_cast<int>(std::max<int64_t>(P, 1));
+  return TNH_OK;
+}
+
+// Sum of v[0 .. n) in a fixed order: lane l of the first wave adds v[l],
+// v[l + 64], ... in turn, then a fixed tree over the 64 lanes.  Every thread
+// of the workgroup calls it and gets the result; the arithmetic does not
+// depend on the workgroup size.
+__device__ inline float fixed_total(const float* v, int n, float* sh) {
+  if (threadIdx.x < 64) {
+    float t = 0.f;
+    for (int k = threadIdx.x; k < n; k += 64) t = t + v[k];
+    sh[threadIdx.x] = t;
   }
-  const float S = static_cast<float>(groups * block);
-  const float m = block_sum(s, sh) / S;
-  float v = 0.f;
-  for (int64_t b = 0; b < groups; ++b) {
-    const float* p = src + (b * nch + i) * block;
-    for (int64_t k = threadIdx.x; k < block; k += kRed) {
-      const float d = p[k] - m;
-      v = v + d * d;
+  __syncthreads();
+  for (int w = 32; w > 0; w >>= 1) {
+    if (threadIdx.x < w) sh[threadIdx.x] = sh[threadIdx.x] + sh[threadIdx.x + w];
+    __syncthreads();
+  }
+  const float r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+// Walks workgroup (p, i)'s units, calling op.add(acc, element index) per
+// element or op.add4(acc, index of 4 elements) per 16 bytes.
+template <bool VEC, class Op>
+__device__ inline void chan_walk(const ChanSplit& s, int p, int64_t i, const Op& op, float* acc) {
+  const int64_t u0 = s.units * p / s.P, u1 = s.units * (p + 1) / s.P;
+  for (int64_t u = u0; u < u1; ++u) {
+    const int64_t b = u / s.kc, c = u - b * s.kc;
+    const int64_t base = (b * s.nch + i) * s.block + c * s.cs;
+    const int64_t len = std::min(s.cs, s.block - c * s.cs);
+    if constexpr (VEC) {
+      for (int64_t k = threadIdx.x; k < len / 4; k += kRed) op.add4(acc, base + 4 * k);
+    } else {
+      for (int64_t k = threadIdx.x; k < len; k += kRed) op.add(acc, base + k);
     }
-  }
-  const float rss = block_sum(v, sh);
-  if (threadIdx.x == 0) {
-    means[i] = m;
-    vars[i] = rss / static_cast<float>(groups * block - 1);
   }
 }
 
-// sMeanAndVarianceDelta (ntensors.pas:8831-8898).
-__global__ __launch_bounds__(kRed) void means_vars_delta_kernel(const float* delta, const float* x, int64_t nch,
-                                                                int64_t block, int64_t groups, const float* mean,
-                                                                const float* variance, float* mean_delta,
-                                                                float* variance_delta) {
+template <int NQ, bool VEC, class Op>
+__global__ __launch_bounds__(kRed) void chan_partial_kernel(Op op, ChanSplit s, float* part) {
   __shared__ float sh[kRed];
+  const int p = blockIdx.x;
+  const int64_t i = blockIdx.y;
+  op.begin(i, s, part, sh);
+  float acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = 0.f;
+  chan_walk<VEC>(s, p, i, op, acc);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const float r = block_sum(acc[q], sh);
+    if (threadIdx.x == 0) part[(q * s.nch + i) * s.P + p] = r;
+  }
+}
+
+__device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// MeansAndVars (ntensors.pas:9102-9180), first pass: sum
+struct SumOp {
+  const float* x;
+  __device__ void begin(int64_t, const ChanSplit&, const float*, float*) {}
+  __device__ void add(float* a, int64_t e) const { a[0] = a[0] + x[e]; }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 v = ld4(x + e);
+    a[0] = a[0] + v.x;
+    a[0] = a[0] + v.y;
+    a[0] = a[0] + v.z;
+    a[0] = a[0] + v.w;
+  }
+};
+
+// second pass: residual sum of squares about the fp32 mean (the mean from
+// the first pass's partials, the same fixed sum the final kernel forms)
+struct RssOp {
+  const float* x;
+  const float* sumPart;  // [nch][P]
+  float S;
+  float m;
+  __device__ void begin(int64_t i, const ChanSplit& s, const float*, float* sh) {
+    m = fixed_total(sumPart + i * s.P, s.P, sh) / S;
+  }
+  __device__ void add(float* a, int64_t e) const {
+    const float d = x[e] - m;
+    a[0] = a[0] + d * d;
+  }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 v = ld4(x + e);
+    float d = v.x - m;
+    a[0] = a[0] + d * d;
+    d = v.y - m;
+    a[0] = a[0] + d * d;
+    d = v.z - m;
+    a[0] = a[0] + d * d;
+    d = v.w - m;
+    a[0] = a[0] + d * d;
+  }
+};
+
+__global__ __launch_bounds__(64) void means_vars_final(const float* part, ChanSplit s, float S, float* means,
+                                                       float* vars, float* rollMean, float* rollVar, float keep,
+                                                       float bm) {
+  __shared__ float sh[64];
   const int64_t i = blockIdx.x;
-  const float mu = mean[i];
-  float sm = 0.f, sv = 0.f;
-  for (int64_t b = 0; b < groups; ++b) {
-    const int64_t base = (b * nch + i) * block;
-    for (int64_t k = threadIdx.x; k < block; k += kRed) {
-      const float d = delta[base + k];
-      sm = sm + d;
-      sv = sv + d * (x[base + k] - mu);
+  const float m = fixed_total(part + i * s.P, s.P, sh) / S;
+  const float rss = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
+  if (threadIdx.x == 0) {
+    const float v = rss / (S - 1.f);
+    means[i] = m;
+    vars[i] = v;
+    if (rollMean) {  // Multiply(1 - momentum), then axpy(momentum, .) (nbaselayer.pas:352-355)
+      rollMean[i] = fmaf(bm, m, keep * rollMean[i]);
+      rollVar[i] = fmaf(bm, v, keep * rollVar[i]);
     }
   }
-  const float m = block_sum(sm, sh);
-  const float v = block_sum(sv, sh);
+}
+
+// sMeanAndVarianceDelta (ntensors.pas:8831-8898): sum(delta) and
+// sum(delta * (x - mean))
+struct MvdOp {
+  const float* delta;
+  const float* x;
+  const float* mean;
+  float mu;
+  __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) { mu = mean[i]; }
+  __device__ void add(float* a, int64_t e) const {
+    const float d = delta[e];
+    a[0] = a[0] + d;
+    a[1] = a[1] + d * (x[e] - mu);
+  }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 d = ld4(delta + e), v = ld4(x + e);
+    a[0] = a[0] + d.x;
+    a[1] = a[1] + d.x * (v.x - mu);
+    a[0] = a[0] + d.y;
+    a[1] = a[1] + d.y * (v.y - mu);
+    a[0] = a[0] + d.z;
+    a[1] = a[1] + d.z * (v.z - mu);
+    a[0] = a[0] + d.w;
+    a[1] = a[1] + d.w * (v.w - mu);
+  }
+};
+
+__global__ __launch_bounds__(64) void means_vars_delta_final(const float* part, ChanSplit s, const float* variance,
+                                                             float* mean_delta, float* variance_delta) {
+  __shared__ float sh[64];
+  const int64_t i = blockIdx.x;
+  const float m = fixed_total(part + i * s.P, s.P, sh);
+  const float v = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
   if (threadIdx.x == 0) {
     const float vc = fmaxf(variance[i], kEps);
     mean_delta[i] = m * (-1.0f / sqrtf(vc));
     // Power(max(var, eps), -3/2) is evaluated in double and the product stored as single
     variance_delta[i] = static_cast<float>(static_cast<double>(v) * -0.5 * pow(static_cast<double>(vc), -1.5));
   }
+}
+
+// addDots (ntensors.pas:7783-7830): sum of a*b
+struct DotOp {
+  const float* x;
+  const float* y;
+  __device__ void begin(int64_t, const ChanSplit&, const float*, float*) {}
+  __device__ void add(float* a, int64_t e) const { a[0] = a[0] + x[e] * y[e]; }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 u = ld4(x + e), v = ld4(y + e);
+    a[0] = a[0] + u.x * v.x;
+    a[0] = a[0] + u.y * v.y;
+    a[0] = a[0] + u.z * v.z;
+    a[0] = a[0] + u.w * v.w;
+  }
+};
+
+__global__ __launch_bounds__(64) void add_dots_final(const float* part, ChanSplit s, float* dst) {
+  __shared__ float sh[64];
+  const int64_t i = blockIdx.x;
+  const float t = fixed_total(part + i * s.P, s.P, sh);
+  if (threadIdx.x == 0) dst[i] = dst[i] + t;
+}
+
+bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Launches the first pass of a channel reduction (nq partials per workgroup).
+template <int NQ, class Op>
+int launch_partial(const Op& op, const ChanSplit& s, bool vec, float* part, hipStream_t st, const char* name) {
+  const dim3 grid(static_cast<unsigned>(s.P), static_cast<unsigned>(s.nch));
+  if (vec)
+    hipLaunchKernelGGL((chan_partial_kernel<NQ, true, Op>), grid, dim3(kRed), 0, st, op, s, part);
+  else
+    hipLaunchKernelGGL((chan_partial_kernel<NQ, false, Op>), grid, dim3(kRed), 0, st, op, s, part);
+  return launch_status(name);
+}
+
+// 16-byte loads are legal when every unit starts 16-byte aligned
+bool chan_vec(const ChanSplit& s, std::initializer_list<const float*> ptrs) {
+  if (s.block % 4 || s.cs % 4) return false;
+  for (const float* p : ptrs)
+    if (!al16p(p)) return false;
+  return true;
+}
+
+int means_vars_impl(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src, int64_t offset,
+                    float* means, float* vars, float* rollMean, float* rollVar, float momentum) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize > 0 && groups > 0 && srcSize > 0 && offset >= 0, "means_vars: bad sizes");
+  TNH_ARG(src && means && vars, "means_vars: NULL buffer");
+  const int64_t block = srcSize / (dstSize * groups);
+  TNH_ARG(block * dstSize * groups == srcSize && groups * block > 1, "means_vars: sizes do not align");
+  ChanSplit s;
+  if (int st = chan_split(s, dstSize, block, groups, 2, cx)) return st;
+  const float* x = src + offset;
+  const bool vec = chan_vec(s, {x});
+  float* sumPart = cx->red;
+  float* rssPart = cx->red + dstSize * s.P;
+  const float S = static_cast<float>(groups * block);
+  if (int st = launch_partial<1>(SumOp{x}, s, vec, sumPart, cx->stream, "chan_partial_kernel<sum>")) return st;
+  if (int st = launch_partial<1>(RssOp{x, sumPart, S, 0.f}, s, vec, rssPart, cx->stream, "chan_partial_kernel<rss>"))
+    return st;
+  const float keep = 1.0f - momentum;
+  hipLaunchKernelGGL(means_vars_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, S,
+                     means, vars, rollMean, rollVar, keep, momentum);
+  return launch_status("means_vars_final");
 }
 
 // sNormalizeDelta (ntensors.pas:8900-8960), element order of
@@ -109,20 +314,6 @@ __global__ void normalize_delta_kernel(float* delta, const float* x, int64_t n, 
     t = t + md;
     delta[e] = delta[e] / sd + t;
   }
-}
-
-// addDots (ntensors.pas:7783-7830): dst[i] += sum over (b, k) of a*b.
-__global__ __launch_bounds__(kRed) void add_dots_kernel(const float* a, const float* b, int64_t nch, int64_t block,
-                                                        int64_t groups, float* dst) {
-  __shared__ float sh[kRed];
-  const int64_t i = blockIdx.x;
-  float s = 0.f;
-  for (int64_t g = 0; g < groups; ++g) {
-    const int64_t base = (g * nch + i) * block;
-    for (int64_t k = threadIdx.x; k < block; k += kRed) s = s + a[base + k] * b[base + k];
-  }
-  const float t = block_sum(s, sh);
-  if (threadIdx.x == 0) dst[i] = dst[i] + t;
 }
 
 // softmax (nsoftmaxlayer.pas:81-105): one thread per (batch, group) row.
@@ -275,14 +466,28 @@ __global__ __launch_bounds__(Cfg::NT) void wgrad_kernel(WgradArgs a) {
   });
 }
 
-__global__ void wgrad_reduce_kernel(WgradArgs a) {
+// Sums the split partials of each output element: one wave per element, lane
+// l adds splits l, l + 64, ... in turn (their loads issued together), then a
+// fixed tree over the lanes; then alpha and beta.  Fixed order: the result
+// does not vary run to run.
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
+  __shared__ float sh[4][64];
   const int64_t total = a.M * a.N;
-  GRID_STRIDE(e, total) {
-    float v = a.part[e];
-    for (int s = 1; s < a.splits; ++s) v = v + a.part[s * total + e];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 4 + w;
+  float v = 0.f;
+  if (e < total)
+    for (int s = lane; s < a.splits; s += 64) v = v + a.part[s * total + e];
+  sh[w][lane] = v;
+  __syncthreads();
+  for (int k = 32; k > 0; k >>= 1) {
+    if (lane < k) sh[w][lane] = sh[w][lane] + sh[w][lane + k];
+    __syncthreads();
+  }
+  if (lane == 0 && e < total) {
     const int64_t r = e / a.N, c = e - r * a.N;
     float* p = a.C + r * a.ldc + c;
-    float out = a.alpha * v;
+    float out = a.alpha * sh[w][0];
     if (a.beta != 0.f) out = out + a.beta * *p;
     *p = out;
   }
@@ -298,7 +503,7 @@ int launch_wgrad(WgradArgs a, hipStream_t s) {
   hipLaunchKernelGGL((wgrad_kernel<WCfg, VA, VB>), grid, dim3(WCfg::NT), 0, s, a);
   if (int st = launch_status("wgrad_kernel")) return st;
   if (a.splits > 1) {
-    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3(grid_1d(a.M * a.N)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3(static_cast<unsigned>((a.M * a.N + 3) / 4)), dim3(256), 0, s, a);
     return launch_status("wgrad_reduce_kernel");
   }
   return TNH_OK;
@@ -311,14 +516,14 @@ using namespace tnh;
 
 extern "C" int32_t tnh_means_vars(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src,
                                   int64_t offset, float* means, float* vars) {
-  TNH_REQUIRE_CTX(cx);
-  TNH_ARG(dstSize > 0 && groups > 0 && srcSize > 0 && offset >= 0, "means_vars: bad sizes");
-  TNH_ARG(src && means && vars, "means_vars: NULL buffer");
-  const int64_t block = srcSize / (dstSize * groups);
-  TNH_ARG(block * dstSize * groups == srcSize && groups * block > 1, "means_vars: sizes do not align");
-  hipLaunchKernelGGL(means_vars_kernel, dim3(static_cast<unsigned>(dstSize)), dim3(kRed), 0, cx->stream,
-                     src + offset, dstSize, block, groups, means, vars);
-  return launch_status("means_vars_kernel");
+  return means_vars_impl(srcSize, dstSize, groups, src, offset, means, vars, nullptr, nullptr, 0.f);
+}
+
+extern "C" int32_t tnh_bn_statistics(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src,
+                                     int64_t offset, float* means, float* vars, float* rollingMeans,
+                                     float* rollingVars, float momentum) {
+  TNH_ARG((rollingMeans == nullptr) == (rollingVars == nullptr), "bn_statistics: give both rolling buffers or none");
+  return means_vars_impl(srcSize, dstSize, groups, src, offset, means, vars, rollingMeans, rollingVars, momentum);
 }
 
 extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_t groups, const float* delta,
@@ -329,9 +534,16 @@ extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_
   TNH_ARG(delta && x && mean && variance && mean_delta && variance_delta, "means_vars_delta: NULL buffer");
   const int64_t block = srcSize / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == srcSize, "means_vars_delta: sizes do not align");
-  hipLaunchKernelGGL(means_vars_delta_kernel, dim3(static_cast<unsigned>(dstSize)), dim3(kRed), 0, cx->stream,
-                     delta + offset, x + offset, dstSize, block, groups, mean, variance, mean_delta, variance_delta);
-  return launch_status("means_vars_delta_kernel");
+  ChanSplit s;
+  if (int st = chan_split(s, dstSize, block, groups, 2, cx)) return st;
+  const float* d = delta + offset;
+  const float* xx = x + offset;
+  if (int st = launch_partial<2>(MvdOp{d, xx, mean, 0.f}, s, chan_vec(s, {d, xx}), cx->red, cx->stream,
+                                 "chan_partial_kernel<mean_var_delta>"))
+    return st;
+  hipLaunchKernelGGL(means_vars_delta_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red,
+                     s, variance, mean_delta, variance_delta);
+  return launch_status("means_vars_delta_final");
 }
 
 extern "C" int32_t tnh_normalize_delta(int64_t deltaSize, int64_t meanSize, int64_t groups, float* delta,
@@ -355,9 +567,14 @@ extern "C" int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups, cons
   TNH_ARG(src1 && src2 && dst, "add_dots: NULL buffer");
   const int64_t block = N / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == N, "add_dots: sizes do not align");
-  hipLaunchKernelGGL(add_dots_kernel, dim3(static_cast<unsigned>(dstSize)), dim3(kRed), 0, cx->stream,
-                     src1 + srcOffset, src2 + srcOffset, dstSize, block, groups, dst);
-  return launch_status("add_dots_kernel");
+  ChanSplit s;
+  if (int st = chan_split(s, dstSize, block, groups, 1, cx)) return st;
+  const float* a = src1 + srcOffset;
+  const float* b = src2 + srcOffset;
+  if (int st = launch_partial<1>(DotOp{a, b}, s, chan_vec(s, {a, b}), cx->red, cx->stream, "chan_partial_kernel<dots>"))
+    return st;
+  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, dst);
+  return launch_status("add_dots_final");
 }
 
 extern "C" int32_t tnh_softmax_batch(int64_t N, const float* input, int64_t iOffset, int64_t batch,

@@ -177,6 +177,13 @@ class Network:
 
         if layout not in ("nchw", "nhwc"):
             raise ValueError(f"layout {layout!r}")
+        if route_mode not in ("image", "reference"):
+            raise ValueError(f"route_mode {route_mode!r}")
+        if layout == "nhwc" and route_mode != "image":
+            # the whole-tensor concat is a layout of NCHW batches; the
+            # channels-last planner writes route inputs into per-image
+            # channel slices and has no equivalent
+            raise NotImplementedError("route_mode='reference' needs layout='nchw'")
         self.hip, self.layers, self.batch = hip, layers, batch
         self.route_mode = route_mode
         self.layout = layout

@@ -100,11 +100,15 @@ _PROTOS = {
     "tnh_maxpool_bwd": [i64] * 10 + [vp, vp, vp],
     "tnh_upsample": [i64, i64, i64, i64, vp, i64, i32, f32, vp, i32],
     "tnh_bn_normalize": [i64, vp, i64, i64, vp, vp, i64],
+    "tnh_normalize": [i64, i64, i64, vp, i64, vp, i64, vp, i64],
+    "tnh_forward_scale_add": [i64, vp, i64, i64, vp, vp, i64, i64],
+    "tnh_bn_forward": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
     "tnh_yolo_detections": [i64, i32, C.POINTER(vp), C.POINTER(i64), i64, i64, C.POINTER(f32), i64, i64, i64, i64,
                             f32, i32, i32, i64, vp, vp, vp, vp],
     "tnh_yolo_nms_sort": [i64, i64, i64, vp, vp, vp, f32],
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
+    "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
     "tnh_normalize_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
     "tnh_add_dots": [i64, i64, i64, vp, vp, i64, vp],
@@ -456,10 +460,30 @@ class TNNHip:
         call("tnh_yolo_nms_sort", batch, classes, capacity, addr(boxes), addr(prob), addr(counts), thresh)
 
     # -- batch norm ------------------------------------------------------------
+    def normalize(self, srcSize, dstSize, groups, means, meansStride, vars, varsStride, dst, dstOffset):
+        """TNNCuda.normalize (nncuda.pas:1371) with the CPU clamp."""
+        call("tnh_normalize", srcSize, dstSize, groups, addr(means), meansStride, addr(vars), varsStride, addr(dst),
+             dstOffset)
+
+    def forwardScaleAdd(self, dstSize, dst, offset, scaleSize, scales, biases, incb, batch):
+        """TNNCuda.forwardScaleAdd (nncuda.pas:1490): dst = fl(scale*dst) + bias."""
+        call("tnh_forward_scale_add", dstSize, addr(dst), offset, scaleSize, addr(scales), addr(biases), incb, batch)
+
+    def bnForward(self, dstSize, N, batch, x, xNorm, out, mean, variance, scales, biases, activation):
+        """Fused batch-norm forward + activation (tnh_bn_forward)."""
+        call("tnh_bn_forward", dstSize, N, batch, addr(x), addr(xNorm), addr(out), addr(mean), addr(variance),
+             addr(scales), addr(biases), activation)
+
     def blockNormalize(self, dstSize, dst, offset, N, mean, variance, batch):
         call("tnh_bn_normalize", dstSize, addr(dst), offset, N, addr(mean), addr(variance), batch)
 
     # -- training direction ----------------------------------------------------
+    def bnStatistics(self, srcSize, dstSize, groups, src, offset, means, vars, rollingMeans, rollingVars,
+                     momentum):
+        """meansAndVars + the rolling-statistics update in one call (tnh_bn_statistics)."""
+        call("tnh_bn_statistics", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars),
+             addr(rollingMeans), addr(rollingVars), momentum)
+
     def meansAndVars(self, srcSize, dstSize, groups, src, offset, means, vars):
         call("tnh_means_vars", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
 

@@ -9,7 +9,8 @@ Plays TNNet.trainEpoch for one batch (nnet.pas:474-530: Propagate = forward
 with the layer semantics of the reference CPU path:
   * TConvolutionalLayer.forward with batch norm in training mode
     (nConvolutionLayer.pas:457-566, TBaseLayer.batchNorm nbaselayer.pas:336-370):
-    conv, MeansAndVars, rolling statistics, normalize, scale, bias, leaky;
+    conv, MeansAndVars, rolling statistics, then normalize, scale, bias and
+    leaky in one pass (tnh_bn_forward, bit-identical to the separate passes);
   * TConvolutionalLayer.backward (nConvolutionLayer.pas:571-671): leaky
     derivative, batchNormBack (nbaselayer.pas:372-392), im2col, weight
     gradient, W^T * delta, col2im; the first layer computes no input delta;
@@ -120,20 +121,13 @@ class CifarTrainer:
             y = t[f"x{i}"]
             hip.conv2dForward(B, c, hh, hh, f, 3, 1, 1, h, 0, self.packed[i], None, acLINEAR, y, 0,
                               weightLayout=WEIGHTS_TAP_MAJOR)
-            hip.meansAndVars(n, f, B, y, 0, t[f"mean{i}"], t[f"var{i}"])
-            bm = float(np.float32(self.bnm))
-            keep = float(np.float32(1) - np.float32(self.bnm))
-            hip.scale(f, keep, p[f"rm{i}"], 1)
-            hip.axpy(f, bm, t[f"mean{i}"], 0, 1, p[f"rm{i}"], 0, 1)
-            hip.scale(f, keep, p[f"rv{i}"], 1)
-            hip.axpy(f, bm, t[f"var{i}"], 0, 1, p[f"rv{i}"], 0, 1)
+            # MeansAndVars, then rolling = (1 - m) * rolling, rolling = axpy(m, stat)
+            hip.bnStatistics(n, f, B, y, 0, t[f"mean{i}"], t[f"var{i}"], p[f"rm{i}"], p[f"rv{i}"],
+                             float(np.float32(self.bnm)))
             xn, out = t[f"xn{i}"], t[f"out{i}"]
-            hip.copy(n, y, 0, 1, xn, 0, 1)
-            hip.blockNormalize(n, xn, 0, f, t[f"mean{i}"], t[f"var{i}"], B)
-            hip.copy(n, xn, 0, 1, out, 0, 1)
-            hip.forwardScale(n, out, 0, f, p[f"s{i}"], 1, B)
-            hip.forwardBias(n, out, 0, f, p[f"b{i}"], 1, B)
-            hip.ActivateArray(n, out, 0, acLEAKY)
+            # x (y) is kept as the layer's pre-normalization copy; one pass
+            # writes x_norm and act(scale * x_norm + bias)
+            hip.bnForward(n, f, B, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"], acLEAKY)
             if i < len(self.dims) - 1:
                 ph = hh // 2
                 hip.forwardMaxPool(B, f, ph, ph, out, f, hh, hh, 2, 2, 0, 2, t[f"pidx{i}"], t[f"pool{i}"])

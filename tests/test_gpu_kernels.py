@@ -85,6 +85,80 @@ def test_sgemm_full_size_exact(hip, ta, tb):
     assert np.array_equal(H(dC, hip), ref.astype(np.float32))
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_sgemm_8192_exact(hip, ta, tb):
+    """BASELINE config 2's largest square size in all four variants (the
+    bench's 8192^3 lines): integer operands in [-2, 2] keep every partial sum
+    below 2^24, so the product is exact in fp32 and must equal a float64
+    product bit for bit."""
+    M = N = K = 8192
+    case(f"sgemm 8192^3 int ta={ta} tb={tb}")
+    g = torch.Generator(device="cuda").manual_seed(8192 + 2 * ta + tb)
+    dA = torch.randint(-2, 3, (M, K), generator=g, device="cuda").float()
+    dB = torch.randint(-2, 3, (K, N), generator=g, device="cuda").float()
+    dC = torch.full((M, N), 5.0, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, dA.shape[1], dB, 0, dB.shape[1], 0.0, dC, 0, N)
+    hip.finish()
+    a64 = dA.double().T if ta else dA.double()
+    b64 = dB.double().T if tb else dB.double()
+    ref = (a64 @ b64).float()
+    assert torch.equal(dC, ref)
+
+
+# the conv-shaped skinny GEMMs of BASELINE config 2 (M = F, N = OH*OW*16,
+# K = 9*C): the bench times all five
+SKINNY = [(64, 692224, 288), (128, 173056, 576), (256, 43264, 1152), (512, 10816, 2304), (1024, 2704, 4608)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY)
+def test_sgemm_skinny_bench_shapes(hip, M, N, K):
+    """The bench's skinny shapes, NN: exact on integer operands at full size,
+    and random U[-1, 1) operands against the oracle (16 rows of A: the
+    oracle's per-row FMA chains do not depend on the other rows)."""
+    case(f"sgemm skinny int {M}x{N}x{K}")
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    dA = torch.randint(-2, 3, (M, K), generator=g, device="cuda").float()
+    dB = torch.randint(-2, 3, (K, N), generator=g, device="cuda").float()
+    dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.gemm(0, 0, M, N, K, 1.0, dA, 0, K, dB, 0, N, 0.0, dC, 0, N)
+    hip.finish()
+    assert torch.equal(dC, (dA.double() @ dB.double()).float())
+    del dA, dB, dC
+    case(f"sgemm skinny rand {M}x{N}x{K} vs oracle")
+    A = synth.uniform(31, (M, K), -1, 1)
+    B = synth.uniform(32, (K, N), -1, 1)
+    dA, dB = D(A), D(B)
+    dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    hip.gemm(0, 0, M, N, K, 1.0, dA, 0, K, dB, 0, N, 0.0, dC, 0, N)
+    got = H(dC, hip)
+    rows = np.linspace(0, M - 1, 16).astype(np.int64)
+    ref = np.zeros((16, N), np.float32)
+    R.sgemm(0, 0, 16, N, K, 1.0, np.ascontiguousarray(A[rows]), K, B, N, 0.0, ref, N)
+    assert R.rel_err(got[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_sgemm_alpha_half_beta_one_full_size(hip, ta, tb):
+    """The config-2 beta = 1 / alpha = 0.5 run at 4096^3: integer operands, so
+    0.5 * sum + C is exact whatever the order (the reference scales A by
+    alpha first, ntensors.pas:2136-2206)."""
+    M = N = K = 4096
+    case(f"sgemm alpha 0.5 beta 1 int ta={ta} tb={tb} 4096^3")
+    g = torch.Generator(device="cuda").manual_seed(77 + ta + tb)
+    dA = torch.randint(-3, 4, (M, K), generator=g, device="cuda").float()
+    dB = torch.randint(-3, 4, (K, N), generator=g, device="cuda").float()
+    C0 = torch.randint(-50, 51, (M, N), generator=g, device="cuda").float()
+    dC = C0.clone()
+    torch.cuda.synchronize()
+    hip.gemm(ta, tb, M, N, K, 0.5, dA, 0, K, dB, 0, N, 1.0, dC, 0, N)
+    hip.finish()
+    a64 = dA.double().T if ta else dA.double()
+    b64 = dB.double().T if tb else dB.double()
+    assert torch.equal(dC, (0.5 * (a64 @ b64) + C0.double()).float())
+
+
 def test_sgemm_alpha_beta_offsets_ld(hip):
     case("sgemm alpha/beta, offsets, padded ld")
     rng = np.random.default_rng(5)
@@ -393,13 +467,55 @@ def test_conv_fused_shortcut_and_strided_io(hip):
     assert np.array_equal(got[:, 32:], H(plain, hip) + res)
 
 
+def test_conv_tuned_dense_then_output_beyond_2gib(hip):
+    """A shape tuned with a dense output, then called with an output batch
+    stride that puts image 1 beyond 2 GiB: the lean kernels cannot address
+    that output, so the cached choice must not be reused (integer data: every
+    tiling gives the same exact sums, so both outputs are compared bit for
+    bit)."""
+    case("conv tuned dense, then output beyond 2 GiB")
+    B, Cc, Hh, F = 2, 64, 26, 64
+    rng = np.random.default_rng(2024)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * 9)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    dx, dW, db = D(x), D(Wt), D(b)
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, 3, dW, packed)
+    dense = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, 1, 1, dx, 0, packed, db, acLINEAR, dense, 0,
+                      weightLayout=WEIGHTS_TAP_MAJOR)
+    want = H(dense, hip)
+    stride = (1 << 29) + 64  # floats: image 1 starts 2 GiB + 256 B into the buffer
+    big = torch.zeros(stride + F * Hh * Hh, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, 1, 1, dx, 0, packed, db, acLINEAR, big, 0, outBatchStride=stride,
+                      weightLayout=WEIGHTS_TAP_MAJOR)
+    hip.finish()
+    img0 = big[:F * Hh * Hh].cpu().numpy().reshape(F, Hh, Hh)
+    img1 = big[stride:].cpu().numpy().reshape(F, Hh, Hh)
+    assert np.array_equal(img0, want[0])
+    assert np.array_equal(img1, want[1])
+    ref = R.conv_forward(x, Wt, b, 3, 1, 1, acLINEAR)
+    assert np.array_equal(want, ref)
+
+
 # ------------------------------------------------------- pool / upsample ----
-@pytest.mark.parametrize("size,stride,pad", [(2, 2, 0), (3, 2, 0), (2, 1, 1), (3, 1, 2), (5, 1, 4)])
-def test_maxpool_forward_backward_bit_exact(hip, size, stride, pad):
-    case(f"maxpool size{size} stride{stride} pad{pad}")
-    B, Cc, Hh, W = 2, 5, 19, 16
+@pytest.mark.parametrize("size,stride,pad,shape", [(2, 2, 0, (2, 5, 19, 16)), (3, 2, 0, (2, 5, 19, 16)),
+                                                   (2, 1, 1, (2, 5, 19, 16)), (3, 1, 2, (2, 5, 19, 16)),
+                                                   (5, 1, 4, (2, 5, 19, 16)), (2, 2, 0, (3, 4, 10, 18)),
+                                                   (2, 2, 1, (2, 3, 12, 12)), (2, 2, 0, (2, 3, 9, 7)),
+                                                   (2, 2, 0, (128, 32, 32, 32))])
+def test_maxpool_forward_backward_bit_exact(hip, size, stride, pad, shape):
+    """Values, int64 indices and the backward scatter-add, bit-exact; the
+    2x2/2 shapes cover the paired kernels (16- and 8-byte input loads, the
+    config-3 layer) and the general kernel (odd width)."""
+    case(f"maxpool size{size} stride{stride} pad{pad} {shape}")
+    B, Cc, Hh, W = shape
     x = synth.normal(61, (B, Cc, Hh, W))
     x[0, 0, :4, :4] = 1.0  # ties
+    x[-1, -1, :2, :2] = -np.inf  # a window of -inf: -MaxSingle, index -1
+    x[0, -1, 2, 3] = np.nan
     out, idx = R.maxpool_fwd(x, size, stride, stride, pad)
     _, _, OH, OW = out.shape
     dout = torch.empty(out.shape, dtype=torch.float32, device="cuda")
@@ -500,6 +616,33 @@ def test_yolo_head_bit_exact(hip):
     assert np.array_equal(H(dout, hip), ref)
 
 
+def test_yolo_logistic_pinned_values(hip):
+    """The yolo kernels (NCHW and channels-last) on the committed exact-mode
+    logistic table (hand-derivable cases, the clamps, +-inf, fraction-1/2
+    points; test_oracle_logistic.py) and NaN: bit for bit."""
+    from tests.test_oracle_logistic import TABLE, from_bits
+
+    case("yolo logistic pinned values")
+    vals = np.array([from_bits(xb) for xb, _ in TABLE] + [np.nan], np.float32)
+    P = vals.size
+    x = np.zeros((1, 6, 1, P), np.float32)  # one anchor, one class: entries 0, 1, 4, 5 get the logistic
+    for e in (0, 1, 4, 5):
+        x[0, e, 0] = vals
+    want = np.array([yb for _, yb in TABLE], np.uint32)
+    dout = torch.empty(x.shape, dtype=torch.float32, device="cuda")
+    hip.yoloForward(1, 1, 1, 1, P, D(x), dout)
+    got = H(dout, hip)
+    xn = np.ascontiguousarray(x.transpose(0, 2, 3, 1))  # [1][1][P][6] channels-last
+    dout2 = torch.empty(x.shape, dtype=torch.float32, device="cuda")
+    hip.yoloForwardNHWC(1, 1, 1, 1, P, D(xn), 0, 6, dout2)
+    got2 = H(dout2, hip)
+    for g in (got, got2):
+        for e in (0, 1, 4, 5):
+            assert np.array_equal(g[0, e, 0, :-1].view(np.uint32), want), e
+            assert np.isnan(g[0, e, 0, -1])
+        assert np.array_equal(g[0, 2:4], x[0, 2:4])
+
+
 def test_bn_normalize_vs_oracle_exact(hip):
     case("bn normalize (exact division)")
     B, F, P = 2, 6, 40
@@ -510,6 +653,73 @@ def test_bn_normalize_vs_oracle_exact(hip):
     dx = D(x)
     hip.blockNormalize(x.size, dx, 0, F, D(mean), D(var), B)
     assert np.array_equal(H(dx, hip), R.bn_normalize(x.copy(), mean, var, B, exact=True))
+
+
+@pytest.mark.parametrize("B,F,P", [(2, 6, 40), (3, 5, 1), (2, 7, 9), (4, 16, 64)])
+def test_normalize_tnncuda_signature(hip, B, F, P):
+    """TNNCuda.normalize's argument list (srcSize = channels, dstSize,
+    groups = batch, strided statistics, destination offset) with the CPU
+    clamps, bit-exact against the oracle: blocks of one element clamp the
+    variance, longer blocks the standard deviation; NaN and zero variances."""
+    case(f"normalize (TNNCuda signature) B{B} F{F} P{P}")
+    x = synth.normal(120, (B, F, P))
+    mean = synth.normal(121, (2 * F,))
+    var = synth.uniform(122, (3 * F,), 0.1, 3.0)
+    var[0], var[3] = 0.0, np.nan
+    ref = R.bn_normalize(x.copy(), np.ascontiguousarray(mean[::2]), np.ascontiguousarray(var[::3]), B)
+    buf = np.concatenate([np.full(5, 9.0, np.float32), x.ravel()])
+    dbuf = D(buf)
+    hip.normalize(F, x.size, B, D(mean), 2, D(var), 3, dbuf, 5)
+    got = H(dbuf, hip)
+    assert np.array_equal(got[:5], buf[:5])
+    assert np.array_equal(got[5:].reshape(x.shape), ref, equal_nan=True)
+
+
+@pytest.mark.parametrize("B,F,P", [(2, 6, 40), (3, 5, 1), (1, 7, 9)])
+def test_forward_scale_add_bit_exact(hip, B, F, P):
+    """TNNCuda.forwardScaleAdd = the CPU's forwardScale then forwardBias."""
+    case(f"forward scale add B{B} F{F} P{P}")
+    x = synth.normal(123, (B, F, P))
+    sc = synth.normal(124, (F,))
+    bi = synth.normal(125, (F,))
+    ref = R.forward_bias(R.forward_scale(x.copy(), sc, B), bi, B)
+    dx = D(x)
+    hip.forwardScaleAdd(x.size, dx, 0, F, D(sc), D(bi), 1, B)
+    assert np.array_equal(H(dx, hip), ref)
+
+
+@pytest.mark.parametrize("B,F,P,act,norm", [(4, 32, 1024, acLEAKY, True), (3, 5, 7, acLEAKY, True),
+                                            (2, 10, 1, acLINEAR, False), (2, 64, 64, acLOGISTIC, True)])
+def test_bn_forward_equals_the_reference_sequence(hip, B, F, P, act, norm):
+    """tnh_bn_forward == copy, blockNormalize, copy, forwardScale,
+    forwardBias, activate (nbaselayer.pas:335-368 + the layer activation) on
+    the GPU, bit for bit, and == the oracle's normalize / scale / bias /
+    activation."""
+    case(f"bn forward B{B} F{F} P{P} act{act} xnorm{norm}")
+    x = synth.normal(126, (B, F, P))
+    mean = synth.normal(127, (F,))
+    var = synth.uniform(128, (F,), 0.1, 3.0)
+    var[0] = 0.0
+    sc, bi = synth.normal(129, (F,)), synth.normal(130, (F,))
+    xn_ref = R.bn_normalize(x.copy(), mean, var, B)
+    out_ref = R.activate(R.forward_bias(R.forward_scale(xn_ref.copy(), sc, B), bi, B), act)
+    dx, dm, dv, ds, db = D(x), D(mean), D(var), D(sc), D(bi)
+    dxn = torch.empty_like(dx) if norm else None
+    dout = torch.empty_like(dx)
+    hip.bnForward(x.size, F, B, dx, dxn, dout, dm, dv, ds, db, act)
+    seq = dx.clone()
+    hip.blockNormalize(x.size, seq, 0, F, dm, dv, B)
+    seqn = seq.clone()
+    hip.forwardScale(x.size, seq, 0, F, ds, 1, B)
+    hip.forwardBias(x.size, seq, 0, F, db, 1, B)
+    hip.ActivateArray(x.size, seq, 0, act)
+    got = H(dout, hip)
+    assert np.array_equal(got, H(seq, hip))
+    if act != acLOGISTIC:  # the oracle's logistic is the reference polynomial, the layer activation is expf
+        assert np.array_equal(got, out_ref)
+    if norm:
+        assert np.array_equal(H(dxn, hip), xn_ref)
+        assert np.array_equal(H(dxn, hip), H(seqn, hip))
 
 
 # --------------------------------------------------------------- errors ----

@@ -54,6 +54,61 @@ def test_means_vars(hip, shape):
     assert R.rel_err(H(dv, hip), v_ref) <= TOL
 
 
+@pytest.mark.parametrize("shape,off", [((128, 64, 16, 16), 0), ((1, 8, 300, 300), 0), ((3, 5, 33, 17), 1),
+                                       ((64, 10, 1, 1), 0)])
+def test_channel_reductions_large_and_ragged(hip, shape, off):
+    """The multi-workgroup channel reductions (statistics, their deltas,
+    addDots) on many workgroups per channel, rows longer than one unit
+    (90 000 floats), an unaligned offset (scalar loads) and one element per
+    channel: within the per-tensor bound of the oracle's float64 sums, and
+    identical bits on a second call (fixed summation order)."""
+    case(f"channel reductions {shape} offset {off}")
+    B, Cc = shape[:2]
+    x = synth.normal(310, shape, 1.5) + np.float32(0.5)
+    d = synth.normal(311, shape)
+    m_ref, v_ref = T.means_vars(x, Cc, B)
+    md_ref, vd_ref = T.means_vars_delta(d, x, m_ref, v_ref, B)
+    acc0 = synth.normal(312, (Cc,))
+    dots_ref = T.add_dots(acc0, x, d, B)
+    dx = D(np.concatenate([np.zeros(off, np.float32), x.ravel()]))
+    dd = D(np.concatenate([np.zeros(off, np.float32), d.ravel()]))
+    res = []
+    for _ in range(2):
+        dm, dv, dmd, dvd = (torch.empty(Cc, dtype=torch.float32, device="cuda") for _ in range(4))
+        dacc = D(acc0)
+        hip.meansAndVars(x.size, Cc, B, dx, off, dm, dv)
+        hip.meansAndVarsDelta(d.size, Cc, B, dd, dx, off, D(m_ref), D(v_ref), dmd, dvd)
+        hip.addDots(x.size, Cc, B, dx, dd, off, dacc)
+        res.append([H(t, hip) for t in (dm, dv, dmd, dvd, dacc)])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+    m, v, md, vd, dots = res[0]
+    for got, ref in ((m, m_ref), (v, v_ref), (md, md_ref), (vd, vd_ref), (dots, dots_ref)):
+        assert R.rel_err(got, ref) <= TOL
+
+
+def test_bn_statistics_equals_the_reference_sequence(hip):
+    """tnh_bn_statistics == meansAndVars, then rolling.Multiply(1 - m) and
+    rolling.axpy(m, stat) (nbaselayer.pas:351-355), bit for bit."""
+    case("bn statistics + rolling update")
+    B, Cc = 32, 48
+    x = synth.normal(313, (B, Cc, 12, 12), 2.0)
+    rm0, rv0 = synth.normal(314, (Cc,)), synth.uniform(315, (Cc,), 0.5, 2.0)
+    mom = float(np.float32(0.1))
+    keep = float(np.float32(1) - np.float32(0.1))
+    dx = D(x)
+    dm, dv, dm2, dv2 = (torch.empty(Cc, dtype=torch.float32, device="cuda") for _ in range(4))
+    rm, rv, rm2, rv2 = D(rm0), D(rv0), D(rm0), D(rv0)
+    hip.bnStatistics(x.size, Cc, B, dx, 0, dm, dv, rm, rv, mom)
+    hip.meansAndVars(x.size, Cc, B, dx, 0, dm2, dv2)
+    hip.scale(Cc, keep, rm2, 1)
+    hip.axpy(Cc, mom, dm2, 0, 1, rm2, 0, 1)
+    hip.scale(Cc, keep, rv2, 1)
+    hip.axpy(Cc, mom, dv2, 0, 1, rv2, 0, 1)
+    for a, b in ((dm, dm2), (dv, dv2), (rm, rm2), (rv, rv2)):
+        assert np.array_equal(H(a, hip), H(b, hip))
+
+
 def test_bn_backward_kernels(hip):
     case("means_vars_delta / normalize_delta / add_dots")
     B, Cc, Hh = 16, 24, 9

@@ -12,6 +12,7 @@ import torch
 from oracle import netref
 from oracle import refcpu as R
 from tensorium_amd import darknet, synth
+from tensorium_amd.nnhip import acLEAKY
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -89,12 +90,20 @@ def test_yolov3_416_batch1_heads(hip, yolo):
 
 
 def test_yolov3_fusion_is_exact(hip, yolo):
-    """Shortcut fused into the conv epilogue == separate addvv, bit for bit."""
+    """Shortcut fused into the conv epilogue == separate addvv, bit for bit,
+    when both networks run the same tilings: with autotuning off the cost
+    model picks each layer's tiling from its GEMM shape alone (the tuner
+    times a convolution with and without a residual separately, so its
+    choices, and the summation order, may differ between the two)."""
     layers, W = yolo
     print("[case] yolov3 fused vs unfused", flush=True)
     x = synth.uniform(8, (1, 3, 416, 416))
-    _, a = run_gpu(hip, layers, W, x, fuse=True)
-    _, b = run_gpu(hip, layers, W, x, fuse=False)
+    hip.setConvAutotune(False, -1)
+    try:
+        _, a = run_gpu(hip, layers, W, x, fuse=True)
+        _, b = run_gpu(hip, layers, W, x, fuse=False)
+    finally:
+        hip.setConvAutotune(True, -1)
     for u, v in zip(a, b):
         assert np.array_equal(u, v)
 
@@ -204,12 +213,12 @@ def test_yolov3_nhwc_matches_nchw_and_replays(hip, yolo):
 def test_yolov3_416_b16_bench_config(hip, yolo):
     """The benchmark's own configuration: YOLOv3-416 at batch 16,
     channels-last, autotuned for batch-16 shapes (tail splits included).
-    Images 0, 7 and 15 of the batch equal batch-1 NCHW runs of the same
-    images (checked against the oracle layer by layer above) at the three
-    head convolutions within the per-tensor bound, and two graph replays of
-    the batch-16 forward equal its eager result bit for bit."""
+    Images 0, 7 and 15 of the batch against the CPU oracle run on the same
+    image: the three pre-logistic head convolutions within the per-tensor
+    1e-5 bound.  Two graph replays of the batch-16 forward equal its eager
+    result bit for bit."""
     layers, W = yolo
-    print("[case] yolov3-416 batch 16 nhwc (bench configuration) vs batch-1 nchw, graph replay", flush=True)
+    print("[case] yolov3-416 batch 16 nhwc (bench configuration) vs the oracle, graph replay", flush=True)
     x = synth.uniform(13, (16, 3, 416, 416))
     dx = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
@@ -217,15 +226,14 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
     eager = [h.cpu().numpy() for h in big.forward(dx)]
     hip.finish()
     heads16 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
-    one = darknet.Network(hip, layers, 1, W)
     for img in (0, 7, 15):
-        xi = torch.from_numpy(np.ascontiguousarray(x[img:img + 1])).cuda()
-        torch.cuda.synchronize()
-        one.forward(xi)
-        hip.finish()
+        print(f"[case] oracle forward of image {img}", flush=True)
+        ref = netref.forward(layers, W, np.ascontiguousarray(x[img:img + 1]))
         for i in (81, 93, 105):
-            e = R.rel_err(heads16[i][img:img + 1], one.output(i).cpu().numpy())
-            assert e <= 2 * TOL, (img, i, e)
+            e = R.rel_err(heads16[i][img:img + 1], ref[i])
+            print(f"image {img} head conv {i}: {e:.3e}", flush=True)
+            assert e <= TOL, (img, i, e)
+        del ref
     try:
         big.capture(dx)
         for rep in range(2):
@@ -239,13 +247,48 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
         hip.useTorchStream()
 
 
+def f64_heads(layers, W, x, heads=(81, 93, 105)):
+    """The network evaluated in float64 with torch on the CPU (conv2d,
+    leaky 0.1, shortcut add, channel concat, nearest upsample): the head
+    convolutions of an fp32 chain free of rounding, as a library-routine
+    reference."""
+    import torch.nn.functional as Fn
+
+    outs, prev = [], torch.from_numpy(x).double()
+    for L in layers:
+        t = L["type"]
+        if t == "convolutional":
+            w, b = W[L["index"]]
+            F, k, C = L["filters"], L["size"], L["in"][0]
+            y = Fn.conv2d(prev, torch.from_numpy(w).double().reshape(F, C, k, k), torch.from_numpy(b).double(),
+                          stride=L["stride"], padding=L["pad"])
+            if L["act"] == acLEAKY:
+                y = torch.where(y < 0, 0.1 * y, y)
+        elif t == "shortcut":
+            y = prev + outs[L["src"]]
+        elif t == "route":
+            y = torch.cat([outs[s_] for s_ in L["srcs"]], 1)
+        elif t == "upsample":
+            y = prev.repeat_interleave(L["stride"], 2).repeat_interleave(L["stride"], 3)
+        else:
+            y = prev
+        outs.append(y)
+        prev = y
+    return {i: outs[i].numpy() for i in heads}
+
+
 def test_yolov3_608_b32_bench_config(hip):
     """BASELINE config 5 at its size: YOLOv3-608 at batch 32, channels-last
-    and autotuned for those shapes; images 0 and 31 equal batch-1 NCHW runs
-    of the same images at the three head convolutions within the bound."""
+    and autotuned for those shapes; images 0 and 31 against the CPU oracle
+    run on the same image and against the float64 evaluation of the same
+    network.  After 105 layers at 608x608 the oracle's own fp32 rounding
+    is 5-7e-6 of the head magnitudes (measured against float64), so the
+    GPU-oracle difference of two independent fp32 chains reaches ~1e-5:
+    the heads are held within 1e-5 of the float64 result and within 1.5e-5
+    of the oracle."""
     _, layers = darknet.load_cfg("yolov3.cfg", 608, 608)
     W = darknet.synthetic_weights(layers)
-    print("[case] yolov3-608 batch 32 nhwc vs batch-1 nchw", flush=True)
+    print("[case] yolov3-608 batch 32 nhwc vs the oracle", flush=True)
     x = synth.uniform(17, (32, 3, 608, 608))
     dx = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
@@ -254,12 +297,52 @@ def test_yolov3_608_b32_bench_config(hip):
     hip.finish()
     heads32 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
     del big
-    one = darknet.Network(hip, layers, 1, W)
     for img in (0, 31):
-        xi = torch.from_numpy(np.ascontiguousarray(x[img:img + 1])).cuda()
-        torch.cuda.synchronize()
-        one.forward(xi)
-        hip.finish()
+        print(f"[case] oracle and float64 forwards of image {img} at 608", flush=True)
+        xi = np.ascontiguousarray(x[img:img + 1])
+        ref = netref.forward(layers, W, xi)
+        r64 = f64_heads(layers, W, xi)
         for i in (81, 93, 105):
-            e = R.rel_err(heads32[i][img:img + 1], one.output(i).cpu().numpy())
-            assert e <= 2 * TOL, (img, i, e)
+            e = R.rel_err(heads32[i][img:img + 1], ref[i])
+            e64 = R.rel_err(heads32[i][img:img + 1], r64[i])
+            o64 = R.rel_err(ref[i], r64[i])
+            print(f"image {img} head conv {i}: vs oracle {e:.3e}, vs float64 {e64:.3e} "
+                  f"(oracle vs float64 {o64:.3e})", flush=True)
+            assert e64 <= TOL, (img, i, e64)
+            assert e <= 1.5 * TOL, (img, i, e)
+        del ref
+
+
+@pytest.mark.parametrize("B", [2, 16])
+def test_yolov3_reference_route_mode(hip, yolo, B):
+    """The reference's whole-tensor route concat (nconcatlayer.pas:115 ->
+    ntensors.pas:12045: every input's whole batched tensor copied back to
+    back, which mixes images at batch > 1), NCHW network at batch 2 and 16,
+    against the oracle run in the same mode on the whole batch: the three
+    head convolutions within 1e-5, and at least one head differs from the
+    per-image (darknet) concat by more than that bound."""
+    layers, W = yolo
+    print(f"[case] yolov3-416 batch {B} route_mode=reference vs the oracle", flush=True)
+    x = synth.uniform(19 + B, (B, 3, 416, 416))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    n = darknet.Network(hip, layers, B, W, route_mode="reference")
+    n.forward(dx)
+    hip.finish()
+    got = {i: n.output(i).cpu().numpy() for i in (81, 93, 105)}
+    del n
+    ref = netref.forward(layers, W, x, route_mode="reference")
+    for i in (81, 93, 105):
+        e = R.rel_err(got[i], ref[i])
+        print(f"batch {B} head conv {i}: {e:.3e}", flush=True)
+        assert e <= TOL, (i, e)
+    per_image = darknet.Network(hip, layers, B, W)
+    per_image.forward(dx)
+    hip.finish()
+    assert max(R.rel_err(per_image.output(i).cpu().numpy(), got[i]) for i in (93, 105)) > 10 * TOL
+
+
+def test_nhwc_rejects_reference_route_mode(hip, yolo):
+    layers, W = yolo
+    with pytest.raises(NotImplementedError):
+        darknet.Network(hip, layers, 2, W, layout="nhwc", route_mode="reference")

@@ -263,6 +263,22 @@ def test_maxpool_ties_and_empty_window():
     assert out[0, 0, 0, 0] == -np.finfo(np.float32).max and idx[0, 0, 0, 0] == -1
 
 
+def test_maxpool_backward_skips_empty_windows():
+    """An index of -1 (a window with no tap above -MaxSingle) contributes
+    nothing: the reference's loop would add into element -1, outside the
+    tensor.  The guard in front of the oracle's buffer stays untouched."""
+    x = np.full((1, 1, 4, 4), -np.inf, np.float32)
+    x[0, 0, 2:, 2:] = 1.0
+    _, idx = R.maxpool_fwd(x, 2, 2, 2, 0)
+    assert (idx == -1).sum() == 3
+    buf = np.zeros(1 + x.size, np.float32)
+    buf[0] = 7.0  # element -1 of the view below
+    dIn = buf[1:]
+    R.maxpool_bwd(idx, np.full(idx.shape, 2.0, np.float32), dIn)
+    assert buf[0] == 7.0
+    assert dIn.sum() == 2.0 and dIn[idx[0, 0, 1, 1]] == 2.0
+
+
 def test_maxpool_backward_scatter():
     rng = np.random.default_rng(11)
     x = rng.standard_normal((2, 2, 6, 6)).astype(np.float32)
@@ -307,6 +323,10 @@ def test_bn_normalize_and_fuse():
     d = np.maximum(np.sqrt(var.astype(np.float64)), 1e-6)
     ref = (x - mean[None, :, None, None].astype(np.float64)) / d[None, :, None, None]
     assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 2 ** -22
+    # NaN variance: Pascal's Max(d, eps) = d > eps ? d : eps gives eps
+    xn = np.ones((1, 2, 2, 2), np.float32)
+    got_nan = R.bn_normalize(xn.copy(), np.zeros(2, np.float32), np.array([np.nan, 4.0], np.float32), 1)
+    assert np.all(got_nan[0, 0] == np.float32(1e6)) and np.all(got_nan[0, 1] == np.float32(0.5))
     faithful = R.bn_normalize(x.copy(), mean, var, 2, exact=False)  # rcpss: ~12 bits
     assert np.max(np.abs(faithful - ref) / np.maximum(np.abs(ref), 1)) < 1.5 * 2 ** -12 * 4
     # folding: conv(W') + b' == BN(conv(W) + b) within the per-tensor tolerance
@@ -360,3 +380,73 @@ def test_yolo_head_entries():
     assert np.array_equal(o[:, :, 2:4], xr[:, :, 2:4])  # w, h untouched
     sig = R.activate(xr[:, :, [0, 1, 4, 5, 6]].copy(), 0)
     assert np.array_equal(o[:, :, [0, 1, 4, 5, 6]], sig)
+
+
+# ------------------------------------------------------------ route -------
+_ROUTE_CFG = """[net]
+height=6
+width=6
+channels=2
+[convolutional]
+filters=3
+size=3
+pad=1
+activation=leaky
+[convolutional]
+filters=2
+size=1
+activation=linear
+[route]
+layers=-1,-2
+"""
+
+
+def test_netref_reference_route_is_whole_tensor_concat():
+    """TConcatLayer.forward -> TTensor.concat (nconcatlayer.pas:115,
+    ntensors.pas:12045-12058): each input's whole batched tensor is copied
+    at the running offset, so with inputs of n0 and n1 floats per image the
+    first element of input 1 lands at flat offset B*n0, and image b of the
+    route output (as [B, C, H, W]) holds floats [b*(n0+n1), (b+1)*(n0+n1))
+    of that stream.  At batch 1 this is the per-image concat."""
+    from oracle import netref
+    from tensorium_amd import darknet
+
+    _, layers = darknet.parse_cfg(_ROUTE_CFG)
+    W = darknet.synthetic_weights(layers, seed=3)
+    B = 3
+    x = np.random.default_rng(40).uniform(0, 1, (B, 2, 6, 6)).astype(np.float32)
+    ref = netref.forward(layers, W, x, route_mode="reference")
+    img = netref.forward(layers, W, x, route_mode="image")
+    src0, src1 = ref[1], ref[0]  # layers=-1,-2 from layer 2: layer 1, then layer 0
+    n0, n1 = src0[0].size, src1[0].size
+    flat = ref[2].ravel()
+    assert ref[2].shape == (B, 5, 6, 6)
+    assert flat[B * n0] == src1.ravel()[0]
+    assert np.array_equal(flat[:B * n0], src0.ravel()) and np.array_equal(flat[B * n0:], src1.ravel())
+    for b in range(B):  # image b's slice of the stream
+        assert np.array_equal(ref[2][b].ravel(), flat[b * (n0 + n1):(b + 1) * (n0 + n1)])
+    # per-image concat: image b = [src0[b] | src1[b]]; differs at B > 1
+    for b in range(B):
+        assert np.array_equal(img[2][b].ravel(), np.concatenate([src0[b].ravel(), src1[b].ravel()]))
+    assert not np.array_equal(img[2], ref[2])
+    one_r = netref.forward(layers, W, x[:1], route_mode="reference")
+    one_i = netref.forward(layers, W, x[:1], route_mode="image")
+    assert np.array_equal(one_r[2], one_i[2])
+
+
+def test_bn_normalize_one_element_per_channel_clamps_the_variance():
+    """blockNormalize with blockSize 1 (a connected layer's batch norm) goes
+    through _snormvv (ntensors.pas:4338): (x - m) / sqrt(max(v, 1e-6)), where
+    longer blocks clamp the standard deviation.  With v = 0 the two differ by
+    a factor 1000: 1/sqrt(1e-6f) against 1/1e-6f."""
+    x = np.ones((3, 4, 1, 1), np.float32)
+    mean = np.zeros(4, np.float32)
+    var = np.array([0.0, 4.0, np.nan, 1e-7], np.float32)
+    got = R.bn_normalize(x.copy(), mean, var, 3).reshape(3, 4)
+    d_eps = np.sqrt(np.float32(1e-6))
+    want = np.array([np.float32(1) / d_eps, np.float32(0.5), np.float32(1) / d_eps, np.float32(1) / d_eps],
+                    np.float32)
+    assert np.array_equal(got, np.tile(want, (3, 1)))
+    assert want[0] != np.float32(1e6)
+    blk = R.bn_normalize(np.ones((1, 4, 1, 2), np.float32), mean, var, 1)
+    assert blk[0, 0, 0, 0] == np.float32(1) / np.float32(1e-6)
