@@ -195,6 +195,33 @@ int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W,
                             const float *bias, int64_t biasOff, int32_t act,
                             const float *residual, int64_t rOff, int64_t rPix,
                             float *out, int64_t outOff, int64_t outPix);
+/* No reference counterpart: tnh_conv2d_fwd_nhwc for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, results and kernels;
+ * it calls no hipMalloc / hipFree / allocating library routine:
+ *  - the K pieces of tail-split or split-K tiles go to a fixed device array
+ *    of tnh_conv2d_noalloc_scratch_bytes() bytes (64 MiB) that each device
+ *    holds from tnh_init until the process ends; a call whose tiling needs
+ *    more fails with TNH_ERR_INVALID_ARG and launches nothing;
+ *  - it never autotunes (a timing graph allocates): it runs the tiling forced
+ *    by tnh_conv2d_set_autotune, else the one tnh_conv2d_fwd_nhwc tuned for
+ *    the same call, else the cost model's choice, so after one tuning call of
+ *    tnh_conv2d_fwd_nhwc its output equals that entry point's bit for bit.
+ * Every call on a device shares that device's array and the array keeps the
+ * last call's contents (nothing in it needs to start at zero): calls that
+ * overlap on one device (several streams or host threads) race. */
+int32_t tnh_conv2d_fwd_nhwc_noalloc(int64_t batch, int64_t C, int64_t H,
+                                    int64_t W, int64_t F, int64_t kh,
+                                    int64_t kw, int64_t pH, int64_t pW,
+                                    int64_t sY, int64_t sX, const float *x,
+                                    int64_t xOff, int64_t xPix,
+                                    const float *weights, int64_t wOff,
+                                    const float *bias, int64_t biasOff,
+                                    int32_t act, const float *residual,
+                                    int64_t rOff, int64_t rPix, float *out,
+                                    int64_t outOff, int64_t outPix);
+/* size of the static scratch of tnh_conv2d_fwd_nhwc_noalloc, in bytes */
+int32_t tnh_conv2d_noalloc_scratch_bytes(int64_t *bytes);
 /* No reference counterpart (layout helper): dst[f][ky][kx][c] =
  * src[f][c][ky][kx] on the device; src and dst must not overlap. */
 int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,

@@ -43,6 +43,11 @@ constexpr int64_t kRedFloats = int64_t(1) << 20;  // 4 MiB of reduction partials
 // (allocation failure, or a stream of the context is being captured).
 void* workspace(Context* c, size_t bytes);
 
+// Looks up, once per device and with that device current, the address of
+// the no-allocation entry point's static scratch on it (conv.hip); called by
+// tnh_init.
+int conv_scratch_setup(int device);
+
 // Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).
 Context* ctx();
 

@@ -137,6 +137,11 @@ extern "C" int32_t tnh_init(int32_t device) {
     return st;
   }
   float* red = nullptr;
+  if (int st = conv_scratch_setup(device)) {
+    (void)hipStreamDestroy(s);
+    (void)hipStreamDestroy(ts);
+    return st;
+  }
   if (int st = hip_status(hipMalloc(&red, kRedFloats * 4), "hipMalloc(reduction partials)")) {
     (void)hipStreamDestroy(s);
     (void)hipStreamDestroy(ts);

@@ -31,9 +31,40 @@
 #include "conv_lean.hpp"
 #include "gemm_core.hpp"
 
+// Scratch of the no-allocation entry point tnh_conv2d_fwd_nhwc_noalloc: the
+// K pieces of tail-split / split-K tiles go here instead of the context's
+// growable workspace.  Each device holds its own copy of the array from the
+// library's init call until the process ends.  Host code never uses the
+// array's name as an address: it keeps the per-device pointer
+// hipGetSymbolAddress returns (conv_scratch_setup) and passes that.
+constexpr int64_t kNoAllocScratchFloats = int64_t(16) << 20;  // 64 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace tnh {
+
+namespace {
+std::mutex g_scratch_mu;
+std::unordered_map<int, float*> g_scratch_ptr;  // device -> address of `scratch` there
+}  // namespace
+
+int conv_scratch_setup(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr.count(device)) return TNH_OK;
+  void* p = nullptr;
+  if (int st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return st;
+  if (!p) return fail(TNH_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL on device %d", device);
+  g_scratch_ptr[device] = static_cast<float*>(p);
+  return TNH_OK;
+}
+
 namespace conv {
 namespace {
+
+float* scratch_for(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(device);
+  return it == g_scratch_ptr.end() ? nullptr : it->second;
+}
 
 
 template <class Cfg, int MODE, bool VA, bool VB>
@@ -893,8 +924,13 @@ bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = fa
 }
 
 // Candidate tile configurations for one convolution call, timed on the
-// first call for its shape (and layout), then launched.
-int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool smallIO, bool nhwc, const TuneKey& key) {
+// first call for its shape (and layout), then launched.  fixed: the static
+// scratch of the no-allocation entry point (nullptr: the context's growable
+// workspace).  With it the call never tunes (a timing graph allocates): it
+// runs the forced, the cached or the cost model's choice, and fails when that
+// choice needs more scratch than the array holds.
+int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool smallIO, bool nhwc, const TuneKey& key,
+                  float* fixed = nullptr) {
   const int64_t F = a.F, N = a.g.N, K = a.g.K, C = a.g.C;
   const int kh = key.k, sY = key.s;
   auto tilesOf = [&](const CfgInfo& ci) -> int64_t {
@@ -943,7 +979,9 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
   };
   auto wsFor = [&](const Cand& c) -> float* {
     const int64_t n = wsFloats(c);
-    return n > 0 ? static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4)) : nullptr;
+    if (n <= 0) return nullptr;
+    if (fixed) return n <= kNoAllocScratchFloats ? fixed : nullptr;
+    return static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4));
   };
   auto runOn = [&](const Cand& c, hipStream_t s) -> int {
     ConvArgs b = a;
@@ -961,7 +999,14 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     }
     return nhwc ? launch_nhwc_cfg(c.cfg, b, mode, cus, s) : launch(c.cfg, b, mode, va, vb, cus, s);
   };
-  auto run = [&](const Cand& c) -> int { return runOn(c, cx->stream); };
+  auto run = [&](const Cand& c) -> int {
+    if (fixed && wsFloats(c) > kNoAllocScratchFloats)
+      return fail(TNH_ERR_INVALID_ARG,
+                  "conv2d_nhwc_noalloc: the tiling of this call needs %lld bytes of scratch, the static scratch "
+                  "holds %lld (split the batch, or choose another tiling with tnh_conv2d_set_autotune)",
+                  (long long)(wsFloats(c) * 4), (long long)(kNoAllocScratchFloats * 4));
+    return runOn(c, cx->stream);
+  };
   Cand best = cands[0];
   {
     float bc = 1e30f;
@@ -984,7 +1029,7 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     }
     auto it = g_tuned.find(key);
     if (it != g_tuned.end() && cfg_valid(it->second.cfg, mode, C, va, smallIO, nhwc)) return run(it->second);
-    if (g_autotune && !aliased) {
+    if (g_autotune && !aliased && !fixed) {
       hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
       if (hipStreamIsCapturing(cx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) tune = true;
     }
@@ -1052,12 +1097,21 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
 using namespace tnh;
 using namespace tnh::conv;
 
-extern "C" int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
-                                       int64_t kw, int64_t pH, int64_t pW, int64_t sY, int64_t sX, const float* x,
-                                       int64_t xOff, int64_t xPix, const float* weights, int64_t wOff,
-                                       const float* bias, int64_t biasOff, int32_t act, const float* residual,
-                                       int64_t rOff, int64_t rPix, float* out, int64_t outOff, int64_t outPix) {
+namespace {
+
+// tnh_conv2d_fwd_nhwc and its no-allocation variant (noAlloc: split pieces in
+// the device's static scratch, no autotuning).
+int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh, int64_t kw, int64_t pH,
+                    int64_t pW, int64_t sY, int64_t sX, const float* x, int64_t xOff, int64_t xPix,
+                    const float* weights, int64_t wOff, const float* bias, int64_t biasOff, int32_t act,
+                    const float* residual, int64_t rOff, int64_t rPix, float* out, int64_t outOff, int64_t outPix,
+                    bool noAlloc) {
   TNH_REQUIRE_CTX(cx);
+  float* fixed = nullptr;
+  if (noAlloc) {
+    fixed = scratch_for(cx->device);
+    if (!fixed) return fail(TNH_ERR_NOT_INITIALIZED, "conv2d_nhwc_noalloc: no static scratch on device %d", cx->device);
+  }
   TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0, "conv2d_nhwc: bad sizes");
   TNH_ARG(kh == kw && (kh == 1 || kh == 3), "conv2d_nhwc: only square 1x1 / 3x3 kernels are supported");
   TNH_ARG(sY > 0 && sX > 0 && pH >= 0 && pW >= 0, "conv2d_nhwc: bad stride/pad");
@@ -1107,7 +1161,34 @@ extern "C" int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int6
           "conv2d_nhwc: needs C %% 32 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
   const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, false, 1, (int)xPix, (int)outPix,
                     residual ? (int)rPix : 0, residual != nullptr, smallIO};
-  return conv_dispatch(cx, a, mode, va, false, smallIO, true, key);
+  return conv_dispatch(cx, a, mode, va, false, smallIO, true, key, fixed);
+}
+
+}  // namespace
+
+extern "C" int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                       int64_t kw, int64_t pH, int64_t pW, int64_t sY, int64_t sX, const float* x,
+                                       int64_t xOff, int64_t xPix, const float* weights, int64_t wOff,
+                                       const float* bias, int64_t biasOff, int32_t act, const float* residual,
+                                       int64_t rOff, int64_t rPix, float* out, int64_t outOff, int64_t outPix) {
+  return conv_nhwc_entry(batch, C, H, W, F, kh, kw, pH, pW, sY, sX, x, xOff, xPix, weights, wOff, bias, biasOff, act,
+                         residual, rOff, rPix, out, outOff, outPix, false);
+}
+
+extern "C" int32_t tnh_conv2d_fwd_nhwc_noalloc(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F,
+                                               int64_t kh, int64_t kw, int64_t pH, int64_t pW, int64_t sY,
+                                               int64_t sX, const float* x, int64_t xOff, int64_t xPix,
+                                               const float* weights, int64_t wOff, const float* bias,
+                                               int64_t biasOff, int32_t act, const float* residual, int64_t rOff,
+                                               int64_t rPix, float* out, int64_t outOff, int64_t outPix) {
+  return conv_nhwc_entry(batch, C, H, W, F, kh, kw, pH, pW, sY, sX, x, xOff, xPix, weights, wOff, bias, biasOff, act,
+                         residual, rOff, rPix, out, outOff, outPix, true);
+}
+
+extern "C" int32_t tnh_conv2d_noalloc_scratch_bytes(int64_t* bytes) {
+  TNH_ARG(bytes != nullptr, "conv2d_noalloc_scratch_bytes: NULL");
+  *bytes = kNoAllocScratchFloats * 4;
+  return TNH_OK;
 }
 
 extern "C" int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw, int64_t pH, int64_t pW,

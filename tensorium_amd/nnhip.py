@@ -80,6 +80,9 @@ _PROTOS = {
     "tnh_conv2d_set_autotune": [i32, i32],
     "tnh_conv2d_fwd_nhwc": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, vp, i64,
                             i32, vp, i64, i64, vp, i64, i64],
+    "tnh_conv2d_fwd_nhwc_noalloc": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64,
+                                    vp, i64, i32, vp, i64, i64, vp, i64, i64],
+    "tnh_conv2d_noalloc_scratch_bytes": [C.POINTER(i64)],
     "tnh_sgemm_set_autotune": [i32, i32],
     "tnh_yolo_fwd_nhwc": [i64, i64, i64, i64, i64, vp, i64, i64, vp],
     "tnh_copy_channels": [i64, i64, vp, i64, i64, vp, i64, i64],
@@ -335,19 +338,28 @@ class TNNHip:
 
     def conv2dForwardNHWC(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
                           biases, activation, output, outOffset, inPix=None, outPix=None, residual=None, resOffset=0,
-                          resPix=None, nchwInput=False):
+                          resPix=None, nchwInput=False, noAlloc=False):
         """Channels-last fused conv (tap-major weights); pixel strides default
-        to the channel counts; nchwInput reads a C <= 4 image as NCHW.
+        to the channel counts; nchwInput reads a C <= 4 image as NCHW;
+        noAlloc calls tnh_conv2d_fwd_nhwc_noalloc (no device allocation:
+        split pieces in the library's static scratch, no autotuning).
         Returns (outH, outW)."""
         oh = (h + 2 * padding - kernelSize) // stride + 1
         ow = (w + 2 * padding - kernelSize) // stride + 1
         xp = 0 if nchwInput else (c if inPix is None else inPix)
         op_ = filters if outPix is None else outPix
         rp = filters if resPix is None else resPix
-        call("tnh_conv2d_fwd_nhwc", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
-             addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, addr(residual), resOffset, rp,
-             addr(output), outOffset, op_)
+        call("tnh_conv2d_fwd_nhwc_noalloc" if noAlloc else "tnh_conv2d_fwd_nhwc", batch, c, h, w, filters,
+             kernelSize, kernelSize, padding, padding, stride, stride, addr(input), inOffset, xp, addr(weights), 0,
+             addr(biases), 0, activation, addr(residual), resOffset, rp, addr(output), outOffset, op_)
         return oh, ow
+
+    @staticmethod
+    def noAllocScratchBytes():
+        """Bytes of the static scratch behind conv2dForwardNHWC(noAlloc=True)."""
+        v = C.c_int64(0)
+        call("tnh_conv2d_noalloc_scratch_bytes", C.byref(v))
+        return v.value
 
     def yoloForwardNHWC(self, batch, n, classes, h, w, input, inOffset, inPix, output):
         """YOLO head on a channels-last input, NCHW head output."""
