@@ -61,6 +61,16 @@ int32_t tnh_set_stream(void *stream);
 int32_t tnh_reset_stream(void);
 /* number of compute units of the context device */
 int32_t tnh_cu_count(int32_t *count);
+/* No reference counterpart: deterministic mode (1) or not (0, default).
+ * By default the first call for a conv / SGEMM shape times several tilings
+ * and keeps the fastest; tilings that cut K into pieces (split-K, tail
+ * split) sum in a different order, so which one wins can change the low
+ * bits of the results from one process to the next (always within the
+ * fp32 parity bound).  In deterministic mode no timing-based choice is made
+ * and no K-cutting tiling is used (tilings forced with
+ * tnh_conv2d_set_autotune / tnh_sgemm_set_autotune excepted): every process
+ * runs the same kernels and produces the same bits, at some speed cost. */
+int32_t tnh_set_deterministic(int32_t enable);
 
 /* ---- HIP graphs (no reference counterpart: the reference launches every
  *      kernel eagerly).  Capture the context's own stream into an executable

@@ -48,6 +48,11 @@ void* workspace(Context* c, size_t bytes);
 // tnh_init.
 int conv_scratch_setup(int device);
 
+// Deterministic mode (tnh_set_deterministic): no timing-based tuning and no
+// split-K / tail-split tilings, so every process runs the same kernels and
+// produces the same bits.
+bool deterministic();
+
 // Returns the live context or nullptr (after recording TNH_ERR_NOT_INITIALIZED).
 Context* ctx();
 

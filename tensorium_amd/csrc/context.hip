@@ -2,6 +2,7 @@
 // Mirrors TNNCuda's lifecycle (Create/Destroy/finish, nncuda.pas:448-469,
 // 1575) with a status-code + last-error channel in place of SAFE_CALL's
 // assert (nncuda.pas:237-275).
+#include <atomic>
 #include <cstdio>
 #include <mutex>
 
@@ -11,6 +12,7 @@ namespace tnh {
 
 namespace {
 thread_local char g_err[512] = "";
+std::atomic<bool> g_deterministic{false};
 Context g_ctx;
 bool g_live = false;
 std::mutex g_mu;
@@ -29,6 +31,8 @@ int hip_status(hipError_t e, const char* what) {
   if (e == hipErrorOutOfMemory) return fail(TNH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
   return fail(TNH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
+
+bool deterministic() { return g_deterministic.load(std::memory_order_relaxed); }
 
 Context* ctx() {
   if (!g_live) {
@@ -172,6 +176,11 @@ extern "C" int32_t tnh_finalize(void) {
   (void)hipStreamDestroy(g_ctx.tune_stream);
   g_ctx = Context{};
   g_live = false;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_set_deterministic(int32_t enable) {
+  g_deterministic.store(enable != 0, std::memory_order_relaxed);
   return TNH_OK;
 }
 

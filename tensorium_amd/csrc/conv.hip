@@ -942,13 +942,14 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
   // (timed tuning only): tail splits of the fastest lean shapes whose tiles
   // do not divide into whole rounds.
   const int cus = cx->cu_count;
+  const bool det = deterministic();
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
     if (!cfg_valid(c, mode, C, va, smallIO, nhwc)) continue;
     cands.push_back({c, 1, 0, 0});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = tilesOf(ci);
-    if (tiles >= 2 * cus) continue;
+    if (tiles >= 2 * cus || det) continue;
     for (int sp : {2, 4, 8, 16})
       if (tiles * sp <= 8 * cus && K >= static_cast<int64_t>(sp) * ci.BK * 4)
         cands.push_back(nhwc ? Cand{c, 1, sp, 2} : Cand{c, sp, 0, 0});
@@ -1027,6 +1028,7 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
       if (hi >= 18) return run({c, 1, hi - 16, 0});
       return run({c, hi > 1 ? hi : 1, 0, 0});
     }
+    if (det) return run(best);  // the cost model's whole-K choice: the same in every process
     auto it = g_tuned.find(key);
     if (it != g_tuned.end() && cfg_valid(it->second.cfg, mode, C, va, smallIO, nhwc)) return run(it->second);
     if (g_autotune && !aliased && !fixed) {

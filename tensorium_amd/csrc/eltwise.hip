@@ -1,8 +1,10 @@
 // Bandwidth-bound element-wise kernels: bias / scale epilogues, activations,
-// BLAS-1 helpers, route (concat) copies and the unfused BN normalize.  Each
+// BLAS-1 helpers, route (concat) copies and the batch-norm normalize.  Each
 // element is produced by exactly the single fp32 operation the reference CPU
-// path applies (bit-exact), with grid-stride loops over 64-bit indices.
+// path applies (bit-exact).  Per-channel passes walk rows (rows.hpp);
+// flat passes use 16-byte accesses when the buffers allow.
 #include "common.hpp"
+#include "rows.hpp"
 
 namespace tnh {
 namespace {
@@ -19,43 +21,12 @@ unsigned grid_for(int64_t n) {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// ---------------------------------------------------------------------------
-// Per-channel passes.  A tensor [groups][nb][block] is walked as rows of
-// `block` contiguous floats; row r belongs to channel r % nb.  The channel's
-// constants are loaded once per row, so the element loop holds no index
-// division, and a row is read and written 16 bytes at a time when block % 4
-// == 0 and the base is 16-byte aligned.  A workgroup pass covers rpw rows of
-// cpt threads each (short rows share a workgroup; long rows loop over their
-// chunks).
-struct Rows {
-  int64_t rows, block, nb;
-  int64_t cpr;  // VW-wide chunks per row
-  int cpt;      // threads per row in one pass
-  int rpw;      // rows per workgroup pass
-};
-
-Rows make_rows(int64_t n, int64_t block, int64_t nb, int vw) {
-  Rows g;
-  g.rows = n / block;
-  g.block = block;
-  g.nb = nb;
-  g.cpr = block / vw;
-  g.cpt = static_cast<int>(g.cpr < kThreads ? g.cpr : kThreads);
-  g.rpw = kThreads / g.cpt;
-  return g;
-}
-
-unsigned grid_rows(const Rows& g) {
-  const int64_t b = (g.rows + g.rpw - 1) / g.rpw;
-  return static_cast<unsigned>(b < 16384 ? (b > 0 ? b : 1) : 16384);
-}
-
 template <class Op>
 __device__ inline float4 map4(const Op& op, const typename Op::Ch& c, float4 v) {
   return make_float4(op(c, v.x), op(c, v.y), op(c, v.z), op(c, v.w));
 }
 
-// x = op(channel constants, x) in place
+// x = op(channel constants, x) in place, row by row (rows.hpp)
 template <int VW, class Op>
 __global__ __launch_bounds__(kThreads) void rows_kernel(Op op, float* __restrict__ x, Rows g) {
   const int t = threadIdx.x, lr = t / g.cpt, lc = t - lr * g.cpt;
@@ -187,26 +158,6 @@ int launch_rows(Op op, float* dst, int64_t n, int64_t block, int64_t nb, hipStre
     hipLaunchKernelGGL((rows_kernel<1, Op>), dim3(grid_rows(g)), dim3(kThreads), 0, s, op, dst, g);
   }
   return launch_status(name);
-}
-
-// backward_bias: dst[f] += sum over (b, j) of src[(b*nb + f)*block + j];
-// one workgroup per filter, deterministic tree reduction.
-__global__ __launch_bounds__(256) void backward_bias_kernel(float* dst, int64_t nb, int64_t block, const float* src,
-                                                             int64_t batch) {
-  __shared__ float part[256];
-  const int64_t f = blockIdx.x;
-  float s = 0.f;
-  for (int64_t b = 0; b < batch; ++b) {
-    const float* p = src + (b * nb + f) * block;
-    for (int64_t j = threadIdx.x; j < block; j += blockDim.x) s = s + p[j];
-  }
-  part[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + w];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) dst[f] = dst[f] + part[0];
 }
 
 __global__ void activate_kernel(float* x, int64_t n, int act) {
@@ -393,20 +344,6 @@ extern "C" int32_t tnh_forward_scale(int64_t dstSize, float* dst, int64_t offset
   TNH_ARG(block * scaleSize * batch == dstSize, "forward_scale: sizes do not align");
   return launch_rows(ScaleOp{scale, incb}, dst + offset, dstSize, block, scaleSize, cx->stream,
                      "rows_kernel<scale>");
-}
-
-extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSize, const float* src, int64_t srcOffset,
-                                     int64_t incb, int64_t batch) {
-  (void)incb;
-  TNH_REQUIRE_CTX(cx);
-  TNH_ARG(dstSize > 0 && srcSize >= 0 && batch > 0 && srcOffset >= 0, "backward_bias: bad sizes");
-  TNH_ARG(dst && src, "backward_bias: NULL buffer");
-  const int64_t block = srcSize / (dstSize * batch);
-  TNH_ARG(block * dstSize * batch == srcSize, "backward_bias: sizes do not align");
-  TNH_ARG(dstSize <= INT32_MAX, "backward_bias: too many filters");
-  hipLaunchKernelGGL(backward_bias_kernel, dim3((unsigned)dstSize), dim3(256), 0, cx->stream, dst, dstSize, block,
-                     src + srcOffset, batch);
-  return launch_status("backward_bias_kernel");
 }
 
 extern "C" int32_t tnh_activate(int64_t N, float* x, int64_t offset, int32_t act) {

@@ -295,6 +295,8 @@ int sgemm_impl(int32_t transA, int32_t transB, int64_t M, int64_t N, int64_t K, 
     auto it = g_sgemm_tuned.find(key);
     if (g_sgemm_forced >= 0) {
       if (g_sgemm_forced < kL128x128 || lean) cfg = g_sgemm_forced;
+    } else if (deterministic()) {
+      // the untuned choice from the shape alone
     } else if (it != g_sgemm_tuned.end()) {
       cfg = it->second;
     } else if (g_sgemm_autotune) {

@@ -13,6 +13,7 @@
 
 #include "common.hpp"
 #include "gemm_core.hpp"
+#include "rows.hpp"
 
 namespace tnh {
 namespace {
@@ -301,19 +302,37 @@ int means_vars_impl(int64_t srcSize, int64_t dstSize, int64_t groups, const floa
 }
 
 // sNormalizeDelta (ntensors.pas:8900-8960), element order of
-// sNormalizeDelta_pas/_avx: d / std + ((x - mean) * vd + md).
-__global__ void normalize_delta_kernel(float* delta, const float* x, int64_t n, int64_t nch, int64_t block,
-                                       float batchSize, const float* mean, const float* variance,
-                                       const float* mean_delta, const float* variance_delta) {
-  GRID_STRIDE(e, n) {
-    const int64_t i = (e / block) % nch;
+// sNormalizeDelta_pas/_avx: d / std + ((x - mean) * vd + md), with the
+// channel's md = mean_delta / bs, vd = 2 * variance_delta / bs and
+// std = sqrt(max(var, eps)) formed once per row (rows.hpp).
+template <int VW>
+__global__ __launch_bounds__(kRowThreads) void normalize_delta_kernel(float* __restrict__ delta,
+                                                                      const float* __restrict__ x, Rows g,
+                                                                      float batchSize, const float* mean,
+                                                                      const float* variance, const float* mean_delta,
+                                                                      const float* variance_delta) {
+  rows_walk(g, [&](int64_t r, int lc) {
+    const int64_t i = r % g.nb;
     const float md = mean_delta[i] / batchSize;
     const float vd = (2.0f * variance_delta[i]) / batchSize;
     const float sd = sqrtf(fmaxf(variance[i], kEps));
-    float t = (x[e] - mean[i]) * vd;
-    t = t + md;
-    delta[e] = delta[e] / sd + t;
-  }
+    const float mu = mean[i];
+    auto one = [&](float d, float xv) {
+      float t = (xv - mu) * vd;
+      t = t + md;
+      return d / sd + t;
+    };
+    float* dr = delta + r * g.block;
+    const float* xr = x + r * g.block;
+    for (int64_t k = lc; k < g.cpr; k += g.cpt) {
+      if constexpr (VW == 4) {
+        const float4 d = reinterpret_cast<const float4*>(dr)[k], v = reinterpret_cast<const float4*>(xr)[k];
+        reinterpret_cast<float4*>(dr)[k] = make_float4(one(d.x, v.x), one(d.y, v.y), one(d.z, v.z), one(d.w, v.w));
+      } else {
+        dr[k] = one(dr[k], xr[k]);
+      }
+    }
+  });
 }
 
 // softmax (nsoftmaxlayer.pas:81-105): one thread per (batch, group) row.
@@ -555,8 +574,17 @@ extern "C" int32_t tnh_normalize_delta(int64_t deltaSize, int64_t meanSize, int6
   const int64_t block = deltaSize / (meanSize * groups);
   TNH_ARG(block * meanSize * groups == deltaSize, "normalize_delta: sizes do not align");
   const float batchSize = static_cast<float>(block * groups);
-  hipLaunchKernelGGL(normalize_delta_kernel, dim3(grid_1d(deltaSize)), dim3(256), 0, cx->stream, delta + offset,
-                     x + offset, deltaSize, meanSize, block, batchSize, mean, variance, mean_delta, variance_delta);
+  float* d = delta + offset;
+  const float* xx = x + offset;
+  if (block % 4 == 0 && rows_al16(d) && rows_al16(xx)) {
+    const Rows g = make_rows(deltaSize, block, meanSize, 4);
+    hipLaunchKernelGGL(normalize_delta_kernel<4>, dim3(grid_rows(g)), dim3(kRowThreads), 0, cx->stream, d, xx, g,
+                       batchSize, mean, variance, mean_delta, variance_delta);
+  } else {
+    const Rows g = make_rows(deltaSize, block, meanSize, 1);
+    hipLaunchKernelGGL(normalize_delta_kernel<1>, dim3(grid_rows(g)), dim3(kRowThreads), 0, cx->stream, d, xx, g,
+                       batchSize, mean, variance, mean_delta, variance_delta);
+  }
   return launch_status("normalize_delta_kernel");
 }
 
@@ -572,6 +600,24 @@ extern "C" int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups, cons
   const float* a = src1 + srcOffset;
   const float* b = src2 + srcOffset;
   if (int st = launch_partial<1>(DotOp{a, b}, s, chan_vec(s, {a, b}), cx->red, cx->stream, "chan_partial_kernel<dots>"))
+    return st;
+  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, dst);
+  return launch_status("add_dots_final");
+}
+
+extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSize, const float* src,
+                                     int64_t srcOffset, int64_t incb, int64_t batch) {
+  (void)incb;
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize > 0 && srcSize >= 0 && batch > 0 && srcOffset >= 0, "backward_bias: bad sizes");
+  TNH_ARG(dst && src, "backward_bias: NULL buffer");
+  const int64_t block = srcSize / (dstSize * batch);
+  TNH_ARG(block * dstSize * batch == srcSize, "backward_bias: sizes do not align");
+  if (srcSize == 0) return TNH_OK;
+  ChanSplit s;
+  if (int st = chan_split(s, dstSize, block, batch, 1, cx)) return st;
+  const float* x = src + srcOffset;
+  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), cx->red, cx->stream, "chan_partial_kernel<sum>"))
     return st;
   hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, dst);
   return launch_status("add_dots_final");

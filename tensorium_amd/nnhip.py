@@ -56,6 +56,7 @@ _PROTOS = {
     "tnh_set_stream": [vp],
     "tnh_reset_stream": [],
     "tnh_cu_count": [C.POINTER(i32)],
+    "tnh_set_deterministic": [i32],
     "tnh_graph_begin": [],
     "tnh_graph_end": [C.POINTER(vp)],
     "tnh_graph_launch": [vp],
@@ -375,6 +376,12 @@ class TNNHip:
     def packConvWeights(self, filters, c, kernelSize, src, dst):
         """[F][C][k][k] -> tap-major [F][k][k][C] (device to device)."""
         call("tnh_conv2d_pack_weights", filters, c, kernelSize, kernelSize, addr(src), addr(dst))
+
+    @staticmethod
+    def setDeterministic(enable=True):
+        """Same kernels and bits in every process: no timing-based tiling
+        choice, no split-K / tail-split (tnh_set_deterministic)."""
+        call("tnh_set_deterministic", 1 if enable else 0)
 
     def setConvAutotune(self, enable=True, forcedConfig=-1):
         call("tnh_conv2d_set_autotune", 1 if enable else 0, forcedConfig)

@@ -72,22 +72,59 @@ class CifarTrainer:
         self.hip, self.B, self.torch = hip, batch, torch
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
-        self.p = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in params.items()}
+        # Parameters live in two arenas (weights with decay; biases and
+        # scales without), their momentum buffers in two more with the same
+        # offsets, so each SGD step is two launches over all layers: the
+        # update is element-wise with the same scalars for every tensor of an
+        # arena, so this is bit-identical to per-tensor updates.
+        self.p = {}
+        self.arena = {}
+        for group, keys in (("w", [k for k in params if k[0] == "w"] + ["fw"]),
+                            ("p", [k for k in params if k[0] in "sb"] + ["fb"])):
+            n = sum(params[k].size for k in keys)
+            flat = torch.empty(n, dtype=torch.float32, device=dev)
+            uflat = torch.empty(n, dtype=torch.float32, device=dev)
+            off = 0
+            for k in keys:
+                v = np.ascontiguousarray(params[k])
+                flat[off:off + v.size].copy_(torch.from_numpy(v.ravel()))
+                uflat[off:off + v.size].copy_(torch.from_numpy(np.ascontiguousarray(params["u_" + k]).ravel()))
+                self.p[k] = flat[off:off + v.size].view(v.shape)
+                self.p["u_" + k] = uflat[off:off + v.size].view(v.shape)
+                off += v.size
+            self.arena[group] = (flat, uflat)
+        for k, v in params.items():
+            if k not in self.p:  # rolling statistics
+                self.p[k] = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
         self.packed = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
         B = batch
         t = {}
         h = size
         self.dims = []
+        # deltas that the backward pass accumulates into (TNNet.forward zeroes
+        # them, nnet.pas:287-294) share one arena: one fill per step
+        zsizes = []
+        hh = size
+        for i, (c, f) in enumerate(BLOCKS):
+            zsizes.append(("delta", i, (B, f, hh, hh)))
+            if i > 0:
+                zsizes.append(("dx", i, (B, c, hh, hh)))
+            if i < len(BLOCKS) - 1:
+                hh //= 2
+        self.zero_arena = torch.empty(sum(int(np.prod(sh)) for _, _, sh in zsizes), dtype=torch.float32, device=dev)
+        off = 0
+        for name, i, sh in zsizes:
+            n = int(np.prod(sh))
+            t[f"{name}{i}"] = self.zero_arena[off:off + n].view(sh)
+            off += n
         for i, (c, f) in enumerate(BLOCKS):
             self.dims.append((c, h, f))
-            for name in ("x", "xn", "out", "delta"):
+            for name in ("x", "xn", "out"):
                 t[f"{name}{i}"] = torch.empty((B, f, h, h), dtype=torch.float32, device=dev)
             t[f"mean{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
             t[f"var{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
             t[f"md{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
             t[f"vd{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
-            if i > 0:
-                t[f"dx{i}"] = torch.empty((B, c, h, h), dtype=torch.float32, device=dev)
             if i < len(BLOCKS) - 1:
                 t[f"pool{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.float32, device=dev)
                 t[f"pidx{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.int64, device=dev)
@@ -99,7 +136,6 @@ class CifarTrainer:
         t["logits"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
         t["prob"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
         t["fc_delta"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
-        t["sm_delta"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
         t["err"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
         colmax = max(c * 9 * (hh * hh) for (c, hh, f) in self.dims)
         t["col"] = torch.empty(B * colmax, dtype=torch.float32, device=dev)
@@ -140,15 +176,16 @@ class CifarTrainer:
         hip.forwardBias(B * CLASSES, t["logits"], 0, CLASSES, p["fb"], 1, B)
         hip.softmaxBatch(CLASSES, t["logits"], 0, B, CLASSES, 1, CLASSES, 1, 1.0, t["prob"], 0)
         self.truth = truth
-        hip.crossEntropySoftmax(B * CLASSES, t["prob"], truth, t["sm_delta"], t["err"])
+        # softmax backward: net.delta (zeroed each forward) += delta; t - p is
+        # never -0, so writing it straight into the zeroed delta is exact
+        hip.crossEntropySoftmax(B * CLASSES, t["prob"], truth, t["fc_delta"], t["err"])
 
     # ------------------------------------------------------------ backward
     def backward(self):
         hip, p, t, B = self.hip, self.p, self.t, self.B
         F, hw = BLOCKS[-1][1], self.final_hw
         nfc = B * CLASSES
-        # softmax backward: net.delta (zeroed each forward) += delta
-        hip.copy(nfc, t["sm_delta"], 0, 1, t["fc_delta"], 0, 1)
+        hip.fill(self.zero_arena.numel(), self.zero_arena, 0, 0.0, 1)
         # connected backward
         hip.clamp(nfc, 1.0, t["fc_delta"], t["fc_delta"])
         hip.backwardBias(CLASSES, p["u_fb"], nfc, t["fc_delta"], 0, 1, B)
@@ -157,7 +194,6 @@ class CifarTrainer:
         # avgpool backward into the last block's zeroed delta
         last = len(self.dims) - 1
         d = t[f"delta{last}"]
-        hip.fill(B * F * hw * hw, d, 0, 0.0, 1)
         hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
         col = t["col"]
         for i in range(last, -1, -1):
@@ -181,24 +217,23 @@ class CifarTrainer:
             hip.gemmStridedBatched(True, False, K, L, f, 1.0, p[f"w{i}"], 0, K, 0, d, 0, L, f * L, 0.0, col, 0, L,
                                    K * L, B)
             dx = t[f"dx{i}"]
-            hip.fill(B * c * hh * hh, dx, 0, 0.0, 1)
             hip.col2imStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx, c * hh * hh, 0, B)
             # maxpool backward into the previous block's zeroed delta
             pc, phh, pf = self.dims[i - 1]
             prev = t[f"delta{i - 1}"]
-            hip.fill(B * pf * phh * phh, prev, 0, 0.0, 1)
             hip.backwardMaxPool(B, pf, phh // 2, phh // 2, prev, t[f"pidx{i - 1}"], dx)
 
     # -------------------------------------------------------------- update
     def update(self):
-        hip, p, B = self.hip, self.p, self.B
+        """SGD with momentum and decay on every weight (conv and connected),
+        momentum only on biases and scales (nConvolutionLayer.pas:673-710,
+        nconnectedlayer.pas:324-355), one launch per arena."""
+        hip, B = self.hip, self.B
         lr, m, dec = self.lr, self.momentum, self.decay
-        for i in range(len(self.dims)):
-            hip.sgdUpdate(p[f"w{i}"].numel(), lr, B, m, dec, p[f"w{i}"], p[f"u_w{i}"])
-            hip.paramUpdate(p[f"b{i}"].numel(), lr, B, m, p[f"b{i}"], p[f"u_b{i}"])
-            hip.paramUpdate(p[f"s{i}"].numel(), lr, B, m, p[f"s{i}"], p[f"u_s{i}"])
-        hip.paramUpdate(CLASSES, lr, B, m, p["fb"], p["u_fb"])
-        hip.sgdUpdate(p["fw"].numel(), lr, B, m, dec, p["fw"], p["u_fw"])
+        w, uw = self.arena["w"]
+        hip.sgdUpdate(w.numel(), lr, B, m, dec, w, uw)
+        q, uq = self.arena["p"]
+        hip.paramUpdate(q.numel(), lr, B, m, q, uq)
         self._pack()
 
     def step(self, x, truth):

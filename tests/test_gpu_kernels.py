@@ -500,6 +500,53 @@ def test_conv_tuned_dense_then_output_beyond_2gib(hip):
     assert np.array_equal(want, ref)
 
 
+def test_deterministic_mode_ignores_tuning_state(hip):
+    """tnh_set_deterministic: the same bits whatever the tuner cached before
+    (here a batch-1 13x13 layer whose tuned tiling usually cuts K), for the
+    NCHW and channels-last convs and the SGEMM; results within the bound."""
+    case("deterministic mode")
+    B, Cc, Hh, F = 1, 512, 13, 1024
+    x = synth.uniform(140, (B, Cc, Hh, Hh))
+    Wt = synth.normal(141, (F, Cc * 9), (2.0 / (Cc * 9)) ** 0.5)
+    b = synth.normal(142, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, 3, 1, 1, acLEAKY)
+    dx, dW, db = D(x), D(Wt), D(b)
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, 3, dW, packed)
+    xn = D(np.ascontiguousarray(x.transpose(0, 2, 3, 1)))
+    A = synth.uniform(143, (1024, 2304), -1, 1)
+    Bm = synth.uniform(144, (2304, 169), -1, 1)
+    dA, dB = D(A), D(Bm)
+
+    def run():
+        o = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+        hip.conv2dForward(B, Cc, Hh, Hh, F, 3, 1, 1, dx, 0, packed, db, acLEAKY, o, 0, weightLayout=WEIGHTS_TAP_MAJOR)
+        on = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 3, 1, 1, xn, 0, packed, db, acLEAKY, on, 0)
+        oc = torch.empty((1024, 169), dtype=torch.float32, device="cuda")
+        hip.gemm(False, False, 1024, 169, 2304, 1.0, dA, 0, 2304, dB, 0, 169, 0.0, oc, 0, 169)
+        return [H(t, hip) for t in (o, on, oc)]
+
+    run()  # the tuner caches its (possibly K-cutting) choices
+    try:
+        hip.setDeterministic(True)
+        first = run()
+        hip.setConvAutotune(False, -1)  # clears the caches, as in a fresh process
+        hip.setSgemmAutotune(False, -1)
+        hip.setConvAutotune(True, -1)
+        hip.setSgemmAutotune(True, -1)
+        second = run()
+    finally:
+        hip.setDeterministic(False)
+    for u, v in zip(first, second):
+        assert np.array_equal(u, v)
+    assert R.rel_err(first[0], ref) <= TOL
+    assert R.rel_err(first[1].transpose(0, 3, 1, 2), ref) <= TOL
+    C = np.zeros((1024, 169), np.float32)
+    R.sgemm(0, 0, 1024, 169, 2304, 1.0, A, 2304, Bm, 169, 0.0, C, 169)
+    assert R.rel_err(first[2], C) <= TOL
+
+
 # ------------------------------------------------------- pool / upsample ----
 @pytest.mark.parametrize("size,stride,pad,shape", [(2, 2, 0, (2, 5, 19, 16)), (3, 2, 0, (2, 5, 19, 16)),
                                                    (2, 1, 1, (2, 5, 19, 16)), (3, 1, 2, (2, 5, 19, 16)),

@@ -214,9 +214,13 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
     """The benchmark's own configuration: YOLOv3-416 at batch 16,
     channels-last, autotuned for batch-16 shapes (tail splits included).
     Images 0, 7 and 15 of the batch against the CPU oracle run on the same
-    image: the three pre-logistic head convolutions within the per-tensor
-    1e-5 bound.  Two graph replays of the batch-16 forward equal its eager
-    result bit for bit."""
+    image and against the float64 evaluation of the network: the three
+    pre-logistic head convolutions within 1e-5 of float64 and within
+    1.25e-5 of the oracle.  (Every convolution fed the oracle's input is
+    held to 1e-5 in test_yolov3_416_layerwise; at the heads two independent
+    fp32 chains of ~100 layers differ by up to ~1e-5, most of it the
+    oracle's own rounding, which the float64 comparison shows.)  Two graph
+    replays of the batch-16 forward equal its eager result bit for bit."""
     layers, W = yolo
     print("[case] yolov3-416 batch 16 nhwc (bench configuration) vs the oracle, graph replay", flush=True)
     x = synth.uniform(13, (16, 3, 416, 416))
@@ -227,12 +231,17 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
     hip.finish()
     heads16 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
     for img in (0, 7, 15):
-        print(f"[case] oracle forward of image {img}", flush=True)
-        ref = netref.forward(layers, W, np.ascontiguousarray(x[img:img + 1]))
+        print(f"[case] oracle and float64 forwards of image {img}", flush=True)
+        xi = np.ascontiguousarray(x[img:img + 1])
+        ref = netref.forward(layers, W, xi)
+        r64 = f64_heads(layers, W, xi)
         for i in (81, 93, 105):
             e = R.rel_err(heads16[i][img:img + 1], ref[i])
-            print(f"image {img} head conv {i}: {e:.3e}", flush=True)
-            assert e <= TOL, (img, i, e)
+            e64 = R.rel_err(heads16[i][img:img + 1], r64[i])
+            print(f"image {img} head conv {i}: vs oracle {e:.3e}, vs float64 {e64:.3e} "
+                  f"(oracle vs float64 {R.rel_err(ref[i], r64[i]):.3e})", flush=True)
+            assert e64 <= TOL, (img, i, e64)
+            assert e <= 1.25 * TOL, (img, i, e)
         del ref
     try:
         big.capture(dx)
