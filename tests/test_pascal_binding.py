@@ -1,0 +1,141 @@
+"""CPU checks of pascal/nnhip.pas, the Free Pascal side of the drop-in.
+
+No Free Pascal compiler is installed in this image or on the GPU boxes, so
+the unit is checked structurally: every C entry point of
+include/tensorium_hip.h has exactly one `external` declaration with the same
+parameter count and matching types; every call the unit makes passes that
+many arguments; and TNNHip<T> declares every public method of the
+reference's TNNCuda<T> (nncuda.pas:100-157)."""
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tensorium_hip.h")
+UNIT = os.path.join(ROOT, "pascal", "nnhip.pas")
+
+# public methods of TNNCuda<T>, nncuda.pas:100-157
+TNNCUDA_METHODS = [
+    "deviceCount", "Create", "Destroy", "CompileLog", "createDeviceBuffer", "freeDeviceBuffer", "readBuffer",
+    "writeBuffer", "ActivateArray", "activateArraySWISH", "DeriveArray", "forwardBias", "backwardBias", "gemm",
+    "gemmBatched", "gemmStridedBatched", "addvv", "subvv", "mulvv", "fmavv", "axpy", "power", "scale",
+    "crossEntropyLogistic", "fill", "copy", "softmaxBatch", "crossEntropySoftmax", "forwardMaxPool",
+    "backwardMaxPool", "im2col", "col2im", "upSample", "fmavss", "meansAndVars", "means", "variances", "normalize",
+    "meansAndVarsDelta", "normalizeDelta", "addDots", "forwardScale", "forwardScaleAdd", "forwardDropout",
+    "backwardDropout", "costL2", "clamp", "inverseSqrt", "finish", "compileToCUBIN", "loadCUBIN", "compileFile",
+    "loadCUBinFile",
+]
+
+C_TO_PAS = {
+    "int32_t": "LongInt", "int64_t": "Int64", "float": "Single", "float*": "PSingle", "int64_t*": "PInt64",
+    "int32_t*": "PLongInt", "void*": "Pointer", "void**": "PPointer", "float**": "PPSingle",
+}
+
+
+def strip_c_comments(text):
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.sub(r"//[^\n]*", "", text)
+
+
+def header_decls():
+    text = strip_c_comments(open(HEADER).read())
+    out = {}
+    for m in re.finditer(r"\b(?:int32_t|const\s+char\s*\*)\s*(tnh_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        name, params = m.group(1), m.group(2).strip()
+        types = []
+        if params and params != "void":
+            for p in params.split(","):
+                p = re.sub(r"\bconst\b", "", p)
+                p = re.sub(r"[A-Za-z_][A-Za-z0-9_]*\s*$", "", p.strip())  # drop the parameter name
+                p = re.sub(r"\s+", "", p)
+                types.append(p)
+        out[name] = types
+    return out
+
+
+def unit_text():
+    text = open(UNIT).read()
+    text = re.sub(r"\{[^}]*\}", "", text)  # { } comments
+    return re.sub(r"//[^\n]*", "", text)
+
+
+def pascal_externals():
+    text = unit_text()
+    out = {}
+    pat = r"function\s+(tnh_[a-z0-9_]+)\s*(?:\(([^)]*)\))?\s*:\s*(\w+)\s*;\s*cdecl\s*;\s*external\s+libtnh\s*;"
+    for m in re.finditer(pat, text):
+        name, params, ret = m.group(1), m.group(2) or "", m.group(3)
+        assert name not in out, "declared twice: " + name
+        types, names = [], []
+        for group in filter(None, (g.strip() for g in params.split(";"))):
+            idents, typ = group.rsplit(":", 1)
+            for ident in idents.split(","):
+                names.append(ident.strip())
+                types.append(typ.strip())
+        lowered = [n.lower() for n in names]
+        assert len(set(lowered)) == len(lowered), "duplicate parameter (Pascal is case-insensitive): " + name
+        out[name] = (types, ret)
+    return out
+
+
+def test_every_header_entry_point_has_one_matching_external():
+    decls = header_decls()
+    ext = pascal_externals()
+    assert len(decls) >= 70
+    assert sorted(decls) == sorted(ext)
+    for name, ctypes_ in decls.items():
+        types, ret = ext[name]
+        assert ret == ("PAnsiChar" if name == "tnh_last_error" else "LongInt"), name
+        assert len(types) == len(ctypes_), name
+        for i, (c, p) in enumerate(zip(ctypes_, types)):
+            assert C_TO_PAS[c] == p, (name, i, c, p)
+
+
+def split_args(s):
+    depth, cur, out = 0, "", []
+    for ch in s:
+        if ch == "(":
+            depth += 1
+        elif ch == ")":
+            depth -= 1
+        if ch == "," and depth == 0:
+            out.append(cur)
+            cur = ""
+        else:
+            cur += ch
+    if cur.strip():
+        out.append(cur)
+    return out
+
+
+def test_every_call_passes_the_declared_number_of_arguments():
+    text = unit_text()
+    impl = text[text.index("implementation"):]
+    ext = pascal_externals()
+    calls = 0
+    for m in re.finditer(r"\b(tnh_[a-z0-9_]+)\(", impl):
+        start = m.end()
+        depth, i = 1, start
+        while depth:
+            depth += {"(": 1, ")": -1}.get(impl[i], 0)
+            i += 1
+        args = split_args(impl[start:i - 1])
+        assert len(args) == len(ext[m.group(1)][0]), (m.group(1), len(args))
+        calls += 1
+    assert calls >= 50
+
+
+def test_tnnhip_declares_every_tnncuda_method():
+    text = unit_text()
+    iface = text[text.index("TNNHip<T> = class"):text.index("implementation")]
+    declared = set(re.findall(r"(?:procedure|function|constructor|destructor)\s+(\w+)", iface))
+    missing = [m for m in TNNCUDA_METHODS if m not in declared]
+    assert not missing, missing
+    impl = text[text.index("implementation"):]
+    for m in declared:
+        assert re.search(r"TNNHip<T>\.%s\b" % m, impl), "no implementation: " + m
+
+
+def test_unit_is_complete_text():
+    raw = open(UNIT).read()
+    assert "…" not in raw and "..." not in raw
+    assert raw.rstrip().endswith("end.")
