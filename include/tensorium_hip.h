@@ -170,8 +170,10 @@ enum { TNH_WEIGHTS_REFERENCE = 0, TNH_WEIGHTS_TAP_MAJOR = 1 };
  * weightLayout: TNH_WEIGHTS_REFERENCE ([F][C][kh][kw], the reference's
  * storage, nConvolutionLayer.pas:206) or TNH_WEIGHTS_TAP_MAJOR
  * ([F][kh][kw][C], from tnh_conv2d_pack_weights; the fast path).
- * Kernels: 1x1/3x3, any stride/padding.  The first call for a shape may
- * time several tile shapes (see tnh_conv2d_set_autotune). */
+ * Kernels: any kh x kw from 1 to 32 per side, any stride/padding,
+ * dilation 1 (1x1 and 3x3 run the fast tiles; other sizes the LDS-staged
+ * tiles 0..5 with a run-time gather).  The first call for a shape may time
+ * several tile shapes (see tnh_conv2d_set_autotune). */
 int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W,
                        int64_t F, int64_t kh, int64_t kw, int64_t pH,
                        int64_t pW, int64_t sY, int64_t sX, const float *x,

@@ -80,6 +80,8 @@ template <class Cfg, bool VA, bool VB>
 struct KernelTraits<Cfg, k1x1, VA, VB> { using BL = Conv1x1Loader<VB, Cfg::BN, Cfg::BK, Cfg::NT>; };
 template <class Cfg, bool VA, bool VB>
 struct KernelTraits<Cfg, kGatherTap3, VA, VB> { using BL = ConvGatherTapLoader<3, 3, Cfg::BN, Cfg::BK, Cfg::NT>; };
+template <class Cfg, bool VA, bool VB>
+struct KernelTraits<Cfg, kGatherDyn, VA, VB> { using BL = ConvGatherDynLoader<Cfg::BN, Cfg::BK, Cfg::NT>; };
 
 template <class Cfg, int MODE, bool VA, bool VB>
 __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
@@ -337,7 +339,9 @@ template <int C, bool TAP, int ACT>
 __global__ __launch_bounds__(256) void conv_smallc_kernel(ConvArgs a, const float* __restrict__ w,
                                                           const float* __restrict__ bias) {
   constexpr int K = 9 * C;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  // consecutive blocks of pixels on one XCD: the input rows a block shares
+  // with its neighbours stay in that XCD's L2
+  const int64_t n = static_cast<int64_t>(xcd_block(blockIdx.x, gridDim.x)) * 256 + threadIdx.x;
   if (n >= a.g.N) return;
   const int F = static_cast<int>(a.F);
   const int OHW = a.g.OHW;
@@ -396,7 +400,9 @@ __global__ __launch_bounds__(256) void conv_smallc_nhwc_kernel(ConvArgs a, const
   constexpr int K = 9 * C, FC = 32;
   __shared__ f32x4 tile[4][64 * FC / 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t nWave = static_cast<int64_t>(blockIdx.x) * 256 + wave * 64;  // first pixel of this wave
+  // first pixel of this wave; consecutive blocks of pixels on one XCD (L2
+  // reuse of the shared input rows)
+  const int64_t nWave = static_cast<int64_t>(xcd_block(blockIdx.x, gridDim.x)) * 256 + wave * 64;
   const int64_t n = nWave + lane;
   const bool valid = n < a.g.N;
   const int F = static_cast<int>(a.F);
@@ -648,6 +654,7 @@ int launch_cfg(const ConvArgs& a, int mode, bool va, bool vb, hipStream_t s) {
     case kGatherRef3: return launch_mode<Cfg, kGatherRef3>(a, va, vb, s);
     case kGatherTap3: return launch_mode<Cfg, kGatherTap3>(a, va, vb, s);
     case kGatherRef1: return launch_mode<Cfg, kGatherRef1>(a, va, vb, s);
+    case kGatherDyn: return launch_mode<Cfg, kGatherDyn>(a, va, vb, s);
     case kTap3: return launch_mode<Cfg, kTap3>(a, va, vb, s);
     default: return launch_mode<Cfg, k1x1>(a, va, vb, s);
   }
@@ -1232,7 +1239,8 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
                                   int64_t outOff, int64_t outBatchStride) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0, "conv2d: bad sizes");
-  TNH_ARG(kh == kw && (kh == 1 || kh == 3), "conv2d: only square 1x1 / 3x3 kernels are supported");
+  TNH_ARG(kh >= 1 && kw >= 1 && kh <= 32 && kw <= 32, "conv2d: kernel %lldx%lld (1..32 per side)", (long long)kh,
+          (long long)kw);
   TNH_ARG(sY > 0 && sX > 0 && pH >= 0 && pW >= 0, "conv2d: bad stride/pad");
   TNH_ARG(x && weights && out, "conv2d: NULL x/weights/out");
   TNH_ARG(weightLayout == TNH_WEIGHTS_REFERENCE || weightLayout == TNH_WEIGHTS_TAP_MAJOR,
@@ -1257,6 +1265,8 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   a.g.C = (int)C; a.g.H = (int)H; a.g.W = (int)W; a.g.OW = (int)OW; a.g.OHW = (int)(OH * OW);
   a.g.sY = (int)sY; a.g.sX = (int)sX; a.g.pH = (int)pH; a.g.pW = (int)pW;
   a.g.N = N; a.g.K = K;
+  a.g.kh = (int)kh; a.g.kw = (int)kw;
+  a.g.tapW = weightLayout == TNH_WEIGHTS_TAP_MAJOR;
   a.w = weights + wOff;
   a.wBytes = F * K * 4;
   a.bias = bias ? bias + biasOff : nullptr;
@@ -1269,12 +1279,14 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   a.F = F;
   a.act = act;
 
-  const bool is1x1 = kh == 1 && sY == 1 && sX == 1 && pH == 0 && pW == 0;
+  const bool is1x1 = kh == 1 && kw == 1 && sY == 1 && sX == 1 && pH == 0 && pW == 0;
   int mode;
   if (is1x1)
     mode = k1x1;  // both layouts coincide for 1x1
-  else if (kh == 1)
+  else if (kh == 1 && kw == 1)
     mode = kGatherRef1;
+  else if (kh != 3 || kw != 3)
+    mode = kGatherDyn;  // any other kernel size: the LDS-staged tiles with a run-time gather
   else if (weightLayout == TNH_WEIGHTS_TAP_MAJOR)
     mode = C % 16 == 0 ? kTap3 : kGatherTap3;
   else
@@ -1285,7 +1297,7 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   const bool smallIO = a.outBytes <= kMaxBufBytes && a.resBytes <= kMaxBufBytes && F * N * 4 <= kMaxBufBytes;
   const bool vb = is1x1 && aligned16(a.g.x) && (OH * OW) % 4 == 0 && (batch == 1 || xBatchStride % 4 == 0);
   if (mode == kTap3 && !va) mode = kGatherTap3;
-  if (kh == 3 && C <= 4 && N / 256 < INT32_MAX) {
+  if (kh == 3 && kw == 3 && C <= 4 && N / 256 < INT32_MAX) {
     // few input channels: per-pixel kernel (no tile choice to tune); a forced
     // tile configuration still selects the GEMM path (tests of every tile)
     bool forced;

@@ -43,7 +43,9 @@ struct ConvArgs {
 };
 
 // K walk / B operand of a convolution kernel
-enum Mode { kGatherRef3 = 0, kGatherTap3 = 1, kGatherRef1 = 2, kTap3 = 3, k1x1 = 4 };
+// kGatherDyn: any kernel size (kh x kw given at run time), either weight
+// layout (tap-major when ConvArgs::tapW)
+enum Mode { kGatherRef3 = 0, kGatherTap3 = 1, kGatherRef1 = 2, kTap3 = 3, k1x1 = 4, kGatherDyn = 5 };
 
 __device__ inline float apply_act(float v, int act) {
   if (act == TNH_AC_LEAKY) return v < 0.f ? 0.1f * v : v;  // leaky_array (nactivation.pas:234)

@@ -224,6 +224,8 @@ struct ConvGeom {
   int C, H, W, OW, OHW;
   int sY, sX, pH, pW;
   int64_t N, K;
+  int kh, kw;  // kernel size (read by the run-time-size gather)
+  int tapW;    // the run-time-size gather: weights tap-major (1) or [F][C][kh][kw] (0)
 };
 
 template <int BN, int BK, int NT>
@@ -304,6 +306,61 @@ struct ConvGatherLoader : ColumnState<BN, BK, NT> {
 
 template <int KH, int KW, int BN, int BK, int NT>
 using ConvGatherTapLoader = ConvGatherLoader<KH, KW, BN, BK, NT, true>;
+
+// The same gather for a kernel size known only at run time (any kh x kw:
+// 5x5, 7x7, 1x3, ... layers), in either K order (g.tapW).  Two integer
+// divisions per element more than the compile-time loaders; for the rare
+// layer shapes those do not cover.
+template <int BN, int BK, int NT>
+struct ConvGatherDynLoader : ColumnState<BN, BK, NT> {
+  using S = ColumnState<BN, BK, NT>;
+  static constexpr bool kKC = false;
+  __amdgpu_buffer_rsrc_t rsrc;
+  int C, H, W, K, KW, KHW;
+  bool tap;
+  uint32_t HW4;
+  float reg[S::PER];
+
+  __device__ inline void init(const ConvGeom& g, int64_t n0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    H = g.H;
+    W = g.W;
+    K = static_cast<int>(g.K);
+    KW = g.kw;
+    KHW = g.kh * g.kw;
+    tap = g.tapW != 0;
+    HW4 = static_cast<uint32_t>(g.H) * static_cast<uint32_t>(g.W) * 4u;
+    S::init_col(g, n0, tid);
+  }
+
+  __device__ inline void load(int64_t k0) {
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) {
+      const int k = static_cast<int>(k0) + S::myRow0 + v * S::RSTEP;
+      int c, r;
+      if (tap) {
+        r = k / C;
+        c = k - r * C;
+      } else {
+        c = k / KHW;
+        r = k - c * KHW;
+      }
+      const int ky = r / KW, kx = r - ky * KW;
+      const int iy = S::iy0 + ky, ix = S::ix0 + kx;
+      const bool ok = S::colOk && k < K && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
+                      static_cast<unsigned>(ix) < static_cast<unsigned>(W);
+      const uint32_t o = S::colOff + static_cast<uint32_t>(c) * HW4 + static_cast<uint32_t>(ky * W + kx) * 4u;
+      reg[v] = buf_ld1(rsrc, sel_off(ok, o));
+    }
+  }
+
+  __device__ inline void store(lds_t* lds, int) const {
+    using L = PanelLayout<false, BN, BK>;
+#pragma unroll
+    for (int v = 0; v < S::PER; ++v) lds[L::at(S::myCol, S::myRow0 + v * S::RSTEP)] = reg[v];
+  }
+};
 
 // Tap-major K order k = (ky*KW + kx)*C + c, weights packed [F][kh][kw][C]
 // (tnh_conv2d_pack_weights).  With C % BK == 0 a panel lies inside one tap,
@@ -521,10 +578,19 @@ struct Conv1x1Loader {
 // contiguous range of tiles, then walk that range in GROUP_M-row groups so
 // the tiles an XCD runs together share A rows and B columns in its L2.
 // ---------------------------------------------------------------------------
+// Workgroup id -> the id of the block of work it takes, such that the
+// workgroups one XCD runs (ids x, x + 8, x + 16, ...: the dispatcher deals
+// workgroups round-robin over the 8 XCDs, each with its own L2) take one
+// contiguous range of blocks.  A bijection on [0, total) for any total.
+__device__ inline int xcd_block(int pid, int total) {
+  constexpr int XCD = 8;
+  const int q = total / XCD, r = total % XCD, x = pid % XCD;
+  return x * q + min(x, r) + pid / XCD;
+}
+
 __device__ inline void tile_coords(int pid, int tilesM, int tilesN, int& tm, int& tn) {
   const int total = tilesM * tilesN;
-  constexpr int XCD = 8;
-  if (total % XCD == 0) pid = (pid % XCD) * (total / XCD) + pid / XCD;
+  pid = xcd_block(pid, total);
   constexpr int GROUP_M = 8;
   const int groupSize = GROUP_M * tilesN;
   const int g = pid / groupSize;

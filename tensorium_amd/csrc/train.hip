@@ -101,18 +101,28 @@ __device__ inline float fixed_total(const float* v, int n, float* sh) {
 }
 
 // Walks workgroup (p, i)'s units, calling op.add(acc, element index) per
-// element or op.add4(acc, index of 4 elements) per 16 bytes.
+// element or op.add4(acc, index of 4 elements) per 16 bytes.  Units of
+// fewer than kRed chunks share a pass: thread t takes chunk t % cpt of unit
+// t / cpt, so short rows (an 8x8 plane, one element per channel) keep every
+// thread busy; a thread's share is fixed, so the sums are too.
 template <bool VEC, class Op>
 __device__ inline void chan_walk(const ChanSplit& s, int p, int64_t i, const Op& op, float* acc) {
   const int64_t u0 = s.units * p / s.P, u1 = s.units * (p + 1) / s.P;
-  for (int64_t u = u0; u < u1; ++u) {
+  constexpr int V = VEC ? 4 : 1;
+  const int64_t cpr = (s.cs + V - 1) / V;  // chunks of a full unit
+  const int cpt = static_cast<int>(cpr < kRed ? cpr : kRed);
+  const int upp = kRed / cpt;  // units per pass
+  const int lu = threadIdx.x / cpt, lc = threadIdx.x - lu * cpt;
+  if (lu >= upp) return;
+  for (int64_t u = u0 + lu; u < u1; u += upp) {
     const int64_t b = u / s.kc, c = u - b * s.kc;
     const int64_t base = (b * s.nch + i) * s.block + c * s.cs;
-    const int64_t len = std::min(s.cs, s.block - c * s.cs);
-    if constexpr (VEC) {
-      for (int64_t k = threadIdx.x; k < len / 4; k += kRed) op.add4(acc, base + 4 * k);
-    } else {
-      for (int64_t k = threadIdx.x; k < len; k += kRed) op.add(acc, base + k);
+    const int64_t len = std::min(s.cs, s.block - c * s.cs) / V;
+    for (int64_t k = lc; k < len; k += cpt) {
+      if constexpr (VEC)
+        op.add4(acc, base + 4 * k);
+      else
+        op.add(acc, base + k);
     }
   }
 }
@@ -489,7 +499,7 @@ __global__ __launch_bounds__(Cfg::NT) void wgrad_kernel(WgradArgs a) {
 // l adds splits l, l + 64, ... in turn (their loads issued together), then a
 // fixed tree over the lanes; then alpha and beta.  Fixed order: the result
 // does not vary run to run.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
+__global__ __launch_bounds__(256) void wgrad_reduce_wave_kernel(WgradArgs a) {
   __shared__ float sh[4][64];
   const int64_t total = a.M * a.N;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -512,6 +522,30 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
   }
 }
 
+// The same sums when there are many output elements: one thread per element
+// adds the splits in split order, eight loads issued together (coalesced
+// along the elements).
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
+  const int64_t total = a.M * a.N;
+  GRID_STRIDE(e, total) {
+    float v = 0.f;
+    int s = 0;
+    for (; s + 8 <= a.splits; s += 8) {
+      float t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] = a.part[(s + j) * total + e];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v = v + t[j];
+    }
+    for (; s < a.splits; ++s) v = v + a.part[s * total + e];
+    const int64_t r = e / a.N, c = e - r * a.N;
+    float* p = a.C + r * a.ldc + c;
+    float out = a.alpha * v;
+    if (a.beta != 0.f) out = out + a.beta * *p;
+    *p = out;
+  }
+}
+
 using WCfg = TileCfg<64, 64, 32, 2, 2, 2>;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -522,7 +556,14 @@ int launch_wgrad(WgradArgs a, hipStream_t s) {
   hipLaunchKernelGGL((wgrad_kernel<WCfg, VA, VB>), grid, dim3(WCfg::NT), 0, s, a);
   if (int st = launch_status("wgrad_kernel")) return st;
   if (a.splits > 1) {
-    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3(static_cast<unsigned>((a.M * a.N + 3) / 4)), dim3(256), 0, s, a);
+    // few outputs: a wave per output element spreads the splits over its
+    // lanes; many: a thread per element keeps the loads coalesced
+    if (a.M * a.N < 8192) {
+      hipLaunchKernelGGL(wgrad_reduce_wave_kernel, dim3(static_cast<unsigned>((a.M * a.N + 3) / 4)), dim3(256), 0, s,
+                         a);
+      return launch_status("wgrad_reduce_wave_kernel");
+    }
+    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3(grid_1d(a.M * a.N)), dim3(256), 0, s, a);
     return launch_status("wgrad_reduce_kernel");
   }
   return TNH_OK;

@@ -325,14 +325,19 @@ class TNNHip:
     # -- fused convolution (new: replaces im2col+gemm+bias+activate) ---------
     def conv2dForward(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
                       biases, activation, output, outOffset, inBatchStride=None, outBatchStride=None,
-                      residual=None, resOffset=0, resBatchStride=None, weightLayout=WEIGHTS_REFERENCE):
-        """Fused conv + bias + activation (+ shortcut add); returns (outH, outW)."""
+                      residual=None, resOffset=0, resBatchStride=None, weightLayout=WEIGHTS_REFERENCE,
+                      kernelWidth=None, padWidth=None):
+        """Fused conv + bias + activation (+ shortcut add); kernelSize and
+        padding are the height ones, kernelWidth / padWidth default to them.
+        Returns (outH, outW)."""
+        kw = kernelSize if kernelWidth is None else kernelWidth
+        pw = padding if padWidth is None else padWidth
         oh = (h + 2 * padding - kernelSize) // stride + 1
-        ow = (w + 2 * padding - kernelSize) // stride + 1
+        ow = (w + 2 * pw - kw) // stride + 1
         xs = c * h * w if inBatchStride is None else inBatchStride
         os_ = filters * oh * ow if outBatchStride is None else outBatchStride
         rs = filters * oh * ow if resBatchStride is None else resBatchStride
-        call("tnh_conv2d_fwd", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride, stride,
+        call("tnh_conv2d_fwd", batch, c, h, w, filters, kernelSize, kw, padding, pw, stride, stride,
              addr(input), inOffset, xs, addr(weights), 0, weightLayout, addr(biases), 0, activation, addr(residual),
              resOffset, rs, addr(output), outOffset, os_)
         return oh, ow
@@ -373,9 +378,10 @@ class TNNHip:
         call("tnh_upsample_nhwc", batch, channels, h, w, stride, scale, addr(input), inOffset, inPix, addr(output),
              outOffset, outPix)
 
-    def packConvWeights(self, filters, c, kernelSize, src, dst):
-        """[F][C][k][k] -> tap-major [F][k][k][C] (device to device)."""
-        call("tnh_conv2d_pack_weights", filters, c, kernelSize, kernelSize, addr(src), addr(dst))
+    def packConvWeights(self, filters, c, kernelSize, src, dst, kernelWidth=None):
+        """[F][C][kh][kw] -> tap-major [F][kh][kw][C] (device to device)."""
+        call("tnh_conv2d_pack_weights", filters, c, kernelSize, kernelSize if kernelWidth is None else kernelWidth,
+             addr(src), addr(dst))
 
     @staticmethod
     def setDeterministic(enable=True):

@@ -433,6 +433,53 @@ def test_conv_tail_split(hip, base, cfg, pieces, B, Cc, Hh, F, k, s):
     assert R.rel_err(got, ref) <= TOL
 
 
+def oracle_conv_any(x, Wt, b, kh, kw, s, pH, pW, act):
+    """Conv2D (ntensors.pas:8252-8345) for any kernel shape through the
+    oracle's im2col and per-image NN SGEMM, then bias and activation."""
+    B = x.shape[0]
+    F = Wt.shape[0]
+    col = R.im2col(x, kh, kw, pH, pW, s, s)
+    L = col.shape[2]
+    out = np.zeros((B, F, L), np.float32)
+    for i in range(B):
+        R.sgemm(0, 0, F, L, col.shape[1], 1.0, Wt, Wt.shape[1], np.ascontiguousarray(col[i]), L, 0.0, out[i], L)
+    out = R.forward_bias(out, b, B)
+    return R.activate(out, act)
+
+
+@pytest.mark.parametrize("B,Cc,Hh,Ww,F,kh,kw,s,pH,pW,tap", [(2, 8, 21, 21, 24, 5, 5, 1, 2, 2, False),
+                                                           (1, 16, 30, 30, 40, 7, 7, 2, 3, 3, True),
+                                                           (2, 5, 12, 16, 9, 2, 2, 2, 0, 0, False),
+                                                           (2, 12, 14, 9, 20, 1, 3, 1, 0, 1, True),
+                                                           (1, 32, 11, 13, 64, 3, 5, 1, 1, 2, False),
+                                                           (2, 3, 33, 33, 16, 5, 5, 1, 2, 2, True)])
+def test_conv_any_kernel_size(hip, B, Cc, Hh, Ww, F, kh, kw, s, pH, pW, tap):
+    """Kernel sizes beyond 1x1 / 3x3 (5x5, 7x7, even, non-square) through
+    tnh_conv2d_fwd in both weight layouts, against the oracle's im2col +
+    SGEMM path; every LDS-staged tile configuration once."""
+    case(f"conv any kernel B{B} C{Cc} {Hh}x{Ww} F{F} k{kh}x{kw} s{s} p{pH},{pW} tap{tap}")
+    x = synth.uniform(150, (B, Cc, Hh, Ww))
+    Wt = synth.normal(151, (F, Cc * kh * kw), (2.0 / (Cc * kh * kw)) ** 0.5)
+    b = synth.normal(152, (F,), 0.1)
+    ref = oracle_conv_any(x, Wt, b, kh, kw, s, pH, pW, acLEAKY)
+    OH, OW = (Hh + 2 * pH - kh) // s + 1, (Ww + 2 * pW - kw) // s + 1
+    dW = D(Wt)
+    if tap:
+        packed = torch.empty_like(dW)
+        hip.packConvWeights(F, Cc, kh, dW, packed, kernelWidth=kw)
+        dW = packed
+    for cfg in (-1, 0, 1, 2, 3, 4, 5):
+        dout = torch.empty((B, F, OH, OW), dtype=torch.float32, device="cuda")
+        hip.setConvAutotune(True, cfg)
+        try:
+            call = dict(weightLayout=WEIGHTS_TAP_MAJOR if tap else 0, kernelWidth=kw, padWidth=pW)
+            hip.conv2dForward(B, Cc, Hh, Ww, F, kh, s, pH, D(x), 0, dW, D(b), acLEAKY, dout, 0, **call)
+            got = H(dout, hip)
+        finally:
+            hip.setConvAutotune(True, -1)
+        assert R.rel_err(got.reshape(B, F, -1), ref) <= TOL, cfg
+
+
 def test_conv_golden_fixture(hip):
     case("conv golden fixture (torch fp64)")
     import os
@@ -776,7 +823,7 @@ def test_invalid_arguments_raise(hip):
     with pytest.raises(TNHError):
         hip.gemm(0, 0, 4, 4, 4, 1.0, dx, 0, 2, dx, 0, 4, 0.0, dx, 0, 4)  # lda < K
     with pytest.raises(TNHError):
-        hip.conv2dForward(1, 1, 4, 4, 1, 5, 1, 2, dx, 0, dx, None, acLEAKY, dx, 0)  # 5x5 unsupported
+        hip.conv2dForward(1, 1, 4, 4, 1, 33, 1, 16, dx, 0, dx, None, acLEAKY, dx, 0)  # kernel above 32
     with pytest.raises(TNHError):
         hip.ActivateArray(4, dx, 0, 123)
     with pytest.raises(TNHError):
