@@ -342,7 +342,9 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
                                                        (2, 3, 37, 32, 1, True, acLEAKY, True),
                                                        (1, 1, 9, 5, 2, False, acLINEAR, False),
                                                        (3, 4, 20, 7, 1, True, acLEAKY, False),
-                                                       (2, 2, 15, 9, 2, True, acLINEAR, True)])
+                                                       (2, 2, 15, 9, 2, True, acLINEAR, True),
+                                                       (1, 3, 50, 12, 2, True, acLINEAR, True),
+                                                       (2, 3, 33, 64, 1, False, acLEAKY, False)])
 def test_conv_few_channels_bit_exact(hip, B, Cc, Hh, F, s, tap, act, resid):
     """C <= 4 3x3 layers (the RGB input layer; config 1 at full size) run the
     per-pixel kernel, whose sequential FMA chain in the reference k order is
