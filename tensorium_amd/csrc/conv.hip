@@ -29,6 +29,7 @@
 #include "common.hpp"
 #include "conv_args.hpp"
 #include "conv_lean.hpp"
+#include "conv_wsplit.hpp"
 #include "gemm_core.hpp"
 
 // Scratch of the no-allocation entry point tnh_conv2d_fwd_nhwc_noalloc: the
@@ -570,14 +571,18 @@ using Lean17 = LeanCfg<128, 64, 32, 4, 2, 2>;
 using Lean18 = LeanCfg<64, 128, 32, 2, 4, 2>;
 using Lean19 = LeanCfg<128, 128, 32, 4, 2, 2>;
 
-enum CfgKind { kLds = 0, kDirect = 1, kLean = 2 };
+// wave-split channels-last tiles (conv_wsplit.hip: K of one tile split over
+// the waves of its workgroup), ids kWsFirst + index into kWsCfgs
+constexpr int kWsFirst = 20;
+
+enum CfgKind { kLds = 0, kDirect = 1, kLean = 2, kWsplit = 3 };
 struct CfgInfo {
   int BM, BN, BK;
   float eff;  // relative per-CU throughput used by the cost model
   int perCU;  // resident workgroups per CU assumed by the cost model
   int kind;
 };
-constexpr int kNumCfg = 20;
+constexpr int kNumCfg = kWsFirst + kNumWs;
 const CfgInfo kCfgs[kNumCfg] = {
     {64, 64, 32, 1.00f, 4, kLds},     {64, 64, 16, 1.00f, 8, kLds},     {128, 64, 16, 0.97f, 5, kLds},
     {128, 128, 16, 0.95f, 2, kLds},   {64, 128, 32, 0.97f, 3, kLds},    {64, 128, 16, 0.95f, 5, kLds},
@@ -586,7 +591,10 @@ const CfgInfo kCfgs[kNumCfg] = {
     {64, 128, 32, 1.10f, 3, kLean},   {128, 64, 32, 1.10f, 3, kLean},   {128, 128, 32, 1.05f, 2, kLean},
     {64, 64, 64, 1.10f, 2, kLean},    {64, 32, 32, 1.10f, 6, kLean},    {128, 64, 32, 1.10f, 2, kLean},
     {64, 128, 32, 1.10f, 2, kLean},   {128, 128, 32, 1.05f, 2, kLean},
+    // wave-split tiles: timed only (the cost model never picks them)
+    {32, 32, 32, 1.f, 1, kWsplit},    {32, 32, 32, 1.f, 1, kWsplit},    {32, 64, 32, 1.f, 1, kWsplit},
 };
+static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == kNumCfg, "one CfgInfo per configuration");
 
 template <class Cfg>
 int grid_for(ConvArgs& a, dim3& grid) {
@@ -814,7 +822,10 @@ int launch_nhwc_cfg(int cfg, const ConvArgs& a, int mode, int cus, hipStream_t s
     case 17: return launch_nhwc<Lean17>(a, mode, cus, s);
     case 18: return launch_nhwc<Lean18>(a, mode, cus, s);
     case 19: return launch_nhwc<Lean19>(a, mode, cus, s);
-    default: return fail(TNH_ERR_UNSUPPORTED, "conv2d: channels-last convolution needs a lean tile (11..19)");
+    default:
+      if (cfg >= kWsFirst && cfg < kNumCfg) return launch_wsplit_nhwc(cfg - kWsFirst, a, mode, s);
+      return fail(TNH_ERR_UNSUPPORTED, "conv2d: channels-last convolution needs a lean or wave-split tile (11..%d)",
+                  kNumCfg - 1);
   }
 }
 
@@ -922,7 +933,8 @@ int g_forced_cfg = -1;
 // The register-direct kernels need whole 16-channel chunks inside one tap
 // and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
 bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = false) {
-  if (nhwc) return kCfgs[c].kind == kLean && smallIO && va && C % kCfgs[c].BK == 0;
+  if (nhwc) return (kCfgs[c].kind == kLean || kCfgs[c].kind == kWsplit) && smallIO && va && C % kCfgs[c].BK == 0;
+  if (kCfgs[c].kind == kWsplit) return false;  // channels-last only
   if (kCfgs[c].kind == kLean && !smallIO) return false;
   if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
   if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;
@@ -953,6 +965,12 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
   std::vector<Cand> cands;
   for (int c = 0; c < kNumCfg; ++c) {
     if (!cfg_valid(c, mode, C, va, smallIO, nhwc)) continue;
+    if (kCfgs[c].kind == kWsplit) {
+      // whole tiles only; timed, never the cost model's pick, so absent from
+      // the deterministic mode's choice
+      if (!det) cands.push_back({c, 1, 0, 0});
+      continue;
+    }
     cands.push_back({c, 1, 0, 0});
     const CfgInfo& ci = kCfgs[c];
     const int64_t tiles = tilesOf(ci);
@@ -1019,6 +1037,7 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
   {
     float bc = 1e30f;
     for (const Cand& c : cands) {
+      if (kCfgs[c.cfg].kind == kWsplit) continue;
       const float v = cost(kCfgs[c.cfg], F, N, K, cx->cu_count, c.splits);
       if (v < bc) bc = v, best = c;
     }
@@ -1030,6 +1049,7 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     if (g_forced_cfg >= 0 && cfg_valid(g_forced_cfg % 64, mode, C, va, smallIO, nhwc)) {
       const int c = g_forced_cfg % 64, hi = g_forced_cfg / 64;
       if (hi > 16 && kCfgs[c].kind != kLean) return fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
+      if (hi > 1 && kCfgs[c].kind == kWsplit) return fail(TNH_ERR_UNSUPPORTED, "conv2d: split of a wave-split tile");
       if (nhwc && hi >= 2 && hi <= 16) return run({c, 1, hi, 2});  // split-K: every tile cut
       if (hi >= 34) return run({c, 1, hi - 32, 1});
       if (hi >= 18) return run({c, 1, hi - 16, 0});
@@ -1063,11 +1083,16 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
         if (wsFloats(c) > maxWs) maxWs = wsFloats(c), maxC = c;
       if (maxWs > 0) (void)wsFor(maxC);
       times.assign(list.size(), 1e30f);
+      // TNH_VERBOSE=2: every candidate's time
+      static const bool all = std::getenv("TNH_VERBOSE") && std::atoi(std::getenv("TNH_VERBOSE")) >= 2;
       for (size_t i = 0; i < list.size(); ++i) {
         const Cand& c = list[i];
         if ((c.splits > 1 || c.tail > 0) && !wsFor(c)) continue;
         if (int st = timeCand(c, times[i])) return st;
         if (times[i] < bestMs) bestMs = times[i], best = c;
+        if (all)
+          std::fprintf(stderr, "[tnh]   candidate cfg %d split %d tail %d%s: %.4f ms\n", c.cfg, c.splits, c.tail,
+                       c.slots == 1 ? "/slots" : (c.slots == 2 ? "/all" : ""), times[i]);
       }
       return TNH_OK;
     };

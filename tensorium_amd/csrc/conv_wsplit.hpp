@@ -1,0 +1,41 @@
+// Channels-last convolution with K split over the waves of a workgroup
+// (conv_wsplit.hip): the tile shapes and the launch entry the tuner in
+// conv.hip calls.
+#pragma once
+#include "conv_args.hpp"
+
+namespace tnh {
+namespace conv {
+
+// One workgroup computes a (32*FM) pixels x (32*FN) filters tile with W
+// waves; wave w accumulates panels [w*P/W, (w+1)*P/W) of the P = K/32
+// panels of 32 k through its own LDS panel, then the W partial tiles are
+// summed through LDS in wave order.
+template <int FM_, int FN_, int W_>
+struct WsCfg {
+  static constexpr int FM = FM_, FN = FN_, W = W_;
+  static constexpr int NT = W * 64;
+  static constexpr int BM = 32 * FM, BN = 32 * FN, BK = 32;
+  static constexpr int UNITS = FM * FN * 4;  // 16-byte register quads of one wave's partial tile
+  static constexpr int RED_FLOATS = W * UNITS * 64 * 4;
+  static constexpr int PANEL_FLOATS = W * (BM + BN) * 32;  // one panel per wave
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16, "waves per workgroup");
+  static_assert(RED_FLOATS <= 16384 && PANEL_FLOATS <= 16384, "LDS above 64 KiB");
+};
+
+// Tile shapes (index into kWsCfgs; the tuner's configurations kWsFirst + i),
+// the ones that won a YOLOv3 layer shape in timed sweeps of (FM, FN, W) in
+// {1, 2} x {1, 2} x {2, 4, 8}: 32x32 with 4 or 8 waves, 32x64 with 4.
+struct WsInfo {
+  int FM, FN, W;
+};
+constexpr int kNumWs = 3;
+constexpr WsInfo kWsCfgs[kNumWs] = {{1, 1, 4}, {1, 1, 8}, {1, 2, 4}};
+
+// Launches tile shape `ws` (0 .. kNumWs-1) for a channels-last convolution
+// whose ConvArgs are filled as for conv_nhwc_kernel (mode kTap3 or k1x1;
+// C % 32 == 0; out and residual within 2 GiB).
+int launch_wsplit_nhwc(int ws, ConvArgs a, int mode, hipStream_t s);
+
+}  // namespace conv
+}  // namespace tnh

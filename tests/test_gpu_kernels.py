@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_NCHW_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -310,7 +310,7 @@ def test_conv_forward_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(H(dout, hip), ref) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(NUM_CONV_CFGS))
+@pytest.mark.parametrize("cfg", range(NUM_CONV_NCHW_CFGS))
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", [(2, 32, 26, 64, 3, 1, 1, acLEAKY), (1, 64, 13, 96, 3, 2, 1, acLEAKY),
                                                  (2, 48, 11, 40, 3, 1, 1, acLINEAR), (1, 3, 20, 16, 3, 1, 1, acLEAKY),
                                                  (2, 40, 9, 70, 1, 1, 0, acLEAKY), (3, 64, 13, 300, 1, 1, 0, acLEAKY),

@@ -10,8 +10,8 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import (CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_CFGS, TNHError,
-                                  acLEAKY, acLINEAR, acLOGISTIC)
+from tensorium_amd.nnhip import (CONV_LEAN_CFGS, CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE,
+                                  CONV_WSPLIT_CFGS, TNHError, acLEAKY, acLINEAR, acLOGISTIC)
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -135,7 +135,7 @@ def test_conv_nhwc_channel_slices(hip, k, s):
     assert np.all(got[..., :32] == 7.0) and np.all(got[..., 32 + F:] == 7.0)
 
 
-@pytest.mark.parametrize("cfg", range(11, NUM_CONV_CFGS))
+@pytest.mark.parametrize("cfg", CONV_LEAN_CFGS)
 @pytest.mark.parametrize("hi", [0, 4, CONV_TAIL_BASE + 3, CONV_TAIL_SLOT_BASE + 2])
 def test_conv_nhwc_forced_configs(hip, cfg, hi):
     """Every lean tile, plain, split-K (every tile cut), and tail splits per
@@ -155,6 +155,82 @@ def test_conv_nhwc_forced_configs(hip, cfg, hi):
     finally:
         hip.setConvAutotune(True, -1)
     assert np.array_equal(H(dout, hip).transpose(0, 3, 1, 2), ref)
+
+
+# (B, C, H, F, k, stride, pad, residual): ragged pixel and filter counts (not
+# multiples of the 32/64 tile), stride 2, 1x1 with one group per wave (K = 32
+# over up to 16 waves: some waves get no group), and YOLOv3's 13x13 batch-1
+# shape
+WSPLIT_SHAPES = [
+    (1, 64, 13, 96, 3, 1, 1, True),
+    (2, 32, 10, 40, 3, 2, 1, False),
+    (1, 32, 9, 70, 1, 1, 0, True),
+    (3, 96, 7, 33, 1, 1, 0, False),
+    (1, 512, 13, 1024, 3, 1, 1, False),
+]
+
+
+@pytest.mark.parametrize("cfg", CONV_WSPLIT_CFGS)
+@pytest.mark.parametrize("shape", WSPLIT_SHAPES)
+def test_conv_nhwc_wsplit_integer(hip, cfg, shape):
+    """Every wave-split tile (K of a tile split over the waves of its
+    workgroup, partial tiles summed in LDS) on integer data: every partial
+    sum is exact, so the result equals the oracle bit for bit; channel-slice
+    strides for x, out and the residual, the rest of the output untouched."""
+    B, Cc, Hh, F, k, s, p, with_res = shape
+    case(f"conv nhwc wsplit cfg{cfg} {shape}")
+    OH = (Hh + 2 * p - k) // s + 1
+    rng = np.random.default_rng(cfg * 1000 + Cc + F)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    ref = R.conv_forward(x, Wt, b, k, s, p, acLEAKY)
+    xin = np.zeros((B, Hh, Hh, Cc + 32), np.float32)
+    xin[..., 32:] = nhwc(x)
+    res = rin = None
+    if with_res:
+        res = rng.integers(-5, 6, (B, F, OH, OH)).astype(np.float32)
+        ref = R.addvv(ref, res)
+        rin = np.zeros((B, OH, OH, F + 4), np.float32)
+        rin[..., 4:] = nhwc(res)
+    dout = D(np.full((B, OH, OH, F + 8), 7.0, np.float32))
+    hip.setConvAutotune(True, cfg)
+    try:
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, s, p, D(xin), 32, D(tap_major(Wt, F, Cc, k)), D(b), acLEAKY,
+                              dout, 8, inPix=Cc + 32, outPix=F + 8,
+                              residual=None if rin is None else D(rin), resOffset=4, resPix=F + 4)
+    finally:
+        hip.setConvAutotune(True, -1)
+    got = H(dout, hip)
+    assert np.array_equal(got[..., 8:].transpose(0, 3, 1, 2), ref)
+    assert np.all(got[..., :8] == 7.0)
+
+
+@pytest.mark.parametrize("cfg", CONV_WSPLIT_CFGS)
+@pytest.mark.parametrize("act", [acLEAKY, acLINEAR, acLOGISTIC])
+def test_conv_nhwc_wsplit_vs_oracle(hip, cfg, act):
+    """Wave-split tiles on YOLOv3's batch-1 26x26 3x3 layer shape (C 256 ->
+    512) with random data: per tensor within 1e-5 of the oracle.  The fused
+    logistic is TNNCuda's 1/(1 + exp(-x)) (cuda_sgemm.cu:305-309), so that
+    case is held against the float64 sigmoid of the oracle's linear output
+    (the oracle's logistic is the CPU path's polynomial)."""
+    B, Cc, Hh, F, k = 1, 256, 26, 512, 3
+    case(f"conv nhwc wsplit cfg{cfg} act{act} vs oracle")
+    x = synth.uniform(90 + cfg, (B, Cc, Hh, Hh))
+    Wt = synth.normal(91, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(92, (F,), 0.1)
+    if act == acLOGISTIC:
+        lin = R.conv_forward(x, Wt, b, k, 1, 1, acLINEAR).astype(np.float64)
+        ref = 1.0 / (1.0 + np.exp(-lin))
+    else:
+        ref = R.conv_forward(x, Wt, b, k, 1, 1, act)
+    dout = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, cfg)
+    try:
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, 1, 1, D(nhwc(x)), 0, D(tap_major(Wt, F, Cc, k)), D(b), act, dout, 0)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert R.rel_err(H(dout, hip).transpose(0, 3, 1, 2), ref) <= TOL
 
 
 def test_conv_nhwc_rejects_unsupported(hip):
