@@ -94,6 +94,15 @@ int32_t tnh_event_create(void **ev);
 int32_t tnh_event_destroy(void *ev);
 int32_t tnh_event_record(void *ev);
 int32_t tnh_event_elapsed_ms(void *start, void *stop, float *ms);
+/* No TNNCuda counterpart (it runs one stream): the context stream waits for
+ * `ev`, recorded with tnh_event_record while another stream was selected.
+ * Forks and joins independent work (a network's yolo head tails) onto a
+ * second stream, eagerly or under graph capture.  Split-K scratch is kept
+ * per stream, so convolutions on different streams may overlap; scratch is
+ * allocated on a stream's first eager use (a stream captured before any
+ * eager call borrows the first stream's scratch and must not run beside
+ * it). */
+int32_t tnh_stream_wait_event(void *ev);
 
 /* ---- GEMM ------------------------------------------------------------- */
 /* TNNCuda.gemm (nncuda.pas:624) / cblas_sgemm (ntensors.pas:2231):

@@ -73,6 +73,7 @@ function tnh_d2h(dst, src: Pointer; bytes: Int64): LongInt; cdecl; external libt
 function tnh_event_create(ev: PPointer): LongInt; cdecl; external libtnh;
 function tnh_event_destroy(ev: Pointer): LongInt; cdecl; external libtnh;
 function tnh_event_record(ev: Pointer): LongInt; cdecl; external libtnh;
+function tnh_stream_wait_event(ev: Pointer): LongInt; cdecl; external libtnh;
 function tnh_event_elapsed_ms(start, stop: Pointer; ms: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgemm(transA, transB: LongInt; M, N, K: Int64; alpha: Single; A: PSingle; aOff, lda: Int64;
   B: PSingle; bOff, ldb: Int64; beta: Single; C: PSingle; cOff, ldc: Int64): LongInt; cdecl; external libtnh;

@@ -23,8 +23,15 @@ struct Context {
   hipStream_t tune_stream = nullptr; // private stream the autotuner captures its timing graphs on
   int cu_count = 0;
   int xcd_count = 8;
-  void* ws = nullptr;     // library scratch (split-K partial sums), grown on demand
-  size_t wsBytes = 0;
+  // Library scratch (split-K partial sums), one buffer per stream the
+  // library has launched on, grown on demand: work on different streams may
+  // run concurrently, so it never shares scratch.
+  struct WsSlot {
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+  };
+  std::vector<WsSlot> ws;
   // Outgrown scratch buffers: a graph captured earlier may still launch
   // kernels that address them, so they are freed only by tnh_finalize.
   std::vector<void*> wsRetired;
@@ -37,10 +44,11 @@ struct Context {
 
 constexpr int64_t kRedFloats = int64_t(1) << 20;  // 4 MiB of reduction partials
 
-// Returns a scratch buffer of at least `bytes` on the context device, growing
-// it (a new hipMalloc; the outgrown buffer stays allocated until
-// tnh_finalize) when needed; returns nullptr when growing is not possible
-// (allocation failure, or a stream of the context is being captured).
+// Returns the current stream's scratch buffer of at least `bytes` on the
+// context device, growing it (a new hipMalloc; the outgrown buffer stays
+// allocated until tnh_finalize) when needed; returns nullptr when growing is
+// not possible (allocation failure, or the stream or the tuning stream is
+// being captured).
 void* workspace(Context* c, size_t bytes);
 
 // Looks up, once per device and with that device current, the address of

@@ -77,25 +77,39 @@ int time_graph(Context* cx, const std::function<int(hipStream_t)>& launch, int r
 }
 
 void* workspace(Context* c, size_t bytes) {
-  if (bytes <= c->wsBytes) return c->ws;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  if (c->tune_stream &&
-      (hipStreamIsCapturing(c->tune_stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone))
+  Context::WsSlot* slot = nullptr;
+  for (Context::WsSlot& w : c->ws)
+    if (w.stream == c->stream) slot = &w;
+  if (slot && bytes <= slot->bytes) return slot->ptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone, ts = hipStreamCaptureStatusNone;
+  const bool capturing = hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+                         (c->tune_stream && (hipStreamIsCapturing(c->tune_stream, &ts) != hipSuccess ||
+                                             ts != hipStreamCaptureStatusNone));
+  if (capturing) {
+    // Nothing can be allocated now.  A stream that has no scratch of its own
+    // (captured after warming up on another stream) borrows the first
+    // stream's, as a single shared scratch would: then the two must not run
+    // at the same time.
+    if (!slot && !c->ws.empty() && bytes <= c->ws[0].bytes) return c->ws[0].ptr;
     return nullptr;
-  if (c->ws) {
-    c->wsRetired.push_back(c->ws);
-    c->ws = nullptr;
-    c->wsBytes = 0;
+  }
+  if (!slot) {
+    c->ws.push_back({c->stream, nullptr, 0});
+    slot = &c->ws.back();
+  }
+  if (slot->ptr) {
+    c->wsRetired.push_back(slot->ptr);
+    slot->ptr = nullptr;
+    slot->bytes = 0;
   }
   const size_t want = bytes + (bytes >> 2);
-  if (hipMalloc(&c->ws, want) != hipSuccess) {
+  if (hipMalloc(&slot->ptr, want) != hipSuccess) {
     (void)hipGetLastError();
-    c->ws = nullptr;
+    slot->ptr = nullptr;
     return nullptr;
   }
-  c->wsBytes = want;
-  return c->ws;
+  slot->bytes = want;
+  return slot->ptr;
 }
 
 }  // namespace tnh
@@ -125,7 +139,8 @@ extern "C" int32_t tnh_init(int32_t device) {
     if (g_ctx.device == device) return TNH_OK;
     (void)hipSetDevice(g_ctx.device);
     (void)hipStreamSynchronize(g_ctx.stream);
-    if (g_ctx.ws) (void)hipFree(g_ctx.ws);
+    for (const Context::WsSlot& w : g_ctx.ws)
+      if (w.ptr) (void)hipFree(w.ptr);
     for (void* p : g_ctx.wsRetired) (void)hipFree(p);
     if (g_ctx.red) (void)hipFree(g_ctx.red);
     (void)hipStreamDestroy(g_ctx.own_stream);
@@ -169,7 +184,8 @@ extern "C" int32_t tnh_finalize(void) {
   if (!g_live) return TNH_OK;
   (void)hipSetDevice(g_ctx.device);
   (void)hipStreamSynchronize(g_ctx.stream);
-  if (g_ctx.ws) (void)hipFree(g_ctx.ws);
+  for (const Context::WsSlot& w : g_ctx.ws)
+    if (w.ptr) (void)hipFree(w.ptr);
   for (void* p : g_ctx.wsRetired) (void)hipFree(p);
   if (g_ctx.red) (void)hipFree(g_ctx.red);
   (void)hipStreamDestroy(g_ctx.own_stream);
@@ -270,6 +286,12 @@ extern "C" int32_t tnh_event_record(void* ev) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(ev != nullptr, "event_record: NULL");
   return hip_status(hipEventRecord(static_cast<hipEvent_t>(ev), cx->stream), "hipEventRecord");
+}
+
+extern "C" int32_t tnh_stream_wait_event(void* ev) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(ev != nullptr, "stream_wait_event: NULL");
+  return hip_status(hipStreamWaitEvent(cx->stream, static_cast<hipEvent_t>(ev), 0), "hipStreamWaitEvent");
 }
 
 extern "C" int32_t tnh_event_elapsed_ms(void* start, void* stop, float* ms) {

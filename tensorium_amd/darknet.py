@@ -216,6 +216,7 @@ class Network:
         self.input_shape = (batch,) + layers[0]["in"]
         if layout == "nhwc":
             self._plan_nhwc(device)
+            self._plan_branches(use)
             return
         # At batch 1 a channel slice of an NCHW route buffer is contiguous, so
         # a route input's producer (convolution, shortcut or upsample) writes
@@ -305,6 +306,28 @@ class Network:
                 if layers[self._owner(s_)]["type"] == "yolo" and L["type"] != "route":
                     raise NotImplementedError(f"layer {L['index']} reads yolo layer {s_}")
 
+    def _plan_branches(self, use):
+        """Yolo head tails that can run beside the rest of the network: the
+        convolutions ending in a yolo layer whose outputs feed only the next
+        layer of the tail (YOLOv3: 80-82 and 92-94, while 83-91 and 95-106
+        continue from layer 79 / 91).  A tail forks after the layer before it
+        and joins at the end of the forward pass; the last yolo layer has
+        nothing beside it and stays on the main stream."""
+        layers = self.layers
+        self.branches = {}  # first layer of a tail -> its yolo layer
+        for L in layers:
+            y = L["index"]
+            if L["type"] != "yolo" or y + 1 >= len(layers):
+                continue
+            s_ = y
+            while (s_ - 1 > 0 and layers[s_ - 1]["type"] == "convolutional" and use[s_ - 1] == [s_]
+                   and s_ - 1 not in self.fused):
+                s_ -= 1
+            if s_ < y and all(c <= y for i in range(s_, y + 1) for c in use[i]):
+                self.branches[s_] = y
+        self._side = None
+        self.use_branches = False
+
     def nhwc_store(self, i):
         """(tensor, channel offset, pixel stride) of layer i's output."""
         return self.store[self._owner(i)]
@@ -326,22 +349,74 @@ class Network:
             return self.out[i + 1]
         return self.out[i]
 
-    def forward(self, x, on_layer=None):
+    def forward(self, x, on_layer=None, branches=None):
         """Runs every layer on the context stream; returns the yolo outputs.
 
         on_layer(i, begin): optional hook called before (begin=True) and after
         (begin=False) the launches of layer i (used to bracket them with
-        events)."""
-        hip, B = self.hip, self.batch
+        events).  branches: run the yolo head tails on a second stream, forked
+        and joined through events (channels-last networks; default:
+        self.use_branches, which is off: in graph replays on ROCm 7.2 the
+        cross-stream edges cost more than the overlap gains, 1.232 against
+        1.188 ms at batch 1 and 8.86 against 8.80 ms at batch 16).  The
+        first forward pass always runs on one stream (it tunes every shape
+        alone on the GPU)."""
+        hip = self.hip
+        tails = getattr(self, "branches", {})
+        if branches is None:
+            branches = getattr(self, "use_branches", False) and on_layer is None
+        if not getattr(self, "_tuned", False):
+            branches = False
+        self._tuned = True
+        if branches and tails:
+            return self._forward_branched(x, tails)
         prev = x
         heads = []
         for L in self.layers:
-            i, t = L["index"], L["type"]
+            i = L["index"]
             if on_layer:
                 on_layer(i, True)
             prev = self._layer(L, prev, heads)
             if on_layer:
                 on_layer(i, False)
+        return heads
+
+    def _forward_branched(self, x, tails):
+        """forward() with each yolo head tail on the side stream: the main
+        stream records an event after the layer before the tail, the side
+        stream waits for it and runs the tail, and the main stream waits for
+        every tail's end event after the last layer (also under graph
+        capture, where the events become the graph's edges)."""
+        hip, torch = self.hip, self.torch
+        if self._side is None:
+            self._side = torch.cuda.Stream()  # default priority
+            self._events = {s_: (hip.eventCreate(), hip.eventCreate()) for s_ in tails}
+        main = hip.stream
+        side = self._side.cuda_stream
+        heads, joins = [], []
+        prev = x
+        skip = -1
+        for L in self.layers:
+            i = L["index"]
+            if i <= skip:
+                continue
+            if i in tails:
+                fork, join = self._events[i]
+                hip.eventRecord(fork)
+                hip.setStream(side)
+                try:
+                    hip.streamWaitEvent(fork)
+                    for j in range(i, tails[i] + 1):
+                        self._layer(self.layers[j], None, heads)
+                    hip.eventRecord(join)
+                finally:
+                    hip.setStream(main)
+                joins.append(join)
+                skip = tails[i]
+                continue
+            prev = self._layer(L, prev, heads)
+        for ev in joins:
+            hip.streamWaitEvent(ev)
         return heads
 
     def _layer_nhwc(self, L, x, heads):
@@ -457,6 +532,10 @@ class Network:
         hip = self.hip
         self.torch.cuda.synchronize()
         hip.resetStream()
+        if getattr(self, "_tuned", False):
+            # one eager pass on the streams the capture uses: their split-K
+            # scratch cannot be allocated while they are being captured
+            self.forward(x)
         hip.finish()
         hip.graphBegin()
         try:

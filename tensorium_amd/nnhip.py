@@ -72,6 +72,7 @@ _PROTOS = {
     "tnh_event_create": [C.POINTER(vp)],
     "tnh_event_destroy": [vp],
     "tnh_event_record": [vp],
+    "tnh_stream_wait_event": [vp],
     "tnh_event_elapsed_ms": [vp, vp, C.POINTER(f32)],
     "tnh_sgemm": [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64],
     "tnh_sgemm_strided_batched": [i32, i32, i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64,
@@ -571,6 +572,10 @@ class TNNHip:
         ms = f32(0)
         call("tnh_event_elapsed_ms", start, stop, C.byref(ms))
         return ms.value
+
+    def streamWaitEvent(self, ev):
+        """The context stream waits for `ev` (recorded on another stream)."""
+        call("tnh_stream_wait_event", ev)
 
     def eventDestroy(self, ev):
         call("tnh_event_destroy", ev)

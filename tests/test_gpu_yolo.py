@@ -192,6 +192,40 @@ def test_yolov3_nhwc_heads(hip, yolo):
         hip.useTorchStream()
 
 
+@pytest.mark.parametrize("B", [1, 4])
+def test_yolov3_nhwc_branches(hip, yolo, B):
+    """The yolo head tails (layers 80-82 and 92-94) forked onto a second
+    stream: the planner finds exactly those two tails, and the branched
+    eager forward and two replays of its graph equal the single-stream
+    forward bit for bit (the same tuned kernels run; only the stream and
+    the split-K scratch differ)."""
+    layers, W = yolo
+    print(f"[case] yolov3-416 batch {B} nhwc head tails on a second stream", flush=True)
+    x = synth.uniform(17, (B, 3, 416, 416))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    n = darknet.Network(hip, layers, B, W, layout="nhwc")
+    assert n.branches == {80: 82, 92: 94}
+    single = [h.cpu().numpy() for h in n.forward(dx, branches=False)]
+    hip.finish()
+    got = [h.cpu().numpy() for h in n.forward(dx, branches=True)]
+    hip.finish()
+    for u, v in zip(got, single):
+        assert np.array_equal(u, v)
+    n.use_branches = True
+    try:
+        n.capture(dx)
+        for rep in range(2):
+            heads = n.replay()
+            hip.finish()
+            for u, v in zip([h.cpu().numpy() for h in heads], single):
+                assert np.array_equal(u, v), rep
+            torch.cuda.synchronize()
+    finally:
+        n.release_graph()
+        hip.useTorchStream()
+
+
 def test_yolov3_nhwc_matches_nchw_and_replays(hip, yolo):
     """Batch 2: the channels-last network's head convolutions equal the NCHW
     network's within the per-tensor bound, the route inputs written in place
