@@ -216,6 +216,39 @@ int32_t tnh_conv2d_fwd_nhwc(int64_t batch, int64_t C, int64_t H, int64_t W,
                             const float *bias, int64_t biasOff, int32_t act,
                             const float *residual, int64_t rOff, int64_t rPix,
                             float *out, int64_t outOff, int64_t outPix);
+/* No reference counterpart: tnh_conv2d_fwd_nhwc whose result is written only
+ * as its nearest-upsampled image, the output of the TUpSampleLayer that
+ * follows it (nupsamplelayer.pas:83-146, upsample forward): output pixel
+ * (b, y, x), channel f goes to pixels (b, s*y + dy, s*x + dx), dy, dx < s,
+ * of out (pixel stride outPix, a channel slice of a route buffer allowed),
+ * times upScale; the convolution's own output is not stored.  One launch
+ * instead of two (conv, then tnh_upsample_nhwc), the same values bit for
+ * bit.  No residual. */
+int32_t tnh_conv2d_fwd_nhwc_upsample(int64_t batch, int64_t C, int64_t H,
+                                     int64_t W, int64_t F, int64_t kh,
+                                     int64_t kw, int64_t pH, int64_t pW,
+                                     int64_t sY, int64_t sX, const float *x,
+                                     int64_t xOff, int64_t xPix,
+                                     const float *weights, int64_t wOff,
+                                     const float *bias, int64_t biasOff,
+                                     int32_t act, int64_t upStride,
+                                     float upScale, float *out,
+                                     int64_t outOff, int64_t outPix);
+/* No reference counterpart: tnh_conv2d_fwd_nhwc for a yolo head: besides out
+ * it writes TYoloLayer.forward's head (nyololayer.pas:786-830, as
+ * tnh_yolo_fwd_nhwc) to the NCHW tensor yoloOut + yoloOff
+ * [batch][F][OH][OW], F = n * (5 + classes): one launch instead of two, the
+ * same values bit for bit.  No residual. */
+int32_t tnh_conv2d_fwd_nhwc_yolo(int64_t batch, int64_t C, int64_t H,
+                                 int64_t W, int64_t F, int64_t kh, int64_t kw,
+                                 int64_t pH, int64_t pW, int64_t sY,
+                                 int64_t sX, const float *x, int64_t xOff,
+                                 int64_t xPix, const float *weights,
+                                 int64_t wOff, const float *bias,
+                                 int64_t biasOff, int32_t act, float *out,
+                                 int64_t outOff, int64_t outPix, int64_t n,
+                                 int64_t classes, float *yoloOut,
+                                 int64_t yoloOff);
 /* No reference counterpart: tnh_conv2d_fwd_nhwc for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, results and kernels;

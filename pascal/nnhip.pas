@@ -101,6 +101,13 @@ function tnh_conv2d_fwd_nhwc_noalloc(batch, C, H, W, F, kh, kw, pH, pW, sY, sX: 
   xOff, xPix: Int64; weights: PSingle; wOff: Int64; bias: PSingle; biasOff: Int64; act: LongInt;
   residual: PSingle; rOff, rPix: Int64; output: PSingle; outOff, outPix: Int64): LongInt; cdecl;
   external libtnh;
+function tnh_conv2d_fwd_nhwc_upsample(batch, C, H, W, F, kh, kw, pH, pW, sY, sX: Int64; x: PSingle;
+  xOff, xPix: Int64; weights: PSingle; wOff: Int64; bias: PSingle; biasOff: Int64; act: LongInt;
+  upStride: Int64; upScale: Single; output: PSingle; outOff, outPix: Int64): LongInt; cdecl; external libtnh;
+function tnh_conv2d_fwd_nhwc_yolo(batch, C, H, W, F, kh, kw, pH, pW, sY, sX: Int64; x: PSingle;
+  xOff, xPix: Int64; weights: PSingle; wOff: Int64; bias: PSingle; biasOff: Int64; act: LongInt;
+  output: PSingle; outOff, outPix, n, classes: Int64; yoloOut: PSingle; yoloOff: Int64): LongInt; cdecl;
+  external libtnh;
 function tnh_conv2d_noalloc_scratch_bytes(bytes: PInt64): LongInt; cdecl; external libtnh;
 function tnh_conv2d_pack_weights(F, C, kh, kw: Int64; src, dst: PSingle): LongInt; cdecl; external libtnh;
 function tnh_conv2d_set_autotune(enable, forcedConfig: LongInt): LongInt; cdecl; external libtnh;

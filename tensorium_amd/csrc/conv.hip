@@ -908,10 +908,11 @@ struct TuneKey {
   int k, s, mode, va, vb;
   int nhwc, xPix, outPix, resPix;
   int hasRes, smallIO;
+  int epi;  // channels-last epilogue variant: 0 plain, 1 upsampled output, 2 yolo head
   bool operator==(const TuneKey& o) const {
     return F == o.F && N == o.N && K == o.K && C == o.C && H == o.H && W == o.W && k == o.k && s == o.s &&
            mode == o.mode && va == o.va && vb == o.vb && nhwc == o.nhwc && xPix == o.xPix && outPix == o.outPix &&
-           resPix == o.resPix && hasRes == o.hasRes && smallIO == o.smallIO;
+           resPix == o.resPix && hasRes == o.hasRes && smallIO == o.smallIO && epi == o.epi;
   }
 };
 struct TuneHash {
@@ -919,7 +920,7 @@ struct TuneHash {
     size_t h = 1469598103934665603ull;
     for (int64_t v : {t.F, t.N, t.K, t.C, t.H, t.W, (int64_t)t.k, (int64_t)t.s, (int64_t)t.mode, (int64_t)t.va,
                       (int64_t)t.vb, (int64_t)t.nhwc, (int64_t)t.xPix, (int64_t)t.outPix, (int64_t)t.resPix,
-                      (int64_t)t.hasRes, (int64_t)t.smallIO})
+                      (int64_t)t.hasRes, (int64_t)t.smallIO, (int64_t)t.epi})
       h = (h ^ static_cast<size_t>(v)) * 1099511628211ull;
     return h;
   }
@@ -1133,13 +1134,22 @@ using namespace tnh::conv;
 
 namespace {
 
-// tnh_conv2d_fwd_nhwc and its no-allocation variant (noAlloc: split pieces in
-// the device's static scratch, no autotuning).
+// Epilogue variant of a channels-last call (ConvArgs::upS / yolo).
+struct NhwcEpi {
+  int64_t upS = 0;
+  float upScale = 1.f;
+  float* yolo = nullptr;
+  int64_t yoloN = 0, yoloClasses = 0;
+};
+
+// tnh_conv2d_fwd_nhwc, its no-allocation variant (noAlloc: split pieces in
+// the device's static scratch, no autotuning) and its upsample / yolo
+// epilogue variants.
 int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh, int64_t kw, int64_t pH,
                     int64_t pW, int64_t sY, int64_t sX, const float* x, int64_t xOff, int64_t xPix,
                     const float* weights, int64_t wOff, const float* bias, int64_t biasOff, int32_t act,
                     const float* residual, int64_t rOff, int64_t rPix, float* out, int64_t outOff, int64_t outPix,
-                    bool noAlloc) {
+                    bool noAlloc, const NhwcEpi& epi = NhwcEpi{}) {
   TNH_REQUIRE_CTX(cx);
   float* fixed = nullptr;
   if (noAlloc) {
@@ -1159,6 +1169,13 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
   const int64_t OH = (H + 2 * pH - kh) / sY + 1, OW = (W + 2 * pW - kw) / sX + 1;
   TNH_ARG(OH > 0 && OW > 0, "conv2d_nhwc: empty output");
   TNH_ARG(kh == 3 || (sY == 1 && sX == 1 && pH == 0 && pW == 0), "conv2d_nhwc: 1x1 needs stride 1, no padding");
+  const bool variant = epi.upS > 0 || epi.yolo;
+  TNH_ARG(!variant || (!xNchw && !residual), "conv2d_nhwc: an upsampled or yolo output takes no residual and "
+                                             "no NCHW image");
+  TNH_ARG(epi.upS >= 0 && epi.upS <= 16, "conv2d_nhwc_upsample: stride %lld (1..16)", (long long)epi.upS);
+  TNH_ARG(!epi.yolo || (epi.yoloN > 0 && epi.yoloClasses >= 0 && F == epi.yoloN * (epi.yoloClasses + 5)),
+          "conv2d_nhwc_yolo: %lld filters for %lld anchors x (5 + %lld classes)", (long long)F, (long long)epi.yoloN,
+          (long long)epi.yoloClasses);
   if (batch == 0) return TNH_OK;
   const int64_t K = C * kh * kw, N = batch * OH * OW;
   const int64_t xElems = xNchw ? batch * C * H * W : (batch * H * W - 1) * xPix + C;
@@ -1186,6 +1203,16 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
   a.rBatchStride = residual ? OH * OW * rPix : 0;
   a.outBytes = ((N - 1) * outPix + F) * 4;
   a.resBytes = residual ? ((N - 1) * rPix + F) * 4 : 0;
+  if (epi.upS > 0) {  // out is the upsampled image
+    a.upS = static_cast<int>(epi.upS);
+    a.upScale = epi.upScale;
+    a.outBatchStride = OH * OW * epi.upS * epi.upS * outPix;
+    a.outBytes = ((N * epi.upS * epi.upS - 1) * outPix + F) * 4;
+  }
+  if (epi.yolo) {
+    a.yolo = epi.yolo;
+    a.yoloEntries = static_cast<int>(epi.yoloClasses + 5);
+  }
   if (xNchw) return launch_smallc<true, true>(a, cx->stream);
 
   const int mode = kh == 3 ? kTap3 : k1x1;
@@ -1194,7 +1221,7 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
   TNH_ARG(va && smallIO && C % 32 == 0,
           "conv2d_nhwc: needs C %% 32 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
   const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, false, 1, (int)xPix, (int)outPix,
-                    residual ? (int)rPix : 0, residual != nullptr, smallIO};
+                    residual ? (int)rPix : 0, residual != nullptr, smallIO, epi.upS > 0 ? 1 : (epi.yolo ? 2 : 0)};
   return conv_dispatch(cx, a, mode, va, false, smallIO, true, key, fixed);
 }
 
@@ -1217,6 +1244,35 @@ extern "C" int32_t tnh_conv2d_fwd_nhwc_noalloc(int64_t batch, int64_t C, int64_t
                                                int64_t rPix, float* out, int64_t outOff, int64_t outPix) {
   return conv_nhwc_entry(batch, C, H, W, F, kh, kw, pH, pW, sY, sX, x, xOff, xPix, weights, wOff, bias, biasOff, act,
                          residual, rOff, rPix, out, outOff, outPix, true);
+}
+
+extern "C" int32_t tnh_conv2d_fwd_nhwc_upsample(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F,
+                                                int64_t kh, int64_t kw, int64_t pH, int64_t pW, int64_t sY,
+                                                int64_t sX, const float* x, int64_t xOff, int64_t xPix,
+                                                const float* weights, int64_t wOff, const float* bias,
+                                                int64_t biasOff, int32_t act, int64_t upStride, float upScale,
+                                                float* out, int64_t outOff, int64_t outPix) {
+  TNH_ARG(upStride >= 1, "conv2d_nhwc_upsample: stride %lld", (long long)upStride);
+  NhwcEpi e;
+  e.upS = upStride;
+  e.upScale = upScale;
+  return conv_nhwc_entry(batch, C, H, W, F, kh, kw, pH, pW, sY, sX, x, xOff, xPix, weights, wOff, bias, biasOff, act,
+                         nullptr, 0, 0, out, outOff, outPix, false, e);
+}
+
+extern "C" int32_t tnh_conv2d_fwd_nhwc_yolo(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                            int64_t kw, int64_t pH, int64_t pW, int64_t sY, int64_t sX,
+                                            const float* x, int64_t xOff, int64_t xPix, const float* weights,
+                                            int64_t wOff, const float* bias, int64_t biasOff, int32_t act,
+                                            float* out, int64_t outOff, int64_t outPix, int64_t n, int64_t classes,
+                                            float* yoloOut, int64_t yoloOff) {
+  TNH_ARG(yoloOut != nullptr && yoloOff >= 0, "conv2d_nhwc_yolo: NULL head or negative offset");
+  NhwcEpi e;
+  e.yolo = yoloOut + yoloOff;
+  e.yoloN = n;
+  e.yoloClasses = classes;
+  return conv_nhwc_entry(batch, C, H, W, F, kh, kw, pH, pW, sY, sX, x, xOff, xPix, weights, wOff, bias, biasOff, act,
+                         nullptr, 0, 0, out, outOff, outPix, false, e);
 }
 
 extern "C" int32_t tnh_conv2d_noalloc_scratch_bytes(int64_t* bytes) {

@@ -7,6 +7,7 @@
 #pragma once
 #include "common.hpp"
 #include "gemm_core.hpp"
+#include "yolo_math.hpp"
 
 namespace tnh {
 namespace conv {
@@ -40,6 +41,18 @@ struct ConvArgs {
   // and res (the channel count of the buffer a tensor lives in, so a tensor
   // can be a channel slice of a wider one); images are H*W*pixel-stride apart.
   int xPix, outPix, resPix;
+  // Channels-last epilogue variants (0 / nullptr: off):
+  //   upS > 0: the result is written only as its nearest-upsampled image, the
+  //     output of the TUpSampleLayer that follows (nupsamplelayer.pas:83-146):
+  //     pixel (b, y, x) goes to pixels (b, upS*y + dy, upS*x + dx) of out
+  //     (pixel stride outPix), times upScale;
+  //   yolo: the result is also written through TYoloLayer.forward's transform
+  //     (nyololayer.pas:786-830) to the NCHW head yolo[b][f][y][x]
+  //     (yoloEntries = 5 + classes channels per anchor).
+  int upS;
+  float upScale;
+  float* yolo;
+  int yoloEntries;
 };
 
 // K walk / B operand of a convolution kernel
@@ -239,6 +252,26 @@ __device__ inline void conv_store_buf(const ConvArgs& a, const f32x16 (&acc)[FM]
   }
 }
 
+// One finished result v of output pixel m, filter f (both in range) under
+// the epilogue variants a.upS / a.yolo (see ConvArgs), channels-last.  Off
+// the hot path: the per-element index arithmetic is plain.
+__device__ inline void store_nhwc_variant(const ConvArgs& a, __amdgpu_buffer_rsrc_t outR, int64_t m, int64_t f,
+                                          float v) {
+  const int64_t OHW = a.g.OHW, OW = a.g.OW;
+  const int64_t b = m / OHW, p = m - b * OHW;
+  if (a.upS > 0) {
+    const int64_t s = a.upS, OH = OHW / OW, y = p / OW, x = p - y * OW, OWs = OW * s;
+    const int64_t base = (b * OH * s + y * s) * OWs + x * s;
+    const float sv = a.upScale * v;
+    for (int64_t dy = 0; dy < s; ++dy)
+      for (int64_t dx = 0; dx < s; ++dx)
+        buf_st1s(outR, sv, static_cast<uint32_t>(((base + dy * OWs + dx) * a.outPix + f) * 4), 0);
+  } else {
+    buf_st1s(outR, v, static_cast<uint32_t>((m * a.outPix + f) * 4), 0);
+  }
+  if (a.yolo) a.yolo[(b * a.F + f) * OHW + p] = yolo_entry(v, static_cast<int>(f % a.yoloEntries));
+}
+
 // Channels-last epilogue (rows m = output pixels, columns = filters): the
 // result of pixel m, filter f goes to out[m * outPix + f] (residual likewise
 // with resPix).  Each lane owns FN filter columns (bias per lane); the pixel
@@ -266,6 +299,25 @@ __device__ inline void conv_store_nhwc(const ConvArgs& a, const f32x16 (&acc)[FM
     vRes[j] = sel_off(okF, static_cast<uint32_t>(rowBase) * rp4 + static_cast<uint32_t>(f) * 4u);
   }
   auto rc = [](int i, int r) { return i * 32 + 8 * (r >> 2) + (r & 3); };
+  if (a.upS > 0 || a.yolo) {  // epilogue variants: generic per-element stores
+    const __amdgpu_buffer_rsrc_t resG = make_rsrc(a.res, a.resBytes);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t f = n0w + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = rowBase + rc(i, r);
+          if (f >= a.F || m >= M) continue;
+          float v = acc[i][j][r] + bias[j];
+          v = apply_act(v, a.act);
+          if (a.res) v = v + buf_ld1s(resG, static_cast<uint32_t>((m * a.resPix + f) * 4), 0);
+          store_nhwc_variant(a, outR, m, f, v);
+        }
+      }
+    return;
+  }
   auto finish = [&](auto actTag, auto resTag) {
     constexpr int ACT = decltype(actTag)::value;
     constexpr bool RES = decltype(resTag)::value;

@@ -263,7 +263,11 @@ __global__ __launch_bounds__(Cfg::NT) void conv_wsplit_nhwc_kernel(ConvArgs a) {
       else if (a.act == TNH_AC_LOGISTIC)
         v = 1.f / (1.f + expf(-v));
       if (a.res) v = v + rv[e];  // the fused shortcut (naddlayer.pas:698)
-      st1(outR, v, vo[e]);
+      if (a.upS > 0 || a.yolo) {   // epilogue variants (upsampled / yolo head)
+        if (okF && mBase + e < M) store_nhwc_variant(a, outR, mBase + e, f, v);
+      } else {
+        st1(outR, v, vo[e]);
+      }
     }
   }
 }

@@ -5,6 +5,7 @@
 // flat passes use 16-byte accesses when the buffers allow.
 #include "common.hpp"
 #include "rows.hpp"
+#include "yolo_math.hpp"
 
 namespace tnh {
 namespace {
@@ -247,29 +248,11 @@ __global__ void route_kernel(RouteArgs r, float* dst, int64_t perImage) {
   }
 }
 
-// logistic_array's exp approximation (nactivation.pas:36-127), IEEE reciprocal
-__device__ inline float logistic_poly(float x) {
-  const float l2e = 1.442695041f, c0 = 1.00172476f, c1 = 0.657636276f, c2 = 0.3371894346f;
-  const float mx = 8.872283E+001f, mn = -8.733654E+001f;
-  float t = 0.f - x;
-  if (t >= mx) t = mx;
-  if (t <= mn) t = mn;
-  t = l2e * t;
-  const float fi = floorf(t);
-  const float f = t - fi;
-  const int i = static_cast<int>(fi);
-  float p = __builtin_fmaf(f, c2, c1);
-  p = __builtin_fmaf(p, f, c0);
-  const float e = __int_as_float(__float_as_int(p) + static_cast<int>(static_cast<unsigned>(i) << 23));
-  const float d = e + 1.f;
-  return 1.f / d;
-}
-
 __global__ void yolo_kernel(int64_t total, int64_t HW, int64_t entries, const float* in, float* out) {
   GRID_STRIDE(e, total) {
     const int64_t entry = (e / HW) % entries;  // channel within the anchor group
     const float v = in[e];
-    out[e] = (entry == 2 || entry == 3) ? v : logistic_poly(v);
+    out[e] = yolo_entry(v, static_cast<int>(entry));
   }
 }
 
@@ -303,7 +286,7 @@ __global__ __launch_bounds__(256) void yolo_nhwc_kernel(int HW, int CH, int entr
     if (c < CH && p < HW) {
       const float x = tile[tx][ty + 8 * k];
       const int entry = c % entries;
-      dst[static_cast<int64_t>(c) * HW + p] = (entry == 2 || entry == 3) ? x : logistic_poly(x);
+      dst[static_cast<int64_t>(c) * HW + p] = yolo_entry(x, entry);
     }
   }
 }

@@ -172,7 +172,7 @@ class Network:
     """Inference runner over the C ABI; buffers are device torch tensors."""
 
     def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True,
-                 layout="nchw"):
+                 layout="nchw", fuse_heads=True):
         import torch
 
         if layout not in ("nchw", "nhwc"):
@@ -214,7 +214,23 @@ class Network:
             self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), wl)
         self.out = [None] * len(layers)
         self.input_shape = (batch,) + layers[0]["in"]
+        self.up_fused, self.yolo_fused = set(), set()
         if layout == "nhwc":
+            if fuse and fuse_heads:
+                # a convolution read only by an upsample stores its result
+                # straight as the upsampled image; one read only by a yolo
+                # layer also writes the yolo head (one launch each instead of
+                # two)
+                for L in layers:
+                    i = L["index"]
+                    if (L["type"] != "convolutional" or i in self.fused or i == 0 or i + 1 >= len(layers)
+                            or use[i] != [i + 1]):
+                        continue
+                    nxt = layers[i + 1]["type"]
+                    if nxt == "upsample":
+                        self.up_fused.add(i)
+                    elif nxt == "yolo":
+                        self.yolo_fused.add(i)
             self._plan_nhwc(device)
             self._plan_branches(use)
             return
@@ -294,8 +310,8 @@ class Network:
                 C, h, w = L["out"]
                 self.out[i] = torch.empty((B, C, h, w), dtype=torch.float32, device=device)
                 continue
-            if (t == "route" and len(L["srcs"]) == 1) or i in self.fused or i in self.store:
-                continue
+            if (t == "route" and len(L["srcs"]) == 1) or i in self.fused or i in self.store or i in self.up_fused:
+                continue  # (an upsample-fused convolution stores only the upsample's output)
             C, h, w = L["out"]
             self.store[i] = (torch.empty((B, h, w, C), dtype=torch.float32, device=device), 0, C)
         for L in layers:  # nothing may read a yolo head as an activation
@@ -337,6 +353,8 @@ class Network:
         permuted view of the channel slice in NHWC mode)."""
         if self.layout == "nchw" or self.layers[i]["type"] == "yolo":
             return self.buffer(i)
+        if i in self.up_fused:
+            raise ValueError(f"layer {i} stores only its upsampled output (layer {i + 1})")
         t, off, pix = self.nhwc_store(i)
         C = self.layers[i]["out"][0]
         return t.view(self.batch, t.shape[1], t.shape[2], pix)[..., off:off + C].permute(0, 3, 1, 2)
@@ -432,7 +450,20 @@ class Network:
             res, roff, rpix = None, 0, None
             if i in self.fused:
                 res, roff, rpix = self.nhwc_store(self.layers[i + 1]["src"])
+            if i in self.up_fused:
+                up = self.layers[i + 1]
+                dst, doff, dpix = self.nhwc_store(i + 1)
+                hip.conv2dForwardNHWCUpsample(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], src, soff,
+                                              w, b, L["act"], up["stride"], up["scale"], dst, doff, inPix=spix,
+                                              outPix=dpix)
+                return x
             dst, doff, dpix = self.nhwc_store(i)
+            if i in self.yolo_fused:
+                Y = self.layers[i + 1]
+                hip.conv2dForwardNHWCYolo(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], src, soff, w,
+                                          b, L["act"], dst, doff, Y["n"], Y["classes"], self.out[i + 1], inPix=spix,
+                                          outPix=dpix)
+                return x
             hip.conv2dForwardNHWC(B, C, h, ww, L["filters"], L["size"], L["stride"], L["pad"], src, soff, w, b,
                                   L["act"], dst, doff, inPix=spix, outPix=dpix, residual=res, resOffset=roff,
                                   resPix=rpix, nchwInput=nchw)
@@ -453,14 +484,16 @@ class Network:
                     src, soff, spix = self.nhwc_store(s_)
                     hip.copyChannels(B * h * ww, self.layers[s_]["out"][0], src, soff, spix, dst, doff + off, dpix)
         elif t == "upsample":
-            C, h, ww = L["in"]
-            src, soff, spix = self.nhwc_store(i - 1)
-            dst, doff, dpix = self.nhwc_store(i)
-            hip.upSampleNHWC(B, C, h, ww, L["stride"], L["scale"], src, soff, spix, dst, doff, dpix)
+            if i - 1 not in self.up_fused:
+                C, h, ww = L["in"]
+                src, soff, spix = self.nhwc_store(i - 1)
+                dst, doff, dpix = self.nhwc_store(i)
+                hip.upSampleNHWC(B, C, h, ww, L["stride"], L["scale"], src, soff, spix, dst, doff, dpix)
         elif t == "yolo":
-            C, h, ww = L["in"]
-            src, soff, spix = self.nhwc_store(i - 1)
-            hip.yoloForwardNHWC(B, L["n"], L["classes"], h, ww, src, soff, spix, self.out[i])
+            if i - 1 not in self.yolo_fused:
+                C, h, ww = L["in"]
+                src, soff, spix = self.nhwc_store(i - 1)
+                hip.yoloForwardNHWC(B, L["n"], L["classes"], h, ww, src, soff, spix, self.out[i])
             heads.append(self.out[i])
         return x
 

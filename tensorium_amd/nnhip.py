@@ -88,6 +88,10 @@ _PROTOS = {
                             i32, vp, i64, i64, vp, i64, i64],
     "tnh_conv2d_fwd_nhwc_noalloc": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64,
                                     vp, i64, i32, vp, i64, i64, vp, i64, i64],
+    "tnh_conv2d_fwd_nhwc_upsample": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64,
+                                     vp, i64, i32, i64, f32, vp, i64, i64],
+    "tnh_conv2d_fwd_nhwc_yolo": [i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, vp,
+                                 i64, i32, vp, i64, i64, i64, i64, vp, i64],
     "tnh_conv2d_noalloc_scratch_bytes": [C.POINTER(i64)],
     "tnh_sgemm_set_autotune": [i32, i32],
     "tnh_yolo_fwd_nhwc": [i64, i64, i64, i64, i64, vp, i64, i64, vp],
@@ -364,6 +368,29 @@ class TNNHip:
              kernelSize, kernelSize, padding, padding, stride, stride, addr(input), inOffset, xp, addr(weights), 0,
              addr(biases), 0, activation, addr(residual), resOffset, rp, addr(output), outOffset, op_)
         return oh, ow
+
+    def conv2dForwardNHWCUpsample(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset,
+                                  weights, biases, activation, upStride, upScale, output, outOffset, inPix=None,
+                                  outPix=None):
+        """Channels-last fused conv whose result is stored only as its nearest
+        upsample (factor upStride, times upScale) into output, the next
+        TUpSampleLayer's tensor (tnh_conv2d_fwd_nhwc_upsample)."""
+        xp = c if inPix is None else inPix
+        op_ = filters if outPix is None else outPix
+        call("tnh_conv2d_fwd_nhwc_upsample", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride,
+             stride, addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, upStride, upScale,
+             addr(output), outOffset, op_)
+
+    def conv2dForwardNHWCYolo(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
+                              biases, activation, output, outOffset, n, classes, yoloOutput, inPix=None,
+                              outPix=None):
+        """Channels-last fused conv that also writes the yolo head (NCHW) of its
+        result (tnh_conv2d_fwd_nhwc_yolo)."""
+        xp = c if inPix is None else inPix
+        op_ = filters if outPix is None else outPix
+        call("tnh_conv2d_fwd_nhwc_yolo", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride,
+             stride, addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, addr(output), outOffset,
+             op_, n, classes, addr(yoloOutput), 0)
 
     @staticmethod
     def noAllocScratchBytes():

@@ -233,6 +233,86 @@ def test_conv_nhwc_wsplit_vs_oracle(hip, cfg, act):
     assert R.rel_err(H(dout, hip).transpose(0, 3, 1, 2), ref) <= TOL
 
 
+# forced tilings that reach every channels-last epilogue: a lean tile, a lean
+# tile with a tail split (the reduction kernel's epilogue), a wave-split tile
+EPI_TILINGS = [11, 12 + CONV_SPLIT_UNIT * (CONV_TAIL_BASE + 3), 20, 22]
+
+
+@pytest.mark.parametrize("forced", EPI_TILINGS)
+@pytest.mark.parametrize("k", [1, 3])
+def test_conv_nhwc_upsample_variant(hip, forced, k):
+    """tnh_conv2d_fwd_nhwc_upsample equals conv2dForwardNHWC followed by
+    upSampleNHWC bit for bit, into a channel slice of a wider (route)
+    buffer whose other channels stay untouched; and the conv itself is
+    within 1e-5 of the oracle."""
+    B, Cc, Hh, F, s, scale = 2, 64, 13, 96, 2, 1.0
+    case(f"conv nhwc upsample variant k{k} forced {forced}")
+    p = k // 2
+    x = synth.uniform(61, (B, Cc, Hh, Hh))
+    Wt = synth.normal(62, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(63, (F,), 0.1)
+    ref = R.upsample_fwd(R.conv_forward(x, Wt, b, k, 1, p, acLEAKY), s, scale)
+    dx, dw, db = D(nhwc(x)), D(tap_major(Wt, F, Cc, k)), D(b)
+    pix = F + 40
+    fused = D(np.full((B, Hh * s, Hh * s, pix), 7.0, np.float32))
+    plain = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+    twostep = D(np.full((B, Hh * s, Hh * s, pix), 7.0, np.float32))
+    hip.setConvAutotune(True, forced)
+    try:
+        hip.conv2dForwardNHWCUpsample(B, Cc, Hh, Hh, F, k, 1, p, dx, 0, dw, db, acLEAKY, s, scale, fused, 24,
+                                      outPix=pix)
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, 1, p, dx, 0, dw, db, acLEAKY, plain, 0)
+    finally:
+        hip.setConvAutotune(True, -1)
+    hip.upSampleNHWC(B, F, Hh, Hh, s, scale, plain, 0, F, twostep, 24, pix)
+    got, want = H(fused, hip), H(twostep, hip)
+    assert np.array_equal(got, want)
+    assert np.all(got[..., :24] == 7.0) and np.all(got[..., 24 + F:] == 7.0)
+    assert R.rel_err(got[..., 24:24 + F].transpose(0, 3, 1, 2), ref) <= TOL
+
+
+@pytest.mark.parametrize("forced", EPI_TILINGS)
+def test_conv_nhwc_yolo_variant(hip, forced):
+    """tnh_conv2d_fwd_nhwc_yolo writes the same channels-last output as
+    conv2dForwardNHWC and the same NCHW head as yoloForwardNHWC on it, bit
+    for bit (3 anchors x (5 + 80 classes) = 255 filters)."""
+    B, Cc, Hh, n, classes = 2, 128, 13, 3, 80
+    F = n * (5 + classes)
+    case(f"conv nhwc yolo variant forced {forced}")
+    x = synth.uniform(64, (B, Cc, Hh, Hh))
+    Wt = synth.normal(65, (F, Cc), (2.0 / Cc) ** 0.5)
+    b = synth.normal(66, (F,), 0.1)
+    dx, dw, db = D(nhwc(x)), D(Wt), D(b)
+    out_f = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
+    head_f = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
+    out_p = torch.empty_like(out_f)
+    head_p = torch.empty_like(head_f)
+    hip.setConvAutotune(True, forced)
+    try:
+        hip.conv2dForwardNHWCYolo(B, Cc, Hh, Hh, F, 1, 1, 0, dx, 0, dw, db, acLINEAR, out_f, 0, n, classes, head_f)
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 1, 1, 0, dx, 0, dw, db, acLINEAR, out_p, 0)
+    finally:
+        hip.setConvAutotune(True, -1)
+    hip.yoloForwardNHWC(B, n, classes, Hh, Hh, out_p, 0, F, head_p)
+    assert np.array_equal(H(out_f, hip), H(out_p, hip))
+    assert np.array_equal(H(head_f, hip), H(head_p, hip))
+    ref = R.conv_forward(x, Wt, b, 1, 1, 0, acLINEAR)
+    assert R.rel_err(H(out_f, hip).transpose(0, 3, 1, 2), ref) <= TOL
+
+
+def test_conv_nhwc_variants_reject(hip):
+    """The epilogue variants refuse a filter count that is not anchors x (5 +
+    classes) and an upsample stride below 1."""
+    x = torch.zeros(1, 4, 4, 32, device="cuda")
+    w = torch.zeros(40, 32, device="cuda")
+    out = torch.zeros(1, 4, 4, 40, device="cuda")
+    head = torch.zeros(1, 40, 4, 4, device="cuda")
+    with pytest.raises(TNHError):
+        hip.conv2dForwardNHWCYolo(1, 32, 4, 4, 40, 1, 1, 0, x, 0, w, None, acLINEAR, out, 0, 3, 80, head)
+    with pytest.raises(TNHError):
+        hip.conv2dForwardNHWCUpsample(1, 32, 4, 4, 40, 1, 1, 0, x, 0, w, None, acLINEAR, 0, 1.0, out, 0)
+
+
 def test_conv_nhwc_rejects_unsupported(hip):
     x = torch.zeros(1, 8, 8, 48, device="cuda")
     w = torch.zeros(32, 9 * 48, device="cuda")

@@ -167,9 +167,12 @@ def test_yolov3_nhwc_heads(hip, yolo):
     heads = [h.cpu().numpy() for h in n.forward(dx)]
     hip.finish()
     errs = {}
+    assert n.up_fused == {84, 96} and n.yolo_fused == {81, 93, 105}
     for L in layers:
         i = L["index"]
-        if L["type"] == "convolutional" and i not in n.fused:
+        if L["type"] == "convolutional" and i not in n.fused and i not in n.up_fused:
+            errs[i] = R.rel_err(n.output(i).cpu().numpy(), ref[i])
+        if L["type"] == "upsample":  # written by the convolution before it
             errs[i] = R.rel_err(n.output(i).cpu().numpy(), ref[i])
     worst = max(errs, key=errs.get)
     print(f"worst intermediate conv error {errs[worst]:.3e} at layer {worst}", flush=True)
@@ -190,6 +193,35 @@ def test_yolov3_nhwc_heads(hip, yolo):
     finally:
         n.release_graph()
         hip.useTorchStream()
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_yolov3_nhwc_fusion_is_exact(hip, yolo, B):
+    """Channels-last head fusions (the upsample written by the conv before
+    it, the yolo head written by the head conv) against the network that
+    launches them separately, bit for bit, when both run the same tilings
+    (autotuning off: the cost model picks each tiling from the GEMM shape
+    alone)."""
+    layers, W = yolo
+    print(f"[case] yolov3 batch {B} nhwc fused vs unfused", flush=True)
+    x = synth.uniform(19, (B, 3, 416, 416))
+    dx = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    hip.setConvAutotune(False, -1)
+    try:
+        a = darknet.Network(hip, layers, B, W, layout="nhwc")
+        ha = [h.cpu().numpy() for h in a.forward(dx)]
+        hip.finish()
+        b = darknet.Network(hip, layers, B, W, layout="nhwc", fuse_heads=False)
+        hb = [h.cpu().numpy() for h in b.forward(dx)]
+        hip.finish()
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert a.up_fused and a.yolo_fused and not b.up_fused and not b.yolo_fused
+    for u, v in zip(ha, hb):
+        assert np.array_equal(u, v)
+    for i in (85, 97, 81, 93, 105):
+        assert np.array_equal(a.output(i).cpu().numpy(), b.output(i).cpu().numpy()), i
 
 
 @pytest.mark.parametrize("B", [1, 4])
