@@ -28,6 +28,7 @@
 
 #include "common.hpp"
 #include "conv_args.hpp"
+#include "conv_first.hpp"
 #include "conv_lean.hpp"
 #include "conv_wsplit.hpp"
 #include "gemm_core.hpp"
@@ -1213,7 +1214,15 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
     a.yolo = epi.yolo;
     a.yoloEntries = static_cast<int>(epi.yoloClasses + 5);
   }
-  if (xNchw) return launch_smallc<true, true>(a, cx->stream);
+  // The network's first layer: on the matrix cores from about 32 blocks of
+  // 32 pixels per CU (YOLOv3-416 from batch 2: measured 23.7 against 25.0 us
+  // at batch 2, 111 against 135 us at batch 16), else the bit-exact
+  // per-pixel kernel, which wins at batch 1 (13.0 against 17.1 us: one
+  // block per wave leaves the MFMA kernel's loads exposed) and serves a
+  // residual, F > 64 and F % 4 != 0.
+  if (xNchw)
+    return first_mfma_ok(a) && a.g.N >= int64_t(32) * 32 * cx->cu_count ? launch_first_mfma(a, cx->stream)
+                                                                        : launch_smallc<true, true>(a, cx->stream);
 
   const int mode = kh == 3 ? kTap3 : k1x1;
   const bool va = aligned16(a.w) && K % 4 == 0 && aligned16(a.g.x) && xPix % 4 == 0;

@@ -1,9 +1,10 @@
 """Channels-last (NHWC) convolution through the C ABI against the CPU oracle
 (NCHW) on identical seeded inputs: the oracle's tensors are transposed to
 channels-last on the host.  Per-tensor max|g - r| / max|r| <= 1e-5 (fp32
-summation order), exact for the few-channel first layer, and exact
-equality on integer-valued data; pixel strides that make a tensor a channel
-slice of a wider buffer leave the rest of the buffer untouched."""
+summation order; the first layer on the matrix cores too), exact for the
+per-pixel first-layer kernel, and exact equality on integer-valued data;
+pixel strides that make a tensor a channel slice of a wider buffer leave the
+rest of the buffer untouched."""
 import numpy as np
 import pytest
 import torch
@@ -76,8 +77,38 @@ def test_conv_nhwc_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act, resid):
     assert R.rel_err(got, ref) <= TOL
 
 
+# The matrix-core kernel serves layers of at least 32 x 32 x (CU count)
+# output pixels (262 144 on 256 CUs); smaller ones run the per-pixel kernel.
+@pytest.mark.parametrize("B,Cc,Hh,F,s,act,bias,pad", [
+    (2, 3, 416, 32, 1, acLEAKY, True, 0),    # YOLOv3 layer 0 at batch 2
+    (2, 3, 517, 44, 1, acLEAKY, True, 4),    # two filter blocks, the second ragged (12), a 16-byte aligned slice
+    (3, 1, 604, 4, 1, acLINEAR, False, 0),   # one store quad, no bias, a ragged last block of pixels
+    (8, 4, 186, 64, 1, acLEAKY, True, 8),    # two whole blocks, C = 4, rows of 186 pixels (blocks cross rows)
+    (6, 2, 420, 16, 2, acLINEAR, True, 0),   # half a block, stride 2
+])
+def test_conv_nhwc_first_layer_mfma(hip, B, Cc, Hh, F, s, act, bias, pad):
+    """C <= 4 image read as NCHW, output channels-last, F % 4 == 0, no
+    residual, 16-byte aligned output, at least 262 144 output pixels: the
+    first layer on the matrix cores (32 filters x 32 pixels per MFMA chain),
+    within 1e-5 of the oracle per tensor; a channel slice of a wider output
+    leaves the other channels untouched."""
+    case(f"conv nhwc first layer mfma B{B} C{Cc} H{Hh} F{F} s{s} act{act} bias{bias} pad{pad}")
+    x = synth.uniform(75, (B, Cc, Hh, Hh))
+    Wt = synth.normal(76, (F, Cc * 9), (2.0 / (9 * Cc)) ** 0.5)
+    b = synth.normal(77, (F,), 0.1) if bias else np.zeros(F, np.float32)
+    ref = R.conv_forward(x, Wt, b, 3, s, 1, act)
+    OH = ref.shape[2]
+    outPix = F + 2 * pad
+    dout = D(np.full((B, OH, OH, outPix), 7.0, np.float32))
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 3, s, 1, D(x), 0, D(tap_major(Wt, F, Cc, 3)), D(b) if bias else None,
+                          act, dout, pad, outPix=outPix, nchwInput=True)
+    got = H(dout, hip)
+    assert R.rel_err(got[..., pad:pad + F].transpose(0, 3, 1, 2), ref) <= TOL
+    assert np.all(got[..., :pad] == 7.0) and np.all(got[..., pad + F:] == 7.0)
+
+
 @pytest.mark.parametrize("B,Cc,Hh,F,s,act,resid,bias,pad", [
-    (2, 3, 416, 32, 1, acLEAKY, False, True, 0),   # YOLOv3 layer 0
+    (2, 3, 416, 32, 1, acLEAKY, True, True, 0),    # YOLOv3 layer 0 with a residual
     (2, 3, 37, 45, 1, acLEAKY, True, True, 4),     # ragged last chunk (13 filters), residual, channel slice
     (2, 3, 21, 45, 1, acLEAKY, False, True, 3),    # unaligned channel slice: scalar stores
     (1, 1, 9, 5, 2, acLINEAR, False, False, 0),    # no bias, fewer filters than one store quad
@@ -85,9 +116,11 @@ def test_conv_nhwc_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act, resid):
     (2, 2, 15, 64, 2, acLINEAR, True, True, 0),    # two whole chunks, stride 2
 ])
 def test_conv_nhwc_first_layer_bit_exact(hip, B, Cc, Hh, F, s, act, resid, bias, pad):
-    """C <= 4 image read as NCHW, output channels-last: the few-channel
-    kernel's sequential FMA chain, bit-exact against the oracle; a channel
-    slice of a wider output leaves the other channels untouched."""
+    """C <= 4 image read as NCHW, output channels-last, in the cases the
+    matrix-core kernel leaves to the per-pixel kernel (a residual, F % 4 != 0,
+    an output slice that is not 16-byte aligned): the reference's sequential
+    FMA chain, bit-exact against the oracle; a channel slice of a wider
+    output leaves the other channels untouched."""
     case(f"conv nhwc few-channel B{B} C{Cc} H{Hh} F{F} s{s} act{act} res{resid} bias{bias} pad{pad}")
     x = synth.uniform(75, (B, Cc, Hh, Hh))
     Wt = synth.normal(76, (F, Cc * 9), (2.0 / (9 * Cc)) ** 0.5)
