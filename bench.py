@@ -42,7 +42,7 @@ PEAK_HBM = 8.0e12
 # WRITE_SIZE, KiB per dispatch, scaled by a 64 MiB copy: read = 2.0 x
 # FETCH_SIZE, write = 1.0 x WRITE_SIZE); profiles/yolov3_416_b16_conv_nhwc_kernel.md
 # holds the figures and the commands.  Other layouts / batches: null.
-TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 66180.6 + 39756.1) * 1024}
+TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 65566.6 + 39756.1) * 1024}
 
 
 def log(*a):
@@ -50,15 +50,17 @@ def log(*a):
 
 
 def kernel_kind(L, batch, layout):
-    """Kernel family a conv layer launches: the lean implicit GEMM over
-    tap-major 3x3 or 1x1 operands (conv_nhwc_kernel for channels-last
-    activations, conv_lean_kernel for NCHW; conv_lean.hpp), or the per-pixel
-    kernel for few input channels (conv_smallc_kernel)."""
+    """Kernel family of a conv layer, by layer shape: the implicit GEMM over
+    tap-major 3x3 or 1x1 operands (named after the lean kernel,
+    conv_nhwc_kernel for channels-last activations, conv_lean_kernel for
+    NCHW, conv_lean.hpp; the tuner may run a layer of the family with the
+    wave-split tiles, conv_wsplit.hip), or the first layer over few input
+    channels (conv_first.hip / conv_smallc_kernel)."""
     lean = "conv_nhwc_kernel" if layout == "nhwc" else "conv_lean_kernel"
     if L["size"] == 1 and L["stride"] == 1 and L["pad"] == 0:
         return f"{lean}<1x1>"
     if L["size"] == 3 and L["in"][0] <= 4:
-        return "conv_smallc_kernel<3x3>"
+        return "first_layer<3x3>"  # conv_first_mfma_kernel (channels-last from 262K pixels) or conv_smallc_kernel
     if L["size"] == 3 and L["in"][0] % 16 == 0:
         return f"{lean}<tap3x3>"
     return f"conv_kernel<gather{L['size']}x{L['size']}>"

@@ -969,8 +969,12 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     if (!cfg_valid(c, mode, C, va, smallIO, nhwc)) continue;
     if (kCfgs[c].kind == kWsplit) {
       // whole tiles only; timed, never the cost model's pick, so absent from
-      // the deterministic mode's choice
-      if (!det) cands.push_back({c, 1, 0, 0});
+      // the deterministic mode's choice; only for layers whose 64x64 tiles
+      // leave the GPU under-filled (below two per CU), where they replace a
+      // K split and its reduction launch: on larger layers their 32-wide
+      // tiles read twice the L2 bytes per FLOP of the lean tiles
+      const int64_t tiles64 = ((N + 63) / 64) * ((F + 63) / 64);
+      if (!det && tiles64 < 2 * static_cast<int64_t>(cus)) cands.push_back({c, 1, 0, 0});
       continue;
     }
     cands.push_back({c, 1, 0, 0});
