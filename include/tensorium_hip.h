@@ -203,8 +203,9 @@ int32_t tnh_conv2d_out_dims(int64_t H, int64_t W, int64_t kh, int64_t kw,
  * channel slice of a wider buffer, e.g. a route/concat destination); out
  * and residual likewise with outPix / rPix and the output geometry.
  * Weights are tap-major [F][kh][kw][C] (tnh_conv2d_pack_weights).  Supports
- * 3x3 (any stride/padding) and 1x1 stride 1; C % 32 == 0, x and weights
- * 16-byte aligned with xPix % 4 == 0, out and residual within 2 GiB each.
+ * 3x3 (any stride/padding) and 1x1 stride 1; C % 4 == 0 (C % 32 == 0 runs
+ * the tuned tiles, other C one fixed tile), x and weights 16-byte aligned
+ * with xPix % 4 == 0, x, out and residual within 2 GiB each.
  * xPix == 0 with C <= 4 and a 3x3 kernel reads x as NCHW [batch][C][H][W]
  * (the network's first layer).  The results equal tnh_conv2d_fwd's on the
  * same data up to the fp32 summation order (the few-channel path: exactly). */
@@ -347,6 +348,18 @@ int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH,
                         int64_t h, int64_t w, int64_t strideX, int64_t strideY,
                         int64_t padding, int64_t kernelSize, int64_t *indexes,
                         float *output);
+/* No reference counterpart: the values of tnh_maxpool_fwd on channels-last
+ * tensors, bit for bit (same window scan, strict '>', -MaxSingle start; no
+ * indices: the channels-last layout serves inference).  Pixel (b, y, x) of
+ * in at in + inOff + ((b*h + y)*w + x)*inPix, of out at out + outOff +
+ * ((b*outH + i)*outW + j)*outPix (channel slices of wider buffers allowed).
+ * outH/outW as tnh_maxpool_fwd checks them; size, strides, padding <= 64. */
+int32_t tnh_maxpool_fwd_nhwc(int64_t batch, int64_t channels, int64_t h,
+                             int64_t w, int64_t outH, int64_t outW,
+                             int64_t strideX, int64_t strideY, int64_t padding,
+                             int64_t kernelSize, const float *in,
+                             int64_t inOff, int64_t inPix, float *out,
+                             int64_t outOff, int64_t outPix);
 /* TNNCuda.backwardMaxPool (nncuda.pas:1121) with the CPU order of
  * backwardMaxPool (nMaxPoolLayer.pas:501-512): delta_in[idx[i]] += delta[i]
  * summed per input element in ascending i (gather, no atomics).  Needs the

@@ -139,6 +139,8 @@ function tnh_upsample(batch, channels, h, w: Int64; input: PSingle; stride: Int6
   scale: Single; output: PSingle; zeroIn: LongInt): LongInt; cdecl; external libtnh;
 function tnh_upsample_nhwc(batch, channels, h, w, stride: Int64; scale: Single; input: PSingle;
   inOff, inPix: Int64; output: PSingle; outOff, outPix: Int64): LongInt; cdecl; external libtnh;
+function tnh_maxpool_fwd_nhwc(batch, channels, h, w, outH, outW, strideX, strideY, padding, kernelSize: Int64;
+  input: PSingle; inOff, inPix: Int64; output: PSingle; outOff, outPix: Int64): LongInt; cdecl; external libtnh;
 function tnh_yolo_fwd(batch, n, classes, h, w: Int64; input, output: PSingle): LongInt; cdecl; external libtnh;
 function tnh_yolo_fwd_nhwc(batch, n, classes, h, w: Int64; input: PSingle; inOff, inPix: Int64;
   output: PSingle): LongInt; cdecl; external libtnh;
@@ -308,6 +310,9 @@ type
       const dst: TCUMem; const dstOffset, dstPix: SizeInt);
     procedure upSampleNHWC(const batch, channels, h, w, stride: SizeInt; const scale: T; const input: TCUMem;
       const inOffset, inPix: SizeInt; const output: TCUMem; const outOffset, outPix: SizeInt);
+    procedure forwardMaxPoolNHWC(const batch, channels, h, w, outH, outW, strideX, strideY, padding,
+      kernelSize: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const output: TCUMem;
+      const outOffset, outPix: SizeInt);
     procedure yoloForward(const batch, n, classes, h, w: SizeInt; const input, output: TCUMem);
     procedure yoloForwardNHWC(const batch, n, classes, h, w: SizeInt; const input: TCUMem;
       const inOffset, inPix: SizeInt; const output: TCUMem);
@@ -738,6 +743,14 @@ procedure TNNHip<T>.upSampleNHWC(const batch, channels, h, w, stride: SizeInt; c
 begin
   check(tnh_upsample_nhwc(batch, channels, h, w, stride, S(scale), PSingle(input), inOffset, inPix, PSingle(output),
     outOffset, outPix));
+end;
+
+procedure TNNHip<T>.forwardMaxPoolNHWC(const batch, channels, h, w, outH, outW, strideX, strideY, padding,
+  kernelSize: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const output: TCUMem;
+  const outOffset, outPix: SizeInt);
+begin
+  check(tnh_maxpool_fwd_nhwc(batch, channels, h, w, outH, outW, strideX, strideY, padding, kernelSize,
+    PSingle(input), inOffset, inPix, PSingle(output), outOffset, outPix));
 end;
 
 procedure TNNHip<T>.yoloForward(const batch, n, classes, h, w: SizeInt; const input, output: TCUMem);

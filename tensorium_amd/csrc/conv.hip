@@ -812,6 +812,31 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
   return TNH_OK;
 }
 
+// Channels-last convolution over C % 4 == 0 channels that are not a
+// multiple of 32 (kTap3Any / k1x1Any): one fixed tile, 64 x 32 for up to 32
+// filters, else 64 x 64; no tuning and no K split (these are the thin early
+// layers of small networks, e.g. 16 channels in YOLOv3-tiny).
+template <class Cfg>
+int launch_nhwc_any_cfg(ConvArgs a, int mode, hipStream_t s) {
+  const int64_t tm = (a.g.N + Cfg::BM - 1) / Cfg::BM, tn = (a.F + Cfg::BN - 1) / Cfg::BN;
+  if (tm * tn > INT32_MAX) return fail(TNH_ERR_UNSUPPORTED, "conv2d: grid too large");
+  a.tilesM = static_cast<int>(tm);
+  a.tilesN = static_cast<int>(tn);
+  a.splits = 1;
+  a.kChunk = a.g.K;
+  a.tailSplits = 0;
+  const dim3 grid(static_cast<unsigned>(tm * tn));
+  if (mode == kTap3Any)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3Any>), grid, dim3(Cfg::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1Any>), grid, dim3(Cfg::NT), 0, s, a);
+  return launch_status("conv_nhwc_kernel");
+}
+
+int launch_nhwc_any(const ConvArgs& a, int mode, hipStream_t s) {
+  return a.F <= 32 ? launch_nhwc_any_cfg<Lean16>(a, mode, s) : launch_nhwc_any_cfg<Lean11>(a, mode, s);
+}
+
 int launch_nhwc_cfg(int cfg, const ConvArgs& a, int mode, int cus, hipStream_t s) {
   switch (cfg) {
     case 11: return launch_nhwc<Lean11>(a, mode, cus, s);
@@ -1231,8 +1256,9 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
   const int mode = kh == 3 ? kTap3 : k1x1;
   const bool va = aligned16(a.w) && K % 4 == 0 && aligned16(a.g.x) && xPix % 4 == 0;
   const bool smallIO = a.outBytes <= kMaxBufBytes && a.resBytes <= kMaxBufBytes;
-  TNH_ARG(va && smallIO && C % 32 == 0,
-          "conv2d_nhwc: needs C %% 32 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
+  TNH_ARG(va && smallIO && C % 4 == 0,
+          "conv2d_nhwc: needs C %% 4 == 0, 16-byte aligned x and weights with xPix %% 4 == 0, out within 2 GiB");
+  if (C % 32 != 0) return launch_nhwc_any(a, kh == 3 ? kTap3Any : k1x1Any, cx->stream);
   const TuneKey key{F, N, K, C, H, W, (int)kh, (int)sY, mode, va, false, 1, (int)xPix, (int)outPix,
                     residual ? (int)rPix : 0, residual != nullptr, smallIO, epi.upS > 0 ? 1 : (epi.yolo ? 2 : 0)};
   return conv_dispatch(cx, a, mode, va, false, smallIO, true, key, fixed);

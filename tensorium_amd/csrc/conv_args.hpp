@@ -58,7 +58,16 @@ struct ConvArgs {
 // K walk / B operand of a convolution kernel
 // kGatherDyn: any kernel size (kh x kw given at run time), either weight
 // layout (tap-major when ConvArgs::tapW)
-enum Mode { kGatherRef3 = 0, kGatherTap3 = 1, kGatherRef1 = 2, kTap3 = 3, k1x1 = 4, kGatherDyn = 5 };
+enum Mode {
+  kGatherRef3 = 0,
+  kGatherTap3 = 1,
+  kGatherRef1 = 2,
+  kTap3 = 3,
+  k1x1 = 4,
+  kGatherDyn = 5,
+  kTap3Any = 6,  // channels-last 3x3 with C % 4 == 0 but C % 32 != 0 (a panel may span taps, K tail)
+  k1x1Any = 7,   // channels-last 1x1 with C % 4 == 0 but C % 32 != 0 (K tail)
+};
 
 __device__ inline float apply_act(float v, int act) {
   if (act == TNH_AC_LEAKY) return v < 0.f ? 0.1f * v : v;  // leaky_array (nactivation.pas:234)

@@ -136,7 +136,10 @@ __global__ __launch_bounds__(256) void conv_first_mfma_kernel(ConvArgs a) {
         t[n * 8 + ((2 * q + h) ^ ((n >> 1) & 7))] = v;
       }
       __builtin_amdgcn_wave_barrier();
-      // lanes 8i .. 8i+7 store pixel row 8*it + i, chunk lane & 7
+      // lanes 8i .. 8i+7 store pixel row 8*it + i, chunk lane & 7; the stores
+      // are non-temporal (the output, 354 MB at batch 16, is far larger than
+      // the caches: 12-15 us less per batch-16 layer in the network than
+      // plain stores)
       const int fq = 32 * j + 4 * rq;
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) void conv_first_mfma_kernel(ConvArgs a) {
         const f32x4 v = t[row * 8 + (rq ^ ((row >> 1) & 7))];
         const int P = p0 + row;
         if (P < M && fq + 4 <= F)  // F % 4 == 0: a chunk is whole or absent
-          *reinterpret_cast<f32x4*>(a.out + static_cast<int64_t>(P) * a.outPix + fq) = v;
+          __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(a.out + static_cast<int64_t>(P) * a.outPix + fq));
       }
       __builtin_amdgcn_wave_barrier();
     }

@@ -67,8 +67,10 @@ struct SwzPanel {
 // ld floats, rows >= `rows` read 0), 16-byte loads.  Thread t owns chunk
 // t % (BK/4) of rows t / (BK/4) + v * ROWSTEP (ROWSTEP % 16 == 0, so every row
 // of a thread has the same swizzle).  The conv weights [F][K] (ld = K), and
-// the GEMM operands A (not transposed) and B (transposed).
-template <int ROWS, int BK_, int NT_>
+// the GEMM operands A (not transposed) and B (transposed).  KT: K is not a
+// multiple of BK (set by klimit()); a chunk at k >= K reads 0 instead of the
+// start of the next row.
+template <int ROWS, int BK_, int NT_, bool KT = false>
 struct LeanRowsK {
   static constexpr int BK = BK_, NT = NT_;
   static constexpr int QPR = BK / 4;
@@ -80,6 +82,7 @@ struct LeanRowsK {
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t voff[PER];
   int ldsOff;
+  int kq4, kLim;  // KT: this thread's k offset in a panel, and K
   f32x4 reg[PER];
 
   __device__ inline void init(const float* p, int64_t bytes, int64_t ld, int64_t rows, int64_t r0, int tid) {
@@ -91,11 +94,20 @@ struct LeanRowsK {
       voff[v] = sel_off(gr < rows, static_cast<uint32_t>((gr * ld + kq * 4) * 4));
     }
     ldsOff = L::chunk(row, kq);
+    kq4 = 4 * kq;
+    kLim = 0;
   }
+  __device__ inline void klimit(int64_t K) { kLim = static_cast<int>(K); }
   __device__ inline void load(int64_t k0) {
     const uint32_t so = static_cast<uint32_t>(k0) * 4u;
+    if constexpr (KT) {
+      const bool in = static_cast<int>(k0) + kq4 < kLim;  // K % 4 == 0: a chunk is whole or past K
 #pragma unroll
-    for (int v = 0; v < PER; ++v) reg[v] = buf_ld4s(rsrc, voff[v], so);
+      for (int v = 0; v < PER; ++v) reg[v] = buf_ld4s(rsrc, sel_off(in, voff[v]), so);
+    } else {
+#pragma unroll
+      for (int v = 0; v < PER; ++v) reg[v] = buf_ld4s(rsrc, voff[v], so);
+    }
   }
   __device__ inline void store(lds_t* stage) const {
 #pragma unroll
@@ -230,6 +242,84 @@ struct NhwcTapRows {
 #pragma unroll
     for (int v = 0; v < PER; ++v)
       reg[v] = buf_ld4s(rsrc, sel_off((tapMask[v] >> tap) & 1u, rowOff[v] + tapOff), static_cast<uint32_t>(c0) * 4u);
+  }
+  __device__ inline void store(lds_t* stage) const {
+#pragma unroll
+    for (int v = 0; v < PER; ++v) *reinterpret_cast<lds_f4*>(stage + ldsOff + v * ROWSTEP * BK) = reg[v];
+  }
+};
+
+// NhwcTapRows for 3x3 windows over any C % 4 == 0: a panel may span taps
+// (C = 4, 8, 16: 32/C taps per panel; C = 48, 80, ...: a panel crosses one
+// tap boundary) and the last panel may run past K = 9C (those chunks read
+// 0).  A thread's chunk sits at k = k0 + 4*(t % (BK/4)): its tap and channel
+// are found per panel (one approximate float division, corrected to the
+// exact quotient); the rows' tap masks and pixel offsets are as in
+// NhwcTapRows, the channel offset is per thread.
+template <int ROWS, int BK_, int NT_>
+struct NhwcTapRowsAny {
+  static constexpr int BK = BK_, NT = NT_;
+  static constexpr int QPR = BK / 4;
+  static constexpr int ROWSTEP = NT / QPR;
+  static constexpr int PER = ROWS / ROWSTEP;
+  using L = SwzPanel<ROWS, BK>;
+  static constexpr int SIZE = L::SIZE;
+  static_assert(NT % QPR == 0 && ROWS % ROWSTEP == 0 && PER >= 1 && ROWSTEP % 16 == 0, "NhwcTapRowsAny split");
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t rowOff[PER];  // byte offset of the row's pixel at tap (0, 0), channel 0, modulo 2^32
+  uint32_t tapMask[PER];
+  uint32_t pix4, rowPix4;
+  int C, K, kq4;
+  float invC;
+  int ldsOff;
+  f32x4 reg[PER];
+
+  __device__ inline void init(const ConvGeom& g, int xPix, int64_t m0, int tid) {
+    rsrc = make_rsrc(g.x, g.xBytes);
+    C = g.C;
+    K = 9 * g.C;
+    invC = 1.f / static_cast<float>(g.C);
+    pix4 = static_cast<uint32_t>(xPix) * 4u;
+    rowPix4 = static_cast<uint32_t>(g.W) * pix4;
+    const int row = tid / QPR, kq = tid % QPR;
+    kq4 = 4 * kq;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int64_t n = m0 + row + v * ROWSTEP;
+      const bool ok = n < g.N;
+      const int64_t nn = ok ? n : 0;
+      const int64_t b = nn / g.OHW;
+      const int p = static_cast<int>(nn - b * g.OHW);
+      const int oy = p / g.OW, ox = p - (p / g.OW) * g.OW;
+      const int iy0 = oy * g.sY - g.pH, ix0 = ox * g.sX - g.pW;
+      rowOff[v] = static_cast<uint32_t>(((b * g.H + iy0) * g.W + ix0) * xPix * 4);
+      uint32_t m = 0;
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx) {
+          const bool in = static_cast<unsigned>(iy0 + ky) < static_cast<unsigned>(g.H) &&
+                          static_cast<unsigned>(ix0 + kx) < static_cast<unsigned>(g.W);
+          m |= (ok && in ? 1u : 0u) << (ky * 3 + kx);
+        }
+      tapMask[v] = m;
+    }
+    ldsOff = L::chunk(row, kq);
+  }
+  __device__ inline void load(int64_t k0) {
+    const int k = static_cast<int>(k0) + kq4;
+    // k / C: the float quotient is within one of the exact one for k < 2^22
+    int tap = static_cast<int>(static_cast<float>(k) * invC);
+    tap += (tap + 1) * C <= k ? 1 : 0;
+    tap -= tap * C > k ? 1 : 0;
+    const int c = k - tap * C;
+    const bool kin = k < K;  // past K: tap >= 9, at most 9 + 31/4
+    const int ky = tap / 3, kx = tap - (tap / 3) * 3;
+    const uint32_t off = static_cast<uint32_t>(ky) * rowPix4 + static_cast<uint32_t>(kx) * pix4 +
+                         static_cast<uint32_t>(c) * 4u;
+#pragma unroll
+    for (int v = 0; v < PER; ++v)
+      reg[v] = buf_ld4s(rsrc, sel_off(kin && ((tapMask[v] >> tap) & 1u), rowOff[v] + off), 0u);
   }
   __device__ inline void store(lds_t* stage) const {
 #pragma unroll
@@ -637,12 +727,18 @@ __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
 // themselves), columns are filters (B: the tap-major weights [F][K], k
 // contiguous), so both operands load 16 bytes along k and the epilogue
 // writes 32 consecutive channels of a pixel per half-wave.  Tail split as in
-// conv_lean_kernel (nFull may be 0: every tile cut into K pieces).
+// conv_lean_kernel (nFull may be 0: every tile cut into K pieces).  The Any
+// modes (C % 32 != 0) take ceil(K / BK) panels with the K tail reading 0, and
+// no tail split.
 template <class Cfg, int MODE>
 __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a) {
-  using AL = typename std::conditional<MODE == kTap3, NhwcTapRows<Cfg::BM, Cfg::BK, Cfg::NT, 3, 3>,
-                                       LeanRowsK<Cfg::BM, Cfg::BK, Cfg::NT>>::type;
-  using BL = LeanRowsK<Cfg::BN, Cfg::BK, Cfg::NT>;
+  constexpr bool ANY = MODE == kTap3Any || MODE == k1x1Any;
+  constexpr bool TAP = MODE == kTap3 || MODE == kTap3Any;
+  using AL = typename std::conditional<
+      MODE == kTap3, NhwcTapRows<Cfg::BM, Cfg::BK, Cfg::NT, 3, 3>,
+      typename std::conditional<MODE == kTap3Any, NhwcTapRowsAny<Cfg::BM, Cfg::BK, Cfg::NT>,
+                                LeanRowsK<Cfg::BM, Cfg::BK, Cfg::NT, ANY>>::type>::type;
+  using BL = LeanRowsK<Cfg::BN, Cfg::BK, Cfg::NT, ANY>;
   using Loop = LeanLoop<Cfg, AL, BL>;
   __shared__ __attribute__((aligned(16))) float smem[Loop::LDS_FLOATS];
   lds_t* lds = (lds_t*)smem;
@@ -661,17 +757,20 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a
   tile_coords(tile, a.tilesM, a.tilesN, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
   AL al;
-  if constexpr (MODE == kTap3)
+  if constexpr (TAP) {
     al.init(a.g, a.xPix, m0, threadIdx.x);
-  else
+  } else {
     al.init(a.g.x, a.g.xBytes, a.xPix, a.g.N, m0, threadIdx.x);
+    if constexpr (ANY) al.klimit(a.g.K);
+  }
   BL bl;
   bl.init(a.w, a.wBytes, a.g.K, a.F, n0, threadIdx.x);
+  if constexpr (ANY) bl.klimit(a.g.K);
   f32x16 acc[Cfg::FM][Cfg::FN];
-  Loop::exec(al, bl, kBegin, (kEnd - kBegin) / Cfg::BK, lds, acc);
+  Loop::exec(al, bl, kBegin, (kEnd - kBegin + Cfg::BK - 1) / Cfg::BK, lds, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (piece >= 0) {
+  if (!ANY && piece >= 0) {
     store_piece<Cfg>(a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN), wave, lane, acc);
     return;
   }

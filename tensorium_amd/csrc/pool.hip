@@ -244,6 +244,58 @@ __global__ __launch_bounds__(kThreads) void upsample_nhwc_kernel(I total, I C, I
   }
 }
 
+// Channels-last max pool, forward values (the inference layout keeps no
+// indices): output pixel (b, i, j), channel c = the maximum over the window
+// at (i*sY + off, j*sX + off), scanned as maxpool_fwd_kernel scans it (rows,
+// then columns, strict '>', from -MaxSingle), so the values are the NCHW
+// kernel's bit for bit (the first of equal values, e.g. +0 / -0, is kept).
+// A tap outside the image reads -MaxSingle in the reference, which never
+// beats the start value: it is skipped.  One thread per output pixel and
+// channel group (four channels, 16-byte loads and stores, when C, both pixel
+// strides and both bases allow); pixel indices in I (32-bit when they fit),
+// element offsets in 64 bits.
+template <bool VEC, class I>
+__global__ __launch_bounds__(kThreads) void maxpool_nhwc_kernel(I total, I CV, I H, I W, I OH, I OW, int size,
+                                                                int sY, int sX, int off, const float* __restrict__ in,
+                                                                int64_t inPix, float* __restrict__ out,
+                                                                int64_t outPix) {
+  constexpr int V = VEC ? 4 : 1;
+  for (I e = static_cast<I>(blockIdx.x) * kThreads + threadIdx.x; e < total;
+       e += static_cast<I>(gridDim.x) * kThreads) {  // e = (output pixel, channel group)
+    const I cg = e % CV, op = e / CV;
+    const I j = op % OW, t = op / OW;
+    const I i = t % OH, b = t / OH;
+    float mx[V];
+#pragma unroll
+    for (int q = 0; q < V; ++q) mx[q] = -FLT_MAX;
+    const I y0 = i * sY + off, x0 = j * sX + off;
+    for (int n = 0; n < size; ++n) {
+      const I ch = y0 + n;
+      if (ch < 0 || ch >= H) continue;
+      for (int m = 0; m < size; ++m) {
+        const I cw = x0 + m;
+        if (cw < 0 || cw >= W) continue;
+        const float* src = in + static_cast<int64_t>((b * H + ch) * W + cw) * inPix + cg * V;
+        float v[V];
+        if constexpr (VEC) {
+          const float4 u = *reinterpret_cast<const float4*>(src);
+          v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+        } else {
+          v[0] = *src;
+        }
+#pragma unroll
+        for (int q = 0; q < V; ++q)
+          if (v[q] > mx[q]) mx[q] = v[q];
+      }
+    }
+    float* dst = out + static_cast<int64_t>(op) * outPix + cg * V;
+    if constexpr (VEC)
+      *reinterpret_cast<float4*>(dst) = make_float4(mx[0], mx[1], mx[2], mx[3]);
+    else
+      *dst = mx[0];
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void upsample_bwd_kernel(int64_t total, int64_t h, int64_t w, int64_t s,
                                                                 float scale, float* __restrict__ in,
                                                                 const float* __restrict__ out, int zeroIn) {
@@ -392,4 +444,45 @@ extern "C" int32_t tnh_upsample_nhwc(int64_t batch, int64_t channels, int64_t h,
   else
     small ? go(std::false_type{}, int{}) : go(std::false_type{}, int64_t{});
   return launch_status("upsample_nhwc_kernel");
+}
+
+extern "C" int32_t tnh_maxpool_fwd_nhwc(int64_t batch, int64_t channels, int64_t h, int64_t w, int64_t outH,
+                                        int64_t outW, int64_t strideX, int64_t strideY, int64_t padding,
+                                        int64_t kernelSize, const float* in, int64_t inOff, int64_t inPix, float* out,
+                                        int64_t outOff, int64_t outPix) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && channels > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 &&
+              padding >= 0,
+          "maxpool_fwd_nhwc: bad geometry");
+  TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
+          "maxpool_fwd_nhwc: output dims do not match (h + pad - size)/stride + 1");
+  TNH_ARG(outH > 0 && outW > 0, "maxpool_fwd_nhwc: empty output");
+  TNH_ARG(in && out && inOff >= 0 && outOff >= 0, "maxpool_fwd_nhwc: NULL buffer or negative offset");
+  TNH_ARG(inPix >= channels && outPix >= channels, "maxpool_fwd_nhwc: pixel stride below the channel count");
+  TNH_ARG(kernelSize <= 64 && padding <= 64 && strideX <= 64 && strideY <= 64,
+          "maxpool_fwd_nhwc: size, stride and padding up to 64");
+  const float* src = in + inOff;
+  float* dst = out + outOff;
+  const int64_t pixels = batch * outH * outW;
+  if (pixels == 0) return TNH_OK;
+  const bool vec = channels % 4 == 0 && inPix % 4 == 0 && outPix % 4 == 0 && al16(src) && al16(dst);
+  const int64_t CV = vec ? channels / 4 : channels;
+  const int64_t total = pixels * CV;
+  // 32-bit pixel arithmetic when every pixel index (input and output, and
+  // the grid-stride index) stays below 2^31
+  const bool small = total + kThreads * 65536LL < INT32_MAX && batch * h * w < INT32_MAX;
+  const int off = static_cast<int>(-padding / 2);
+  auto go = [&](auto vecTag, auto idx) {
+    constexpr bool VEC = decltype(vecTag)::value;
+    using I = decltype(idx);
+    hipLaunchKernelGGL((maxpool_nhwc_kernel<VEC, I>), dim3(grid_for(total)), dim3(kThreads), 0, cx->stream,
+                       static_cast<I>(total), static_cast<I>(CV), static_cast<I>(h), static_cast<I>(w),
+                       static_cast<I>(outH), static_cast<I>(outW), static_cast<int>(kernelSize),
+                       static_cast<int>(strideY), static_cast<int>(strideX), off, src, inPix, dst, outPix);
+  };
+  if (vec)
+    small ? go(std::true_type{}, int{}) : go(std::true_type{}, int64_t{});
+  else
+    small ? go(std::false_type{}, int{}) : go(std::false_type{}, int64_t{});
+  return launch_status("maxpool_nhwc_kernel");
 }

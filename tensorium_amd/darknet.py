@@ -168,11 +168,33 @@ def consumers(layers):
     return use
 
 
+# The largest tensor one kernel call addresses: the kernels reach their
+# operands through buffer resources of at most this many bytes.
+MAX_CALL_BYTES = 0x7FFFFFF0
+
+
+def pass_batch(layers, batch, max_pass_batch=None):
+    """Images per forward pass: the largest count whose every activation
+    tensor (the input image, each layer's output, each route buffer) stays
+    within MAX_CALL_BYTES, capped by `max_pass_batch`.  A batch above it runs
+    as several passes over the same buffers."""
+    per_image = 4 * max([int(np.prod(layers[0]["in"]))] + [int(np.prod(L["out"])) for L in layers])
+    limit = max(1, MAX_CALL_BYTES // per_image)
+    if max_pass_batch is not None:
+        limit = min(limit, max(1, int(max_pass_batch)))
+    return min(batch, limit)
+
+
 class Network:
-    """Inference runner over the C ABI; buffers are device torch tensors."""
+    """Inference runner over the C ABI; buffers are device torch tensors.
+
+    A batch whose activations would exceed the 2 GiB a kernel call addresses
+    runs as consecutive passes of pass_batch() images over buffers sized for
+    one pass; the yolo outputs cover the whole batch.  `max_pass_batch`
+    lowers the pass size."""
 
     def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True,
-                 layout="nchw", fuse_heads=True):
+                 layout="nchw", fuse_heads=True, max_pass_batch=None):
         import torch
 
         if layout not in ("nchw", "nhwc"):
@@ -184,6 +206,14 @@ class Network:
             # channels-last planner writes route inputs into per-image
             # channel slices and has no equivalent
             raise NotImplementedError("route_mode='reference' needs layout='nchw'")
+        self.full_batch = batch
+        self.pass_batch = pass_batch(layers, batch, max_pass_batch)
+        if self.pass_batch < batch and route_mode != "image":
+            # the whole-tensor concat mixes images across the batch, so it
+            # cannot be split into passes
+            raise NotImplementedError(f"route_mode='reference' with a batch above {self.pass_batch} "
+                                      "(2 GiB per kernel call)")
+        batch = self.pass_batch  # buffers hold one pass
         self.hip, self.layers, self.batch = hip, layers, batch
         self.route_mode = route_mode
         self.layout = layout
@@ -213,7 +243,7 @@ class Network:
                 dw, wl = packed, WEIGHTS_TAP_MAJOR
             self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), wl)
         self.out = [None] * len(layers)
-        self.input_shape = (batch,) + layers[0]["in"]
+        self.input_shape = (self.full_batch,) + layers[0]["in"]
         self.up_fused, self.yolo_fused = set(), set()
         if layout == "nhwc":
             if fuse and fuse_heads:
@@ -233,6 +263,7 @@ class Network:
                         self.yolo_fused.add(i)
             self._plan_nhwc(device)
             self._plan_branches(use)
+            self._full_heads(device)
             return
         # At batch 1 a channel slice of an NCHW route buffer is contiguous, so
         # a route input's producer (convolution, shortcut or upsample) writes
@@ -264,6 +295,18 @@ class Network:
             C, h, w = L["out"]
             self.out[i] = placed[i] if i in placed else torch.empty((batch, C, h, w), dtype=torch.float32,
                                                                      device=device)
+        self._full_heads(device)
+
+    def _full_heads(self, device):
+        """Yolo outputs for the whole batch when it runs in several passes
+        (each pass writes its images' slice); the batch size seen by the
+        caller is the whole batch again."""
+        if self.pass_batch < self.full_batch:
+            for L in self.layers:
+                if L["type"] == "yolo":
+                    self.out[L["index"]] = self.torch.empty((self.full_batch,) + L["out"], dtype=self.torch.float32,
+                                                            device=device)
+        self.batch = self.full_batch
 
     # -- channels-last storage plan --------------------------------------------
     def _owner(self, i):
@@ -296,7 +339,8 @@ class Network:
                 for s_ in L["srcs"]:
                     o = self._owner(s_)
                     cs = layers[s_]["out"][0]
-                    if o not in self.store and layers[o]["type"] in ("convolutional", "shortcut", "upsample"):
+                    if o not in self.store and layers[o]["type"] in ("convolutional", "shortcut", "upsample",
+                                                                      "maxpool"):
                         self.store[o] = (buf, off, C)
                     else:
                         copies.append((s_, off))
@@ -304,8 +348,6 @@ class Network:
                 self.copy_srcs[L["index"]] = copies
         for L in layers:
             i, t = L["index"], L["type"]
-            if t == "maxpool":
-                raise NotImplementedError("maxpool has no channels-last kernel")
             if t == "yolo":
                 C, h, w = L["out"]
                 self.out[i] = torch.empty((B, C, h, w), dtype=torch.float32, device=device)
@@ -351,7 +393,12 @@ class Network:
     def output(self, i):
         """Layer i's output as a [B, C, h, w] tensor (a view in NCHW mode, a
         permuted view of the channel slice in NHWC mode)."""
-        if self.layout == "nchw" or self.layers[i]["type"] == "yolo":
+        if self.layers[i]["type"] == "yolo":
+            return self.buffer(i)
+        if self.pass_batch < self.full_batch:
+            raise ValueError(f"the batch runs in passes of {self.pass_batch} images: only the yolo outputs "
+                             "cover the whole batch")
+        if self.layout == "nchw":
             return self.buffer(i)
         if i in self.up_fused:
             raise ValueError(f"layer {i} stores only its upsampled output (layer {i + 1})")
@@ -379,6 +426,8 @@ class Network:
         1.188 ms at batch 1 and 8.86 against 8.80 ms at batch 16).  The
         first forward pass always runs on one stream (it tunes every shape
         alone on the GPU)."""
+        if self.pass_batch < self.full_batch:
+            return self._forward_passes(x, on_layer)
         hip = self.hip
         tails = getattr(self, "branches", {})
         if branches is None:
@@ -398,6 +447,33 @@ class Network:
             if on_layer:
                 on_layer(i, False)
         return heads
+
+    def _forward_passes(self, x, on_layer):
+        """forward() over a batch above pass_batch: consecutive passes over
+        images [c0, c0 + c) through the one-pass buffers (a last, smaller
+        pass uses their first c images), each yolo layer writing its slice of
+        the whole-batch output."""
+        ys = [L["index"] for L in self.layers if L["type"] == "yolo"]
+        full = {y: self.out[y] for y in ys}
+        try:
+            for c0 in range(0, self.full_batch, self.pass_batch):
+                c = min(self.pass_batch, self.full_batch - c0)
+                self.batch = c
+                for y in ys:
+                    self.out[y] = full[y][c0:c0 + c]
+                prev = x[c0:c0 + c]
+                for L in self.layers:
+                    if on_layer:
+                        on_layer(L["index"], True)
+                    prev = self._layer(L, prev, [])
+                    if on_layer:
+                        on_layer(L["index"], False)
+        finally:
+            self.batch = self.full_batch
+            for y in ys:
+                self.out[y] = full[y]
+        self._tuned = True
+        return [full[y] for y in ys]
 
     def _forward_branched(self, x, tails):
         """forward() with each yolo head tail on the side stream: the main
@@ -489,6 +565,13 @@ class Network:
                 src, soff, spix = self.nhwc_store(i - 1)
                 dst, doff, dpix = self.nhwc_store(i)
                 hip.upSampleNHWC(B, C, h, ww, L["stride"], L["scale"], src, soff, spix, dst, doff, dpix)
+        elif t == "maxpool":
+            C, h, ww = L["in"]
+            _, oh, ow = L["out"]
+            src, soff, spix = self.nhwc_store(i - 1)
+            dst, doff, dpix = self.nhwc_store(i)
+            hip.forwardMaxPoolNHWC(B, C, h, ww, oh, ow, L["stride"], L["stride"], L["pad"], L["size"], src, soff, spix,
+                                   dst, doff, dpix)
         elif t == "yolo":
             if i - 1 not in self.yolo_fused:
                 C, h, ww = L["in"]

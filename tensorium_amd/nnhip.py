@@ -97,6 +97,7 @@ _PROTOS = {
     "tnh_yolo_fwd_nhwc": [i64, i64, i64, i64, i64, vp, i64, i64, vp],
     "tnh_copy_channels": [i64, i64, vp, i64, i64, vp, i64, i64],
     "tnh_upsample_nhwc": [i64, i64, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64],
+    "tnh_maxpool_fwd_nhwc": [i64] * 10 + [vp, i64, i64, vp, i64, i64],
     "tnh_conv2d_out_dims": [i64] * 8 + [C.POINTER(i64), C.POINTER(i64)],
     "tnh_forward_bias": [i64, vp, i64, i64, vp, i64, i64],
     "tnh_forward_scale": [i64, vp, i64, i64, vp, i64, i64],
@@ -409,6 +410,11 @@ class TNNHip:
     def upSampleNHWC(self, batch, channels, h, w, stride, scale, input, inOffset, inPix, output, outOffset, outPix):
         call("tnh_upsample_nhwc", batch, channels, h, w, stride, scale, addr(input), inOffset, inPix, addr(output),
              outOffset, outPix)
+
+    def forwardMaxPoolNHWC(self, batch, channels, h, w, outH, outW, strideX, strideY, padding, kernelSize, input,
+                           inOffset, inPix, output, outOffset, outPix):
+        call("tnh_maxpool_fwd_nhwc", batch, channels, h, w, outH, outW, strideX, strideY, padding, kernelSize,
+             addr(input), inOffset, inPix, addr(output), outOffset, outPix)
 
     def packConvWeights(self, filters, c, kernelSize, src, dst, kernelWidth=None):
         """[F][C][kh][kw] -> tap-major [F][kh][kw][C] (device to device)."""

@@ -49,6 +49,16 @@ CONVS = [  # batch, C, H, F, k, s, p, act, residual
     (2, 256, 13, 512, 3, 1, 1, acLEAKY, True),
     (1, 64, 30, 130, 3, 1, 1, acLOGISTIC, False),
     (2, 32, 17, 96, 3, 2, 1, acLEAKY, False),
+    # C % 32 != 0 (one fixed tile, K tail): YOLOv3-tiny's 16-channel layer,
+    # C = 8 with stride 2, C = 4 read channels-last, C = 48 / 80 (panels that
+    # cross a tap), 1x1 with C = 20 and 100
+    (2, 16, 52, 32, 3, 1, 1, acLEAKY, False),
+    (2, 8, 33, 48, 3, 2, 1, acLEAKY, True),
+    (1, 4, 40, 70, 3, 1, 1, acLINEAR, False),
+    (2, 48, 21, 64, 3, 1, 1, acLEAKY, True),
+    (2, 80, 13, 40, 3, 1, 1, acLEAKY, False),
+    (2, 20, 19, 24, 1, 1, 0, acLEAKY, False),
+    (1, 100, 15, 130, 1, 1, 0, acLOGISTIC, False),
 ]
 
 
@@ -166,6 +176,33 @@ def test_conv_nhwc_channel_slices(hip, k, s):
     got = H(dout, hip)
     assert np.array_equal(got[..., 32:32 + F].transpose(0, 3, 1, 2), ref)
     assert np.all(got[..., :32] == 7.0) and np.all(got[..., 32 + F:] == 7.0)
+
+
+@pytest.mark.parametrize("Cc,k,s,F", [(4, 3, 1, 24), (8, 3, 2, 40), (16, 3, 1, 32), (20, 3, 1, 72), (48, 3, 1, 64),
+                                       (80, 3, 2, 33), (20, 1, 1, 24), (100, 1, 1, 130), (4, 1, 1, 8)])
+def test_conv_nhwc_any_channels_integer(hip, Cc, k, s, F):
+    """C % 4 == 0 but not a multiple of 32, on integer data (exact sums):
+    the input is a channel slice whose neighbouring channels hold 1e30, so a
+    chunk read past the pixel's C channels (the K tail of a 1x1, a panel
+    that spans taps) would show; the output is a slice too."""
+    case(f"conv nhwc any-C C{Cc} k{k} s{s} F{F}")
+    B, Hh = 2, 23
+    p = k // 2
+    OH = (Hh + 2 * p - k) // s + 1
+    rng = np.random.default_rng(Cc * 10 + k)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    ref = R.conv_forward(x, Wt, b, k, s, p, acLEAKY)
+    xin = np.full((B, Hh, Hh, Cc + 12), 1e30, np.float32)
+    xin[..., 4:4 + Cc] = nhwc(x)
+    outbuf = np.full((B, OH, OH, F + 8), 7.0, np.float32)
+    dout = D(outbuf)
+    hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, s, p, D(xin), 4, D(tap_major(Wt, F, Cc, k)), D(b), acLEAKY, dout, 4,
+                          inPix=Cc + 12, outPix=F + 8)
+    got = H(dout, hip)
+    assert np.array_equal(got[..., 4:4 + F].transpose(0, 3, 1, 2), ref)
+    assert np.all(got[..., :4] == 7.0) and np.all(got[..., 4 + F:] == 7.0)
 
 
 @pytest.mark.parametrize("cfg", CONV_LEAN_CFGS)
@@ -350,8 +387,8 @@ def test_conv_nhwc_rejects_unsupported(hip):
     x = torch.zeros(1, 8, 8, 48, device="cuda")
     w = torch.zeros(32, 9 * 48, device="cuda")
     out = torch.zeros(1, 8, 8, 32, device="cuda")
-    with pytest.raises(TNHError):  # C % 32 != 0
-        hip.conv2dForwardNHWC(1, 48, 8, 8, 32, 3, 1, 1, x, 0, w, None, acLEAKY, out, 0)
+    with pytest.raises(TNHError):  # C % 4 != 0
+        hip.conv2dForwardNHWC(1, 6, 8, 8, 32, 3, 1, 1, x, 0, w, None, acLEAKY, out, 0, inPix=48)
     with pytest.raises(TNHError):  # 1x1 with stride 2
         hip.conv2dForwardNHWC(1, 32, 8, 8, 32, 1, 2, 0, x, 0, w, None, acLEAKY, out, 0, inPix=48)
 
@@ -377,3 +414,42 @@ def test_upsample_nhwc_vs_oracle(hip, B, Cc, Hh, Ww, s, scale, inPad, outPad, ou
     assert np.array_equal(got[..., outOff:outOff + Cc].transpose(0, 3, 1, 2), ref)
     rest = np.concatenate([got[..., :outOff], got[..., outOff + Cc:]], axis=-1)
     assert np.all(rest == 7.0)
+
+
+@pytest.mark.parametrize("B,Cc,Hh,Ww,size,s,pad,inPad,outPad", [
+    (2, 16, 416, 416, 2, 2, 1, 0, 0),       # YOLOv3-tiny's first maxpool (16-byte path)
+    (1, 512, 13, 13, 2, 1, 1, 0, 0),        # the stride-1 maxpool: the last row and column see one tap inside
+    (2, 256, 26, 26, 2, 2, 1, 128, 0),      # input a channel slice of a route buffer
+    (3, 6, 11, 9, 3, 2, 2, 1, 3),           # odd channels (scalar path), window offset -1, slices both sides
+    (1, 8, 7, 7, 5, 3, 4, 0, 8),            # windows wider than the stride, output slice
+])
+def test_maxpool_nhwc_vs_oracle(hip, B, Cc, Hh, Ww, size, s, pad, inPad, outPad):
+    """Channels-last max pool: the oracle's values (tnh_maxpool_fwd's CPU
+    semantics) bit for bit, on data with ties and signed zeros (the first of
+    equal values is kept: +0 / -0 order shows), channel slices in and out
+    leaving the rest of the output buffer untouched."""
+    case(f"maxpool nhwc B{B} C{Cc} {Hh}x{Ww} size{size} s{s} pad{pad}")
+    rng = np.random.default_rng(Cc + size)
+    x = rng.integers(-2, 3, (B, Cc, Hh, Ww)).astype(np.float32)
+    x[x == 0] = np.where(rng.random(int((x == 0).sum())) < 0.5, -0.0, 0.0).astype(np.float32)
+    ref, _ = R.maxpool_fwd(x, size, s, s, pad, with_idx=False)
+    OH, OW = ref.shape[2:]
+    xin = np.full((B, Hh, Ww, Cc + inPad), 9.0, np.float32)
+    xin[..., inPad:] = nhwc(x)
+    outbuf = np.full((B, OH, OW, Cc + outPad), 7.0, np.float32)
+    dout = D(outbuf)
+    hip.forwardMaxPoolNHWC(B, Cc, Hh, Ww, OH, OW, s, s, pad, size, D(xin), inPad, Cc + inPad, dout, outPad,
+                           Cc + outPad)
+    got = H(dout, hip)
+    g = got[..., outPad:].transpose(0, 3, 1, 2)
+    assert np.array_equal(g.view(np.uint32), np.ascontiguousarray(ref).view(np.uint32))
+    assert np.all(got[..., :outPad] == 7.0)
+
+
+def test_maxpool_nhwc_rejects(hip):
+    x = torch.zeros(1, 4, 4, 8, device="cuda")
+    out = torch.zeros(1, 2, 2, 8, device="cuda")
+    with pytest.raises(TNHError):  # output dims that do not match
+        hip.forwardMaxPoolNHWC(1, 8, 4, 4, 3, 3, 2, 2, 0, 2, x, 0, 8, out, 0, 8)
+    with pytest.raises(TNHError):  # pixel stride below the channel count
+        hip.forwardMaxPoolNHWC(1, 8, 4, 4, 2, 2, 2, 2, 0, 2, x, 0, 4, out, 0, 8)

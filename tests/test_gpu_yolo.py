@@ -434,3 +434,62 @@ def test_nhwc_rejects_reference_route_mode(hip, yolo):
     layers, W = yolo
     with pytest.raises(NotImplementedError):
         darknet.Network(hip, layers, 2, W, layout="nhwc", route_mode="reference")
+
+
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_yolov3_batch_in_passes(hip, layout):
+    """A batch run as several passes over one-pass buffers (max_pass_batch=2:
+    images 0-1, 2-3, then 4 alone) gives the heads of the single-pass network
+    within the per-tensor bound, eagerly and in a graph replay; intermediate
+    outputs are refused (only the last pass is held)."""
+    print(f"[case] yolov3-128 batch 5 in passes of 2, {layout}", flush=True)
+    _, layers = darknet.load_cfg("yolov3.cfg", 128, 128)
+    W = darknet.synthetic_weights(layers)
+    dx = torch.from_numpy(synth.uniform(11, (5, 3, 128, 128))).cuda()
+    torch.cuda.synchronize()
+    one = darknet.Network(hip, layers, 5, W, layout=layout)
+    ref = [h.cpu().numpy() for h in one.forward(dx)]
+    hip.finish()
+    net = darknet.Network(hip, layers, 5, W, layout=layout, max_pass_batch=2)
+    assert (net.pass_batch, net.batch) == (2, 5)
+    heads = net.forward(dx)
+    hip.finish()
+    for h, r in zip(heads, ref):
+        assert h.shape == r.shape
+        assert R.rel_err(h.cpu().numpy(), r) <= TOL
+    heads = net.capture(dx)
+    for _ in range(2):
+        for h in heads:
+            h.zero_()
+        torch.cuda.synchronize()
+        net.replay()
+        hip.finish()
+        for h, r in zip(heads, ref):
+            assert R.rel_err(h.cpu().numpy(), r) <= TOL
+    net.release_graph()
+    with pytest.raises(ValueError, match="passes"):
+        net.output(3)
+
+
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_yolov3_tiny_vs_oracle(hip, layout):
+    """YOLOv3-tiny (maxpools, a stride-1 maxpool, a 16-channel convolution
+    input, a route over a maxpool's input) end to end at batch 2 against the
+    oracle run per image: the two pre-logistic head convolutions (15, 22)
+    within the per-tensor bound, the yolo outputs within it too."""
+    print(f"[case] yolov3-tiny-416 batch 2 {layout} vs oracle", flush=True)
+    _, layers = darknet.load_cfg("yolov3-tiny.cfg")
+    W = darknet.synthetic_weights(layers)
+    x = synth.uniform(5, (2, 3, 416, 416))
+    net = darknet.Network(hip, layers, 2, W, layout=layout)
+    heads = net.forward(torch.from_numpy(x).cuda())
+    hip.finish()
+    for b in range(2):
+        ref = netref.forward(layers, W, x[b:b + 1])
+        for i in (15, 22):
+            got = net.output(i)[b:b + 1].cpu().numpy()
+            e = R.rel_err(got, ref[i])
+            print(f"image {b} head conv {i}: {e:.3e}", flush=True)
+            assert e <= TOL, (b, i, e)
+        for h, i in zip(heads, (16, 23)):
+            assert R.rel_err(h[b:b + 1].cpu().numpy(), ref[i]) <= TOL
