@@ -726,7 +726,10 @@ def main():
                    "activation_layout": layout_for(args.batch)},
         "conv_gflops": round(gflops, 1),
         "conv_frac_fp32_mfma_peak": round(gflops * 1e9 / PEAK_FP32_MFMA, 4),
-        "conv_kernel_ms_per_step": round(conv_ms, 4),
+        # the per-layer event brackets of one eager pass (each includes its
+        # launch gaps), summed over the conv layers: a breakdown of an eager
+        # forward, not a part of ms_per_step (a graph replay)
+        "conv_ms_eager_layer_events": round(conv_ms, 4),
         "img_s_batch1": None if b1 is None else round(b1, 2),
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved / 1e12, 3),
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",

@@ -272,6 +272,159 @@ __global__ __launch_bounds__(Cfg::NT) void conv_wsplit_nhwc_kernel(ConvArgs a) {
   }
 }
 
+// The 16-row tile (Ws16Cfg): as conv_wsplit_nhwc_kernel with 16x16x4
+// MFMAs.  Operand layouts of v_mfma_f32_16x16x4_f32: lane l supplies
+// A[i = l % 16][k = l / 16] and B[k = l / 16][j = l % 16]; accumulator
+// register r of lane l is D[i = 4*(l / 16) + r][j = l % 16].  A lane reads 16
+// bytes (4 consecutive k) of its row per 16-deep chunk and uses element e at
+// MFMA step e: step e pairs k = 16c + 4*(l/16) + e of A and B alike, so every
+// k of the chunk is summed once (in MFMA order).
+template <class Cfg, int MODE>
+__global__ __launch_bounds__(Cfg::NT) void conv_wsplit16_nhwc_kernel(ConvArgs a) {
+  constexpr int W = Cfg::W, BLK = Cfg::BLK, UNITS = Cfg::UNITS;
+  using AL = typename std::conditional<MODE == kTap3, WaveTapRows<16>, WaveRowsK<16>>::type;
+  using BL = WaveRowsK<Cfg::BN>;
+  constexpr int STAGE = AL::SIZE + BL::SIZE;
+  constexpr int LDS = W * STAGE > Cfg::RED_FLOATS ? W * STAGE : Cfg::RED_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+  const int64_t M = a.g.N, K = a.g.K;
+
+  AL a0, a1;
+  BL b0, b1;
+  if constexpr (MODE == kTap3) {
+    a0.init(a, m0, lane);
+    a1.init(a, m0, lane);
+  } else {
+    a0.init(a.g.x, a.g.xBytes, a.xPix, M, m0, lane);
+    a1.init(a.g.x, a.g.xBytes, a.xPix, M, m0, lane);
+  }
+  b0.init(a.w, a.wBytes, K, a.F, n0, lane);
+  b1.init(a.w, a.wBytes, K, a.F, n0, lane);
+
+  // LDS offsets of this lane's 16-byte operand reads, chunk c: A row r16,
+  // B rows 16*jj + r16, quad 4c + g
+  int aOff[2], bOff[2][BLK];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    aOff[c] = SwzPanel<16, 32>::chunk(r16, 4 * c + g);
+#pragma unroll
+    for (int jj = 0; jj < BLK; ++jj) bOff[c][jj] = AL::SIZE + SwzPanel<Cfg::BN, 32>::chunk(16 * jj + r16, 4 * c + g);
+  }
+  f32x4 acc[BLK];
+#pragma unroll
+  for (int jj = 0; jj < BLK; ++jj) acc[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  lds_t* panel = (lds_t*)smem + wave * STAGE;
+  const int P = static_cast<int>(K / 32);
+  const int p0 = wave * P / W, np = (wave + 1) * P / W - p0;
+  auto kOf = [&](int i) { return 32 * (p0 + min(i, np - 1)); };
+  auto multiply = [&]() {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const f32x4 fa = *reinterpret_cast<const lds_f4*>(panel + aOff[c]);
+      f32x4 fb[BLK];
+#pragma unroll
+      for (int jj = 0; jj < BLK; ++jj) fb[jj] = *reinterpret_cast<const lds_f4*>(panel + bOff[c][jj]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int jj = 0; jj < BLK; ++jj) acc[jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[e], fb[jj][e], acc[jj], 0, 0, 0);
+    }
+  };
+  if (np > 0) {
+    a0.load(kOf(0));
+    b0.load(kOf(0));
+    a1.load(kOf(1));
+    b1.load(kOf(1));
+    for (int i = 0; i < np; i += 2) {
+      a0.store(panel);
+      b0.store(panel + AL::SIZE);
+      a0.load(kOf(i + 2));
+      b0.load(kOf(i + 2));
+      multiply();
+      if (i + 1 < np) {
+        a1.store(panel);
+        b1.store(panel + AL::SIZE);
+      }
+      a1.load(kOf(i + 3));
+      b1.load(kOf(i + 3));
+      if (i + 1 < np) multiply();
+    }
+  }
+  __syncthreads();
+
+  // partial tiles to LDS: quad jj of wave w at red[(w*UNITS + jj)*64 + lane]
+  lds_f4* R = (lds_f4*)smem;
+#pragma unroll
+  for (int jj = 0; jj < BLK; ++jj) R[(wave * UNITS + jj) * 64 + lane] = acc[jj];
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t outR = make_rsrc(a.out, a.outBytes);
+  const __amdgpu_buffer_rsrc_t resR = make_rsrc(a.res, a.resBytes);
+  const uint32_t op4 = static_cast<uint32_t>(a.outPix) * 4u, rp4 = static_cast<uint32_t>(a.resPix) * 4u;
+  for (int u = wave; u < UNITS; u += W) {
+    f32x4 p[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) p[w] = R[(w * UNITS + u) * 64 + lane];
+    f32x4 s = p[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) s = s + p[w];
+    // lane owns filter f = n0 + 16u + r16; register e is pixel m0 + 4g + e
+    const int64_t f = n0 + 16 * u + r16;
+    const bool okF = f < a.F;
+    const float bias = a.bias && okF ? a.bias[f] : -0.f;
+    const int64_t mBase = m0 + 4 * g;
+    uint32_t vo[4], vr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool ok = okF && mBase + e < M;
+      vo[e] = sel_off(ok, static_cast<uint32_t>(mBase + e) * op4 + static_cast<uint32_t>(f) * 4u);
+      vr[e] = sel_off(ok, static_cast<uint32_t>(mBase + e) * rp4 + static_cast<uint32_t>(f) * 4u);
+    }
+    float rv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.res) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rv[e] = buf_ld1s(resR, vr[e], 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = s[e] + bias;  // nConvolutionLayer.pas:524 (forwardBias)
+      if (a.act == TNH_AC_LEAKY)
+        v = v < 0.f ? 0.1f * v : v;  // leaky_array (nactivation.pas:234)
+      else if (a.act == TNH_AC_LOGISTIC)
+        v = 1.f / (1.f + expf(-v));
+      if (a.res) v = v + rv[e];  // the fused shortcut (naddlayer.pas:698)
+      if (a.upS > 0 || a.yolo) {
+        if (okF && mBase + e < M) store_nhwc_variant(a, outR, mBase + e, f, v);
+      } else {
+        st1(outR, v, vo[e]);
+      }
+    }
+  }
+}
+
+template <class Cfg>
+int launch_cfg16(ConvArgs a, int mode, hipStream_t s) {
+  const int64_t tm = (a.g.N + Cfg::BM - 1) / Cfg::BM, tn = (a.F + Cfg::BN - 1) / Cfg::BN;
+  if (tm * tn > INT32_MAX) return fail(TNH_ERR_UNSUPPORTED, "conv2d: grid too large");
+  a.tilesM = static_cast<int>(tm);
+  a.tilesN = static_cast<int>(tn);
+  a.splits = 1;
+  a.tailSplits = 0;
+  a.kChunk = a.g.K;
+  const dim3 grid(static_cast<unsigned>(tm * tn));
+  if (mode == kTap3)
+    hipLaunchKernelGGL((conv_wsplit16_nhwc_kernel<Cfg, kTap3>), grid, dim3(Cfg::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((conv_wsplit16_nhwc_kernel<Cfg, k1x1>), grid, dim3(Cfg::NT), 0, s, a);
+  return launch_status("conv_wsplit16_nhwc_kernel");
+}
+
 template <class Cfg>
 int launch_cfg(ConvArgs a, int mode, hipStream_t s) {
   const int64_t tm = (a.g.N + Cfg::BM - 1) / Cfg::BM, tn = (a.F + Cfg::BN - 1) / Cfg::BN;
@@ -298,6 +451,8 @@ int launch_wsplit_nhwc(int ws, ConvArgs a, int mode, hipStream_t s) {
     case 0: return launch_cfg<WsCfg<1, 1, 4>>(a, mode, s);
     case 1: return launch_cfg<WsCfg<1, 1, 8>>(a, mode, s);
     case 2: return launch_cfg<WsCfg<1, 2, 4>>(a, mode, s);
+    case 3: return launch_cfg16<Ws16Cfg<1, 4>>(a, mode, s);
+    case 4: return launch_cfg16<Ws16Cfg<1, 8>>(a, mode, s);
     default: return fail(TNH_ERR_UNSUPPORTED, "conv2d: wave-split tile %d", ws);
   }
 }
