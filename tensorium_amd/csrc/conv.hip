@@ -594,7 +594,8 @@ const CfgInfo kCfgs[kNumCfg] = {
     {64, 128, 32, 1.10f, 2, kLean},   {128, 128, 32, 1.05f, 2, kLean},
     // wave-split tiles: timed only (the cost model never picks them)
     {32, 32, 32, 1.f, 1, kWsplit},    {32, 32, 32, 1.f, 1, kWsplit},    {32, 64, 32, 1.f, 1, kWsplit},
-    {16, 32, 32, 1.f, 1, kWsplit},    {16, 32, 32, 1.f, 1, kWsplit},
+    {16, 32, 32, 1.f, 1, kWsplit},    {16, 32, 32, 1.f, 1, kWsplit},    {16, 16, 32, 1.f, 1, kWsplit},
+    {16, 16, 32, 1.f, 1, kWsplit},
 };
 static_assert(sizeof(kCfgs) / sizeof(kCfgs[0]) == kNumCfg, "one CfgInfo per configuration");
 

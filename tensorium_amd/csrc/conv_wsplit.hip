@@ -451,8 +451,10 @@ int launch_wsplit_nhwc(int ws, ConvArgs a, int mode, hipStream_t s) {
     case 0: return launch_cfg<WsCfg<1, 1, 4>>(a, mode, s);
     case 1: return launch_cfg<WsCfg<1, 1, 8>>(a, mode, s);
     case 2: return launch_cfg<WsCfg<1, 2, 4>>(a, mode, s);
-    case 3: return launch_cfg16<Ws16Cfg<1, 4>>(a, mode, s);
-    case 4: return launch_cfg16<Ws16Cfg<1, 8>>(a, mode, s);
+    case 3: return launch_cfg16<Ws16Cfg<2, 4>>(a, mode, s);
+    case 4: return launch_cfg16<Ws16Cfg<2, 8>>(a, mode, s);
+    case 5: return launch_cfg16<Ws16Cfg<1, 4>>(a, mode, s);
+    case 6: return launch_cfg16<Ws16Cfg<1, 8>>(a, mode, s);
     default: return fail(TNH_ERR_UNSUPPORTED, "conv2d: wave-split tile %d", ws);
   }
 }
