@@ -128,9 +128,12 @@ int32_t tnh_sgemm_strided_batched(int32_t transA, int32_t transB, int64_t M,
  * 128x128 / 128x64 / 64x128 / 64x64 tiles (need K % 32 == 0, 16-byte
  * aligned operands with ld % 4 == 0, M and N multiples of 4 where that
  * operand is row-contiguous, C within 2 GiB; other calls fall back to the
- * general tiles); -1 lets the library choose.  Every non-split
- * configuration sums k in the same order, so the choice does not change the
- * results.  The first call for a shape times the candidates as graph
+ * general tiles), 6..8 the wave-split 32x32 (4 or 8 waves) and 32x64 tiles
+ * (K split over the waves of one workgroup; the lean tiles' requirements);
+ * -1 lets the library choose.  The whole-K configurations sum k in the same
+ * order; the wave-split ones (timed only for problems whose 64x64 tiles
+ * number under two per CU, never in the deterministic mode) sum per-wave
+ * partials.  The first call for a shape times the candidates as graph
  * replays into a scratch C. */
 int32_t tnh_sgemm_set_autotune(int32_t enable, int32_t forcedConfig);
 

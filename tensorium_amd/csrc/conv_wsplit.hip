@@ -25,6 +25,7 @@
 #include "conv_lean.hpp"
 #include "conv_wsplit.hpp"
 #include "gemm_core.hpp"
+#include "wave_panels.hpp"
 
 namespace tnh {
 namespace conv {
@@ -33,39 +34,6 @@ namespace {
 __device__ inline void st1(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff) {
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, 0, 0);
 }
-
-// One wave's k-contiguous operand rows r0 .. r0 + ROWS - 1 (row stride ld
-// floats, rows >= `rows` read 0): lane t fetches chunk t % 8 (16 bytes) of
-// rows t / 8 + 8v.  The weights [F][K], and for a 1x1 stride-1 conv the
-// input pixels themselves.
-template <int ROWS>
-struct WaveRowsK {
-  static constexpr int PER = ROWS / 8;
-  using L = SwzPanel<ROWS, 32>;
-  static constexpr int SIZE = L::SIZE;
-  __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t voff[PER];
-  int ldsOff[PER];
-  f32x4 reg[PER];
-  __device__ inline void init(const float* p, int64_t bytes, int64_t ld, int64_t rows, int64_t r0, int lane) {
-    rsrc = make_rsrc(p, bytes);
-#pragma unroll
-    for (int v = 0; v < PER; ++v) {
-      const int row = lane / 8 + 8 * v, q = lane % 8;
-      const int64_t gr = r0 + row;
-      voff[v] = sel_off(gr < rows, static_cast<uint32_t>((gr * ld + 4 * q) * 4));
-      ldsOff[v] = L::chunk(row, q);
-    }
-  }
-  __device__ inline void load(int k0) {
-#pragma unroll
-    for (int v = 0; v < PER; ++v) reg[v] = buf_ld4s(rsrc, voff[v], static_cast<uint32_t>(k0) * 4u);
-  }
-  __device__ inline void store(lds_t* panel) const {
-#pragma unroll
-    for (int v = 0; v < PER; ++v) *reinterpret_cast<lds_f4*>(panel + ldsOff[v]) = reg[v];
-  }
-};
 
 // One wave's channels-last 3x3 tap gather rows (output pixels m0 ..
 // m0 + ROWS - 1): row r at k = tap*C + c reads input pixel (iy0 + ky,

@@ -11,7 +11,9 @@
 
 #include "common.hpp"
 #include "conv_lean.hpp"
+#include "conv_wsplit.hpp"
 #include "gemm_core.hpp"
+#include "wave_panels.hpp"
 
 namespace tnh {
 namespace {
@@ -144,6 +146,142 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void sgemm_lean_kernel(SgemmArgs
   }
 }
 
+// Wave-split SGEMM for problems whose lean tiles leave CUs idle (512^3 has
+// 64 tiles of 64x64 for 256 CUs): one (32*FM) x (32*FN) tile per workgroup,
+// its K range split over the W waves (conv_wsplit.hip's scheme: each wave
+// fetches its own panels into its own LDS panel, no barrier in the K loop),
+// the W partial tiles summed in wave order through LDS, then alpha / beta.
+// Same operand requirements as the lean tiles.
+template <class Cfg, bool TA, bool TB>
+__global__ __launch_bounds__(Cfg::NT) void sgemm_wsplit_kernel(SgemmArgs a) {
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, W = Cfg::W, UNITS = Cfg::UNITS;
+  using AL = typename std::conditional<TA, conv::WaveRowsMN<32 * FM>, conv::WaveRowsK<32 * FM>>::type;
+  using BL = typename std::conditional<TB, conv::WaveRowsK<32 * FN>, conv::WaveRowsMN<32 * FN>>::type;
+  using Pan = conv::LeanCfg<32 * FM, 32 * FN, 32, 1, 1, 1>;
+  using Loop = conv::LeanLoop<Pan, AL, BL>;
+  constexpr int STAGE = AL::SIZE + BL::SIZE;
+  constexpr int LDS = W * STAGE > Cfg::RED_FLOATS ? W * STAGE : Cfg::RED_FLOATS;
+  __shared__ __attribute__((aligned(16))) float smem[LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t bz = blockIdx.y;
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+
+  AL a0, a1;
+  BL b0, b1;
+  a0.init(a.A + bz * a.strideA, a.aBytes, a.lda, a.M, m0, lane);
+  a1.init(a.A + bz * a.strideA, a.aBytes, a.lda, a.M, m0, lane);
+  b0.init(a.B + bz * a.strideB, a.bBytes, a.ldb, a.N, n0, lane);
+  b1.init(a.B + bz * a.strideB, a.bBytes, a.ldb, a.N, n0, lane);
+
+  typename Loop::Lanes LN;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) LN.lo[c][e] = conv::SwzPanel<32, 32>::chunk(r, 4 * c + 2 * h + e);
+  LN.aRow = 0;
+  LN.bRow = 0;
+  f32x16 acc[FM][FN];
+  Loop::zero(acc);
+  lds_t* panel = (lds_t*)smem + wave * STAGE;
+  const int P = static_cast<int>(a.K / 32);
+  const int p0 = wave * P / W, np = (wave + 1) * P / W - p0;
+  // loads issued unconditionally, clamped to the wave's last panel (a
+  // conditional load makes the compiler wait for every load in flight)
+  auto kOf = [&](int i) { return 32 * (p0 + min(i, np - 1)); };
+  auto multiply = [&]() {
+    typename Loop::Frag f0, f1;
+    Loop::read(panel, 0, LN, f0);
+    Loop::read(panel, 1, LN, f1);
+    Loop::mma(f0, acc);
+    Loop::mma(f1, acc);
+  };
+  if (np > 0) {
+    a0.load(kOf(0));
+    b0.load(kOf(0));
+    a1.load(kOf(1));
+    b1.load(kOf(1));
+    for (int i = 0; i < np; i += 2) {
+      a0.store(panel);
+      b0.store(panel + AL::SIZE);
+      a0.load(kOf(i + 2));
+      b0.load(kOf(i + 2));
+      multiply();
+      if (i + 1 < np) {
+        a1.store(panel);
+        b1.store(panel + AL::SIZE);
+      }
+      a1.load(kOf(i + 3));
+      b1.load(kOf(i + 3));
+      if (i + 1 < np) multiply();
+    }
+  }
+  __syncthreads();
+  lds_f4* R = (lds_f4*)smem;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        R[(wave * UNITS + (i * FN + j) * 4 + q) * 64 + lane] =
+            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+  __syncthreads();
+
+  const __amdgpu_buffer_rsrc_t cR = make_rsrc(a.C + bz * a.strideC, a.cBytes);
+  const uint32_t ldc4 = static_cast<uint32_t>(a.ldc) * 4u;
+  const float alpha = a.alpha, beta = a.beta;
+  for (int u = wave; u < UNITS; u += W) {
+    const int i = u / (FN * 4), j = (u / 4) % FN, q = u % 4;
+    f32x4 p[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) p[w] = R[(w * UNITS + u) * 64 + lane];
+    f32x4 sum = p[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum = sum + p[w];
+    // lane owns column n; register e of the quad is row m0 + 32i + 8q + 4h + e
+    const int64_t n = n0 + 32 * j + r;
+    const int64_t mBase = m0 + 32 * i + 8 * q + 4 * h;
+    uint32_t vo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      vo[e] = sel_off(n < a.N && mBase + e < a.M,
+                      static_cast<uint32_t>(mBase + e) * ldc4 + static_cast<uint32_t>(n) * 4u);
+    float cv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (beta != 0.f) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cv[e] = buf_ld1s(cR, vo[e], 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      conv::buf_st1s(cR, beta != 0.f ? alpha * sum[e] + beta * cv[e] : alpha * sum[e], vo[e], 0);
+  }
+}
+
+template <class Cfg>
+int launch_wsplit(const SgemmArgs& a0, int64_t batch, bool ta, bool tb, hipStream_t s) {
+  SgemmArgs a = a0;
+  const int64_t tm = (a.M + Cfg::BM - 1) / Cfg::BM, tn = (a.N + Cfg::BN - 1) / Cfg::BN;
+  if (tm * tn > INT32_MAX || batch > 65535)
+    return fail(TNH_ERR_UNSUPPORTED, "sgemm: grid too large (%lld tiles, batch %lld)",
+                (long long)(tm * tn), (long long)batch);
+  a.tilesM = static_cast<int>(tm);
+  a.tilesN = static_cast<int>(tn);
+  const dim3 grid(static_cast<unsigned>(tm * tn), static_cast<unsigned>(batch));
+  if (!ta && !tb)
+    hipLaunchKernelGGL((sgemm_wsplit_kernel<Cfg, false, false>), grid, dim3(Cfg::NT), 0, s, a);
+  else if (!ta)
+    hipLaunchKernelGGL((sgemm_wsplit_kernel<Cfg, false, true>), grid, dim3(Cfg::NT), 0, s, a);
+  else if (!tb)
+    hipLaunchKernelGGL((sgemm_wsplit_kernel<Cfg, true, false>), grid, dim3(Cfg::NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((sgemm_wsplit_kernel<Cfg, true, true>), grid, dim3(Cfg::NT), 0, s, a);
+  return launch_status("sgemm_wsplit_kernel");
+}
+
 using Lean128x128 = conv::LeanCfg<128, 128, 32, 4, 2, 2>;
 using Lean128x64 = conv::LeanCfg<128, 64, 32, 2, 2, 3>;
 using Lean64x128 = conv::LeanCfg<64, 128, 32, 2, 2, 3>;
@@ -201,8 +339,20 @@ int launch_lean(const SgemmArgs& a0, int64_t batch, bool ta, bool tb, hipStream_
 }
 
 // Tile configurations: 0, 1 the general kernel (any K, alignment or size),
-// 2..5 lean (see sgemm_lean_kernel for their requirements).
-enum SgemmCfg { kG128 = 0, kG64, kL128x128, kL128x64, kL64x128, kL64x64, kNumSgemmCfg };
+// 2..5 lean (see sgemm_lean_kernel for their requirements), 6..8 wave-split
+// (32x32 with 4 or 8 waves, 32x64 with 4; the lean tiles' requirements).
+enum SgemmCfg {
+  kG128 = 0,
+  kG64,
+  kL128x128,
+  kL128x64,
+  kL64x128,
+  kL64x64,
+  kW32x32x4,
+  kW32x32x8,
+  kW32x64x4,
+  kNumSgemmCfg
+};
 
 int launch_sgemm(int cfg, const SgemmArgs& a, int64_t batch, bool ta, bool tb, bool va, bool vb, hipStream_t s) {
   switch (cfg) {
@@ -211,7 +361,10 @@ int launch_sgemm(int cfg, const SgemmArgs& a, int64_t batch, bool ta, bool tb, b
     case kL128x128: return launch_lean<Lean128x128>(a, batch, ta, tb, s);
     case kL128x64: return launch_lean<Lean128x64>(a, batch, ta, tb, s);
     case kL64x128: return launch_lean<Lean64x128>(a, batch, ta, tb, s);
-    default: return launch_lean<Lean64x64>(a, batch, ta, tb, s);
+    case kL64x64: return launch_lean<Lean64x64>(a, batch, ta, tb, s);
+    case kW32x32x4: return launch_wsplit<conv::WsCfg<1, 1, 4>>(a, batch, ta, tb, s);
+    case kW32x32x8: return launch_wsplit<conv::WsCfg<1, 1, 8>>(a, batch, ta, tb, s);
+    default: return launch_wsplit<conv::WsCfg<1, 2, 4>>(a, batch, ta, tb, s);
   }
 }
 
@@ -307,8 +460,10 @@ int sgemm_impl(int32_t transA, int32_t transB, int64_t M, int64_t N, int64_t K, 
   if (tune) {
     // First call for this shape: time every valid configuration as a graph
     // replay (time_graph), writing a scratch copy of C so the caller's C is
-    // untouched (beta != 0 reads it).  Every non-split configuration sums k
-    // in the same order, so the choice does not change the results.
+    // untouched (beta != 0 reads it).  Every whole-K configuration sums k in
+    // the same order; the wave-split tiles (timed only where the 64x64 tiles
+    // number under two per CU) sum per-wave partials, so their pick can
+    // change the last bits (the deterministic mode never times them).
     const size_t cBytesAll = static_cast<size_t>((batch - 1) * strideC + cElems) * 4;
     void* scratch = nullptr;
     if (int st = hip_status(hipStreamSynchronize(cx->stream), "hipStreamSynchronize")) return st;
@@ -318,8 +473,10 @@ int sgemm_impl(int32_t transA, int32_t transB, int64_t M, int64_t N, int64_t K, 
       float bestMs = 1e30f;
       int bestCfg = cfg;
       int st = TNH_OK;
+      const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * batch;
       for (int c = 0; c < kNumSgemmCfg && !st; ++c) {
         if (c >= kL128x128 && !lean) continue;
+        if (c >= kW32x32x4 && tiles64 >= 2 * static_cast<int64_t>(cx->cu_count)) continue;
         float ms = 0.f;
         st = time_graph(cx, [&](hipStream_t s) { return launch_sgemm(c, t, batch, ta, tb, va, vb, s); }, 3, ms);
         if (!st && ms < bestMs) bestMs = ms, bestCfg = c;

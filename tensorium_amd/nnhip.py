@@ -44,8 +44,9 @@ CONV_WSPLIT_CFGS = range(20, 27)
 CONV_SPLIT_UNIT = 64
 CONV_TAIL_BASE = 16
 CONV_TAIL_SLOT_BASE = 32
-# SGEMM tile configurations (tnh_sgemm_set_autotune): 0, 1 general, 2..5 lean
-NUM_SGEMM_CFGS = 6
+# SGEMM tile configurations (tnh_sgemm_set_autotune): 0, 1 general, 2..5 lean,
+# 6..8 wave-split
+NUM_SGEMM_CFGS = 9
 
 i32, i64, f32, vp = C.c_int32, C.c_int64, C.c_float, C.c_void_p
 
