@@ -385,8 +385,10 @@ def extra_train(hip, steps, warmup, cpu_steps):
     return out
 
 
-def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
-    """Config 5: YOLOv3-608 inference at batch 32 (HIP graph replay)."""
+def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608, name="YOLOv3"):
+    """Config 5: YOLOv3-608 inference at batch 32 (HIP graph replay); also
+    YOLOv3-tiny-416 at batch 16 (channels-last with maxpools and a
+    16-channel convolution input)."""
     import torch
 
     from tensorium_amd import darknet, synth
@@ -399,7 +401,7 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608):
     flop = darknet.conv_flops(layers608) * batch
     del net, x
     torch.cuda.empty_cache()
-    return {"workload": f"YOLOv3-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
+    return {"workload": f"{name}-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
             "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
 
 
@@ -594,9 +596,10 @@ def main():
                          "channels-last")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the other BASELINE configurations (single conv, SGEMM sweep, training step, "
-                         "YOLOv3-608 batch 32)")
+                         "YOLOv3-608 batch 32) and the YOLOv3-tiny / detection / bandwidth figures")
     ap.add_argument("--only", choices=("single_conv_416", "sgemm", "train_cifar_b128", "yolov3_608_b32",
-                                       "yolo_detect_nms_b16", "bandwidth", "batch1"), default=None,
+                                       "yolo_detect_nms_b16", "bandwidth", "batch1", "yolov3_tiny_416_b16"),
+                    default=None,
                     help="run one secondary configuration alone and print its figures (for profiling runs)")
     ap.add_argument("--counter-pass", action="store_true",
                     help="for rocprofv3 --pmc: tune, then run ONE eager forward and a 64 MiB copy "
@@ -629,6 +632,7 @@ def main():
         counter_pass(hip, darknet.Network(hip, layers, args.batch, weights, layout=layout_for(args.batch)), args)
         return
     if args.only:
+        tiny = darknet.load_cfg("yolov3-tiny.cfg")[1]
         only = {
             "single_conv_416": lambda: extra_single_conv(hip),
             "sgemm": lambda: extra_sgemm(hip),
@@ -638,6 +642,8 @@ def main():
             "yolo_detect_nms_b16": lambda: extra_detect(hip, layers, weights),
             "bandwidth": lambda: extra_bandwidth(hip),
             "batch1": lambda: extra_batch1(hip, layers, weights, args.steps, args.warmup),
+            "yolov3_tiny_416_b16": lambda: extra_yolo(hip, tiny, darknet.synthetic_weights(tiny), args.steps,
+                                                      args.warmup, batch=16, size=416, name="YOLOv3-tiny"),
         }[args.only]
         print(json.dumps({args.only: only()}), flush=True)
         return
@@ -703,6 +709,9 @@ def main():
         guarded("train_cifar_b128", lambda: extra_train(hip, 50, 2, 0 if args.no_cpu_baseline else 2))
         _, l608 = darknet.load_cfg("yolov3.cfg", 608, 608)
         guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2))
+        _, ltiny = darknet.load_cfg("yolov3-tiny.cfg")
+        guarded("yolov3_tiny_416_b16", lambda: extra_yolo(hip, ltiny, darknet.synthetic_weights(ltiny), 20, 3,
+                                                          batch=16, size=416, name="YOLOv3-tiny"))
         guarded("yolo_detect_nms_b16", lambda: extra_detect(hip, layers, weights))
         guarded("bandwidth", lambda: extra_bandwidth(hip))
 
