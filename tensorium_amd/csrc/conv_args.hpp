@@ -145,8 +145,14 @@ __device__ inline void conv_store(const ConvArgs& a, const f32x16 (&acc)[FM][FN]
   }
 }
 
+// Output stores of the conv and GEMM epilogues: system-scope (sc0 sc1), so
+// they write through the XCD's L2 as the tiles finish instead of staying
+// dirty there until the end-of-kernel release writes the whole output back
+// at once (measured on YOLOv3-416 batch 16: 8.81-8.82 -> 8.73 ms; device
+// scope alone: 8.75).
+constexpr int kStoreThrough = 17;  // buffer cache-policy bits: sc0 | sc1
 __device__ inline void buf_st1s(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, kStoreThrough);
 }
 
 // conv_store through buffer instructions (same results): each lane's

@@ -32,7 +32,7 @@ namespace conv {
 namespace {
 
 __device__ inline void st1(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, 0, kStoreThrough);
 }
 
 // One wave's channels-last 3x3 tap gather rows (output pixels m0 ..
