@@ -618,16 +618,23 @@ __device__ inline int piece_quad(int wave, int lane, int i, int j, int q) {
   return (((wave * Cfg::FM * Cfg::FN + i * Cfg::FN + j) * 4 + q) * 64 + lane) * 4;
 }
 
+// Pieces are written through (kStoreThrough), like the epilogue's outputs:
+// they are written in the last round and would otherwise stay dirty in L2
+// until the end-of-kernel release.
 template <class Cfg>
 __device__ inline void store_piece(float* dst, int wave, int lane, const f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(dst, static_cast<int64_t>(Cfg::BM) * Cfg::BN * 4);
 #pragma unroll
   for (int i = 0; i < Cfg::FM; ++i)
 #pragma unroll
     for (int j = 0; j < Cfg::FN; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<f32x4*>(dst + piece_quad<Cfg>(wave, lane, i, j, q)) =
-            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, v), r,
+                                               static_cast<uint32_t>(piece_quad<Cfg>(wave, lane, i, j, q)) * 4u, 0,
+                                               kStoreThrough);
+      }
 }
 
 template <class Cfg, int MODE, bool VB>
