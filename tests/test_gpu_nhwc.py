@@ -227,6 +227,34 @@ def test_conv_nhwc_forced_configs(hip, cfg, hi):
     assert np.array_equal(H(dout, hip).transpose(0, 3, 1, 2), ref)
 
 
+@pytest.mark.parametrize("cfg", [11, 12, 13, 16, 18])
+@pytest.mark.parametrize("tail", [CONV_TAIL_BASE + 3, CONV_TAIL_SLOT_BASE + 2])
+def test_conv_nhwc_tail_split_residual(hip, cfg, tail):
+    """Tail splits with a fused residual read from a channel slice (the
+    reduction launch loads the residual with the pieces) on integer data:
+    exact, and the rest of the output buffer untouched."""
+    B, Cc, Hh, F, k = 4, 64, 52, 96, 3
+    case(f"conv nhwc tail-split residual cfg{cfg} hi{tail}")
+    rng = np.random.default_rng(cfg * 13 + tail)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    res = rng.integers(-5, 6, (B, F, Hh, Hh)).astype(np.float32)
+    ref = R.addvv(R.conv_forward(x, Wt, b, k, 1, 1, acLEAKY), res).reshape(B, F, Hh, Hh)
+    rin = np.zeros((B, Hh, Hh, F + 8), np.float32)
+    rin[..., 8:] = nhwc(res)
+    dout = D(np.full((B, Hh, Hh, F + 4), 7.0, np.float32))
+    hip.setConvAutotune(True, cfg + CONV_SPLIT_UNIT * tail)
+    try:
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, 1, 1, D(nhwc(x)), 0, D(tap_major(Wt, F, Cc, k)), D(b), acLEAKY,
+                              dout, 4, outPix=F + 4, residual=D(rin), resOffset=8, resPix=F + 8)
+    finally:
+        hip.setConvAutotune(True, -1)
+    got = H(dout, hip)
+    assert np.array_equal(got[..., 4:].transpose(0, 3, 1, 2), ref)
+    assert np.all(got[..., :4] == 7.0)
+
+
 # (B, C, H, F, k, stride, pad, residual): ragged pixel and filter counts (not
 # multiples of the 32/64 tile), stride 2, 1x1 with one group per wave (K = 32
 # over up to 16 waves: some waves get no group), and YOLOv3's 13x13 batch-1
