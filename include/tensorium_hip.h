@@ -287,8 +287,10 @@ int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
 /* No reference counterpart: enable (1, default) or disable per-shape
  * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape:
  * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 6..10
- * register-direct, 11..19 lean software-pipelined; a shape invalid for the
- * call falls back to the library's choice) and forcedConfig / 64 either the
+ * register-direct, 11..19 lean software-pipelined, 20..26 wave-split: K of
+ * one tile split over the waves of its workgroup, for 3x3 tap-major or 1x1
+ * layers with C % 32 == 0; a shape invalid for the call falls back to the
+ * library's choice) and forcedConfig / 64 either the
  * split-K factor (0 or 1: none; up to 16) or a tail split (lean shapes only:
  * the tiles beyond the last whole round are cut into K pieces, summed in K
  * order by a second kernel): 18..31 = forcedConfig / 64 - 16 pieces with

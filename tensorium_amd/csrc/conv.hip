@@ -572,7 +572,7 @@ using Lean17 = LeanCfg<128, 64, 32, 4, 2, 2>;
 using Lean18 = LeanCfg<64, 128, 32, 2, 4, 2>;
 using Lean19 = LeanCfg<128, 128, 32, 4, 2, 2>;
 
-// wave-split channels-last tiles (conv_wsplit.hip: K of one tile split over
+// wave-split tiles, both layouts (conv_wsplit.hip: K of one tile split over
 // the waves of its workgroup), ids kWsFirst + index into kWsCfgs
 constexpr int kWsFirst = 20;
 
@@ -890,7 +890,10 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, int cus, hipS
     case 16: return launch_lean<Lean16>(a, mode, vb, cus, s);
     case 17: return launch_lean<Lean17>(a, mode, vb, cus, s);
     case 18: return launch_lean<Lean18>(a, mode, vb, cus, s);
-    default: return launch_lean<Lean19>(a, mode, vb, cus, s);
+    case 19: return launch_lean<Lean19>(a, mode, vb, cus, s);
+    default:
+      if (cfg >= kWsFirst && cfg < kNumCfg) return launch_wsplit_nchw(cfg - kWsFirst, a, mode, vb, s);
+      return fail(TNH_ERR_UNSUPPORTED, "conv2d: tile configuration %d (0..%d)", cfg, kNumCfg - 1);
   }
 }
 
@@ -960,10 +963,11 @@ bool g_autotune = true;
 int g_forced_cfg = -1;
 
 // The register-direct kernels need whole 16-channel chunks inside one tap
-// and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va).
+// and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va); the
+// wave-split tiles whole 32-channel panels inside one tap.
 bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = false) {
   if (nhwc) return (kCfgs[c].kind == kLean || kCfgs[c].kind == kWsplit) && smallIO && va && C % kCfgs[c].BK == 0;
-  if (kCfgs[c].kind == kWsplit) return false;  // channels-last only
+  if (kCfgs[c].kind == kWsplit) return (mode == kTap3 || mode == k1x1) && va && smallIO && C % 32 == 0;
   if (kCfgs[c].kind == kLean && !smallIO) return false;
   if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
   if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;

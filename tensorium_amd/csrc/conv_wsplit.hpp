@@ -1,13 +1,13 @@
-// Channels-last convolution with K split over the waves of a workgroup
-// (conv_wsplit.hip): the tile shapes and the launch entry the tuner in
-// conv.hip calls.
+// Convolution with K split over the waves of a workgroup (conv_wsplit.hip):
+// the tile shapes and the launch entries the tuner in conv.hip calls.
 #pragma once
 #include "conv_args.hpp"
 
 namespace tnh {
 namespace conv {
 
-// One workgroup computes a (32*FM) pixels x (32*FN) filters tile with W
+// One workgroup computes a (32*FM) x (32*FN) tile (channels-last: pixels x
+// filters; NCHW: filters x pixels) with W
 // waves; wave w accumulates panels [w*P/W, (w+1)*P/W) of the P = K/32
 // panels of 32 k through its own LDS panel, then the W partial tiles are
 // summed through LDS in wave order.
@@ -56,6 +56,12 @@ constexpr WsInfo kWsCfgs[kNumWs] = {{32, 32, 4}, {32, 32, 8}, {32, 64, 4}, {16, 
 // whose ConvArgs are filled as for conv_nhwc_kernel (mode kTap3 or k1x1;
 // C % 32 == 0; out and residual within 2 GiB).
 int launch_wsplit_nhwc(int ws, ConvArgs a, int mode, hipStream_t s);
+
+// The same tiles for an NCHW convolution whose ConvArgs are filled as for
+// conv_lean_kernel (mode kTap3 with tap-major weights, or k1x1; C % 32 == 0;
+// out and residual within 2 GiB); vb: the 1x1 input may be read as 16-byte
+// pixel vectors (16-byte aligned, HW and the batch stride multiples of 4).
+int launch_wsplit_nchw(int ws, ConvArgs a, int mode, bool vb, hipStream_t s);
 
 }  // namespace conv
 }  // namespace tnh

@@ -31,14 +31,15 @@ acLOGISTIC, acLINEAR, acLEAKY = 0, 4, 9
 WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 # number of compiled conv tile configurations (tnh_conv2d_set_autotune ids
 # 0..NUM_CONV_CFGS-1: 0-5 LDS-staged, 6-10 register-direct, 11-19 lean
-# software-pipelined, 20-26 wave-split channels-last); the first
-# NUM_CONV_NCHW_CFGS serve tnh_conv2d_fwd; a forced id is
+# software-pipelined, 20-26 wave-split); the first NUM_CONV_NCHW_CFGS serve
+# tnh_conv2d_fwd, CONV_LEAN_CFGS and CONV_WSPLIT_CFGS
+# tnh_conv2d_fwd_nhwc; a forced id is
 # tile + CONV_SPLIT_UNIT * splits (uniform split-K, up to 16), or, for a lean
 # tile, tile + CONV_SPLIT_UNIT * (base + pieces) (tail split; base
 # CONV_TAIL_BASE: rounds of one tile per CU, CONV_TAIL_SLOT_BASE: rounds of
 # one tile per resident workgroup slot)
 NUM_CONV_CFGS = 27
-NUM_CONV_NCHW_CFGS = 20
+NUM_CONV_NCHW_CFGS = 27
 CONV_LEAN_CFGS = range(11, 20)
 CONV_WSPLIT_CFGS = range(20, 27)
 CONV_SPLIT_UNIT = 64

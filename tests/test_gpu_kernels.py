@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, NUM_CONV_NCHW_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, CONV_WSPLIT_CFGS, NUM_CONV_NCHW_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -336,6 +336,66 @@ def test_conv_packed_every_config(hip, cfg, B, Cc, Hh, F, k, s, p, act):
     finally:
         hip.setConvAutotune(True, -1)
     assert R.rel_err(got, ref) <= TOL
+
+
+# (B, C, H, F, k, stride, residual): ragged pixel and filter counts, stride 2,
+# 1x1 with HW % 4 != 0 (scalar pixel loads) and == 0 (16-byte pixel
+# vectors), K = 32 over up to 8 waves (some waves get no panel), and
+# YOLOv3's 13x13 batch-1 3x3 shape
+WSPLIT_NCHW_SHAPES = [
+    (1, 64, 13, 96, 3, 1, True),
+    (2, 32, 10, 40, 3, 2, False),
+    (1, 32, 9, 70, 1, 1, True),
+    (3, 96, 8, 33, 1, 1, False),
+    (2, 64, 12, 40, 1, 1, True),
+    (1, 512, 13, 1024, 3, 1, False),
+]
+
+
+@pytest.mark.parametrize("cfg", CONV_WSPLIT_CFGS)
+@pytest.mark.parametrize("shape", WSPLIT_NCHW_SHAPES)
+def test_conv_nchw_wsplit_integer(hip, cfg, shape):
+    """Every wave-split tile through tnh_conv2d_fwd (rows = filters, columns =
+    output pixels) on integer data, so every partial sum is exact and the
+    result equals the oracle bit for bit; input, output and residual at
+    offsets with batch strides wider than one image (route slices), the
+    rest of the output untouched."""
+    B, Cc, Hh, F, k, s, with_res = shape
+    p = k // 2
+    case(f"conv nchw wsplit cfg{cfg} {shape}")
+    OH = (Hh + 2 * p - k) // s + 1
+    rng = np.random.default_rng(cfg * 1000 + Cc + F)
+    x = rng.integers(-3, 4, (B, Cc, Hh, Hh)).astype(np.float32)
+    Wt = rng.integers(-2, 3, (F, Cc * k * k)).astype(np.float32)
+    b = rng.integers(-5, 6, F).astype(np.float32)
+    ref = R.conv_forward(x, Wt, b, k, s, p, acLEAKY)
+    xs, os_, rs = Cc * Hh * Hh + 12, F * OH * OH + 20, F * OH * OH + 8
+    xin = np.zeros(8 + B * xs, np.float32)
+    for i in range(B):
+        xin[8 + i * xs:8 + i * xs + Cc * Hh * Hh] = x[i].ravel()
+    res = rin = None
+    if with_res:
+        res = rng.integers(-5, 6, (B, F, OH, OH)).astype(np.float32)
+        ref = R.addvv(ref, res)
+        rin = np.zeros(4 + B * rs, np.float32)
+        for i in range(B):
+            rin[4 + i * rs:4 + i * rs + F * OH * OH] = res[i].ravel()
+    dout = D(np.full(16 + B * os_, 7.0, np.float32))
+    wt = Wt.reshape(F, Cc, k, k).transpose(0, 2, 3, 1).reshape(F, -1) if k > 1 else Wt
+    hip.setConvAutotune(True, cfg)
+    try:
+        hip.conv2dForward(B, Cc, Hh, Hh, F, k, s, p, D(xin), 8, D(np.ascontiguousarray(wt)), D(b), acLEAKY, dout, 16,
+                          inBatchStride=xs, outBatchStride=os_, residual=None if rin is None else D(rin),
+                          resOffset=4, resBatchStride=rs, weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
+    finally:
+        hip.setConvAutotune(True, -1)
+    got = H(dout, hip)
+    mask = np.ones(got.shape, bool)
+    for i in range(B):
+        seg = got[16 + i * os_:16 + i * os_ + F * OH * OH].reshape(F, OH, OH)
+        assert np.array_equal(seg, ref[i]), f"image {i}"
+        mask[16 + i * os_:16 + i * os_ + F * OH * OH] = False
+    assert np.all(got[mask] == 7.0)
 
 
 @pytest.mark.parametrize("B,Cc,Hh,F,s,tap,act,resid", [(1, 3, 416, 16, 1, False, acLEAKY, False),
