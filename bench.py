@@ -516,6 +516,81 @@ def extra_bandwidth(hip):
     return {"copy_gb_s": round(copy_gbs, 1), "kernels": out}
 
 
+# YOLOv3-416 layer shapes at batch 16 (label, C, H, F, k, stride)
+IM2COL_VS_FUSED = (("416->208 3x3 s2", 32, 416, 64, 3, 2), ("104x104 3x3", 64, 104, 128, 3, 1),
+                   ("52x52 3x3", 128, 52, 256, 3, 1), ("26x26 3x3", 256, 26, 512, 3, 1),
+                   ("13x13 3x3", 512, 13, 1024, 3, 1), ("52x52 1x1", 256, 52, 128, 1, 1))
+
+
+def extra_im2col_vs_fused(hip, batch=16):
+    """The two ways to run a conv layer on the GPU, on YOLOv3-416 layer shapes
+    at batch 16 (NCHW, leaky): (a) the sequence of TConvolutionalLayer's GPU
+    forward (nConvolutionLayer.pas:1047-1097) as separate launches -- im2col
+    of every image into a materialised column matrix (one batched launch
+    here; a 1x1 stride-1 layer skips it and reads the input directly), one
+    gemmStridedBatched W x col_b, forwardBias, then the activation -- and (b)
+    the implicit-GEMM conv (tnh_conv2d_fwd: the gather inside the GEMM's
+    operand loader, bias and leaky in its epilogue).  Each is timed as a
+    graph replay after an eager (tuning) call."""
+    import torch
+
+    from tensorium_amd import synth
+    from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, acLEAKY
+
+    out = []
+    for label, C, H, F, k, s in IM2COL_VS_FUSED:
+        p = k // 2
+        OH = (H + 2 * p - k) // s + 1
+        HW, K = OH * OH, C * k * k
+        x = torch.from_numpy(synth.uniform(11, (batch, C, H, H))).cuda()
+        w = torch.from_numpy(synth.normal(12, (F, K), (2.0 / K) ** 0.5)).cuda()
+        wt = torch.empty_like(w)
+        hip.packConvWeights(F, C, k, w, wt)
+        b = torch.from_numpy(synth.normal(13, (F,), 0.1)).cuda()
+        y = torch.empty((batch, F, OH, OH), dtype=torch.float32, device="cuda")
+        col = torch.empty(batch * K * HW, dtype=torch.float32, device="cuda") if k > 1 else None
+        torch.cuda.synchronize()
+
+        def fused():
+            hip.conv2dForward(batch, C, H, H, F, k, s, p, x, 0, wt if k > 1 else w, b, acLEAKY, y, 0,
+                              weightLayout=WEIGHTS_TAP_MAJOR if k > 1 else 0)
+
+        def im2col():
+            hip.im2colStridedBatched(C, H, H, k, k, p, p, s, s, 1, 1, x, C * H * H, 0, col, K * HW, 0, batch)
+
+        def gemm():
+            src, stride = (col, K * HW) if k > 1 else (x, C * H * H)
+            hip.gemmStridedBatched(False, False, F, HW, K, 1.0, w, 0, K, 0, src, 0, HW, stride, 0.0, y, 0, HW,
+                                   F * HW, batch)
+
+        def epilogue():
+            hip.forwardBias(batch * F * HW, y, 0, F, b, 1, batch)
+            hip.ActivateArray(batch * F * HW, y, 0, acLEAKY)
+
+        def sequence():
+            if k > 1:
+                im2col()
+            gemm()
+            epilogue()
+
+        for f in (fused, sequence):
+            f()
+        t_fused = time_graph(hip, fused, 10)
+        t_seq = time_graph(hip, sequence, 10)
+        t_i2c = time_graph(hip, im2col, 10) if k > 1 else 0.0
+        t_gemm = time_graph(hip, gemm, 10)
+        t_epi = time_graph(hip, epilogue, 10)
+        flop = 2.0 * batch * F * HW * K
+        out.append({"layer": f"{label} C{C}->F{F} B{batch}", "fused_us": round(t_fused * 1e3, 1),
+                    "sequence_us": round(t_seq * 1e3, 1), "im2col_us": round(t_i2c * 1e3, 1),
+                    "gemm_us": round(t_gemm * 1e3, 1), "bias_act_us": round(t_epi * 1e3, 1),
+                    "fused_tflops": round(flop / t_fused / 1e9, 1), "speedup": round(t_seq / t_fused, 3)})
+        del x, w, wt, b, y, col
+        torch.cuda.empty_cache()
+    return {"workload": "YOLOv3-416 conv layers at batch 16, NCHW: implicit GEMM against im2col + SGEMM + "
+                        "bias + leaky", "layers": out}
+
+
 def extra_detect(hip, layers, weights, batch=16, thresh=0.5, nms=0.45):
     """YOLO detection list + per-class NMS on the device (the reference's
     TNNet.Detections, nnet.pas:584, and doNMSSort, ntypes.pas:1612) after a YOLOv3-416
@@ -598,7 +673,8 @@ def main():
                     help="skip the other BASELINE configurations (single conv, SGEMM sweep, training step, "
                          "YOLOv3-608 batch 32) and the YOLOv3-tiny / detection / bandwidth figures")
     ap.add_argument("--only", choices=("single_conv_416", "sgemm", "train_cifar_b128", "yolov3_608_b32",
-                                       "yolo_detect_nms_b16", "bandwidth", "batch1", "yolov3_tiny_416_b16"),
+                                       "yolo_detect_nms_b16", "bandwidth", "batch1", "yolov3_tiny_416_b16",
+                                       "im2col_vs_fused"),
                     default=None,
                     help="run one secondary configuration alone and print its figures (for profiling runs)")
     ap.add_argument("--counter-pass", action="store_true",
@@ -641,6 +717,7 @@ def main():
                                                  args.steps, args.warmup),
             "yolo_detect_nms_b16": lambda: extra_detect(hip, layers, weights),
             "bandwidth": lambda: extra_bandwidth(hip),
+            "im2col_vs_fused": lambda: extra_im2col_vs_fused(hip),
             "batch1": lambda: extra_batch1(hip, layers, weights, args.steps, args.warmup),
             "yolov3_tiny_416_b16": lambda: extra_yolo(hip, tiny, darknet.synthetic_weights(tiny), args.steps,
                                                       args.warmup, batch=16, size=416, name="YOLOv3-tiny"),
@@ -714,6 +791,7 @@ def main():
                                                           batch=16, size=416, name="YOLOv3-tiny"))
         guarded("yolo_detect_nms_b16", lambda: extra_detect(hip, layers, weights))
         guarded("bandwidth", lambda: extra_bandwidth(hip))
+        guarded("im2col_vs_fused", lambda: extra_im2col_vs_fused(hip))
 
     out = {
         "metric": METRIC,
