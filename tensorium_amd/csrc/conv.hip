@@ -801,14 +801,23 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
   } else {
     a.tailSplits = 0;
   }
-  if (mode == kTap3)
-    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3>), dim3(static_cast<unsigned>(grid)), dim3(Cfg::NT), 0, s, a);
+  const bool var = a.upS > 0 || a.yolo;  // epilogue variant: its own instantiations
+  const dim3 g(static_cast<unsigned>(grid)), nt(Cfg::NT);
+  if (mode == kTap3 && var)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3, true>), g, nt, 0, s, a);
+  else if (mode == kTap3)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3>), g, nt, 0, s, a);
+  else if (var)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1, true>), g, nt, 0, s, a);
   else
-    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1>), dim3(static_cast<unsigned>(grid)), dim3(Cfg::NT), 0, s, a);
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1>), g, nt, 0, s, a);
   if (int st = launch_status("conv_nhwc_kernel")) return st;
   if (a.tailSplits > 0) {
-    hipLaunchKernelGGL((conv_tail_reduce<Cfg, true>), dim3(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64))),
-                       dim3(64), 0, s, a);
+    const dim3 rg(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64)));
+    if (var)
+      hipLaunchKernelGGL((conv_tail_reduce<Cfg, true, true>), rg, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL((conv_tail_reduce<Cfg, true>), rg, dim3(64), 0, s, a);
     return launch_status("conv_tail_reduce");
   }
   return TNH_OK;
@@ -828,8 +837,13 @@ int launch_nhwc_any_cfg(ConvArgs a, int mode, hipStream_t s) {
   a.kChunk = a.g.K;
   a.tailSplits = 0;
   const dim3 grid(static_cast<unsigned>(tm * tn));
-  if (mode == kTap3Any)
+  const bool var = a.upS > 0 || a.yolo;
+  if (mode == kTap3Any && var)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3Any, true>), grid, dim3(Cfg::NT), 0, s, a);
+  else if (mode == kTap3Any)
     hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, kTap3Any>), grid, dim3(Cfg::NT), 0, s, a);
+  else if (var)
+    hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1Any, true>), grid, dim3(Cfg::NT), 0, s, a);
   else
     hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1Any>), grid, dim3(Cfg::NT), 0, s, a);
   return launch_status("conv_nhwc_kernel");
@@ -1248,6 +1262,8 @@ int conv_nhwc_entry(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, i
   if (epi.yolo) {
     a.yolo = epi.yolo;
     a.yoloEntries = static_cast<int>(epi.yoloClasses + 5);
+    a.yoloBytes = N * F * 4 <= kMaxBufBytes ? N * F * 4 : 0;
+    a.yoloVec = (OH * OW) % 4 == 0 && aligned16(epi.yolo);
   }
   // The network's first layer: on the matrix cores from about 32 blocks of
   // 32 pixels per CU (YOLOv3-416 from batch 2: measured 23.7 against 25.0 us

@@ -53,6 +53,11 @@ struct ConvArgs {
   float upScale;
   float* yolo;
   int yoloEntries;
+  // yolo head extent in bytes when it lies within 2 GiB (0: per-element
+  // stores), and whether 4 consecutive pixels of one channel are one aligned
+  // 16-byte vector there (OH*OW % 4 == 0, 16-byte aligned head)
+  int64_t yoloBytes;
+  int yoloVec;
 };
 
 // K walk / B operand of a convolution kernel
@@ -292,8 +297,8 @@ __device__ inline void store_nhwc_variant(const ConvArgs& a, __amdgpu_buffer_rsr
 // with resPix).  Each lane owns FN filter columns (bias per lane); the pixel
 // part of an offset is wave-uniform (scalar operand).  Residual loads are all
 // issued before the first store; out-of-range elements get kOOB.
-template <int FM, int FN>
-__device__ inline void conv_store_nhwc(const ConvArgs& a, const f32x16 (&acc)[FM][FN], int64_t m0w, int64_t n0w,
+template <int FM, int FN, bool VAR = false>
+__device__ __attribute__((always_inline)) inline void conv_store_nhwc(const ConvArgs& a, const f32x16 (&acc)[FM][FN], int64_t m0w, int64_t n0w,
                                        int lane) {
   const int h = lane >> 5;
   const int64_t M = a.g.N;
@@ -314,24 +319,70 @@ __device__ inline void conv_store_nhwc(const ConvArgs& a, const f32x16 (&acc)[FM
     vRes[j] = sel_off(okF, static_cast<uint32_t>(rowBase) * rp4 + static_cast<uint32_t>(f) * 4u);
   }
   auto rc = [](int i, int r) { return i * 32 + 8 * (r >> 2) + (r & 3); };
-  if (a.upS > 0 || a.yolo) {  // epilogue variants: generic per-element stores
-    const __amdgpu_buffer_rsrc_t resG = make_rsrc(a.res, a.resBytes);
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
+  if constexpr (VAR) {  // epilogue variants (a.upS > 0 or a.yolo): their own kernel instantiations
+    if (a.yolo && a.upS == 0 && a.yoloBytes > 0 && !a.res) {
+      // A yolo head: the plain stores of `out` and the NCHW head
+      // yolo[(b*F + f)*OHW + p].  Registers 4g .. 4g+3 of a lane hold 4
+      // consecutive pixels of its filter, so with yoloVec they are one 16-byte
+      // store into the head (lanes l and l + 32 fill 32 consecutive bytes, the
+      // four groups g a 128-byte line); else 4 single stores.
+      const uint32_t OHW = static_cast<uint32_t>(a.g.OHW), F32 = static_cast<uint32_t>(a.F);
+      const __amdgpu_buffer_rsrc_t yR = make_rsrc(a.yolo, a.yoloBytes);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int64_t f = n0w + j * 32 + (lane & 31);
+        const bool okF = f < a.F;
+        const uint32_t fu = okF ? static_cast<uint32_t>(f) : 0u;
+        const int entry = static_cast<int>(fu % static_cast<uint32_t>(a.yoloEntries));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = rowBase + rc(i, r);
-          if (f >= a.F || m >= M) continue;
-          float v = acc[i][j][r] + bias[j];
-          v = apply_act(v, a.act);
-          if (a.res) v = v + buf_ld1s(resG, static_cast<uint32_t>((m * a.resPix + f) * 4), 0);
-          store_nhwc_variant(a, outR, m, f, v);
-        }
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int c0 = i * 32 + 8 * g;  // row of register 4g, relative to rowBase
+            float v[4], y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v[e] = apply_act(acc[i][j][4 * g + e] + bias[j], a.act);
+              y[e] = yolo_entry(v[e], entry);
+              buf_st1s(outR, v[e], rowOk(c0 + e) ? vOut[j] : kOOB, static_cast<uint32_t>(c0 + e) * op4);
+            }
+            const uint32_t m = static_cast<uint32_t>(rowBase + c0);
+            if (a.yoloVec) {  // m % 4 == 0 and M % 4 == 0: the 4 pixels are in range together, in one image
+              const uint32_t b = m / OHW, px = m - b * OHW;
+              const uint32_t off = sel_off(okF && rowOk(c0), ((b * F32 + fu) * OHW + px) * 4u);
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, f32x4{y[0], y[1], y[2], y[3]}), yR,
+                  off, 0, kStoreThrough);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t b = (m + e) / OHW, px = m + e - b * OHW;
+                buf_st1s(yR, y[e], sel_off(okF && rowOk(c0 + e), ((b * F32 + fu) * OHW + px) * 4u), 0);
+              }
+            }
+          }
       }
-    return;
+      return;
+    }
+    if (a.upS > 0 || a.yolo) {  // epilogue variants: generic per-element stores
+      const __amdgpu_buffer_rsrc_t resG = make_rsrc(a.res, a.resBytes);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int64_t f = n0w + j * 32 + (lane & 31);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t m = rowBase + rc(i, r);
+            if (f >= a.F || m >= M) continue;
+            float v = acc[i][j][r] + bias[j];
+            v = apply_act(v, a.act);
+            if (a.res) v = v + buf_ld1s(resG, static_cast<uint32_t>((m * a.resPix + f) * 4), 0);
+            store_nhwc_variant(a, outR, m, f, v);
+          }
+        }
+      return;
+    }
   }
   auto finish = [&](auto actTag, auto resTag) {
     constexpr int ACT = decltype(actTag)::value;

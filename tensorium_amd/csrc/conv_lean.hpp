@@ -678,7 +678,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
 // pieces in K order (piece 0 first, as conv_splitk_reduce does) into the
 // accumulator registers the conv kernel would have held, then applies the
 // conv kernel's own epilogue.
-template <class Cfg, bool NHWC = false>
+template <class Cfg, bool NHWC = false, bool VAR = false>
 __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
   // one single-wave workgroup per wave of a tail tile: the reduction of a
   // few tail tiles still spreads over every CU
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   if constexpr (NHWC)
-    conv_store_nhwc<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+    conv_store_nhwc<Cfg::FM, Cfg::FN, VAR>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
   else
     conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
@@ -736,8 +736,9 @@ __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
 // writes 32 consecutive channels of a pixel per half-wave.  Tail split as in
 // conv_lean_kernel (nFull may be 0: every tile cut into K pieces).  The Any
 // modes (C % 32 != 0) take ceil(K / BK) panels with the K tail reading 0, and
-// no tail split.
-template <class Cfg, int MODE>
+// no tail split.  VAR: the instantiation for the epilogue variants (an
+// upsampled output or a yolo head; the plain kernels carry no code for them).
+template <class Cfg, int MODE, bool VAR = false>
 __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a) {
   constexpr bool ANY = MODE == kTap3Any || MODE == k1x1Any;
   constexpr bool TAP = MODE == kTap3 || MODE == kTap3Any;
@@ -782,7 +783,7 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a
     return;
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-  conv_store_nhwc<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
+  conv_store_nhwc<Cfg::FM, Cfg::FN, VAR>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
 
 }  // namespace conv

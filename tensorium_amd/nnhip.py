@@ -386,14 +386,14 @@ class TNNHip:
 
     def conv2dForwardNHWCYolo(self, batch, c, h, w, filters, kernelSize, stride, padding, input, inOffset, weights,
                               biases, activation, output, outOffset, n, classes, yoloOutput, inPix=None,
-                              outPix=None):
+                              outPix=None, yoloOffset=0):
         """Channels-last fused conv that also writes the yolo head (NCHW) of its
         result (tnh_conv2d_fwd_nhwc_yolo)."""
         xp = c if inPix is None else inPix
         op_ = filters if outPix is None else outPix
         call("tnh_conv2d_fwd_nhwc_yolo", batch, c, h, w, filters, kernelSize, kernelSize, padding, padding, stride,
              stride, addr(input), inOffset, xp, addr(weights), 0, addr(biases), 0, activation, addr(output), outOffset,
-             op_, n, classes, addr(yoloOutput), 0)
+             op_, n, classes, addr(yoloOutput), yoloOffset)
 
     @staticmethod
     def noAllocScratchBytes():

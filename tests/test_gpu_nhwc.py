@@ -369,32 +369,44 @@ def test_conv_nhwc_upsample_variant(hip, forced, k):
     assert R.rel_err(got[..., 24:24 + F].transpose(0, 3, 1, 2), ref) <= TOL
 
 
+# (H, k, head offset in floats): 13x13 (169 pixels, single head stores),
+# 26x26 (16-byte head stores), 26x26 with a head offset that is not 16-byte
+# aligned (single stores again), a 3x3 head
+YOLO_VARIANTS = [(13, 1, 0), (26, 1, 0), (26, 1, 1), (26, 3, 0)]
+
+
 @pytest.mark.parametrize("forced", EPI_TILINGS)
-def test_conv_nhwc_yolo_variant(hip, forced):
+@pytest.mark.parametrize("Hh,k,yoff", YOLO_VARIANTS)
+def test_conv_nhwc_yolo_variant(hip, forced, Hh, k, yoff):
     """tnh_conv2d_fwd_nhwc_yolo writes the same channels-last output as
     conv2dForwardNHWC and the same NCHW head as yoloForwardNHWC on it, bit
-    for bit (3 anchors x (5 + 80 classes) = 255 filters)."""
-    B, Cc, Hh, n, classes = 2, 128, 13, 3, 80
+    for bit (3 anchors x (5 + 80 classes) = 255 filters), and nothing
+    outside the head."""
+    B, Cc, n, classes = 2, 128, 3, 80
     F = n * (5 + classes)
-    case(f"conv nhwc yolo variant forced {forced}")
+    p = k // 2
+    case(f"conv nhwc yolo variant forced {forced} H{Hh} k{k} head offset {yoff}")
     x = synth.uniform(64, (B, Cc, Hh, Hh))
-    Wt = synth.normal(65, (F, Cc), (2.0 / Cc) ** 0.5)
+    Wt = synth.normal(65, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
     b = synth.normal(66, (F,), 0.1)
-    dx, dw, db = D(nhwc(x)), D(Wt), D(b)
+    dx, dw, db = D(nhwc(x)), D(tap_major(Wt, F, Cc, k)), D(b)
     out_f = torch.empty((B, Hh, Hh, F), dtype=torch.float32, device="cuda")
-    head_f = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
+    head_buf = D(np.full(yoff + B * F * Hh * Hh + 8, 7.0, np.float32))
     out_p = torch.empty_like(out_f)
-    head_p = torch.empty_like(head_f)
+    head_p = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
     hip.setConvAutotune(True, forced)
     try:
-        hip.conv2dForwardNHWCYolo(B, Cc, Hh, Hh, F, 1, 1, 0, dx, 0, dw, db, acLINEAR, out_f, 0, n, classes, head_f)
-        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, 1, 1, 0, dx, 0, dw, db, acLINEAR, out_p, 0)
+        hip.conv2dForwardNHWCYolo(B, Cc, Hh, Hh, F, k, 1, p, dx, 0, dw, db, acLINEAR, out_f, 0, n, classes, head_buf,
+                                  yoloOffset=yoff)
+        hip.conv2dForwardNHWC(B, Cc, Hh, Hh, F, k, 1, p, dx, 0, dw, db, acLINEAR, out_p, 0)
     finally:
         hip.setConvAutotune(True, -1)
     hip.yoloForwardNHWC(B, n, classes, Hh, Hh, out_p, 0, F, head_p)
     assert np.array_equal(H(out_f, hip), H(out_p, hip))
-    assert np.array_equal(H(head_f, hip), H(head_p, hip))
-    ref = R.conv_forward(x, Wt, b, 1, 1, 0, acLINEAR)
+    got = H(head_buf, hip)
+    assert np.array_equal(got[yoff:yoff + B * F * Hh * Hh].reshape(B, F, Hh, Hh), H(head_p, hip))
+    assert np.all(got[:yoff] == 7.0) and np.all(got[yoff + B * F * Hh * Hh:] == 7.0)
+    ref = R.conv_forward(x, Wt, b, k, 1, p, acLINEAR)
     assert R.rel_err(H(out_f, hip).transpose(0, 3, 1, 2), ref) <= TOL
 
 
