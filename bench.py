@@ -451,6 +451,9 @@ def extra_bandwidth(hip):
     ms = time_graph(hip, lambda: hip.copy(n, src, 0, 1, dst, 0, 1), 20)
     copy_gbs = 8.0 * n / ms / 1e6
     out.append(_bw_entry("copy 256 MiB", ms, 8.0 * n, None))
+    # writes only: the bound of a store-dominated kernel (the first conv layer)
+    ms = time_graph(hip, lambda: hip.fill(n, dst, 0, 0.5, 1), 20)
+    out.append(_bw_entry("fill 256 MiB (writes only)", ms, 4.0 * n, copy_gbs))
     del src, dst
 
     def im2col_case(label, B, C, H, k, p, s):

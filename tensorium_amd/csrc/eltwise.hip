@@ -221,6 +221,11 @@ __global__ void fill_kernel(int64_t n, float* x, float v, int64_t stride) {
   GRID_STRIDE(i, n) x[i * stride] = v;
 }
 
+// contiguous, 16-byte aligned, N % 4 == 0: one 16-byte store per element quad
+__global__ void fill4_kernel(int64_t n4, float4* x, float v) {
+  GRID_STRIDE(i, n4) x[i] = float4{v, v, v, v};
+}
+
 __global__ void copy_kernel(int64_t n, const float* s, int64_t is, float* d, int64_t id) {
   GRID_STRIDE(i, n) d[i * id] = s[i * is];
 }
@@ -418,7 +423,13 @@ extern "C" int32_t tnh_fill(int64_t N, float* x, int64_t offset, float val, int6
   TNH_ARG(N >= 0 && offset >= 0, "fill: bad size");
   if (N == 0) return TNH_OK;
   TNH_ARG(x != nullptr, "fill: NULL buffer");
-  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, N, x + offset, val, stride);
+  float* d = x + offset;
+  if (stride == 1 && N % 4 == 0 && al16(d)) {
+    hipLaunchKernelGGL(fill4_kernel, dim3(grid_for(N / 4)), dim3(kThreads), 0, cx->stream, N / 4,
+                       reinterpret_cast<float4*>(d), val);
+    return launch_status("fill4_kernel");
+  }
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(N)), dim3(kThreads), 0, cx->stream, N, d, val, stride);
   return launch_status("fill_kernel");
 }
 

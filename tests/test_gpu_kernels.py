@@ -753,6 +753,14 @@ def test_copy_fill_axpy_addvv_route(hip):
     hip.fill(500, dc, 1, 7.0, 2)
     got = H(dc, hip)
     assert np.all(got[1:1000:2] == 7.0)
+    # contiguous: 16-byte stores when aligned (offset 4), single ones when not
+    # (offset 1, and 998 elements); the elements around the range stay
+    for off, n in ((4, 992), (1, 996), (0, 998)):
+        hip.copy(1000, da, 0, 1, dc, 0, 1)
+        hip.fill(n, dc, off, -2.5, 1)
+        want = a.copy()
+        want[off:off + n] = -2.5
+        assert np.array_equal(H(dc, hip), want), (off, n)
     hip.copy(1000, da, 0, 1, dc, 0, 1)
     assert np.array_equal(H(dc, hip), a)
     hip.scale(1000, 3.0, dc, 1)
