@@ -42,7 +42,7 @@ PEAK_HBM = 8.0e12
 # WRITE_SIZE, KiB per dispatch, scaled by a 64 MiB copy: read = 2.0 x
 # FETCH_SIZE, write = 1.0 x WRITE_SIZE); profiles/yolov3_416_b16_conv_nhwc_kernel.md
 # holds the figures and the commands.  Other layouts / batches: null.
-TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 67508.2 + 39756.1) * 1024}
+TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 66843.1 + 39756.1) * 1024}
 
 
 def log(*a):
