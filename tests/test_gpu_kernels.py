@@ -398,6 +398,33 @@ def test_conv_nchw_wsplit_integer(hip, cfg, shape):
     assert np.all(got[mask] == 7.0)
 
 
+@pytest.mark.parametrize("cfg", CONV_WSPLIT_CFGS)
+@pytest.mark.parametrize("act", [acLEAKY, acLINEAR, acLOGISTIC])
+def test_conv_nchw_wsplit_vs_oracle(hip, cfg, act):
+    """Wave-split tiles through tnh_conv2d_fwd on YOLOv3's batch-1 26x26 3x3
+    layer (C 256 -> 512), random data: per tensor within 1e-5 of the oracle.
+    The fused logistic is TNNCuda's 1/(1 + exp(-x)) (cuda_sgemm.cu:305-309),
+    held against the float64 sigmoid of the oracle's linear output."""
+    B, Cc, Hh, F, k = 1, 256, 26, 512, 3
+    case(f"conv nchw wsplit cfg{cfg} act{act} vs oracle")
+    x = synth.uniform(95 + cfg, (B, Cc, Hh, Hh))
+    Wt = synth.normal(96, (F, Cc * k * k), (2.0 / (Cc * k * k)) ** 0.5)
+    b = synth.normal(97, (F,), 0.1)
+    if act == acLOGISTIC:
+        ref = 1.0 / (1.0 + np.exp(-R.conv_forward(x, Wt, b, k, 1, 1, acLINEAR).astype(np.float64)))
+    else:
+        ref = R.conv_forward(x, Wt, b, k, 1, 1, act)
+    wt = np.ascontiguousarray(Wt.reshape(F, Cc, k, k).transpose(0, 2, 3, 1).reshape(F, -1))
+    dout = torch.empty((B, F, Hh, Hh), dtype=torch.float32, device="cuda")
+    hip.setConvAutotune(True, cfg)
+    try:
+        hip.conv2dForward(B, Cc, Hh, Hh, F, k, 1, 1, D(x), 0, D(wt), D(b), act, dout, 0,
+                          weightLayout=WEIGHTS_TAP_MAJOR)
+    finally:
+        hip.setConvAutotune(True, -1)
+    assert R.rel_err(H(dout, hip), ref) <= TOL
+
+
 @pytest.mark.parametrize("B,Cc,Hh,F,s,tap,act,resid", [(1, 3, 416, 16, 1, False, acLEAKY, False),
                                                        (2, 3, 37, 32, 1, True, acLEAKY, True),
                                                        (1, 1, 9, 5, 2, False, acLINEAR, False),
