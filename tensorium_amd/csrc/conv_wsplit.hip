@@ -378,6 +378,12 @@ __global__ __launch_bounds__(Cfg::NT) void conv_wsplit16_nhwc_kernel(ConvArgs a)
   }
 }
 
+// ---- NCHW (tnh_conv2d_fwd) forms of the two kernels above.  They repeat
+// the K loop instead of sharing a templated body with the channels-last
+// kernels: a shared body compiled the channels-last epilogue to a schedule
+// that waited on the bias load before computing its store offsets, 5-7%
+// slower for the 16-row tiles.
+
 // One wave as the workgroup of conv_lean.hpp's NCHW pixel loaders (LeanTapB,
 // Lean1x1B): a COLS-pixel x 32-k panel, the same swizzled [COLS][32] layout
 // as a WaveRowsK panel.
