@@ -325,10 +325,11 @@ __device__ __attribute__((always_inline)) inline void conv_store_nhwc(const Conv
       // yolo[(b*F + f)*OHW + p].  Registers 4g .. 4g+3 of a lane hold 4
       // consecutive pixels of its filter, so with yoloVec they are one 16-byte
       // store into the head (lanes l and l + 32 fill 32 consecutive bytes, the
-      // four groups g a 128-byte line); else 4 single stores.  The head is
-      // stored with the default cache policy, not written through: each
-      // store covers 32 bytes of 32 lines, and L2 merges the four that make
-      // up a line (52x52 head at batch 16: 82 -> 74 us).
+      // four groups g a 128-byte line); else 4 single stores.  Both outputs
+      // are stored with the default cache policy, not written through: a
+      // head store covers 32 bytes of 32 lines, and a pixel row of `out`
+      // (5 + classes values per anchor, e.g. 255) is not line-aligned, so L2
+      // merges the partial lines (52x52 head at batch 16: 82 -> 74 -> 67 us).
       const uint32_t OHW = static_cast<uint32_t>(a.g.OHW), F32 = static_cast<uint32_t>(a.F);
       const __amdgpu_buffer_rsrc_t yR = make_rsrc(a.yolo, a.yoloBytes);
 #pragma unroll
@@ -347,7 +348,9 @@ __device__ __attribute__((always_inline)) inline void conv_store_nhwc(const Conv
             for (int e = 0; e < 4; ++e) {
               v[e] = apply_act(acc[i][j][4 * g + e] + bias[j], a.act);
               y[e] = yolo_entry(v[e], entry);
-              buf_st1s(outR, v[e], rowOk(c0 + e) ? vOut[j] : kOOB, static_cast<uint32_t>(c0 + e) * op4);
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[e]), outR,
+                                                    rowOk(c0 + e) ? vOut[j] : kOOB,
+                                                    static_cast<uint32_t>(c0 + e) * op4, 0);
             }
             const uint32_t m = static_cast<uint32_t>(rowBase + c0);
             if (a.yoloVec) {  // m % 4 == 0 and M % 4 == 0: the 4 pixels are in range together, in one image
