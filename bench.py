@@ -172,9 +172,16 @@ def baseline_threads():
     return max(min(avail, CPU_SHARE), 4), nproc, avail, model
 
 
-def cpu_baseline(layers, weights, budget_s=12.0):
+HEADS = (81, 93, 105)  # the pre-logistic head convolutions (darknet layer indices)
+PARITY_TOL = 1e-5  # per tensor: max|gpu - oracle| / max|oracle|
+
+
+def cpu_baseline(layers, weights, budget_s=12.0, size=416):
     """Oracle YOLOv3-416 forward at batch 1 on the host cores, repeated until
-    ~budget_s of work; returns (img/s, threads, images, host description)."""
+    ~budget_s of work, on image 0 of the timed batch (synth.uniform(7) draws
+    the batch image by image, so its first 3x416x416 values are this image);
+    returns (img/s, threads, images, host description, the oracle's head
+    convolutions of that image)."""
     import numpy as np
 
     from oracle import netref
@@ -183,8 +190,10 @@ def cpu_baseline(layers, weights, budget_s=12.0):
 
     threads, nproc, avail, model = baseline_threads()
     R.set_threads(threads)
-    x = synth.uniform(7, (1, 3, 416, 416))
-    netref.forward(layers, weights, x)  # warm-up
+    x = synth.uniform(7, (1, 3, size, size))
+    outs = netref.forward(layers, weights, x)  # warm-up
+    heads = {i: outs[i] for i in HEADS}
+    del outs
     n, t0 = 0, time.perf_counter()
     while True:
         netref.forward(layers, weights, x)
@@ -193,7 +202,21 @@ def cpu_baseline(layers, weights, budget_s=12.0):
             break
     dt = time.perf_counter() - t0
     del np
-    return n / dt, threads, n, {"nproc": nproc, "cpus_available": avail, "cpu_model": model, "P": threads}
+    return n / dt, threads, n, {"nproc": nproc, "cpus_available": avail, "cpu_model": model, "P": threads}, heads
+
+
+def head_parity(gpu_heads, ref_heads):
+    """Per-tensor relative error (max|g - r| / max|r|) of the timed network's
+    head convolutions for image 0 against the CPU oracle's forward of the
+    same image."""
+    from oracle import refcpu as R
+
+    errs = {f"head{i}": float(R.rel_err(gpu_heads[i], ref_heads[i])) for i in HEADS}
+    worst = max(errs.values())
+    return {**{k: float(f"{v:.3e}") for k, v in errs.items()}, "tolerance": PARITY_TOL,
+            "pass": bool(worst <= PARITY_TOL), "image": 0,
+            "against": "CPU oracle forward of the same image (batch 1, per-image route concat)",
+            "metric": "max|gpu - oracle| / max|oracle| per head tensor (pre-logistic conv output)"}
 
 
 COPY_BYTES = 64 << 20
@@ -669,6 +692,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batch1", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph replay")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="tnh_set_deterministic(1): every conv and SGEMM shape takes a fixed tiling with no split-K "
+                         "or tail split, so results do not depend on what the autotuner timed")
     ap.add_argument("--layout", choices=("auto", "nhwc", "nchw"), default="auto",
                     help="activation layout between layers (the image and the yolo heads stay NCHW); auto: "
                          "channels-last")
@@ -698,6 +724,8 @@ def main():
 
     hip = TNNHip(0)
     hip.useTorchStream()  # one ordered stream for torch's buffers and the kernels
+    if args.deterministic:
+        TNNHip.setDeterministic(True)
     _, layers = darknet.load_cfg("yolov3.cfg", args.size, args.size)
     if args.weights:
         from tensorium_amd import weights as WT
@@ -751,6 +779,9 @@ def main():
         log(f"  {k}: {s['ms']:.3f} ms over {s['launches']:.0f} launches, "
             f"{s['flop'] / (s['ms'] / 1e3) / 1e12:.1f} TFLOP/s")
     conv_ms = sum(stats[k]["ms"] for k in conv_kinds)
+    # image 0's head convolutions as the timed network computed them (the
+    # profile pass above is one more eager forward of the same input)
+    gpu_heads = {i: net.output(i)[0:1].contiguous().cpu().numpy() for i in HEADS}
     del net, x
     torch.cuda.empty_cache()
 
@@ -761,10 +792,14 @@ def main():
         log(f"batch 1: {ms1 / max(args.steps, 20):.3f} ms/img, {b1:.1f} img/s")
 
     cpu = None
+    parity = None
     if not args.no_cpu_baseline:
-        v, threads, n, hostd = cpu_baseline(layers, weights, args.cpu_budget)
+        v, threads, n, hostd, ref_heads = cpu_baseline(layers, weights, args.cpu_budget, args.size)
+        parity = head_parity(gpu_heads, ref_heads)
+        log(f"parity (image 0 heads vs the oracle): {parity}")
+        del ref_heads
         cpu = {"value": round(v, 4), "unit": "img/s", "cores": threads, "kind": "port",
-               "sample": f"YOLOv3-416 batch-1 forward x{n} on the CPU oracle (C AVX2+FMA restatement of the "
+               "sample": f"YOLOv3-{args.size} batch-1 forward x{n} on the CPU oracle (C AVX2+FMA restatement of the "
                          f"reference path, P = {threads} worker threads, BN folded); measured at batch 1, "
                          f"not extrapolated",
                **hostd}
@@ -813,7 +848,10 @@ def main():
                  else f"synthetic images, weights from {os.path.basename(args.weights)} (BN folded)"),
         "config": {"workload": f"YOLOv3-{args.size} fp32 inference, batch {args.batch}, 1 GPU",
                    "global_batch": args.batch, "image": [3, args.size, args.size],
-                   "activation_layout": layout_for(args.batch)},
+                   "activation_layout": layout_for(args.batch),
+                   "tiling": ("deterministic (fixed tiling, no split-K or tail split)" if args.deterministic
+                              else "autotuned (split-K / tail splits chosen by time; the sum order may differ "
+                                   "between processes)")},
         "conv_gflops": round(gflops, 1),
         "conv_frac_fp32_mfma_peak": round(gflops * 1e9 / PEAK_FP32_MFMA, 4),
         # the per-layer event brackets of one eager pass (each includes its
@@ -830,6 +868,7 @@ def main():
                      "launches_per_step": round(d["launches"]),
                      "flop_per_launch": round(d["flop"] / max(d["launches"], 1))},
         "cpu_baseline": cpu,
+        "parity": parity,
         "other_configs": extras,
     }
     print(json.dumps(out), flush=True)

@@ -36,13 +36,31 @@ struct Context {
   // kernels that address them, so they are freed only by tnh_finalize.
   std::vector<void*> wsRetired;
   // Partial sums of the multi-workgroup channel reductions (batch-norm
-  // statistics and their deltas, weight-gradient split sums): allocated by
-  // tnh_init, so calls made under graph capture find it.
-  float* red = nullptr;
+  // statistics and their deltas, bias gradients, addDots), redFloats floats
+  // per stream the reductions have run on: reductions on different streams
+  // may run concurrently, so no two streams share one.  tnh_init allocates
+  // kRedSpare buffers up front, which streams first used under graph capture
+  // (when nothing can be allocated) take; later streams allocate their own.
+  struct RedSlot {
+    hipStream_t stream;
+    float* ptr;
+  };
+  std::vector<RedSlot> red;
+  std::vector<float*> redSpare;
   int64_t redFloats = 0;
 };
 
-constexpr int64_t kRedFloats = int64_t(1) << 20;  // 4 MiB of reduction partials
+constexpr int64_t kRedFloats = int64_t(1) << 20;  // 4 MiB of reduction partials per stream
+constexpr int kRedSpare = 4;
+
+// True when the context stream (or the autotuner's stream) is being
+// captured into a graph, so that nothing may be allocated.
+bool capturing(const Context* c);
+
+// The current stream's reduction-partials buffer (redFloats floats), or
+// nullptr when the stream has none, no spare is left and none can be
+// allocated (allocation failure, or the stream is being captured).
+float* reduction_buffer(Context* c);
 
 // Returns the current stream's scratch buffer of at least `bytes` on the
 // context device, growing it (a new hipMalloc; the outgrown buffer stays

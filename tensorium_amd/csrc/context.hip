@@ -76,23 +76,22 @@ int time_graph(Context* cx, const std::function<int(hipStream_t)>& launch, int r
   return st;
 }
 
+bool capturing(const Context* c) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone, ts = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
+         (c->tune_stream &&
+          (hipStreamIsCapturing(c->tune_stream, &ts) != hipSuccess || ts != hipStreamCaptureStatusNone));
+}
+
 void* workspace(Context* c, size_t bytes) {
   Context::WsSlot* slot = nullptr;
   for (Context::WsSlot& w : c->ws)
     if (w.stream == c->stream) slot = &w;
   if (slot && bytes <= slot->bytes) return slot->ptr;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone, ts = hipStreamCaptureStatusNone;
-  const bool capturing = hipStreamIsCapturing(c->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone ||
-                         (c->tune_stream && (hipStreamIsCapturing(c->tune_stream, &ts) != hipSuccess ||
-                                             ts != hipStreamCaptureStatusNone));
-  if (capturing) {
-    // Nothing can be allocated now.  A stream that has no scratch of its own
-    // (captured after warming up on another stream) borrows the first
-    // stream's, as a single shared scratch would: then the two must not run
-    // at the same time.
-    if (!slot && !c->ws.empty() && bytes <= c->ws[0].bytes) return c->ws[0].ptr;
-    return nullptr;
-  }
+  // Nothing can be allocated under capture.  A stream without scratch of its
+  // own gets none (its callers then run whole-K tilings, or compute without
+  // the scratch): borrowing another stream's would race when both run.
+  if (capturing(c)) return nullptr;
   if (!slot) {
     c->ws.push_back({c->stream, nullptr, 0});
     slot = &c->ws.back();
@@ -110,6 +109,36 @@ void* workspace(Context* c, size_t bytes) {
   }
   slot->bytes = want;
   return slot->ptr;
+}
+
+float* reduction_buffer(Context* c) {
+  for (const Context::RedSlot& r : c->red)
+    if (r.stream == c->stream) return r.ptr;
+  float* p = nullptr;
+  if (!c->redSpare.empty()) {
+    p = c->redSpare.back();
+    c->redSpare.pop_back();
+  } else {
+    if (capturing(c)) return nullptr;
+    if (hipMalloc(&p, static_cast<size_t>(c->redFloats) * 4) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  c->red.push_back({c->stream, p});
+  return p;
+}
+
+// Frees every buffer of the context and destroys its streams.
+void release(Context& c) {
+  for (const Context::WsSlot& w : c.ws)
+    if (w.ptr) (void)hipFree(w.ptr);
+  for (void* p : c.wsRetired) (void)hipFree(p);
+  for (const Context::RedSlot& r : c.red) (void)hipFree(r.ptr);
+  for (float* p : c.redSpare) (void)hipFree(p);
+  if (c.own_stream) (void)hipStreamDestroy(c.own_stream);
+  if (c.tune_stream) (void)hipStreamDestroy(c.tune_stream);
+  c = Context{};
 }
 
 }  // namespace tnh
@@ -139,42 +168,30 @@ extern "C" int32_t tnh_init(int32_t device) {
     if (g_ctx.device == device) return TNH_OK;
     (void)hipSetDevice(g_ctx.device);
     (void)hipStreamSynchronize(g_ctx.stream);
-    for (const Context::WsSlot& w : g_ctx.ws)
-      if (w.ptr) (void)hipFree(w.ptr);
-    for (void* p : g_ctx.wsRetired) (void)hipFree(p);
-    if (g_ctx.red) (void)hipFree(g_ctx.red);
-    (void)hipStreamDestroy(g_ctx.own_stream);
-    (void)hipStreamDestroy(g_ctx.tune_stream);
-    g_ctx = Context{};
+    release(g_ctx);
     g_live = false;
   }
   if (int st = hip_status(hipSetDevice(device), "hipSetDevice")) return st;
-  hipStream_t s = nullptr, ts = nullptr;
-  if (int st = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return st;
-  if (int st = hip_status(hipStreamCreateWithFlags(&ts, hipStreamNonBlocking), "hipStreamCreate")) {
-    (void)hipStreamDestroy(s);
-    return st;
+  Context c;
+  int st = hip_status(hipStreamCreateWithFlags(&c.own_stream, hipStreamNonBlocking), "hipStreamCreate");
+  if (!st) st = hip_status(hipStreamCreateWithFlags(&c.tune_stream, hipStreamNonBlocking), "hipStreamCreate");
+  if (!st) st = conv_scratch_setup(device);
+  for (int i = 0; i < kRedSpare && !st; ++i) {
+    float* p = nullptr;
+    st = hip_status(hipMalloc(&p, kRedFloats * 4), "hipMalloc(reduction partials)");
+    if (!st) c.redSpare.push_back(p);
   }
-  float* red = nullptr;
-  if (int st = conv_scratch_setup(device)) {
-    (void)hipStreamDestroy(s);
-    (void)hipStreamDestroy(ts);
-    return st;
-  }
-  if (int st = hip_status(hipMalloc(&red, kRedFloats * 4), "hipMalloc(reduction partials)")) {
-    (void)hipStreamDestroy(s);
-    (void)hipStreamDestroy(ts);
+  if (st) {
+    release(c);
     return st;
   }
   int cus = 0;
   (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-  g_ctx.device = device;
-  g_ctx.own_stream = s;
-  g_ctx.stream = s;
-  g_ctx.tune_stream = ts;
-  g_ctx.cu_count = cus > 0 ? cus : 256;
-  g_ctx.red = red;
-  g_ctx.redFloats = kRedFloats;
+  c.device = device;
+  c.stream = c.own_stream;
+  c.cu_count = cus > 0 ? cus : 256;
+  c.redFloats = kRedFloats;
+  g_ctx = c;
   g_live = true;
   return TNH_OK;
 }
@@ -184,13 +201,7 @@ extern "C" int32_t tnh_finalize(void) {
   if (!g_live) return TNH_OK;
   (void)hipSetDevice(g_ctx.device);
   (void)hipStreamSynchronize(g_ctx.stream);
-  for (const Context::WsSlot& w : g_ctx.ws)
-    if (w.ptr) (void)hipFree(w.ptr);
-  for (void* p : g_ctx.wsRetired) (void)hipFree(p);
-  if (g_ctx.red) (void)hipFree(g_ctx.red);
-  (void)hipStreamDestroy(g_ctx.own_stream);
-  (void)hipStreamDestroy(g_ctx.tune_stream);
-  g_ctx = Context{};
+  release(g_ctx);
   g_live = false;
   return TNH_OK;
 }

@@ -993,8 +993,9 @@ bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = fa
 // first call for its shape (and layout), then launched.  fixed: the static
 // scratch of the no-allocation entry point (nullptr: the context's growable
 // workspace).  With it the call never tunes (a timing graph allocates): it
-// runs the forced, the cached or the cost model's choice, and fails when that
-// choice needs more scratch than the array holds.
+// runs the forced, the cached or the cost model's choice; a cached choice
+// whose split pieces do not fit the array gives way to the cost model's
+// (whole K if need be), and only a forced tiling that does not fit fails.
 int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool smallIO, bool nhwc, const TuneKey& key,
                   float* fixed = nullptr) {
   const int64_t F = a.F, N = a.g.N, K = a.g.K, C = a.g.C;
@@ -1076,14 +1077,6 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     }
     return nhwc ? launch_nhwc_cfg(c.cfg, b, mode, cus, s) : launch(c.cfg, b, mode, va, vb, cus, s);
   };
-  auto run = [&](const Cand& c) -> int {
-    if (fixed && wsFloats(c) > kNoAllocScratchFloats)
-      return fail(TNH_ERR_INVALID_ARG,
-                  "conv2d_nhwc_noalloc: the tiling of this call needs %lld bytes of scratch, the static scratch "
-                  "holds %lld (split the batch, or choose another tiling with tnh_conv2d_set_autotune)",
-                  (long long)(wsFloats(c) * 4), (long long)(kNoAllocScratchFloats * 4));
-    return runOn(c, cx->stream);
-  };
   Cand best = cands[0];
   {
     float bc = 1e30f;
@@ -1093,6 +1086,23 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
       if (v < bc) bc = v, best = c;
     }
   }
+  const Cand model = best;  // the cost model's choice (timed tuning may replace `best`)
+  // forced: a tiling the caller chose with tnh_conv2d_set_autotune
+  auto run = [&](const Cand& c, bool forced = false) -> int {
+    if (fixed && wsFloats(c) > kNoAllocScratchFloats) {
+      if (forced)
+        return fail(TNH_ERR_INVALID_ARG,
+                    "conv2d_nhwc_noalloc: the forced tiling needs %lld bytes of scratch, the static scratch holds "
+                    "%lld (split the batch, or force another tiling with tnh_conv2d_set_autotune)",
+                    (long long)(wsFloats(c) * 4), (long long)(kNoAllocScratchFloats * 4));
+      // a tiling tuned by the allocating entry point whose split pieces do
+      // not fit the static scratch: the cost model's choice instead, whose
+      // pieces (if it splits and they do not fit either) runOn drops for a
+      // whole-K launch of the same tile
+      return runOn(model, cx->stream);
+    }
+    return runOn(c, cx->stream);
+  };
   bool tune = false;
   const bool aliased = a.res && a.res == a.out;  // in-place add: reruns would accumulate
   {
@@ -1101,10 +1111,10 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
       const int c = g_forced_cfg % 64, hi = g_forced_cfg / 64;
       if (hi > 16 && kCfgs[c].kind != kLean) return fail(TNH_ERR_UNSUPPORTED, "conv2d: tail split of a non-lean tile");
       if (hi > 1 && kCfgs[c].kind == kWsplit) return fail(TNH_ERR_UNSUPPORTED, "conv2d: split of a wave-split tile");
-      if (nhwc && hi >= 2 && hi <= 16) return run({c, 1, hi, 2});  // split-K: every tile cut
-      if (hi >= 34) return run({c, 1, hi - 32, 1});
-      if (hi >= 18) return run({c, 1, hi - 16, 0});
-      return run({c, hi > 1 ? hi : 1, 0, 0});
+      if (nhwc && hi >= 2 && hi <= 16) return run({c, 1, hi, 2}, true);  // split-K: every tile cut
+      if (hi >= 34) return run({c, 1, hi - 32, 1}, true);
+      if (hi >= 18) return run({c, 1, hi - 16, 0}, true);
+      return run({c, hi > 1 ? hi : 1, 0, 0}, true);
     }
     if (det) return run(best);  // the cost model's whole-K choice: the same in every process
     auto it = g_tuned.find(key);

@@ -62,11 +62,17 @@ struct ChanSplit {
 };
 
 // nq partial sums per workgroup; about four workgroups per CU over all
-// channels, at least ~1024 elements each.
-int chan_split(ChanSplit& s, int64_t nch, int64_t block, int64_t groups, int nq, const Context* cx) {
-  TNH_ARG(nch <= 65535, "channel reduction: %lld channels (at most 65535)", (long long)nch);
+// channels, at least ~1024 elements each.  part: the current stream's
+// partial-sum buffer (each stream has its own, so reductions forked onto
+// several streams do not share one).
+int chan_split(ChanSplit& s, float*& part, int64_t nch, int64_t block, int64_t groups, int nq, Context* cx) {
   TNH_ARG(nch * nq <= cx->redFloats, "channel reduction: %lld channels do not fit the partial-sum buffer",
           (long long)nch);
+  part = reduction_buffer(cx);
+  if (!part)
+    return fail(TNH_ERR_OUT_OF_MEMORY,
+                "channel reduction: no partial-sum buffer for this stream (the spares are taken and it cannot be "
+                "allocated now; run one reduction on the stream before capturing it)");
   s.nch = nch;
   s.block = block;
   s.groups = groups;
@@ -75,7 +81,7 @@ int chan_split(ChanSplit& s, int64_t nch, int64_t block, int64_t groups, int nq,
   s.units = groups * s.kc;
   int64_t P = (4 * static_cast<int64_t>(cx->cu_count) + nch - 1) / nch;
   P = std::min<int64_t>(P, std::max<int64_t>(1, groups * block / 1024));
-  P = std::min<int64_t>({P, s.units, cx->redFloats / (nq * nch), 4096});
+  P = std::min<int64_t>({P, s.units, cx->redFloats / (nq * nch), 4096});  // grid.y holds P
   s.P = static_cast<int>(std::max<int64_t>(P, 1));
   return TNH_OK;
 }
@@ -127,11 +133,13 @@ __device__ inline void chan_walk(const ChanSplit& s, int p, int64_t i, const Op&
   }
 }
 
+// grid: (channel, workgroup of the channel); channels in x, which holds up
+// to 2^31 - 1 of them
 template <int NQ, bool VEC, class Op>
 __global__ __launch_bounds__(kRed) void chan_partial_kernel(Op op, ChanSplit s, float* part) {
   __shared__ float sh[kRed];
-  const int p = blockIdx.x;
-  const int64_t i = blockIdx.y;
+  const int64_t i = blockIdx.x;
+  const int p = blockIdx.y;
   op.begin(i, s, part, sh);
   float acc[NQ];
 #pragma unroll
@@ -272,7 +280,7 @@ bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // Launches the first pass of a channel reduction (nq partials per workgroup).
 template <int NQ, class Op>
 int launch_partial(const Op& op, const ChanSplit& s, bool vec, float* part, hipStream_t st, const char* name) {
-  const dim3 grid(static_cast<unsigned>(s.P), static_cast<unsigned>(s.nch));
+  const dim3 grid(static_cast<unsigned>(s.nch), static_cast<unsigned>(s.P));
   if (vec)
     hipLaunchKernelGGL((chan_partial_kernel<NQ, true, Op>), grid, dim3(kRed), 0, st, op, s, part);
   else
@@ -296,17 +304,18 @@ int means_vars_impl(int64_t srcSize, int64_t dstSize, int64_t groups, const floa
   const int64_t block = srcSize / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == srcSize && groups * block > 1, "means_vars: sizes do not align");
   ChanSplit s;
-  if (int st = chan_split(s, dstSize, block, groups, 2, cx)) return st;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 2, cx)) return st;
   const float* x = src + offset;
   const bool vec = chan_vec(s, {x});
-  float* sumPart = cx->red;
-  float* rssPart = cx->red + dstSize * s.P;
+  float* sumPart = red;
+  float* rssPart = red + dstSize * s.P;
   const float S = static_cast<float>(groups * block);
   if (int st = launch_partial<1>(SumOp{x}, s, vec, sumPart, cx->stream, "chan_partial_kernel<sum>")) return st;
   if (int st = launch_partial<1>(RssOp{x, sumPart, S, 0.f}, s, vec, rssPart, cx->stream, "chan_partial_kernel<rss>"))
     return st;
   const float keep = 1.0f - momentum;
-  hipLaunchKernelGGL(means_vars_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, S,
+  hipLaunchKernelGGL(means_vars_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, S,
                      means, vars, rollMean, rollVar, keep, momentum);
   return launch_status("means_vars_final");
 }
@@ -595,13 +604,14 @@ extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_
   const int64_t block = srcSize / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == srcSize, "means_vars_delta: sizes do not align");
   ChanSplit s;
-  if (int st = chan_split(s, dstSize, block, groups, 2, cx)) return st;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 2, cx)) return st;
   const float* d = delta + offset;
   const float* xx = x + offset;
-  if (int st = launch_partial<2>(MvdOp{d, xx, mean, 0.f}, s, chan_vec(s, {d, xx}), cx->red, cx->stream,
+  if (int st = launch_partial<2>(MvdOp{d, xx, mean, 0.f}, s, chan_vec(s, {d, xx}), red, cx->stream,
                                  "chan_partial_kernel<mean_var_delta>"))
     return st;
-  hipLaunchKernelGGL(means_vars_delta_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red,
+  hipLaunchKernelGGL(means_vars_delta_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red,
                      s, variance, mean_delta, variance_delta);
   return launch_status("means_vars_delta_final");
 }
@@ -637,12 +647,13 @@ extern "C" int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups, cons
   const int64_t block = N / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == N, "add_dots: sizes do not align");
   ChanSplit s;
-  if (int st = chan_split(s, dstSize, block, groups, 1, cx)) return st;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
   const float* a = src1 + srcOffset;
   const float* b = src2 + srcOffset;
-  if (int st = launch_partial<1>(DotOp{a, b}, s, chan_vec(s, {a, b}), cx->red, cx->stream, "chan_partial_kernel<dots>"))
+  if (int st = launch_partial<1>(DotOp{a, b}, s, chan_vec(s, {a, b}), red, cx->stream, "chan_partial_kernel<dots>"))
     return st;
-  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, dst);
+  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, dst);
   return launch_status("add_dots_final");
 }
 
@@ -656,11 +667,12 @@ extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSiz
   TNH_ARG(block * dstSize * batch == srcSize, "backward_bias: sizes do not align");
   if (srcSize == 0) return TNH_OK;
   ChanSplit s;
-  if (int st = chan_split(s, dstSize, block, batch, 1, cx)) return st;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, batch, 1, cx)) return st;
   const float* x = src + srcOffset;
-  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), cx->red, cx->stream, "chan_partial_kernel<sum>"))
+  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), red, cx->stream, "chan_partial_kernel<sum>"))
     return st;
-  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, cx->red, s, dst);
+  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, dst);
   return launch_status("add_dots_final");
 }
 

@@ -243,12 +243,17 @@ class CifarTrainer:
 
     def capture(self, x, truth):
         """Records one step (forward, backward, update) over the fixed input
-        buffers into a HIP graph on the library's own stream; run one eager
-        step first so autotuning and scratch allocation are done.  Each
-        replay() then trains on the same buffers (contents may change)."""
+        buffers into a HIP graph on the library's own stream.  It first runs
+        one eager step on that stream (so the parameters advance by one
+        step): scratch of the weight-gradient split sums cannot be allocated
+        while a stream is being captured, and without it the captured step
+        would sum without splits (slower, and in another order than the
+        eager steps).  Each replay() then trains on the same buffers
+        (contents may change)."""
         hip = self.hip
         self.torch.cuda.synchronize()
         hip.resetStream()
+        self.step(x, truth)
         hip.finish()
         hip.graphBegin()
         try:

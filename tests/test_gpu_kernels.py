@@ -106,6 +106,43 @@ def test_sgemm_8192_exact(hip, ta, tb):
     assert torch.equal(dC, ref)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_sgemm_mid_square_exact(hip, n, ta, tb):
+    """The bench's 1024^3 and 2048^3 lines in all four variants (the sizes
+    where the wave-split tiles compete with the lean ones): integer operands
+    in [-4, 4] keep every partial sum exact in fp32, so the product equals a
+    float64 product bit for bit; then U[-1, 1) operands against the oracle on
+    16 sampled rows of C (the oracle's per-row chains do not depend on the
+    other rows of A)."""
+    M = N = K = n
+    case(f"sgemm {n}^3 int ta={ta} tb={tb}")
+    g = torch.Generator(device="cuda").manual_seed(n + 2 * ta + tb)
+    dA = torch.randint(-4, 5, (M, K), generator=g, device="cuda").float()
+    dB = torch.randint(-4, 5, (K, N), generator=g, device="cuda").float()
+    dC = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, n, dB, 0, n, 0.0, dC, 0, N)
+    hip.finish()
+    a64 = dA.double().T if ta else dA.double()
+    b64 = dB.double().T if tb else dB.double()
+    assert torch.equal(dC, (a64 @ b64).float())
+    del dA, dB, dC
+    case(f"sgemm {n}^3 rand ta={ta} tb={tb} vs oracle (16 rows)")
+    A = synth.uniform(41 + n, (n, n), -1, 1)
+    B = synth.uniform(42 + n, (n, n), -1, 1)
+    dA, dB = D(A), D(B)
+    dC = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+    hip.gemm(ta, tb, M, N, K, 1.0, dA, 0, n, dB, 0, n, 0.0, dC, 0, N)
+    got = H(dC, hip)
+    rows = np.linspace(0, M - 1, 16).astype(np.int64)
+    # rows r of op(A): A[r, :] for NN/NT, column r of A (row r of A^T) for TN/TT
+    Ar = np.ascontiguousarray(A.T[rows] if ta else A[rows])
+    ref = np.zeros((16, N), np.float32)
+    R.sgemm(0, tb, 16, N, K, 1.0, Ar, K, B, n, 0.0, ref, N)
+    assert R.rel_err(got[rows], ref) <= TOL
+
+
 # the conv-shaped skinny GEMMs of BASELINE config 2 (M = F, N = OH*OW*16,
 # K = 9*C): the bench times all five
 SKINNY = [(64, 692224, 288), (128, 173056, 576), (256, 43264, 1152), (512, 10816, 2304), (1024, 2704, 4608)]

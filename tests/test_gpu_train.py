@@ -55,12 +55,13 @@ def test_means_vars(hip, shape):
 
 
 @pytest.mark.parametrize("shape,off", [((128, 64, 16, 16), 0), ((1, 8, 300, 300), 0), ((3, 5, 33, 17), 1),
-                                       ((64, 10, 1, 1), 0)])
+                                       ((64, 10, 1, 1), 0), ((3, 70000, 1, 1), 0)])
 def test_channel_reductions_large_and_ragged(hip, shape, off):
     """The multi-workgroup channel reductions (statistics, their deltas,
     addDots) on many workgroups per channel, rows longer than one unit
-    (90 000 floats), an unaligned offset (scalar loads) and one element per
-    channel: within the per-tensor bound of the oracle's float64 sums, and
+    (90 000 floats), an unaligned offset (scalar loads), one element per
+    channel and more channels than a grid's y dimension holds (70 000, as a
+    wide connected layer's statistics): within the per-tensor bound of the oracle's float64 sums, and
     identical bits on a second call (fixed summation order)."""
     case(f"channel reductions {shape} offset {off}")
     B, Cc = shape[:2]
@@ -70,20 +71,23 @@ def test_channel_reductions_large_and_ragged(hip, shape, off):
     md_ref, vd_ref = T.means_vars_delta(d, x, m_ref, v_ref, B)
     acc0 = synth.normal(312, (Cc,))
     dots_ref = T.add_dots(acc0, x, d, B)
+    # backwardBias: dst[i] += the sum of channel i's deltas (= addDots with ones)
+    bias_ref = T.add_dots(acc0, np.ones_like(d), d, B)
     dx = D(np.concatenate([np.zeros(off, np.float32), x.ravel()]))
     dd = D(np.concatenate([np.zeros(off, np.float32), d.ravel()]))
     res = []
     for _ in range(2):
         dm, dv, dmd, dvd = (torch.empty(Cc, dtype=torch.float32, device="cuda") for _ in range(4))
-        dacc = D(acc0)
+        dacc, dbias = D(acc0), D(acc0)
         hip.meansAndVars(x.size, Cc, B, dx, off, dm, dv)
         hip.meansAndVarsDelta(d.size, Cc, B, dd, dx, off, D(m_ref), D(v_ref), dmd, dvd)
         hip.addDots(x.size, Cc, B, dx, dd, off, dacc)
-        res.append([H(t, hip) for t in (dm, dv, dmd, dvd, dacc)])
+        hip.backwardBias(Cc, dbias, d.size, dd, off, 1, B)
+        res.append([H(t, hip) for t in (dm, dv, dmd, dvd, dacc, dbias)])
     for a, b in zip(*res):
         assert np.array_equal(a, b)
-    m, v, md, vd, dots = res[0]
-    for got, ref in ((m, m_ref), (v, v_ref), (md, md_ref), (vd, vd_ref), (dots, dots_ref)):
+    m, v, md, vd, dots, bias = res[0]
+    for got, ref in ((m, m_ref), (v, v_ref), (md, md_ref), (vd, vd_ref), (dots, dots_ref), (bias, bias_ref)):
         assert R.rel_err(got, ref) <= TOL
 
 
@@ -266,3 +270,89 @@ def test_cifar_train_loss_falls(hip):
         gpu.step(dx, dt)
         losses.append(float(gpu.cost()))
     assert np.all(np.isfinite(losses)) and losses[-1] < losses[0]
+
+
+def test_reductions_on_two_forked_streams(hip):
+    """Channel reductions forked onto two streams at once, each with many
+    workgroups per channel: backwardBias on the main stream while
+    meansAndVars and addDots run on a second stream.  Each stream keeps its
+    own partial-sum buffer, so the results equal the same calls made one
+    after another on one stream, bit for bit."""
+    case("channel reductions on two forked streams")
+    B, Cc, Hh = 64, 64, 32
+    x = synth.normal(340, (B, Cc, Hh, Hh), 1.5) + np.float32(0.5)
+    d = synth.normal(341, (B, Cc, Hh, Hh))
+    acc0 = synth.normal(342, (Cc,))
+    dx, dd = D(x), D(d)
+    n = x.size
+
+    def bufs():
+        return [torch.empty(Cc, dtype=torch.float32, device="cuda") for _ in range(2)] + [D(acc0), D(acc0)]
+
+    m1, v1, acc1, bb1 = bufs()
+    hip.meansAndVars(n, Cc, B, dx, 0, m1, v1)
+    hip.addDots(n, Cc, B, dx, dd, 0, acc1)
+    hip.backwardBias(Cc, bb1, n, dd, 0, 1, B)
+    one = [H(t, hip) for t in (m1, v1, acc1, bb1)]
+
+    m2, v2, acc2, bb2 = bufs()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()  # default priority
+    main = hip.stream
+    fork, join = hip.eventCreate(), hip.eventCreate()
+    try:
+        for rep in range(3):
+            hip.eventRecord(fork)
+            hip.setStream(side.cuda_stream)
+            hip.streamWaitEvent(fork)
+            hip.meansAndVars(n, Cc, B, dx, 0, m2, v2)
+            hip.addDots(n, Cc, B, dx, dd, 0, acc2)
+            hip.eventRecord(join)
+            hip.setStream(main)
+            hip.backwardBias(Cc, bb2, n, dd, 0, 1, B)
+            hip.streamWaitEvent(join)
+            got = [H(t, hip) for t in (m2, v2, acc2, bb2)]
+            for name, a, b in zip(("means", "vars", "dots", "bias"), got, one):
+                assert np.array_equal(a, b), (rep, name)
+            acc2.copy_(torch.from_numpy(acc0))
+            bb2.copy_(torch.from_numpy(acc0))
+            torch.cuda.synchronize()
+    finally:
+        hip.setStream(main)
+        hip.eventDestroy(fork)
+        hip.eventDestroy(join)
+
+
+def test_cifar_train_step_graph_replays_equal_eager(hip):
+    """The config-3 step captured into a HIP graph (as bench.py times it) and
+    replayed three times, with eager work and synchronizations between the
+    replays, against a second trainer from the same parameters stepping
+    eagerly: every parameter, momentum buffer and the loss equal after each
+    step, bit for bit (the captured step launches the kernels the eager one
+    does, with the same scratch splits)."""
+    case("cifar train step: graph replays vs eager steps, B 32")
+    B = 32
+    x, truth = _batch(350, B)
+    params = trainnet.init_params()
+    a = trainnet.CifarTrainer(hip, params, B)
+    b = trainnet.CifarTrainer(hip, params, B)
+    dx, dt = D(x), D(truth)
+    keys = ("w0", "w1", "w2", "s0", "s2", "fw", "fb", "u_w0", "u_w2", "u_s1", "u_fw", "rm1", "rv2")
+    try:
+        a.capture(dx, dt)  # runs one eager step first
+        hip.useTorchStream()
+        b.step(dx, dt)
+        for rep in range(3):
+            hip.resetStream()
+            a.replay()
+            hip.finish()
+            hip.useTorchStream()
+            b.step(dx, dt)
+            hip.finish()
+            for k in keys:
+                assert np.array_equal(a.host(k), b.host(k)), (rep, k)
+            assert float(a.cost()) == float(b.cost()), rep
+            torch.cuda.synchronize()
+    finally:
+        a.release_graph()
+        hip.useTorchStream()

@@ -3,9 +3,10 @@ cannot allocate device memory) against tnh_conv2d_fwd_nhwc through the C ABI:
 bit-identical outputs on two calls in a row, the second with a smaller
 input (the static scratch still holds the first call's pieces), with the
 tiling the allocating entry point tuned and with forced tail-split and
-split-K tilings (the ones that use the scratch); a tiling that needs more
-scratch than the array holds is refused without a launch; the calls leave
-the device's free memory unchanged.  Both are also checked against the CPU
+split-K tilings (the ones that use the scratch); a forced tiling that needs
+more scratch than the array holds is refused without a launch, while a tuned
+one gives way to the cost model's tiling; the calls leave the device's free
+memory unchanged.  Both are also checked against the CPU
 oracle (per-tensor 1e-5)."""
 import numpy as np
 import pytest
@@ -119,3 +120,28 @@ def test_noalloc_refuses_a_tiling_beyond_the_scratch(hip, restore_autotune):
     L.run(hip, False, out)
     assert R.rel_err(out.cpu().numpy(), L.ref) <= TOL
     assert E is TNHError
+
+
+def test_noalloc_after_tuning_never_refuses(hip, restore_autotune):
+    """A layer whose timed tuning may choose split pieces larger than the
+    static scratch (8 x 52 x 52 x 256, 3x3 over 256 channels: split-K into 4
+    pieces of every 128x128 tile would need 88 MB): after the allocating
+    entry point tuned it, the no-alloc call runs without an error, on two
+    calls in a row, the second with a smaller batch.  Its output equals the
+    allocating entry point's bit for bit when the tuned pieces fit the
+    scratch; otherwise it runs the cost model's tiling (whole K if need be)
+    and stays within the oracle's bound."""
+    L = Layer(8, 256, 52, 256, 911)
+    S = Layer(2, 256, 52, 256, 921)
+    hip.setConvAutotune(True, -1)
+    case("conv nhwc noalloc after tuning: allocating entry point (tunes)")
+    want = L.run(hip, False).cpu().numpy()
+    want_s = S.run(hip, False).cpu().numpy()
+    case("conv nhwc noalloc after tuning: no-alloc entry point, big then small")
+    got = L.run(hip, True).cpu().numpy()
+    got_s = S.run(hip, True).cpu().numpy()
+    print(f"noalloc after tuning: equal to the allocating call: {np.array_equal(got, want)} (8 images), "
+          f"{np.array_equal(got_s, want_s)} (2 images)", flush=True)
+    assert R.rel_err(got, L.ref) <= TOL
+    assert R.rel_err(got_s, S.ref) <= TOL
+    assert R.rel_err(want, L.ref) <= TOL
