@@ -97,11 +97,13 @@ int32_t tnh_event_elapsed_ms(void *start, void *stop, float *ms);
 /* No TNNCuda counterpart (it runs one stream): the context stream waits for
  * `ev`, recorded with tnh_event_record while another stream was selected.
  * Forks and joins independent work (a network's yolo head tails) onto a
- * second stream, eagerly or under graph capture.  Split-K scratch is kept
- * per stream, so convolutions on different streams may overlap; scratch is
- * allocated on a stream's first eager use (a stream captured before any
- * eager call borrows the first stream's scratch and must not run beside
- * it). */
+ * second stream, eagerly or under graph capture.  Scratch is kept per
+ * stream (split-K pieces, the channel reductions' partial sums), so calls on
+ * different streams may overlap.  Split-K scratch is allocated on a stream's
+ * first eager use; a stream captured before any eager call gets none and
+ * runs whole-K tilings (correct, possibly slower).  Reduction partials come
+ * from spares allocated by tnh_init (4 streams) or on a stream's first eager
+ * reduction. */
 int32_t tnh_stream_wait_event(void *ev);
 
 /* ---- GEMM ------------------------------------------------------------- */
@@ -365,15 +367,31 @@ int32_t tnh_maxpool_fwd_nhwc(int64_t batch, int64_t channels, int64_t h,
                              int64_t kernelSize, const float *in,
                              int64_t inOff, int64_t inPix, float *out,
                              int64_t outOff, int64_t outPix);
-/* TNNCuda.backwardMaxPool (nncuda.pas:1121) with the CPU order of
- * backwardMaxPool (nMaxPoolLayer.pas:501-512): delta_in[idx[i]] += delta[i]
- * summed per input element in ascending i (gather, no atomics).  Needs the
- * forward geometry to enumerate each input's candidate windows. */
+/* TNNCuda.backwardMaxPool (nncuda.pas:1121, called at nMaxPoolLayer.pas:699)
+ * with its arguments: output = the pooled layer's input delta (accumulated),
+ * delta = the layer's own delta.  Result: the CPU order of backwardMaxPool
+ * (nMaxPoolLayer.pas:501-512), output[indexes[i]] += delta[i] in ascending
+ * i, bit for bit; index -1 (a window of -inf) is skipped.  The library
+ * remembers the geometry of the tnh_maxpool_fwd call that last wrote
+ * `indexes` (keyed by the pointer, with batch and output shape checked;
+ * tnh_free forgets it).  Windows that do not overlap (size <= stride) are
+ * scattered, one thread per output (each input element receives at most one
+ * delta, so no order matters); overlapping ones are gathered per input
+ * element in ascending i.  Indexes that no tnh_maxpool_fwd wrote are
+ * scattered with atomic adds: exact when no two windows name one input
+ * element.  Only elements that some index names are read or written. */
 int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH,
-                        int64_t outW, int64_t h, int64_t w, int64_t strideX,
-                        int64_t strideY, int64_t padding, int64_t kernelSize,
-                        const int64_t *indexes, const float *delta,
-                        float *deltaIn);
+                        int64_t outW, float *output, const int64_t *indexes,
+                        const float *delta);
+/* No reference counterpart: tnh_maxpool_bwd with the forward geometry given
+ * (h, w, strides, padding and size of the forward call), for indexes the
+ * library did not write; the same gather and results. */
+int32_t tnh_maxpool_bwd_geom(int64_t batch, int64_t outC, int64_t outH,
+                             int64_t outW, float *output,
+                             const int64_t *indexes, const float *delta,
+                             int64_t h, int64_t w, int64_t strideX,
+                             int64_t strideY, int64_t padding,
+                             int64_t kernelSize);
 /* TNNCuda.upSample (nncuda.pas:1267) / upsample (nupsamplelayer.pas:83):
  * h,w are the small-side dims.  isForward=1: out = scale*in (nearest);
  * isForward=0: in += scale*out summed per input pixel in raster order
@@ -493,6 +511,18 @@ int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch,
 int32_t tnh_means_vars(int64_t srcSize, int64_t dstSize, int64_t groups,
                        const float *src, int64_t offset, float *means,
                        float *vars);
+/* TNNCuda.means (nncuda.pas:1330, called by TBaseLayer.batchNormGPU at
+ * nbaselayer.pas:583): the means of tnh_means_vars alone, the same bits. */
+int32_t tnh_means(int64_t srcSize, int64_t dstSize, int64_t groups,
+                  const float *src, int64_t offset, float *means);
+/* TNNCuda.variances (nncuda.pas:1350, nbaselayer.pas:584): vars[i] =
+ * sum (x - means[i])^2 / (groups*block - 1) about the means passed in, the
+ * unbiased divisor of the CPU path (ntensors.pas:9102-9180; TNNCuda's `vars`
+ * kernel divides by groups*block).  With the means of tnh_means the result
+ * equals tnh_means_vars' variances bit for bit. */
+int32_t tnh_variances(int64_t srcSize, int64_t dstSize, int64_t groups,
+                      const float *src, int64_t offset, const float *means,
+                      float *vars);
 /* No reference counterpart: tnh_means_vars followed by the rolling-statistics
  * update of TBaseLayer.batchNorm in training (nbaselayer.pas:351-355:
  * rolling.Multiply(1 - momentum), then rolling.axpy(momentum, stat)), in

@@ -133,8 +133,10 @@ function tnh_route(batch: Int64; n: LongInt; srcs: PPSingle; sizes: PInt64; dst:
 function tnh_maxpool_fwd(batch, outC, outH, outW: Int64; input: PSingle;
   c, h, w, strideX, strideY, padding, kernelSize: Int64; indexes: PInt64; output: PSingle): LongInt; cdecl;
   external libtnh;
-function tnh_maxpool_bwd(batch, outC, outH, outW, h, w, strideX, strideY, padding, kernelSize: Int64;
-  indexes: PInt64; delta, deltaIn: PSingle): LongInt; cdecl; external libtnh;
+function tnh_maxpool_bwd(batch, outC, outH, outW: Int64; output: PSingle; indexes: PInt64;
+  delta: PSingle): LongInt; cdecl; external libtnh;
+function tnh_maxpool_bwd_geom(batch, outC, outH, outW: Int64; output: PSingle; indexes: PInt64; delta: PSingle;
+  h, w, strideX, strideY, padding, kernelSize: Int64): LongInt; cdecl; external libtnh;
 function tnh_upsample(batch, channels, h, w: Int64; input: PSingle; stride: Int64; isForward: LongInt;
   scale: Single; output: PSingle; zeroIn: LongInt): LongInt; cdecl; external libtnh;
 function tnh_upsample_nhwc(batch, channels, h, w, stride: Int64; scale: Single; input: PSingle;
@@ -160,6 +162,10 @@ function tnh_forward_scale_add(dstSize: Int64; dst: PSingle; offset, scaleSize: 
 function tnh_bn_forward(dstSize, N, batch: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
   act: LongInt): LongInt; cdecl; external libtnh;
 function tnh_means_vars(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
+  means, vars: PSingle): LongInt; cdecl; external libtnh;
+function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
+  means: PSingle): LongInt; cdecl; external libtnh;
+function tnh_variances(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_statistics(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars, rollingMeans, rollingVars: PSingle; momentum: Single): LongInt; cdecl; external libtnh;
@@ -245,11 +251,9 @@ type
     procedure crossEntropySoftmax(const N: SizeInt; const pred, truth: TCUMem; delta, error: TCUMem);
     procedure forwardMaxPool(const aBatch, outC, outH, outW: SizeInt; const input: TCUMem; const c, h, w: SizeInt;
       const stride_x, stride_y, padding, kernelSize: SizeInt; indexes, output: TCUMem);
-    // TNNCuda.backwardMaxPool takes the output geometry only; the gather here
-    // also needs the forward one, which TMaxPoolLayer holds (h, w, strides,
-    // padding, size): the reference's signature plus those six
-    procedure backwardMaxPool(const aBatch, outC, outH, outW: SizeInt; output: TCUMem; const indexes, delta: TCUMem;
-      const h, w, stride_x, stride_y, padding, kernelSize: SizeInt);
+    // the library remembers the geometry of the forwardMaxPool call that
+    // wrote `indexes` and gathers in the CPU order
+    procedure backwardMaxPool(const aBatch, outC, outH, outW: SizeInt; output: TCUMem; const indexes, delta: TCUMem);
     procedure im2col(const aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
       strideY, strideX, dilationY, dilationX: SizeInt; const im: TCUMem; const imOffset: SizeInt;
       const col: TCUMem; const colOffset: SizeInt);
@@ -543,10 +547,9 @@ begin
 end;
 
 procedure TNNHip<T>.backwardMaxPool(const aBatch, outC, outH, outW: SizeInt; output: TCUMem;
-  const indexes, delta: TCUMem; const h, w, stride_x, stride_y, padding, kernelSize: SizeInt);
+  const indexes, delta: TCUMem);
 begin
-  check(tnh_maxpool_bwd(aBatch, outC, outH, outW, h, w, stride_x, stride_y, padding, kernelSize, PInt64(indexes),
-    PSingle(delta), PSingle(output)));
+  check(tnh_maxpool_bwd(aBatch, outC, outH, outW, PSingle(output), PInt64(indexes), PSingle(delta)));
 end;
 
 procedure TNNHip<T>.im2col(const aChannels, aHeight, aWidth, kernelHeight, kernelWidth, padHeight, padWidth,
@@ -587,13 +590,13 @@ end;
 procedure TNNHip<T>.means(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
   means: TCUMem);
 begin
-  unsupported('means (meansAndVars computes both statistics)');
+  check(tnh_means(srcSize, dstSize, groups, PSingle(src), offset, PSingle(means)));
 end;
 
 procedure TNNHip<T>.variances(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
   means, vars: TCUMem);
 begin
-  unsupported('variances (meansAndVars computes both statistics)');
+  check(tnh_variances(srcSize, dstSize, groups, PSingle(src), offset, PSingle(means), PSingle(vars)));
 end;
 
 procedure TNNHip<T>.normalize(const srcSize, dstSize, groups: SizeInt; means: TCUMem; const meansStride: SizeInt;

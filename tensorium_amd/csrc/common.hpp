@@ -74,6 +74,10 @@ void* workspace(Context* c, size_t bytes);
 // tnh_init.
 int conv_scratch_setup(int device);
 
+// Forgets the maxpool forward geometry recorded for an indexes buffer at p
+// (pool.hip); tnh_free calls it for every buffer it releases.
+void pool_forget(const void* p);
+
 // Deterministic mode (tnh_set_deterministic): no timing-based tuning and no
 // split-K / tail-split tilings, so every process runs the same kernels and
 // produces the same bits.

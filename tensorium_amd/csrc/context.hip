@@ -253,6 +253,7 @@ extern "C" int32_t tnh_malloc(int64_t bytes, void** ptr) {
 extern "C" int32_t tnh_free(void* ptr) {
   TNH_REQUIRE_CTX(cx);
   if (!ptr) return TNH_OK;
+  pool_forget(ptr);
   return hip_status(hipFree(ptr), "hipFree");
 }
 

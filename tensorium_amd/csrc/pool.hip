@@ -4,14 +4,17 @@
 // window origin (i*sY + off, j*sX + off) with off = -pad div 2, out-of-range
 // taps read as -MaxSingle, windows scanned n-major then m, strict '>' keeps
 // the first maximum, indices are global flat int64, -1 when no tap beats
-// -MaxSingle.  Backward is a gather: each input element sums, in ascending
-// output index (the order of the serial scatter at :501-512), the deltas of
-// the windows whose recorded index is that element.
+// -MaxSingle.  Backward: where windows overlap, a gather (each input element
+// sums, in ascending output index, the order of the serial scatter at
+// :501-512, the deltas of the windows whose recorded index is that element);
+// where they do not, the scatter itself (one delta per input element).
 //
 // Upsample (nupsamplelayer.pas:83-113): forward out = scale*in per output
 // pixel; backward gathers the stride^2 output pixels of each input pixel in
 // raster order, in += scale*out each, bit-identical to the serial loop.
 #include <cfloat>
+#include <mutex>
+#include <unordered_map>
 
 #include "common.hpp"
 
@@ -115,33 +118,28 @@ __global__ __launch_bounds__(kThreads) void maxpool2_fwd_kernel(int total, int O
   }
 }
 
-// Backward of the 2x2 / stride-2 case above: input pixel (y, x) lies in
-// exactly one window (y/2, x/2) (when inside the output), so each thread
-// takes four consecutive pixels of a row (two windows), adds a window's
-// delta to the pixel its index names (dIn += delta, the serial scatter's one
-// contribution) and rewrites the four pixels with one 16-byte store.
-__global__ __launch_bounds__(kThreads) void maxpool2_bwd_kernel(int total, int H, int W4, int OH, int OW,
-                                                                const int64_t* __restrict__ idx,
-                                                                const float* __restrict__ delta,
-                                                                float* __restrict__ dIn) {
-  for (int t = blockIdx.x * kThreads + threadIdx.x; t < total; t += gridDim.x * kThreads) {
-    const int q = t % W4, r = t / W4;  // r = plane*H + y
-    const int y = r % H, plane = r / H;
-    const int i = y >> 1;
-    if (i >= OH) continue;
-    const int64_t e0 = static_cast<int64_t>(r) * (4 * W4) + 4 * q;
-    float4 v = *reinterpret_cast<const float4*>(dIn + e0);
-    float w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int j = 2 * q + h;
-      if (j >= OW) break;
-      const int64_t o = (static_cast<int64_t>(plane) * OH + i) * OW + j;
-      const int64_t k = idx[o];
-      const int64_t d = k - (e0 + 2 * h);
-      if (d == 0 || d == 1) w[2 * h + d] = w[2 * h + d] + delta[o];
-    }
-    *reinterpret_cast<float4*>(dIn + e0) = make_float4(w[0], w[1], w[2], w[3]);
+// Backward as the reference's scatter, dIn[idx[o]] += delta[o]
+// (TNNCuda.backwardMaxPool, nncuda.pas:1121), one thread per output with an
+// atomic add, skipping index -1.  Where the windows do not overlap (size <=
+// stride) each input element receives at most one delta, so the result is
+// the serial loop's bit for bit and needs no geometry; where two outputs
+// name one input, the order of their adds is unspecified (the gather below
+// keeps the serial order there).  Each thread reads its index and delta once
+// (coalesced) and touches only the element its index names.
+// ATOMIC: the adds are atomic (indexes whose geometry the library does not
+// know); otherwise plain read-modify-writes, for windows known not to
+// overlap, where no two threads name one element.
+template <bool ATOMIC>
+__global__ __launch_bounds__(kThreads) void maxpool_scatter_kernel(int64_t total, const int64_t* __restrict__ idx,
+                                                                   const float* __restrict__ delta,
+                                                                   float* __restrict__ dIn) {
+  GRID_STRIDE(o, total) {
+    const int64_t k = idx[o];
+    if (k < 0) continue;
+    if constexpr (ATOMIC)
+      atomicAdd(dIn + k, delta[o]);
+    else
+      dIn[k] = dIn[k] + delta[o];
   }
 }
 
@@ -168,12 +166,15 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(PoolGeom g, int64
     if (i1 < 0 || j1 < 0) continue;
     i1 = min(i1 / g.sY, g.OH - 1);
     j1 = min(j1 / g.sX, g.OW - 1);
-    float v = dIn[e];
+    // dIn is read and written only where an index names e, so the kernel
+    // touches no element that the scatter it replaces would not
+    float v = 0.f;
     bool hit = false;
     for (int64_t i = i0; i <= i1; ++i)
       for (int64_t j = j0; j <= j1; ++j) {
         const int64_t o = (plane * g.OH + i) * g.OW + j;
         if (idx[o] == e) {
+          if (!hit) v = dIn[e];
           v = v + delta[o];
           hit = true;
         }
@@ -327,7 +328,25 @@ bool pool2_fast(const PoolGeom& g, int64_t batch, const float* in, const float* 
          batch * g.C * g.H * g.W + 65536LL * kThreads < INT32_MAX;
 }
 
+// Forward geometry of the maxpool calls that wrote an indexes buffer, so
+// that the backward (which, like TNNCuda.backwardMaxPool, receives only the
+// output shape and the buffers) can run the gather in the reference's order.
+// Keyed by the indexes pointer; a later forward into the same buffer
+// replaces the entry.
+struct PoolRecord {
+  PoolGeom g;
+  int64_t batch;
+};
+std::mutex g_pool_mu;
+std::unordered_map<const int64_t*, PoolRecord> g_pool_geom;
+
 }  // namespace
+
+void pool_forget(const void* p) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool_geom.erase(static_cast<const int64_t*>(p));
+}
+
 }  // namespace tnh
 
 using namespace tnh;
@@ -347,6 +366,10 @@ extern "C" int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH, in
   const int64_t total = batch * outC * outH * outW;
   if (total == 0) return TNH_OK;
   PoolGeom g{c, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  if (indexes) {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    g_pool_geom[indexes] = PoolRecord{g, batch};
+  }
   if (pool2_fast(g, batch, input, output, indexes)) {
     const int tot = static_cast<int>(total / 2);
     if (w % 4 == 0 && al16(input))
@@ -364,28 +387,64 @@ extern "C" int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH, in
   return launch_status("maxpool_fwd_kernel");
 }
 
-extern "C" int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH, int64_t outW, int64_t h, int64_t w,
-                                   int64_t strideX, int64_t strideY, int64_t padding, int64_t kernelSize,
-                                   const int64_t* indexes, const float* delta, float* deltaIn) {
-  TNH_REQUIRE_CTX(cx);
-  TNH_ARG(batch >= 0 && outC > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 && padding >= 0,
-          "maxpool_bwd: bad geometry");
-  TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
-          "maxpool_bwd: output dims do not match the forward geometry");
-  TNH_ARG(indexes && delta && deltaIn, "maxpool_bwd: NULL buffer");
-  const int64_t total = batch * outC * h * w;
-  if (total == 0) return TNH_OK;
-  PoolGeom g{outC, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
-  if (pool2_fast(g, batch, deltaIn, delta, indexes) && w % 4 == 0 && al16(deltaIn)) {
-    const int tot = static_cast<int>(total / 4);
-    hipLaunchKernelGGL(maxpool2_bwd_kernel, dim3(grid_for(tot)), dim3(kThreads), 0, cx->stream, tot,
-                       static_cast<int>(h), static_cast<int>(w / 4), static_cast<int>(outH), static_cast<int>(outW),
+namespace {
+
+// Backward with a known forward geometry: windows that do not overlap
+// (size <= stride both ways) scatter (exact, no ordering needed); overlapping
+// ones gather in the serial order.
+int maxpool_bwd_known(Context* cx, int64_t batch, const PoolGeom& g, const int64_t* indexes, const float* delta,
+                      float* deltaIn) {
+  if (g.size <= g.sX && g.size <= g.sY) {
+    const int64_t total = batch * g.C * g.OH * g.OW;
+    if (total == 0) return TNH_OK;
+    hipLaunchKernelGGL(maxpool_scatter_kernel<false>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
                        indexes, delta, deltaIn);
-    return launch_status("maxpool2_bwd_kernel");
+    return launch_status("maxpool_scatter_kernel");
   }
+  const int64_t total = batch * g.C * g.H * g.W;
+  if (total == 0) return TNH_OK;
   hipLaunchKernelGGL(maxpool_bwd_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, g, total, indexes,
                      delta, deltaIn);
   return launch_status("maxpool_bwd_kernel");
+}
+
+}  // namespace
+
+extern "C" int32_t tnh_maxpool_bwd(int64_t batch, int64_t outC, int64_t outH, int64_t outW, float* output,
+                                   const int64_t* indexes, const float* delta) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && outC > 0 && outH > 0 && outW > 0, "maxpool_bwd: bad sizes");
+  TNH_ARG(indexes && delta && output, "maxpool_bwd: NULL buffer");
+  PoolRecord rec{};
+  bool known = false;
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    auto it = g_pool_geom.find(indexes);
+    if (it != g_pool_geom.end()) {
+      const PoolGeom& g = it->second.g;
+      known = g.C == outC && g.OH == outH && g.OW == outW && it->second.batch == batch;
+      rec = it->second;
+    }
+  }
+  if (known) return maxpool_bwd_known(cx, batch, rec.g, indexes, delta, output);
+  const int64_t total = batch * outC * outH * outW;
+  if (total == 0) return TNH_OK;
+  hipLaunchKernelGGL(maxpool_scatter_kernel<true>, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total,
+                     indexes, delta, output);
+  return launch_status("maxpool_scatter_kernel<atomic>");
+}
+
+extern "C" int32_t tnh_maxpool_bwd_geom(int64_t batch, int64_t outC, int64_t outH, int64_t outW, float* output,
+                                        const int64_t* indexes, const float* delta, int64_t h, int64_t w,
+                                        int64_t strideX, int64_t strideY, int64_t padding, int64_t kernelSize) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && outC > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 && padding >= 0,
+          "maxpool_bwd_geom: bad geometry");
+  TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
+          "maxpool_bwd_geom: output dims do not match the forward geometry");
+  TNH_ARG(indexes && delta && output, "maxpool_bwd_geom: NULL buffer");
+  const PoolGeom g{outC, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};
+  return maxpool_bwd_known(cx, batch, g, indexes, delta, output);
 }
 
 extern "C" int32_t tnh_upsample(int64_t batch, int64_t channels, int64_t h, int64_t w, float* in, int64_t stride,

@@ -195,6 +195,38 @@ struct RssOp {
   }
 };
 
+// second pass of tnh_variances: residual sum of squares about the caller's
+// means (TNNCuda.variances takes them as an argument, nncuda.pas:1350)
+struct RssGivenOp {
+  const float* x;
+  const float* means;
+  float m;
+  __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) { m = means[i]; }
+  __device__ void add(float* a, int64_t e) const {
+    const float d = x[e] - m;
+    a[0] = a[0] + d * d;
+  }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 v = ld4(x + e);
+    float d = v.x - m;
+    a[0] = a[0] + d * d;
+    d = v.y - m;
+    a[0] = a[0] + d * d;
+    d = v.z - m;
+    a[0] = a[0] + d * d;
+    d = v.w - m;
+    a[0] = a[0] + d * d;
+  }
+};
+
+// dst[i] = (the channel's fixed-order partial total) / div
+__global__ __launch_bounds__(64) void total_div_final(const float* part, ChanSplit s, float div, float* dst) {
+  __shared__ float sh[64];
+  const int64_t i = blockIdx.x;
+  const float t = fixed_total(part + i * s.P, s.P, sh);
+  if (threadIdx.x == 0) dst[i] = t / div;
+}
+
 __global__ __launch_bounds__(64) void means_vars_final(const float* part, ChanSplit s, float S, float* means,
                                                        float* vars, float* rollMean, float* rollVar, float keep,
                                                        float bm) {
@@ -593,6 +625,43 @@ extern "C" int32_t tnh_bn_statistics(int64_t srcSize, int64_t dstSize, int64_t g
                                      float* rollingVars, float momentum) {
   TNH_ARG((rollingMeans == nullptr) == (rollingVars == nullptr), "bn_statistics: give both rolling buffers or none");
   return means_vars_impl(srcSize, dstSize, groups, src, offset, means, vars, rollingMeans, rollingVars, momentum);
+}
+
+extern "C" int32_t tnh_means(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src, int64_t offset,
+                             float* means) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize > 0 && groups > 0 && srcSize > 0 && offset >= 0, "means: bad sizes");
+  TNH_ARG(src && means, "means: NULL buffer");
+  const int64_t block = srcSize / (dstSize * groups);
+  TNH_ARG(block * dstSize * groups == srcSize, "means: sizes do not align");
+  ChanSplit s;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
+  const float* x = src + offset;
+  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), red, cx->stream, "chan_partial_kernel<sum>"))
+    return st;
+  hipLaunchKernelGGL(total_div_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s,
+                     static_cast<float>(groups * block), means);
+  return launch_status("total_div_final");
+}
+
+extern "C" int32_t tnh_variances(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src, int64_t offset,
+                                 const float* means, float* vars) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(dstSize > 0 && groups > 0 && srcSize > 0 && offset >= 0, "variances: bad sizes");
+  TNH_ARG(src && means && vars, "variances: NULL buffer");
+  const int64_t block = srcSize / (dstSize * groups);
+  TNH_ARG(block * dstSize * groups == srcSize && groups * block > 1, "variances: sizes do not align");
+  ChanSplit s;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
+  const float* x = src + offset;
+  if (int st = launch_partial<1>(RssGivenOp{x, means, 0.f}, s, chan_vec(s, {x}), red, cx->stream,
+                                 "chan_partial_kernel<rss>"))
+    return st;
+  hipLaunchKernelGGL(total_div_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s,
+                     static_cast<float>(groups * block) - 1.f, vars);
+  return launch_status("total_div_final");
 }
 
 extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_t groups, const float* delta,

@@ -113,7 +113,8 @@ _PROTOS = {
     "tnh_copy": [i64, vp, i64, i64, vp, i64, i64],
     "tnh_route": [i64, i32, C.POINTER(vp), C.POINTER(i64), vp],
     "tnh_maxpool_fwd": [i64] * 4 + [vp] + [i64] * 7 + [vp, vp],
-    "tnh_maxpool_bwd": [i64] * 10 + [vp, vp, vp],
+    "tnh_maxpool_bwd": [i64] * 4 + [vp, vp, vp],
+    "tnh_maxpool_bwd_geom": [i64] * 4 + [vp, vp, vp] + [i64] * 6,
     "tnh_upsample": [i64, i64, i64, i64, vp, i64, i32, f32, vp, i32],
     "tnh_bn_normalize": [i64, vp, i64, i64, vp, vp, i64],
     "tnh_normalize": [i64, i64, i64, vp, i64, vp, i64, vp, i64],
@@ -124,6 +125,8 @@ _PROTOS = {
                             f32, i32, i32, i64, vp, vp, vp, vp],
     "tnh_yolo_nms_sort": [i64, i64, i64, vp, vp, vp, f32],
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
+    "tnh_means": [i64, i64, i64, vp, i64, vp],
+    "tnh_variances": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
     "tnh_normalize_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -230,7 +233,6 @@ class TNNHip:
     def __init__(self, deviceIndex=0):
         call("tnh_init", deviceIndex)
         self.deviceIndex = deviceIndex
-        self._pool_geom = {}
 
     # -- lifecycle -------------------------------------------------------
     def Destroy(self):
@@ -479,22 +481,21 @@ class TNNHip:
                        indexes, output):
         call("tnh_maxpool_fwd", aBatch, outC, outH, outW, addr(input), c, h, w, stride_x, stride_y, padding,
              kernelSize, addr(indexes), addr(output))
-        if indexes is not None:
-            self._pool_geom[addr(indexes)] = (h, w, stride_x, stride_y, padding, kernelSize)
 
     def backwardMaxPool(self, aBatch, outC, outH, outW, output, indexes, delta, geometry=None):
         """output = delta of the layer input (accumulated), as in the reference.
 
-        The gather formulation needs the forward geometry; it is remembered
-        from the forwardMaxPool call that filled ``indexes`` unless given as
-        ``geometry=(h, w, stride_x, stride_y, padding, kernelSize)``.
+        The library gathers in the reference's order with the geometry of the
+        forwardMaxPool call that wrote ``indexes``; ``geometry=(h, w,
+        stride_x, stride_y, padding, kernelSize)`` gives it explicitly
+        (tnh_maxpool_bwd_geom) for indexes written elsewhere.
         """
-        g = geometry or self._pool_geom.get(addr(indexes))
-        if g is None:
-            raise TNHError("tnh_maxpool_bwd", 2, "unknown forward geometry for these indexes")
-        h, w, sx, sy, pad, k = g
-        call("tnh_maxpool_bwd", aBatch, outC, outH, outW, h, w, sx, sy, pad, k, addr(indexes), addr(delta),
-             addr(output))
+        if geometry is None:
+            call("tnh_maxpool_bwd", aBatch, outC, outH, outW, addr(output), addr(indexes), addr(delta))
+            return
+        h, w, sx, sy, pad, k = geometry
+        call("tnh_maxpool_bwd_geom", aBatch, outC, outH, outW, addr(output), addr(indexes), addr(delta), h, w, sx,
+             sy, pad, k)
 
     def upSample(self, aBatch, aChannels, outHeight, outWidth, in_, stride, isForward, scale, out, zeroIn=0):
         call("tnh_upsample", aBatch, aChannels, outHeight, outWidth, addr(in_), stride, isForward, scale, addr(out),
@@ -551,6 +552,13 @@ class TNNHip:
 
     def meansAndVars(self, srcSize, dstSize, groups, src, offset, means, vars):
         call("tnh_means_vars", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
+
+    def means(self, srcSize, dstSize, groups, src, offset, means):
+        call("tnh_means", srcSize, dstSize, groups, addr(src), offset, addr(means))
+
+    def variances(self, srcSize, dstSize, groups, src, offset, means, vars):
+        """Unbiased variances about the given means (the CPU path's divisor)."""
+        call("tnh_variances", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
 
     def meansAndVarsDelta(self, srcSize, dstSize, groups, delta, x, offset, mean, variance, mean_delta,
                           variance_delta):

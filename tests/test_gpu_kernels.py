@@ -747,8 +747,25 @@ def test_maxpool_forward_backward_bit_exact(hip, size, stride, pad, shape):
     dIn0 = synth.normal(63, x.shape)
     ref = R.maxpool_bwd(idx, delta, dIn0.copy())
     ddIn = D(dIn0)
-    hip.backwardMaxPool(B, Cc, OH, OW, ddIn, didx, D(delta))
+    hip.backwardMaxPool(B, Cc, OH, OW, ddIn, didx, D(delta))  # TNNCuda's 7 arguments
     assert np.array_equal(H(ddIn, hip), ref)
+    # the same indexes in a buffer no forward wrote: with the geometry given
+    # (tnh_maxpool_bwd_geom), and, where windows do not overlap, without it
+    # (the scatter)
+    other = torch.empty(out.shape, dtype=torch.int64, device="cuda")
+    other.copy_(didx)
+    ddIn = D(dIn0)
+    hip.backwardMaxPool(B, Cc, OH, OW, ddIn, other, D(delta), geometry=(Hh, W, stride, stride, pad, size))
+    assert np.array_equal(H(ddIn, hip), ref)
+    if size <= stride:
+        hip.forwardMaxPool(B, Cc, OH, OW, D(x), Cc, Hh, W, stride, stride, pad, size, other, dout)
+        H(other, hip)
+        del other  # forget nothing: the buffer of a fresh allocation below may reuse the address
+        fresh = torch.empty(out.shape, dtype=torch.int64, device="cuda")
+        fresh.copy_(didx)
+        ddIn = D(dIn0)
+        hip.backwardMaxPool(B, Cc, OH, OW, ddIn, fresh, D(delta))
+        assert np.array_equal(H(ddIn, hip), ref)
 
 
 def test_maxpool_inference_no_indexes(hip):

@@ -356,3 +356,32 @@ def test_cifar_train_step_graph_replays_equal_eager(hip):
     finally:
         a.release_graph()
         hip.useTorchStream()
+
+
+@pytest.mark.parametrize("shape,off", [((128, 32, 32, 32), 0), ((3, 5, 33, 17), 1), ((64, 10, 1, 1), 0)])
+def test_means_then_variances(hip, shape, off):
+    """TNNCuda.means then TNNCuda.variances with those means, as
+    TBaseLayer.batchNormGPU calls them in training (nbaselayer.pas:583-584):
+    equal to meansAndVars bit for bit, and within the per-tensor bound of the
+    oracle (CPU MeansAndVars: the unbiased S - 1 divisor)."""
+    case(f"means + variances {shape} offset {off}")
+    B, Cc = shape[:2]
+    x = synth.normal(360, shape, 2.0) + np.float32(0.7)
+    m_ref, v_ref = T.means_vars(x, Cc, B)
+    dx = D(np.concatenate([np.zeros(off, np.float32), x.ravel()]))
+    dm, dv, dm2, dv2 = (torch.empty(Cc, dtype=torch.float32, device="cuda") for _ in range(4))
+    hip.means(x.size, Cc, B, dx, off, dm)
+    hip.variances(x.size, Cc, B, dx, off, dm, dv)
+    hip.meansAndVars(x.size, Cc, B, dx, off, dm2, dv2)
+    m, v = H(dm, hip), H(dv, hip)
+    assert np.array_equal(m, H(dm2, hip))
+    assert np.array_equal(v, H(dv2, hip))
+    assert R.rel_err(m, m_ref) <= TOL
+    assert R.rel_err(v, v_ref) <= TOL
+    # variances about means the caller supplies (not the batch's): the
+    # residual sum of squares about those values, / (S - 1)
+    shift = (m_ref + np.float32(0.25)).astype(np.float32)
+    hip.variances(x.size, Cc, B, dx, off, D(shift), dv)
+    xx = x.reshape(B, Cc, -1).astype(np.float64)
+    want = ((xx - shift.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2)) / (x.size // Cc - 1)
+    assert R.rel_err(H(dv, hip), want.astype(np.float32)) <= TOL

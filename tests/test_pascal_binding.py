@@ -5,25 +5,27 @@ the unit is checked structurally: every C entry point of
 include/tensorium_hip.h has exactly one `external` declaration with the same
 parameter count and matching types; every call the unit makes passes that
 many arguments; and TNNHip<T> declares every public method of the
-reference's TNNCuda<T> (nncuda.pas:100-157)."""
+reference's TNNCuda<T> (nncuda.pas:100-157) with the same signature."""
+import json
 import os
 import re
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+from pascal_sig import parse_methods  # noqa: E402
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "tensorium_hip.h")
 UNIT = os.path.join(ROOT, "pascal", "nnhip.pas")
 
-# public methods of TNNCuda<T>, nncuda.pas:100-157
-TNNCUDA_METHODS = [
-    "deviceCount", "Create", "Destroy", "CompileLog", "createDeviceBuffer", "freeDeviceBuffer", "readBuffer",
-    "writeBuffer", "ActivateArray", "activateArraySWISH", "DeriveArray", "forwardBias", "backwardBias", "gemm",
-    "gemmBatched", "gemmStridedBatched", "addvv", "subvv", "mulvv", "fmavv", "axpy", "power", "scale",
-    "crossEntropyLogistic", "fill", "copy", "softmaxBatch", "crossEntropySoftmax", "forwardMaxPool",
-    "backwardMaxPool", "im2col", "col2im", "upSample", "fmavss", "meansAndVars", "means", "variances", "normalize",
-    "meansAndVarsDelta", "normalizeDelta", "addDots", "forwardScale", "forwardScaleAdd", "forwardDropout",
-    "backwardDropout", "costL2", "clamp", "inverseSqrt", "finish", "compileToCUBIN", "loadCUBIN", "compileFile",
-    "loadCUBinFile",
-]
+# public method signatures of TNNCuda<T>, nncuda.pas:100-157, recorded by
+# tests/golden/make_tnncuda_signatures.py
+SIGNATURES = os.path.join(ROOT, "tests", "golden", "tnncuda_signatures.json")
+
+
+def tnncuda_methods():
+    return json.load(open(SIGNATURES))["methods"]
+
 
 C_TO_PAS = {
     "int32_t": "LongInt", "int64_t": "Int64", "float": "Single", "float*": "PSingle", "int64_t*": "PInt64",
@@ -124,15 +126,43 @@ def test_every_call_passes_the_declared_number_of_arguments():
     assert calls >= 50
 
 
-def test_tnnhip_declares_every_tnncuda_method():
+def tnnhip_methods():
     text = unit_text()
-    iface = text[text.index("TNNHip<T> = class"):text.index("implementation")]
-    declared = set(re.findall(r"(?:procedure|function|constructor|destructor)\s+(\w+)", iface))
-    missing = [m for m in TNNCUDA_METHODS if m not in declared]
-    assert not missing, missing
+    return parse_methods(text[text.index("TNNHip<T> = class"):text.index("implementation")])
+
+
+def test_tnnhip_declares_every_tnncuda_method_with_its_signature():
+    """Every public method of TNNCuda<T> is declared in TNNHip<T> with the
+    same kind, parameter names, modifiers (const / var), types, defaults and
+    order, and the same result type, so `cuda.` -> `hip.` compiles at every
+    call site; each is implemented."""
+    mine = {m["name"]: m for m in tnnhip_methods()}
+    ref = tnncuda_methods()
+    assert len(ref) == 53
+    for r in ref:
+        assert r["name"] in mine, "not declared: " + r["name"]
+        m = mine[r["name"]]
+        assert m["kind"] == r["kind"], (r["name"], m["kind"], r["kind"])
+        assert m["result"] == r["result"], (r["name"], m["result"], r["result"])
+        assert len(m["params"]) == len(r["params"]), (r["name"], m["params"], r["params"])
+        for i, (a, b) in enumerate(zip(m["params"], r["params"])):
+            assert a == b, (r["name"], i, a, b)
+    text = unit_text()
     impl = text[text.index("implementation"):]
-    for m in declared:
-        assert re.search(r"TNNHip<T>\.%s\b" % m, impl), "no implementation: " + m
+    for name in mine:
+        assert re.search(r"TNNHip<T>\.%s\b" % name, impl), "no implementation: " + name
+
+
+def test_signature_parser_catches_a_changed_parameter():
+    """The comparison above sees a parameter added, renamed or retyped."""
+    base = "procedure backwardMaxPool(const aBatch, outC: SizeInt; output: TCUMem; const indexes: TCUMem);"
+    ref = parse_methods(base)[0]
+    for variant in (base.replace("const indexes", "indexes"),
+                    base.replace("outC", "outChannels"),
+                    base.replace("output: TCUMem", "output: PSingle"),
+                    base.replace(");", "; const h: SizeInt);")):
+        assert parse_methods(variant)[0]["params"] != ref["params"], variant
+    assert ref["params"][0] == ["const", "abatch", "sizeint", ""]
 
 
 def test_unit_is_complete_text():
