@@ -446,6 +446,40 @@ def extra_batch1(hip, layers, weights, steps, warmup):
             "img_s": round(1e3 / ms, 2), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
 
 
+def extra_dropin(hip, layers, weights, steps, warmup, batch=16):
+    """YOLOv3-416 at batch 16 through the per-layer calls a Tensorium build
+    with the USE_HIP branches makes (TConvolutionalLayer.forwardGPU and the
+    shortcut, route, upsample and yolo GPU hooks): NCHW activations, one
+    tnh_conv2d_fwd per convolution with bias and activation fused, and a
+    separate launch for every shortcut (addvv), route copy, upsample and yolo
+    layer.  Three weight arrangements, each as a HIP graph replay:
+      reference_layout  the layer's weights as stored ([F][C][k][k],
+                        TNH_WEIGHTS_REFERENCE), as forwardGPU passes them;
+      packed_in_layer   a tap-major copy the layer packs once after
+                        fuseBatchNorm / each update (TNH_WEIGHTS_TAP_MAJOR);
+      packed_fused      the same with each shortcut folded into the preceding
+                        convolution's epilogue (darknet.Network's NCHW plan)."""
+    import torch
+
+    from tensorium_amd import darknet, synth
+
+    x = torch.from_numpy(synth.uniform(7, (batch, 3, 416, 416))).cuda()
+    flop = darknet.conv_flops(layers) * batch
+    out = {"workload": f"YOLOv3-416 fp32 inference, batch {batch}, NCHW, per-layer TNNHip calls"}
+    for name, fuse, pack in (("reference_layout", False, False), ("packed_in_layer", False, True),
+                             ("packed_fused", True, True)):
+        net = darknet.Network(hip, layers, batch, weights, fuse=fuse, pack=pack, layout="nchw")
+        torch.cuda.synchronize()
+        ms, _ = time_forward(hip, net, x, steps, warmup, graph=True)
+        ms /= steps
+        out[name] = {"ms_per_step": round(ms, 3), "img_s": round(batch / ms * 1e3, 1),
+                     "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+        del net
+        torch.cuda.empty_cache()
+    del x
+    return out
+
+
 def _bw_entry(name, ms, byts, copy_gbs):
     gbs = byts / ms / 1e6
     return {"kernel": name, "us": round(ms * 1e3, 2), "bytes": int(byts), "gb_s": round(gbs, 1),
@@ -703,7 +737,7 @@ def main():
                          "YOLOv3-608 batch 32) and the YOLOv3-tiny / detection / bandwidth figures")
     ap.add_argument("--only", choices=("single_conv_416", "sgemm", "train_cifar_b128", "yolov3_608_b32",
                                        "yolo_detect_nms_b16", "bandwidth", "batch1", "yolov3_tiny_416_b16",
-                                       "im2col_vs_fused"),
+                                       "im2col_vs_fused", "yolov3_416_b16_dropin"),
                     default=None,
                     help="run one secondary configuration alone and print its figures (for profiling runs)")
     ap.add_argument("--counter-pass", action="store_true",
@@ -749,6 +783,7 @@ def main():
             "yolo_detect_nms_b16": lambda: extra_detect(hip, layers, weights),
             "bandwidth": lambda: extra_bandwidth(hip),
             "im2col_vs_fused": lambda: extra_im2col_vs_fused(hip),
+            "yolov3_416_b16_dropin": lambda: extra_dropin(hip, layers, weights, args.steps, args.warmup),
             "batch1": lambda: extra_batch1(hip, layers, weights, args.steps, args.warmup),
             "yolov3_tiny_416_b16": lambda: extra_yolo(hip, tiny, darknet.synthetic_weights(tiny), args.steps,
                                                       args.warmup, batch=16, size=416, name="YOLOv3-tiny"),
@@ -830,6 +865,7 @@ def main():
         guarded("yolo_detect_nms_b16", lambda: extra_detect(hip, layers, weights))
         guarded("bandwidth", lambda: extra_bandwidth(hip))
         guarded("im2col_vs_fused", lambda: extra_im2col_vs_fused(hip))
+        guarded("yolov3_416_b16_dropin", lambda: extra_dropin(hip, layers, weights, 10, 2))
 
     out = {
         "metric": METRIC,

@@ -32,6 +32,9 @@ struct Context {
     size_t bytes;
   };
   std::vector<WsSlot> ws;
+  // Per-stream copies of reference-layout 3x3 weights repacked tap-major for
+  // the call being made (pack_buffer), same growth rules as ws.
+  std::vector<WsSlot> pk;
   // Outgrown scratch buffers: a graph captured earlier may still launch
   // kernels that address them, so they are freed only by tnh_finalize.
   std::vector<void*> wsRetired;
@@ -68,6 +71,10 @@ float* reduction_buffer(Context* c);
 // not possible (allocation failure, or the stream or the tuning stream is
 // being captured).
 void* workspace(Context* c, size_t bytes);
+
+// The current stream's weight-repacking buffer of at least `bytes`, grown
+// like workspace() (nullptr when it cannot be).
+void* pack_buffer(Context* c, size_t bytes);
 
 // Looks up, once per device and with that device current, the address of
 // the no-allocation entry point's static scratch on it (conv.hip); called by

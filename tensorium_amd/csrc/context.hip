@@ -83,9 +83,12 @@ bool capturing(const Context* c) {
           (hipStreamIsCapturing(c->tune_stream, &ts) != hipSuccess || ts != hipStreamCaptureStatusNone));
 }
 
-void* workspace(Context* c, size_t bytes) {
+namespace {
+
+// One growable buffer per stream in `slots`.
+void* stream_buffer(Context* c, std::vector<Context::WsSlot>& slots, size_t bytes) {
   Context::WsSlot* slot = nullptr;
-  for (Context::WsSlot& w : c->ws)
+  for (Context::WsSlot& w : slots)
     if (w.stream == c->stream) slot = &w;
   if (slot && bytes <= slot->bytes) return slot->ptr;
   // Nothing can be allocated under capture.  A stream without scratch of its
@@ -93,8 +96,8 @@ void* workspace(Context* c, size_t bytes) {
   // the scratch): borrowing another stream's would race when both run.
   if (capturing(c)) return nullptr;
   if (!slot) {
-    c->ws.push_back({c->stream, nullptr, 0});
-    slot = &c->ws.back();
+    slots.push_back({c->stream, nullptr, 0});
+    slot = &slots.back();
   }
   if (slot->ptr) {
     c->wsRetired.push_back(slot->ptr);
@@ -110,6 +113,12 @@ void* workspace(Context* c, size_t bytes) {
   slot->bytes = want;
   return slot->ptr;
 }
+
+}  // namespace
+
+void* workspace(Context* c, size_t bytes) { return stream_buffer(c, c->ws, bytes); }
+
+void* pack_buffer(Context* c, size_t bytes) { return stream_buffer(c, c->pk, bytes); }
 
 float* reduction_buffer(Context* c) {
   for (const Context::RedSlot& r : c->red)
@@ -132,6 +141,8 @@ float* reduction_buffer(Context* c) {
 // Frees every buffer of the context and destroys its streams.
 void release(Context& c) {
   for (const Context::WsSlot& w : c.ws)
+    if (w.ptr) (void)hipFree(w.ptr);
+  for (const Context::WsSlot& w : c.pk)
     if (w.ptr) (void)hipFree(w.ptr);
   for (void* p : c.wsRetired) (void)hipFree(p);
   for (const Context::RedSlot& r : c.red) (void)hipFree(r.ptr);

@@ -914,13 +914,17 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, int cus, hipS
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // [F][C][taps] -> [F][taps][C]
-__global__ void pack_weights_kernel(int64_t total, int64_t C, int64_t taps, const float* __restrict__ src,
+// dst[f][t][c] = src[f][c][t] over fc = F*C filter channels: thread q =
+// f*C + c reads its `taps` consecutive floats (a wave reads one contiguous
+// span) and writes them `C` apart (for each t, consecutive threads write
+// consecutive floats).
+__global__ void pack_weights_kernel(int64_t fc, int64_t C, int64_t taps, const float* __restrict__ src,
                                     float* __restrict__ dst) {
-  for (int64_t o = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; o < total; o += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t c = o % C;
-    const int64_t t = (o / C) % taps;
-    const int64_t f = o / (C * taps);
-    dst[o] = src[(f * C + c) * taps + t];
+  for (int64_t q = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; q < fc; q += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t f = q / C, c = q - f * C;
+    const float* s = src + q * taps;
+    float* d = dst + f * C * taps + c;
+    for (int64_t t = 0; t < taps; ++t) d[t * C] = s[t];
   }
 }
 
@@ -1376,10 +1380,9 @@ extern "C" int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int
                                            float* dst) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(F > 0 && C > 0 && kh > 0 && kw > 0 && src && dst && src != dst, "conv2d_pack_weights: bad arguments");
-  const int64_t total = F * C * kh * kw;
-  const int64_t blocks = (total + 255) / 256;
+  const int64_t blocks = (F * C + 255) / 256;
   hipLaunchKernelGGL(pack_weights_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
-                     cx->stream, total, C, kh * kw, src, dst);
+                     cx->stream, F * C, C, kh * kw, src, dst);
   return launch_status("pack_weights_kernel");
 }
 
@@ -1443,6 +1446,29 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
     mode = C % 16 == 0 ? kTap3 : kGatherTap3;
   else
     mode = kGatherRef3;
+  bool forced;
+  {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    forced = g_forced_cfg >= 0;
+  }
+  if (mode == kGatherRef3 && C % 16 == 0 && !forced) {
+    // Reference-layout 3x3 weights (as TConvolutionalLayer stores them): the
+    // call repacks them tap-major into the stream's packing buffer (one
+    // F*K-float read and write, in order before the convolution on the same
+    // stream) and runs the tap-major tiles, which read whole 16-channel
+    // chunks of one tap per panel.  Nothing is cached, so weights updated
+    // between calls need no notice.  Without the buffer (a stream captured
+    // before any eager call) the LDS-staged reference-layout tiles run.
+    if (float* pk = static_cast<float*>(pack_buffer(cx, static_cast<size_t>(F * K) * 4))) {
+      const int64_t blocks = (F * C + 255) / 256;
+      hipLaunchKernelGGL(pack_weights_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
+                         dim3(256), 0, cx->stream, F * C, C, kh * kw, a.w, pk);
+      if (int st = launch_status("pack_weights_kernel")) return st;
+      a.w = pk;
+      a.g.tapW = true;
+      mode = kTap3;
+    }
+  }
   const bool va = aligned16(a.w) && K % 4 == 0;
   // the buffer-store epilogue of the lean kernels addresses out, residual and
   // one split's partial sums through 2 GiB buffer resources
@@ -1452,11 +1478,6 @@ extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W
   if (kh == 3 && kw == 3 && C <= 4 && N / 256 < INT32_MAX) {
     // few input channels: per-pixel kernel (no tile choice to tune); a forced
     // tile configuration still selects the GEMM path (tests of every tile)
-    bool forced;
-    {
-      std::lock_guard<std::mutex> lk(g_tune_mu);
-      forced = g_forced_cfg >= 0;
-    }
     if (!forced)
       return weightLayout == TNH_WEIGHTS_TAP_MAJOR ? launch_smallc<true, false>(a, cx->stream)
                                                    : launch_smallc<false, false>(a, cx->stream);

@@ -347,6 +347,48 @@ def test_conv_forward_vs_oracle(hip, B, Cc, Hh, F, k, s, p, act):
     assert R.rel_err(H(dout, hip), ref) <= TOL
 
 
+@pytest.mark.parametrize("B,Cc,Hh,F,s,res", [(2, 64, 20, 96, 1, False), (3, 32, 17, 64, 2, False),
+                                             (1, 128, 13, 256, 1, True)])
+def test_conv_reference_layout_repacks(hip, B, Cc, Hh, F, s, res):
+    """A 3x3 call with reference-layout weights ([F][C][3][3], as the layer
+    stores them) repacks them tap-major for the call and runs the tap-major
+    tiles: bit-identical to a call with weights packed by packConvWeights
+    (same kernel, same tuned tile), within the bound of the oracle, and the
+    caller's weights are left as they were.  A second call after the weights
+    change sees the new weights (nothing is cached)."""
+    case(f"conv reference layout repacked B{B} C{Cc} H{Hh} F{F} s{s} residual={res}")
+    x = synth.uniform(47, (B, Cc, Hh, Hh))
+    Wt = synth.normal(48, (F, Cc * 9), (2.0 / (Cc * 9)) ** 0.5)
+    b = synth.normal(49, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, 3, s, 1, acLEAKY)
+    OH = ref.shape[2]
+    r = synth.uniform(50, ref.shape, -1, 1) if res else None
+    if res:
+        ref = (ref + r).astype(np.float32)
+    dx, dW, db = D(x), D(Wt), D(b)
+    dr = D(r) if res else None
+    packed = torch.empty_like(dW)
+    hip.packConvWeights(F, Cc, 3, dW, packed)
+    outs = []
+    for w, layout in ((packed, WEIGHTS_TAP_MAJOR), (dW, 0)):
+        dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+        hip.conv2dForward(B, Cc, Hh, Hh, F, 3, s, 1, dx, 0, w, db, acLEAKY, dout, 0, weightLayout=layout,
+                          residual=dr)
+        outs.append(H(dout, hip))
+    assert np.array_equal(outs[0], outs[1])
+    assert R.rel_err(outs[1], ref) <= TOL
+    assert np.array_equal(H(dW, hip), Wt)
+    W2 = (Wt * np.float32(-0.5)).astype(np.float32)
+    dW.copy_(torch.from_numpy(W2))
+    dout = torch.empty(ref.shape, dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, Cc, Hh, Hh, F, 3, s, 1, dx, 0, dW, db, acLEAKY, dout, 0, weightLayout=0, residual=dr)
+    ref2 = R.conv_forward(x, W2, b, 3, s, 1, acLEAKY)
+    if res:
+        ref2 = (ref2 + r).astype(np.float32)
+    assert R.rel_err(H(dout, hip), ref2) <= TOL
+    assert OH > 0
+
+
 @pytest.mark.parametrize("cfg", range(NUM_CONV_NCHW_CFGS))
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", [(2, 32, 26, 64, 3, 1, 1, acLEAKY), (1, 64, 13, 96, 3, 2, 1, acLEAKY),
                                                  (2, 48, 11, 40, 3, 1, 1, acLINEAR), (1, 3, 20, 16, 3, 1, 1, acLEAKY),
