@@ -35,6 +35,10 @@ struct Context {
   // Per-stream copies of reference-layout 3x3 weights repacked tap-major for
   // the call being made (pack_buffer), same growth rules as ws.
   std::vector<WsSlot> pk;
+  // Per-stream arrival counters of the conv kernels' in-kernel tail
+  // reductions (kTileCounters ints each), zeroed when allocated; every
+  // launch that uses them leaves them zero.
+  std::vector<WsSlot> cnt;
   // Outgrown scratch buffers: a graph captured earlier may still launch
   // kernels that address them, so they are freed only by tnh_finalize.
   std::vector<void*> wsRetired;
@@ -71,6 +75,13 @@ float* reduction_buffer(Context* c);
 // not possible (allocation failure, or the stream or the tuning stream is
 // being captured).
 void* workspace(Context* c, size_t bytes);
+
+constexpr int64_t kTileCounters = int64_t(1) << 16;
+
+// The current stream's tail-tile arrival counters (kTileCounters ints, all
+// zero between launches), or nullptr when the stream has none and they
+// cannot be allocated now (allocation failure, or a capture in progress).
+int* tile_counters(Context* c);
 
 // The current stream's weight-repacking buffer of at least `bytes`, grown
 // like workspace() (nullptr when it cannot be).

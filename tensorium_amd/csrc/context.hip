@@ -120,6 +120,26 @@ void* workspace(Context* c, size_t bytes) { return stream_buffer(c, c->ws, bytes
 
 void* pack_buffer(Context* c, size_t bytes) { return stream_buffer(c, c->pk, bytes); }
 
+int* tile_counters(Context* c) {
+  for (const Context::WsSlot& w : c->cnt)
+    if (w.stream == c->stream) return static_cast<int*>(w.ptr);
+  if (capturing(c)) return nullptr;
+  void* p = nullptr;
+  const size_t bytes = static_cast<size_t>(kTileCounters) * sizeof(int);
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  // zeroed in stream order, before any kernel of this stream uses them
+  if (hipMemsetAsync(p, 0, bytes, c->stream) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(p);
+    return nullptr;
+  }
+  c->cnt.push_back({c->stream, p, bytes});
+  return static_cast<int*>(p);
+}
+
 float* reduction_buffer(Context* c) {
   for (const Context::RedSlot& r : c->red)
     if (r.stream == c->stream) return r.ptr;
@@ -143,6 +163,8 @@ void release(Context& c) {
   for (const Context::WsSlot& w : c.ws)
     if (w.ptr) (void)hipFree(w.ptr);
   for (const Context::WsSlot& w : c.pk)
+    if (w.ptr) (void)hipFree(w.ptr);
+  for (const Context::WsSlot& w : c.cnt)
     if (w.ptr) (void)hipFree(w.ptr);
   for (void* p : c.wsRetired) (void)hipFree(p);
   for (const Context::RedSlot& r : c.red) (void)hipFree(r.ptr);

@@ -696,6 +696,7 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
   } else {
     a.tailSplits = 0;
   }
+  if (a.tailSplits == 0 || tiles - a.nFull > kTileCounters) a.tileCount = nullptr;
   if (mode == kTap3)
     hipLaunchKernelGGL((conv_lean_kernel<Cfg, kTap3, false>), grid, dim3(Cfg::NT), 0, s, a);
   else if (vb)
@@ -703,7 +704,7 @@ int launch_lean(ConvArgs a, int mode, bool vb, int cus, hipStream_t s) {
   else
     hipLaunchKernelGGL((conv_lean_kernel<Cfg, k1x1, false>), grid, dim3(Cfg::NT), 0, s, a);
   if (int st = launch_status("conv_lean_kernel")) return st;
-  if (a.tailSplits > 0) {
+  if (a.tailSplits > 0 && !a.tileCount) {
     hipLaunchKernelGGL((conv_tail_reduce<Cfg>), dim3(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64))),
                        dim3(64), 0, s, a);
     return launch_status("conv_tail_reduce");
@@ -801,6 +802,7 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
   } else {
     a.tailSplits = 0;
   }
+  if (a.tailSplits == 0 || tiles - a.nFull > kTileCounters) a.tileCount = nullptr;
   const bool var = a.upS > 0 || a.yolo;  // epilogue variant: its own instantiations
   const dim3 g(static_cast<unsigned>(grid)), nt(Cfg::NT);
   if (mode == kTap3 && var)
@@ -812,7 +814,7 @@ int launch_nhwc(ConvArgs a, int mode, int cus, hipStream_t s) {
   else
     hipLaunchKernelGGL((conv_nhwc_kernel<Cfg, k1x1>), g, nt, 0, s, a);
   if (int st = launch_status("conv_nhwc_kernel")) return st;
-  if (a.tailSplits > 0) {
+  if (a.tailSplits > 0 && !a.tileCount) {
     const dim3 rg(static_cast<unsigned>((tiles - a.nFull) * (Cfg::NT / 64)));
     if (var)
       hipLaunchKernelGGL((conv_tail_reduce<Cfg, true, true>), rg, dim3(64), 0, s, a);
@@ -1065,18 +1067,23 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
     if (fixed) return n <= kNoAllocScratchFloats ? fixed : nullptr;
     return static_cast<float*>(workspace(cx, static_cast<size_t>(n) * 4));
   };
+  // arrival counters of the in-kernel tail reduction (not for the
+  // no-allocation entry point, whose tail splits reduce in a second launch)
+  int* counters = fixed ? nullptr : tile_counters(cx);
   auto runOn = [&](const Cand& c, hipStream_t s) -> int {
     ConvArgs b = a;
     b.splits = 1;
     b.tailSplits = 0;
     b.tailUnit = 0;
     b.part = nullptr;
+    b.tileCount = nullptr;
     if (c.splits > 1 || c.tail > 0) {
       b.part = wsFor(c);
       if (b.part) {
         b.splits = c.splits;
         b.tailSplits = c.tail;
         b.tailUnit = c.tail > 0 ? static_cast<int>(unitOf(c)) : 0;  // -1: every tile
+        b.tileCount = c.tail > 0 ? counters : nullptr;
       }
     }
     return nhwc ? launch_nhwc_cfg(c.cfg, b, mode, cus, s) : launch(c.cfg, b, mode, va, vb, cus, s);

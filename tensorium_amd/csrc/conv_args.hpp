@@ -37,6 +37,11 @@ struct ConvArgs {
   int tailSplits;
   int nFull;
   int tailUnit;  // host only: tiles per whole round (the CU count, or CUs x resident workgroups)
+  // One arrival counter per tail tile (zero between launches), or nullptr.
+  // With counters the workgroup that stores a tail tile's last piece sums
+  // the tile's pieces and runs the epilogue itself; without them a second
+  // launch (conv_tail_reduce) does.
+  int* tileCount;
   // Channels-last (NHWC) tensors: floats between consecutive pixels of x, out
   // and res (the channel count of the buffer a tensor lives in, so a tensor
   // can be a channel slice of a wider one); images are H*W*pixel-stride apart.

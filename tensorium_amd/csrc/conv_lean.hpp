@@ -570,6 +570,26 @@ struct LeanLoop {
     read(lds, 0, L, f0);
   }
 
+  __device__ static inline void add(f32x16 (&acc)[FM][FN], const f32x16 (&g)[FM][FN]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = acc[i][j][e] + g[i][j][e];
+  }
+
+  // Two-level sum over K: the MFMAs of each pair of panels (64 k) accumulate
+  // from zero into g, which is then added to acc (the last partial sum may
+  // hold up to three panels).  The matrix cores round
+  // every step of a running sum; a long K (4608 in YOLOv3) summed in one
+  // chain carries a rounding error several times that of 72 partial sums of
+  // 64 products added in order, and that error compounds over a network's
+  // layers (the CPU reference's own rounding is of the single-chain size,
+  // so the GPU result's distance to it is mostly the reference's).
+  // Measured on YOLOv3 against a float64 evaluation: head convolutions
+  // 3.5-8.3e-6 -> 0.8-2.2e-6 (per tensor), batch-16 forward +0.8% (flushing
+  // every 4 or 8 panels was no faster and less accurate).
   __device__ static inline void exec(AL& al, BL& bl, int64_t kBegin, int64_t nk, lds_t* lds,
                                      f32x16 (&acc)[FM][FN]) {
     const Lanes L = lanes();
@@ -577,22 +597,27 @@ struct LeanLoop {
     if (nk <= 0) return;
     Frag f0, f1;
     prologue(al, bl, kBegin, nk, lds, L, f0);
+    f32x16 g[FM][FN];
+    zero(g);
     int64_t p = 0;
     for (; p + 3 < nk; p += 2) {
-      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, acc);
-      panel<1, true, true>(al, bl, kBegin + (p + 3) * BK, lds, f0, f1, L, acc);
+      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, g);
+      panel<1, true, true>(al, bl, kBegin + (p + 3) * BK, lds, f0, f1, L, g);
+      add(acc, g);
+      zero(g);
     }
     const int64_t rest = nk - p;  // 1, 2 or 3 panels left; p is even (stage 0)
     if (rest == 3) {
-      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, acc);
-      panel<1, true, false>(al, bl, 0, lds, f0, f1, L, acc);
-      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+      panel<0, true, true>(al, bl, kBegin + (p + 2) * BK, lds, f0, f1, L, g);
+      panel<1, true, false>(al, bl, 0, lds, f0, f1, L, g);
+      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, g);
     } else if (rest == 2) {
-      panel<0, true, false>(al, bl, 0, lds, f0, f1, L, acc);
-      panel<1, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+      panel<0, true, false>(al, bl, 0, lds, f0, f1, L, g);
+      panel<1, false, false>(al, bl, 0, lds, f0, f1, L, g);
     } else {
-      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, acc);
+      panel<0, false, false>(al, bl, 0, lds, f0, f1, L, g);
     }
+    add(acc, g);
   }
 };
 
@@ -637,6 +662,79 @@ __device__ inline void store_piece(float* dst, int wave, int lane, const f32x16 
       }
 }
 
+// Sums the P pieces of one tail tile (src: piece 0 of the tile) in K order,
+// piece 0 first, into the accumulator registers of `wave` that the conv
+// kernel would have held.  The loads of G pieces are issued together (one
+// memory round trip per G pieces instead of per piece); the sum still runs
+// in piece order, so the result does not depend on which workgroup sums.
+// SYS: the loads are system-scope (they read the pieces where the pieces'
+// write-through stores put them, past any copy in this XCD's caches), for a
+// reduction inside the kernel that wrote them.
+template <class Cfg, bool SYS = false>
+__device__ inline void sum_pieces(const float* src, int P, int wave, int lane, f32x16 (&acc)[Cfg::FM][Cfg::FN]) {
+  constexpr int TILE = Cfg::BM * Cfg::BN;
+  constexpr int G = Cfg::FM * Cfg::FN <= 2 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, static_cast<int64_t>(P) * TILE * 4);
+  for (int s0 = 0; s0 < P; s0 += G) {
+    f32x4 part[G][Cfg::FM][Cfg::FN][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t base = static_cast<int64_t>(s0 + g < P ? s0 + g : P - 1) * TILE;
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t e = base + piece_quad<Cfg>(wave, lane, i, j, q);
+            if constexpr (SYS)
+              part[g][i][j][q] = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<uint32_t>(e) * 4u, 0, kStoreThrough));
+            else
+              part[g][i][j][q] = *reinterpret_cast<const f32x4*>(src + e);
+          }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (s0 + g >= P) break;  // uniform
+#pragma unroll
+      for (int i = 0; i < Cfg::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = part[g][i][j][r >> 2][r & 3];
+            acc[i][j][r] = s0 + g == 0 ? v : acc[i][j][r] + v;
+          }
+    }
+  }
+}
+
+// A piece's workgroup, after storing its piece, counts itself in tile t's
+// arrival counter; returns true in every thread of the workgroup that
+// arrives last, which then owns the tile's reduction and epilogue and has
+// reset the counter to 0 for the next launch.  The pieces are stored
+// write-through at system scope (store_piece), so once each wave's stores
+// have completed (s_waitcnt 0, before the barrier that precedes thread 0's
+// increment) they are in memory; the last workgroup reads them back with
+// system-scope loads (sum_pieces<Cfg, true>), which fetch from memory past
+// its XCD's caches.  An agent-scope fence pair would do the same at the cost
+// of an L2 write-back per piece and an L2 invalidation under the workgroups
+// still running on that XCD (measured: +0.45 ms per batch-16 YOLOv3
+// forward).  No workgroup waits for another.
+__device__ inline bool tail_arrive(const ConvArgs& a, int t, int* flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int before = __hip_atomic_fetch_add(a.tileCount + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before == a.tailSplits - 1;
+    if (last) __hip_atomic_store(a.tileCount + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  return *flag != 0;
+}
+
 template <class Cfg, int MODE, bool VB>
 __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a) {
   using AL = LeanA<Cfg>;
@@ -668,7 +766,12 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_lean_kernel(ConvArgs a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (piece >= 0) {
     store_piece<Cfg>(a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN), wave, lane, acc);
-    return;
+    if (!a.tileCount) return;
+    __shared__ int lastFlag;
+    const int t = tile - a.nFull;
+    if (!tail_arrive(a, t, &lastFlag)) return;
+    sum_pieces<Cfg, true>(a.part + static_cast<int64_t>(t) * a.tailSplits * (Cfg::BM * Cfg::BN), a.tailSplits,
+                          wave, lane, acc);
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   conv_store_buf<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
@@ -690,38 +793,8 @@ __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
   const int lane = threadIdx.x, wave = blockIdx.x - t * NW;
   constexpr int TILE = Cfg::BM * Cfg::BN;
   const int P = a.tailSplits;
-  const float* src = a.part + static_cast<int64_t>(t) * P * TILE;
-  // The loads of G pieces are issued together (one memory round trip per G
-  // pieces instead of per piece); the sum still runs in piece order.
-  constexpr int G = Cfg::FM * Cfg::FN <= 2 ? 4 : 2;
   f32x16 acc[Cfg::FM][Cfg::FN];
-  for (int s0 = 0; s0 < P; s0 += G) {
-    f32x4 part[G][Cfg::FM][Cfg::FN][4];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float* ps = src + static_cast<int64_t>(s0 + g < P ? s0 + g : P - 1) * TILE;
-#pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            part[g][i][j][q] = *reinterpret_cast<const f32x4*>(ps + piece_quad<Cfg>(wave, lane, i, j, q));
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      if (s0 + g >= P) break;  // uniform
-#pragma unroll
-      for (int i = 0; i < Cfg::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::FN; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float v = part[g][i][j][r >> 2][r & 3];
-            acc[i][j][r] = s0 + g == 0 ? v : acc[i][j][r] + v;
-          }
-    }
-  }
+  sum_pieces<Cfg>(a.part + static_cast<int64_t>(t) * P * TILE, P, wave, lane, acc);
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   if constexpr (NHWC)
     conv_store_nhwc<Cfg::FM, Cfg::FN, VAR>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
@@ -734,7 +807,8 @@ __global__ __launch_bounds__(64) void conv_tail_reduce(ConvArgs a) {
 // themselves), columns are filters (B: the tap-major weights [F][K], k
 // contiguous), so both operands load 16 bytes along k and the epilogue
 // writes 32 consecutive channels of a pixel per half-wave.  Tail split as in
-// conv_lean_kernel (nFull may be 0: every tile cut into K pieces).  The Any
+// conv_lean_kernel (nFull may be 0: every tile cut into K pieces; with
+// ConvArgs::tileCount the last piece's workgroup reduces the tile).  The Any
 // modes (C % 32 != 0) take ceil(K / BK) panels with the K tail reading 0, and
 // no tail split.  VAR: the instantiation for the epilogue variants (an
 // upsampled output or a yolo head; the plain kernels carry no code for them).
@@ -780,7 +854,12 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_nhwc_kernel(ConvArgs a
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (!ANY && piece >= 0) {
     store_piece<Cfg>(a.part + static_cast<int64_t>(piece) * (Cfg::BM * Cfg::BN), wave, lane, acc);
-    return;
+    if (!a.tileCount) return;
+    __shared__ int lastFlag;
+    const int t = tile - a.nFull;
+    if (!tail_arrive(a, t, &lastFlag)) return;
+    sum_pieces<Cfg, true>(a.part + static_cast<int64_t>(t) * a.tailSplits * (Cfg::BM * Cfg::BN), a.tailSplits, wave,
+                    lane, acc);
   }
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   conv_store_nhwc<Cfg::FM, Cfg::FN, VAR>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
