@@ -219,6 +219,25 @@ def head_parity(gpu_heads, ref_heads):
             "metric": "max|gpu - oracle| / max|oracle| per head tensor (pre-logistic conv output)"}
 
 
+def cpu_timed(fn, budget_s):
+    """Calls fn() once to warm up, then until ~budget_s have passed; returns
+    (seconds per call, calls)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_info(threads):
+    _, nproc, avail, model = baseline_threads()
+    return {"cores": threads, "kind": "port", "nproc": nproc, "cpus_available": avail, "cpu_model": model,
+            "P": threads}
+
+
 COPY_BYTES = 64 << 20
 
 
@@ -263,9 +282,11 @@ def time_graph(hip, fn, reps):
     return best
 
 
-def extra_single_conv(hip):
+def extra_single_conv(hip, cpu_budget=0.0):
     """Config 1: one conv layer forward, batch 1, 3x416x416 -> 16 filters 3x3
-    s1 p1, weights N(0, 0.05), bias 0, leaky 0.1 (GEMM M=16, N=173056, K=27)."""
+    s1 p1, weights N(0, 0.05), bias 0, leaky 0.1 (GEMM M=16, N=173056, K=27);
+    with cpu_budget > 0 the CPU oracle's forward of the same layer (im2col,
+    sgemm, bias, leaky) timed beside it."""
     import numpy as np
     import torch
 
@@ -287,11 +308,25 @@ def extra_single_conv(hip):
     ms = time_graph(hip, fn, 50)
     flop = 2.0 * 16 * 27 * 416 * 416
     byts = 4.0 * (3 * 416 * 416 + 16 * 416 * 416 + 16 * 27)
+    out = {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "launch": "hip_graph",
+           "us": round(ms * 1e3, 2), "us_eager": round(eager * 1e3, 2),
+           "gflops": round(flop / ms / 1e6, 1), "gb_s": round(byts / ms / 1e6, 1),
+           "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4)}
+    if cpu_budget > 0:
+        from oracle import refcpu as R
+        from tensorium_amd import synth as S
+        from tensorium_amd.nnhip import acLEAKY as LK
+
+        threads = baseline_threads()[0]
+        R.set_threads(threads)
+        xh, wh = S.uniform(1, (1, 3, 416, 416)), S.normal(2, (16, 27), 0.05)
+        bh = np.zeros(16, np.float32)
+        sec, n = cpu_timed(lambda: R.conv_forward(xh, wh, bh, 3, 1, 1, LK), cpu_budget)
+        out["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us/layer", "gflops": round(flop / sec / 1e9, 2),
+                               "sample": f"the same layer x{n} on the CPU oracle (im2col + AVX2 sgemm + bias + leaky)",
+                               **cpu_info(threads)}
     del np
-    return {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "launch": "hip_graph",
-            "us": round(ms * 1e3, 2), "us_eager": round(eager * 1e3, 2),
-            "gflops": round(flop / ms / 1e6, 1), "gb_s": round(byts / ms / 1e6, 1),
-            "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4)}
+    return out
 
 
 SGEMM_SQUARES = (512, 1024, 2048, 4096, 8192)
@@ -300,13 +335,14 @@ SGEMM_SKINNY = ((64, 692224, 288), (128, 173056, 576), (256, 43264, 1152), (512,
                 (1024, 2704, 4608))
 
 
-def extra_sgemm(hip):
+def extra_sgemm(hip, cpu_budget=0.0):
     """Config 2: C = alpha*op(A)*op(B) + beta*C with A and B ~ U[-1, 1):
     the four NN/NT/TN/TT variants at M = N = K in 512 .. 8192 (beta 0), the
     conv-shaped skinny GEMMs (NN, beta 0) and one alpha = 0.5 / beta = 1 run
     at 4096^3, each timed as a graph replay after the first (tuning) call.
     Operands are cut from one seeded U[-1, 1) pool of 2^26 floats (copied
     on the device where a matrix is larger)."""
+    import numpy as np
     import torch
 
     from tensorium_amd import synth
@@ -351,7 +387,26 @@ def extra_sgemm(hip):
     bufs.clear()
     del pool
     torch.cuda.empty_cache()
-    return res
+    if cpu_budget <= 0:
+        return res
+    # the CPU oracle's sgemm (saxpy_avx2 row workers, rows chunked over P
+    # threads) on a row sample of the 4096^3 NN product: every row of C is
+    # the same work, so the sample's rate is the whole product's rate
+    from oracle import refcpu as R
+
+    threads = baseline_threads()[0]
+    R.set_threads(threads)
+    n, rows = 4096, 4 * threads
+    A = synth.uniform(11, (rows, n), -1, 1)
+    Bm = synth.uniform(12, (n, n), -1, 1)
+    Cm = np.zeros((rows, n), np.float32)
+    sec, calls = cpu_timed(lambda: R.sgemm(0, 0, rows, n, n, 1.0, A, n, Bm, n, 0.0, Cm, n), cpu_budget)
+    gf = 2.0 * rows * n * n / sec / 1e9
+    cpu = {"value": round(gf, 2), "unit": "GFLOP/s", "full_gemm_s": round(2.0 * n ** 3 / (gf * 1e9), 2),
+           "sample": f"NN sgemm, {rows} of 4096 rows of A (M={rows}, N=K=4096) x{calls} on the CPU oracle; "
+                     "full_gemm_s = the 4096^3 product at that rate (rows are independent and equal work)",
+           **cpu_info(threads)}
+    return {"cases": res, "cpu_baseline": cpu}
 
 
 def extra_train(hip, steps, warmup, cpu_steps):
@@ -396,22 +451,24 @@ def extra_train(hip, steps, warmup, cpu_steps):
 
         threads, nproc, avail, model = baseline_threads()
         R.set_threads(threads)
-        ref = T.CifarStep(params)
+        ref = T.CifarStep(params, avx2=True)  # the reference's routines on an AVX2 host
         ref.step(x, truth)
         t0 = time.perf_counter()
         for _ in range(cpu_steps):
             ref.step(x, truth)
         cms = (time.perf_counter() - t0) / cpu_steps * 1e3
         out["cpu_baseline"] = {"value": round(cms, 1), "unit": "ms/step", "cores": R.get_threads(), "kind": "port",
-                               "sample": f"{cpu_steps} oracle steps (C AVX2 GEMM/im2col/col2im + numpy BN/softmax)",
+                               "sample": f"{cpu_steps} oracle steps (C restatement: AVX2 GEMM, im2col/col2im, the AVX2 host's "
+                                         "batch-norm reductions, softmax)",
                                "nproc": nproc, "cpus_available": avail, "cpu_model": model, "P": threads}
     return out
 
 
-def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608, name="YOLOv3"):
+def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608, name="YOLOv3", cpu_budget=0.0):
     """Config 5: YOLOv3-608 inference at batch 32 (HIP graph replay); also
     YOLOv3-tiny-416 at batch 16 (channels-last with maxpools and a
-    16-channel convolution input)."""
+    16-channel convolution input).  With cpu_budget > 0 the CPU oracle's
+    forward of image 0 (batch 1) is timed beside it."""
     import torch
 
     from tensorium_amd import darknet, synth
@@ -424,8 +481,21 @@ def extra_yolo(hip, layers608, weights608, steps, warmup, batch=32, size=608, na
     flop = darknet.conv_flops(layers608) * batch
     del net, x
     torch.cuda.empty_cache()
-    return {"workload": f"{name}-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
-            "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+    out = {"workload": f"{name}-{size} fp32 inference, batch {batch}", "ms_per_step": round(ms, 3),
+           "img_s": round(batch / ms * 1e3, 1), "conv_frac_fp32_mfma_peak": round(flop / ms * 1e3 / PEAK_FP32_MFMA, 4)}
+    if cpu_budget > 0:
+        from oracle import netref
+        from oracle import refcpu as R
+
+        threads = baseline_threads()[0]
+        R.set_threads(threads)
+        x1 = synth.uniform(9, (1, 3, size, size))
+        sec, n = cpu_timed(lambda: netref.forward(layers608, weights608, x1), cpu_budget)
+        out["cpu_baseline"] = {"value": round(1.0 / sec, 4), "unit": "img/s",
+                               "sample": f"{name}-{size} batch-1 forward (image 0 of the batch) x{n} on the CPU "
+                                         "oracle, BN folded; measured at batch 1, not extrapolated",
+                               **cpu_info(threads)}
+    return out
 
 
 def extra_batch1(hip, layers, weights, steps, warmup):
@@ -854,11 +924,12 @@ def main():
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
 
-        guarded("single_conv_416", lambda: extra_single_conv(hip))
-        guarded("sgemm", lambda: extra_sgemm(hip))
+        cb = 0.0 if args.no_cpu_baseline else 3.0
+        guarded("single_conv_416", lambda: extra_single_conv(hip, cb))
+        guarded("sgemm", lambda: extra_sgemm(hip, cb))
         guarded("train_cifar_b128", lambda: extra_train(hip, 50, 2, 0 if args.no_cpu_baseline else 2))
         _, l608 = darknet.load_cfg("yolov3.cfg", 608, 608)
-        guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2))
+        guarded("yolov3_608_b32", lambda: extra_yolo(hip, l608, weights, 5, 2, cpu_budget=cb))
         _, ltiny = darknet.load_cfg("yolov3-tiny.cfg")
         guarded("yolov3_tiny_416_b16", lambda: extra_yolo(hip, ltiny, darknet.synthetic_weights(ltiny), 20, 3,
                                                           batch=16, size=416, name="YOLOv3-tiny"))

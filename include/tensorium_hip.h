@@ -288,14 +288,15 @@ int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
                                 const float *src, float *dst);
 /* No reference counterpart: enable (1, default) or disable per-shape
  * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape:
- * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 6..10
- * register-direct, 11..19 lean software-pipelined, 20..26 wave-split: K of
- * one tile split over the waves of its workgroup, for 3x3 tap-major or 1x1
- * layers with C % 32 == 0; a shape invalid for the call falls back to the
+ * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 11..19 lean
+ * software-pipelined, 20..26 wave-split: K of one tile split over the waves
+ * of its workgroup, for 3x3 tap-major or 1x1 layers with C % 32 == 0; 6..10
+ * are retired and refused; a shape invalid for the call falls back to the
  * library's choice) and forcedConfig / 64 either the
  * split-K factor (0 or 1: none; up to 16) or a tail split (lean shapes only:
  * the tiles beyond the last whole round are cut into K pieces, summed in K
- * order by a second kernel): 18..31 = forcedConfig / 64 - 16 pieces with
+ * order by the workgroup that finishes a tile's last piece, or by a second
+ * kernel where the stream has no arrival counters): 18..31 = forcedConfig / 64 - 16 pieces with
  * rounds of one tile per CU, 34..47 = forcedConfig / 64 - 32 pieces with
  * rounds of one tile per resident workgroup slot; -1 lets the library
  * choose.  Autotuning times each candidate as a graph replay of a few

@@ -593,6 +593,216 @@ void ref_fuse_bn(int64_t F, int64_t filterSize, float *W, float *bias,
 }
 
 /* ------------------------------------------------------------------------
+ * training-mode batch norm: channel statistics and their deltas, addDots,
+ * softmax.  Two coherent configurations of the reference are restated:
+ *   avx2 = 1  the Makefile build on an AVX2 host (AVX2Support true): the
+ *             assembler routines vssum_avx2, srss, sVarinceDelta_avx, sdot;
+ *   avx2 = 0  the same build on a host without AVX2: the Pascal loops.
+ * srss and sVarinceDelta_avx drop the upper four lanes of their eight-lane
+ * accumulator when N % 8 == 0 (they fold lanes 4..7 into 0..3 only on the
+ * path that handles a remainder, ntensors.pas:1508-1513, 8738-8743, and
+ * reduce xmm0 alone otherwise), so on an AVX2 host the variances and
+ * variance deltas of blocks whose length is a multiple of 8 sum only the
+ * elements k with k % 8 < 4.  The parity target is the avx2 = 0 form (the
+ * definition the Pascal loops and TNNCuda's kernels compute).
+ * ---------------------------------------------------------------------- */
+
+/* vssum_avx2 (ntensors.pas:3530-3560): lane l sums a[8q + l]; the lanes
+ * fold t[l] = acc[l] + acc[l + 4], two haddps give (t0 + t1) + (t2 + t3),
+ * then the n % 8 tail is added in order. */
+static float vssum8(int64_t n, const float *a) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t q = n >> 3, j = 0;
+  for (int64_t i = 0; i < q; ++i, j += 8)
+    for (int l = 0; l < 8; ++l) acc[l] = acc[l] + a[j + l];
+  float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
+  float s = (t0 + t1) + (t2 + t3);
+  for (; j < n; ++j) s = s + a[j];
+  return s;
+}
+
+/* vsSumI's Pascal loop (ntensors.pas:3631-3633) */
+static float sum_scalar(int64_t n, const float *a) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) s = s + a[i];
+  return s;
+}
+
+/* The common tail of srss / sVarinceDelta_avx: with a remainder the upper
+ * lanes fold into the lower ones and the remainder terms add to lane 0 in
+ * order; with none lanes 4..7 are dropped; then two haddps. */
+static float lane_tail(float acc[8], const float *terms, int64_t r) {
+  float t0 = acc[0], t1 = acc[1], t2 = acc[2], t3 = acc[3];
+  if (r) {
+    t0 = t0 + acc[4];
+    t1 = t1 + acc[5];
+    t2 = t2 + acc[6];
+    t3 = t3 + acc[7];
+    for (int64_t i = 0; i < r; ++i) t0 = t0 + terms[i];
+  }
+  return (t0 + t1) + (t2 + t3);
+}
+
+/* srss (ntensors.pas:1493-1525): acc[l] += (mean - a)^2 (vsubps, vmulps,
+ * vaddps: separate roundings). */
+static float srss8(int64_t n, float mean, const float *a) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, tail[8];
+  int64_t q = n >> 3, j = 0, r = n & 7;
+  for (int64_t i = 0; i < q; ++i, j += 8)
+    for (int l = 0; l < 8; ++l) {
+      float d = mean - a[j + l];
+      acc[l] = acc[l] + d * d;
+    }
+  for (int64_t i = 0; i < r; ++i) {
+    float d = mean - a[j + i];
+    tail[i] = d * d;
+  }
+  return lane_tail(acc, tail, r);
+}
+
+/* vsRSS's Pascal loop (ntensors.pas:1655-1657): sqr(a - mean) in order */
+static float rss_scalar(int64_t n, float mean, const float *a) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    float d = a[i] - mean;
+    s = s + d * d;
+  }
+  return s;
+}
+
+/* sVarinceDelta_avx (ntensors.pas:8721-8756): acc[l] += (x - mean) * delta */
+static float var_delta8(int64_t n, float mean, const float *delta, const float *x) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, tail[8];
+  int64_t q = n >> 3, j = 0, r = n & 7;
+  for (int64_t i = 0; i < q; ++i, j += 8)
+    for (int l = 0; l < 8; ++l) {
+      float d = x[j + l] - mean;
+      acc[l] = acc[l] + d * delta[j + l];
+    }
+  for (int64_t i = 0; i < r; ++i) {
+    float d = x[j + i] - mean;
+    tail[i] = d * delta[j + i];
+  }
+  return lane_tail(acc, tail, r);
+}
+
+typedef struct {
+  const float *src, *delta, *x, *mean, *var;
+  float *o1, *o2;
+  int64_t nch, block, groups;
+  int avx2;
+} bn_ctx;
+
+/* MnV of TTensor.MeansAndVars (ntensors.pas:9119-9136) for channels [f, t] */
+static void mnv_range(int64_t f, int64_t t, void *p) {
+  const bn_ctx *c = (const bn_ctx *)p;
+  const float S = (float)(c->groups * c->block), S2 = (float)(c->groups * c->block - 1);
+  for (int64_t i = f; i <= t; ++i) {
+    float m = 0.0f, v = 0.0f;
+    for (int64_t b = 0; b < c->groups; ++b) {
+      const float *d = c->src + (i + b * c->nch) * c->block;
+      m = m + (c->avx2 ? vssum8(c->block, d) : sum_scalar(c->block, d));
+    }
+    m = m / S;
+    c->o1[i] = m;
+    for (int64_t b = 0; b < c->groups; ++b) {
+      const float *d = c->src + (i + b * c->nch) * c->block;
+      v = v + (c->avx2 ? srss8(c->block, m, d) : rss_scalar(c->block, m, d));
+    }
+    c->o2[i] = v / S2;
+  }
+}
+
+void ref_means_vars(const float *src, int64_t nch, int64_t block, int64_t groups, float *means, float *vars,
+                    int avx2) {
+  bn_ctx c = {src, NULL, NULL, NULL, NULL, means, vars, nch, block, groups, avx2};
+  par_for_chunked(mnv_range, 0, nch - 1, &c); /* mp.&For(MnV, 0, N) */
+}
+
+/* MnVD of sMeanAndVarianceDelta (ntensors.pas:8838-8865) for channels [f, t]:
+ * m sums the deltas (vsSumI); v sums delta * (x - mean) per block through
+ * sVarinceDelta_avx on AVX2 hosts, else in one Pascal loop over every block;
+ * mean_delta = m * (-1 / sqrt(max(var, eps))) in single precision,
+ * variance_delta = v * -0.5 * Power(max(var, eps), -1.5) with Power in double. */
+static void mnvd_range(int64_t f, int64_t t, void *p) {
+  const bn_ctx *c = (const bn_ctx *)p;
+  for (int64_t i = f; i <= t; ++i) {
+    float m = 0.0f, v = 0.0f;
+    const float mu = c->mean[i];
+    for (int64_t j = 0; j < c->groups; ++j) {
+      const int64_t idx = (i + j * c->nch) * c->block;
+      m = m + (c->avx2 ? vssum8(c->block, c->delta + idx) : sum_scalar(c->block, c->delta + idx));
+      if (c->avx2) {
+        v = v + var_delta8(c->block, mu, c->delta + idx, c->x + idx);
+      } else {
+        for (int64_t k = 0; k < c->block; ++k) {
+          float d = c->x[idx + k] - mu;
+          v = v + c->delta[idx + k] * d;
+        }
+      }
+    }
+    float vc = c->var[i] > 1e-6f ? c->var[i] : 1e-6f;
+    float r = -1.0f / sqrtf(vc);
+    c->o1[i] = m * r;
+    c->o2[i] = (float)((double)(v * -0.5f) * pow((double)vc, -1.5));
+  }
+}
+
+void ref_means_vars_delta(const float *delta, const float *x, const float *mean, const float *var, int64_t nch,
+                          int64_t block, int64_t groups, float *mean_delta, float *variance_delta, int avx2) {
+  bn_ctx c = {NULL, delta, x, mean, var, mean_delta, variance_delta, nch, block, groups, avx2};
+  par_for_chunked(mnvd_range, 0, nch - 1, &c);
+}
+
+/* TTensor.addDots (ntensors.pas:7783-7830): dst[i] += sum over groups of
+ * cblas_sdot of the channel's block (sdot_avx2 on AVX2 hosts, ntensors.pas:
+ * 12731, else the Pascal loop); one element per channel: one strided dot
+ * over the groups (cblas_sdot's loop, :2217-2219). */
+void ref_add_dots(float *dst, const float *a, const float *b, int64_t nch, int64_t block, int64_t groups,
+                  int avx2) {
+  for (int64_t i = 0; i < nch; ++i) {
+    if (block == 1) {
+      float s = 0.0f;
+      for (int64_t g = 0; g < groups; ++g) s = s + a[i + g * nch] * b[i + g * nch];
+      dst[i] = dst[i] + s;
+      continue;
+    }
+    float sum = 0.0f;
+    for (int64_t g = 0; g < groups; ++g) {
+      const int64_t idx = (i + g * nch) * block;
+      float d;
+      if (avx2) {
+        d = sdot8(block, a + idx, b + idx);
+      } else {
+        d = 0.0f;
+        for (int64_t k = 0; k < block; ++k) d = d + a[idx + k] * b[idx + k];
+      }
+      sum = sum + d;
+    }
+    dst[i] = dst[i] + sum;
+  }
+}
+
+/* softmax (nsoftmaxlayer.pas:81-105) over `rows` rows of n values:
+ * e = exp((x - largest) / temp) with exp in double and e stored as single,
+ * sum accumulated in order in single, out = e / sum. */
+void ref_softmax_rows(const float *x, int64_t rows, int64_t n, float temp, float *out) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *in = x + r * n;
+    float *o = out + r * n;
+    float largest = in[0], sum = 0.0f;
+    for (int64_t i = 1; i < n; ++i)
+      if (in[i] > largest) largest = in[i];
+    for (int64_t i = 0; i < n; ++i) {
+      float e = (float)exp((double)((in[i] - largest) / temp));
+      sum = sum + e;
+      o[i] = e;
+    }
+    for (int64_t i = 0; i < n; ++i) o[i] = o[i] / sum;
+  }
+}
+
+/* ------------------------------------------------------------------------
  * convolutional layer forward (BN folded)
  * ---------------------------------------------------------------------- */
 void ref_conv_forward(int64_t batch, int64_t C, int64_t H, int64_t W,

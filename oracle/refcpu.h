@@ -97,6 +97,21 @@ void ref_bn_normalize(float *x, int64_t nb, int64_t blockSize,
 void ref_fuse_bn(int64_t F, int64_t filterSize, float *W, float *bias,
                  const float *scales, const float *mean, const float *var);
 
+/* Training-mode batch norm (avx2: 1 = the reference on an AVX2 host, with
+ * srss / sVarinceDelta_avx dropping lanes 4..7 when the block length is a
+ * multiple of 8; 0 = its Pascal loops, the parity target).
+ * TTensor.MeansAndVars (ntensors.pas:9102-9180) over [groups][nch][block]. */
+void ref_means_vars(const float *src, int64_t nch, int64_t block, int64_t groups, float *means, float *vars,
+                    int avx2);
+/* sMeanAndVarianceDelta (ntensors.pas:8831-8898) */
+void ref_means_vars_delta(const float *delta, const float *x, const float *mean, const float *var, int64_t nch,
+                          int64_t block, int64_t groups, float *mean_delta, float *variance_delta, int avx2);
+/* TTensor.addDots (ntensors.pas:7783-7830): dst[i] += dots of channel i */
+void ref_add_dots(float *dst, const float *a, const float *b, int64_t nch, int64_t block, int64_t groups,
+                  int avx2);
+/* softmax (nsoftmaxlayer.pas:81-105) row by row */
+void ref_softmax_rows(const float *x, int64_t rows, int64_t n, float temp, float *out);
+
 /* TConvolutionalLayer.forward (nConvolutionLayer.pas:457-566) with
  * Conv2D (ntensors.pas:8252-8345), forwardBias and activate; BN folded.
  * workspace: >= batch*C*k*k*OH*OW floats (unused for 1x1/s1). */

@@ -37,6 +37,10 @@ _PROTOS = {
     "ref_yolo_fwd": ([i64] * 5 + [P, P, i32], None),
     "ref_fuse_bn": ([i64, i64, P, P, P, P, P], None),
     "ref_conv_forward": ([i64] * 8 + [P, P, P, i32, P, P], None),
+    "ref_means_vars": ([P, i64, i64, i64, P, P, i32], None),
+    "ref_means_vars_delta": ([P, P, P, P, i64, i64, i64, P, P, i32], None),
+    "ref_add_dots": ([P, P, P, i64, i64, i64, i32], None),
+    "ref_softmax_rows": ([P, i64, i64, f32, P], None),
 }
 
 _lib = None
@@ -253,3 +257,42 @@ def rel_err(got, ref):
     if den == 0:
         return float(np.max(np.abs(got)))
     return float(np.max(np.abs(got - ref)) / den)
+
+
+def means_vars(x, nch, groups, avx2=False):
+    """TTensor.MeansAndVars over x viewed as [groups][nch][block]; avx2: the
+    AVX2 host's routines (srss drops lanes 4..7 of blocks whose length is a
+    multiple of 8), else the Pascal loops (the parity target)."""
+    x = _f32(x)
+    block = x.size // (nch * groups)
+    m, v = np.empty(nch, np.float32), np.empty(nch, np.float32)
+    lib().ref_means_vars(_p(x), nch, block, groups, _p(m), _p(v), int(avx2))
+    return m, v
+
+
+def means_vars_delta(delta, x, mean, var, groups, avx2=False):
+    """sMeanAndVarianceDelta: (mean_delta, variance_delta) per channel."""
+    delta, x, mean, var = _f32(delta), _f32(x), _f32(mean), _f32(var)
+    nch = mean.size
+    block = delta.size // (nch * groups)
+    md, vd = np.empty(nch, np.float32), np.empty(nch, np.float32)
+    lib().ref_means_vars_delta(_p(delta), _p(x), _p(mean), _p(var), nch, block, groups, _p(md), _p(vd), int(avx2))
+    return md, vd
+
+
+def add_dots(dst, a, b, groups, avx2=False):
+    """TTensor.addDots: dst + the per-channel dots of a and b (a new array)."""
+    out = _f32(dst).copy()
+    a, b = _f32(a), _f32(b)
+    nch = out.size
+    block = a.size // (nch * groups)
+    lib().ref_add_dots(_p(out), _p(a), _p(b), nch, block, groups, int(avx2))
+    return out
+
+
+def softmax_rows(x, temp=1.0):
+    """softmax of each row of a 2-D array."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().ref_softmax_rows(_p(x), x.shape[0], x.shape[1], float(temp), _p(out))
+    return out

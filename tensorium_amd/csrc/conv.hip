@@ -112,162 +112,6 @@ __global__ __launch_bounds__(Cfg::NT, Cfg::OCC) void conv_kernel(ConvArgs a) {
   conv_store<Cfg::FM, Cfg::FN>(a, acc, m0 + wm * Cfg::WTM, n0 + wn * Cfg::WTN, lane);
 }
 
-// ---------------------------------------------------------------------------
-// Register-direct variant: no LDS and no barriers.  Each wave owns a
-// (32*FM) x (32*FN) output tile and loads its own MFMA operands from global
-// memory (L1/L2) straight into registers, one 16-deep K chunk ahead of the
-// chunk it multiplies.  For v_mfma_f32_32x32x2_f32 with the chunk pairing
-// (step s uses k = s on lanes 0-31 and k = 8 + s on lanes 32-63) a lane
-// needs 8 consecutive k of one row of A (two 16-byte loads of the
-// k-contiguous weights) and 8 consecutive k of one column of B: with
-// tap-major weights and C % 16 == 0 those are 8 consecutive channels of one
-// input pixel, i.e. 8 loads HW floats apart.  Everything that varies along K
-// is uniform across the wave (tap, channel) and rides in the buffer
-// instruction's scalar offset, so the inner loop is loads and MFMAs only;
-// the per-lane offsets are recomputed once per tap.  The waves of a
-// workgroup cover adjacent tiles and share A rows / B columns through L1.
-// ---------------------------------------------------------------------------
-template <int FM_, int FN_, int WM_, int WN_, int OCC_, int PF_ = 1>
-struct DirectCfg {
-  static constexpr int FM = FM_, FN = FN_, WM = WM_, WN = WN_, OCC = OCC_;
-  static constexpr int PF = PF_;  // chunks loaded ahead of the one multiplied (1 or 2)
-  static constexpr int NT = WM * WN * 64;
-  static constexpr int WTM = FM * 32, WTN = FN * 32;
-  static constexpr int BM = WM * WTM, BN = WN * WTN, BK = 16;
-};
-
-
-template <class D, int KH, int KW>
-__global__ __launch_bounds__(D::NT, D::OCC) void conv_direct_kernel(ConvArgs a) {
-  constexpr int FM = D::FM, FN = D::FN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / D::WN, wn = wave % D::WN;
-  const int r = lane & 31, h = lane >> 5;
-  int tm, tn;
-  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * D::BM + wm * D::WTM;
-  const int64_t n0 = static_cast<int64_t>(tn) * D::BN + wn * D::WTN;
-
-  const int C = a.g.C, H = a.g.H, W = a.g.W;
-  const int64_t K = a.g.K;
-  const uint32_t HW4 = static_cast<uint32_t>(H) * static_cast<uint32_t>(W) * 4u;
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.wBytes);
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.g.x, a.g.xBytes);
-
-  // A: lane (r, h) of row block i reads W[m0 + 32i + r][k0 + 8h .. k0 + 8h + 7]
-  uint32_t aOff[FM];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int64_t row = m0 + 32 * i + r;
-    aOff[i] = sel_off(row < a.F, static_cast<uint32_t>((row * K + 8 * h) * 4));
-  }
-  // B: lane (r, h) of column block j reads channels c0 + 8h .. c0 + 8h + 7
-  // of input pixel (iy0 + ky, ix0 + kx) of its column's image.  cOff is the
-  // byte offset of (iy0, ix0) modulo 2^32 (it may wrap; in-range taps add
-  // back to the exact offset).
-  int iy0[FN], ix0[FN];
-  uint32_t cOff[FN];
-  bool cOk[FN];
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int64_t n = n0 + 32 * j + r;
-    cOk[j] = n < a.g.N;
-    const int64_t nn = cOk[j] ? n : 0;
-    const int64_t b = nn / a.g.OHW;
-    const int p = static_cast<int>(nn - b * a.g.OHW);
-    const int oy = p / a.g.OW, ox = p - (p / a.g.OW) * a.g.OW;
-    iy0[j] = oy * a.g.sY - a.g.pH;
-    ix0[j] = ox * a.g.sX - a.g.pW;
-    cOff[j] = static_cast<uint32_t>((b * a.g.xBatchStride + static_cast<int64_t>(iy0[j]) * W + ix0[j]) * 4) +
-              static_cast<uint32_t>(8 * h) * HW4;
-  }
-
-  // K is walked channel-chunk outer, tap inner: chunk q covers channels
-  // c0 = 16*(q / TAPS) .. c0 + 15 of tap q % TAPS (k = tap*C + c0 in the
-  // tap-major weights).  The nine taps of one channel chunk read nearly the
-  // same input lines back to back, so they hit in L1/L2 instead of
-  // re-streaming every channel of the input once per tap.
-  constexpr int TAPS = KH * KW;
-  const int qBegin = static_cast<int>(blockIdx.y * a.kChunk / 16);
-  const int qEnd = static_cast<int>(min(K, (blockIdx.y + 1) * a.kChunk) / 16);
-  const int nq = qEnd - qBegin;
-  int q = qBegin;
-  auto load = [&](f32x4 (&A)[FM][2], float (&B)[FN][8]) {
-    const int cc = q / TAPS, tap = q - cc * TAPS;
-    const int c0 = cc * 16;
-    const uint32_t ks = static_cast<uint32_t>(tap * C + c0) * 4u;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      A[i][0] = buf_ld4s(wr, aOff[i], ks);
-      A[i][1] = buf_ld4s(wr, aOff[i], ks + 16);
-    }
-    const int ky = tap / KW, kx = tap - (tap / KW) * KW;
-    const uint32_t tapOff = static_cast<uint32_t>(ky * W + kx) * 4u;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int iy = iy0[j] + ky, ix = ix0[j] + kx;
-      const bool ok = cOk[j] && static_cast<unsigned>(iy) < static_cast<unsigned>(H) &&
-                      static_cast<unsigned>(ix) < static_cast<unsigned>(W);
-      const uint32_t vo = sel_off(ok, cOff[j] + tapOff);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) B[j][s] = buf_ld1s(xr, vo, static_cast<uint32_t>(c0 + s) * HW4);
-    }
-    ++q;
-  };
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-  auto compute = [&](const f32x4 (&A)[FM][2], const float (&B)[FN][8]) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(A[i][s >> 2][s & 3], B[j][s], acc[i][j], 0, 0, 0);
-  };
-
-  // Single-exit loop over chunk pairs (accumulators stay in place; a loop
-  // with an exit between the two halves makes the compiler shuttle them
-  // between register files every iteration).
-  if (nq > 0 && D::PF == 1) {
-    f32x4 A0[FM][2], A1[FM][2];
-    float B0[FN][8], B1[FN][8];
-    load(A0, B0);  // chunk 0
-    int i = 0;
-    for (; i + 1 < nq; i += 2) {
-      load(A1, B1);  // chunk i + 1
-      compute(A0, B0);
-      if (i + 2 < nq) load(A0, B0);  // chunk i + 2
-      compute(A1, B1);
-    }
-    if (i < nq) compute(A0, B0);  // odd count: the last chunk
-  } else if (nq > 0) {
-    // two chunks in flight: three register sets in rotation
-    f32x4 A0[FM][2], A1[FM][2], A2[FM][2];
-    float B0[FN][8], B1[FN][8], B2[FN][8];
-    load(A0, B0);  // chunk 0
-    if (nq > 1) load(A1, B1);  // chunk 1
-    int i = 0;
-    for (; i + 2 < nq; i += 3) {  // chunks i, i + 1 are in sets 0, 1
-      load(A2, B2);  // chunk i + 2
-      compute(A0, B0);
-      if (i + 3 < nq) load(A0, B0);  // chunk i + 3
-      compute(A1, B1);
-      if (i + 4 < nq) load(A1, B1);  // chunk i + 4
-      compute(A2, B2);
-    }
-    if (i < nq) compute(A0, B0);
-    if (i + 1 < nq) compute(A1, B1);
-  }
-
-  conv_store<FM, FN>(a, acc, m0, n0, lane);
-}
 
 // Few-channel 3x3 convolution (C <= 4, e.g. the RGB input layer): the
 // output is store-bound (F outputs per pixel against 9*C inputs), so instead
@@ -547,20 +391,15 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
 // LDS-staged tiles (tile M x N x K depth, waves M x N, prefetch depth,
 // occupancy), chosen from sweeps of the YOLOv3 layer shapes: small tiles
 // with two panels of prefetch keep the most waves resident and win on most
-// shapes.  The register-direct tiles win some large-M and 1x1 shapes; the
-// autotuner picks per layer shape.
+// shapes; the autotuner picks per layer shape.
 using Cfg0 = TileCfg<64, 64, 32, 2, 2, 2, 1>;
 using Cfg1 = TileCfg<64, 64, 16, 2, 2, 2, 8>;
 using Cfg2 = TileCfg<128, 64, 16, 2, 2, 2, 5>;
 using Cfg3 = TileCfg<128, 128, 16, 2, 2, 1, 1>;
 using Cfg4 = TileCfg<64, 128, 32, 2, 2, 2, 1>;
 using Cfg5 = TileCfg<64, 128, 16, 2, 2, 2, 5>;
-// register-direct tiles (FM x FN 32x32 blocks per wave, WM x WN waves)
-using Dir6 = DirectCfg<2, 2, 4, 1, 3>;
-using Dir7 = DirectCfg<2, 1, 1, 4, 4>;
-using Dir8 = DirectCfg<2, 2, 2, 2, 3>;
-using Dir9 = DirectCfg<2, 2, 1, 4, 3>;
-using Dir10 = DirectCfg<1, 2, 4, 1, 4>;
+// ids 6-10 are retired (register-direct tiles that the tuner never chose on
+// any profiled shape); the ids of the other tiles stay as they were
 // lean tiles (conv_lean.hpp: tile M x N x K depth, waves M x N, occupancy)
 using Lean11 = LeanCfg<64, 64, 32, 2, 2, 4>;
 using Lean12 = LeanCfg<64, 128, 32, 2, 2, 3>;
@@ -576,7 +415,7 @@ using Lean19 = LeanCfg<128, 128, 32, 4, 2, 2>;
 // the waves of its workgroup), ids kWsFirst + index into kWsCfgs
 constexpr int kWsFirst = 20;
 
-enum CfgKind { kLds = 0, kDirect = 1, kLean = 2, kWsplit = 3 };
+enum CfgKind { kLds = 0, kRetired = 1, kLean = 2, kWsplit = 3 };
 struct CfgInfo {
   int BM, BN, BK;
   float eff;  // relative per-CU throughput used by the cost model
@@ -587,8 +426,8 @@ constexpr int kNumCfg = kWsFirst + kNumWs;
 const CfgInfo kCfgs[kNumCfg] = {
     {64, 64, 32, 1.00f, 4, kLds},     {64, 64, 16, 1.00f, 8, kLds},     {128, 64, 16, 0.97f, 5, kLds},
     {128, 128, 16, 0.95f, 2, kLds},   {64, 128, 32, 0.97f, 3, kLds},    {64, 128, 16, 0.95f, 5, kLds},
-    {256, 64, 16, 0.95f, 3, kDirect}, {64, 128, 16, 0.95f, 4, kDirect}, {128, 128, 16, 0.95f, 3, kDirect},
-    {64, 256, 16, 0.95f, 3, kDirect}, {128, 64, 16, 0.95f, 4, kDirect}, {64, 64, 32, 1.15f, 4, kLean},
+    {0, 0, 0, 0.f, 0, kRetired},      {0, 0, 0, 0.f, 0, kRetired},      {0, 0, 0, 0.f, 0, kRetired},
+    {0, 0, 0, 0.f, 0, kRetired},      {0, 0, 0, 0.f, 0, kRetired},      {64, 64, 32, 1.15f, 4, kLean},
     {64, 128, 32, 1.10f, 3, kLean},   {128, 64, 32, 1.10f, 3, kLean},   {128, 128, 32, 1.05f, 2, kLean},
     {64, 64, 64, 1.10f, 2, kLean},    {64, 32, 32, 1.10f, 6, kLean},    {128, 64, 32, 1.10f, 2, kLean},
     {64, 128, 32, 1.10f, 2, kLean},   {128, 128, 32, 1.05f, 2, kLean},
@@ -873,18 +712,6 @@ int launch_nhwc_cfg(int cfg, const ConvArgs& a, int mode, int cus, hipStream_t s
   }
 }
 
-template <class D>
-int launch_direct(ConvArgs a, int mode, hipStream_t s) {
-  dim3 grid;
-  if (int st = grid_for<D>(a, grid)) return st;
-  if (mode == kTap3)
-    hipLaunchKernelGGL((conv_direct_kernel<D, 3, 3>), grid, dim3(D::NT), 0, s, a);
-  else
-    hipLaunchKernelGGL((conv_direct_kernel<D, 1, 1>), grid, dim3(D::NT), 0, s, a);
-  if (int st = launch_status("conv_direct_kernel")) return st;
-  return launch_reduce(a, s);
-}
-
 int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, int cus, hipStream_t s) {
   switch (cfg) {
     case 0: return launch_cfg<Cfg0>(a, mode, va, vb, s);
@@ -893,11 +720,6 @@ int launch(int cfg, const ConvArgs& a, int mode, bool va, bool vb, int cus, hipS
     case 3: return launch_cfg<Cfg3>(a, mode, va, vb, s);
     case 4: return launch_cfg<Cfg4>(a, mode, va, vb, s);
     case 5: return launch_cfg<Cfg5>(a, mode, va, vb, s);
-    case 6: return launch_direct<Dir6>(a, mode, s);
-    case 7: return launch_direct<Dir7>(a, mode, s);
-    case 8: return launch_direct<Dir8>(a, mode, s);
-    case 9: return launch_direct<Dir9>(a, mode, s);
-    case 10: return launch_direct<Dir10>(a, mode, s);
     case 11: return launch_lean<Lean11>(a, mode, vb, cus, s);
     case 12: return launch_lean<Lean12>(a, mode, vb, cus, s);
     case 13: return launch_lean<Lean13>(a, mode, vb, cus, s);
@@ -982,14 +804,13 @@ std::unordered_map<TuneKey, Cand, TuneHash> g_tuned;
 bool g_autotune = true;
 int g_forced_cfg = -1;
 
-// The register-direct kernels need whole 16-channel chunks inside one tap
-// and 16-byte weight rows (tap-major 3x3, or 1x1 stride 1, with va); the
-// wave-split tiles whole 32-channel panels inside one tap.
+// The wave-split tiles need whole 32-channel panels inside one tap; the
+// retired ids take nothing.
 bool cfg_valid(int c, int mode, int64_t C, bool va, bool smallIO, bool nhwc = false) {
   if (nhwc) return (kCfgs[c].kind == kLean || kCfgs[c].kind == kWsplit) && smallIO && va && C % kCfgs[c].BK == 0;
   if (kCfgs[c].kind == kWsplit) return (mode == kTap3 || mode == k1x1) && va && smallIO && C % 32 == 0;
   if (kCfgs[c].kind == kLean && !smallIO) return false;
-  if (kCfgs[c].kind == kDirect) return (mode == kTap3 || mode == k1x1) && C % 16 == 0 && va;
+  if (kCfgs[c].kind == kRetired) return false;
   if (kCfgs[c].kind == kLean) return va && (mode == k1x1 || mode == kTap3) && C % kCfgs[c].BK == 0;
   if (mode == kTap3) return C % kCfgs[c].BK == 0;
   return true;
@@ -1377,6 +1198,8 @@ extern "C" int32_t tnh_conv2d_set_autotune(int32_t enable, int32_t forcedConfig)
   TNH_ARG(forcedConfig >= -1 && forcedConfig % 64 < kNumCfg && forcedConfig / 64 <= 47 &&
               forcedConfig / 64 != 17 && forcedConfig / 64 != 32 && forcedConfig / 64 != 33,
           "conv2d_set_autotune: config %d", forcedConfig);
+  TNH_ARG(forcedConfig < 0 || kCfgs[forcedConfig % 64].kind != kRetired,
+          "conv2d_set_autotune: tile %d is retired (ids 6..10)", forcedConfig % 64);
   g_autotune = enable != 0;
   g_forced_cfg = forcedConfig;
   if (!g_autotune) g_tuned.clear();

@@ -30,9 +30,9 @@ acLOGISTIC, acLINEAR, acLEAKY = 0, 4, 9
 # conv weight layouts
 WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 # number of compiled conv tile configurations (tnh_conv2d_set_autotune ids
-# 0..NUM_CONV_CFGS-1: 0-5 LDS-staged, 6-10 register-direct, 11-19 lean
-# software-pipelined, 20-26 wave-split); the first NUM_CONV_NCHW_CFGS serve
-# tnh_conv2d_fwd, CONV_LEAN_CFGS and CONV_WSPLIT_CFGS
+# 0..NUM_CONV_CFGS-1: 0-5 LDS-staged, 11-19 lean software-pipelined, 20-26
+# wave-split; 6-10 retired); CONV_NCHW_CFGS serve tnh_conv2d_fwd,
+# CONV_LEAN_CFGS and CONV_WSPLIT_CFGS
 # tnh_conv2d_fwd_nhwc; a forced id is
 # tile + CONV_SPLIT_UNIT * splits (uniform split-K, up to 16), or, for a lean
 # tile, tile + CONV_SPLIT_UNIT * (base + pieces) (tail split; base
@@ -40,6 +40,8 @@ WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR = 0, 1
 # one tile per resident workgroup slot)
 NUM_CONV_CFGS = 27
 NUM_CONV_NCHW_CFGS = 27
+CONV_RETIRED_CFGS = range(6, 11)
+CONV_NCHW_CFGS = [c for c in range(NUM_CONV_NCHW_CFGS) if c not in CONV_RETIRED_CFGS]
 CONV_LEAN_CFGS = range(11, 20)
 CONV_WSPLIT_CFGS = range(20, 27)
 CONV_SPLIT_UNIT = 64

@@ -9,7 +9,7 @@ import torch
 
 from oracle import refcpu as R
 from tensorium_amd import synth
-from tensorium_amd.nnhip import CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, CONV_WSPLIT_CFGS, NUM_CONV_NCHW_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
+from tensorium_amd.nnhip import CONV_NCHW_CFGS, CONV_RETIRED_CFGS, CONV_SPLIT_UNIT, CONV_TAIL_BASE, CONV_TAIL_SLOT_BASE, CONV_WSPLIT_CFGS, NUM_SGEMM_CFGS, WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -389,7 +389,7 @@ def test_conv_reference_layout_repacks(hip, B, Cc, Hh, F, s, res):
     assert OH > 0
 
 
-@pytest.mark.parametrize("cfg", range(NUM_CONV_NCHW_CFGS))
+@pytest.mark.parametrize("cfg", CONV_NCHW_CFGS)
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s,p,act", [(2, 32, 26, 64, 3, 1, 1, acLEAKY), (1, 64, 13, 96, 3, 2, 1, acLEAKY),
                                                  (2, 48, 11, 40, 3, 1, 1, acLINEAR), (1, 3, 20, 16, 3, 1, 1, acLEAKY),
                                                  (2, 40, 9, 70, 1, 1, 0, acLEAKY), (3, 64, 13, 300, 1, 1, 0, acLEAKY),
@@ -1012,6 +1012,10 @@ def test_bn_forward_equals_the_reference_sequence(hip, B, F, P, act, norm):
 # --------------------------------------------------------------- errors ----
 def test_invalid_arguments_raise(hip):
     case("argument checks")
+    for c in CONV_RETIRED_CFGS:  # retired tile ids are refused, not silently replaced
+        with pytest.raises(TNHError):
+            hip.setConvAutotune(True, c)
+    hip.setConvAutotune(True, -1)
     dx = D(np.zeros(16, np.float32))
     with pytest.raises(TNHError):
         hip.gemm(0, 0, 4, 4, 4, 1.0, dx, 0, 2, dx, 0, 4, 0.0, dx, 0, 4)  # lda < K

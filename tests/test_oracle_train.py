@@ -151,3 +151,87 @@ def test_cifar_step_learns():
     assert losses[-1] < losses[0]
     # BN biases never receive gradient (reference quirk), scales do
     assert np.all(net.p["b0"] == 0) and np.any(net.p["s0"] != 1)
+
+
+# ------------------------------------------ C restatement of the BN training
+def test_means_vars_c_pascal_loops_match_definition():
+    """refcpu's MeansAndVars in the Pascal-loop form (the parity target):
+    the float64 mean and unbiased variance within fp32 summation error, and
+    the numpy restatement within the same bound."""
+    for shape in ((4, 6, 5, 7), (3, 5, 8, 8), (2, 70, 1, 1)):
+        x = synth.normal(205, shape, 2.0) + np.float32(3)
+        B, Cc = shape[:2]
+        m, v = R.means_vars(x, Cc, B)
+        x64 = x.astype(np.float64).transpose(1, 0, 2, 3).reshape(Cc, -1)
+        assert np.allclose(m, x64.mean(axis=1), rtol=2e-6, atol=1e-7)
+        assert np.allclose(v, x64.var(axis=1, ddof=1), rtol=4e-6, atol=0)
+
+
+def test_srss_lane_drop_hand_derived():
+    """srss (ntensors.pas:1493-1525) on an AVX2 host: with no remainder
+    (N % 8 == 0) the upper four lanes are never folded in.  One channel of
+    eight values 1,1,1,1,9,9,9,9: mean 5, and every deviation squared is 16;
+    the Pascal loop sums eight of them (128 / 7), the AVX2 routine only lanes
+    0..3 (64 / 7).  With a ninth value (5, deviation 0) the remainder path
+    folds the lanes: both give 128 / 8."""
+    x = np.array([1, 1, 1, 1, 9, 9, 9, 9], np.float32).reshape(1, 1, 1, 8)
+    m, v = R.means_vars(x, 1, 1)
+    ma, va = R.means_vars(x, 1, 1, avx2=True)
+    assert m[0] == 5 and ma[0] == 5
+    assert v[0] == np.float32(128) / np.float32(7)
+    assert va[0] == np.float32(64) / np.float32(7)
+    x9 = np.array([1, 1, 1, 1, 9, 9, 9, 9, 5], np.float32).reshape(1, 1, 1, 9)
+    assert R.means_vars(x9, 1, 1, avx2=True)[1][0] == R.means_vars(x9, 1, 1)[1][0] == np.float32(16)
+    # the same half-lane sum by its closed form on a larger block: the
+    # elements k with k % 8 < 4 of every block, over the unbiased divisor
+    x = synth.normal(206, (3, 4, 8, 8), 1.5) + np.float32(0.5)
+    m, va = R.means_vars(x, 4, 3, avx2=True)
+    d = x.reshape(3, 4, 64).astype(np.float64) - m.astype(np.float64)[None, :, None]
+    half = (d[:, :, (np.arange(64) % 8) < 4] ** 2).sum(axis=(0, 2)) / (3 * 64 - 1)
+    assert np.allclose(va, half, rtol=4e-6, atol=0)
+    full = (d ** 2).sum(axis=(0, 2)) / (3 * 64 - 1)
+    assert not np.allclose(va, full, rtol=0.1, atol=0)
+
+
+def test_variance_delta_lane_drop_hand_derived():
+    """sVarinceDelta_avx (ntensors.pas:8721-8756) drops lanes 4..7 in the
+    same way: delta = 1 everywhere, x = 1,1,1,1,9,9,9,9 about mean 5 gives
+    sum(delta * (x - mean)) = -16 + 16 = 0 in full and -16 over lanes 0..3;
+    variance_delta = v * -0.5 * max(var, eps)^-1.5.  mean_delta is the sum of
+    the deltas (8) times -1 / sqrt(var) in both forms."""
+    x = np.array([1, 1, 1, 1, 9, 9, 9, 9], np.float32)
+    d = np.ones(8, np.float32)
+    mean, var = np.array([5], np.float32), np.array([4], np.float32)
+    md, vd = R.means_vars_delta(d, x, mean, var, 1)
+    mda, vda = R.means_vars_delta(d, x, mean, var, 1, avx2=True)
+    assert md[0] == mda[0] == np.float32(8) * (np.float32(-1) / np.float32(2))
+    assert vd[0] == 0
+    assert vda[0] == np.float32(-16 * -0.5 * 4.0 ** -1.5)
+
+
+def test_means_vars_delta_c_matches_numpy_restatement():
+    """refcpu's sMeanAndVarianceDelta (Pascal loops) against trainref's
+    float64-accumulated numpy restatement, and addDots against a float64
+    closed form, within fp32 summation error."""
+    x = synth.normal(207, (8, 6, 9, 9), 1.5) + np.float32(0.3)
+    dy = synth.normal(208, (8, 6, 9, 9))
+    mean, var = R.means_vars(x, 6, 8)
+    md, vd = R.means_vars_delta(dy, x, mean, var, 8)
+    md64 = dy.astype(np.float64).transpose(1, 0, 2, 3).reshape(6, -1).sum(axis=1) * (-1 / np.sqrt(var.astype(np.float64)))
+    # sums of N(0, 1) deltas cancel: per tensor, max|err| / max|ref|
+    assert R.rel_err(md, md64.astype(np.float32)) <= 2e-6
+    xc = x.astype(np.float64) - mean.astype(np.float64)[None, :, None, None]
+    v64 = (dy.astype(np.float64) * xc).transpose(1, 0, 2, 3).reshape(6, -1).sum(axis=1)
+    assert R.rel_err(vd, (v64 * -0.5 * var.astype(np.float64) ** -1.5).astype(np.float32)) <= 2e-6
+    acc = synth.normal(209, (6,))
+    got = R.add_dots(acc, x, dy, 8)
+    want = acc.astype(np.float64) + (x.astype(np.float64) * dy).transpose(1, 0, 2, 3).reshape(6, -1).sum(axis=1)
+    assert R.rel_err(got, want.astype(np.float32)) <= 2e-6
+    assert R.rel_err(R.add_dots(acc, x, dy, 8, avx2=True), want.astype(np.float32)) <= 2e-6
+
+
+def test_softmax_c_equals_numpy_restatement():
+    """refcpu's softmax and trainref's numpy restatement follow the same
+    operation order: bit for bit."""
+    x = synth.normal(210, (32, 10), 3.0)
+    assert np.array_equal(R.softmax_rows(x), T.softmax_batch(x))
