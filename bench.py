@@ -451,7 +451,7 @@ def extra_train(hip, steps, warmup, cpu_steps):
 
         threads, nproc, avail, model = baseline_threads()
         R.set_threads(threads)
-        ref = T.CifarStep(params, avx2=True)  # the reference's routines on an AVX2 host
+        ref = T.CifarStep(params, form="avx2")  # the reference's routines on an AVX2 host
         ref.step(x, truth)
         t0 = time.perf_counter()
         for _ in range(cpu_steps):

@@ -556,6 +556,17 @@ int32_t tnh_normalize_delta(int64_t deltaSize, int64_t meanSize,
 int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups,
                      const float *src1, const float *src2, int64_t srcOffset,
                      float *dst);
+/* No reference counterpart: the first three steps of batchNormBack
+ * (nbaselayer.pas:372-392) in one pass over delta, viewed as
+ * [groups][dstSize][block]: delta *= act'(output) (TNNCuda.DeriveArray),
+ * scaleUpdates[i] += sum x_norm * delta (addDots), delta *= scales[i]
+ * (forwardScale); the same operations per element and the same fixed
+ * summation order as those three calls, so the results equal theirs bit for
+ * bit.  act: TNH_AC_LINEAR, TNH_AC_LEAKY or TNH_AC_LOGISTIC. */
+int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
+                              const float *output, int32_t act,
+                              const float *xNorm, const float *scales,
+                              float *delta, float *scaleUpdates);
 /* TNNCuda.softmaxBatch (nncuda.pas:1056) / softmax (nsoftmaxlayer.pas:81):
  * per (batch, group) row of N values (stride apart): e = exp((x-max)/temp),
  * out = e / sum(e). */

@@ -165,6 +165,8 @@ function tnh_means_vars(srcSize, dstSize, groups: Int64; src: PSingle; offset: I
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means: PSingle): LongInt; cdecl; external libtnh;
+function tnh_bn_backward_scale(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, scales, delta,
+  scaleUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_variances(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_statistics(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -332,6 +334,9 @@ type
       biases: TCUMem; const activation: longint);
     procedure bnStatistics(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
       means, vars, rollingMeans, rollingVars: TCUMem; const momentum: T);
+    // DeriveArray + addDots + forwardScale of batchNormBack in one pass
+    procedure bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
+      const xNorm, scales, delta, scaleUpdates: TCUMem);
     procedure avgPoolForward(const batch, c, h, w: SizeInt; const input, output: TCUMem);
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
@@ -803,6 +808,13 @@ procedure TNNHip<T>.bnStatistics(const srcSize, dstSize, groups: SizeInt; const 
 begin
   check(tnh_bn_statistics(srcSize, dstSize, groups, PSingle(src), offset, PSingle(means), PSingle(vars),
     PSingle(rollingMeans), PSingle(rollingVars), S(momentum)));
+end;
+
+procedure TNNHip<T>.bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem;
+  const activation: longint; const xNorm, scales, delta, scaleUpdates: TCUMem);
+begin
+  check(tnh_bn_backward_scale(N, dstSize, groups, PSingle(output), activation, PSingle(xNorm), PSingle(scales),
+    PSingle(delta), PSingle(scaleUpdates)));
 end;
 
 procedure TNNHip<T>.avgPoolForward(const batch, c, h, w: SizeInt; const input, output: TCUMem);

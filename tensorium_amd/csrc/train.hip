@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <initializer_list>
+#include <type_traits>
 
 #include "common.hpp"
 #include "gemm_core.hpp"
@@ -133,8 +134,19 @@ __device__ inline void chan_walk(const ChanSplit& s, int p, int64_t i, const Op&
   }
 }
 
+// A reduction without a per-channel final step (the first pass of a
+// two-pass statistic).
+struct NoFin {
+  __device__ void run(int64_t, const ChanSplit&, float*) const {}
+};
+
 // grid: (channel, workgroup of the channel); channels in x, which holds up
-// to 2^31 - 1 of them
+// to 2^31 - 1 of them.  Each workgroup stores its NQ partials; a second
+// launch (chan_final_kernel) runs the channel's final step.  (A final step
+// run by the channel's last-arriving workgroup, found with an arrival
+// counter, was measured slower on the config-3 step: its chain of
+// write-through stores, the atomic and the system-scope loads at the end of
+// the launch outlasts a separate 64-thread launch.)
 template <int NQ, bool VEC, class Op>
 __global__ __launch_bounds__(kRed) void chan_partial_kernel(Op op, ChanSplit s, float* part) {
   __shared__ float sh[kRed];
@@ -150,6 +162,14 @@ __global__ __launch_bounds__(kRed) void chan_partial_kernel(Op op, ChanSplit s, 
     const float r = block_sum(acc[q], sh);
     if (threadIdx.x == 0) part[(q * s.nch + i) * s.P + p] = r;
   }
+}
+
+// The second launch of a reduction: one 64-thread workgroup per channel
+// runs the final step.
+template <class Fin>
+__global__ __launch_bounds__(64) void chan_final_kernel(Fin fin, ChanSplit s) {
+  __shared__ float sh[64];
+  fin.run(blockIdx.x, s, sh);
 }
 
 __device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -220,30 +240,41 @@ struct RssGivenOp {
 };
 
 // dst[i] = (the channel's fixed-order partial total) / div
-__global__ __launch_bounds__(64) void total_div_final(const float* part, ChanSplit s, float div, float* dst) {
-  __shared__ float sh[64];
-  const int64_t i = blockIdx.x;
-  const float t = fixed_total(part + i * s.P, s.P, sh);
-  if (threadIdx.x == 0) dst[i] = t / div;
-}
+// dst[i] = (the channel's fixed-order partial total) / div
+struct TotalDivFin {
+  const float* part;
+  float div;
+  float* dst;
+  __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
+    const float t = fixed_total(part + i * s.P, s.P, sh);
+    if (threadIdx.x == 0) dst[i] = t / div;
+  }
+};
 
-__global__ __launch_bounds__(64) void means_vars_final(const float* part, ChanSplit s, float S, float* means,
-                                                       float* vars, float* rollMean, float* rollVar, float keep,
-                                                       float bm) {
-  __shared__ float sh[64];
-  const int64_t i = blockIdx.x;
-  const float m = fixed_total(part + i * s.P, s.P, sh) / S;
-  const float rss = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
-  if (threadIdx.x == 0) {
-    const float v = rss / (S - 1.f);
-    means[i] = m;
-    vars[i] = v;
-    if (rollMean) {  // Multiply(1 - momentum), then axpy(momentum, .) (nbaselayer.pas:352-355)
-      rollMean[i] = fmaf(bm, m, keep * rollMean[i]);
-      rollVar[i] = fmaf(bm, v, keep * rollVar[i]);
+// mean = sum / S and variance = residual sum / (S - 1), then the rolling
+// statistics (part: [2][nch][P], the sums then the residual sums)
+struct MeanVarFin {
+  const float* part;
+  float S;
+  float* means;
+  float* vars;
+  float* rollMean;
+  float* rollVar;
+  float keep, bm;
+  __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
+    const float m = fixed_total(part + i * s.P, s.P, sh) / S;
+    const float rss = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
+    if (threadIdx.x == 0) {
+      const float v = rss / (S - 1.f);
+      means[i] = m;
+      vars[i] = v;
+      if (rollMean) {  // Multiply(1 - momentum), then axpy(momentum, .) (nbaselayer.pas:352-355)
+        rollMean[i] = fmaf(bm, m, keep * rollMean[i]);
+        rollVar[i] = fmaf(bm, v, keep * rollVar[i]);
+      }
     }
   }
-}
+};
 
 // sMeanAndVarianceDelta (ntensors.pas:8831-8898): sum(delta) and
 // sum(delta * (x - mean))
@@ -271,19 +302,22 @@ struct MvdOp {
   }
 };
 
-__global__ __launch_bounds__(64) void means_vars_delta_final(const float* part, ChanSplit s, const float* variance,
-                                                             float* mean_delta, float* variance_delta) {
-  __shared__ float sh[64];
-  const int64_t i = blockIdx.x;
-  const float m = fixed_total(part + i * s.P, s.P, sh);
-  const float v = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
-  if (threadIdx.x == 0) {
-    const float vc = fmaxf(variance[i], kEps);
-    mean_delta[i] = m * (-1.0f / sqrtf(vc));
-    // Power(max(var, eps), -3/2) is evaluated in double and the product stored as single
-    variance_delta[i] = static_cast<float>(static_cast<double>(v) * -0.5 * pow(static_cast<double>(vc), -1.5));
+struct MvdFin {
+  const float* part;
+  const float* variance;
+  float* mean_delta;
+  float* variance_delta;
+  __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
+    const float m = fixed_total(part + i * s.P, s.P, sh);
+    const float v = fixed_total(part + (s.nch + i) * s.P, s.P, sh);
+    if (threadIdx.x == 0) {
+      const float vc = fmaxf(variance[i], kEps);
+      mean_delta[i] = m * (-1.0f / sqrtf(vc));
+      // Power(max(var, eps), -3/2) is evaluated in double and the product stored as single
+      variance_delta[i] = static_cast<float>(static_cast<double>(v) * -0.5 * pow(static_cast<double>(vc), -1.5));
+    }
   }
-}
+};
 
 // addDots (ntensors.pas:7783-7830): sum of a*b
 struct DotOp {
@@ -300,24 +334,67 @@ struct DotOp {
   }
 };
 
-__global__ __launch_bounds__(64) void add_dots_final(const float* part, ChanSplit s, float* dst) {
-  __shared__ float sh[64];
-  const int64_t i = blockIdx.x;
-  const float t = fixed_total(part + i * s.P, s.P, sh);
-  if (threadIdx.x == 0) dst[i] = dst[i] + t;
-}
+// dst[i] += the channel's total (addDots, addSums / backward_bias)
+struct AddFin {
+  const float* part;
+  float* dst;
+  __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
+    const float t = fixed_total(part + i * s.P, s.P, sh);
+    if (threadIdx.x == 0) dst[i] = dst[i] + t;
+  }
+};
+
+// batchNormBack's first three steps (nbaselayer.pas:372-392) in one pass:
+// DeriveArray (delta *= act'(out)), addDots (dgamma += sum x_norm * delta)
+// and forwardScale (delta *= gamma), each element visited once with each
+// step's own operation, so the deltas and the dot equal the three separate
+// passes bit for bit.
+struct BnBackOp {
+  float* delta;
+  const float* out;
+  const float* xn;
+  const float* gamma;
+  int act;
+  float g;
+  __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) { g = gamma[i]; }
+  __device__ static float grad(float v, int act) {
+    if (act == TNH_AC_LEAKY) return v > 0.f ? 1.f : 0.1f;
+    if (act == TNH_AC_LOGISTIC) return (1.f - v) * v;
+    return 1.f;
+  }
+  __device__ float one(float* a, float d, float o, float x) const {
+    const float d1 = d * grad(o, act);
+    a[0] = a[0] + x * d1;
+    return g * d1;
+  }
+  __device__ void add(float* a, int64_t e) const { delta[e] = one(a, delta[e], out[e], xn[e]); }
+  __device__ void add4(float* a, int64_t e) const {
+    const float4 d = ld4(delta + e), o = ld4(out + e), x = ld4(xn + e);
+    float4 r;
+    r.x = one(a, d.x, o.x, x.x);
+    r.y = one(a, d.y, o.y, x.y);
+    r.z = one(a, d.z, o.z, x.z);
+    r.w = one(a, d.w, o.w, x.w);
+    *reinterpret_cast<float4*>(delta + e) = r;
+  }
+};
 
 bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Launches the first pass of a channel reduction (nq partials per workgroup).
-template <int NQ, class Op>
-int launch_partial(const Op& op, const ChanSplit& s, bool vec, float* part, hipStream_t st, const char* name) {
+// Launches a channel reduction (NQ partials per workgroup) and, for a Fin
+// other than NoFin, the launch of its per-channel final step.
+template <int NQ, class Op, class Fin = NoFin>
+int launch_partial(Context* cx, const Op& op, const ChanSplit& s, bool vec, float* part, const char* name,
+                   const Fin& fin = Fin{}) {
   const dim3 grid(static_cast<unsigned>(s.nch), static_cast<unsigned>(s.P));
   if (vec)
-    hipLaunchKernelGGL((chan_partial_kernel<NQ, true, Op>), grid, dim3(kRed), 0, st, op, s, part);
+    hipLaunchKernelGGL((chan_partial_kernel<NQ, true, Op>), grid, dim3(kRed), 0, cx->stream, op, s, part);
   else
-    hipLaunchKernelGGL((chan_partial_kernel<NQ, false, Op>), grid, dim3(kRed), 0, st, op, s, part);
-  return launch_status(name);
+    hipLaunchKernelGGL((chan_partial_kernel<NQ, false, Op>), grid, dim3(kRed), 0, cx->stream, op, s, part);
+  if (int st = launch_status(name)) return st;
+  if (std::is_same<Fin, NoFin>::value) return TNH_OK;
+  hipLaunchKernelGGL((chan_final_kernel<Fin>), dim3(static_cast<unsigned>(s.nch)), dim3(64), 0, cx->stream, fin, s);
+  return launch_status("chan_final_kernel");
 }
 
 // 16-byte loads are legal when every unit starts 16-byte aligned
@@ -343,13 +420,10 @@ int means_vars_impl(int64_t srcSize, int64_t dstSize, int64_t groups, const floa
   float* sumPart = red;
   float* rssPart = red + dstSize * s.P;
   const float S = static_cast<float>(groups * block);
-  if (int st = launch_partial<1>(SumOp{x}, s, vec, sumPart, cx->stream, "chan_partial_kernel<sum>")) return st;
-  if (int st = launch_partial<1>(RssOp{x, sumPart, S, 0.f}, s, vec, rssPart, cx->stream, "chan_partial_kernel<rss>"))
-    return st;
+  if (int st = launch_partial<1>(cx, SumOp{x}, s, vec, sumPart, "chan_partial_kernel<sum>")) return st;
   const float keep = 1.0f - momentum;
-  hipLaunchKernelGGL(means_vars_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, S,
-                     means, vars, rollMean, rollVar, keep, momentum);
-  return launch_status("means_vars_final");
+  return launch_partial<1>(cx, RssOp{x, sumPart, S, 0.f}, s, vec, rssPart, "chan_partial_kernel<rss>",
+                           MeanVarFin{red, S, means, vars, rollMean, rollVar, keep, momentum});
 }
 
 // sNormalizeDelta (ntensors.pas:8900-8960), element order of
@@ -638,11 +712,8 @@ extern "C" int32_t tnh_means(int64_t srcSize, int64_t dstSize, int64_t groups, c
   float* red = nullptr;
   if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
   const float* x = src + offset;
-  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), red, cx->stream, "chan_partial_kernel<sum>"))
-    return st;
-  hipLaunchKernelGGL(total_div_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s,
-                     static_cast<float>(groups * block), means);
-  return launch_status("total_div_final");
+  return launch_partial<1>(cx, SumOp{x}, s, chan_vec(s, {x}), red, "chan_partial_kernel<sum>",
+                           TotalDivFin{red, static_cast<float>(groups * block), means});
 }
 
 extern "C" int32_t tnh_variances(int64_t srcSize, int64_t dstSize, int64_t groups, const float* src, int64_t offset,
@@ -656,12 +727,8 @@ extern "C" int32_t tnh_variances(int64_t srcSize, int64_t dstSize, int64_t group
   float* red = nullptr;
   if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
   const float* x = src + offset;
-  if (int st = launch_partial<1>(RssGivenOp{x, means, 0.f}, s, chan_vec(s, {x}), red, cx->stream,
-                                 "chan_partial_kernel<rss>"))
-    return st;
-  hipLaunchKernelGGL(total_div_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s,
-                     static_cast<float>(groups * block) - 1.f, vars);
-  return launch_status("total_div_final");
+  return launch_partial<1>(cx, RssGivenOp{x, means, 0.f}, s, chan_vec(s, {x}), red, "chan_partial_kernel<rss>",
+                           TotalDivFin{red, static_cast<float>(groups * block) - 1.f, vars});
 }
 
 extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_t groups, const float* delta,
@@ -677,12 +744,8 @@ extern "C" int32_t tnh_means_vars_delta(int64_t srcSize, int64_t dstSize, int64_
   if (int st = chan_split(s, red, dstSize, block, groups, 2, cx)) return st;
   const float* d = delta + offset;
   const float* xx = x + offset;
-  if (int st = launch_partial<2>(MvdOp{d, xx, mean, 0.f}, s, chan_vec(s, {d, xx}), red, cx->stream,
-                                 "chan_partial_kernel<mean_var_delta>"))
-    return st;
-  hipLaunchKernelGGL(means_vars_delta_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red,
-                     s, variance, mean_delta, variance_delta);
-  return launch_status("means_vars_delta_final");
+  return launch_partial<2>(cx, MvdOp{d, xx, mean, 0.f}, s, chan_vec(s, {d, xx}), red,
+                           "chan_partial_kernel<mean_var_delta>", MvdFin{red, variance, mean_delta, variance_delta});
 }
 
 extern "C" int32_t tnh_normalize_delta(int64_t deltaSize, int64_t meanSize, int64_t groups, float* delta,
@@ -720,10 +783,8 @@ extern "C" int32_t tnh_add_dots(int64_t N, int64_t dstSize, int64_t groups, cons
   if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
   const float* a = src1 + srcOffset;
   const float* b = src2 + srcOffset;
-  if (int st = launch_partial<1>(DotOp{a, b}, s, chan_vec(s, {a, b}), red, cx->stream, "chan_partial_kernel<dots>"))
-    return st;
-  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, dst);
-  return launch_status("add_dots_final");
+  return launch_partial<1>(cx, DotOp{a, b}, s, chan_vec(s, {a, b}), red, "chan_partial_kernel<dots>",
+                           AddFin{red, dst});
 }
 
 extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSize, const float* src,
@@ -739,10 +800,25 @@ extern "C" int32_t tnh_backward_bias(int64_t dstSize, float* dst, int64_t srcSiz
   float* red = nullptr;
   if (int st = chan_split(s, red, dstSize, block, batch, 1, cx)) return st;
   const float* x = src + srcOffset;
-  if (int st = launch_partial<1>(SumOp{x}, s, chan_vec(s, {x}), red, cx->stream, "chan_partial_kernel<sum>"))
-    return st;
-  hipLaunchKernelGGL(add_dots_final, dim3(static_cast<unsigned>(dstSize)), dim3(64), 0, cx->stream, red, s, dst);
-  return launch_status("add_dots_final");
+  return launch_partial<1>(cx, SumOp{x}, s, chan_vec(s, {x}), red, "chan_partial_kernel<sum>", AddFin{red, dst});
+}
+
+extern "C" int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups, const float* output,
+                                         int32_t act, const float* xNorm, const float* scales, float* delta,
+                                         float* scaleUpdates) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "bn_backward_scale: bad sizes");
+  TNH_ARG(output && xNorm && scales && delta && scaleUpdates, "bn_backward_scale: NULL buffer");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_backward_scale: activation %d",
+          act);
+  const int64_t block = N / (dstSize * groups);
+  TNH_ARG(block * dstSize * groups == N, "bn_backward_scale: sizes do not align");
+  ChanSplit s;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, dstSize, block, groups, 1, cx)) return st;
+  return launch_partial<1>(cx, BnBackOp{delta, output, xNorm, scales, act, 0.f}, s,
+                           chan_vec(s, {delta, output, xNorm}), red, "chan_partial_kernel<bn_back>",
+                           AddFin{red, scaleUpdates});
 }
 
 extern "C" int32_t tnh_softmax_batch(int64_t N, const float* input, int64_t iOffset, int64_t batch,

@@ -128,6 +128,7 @@ _PROTOS = {
     "tnh_yolo_nms_sort": [i64, i64, i64, vp, vp, vp, f32],
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_means": [i64, i64, i64, vp, i64, vp],
+    "tnh_bn_backward_scale": [i64, i64, i64, vp, i32, vp, vp, vp, vp],
     "tnh_variances": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -561,6 +562,12 @@ class TNNHip:
     def variances(self, srcSize, dstSize, groups, src, offset, means, vars):
         """Unbiased variances about the given means (the CPU path's divisor)."""
         call("tnh_variances", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
+
+    def bnBackwardScale(self, N, dstSize, groups, output, activation, xNorm, scales, delta, scaleUpdates):
+        """DeriveArray + addDots + forwardScale of batchNormBack in one pass
+        (tnh_bn_backward_scale)."""
+        call("tnh_bn_backward_scale", N, dstSize, groups, addr(output), activation, addr(xNorm), addr(scales),
+             addr(delta), addr(scaleUpdates))
 
     def meansAndVarsDelta(self, srcSize, dstSize, groups, delta, x, offset, mean, variance, mean_delta,
                           variance_delta):

@@ -200,10 +200,9 @@ class CifarTrainer:
             c, hh, f = self.dims[i]
             n = B * f * hh * hh
             d = t[f"delta{i}"]
-            hip.DeriveArray(n, t[f"out{i}"], 0, acLEAKY, d)
-            # batchNormBack
-            hip.addDots(n, f, B, t[f"xn{i}"], d, 0, p[f"u_s{i}"])
-            hip.forwardScale(n, d, 0, f, p[f"s{i}"], 1, B)
+            # leaky gradient, then batchNormBack's dgamma (addDots) and
+            # delta *= gamma (forwardScale), in one pass
+            hip.bnBackwardScale(n, f, B, t[f"out{i}"], acLEAKY, t[f"xn{i}"], p[f"s{i}"], d, p[f"u_s{i}"])
             hip.meansAndVarsDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
             hip.normalizeDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
             # conv weight gradient: im2col of the layer input, then sum_b delta_b * col_b^T

@@ -385,3 +385,33 @@ def test_means_then_variances(hip, shape, off):
     xx = x.reshape(B, Cc, -1).astype(np.float64)
     want = ((xx - shift.astype(np.float64)[None, :, None]) ** 2).sum(axis=(0, 2)) / (x.size // Cc - 1)
     assert R.rel_err(H(dv, hip), want.astype(np.float32)) <= TOL
+
+
+@pytest.mark.parametrize("shape,off,act", [((128, 32, 16, 16), 0, 9), ((3, 5, 33, 17), 1, 9), ((64, 10, 1, 1), 0, 0),
+                                           ((8, 24, 9, 9), 0, 4)])
+def test_bn_backward_scale_equals_three_calls(hip, shape, off, act):
+    """tnh_bn_backward_scale (DeriveArray + addDots + forwardScale of
+    batchNormBack in one pass) against the three separate calls: the deltas
+    and the scale updates bit for bit (16-byte and scalar walks, leaky,
+    logistic and linear)."""
+    case(f"bn backward scale {shape} offset {off} act {act}")
+    B, Cc = shape[:2]
+    out = synth.normal(370, shape, 1.0)
+    if act == 0:
+        out = (np.float32(1) / (np.float32(1) + np.exp(-out))).astype(np.float32)
+    xn = synth.normal(371, shape)
+    d0 = synth.normal(372, shape)
+    g = synth.uniform(373, (Cc,), 0.5, 1.5)
+    acc0 = synth.normal(374, (Cc,))
+    n = d0.size
+    pad = np.zeros(off, np.float32)
+    dout, dxn = D(np.concatenate([pad, out.ravel()])), D(np.concatenate([pad, xn.ravel()]))
+    da, db = D(np.concatenate([pad, d0.ravel()])), D(np.concatenate([pad, d0.ravel()]))
+    ua, ub, dg = D(acc0), D(acc0), D(g)
+    ov, xv, av, bv = (t[off:] for t in (dout, dxn, da, db))
+    hip.bnBackwardScale(n, Cc, B, ov, act, xv, dg, av, ua)
+    hip.DeriveArray(n, ov, 0, act, bv)
+    hip.addDots(n, Cc, B, xv, bv, 0, ub)
+    hip.forwardScale(n, bv, 0, Cc, dg, 1, B)
+    assert np.array_equal(H(da, hip), H(db, hip))
+    assert np.array_equal(H(ua, hip), H(ub, hip))
