@@ -503,6 +503,60 @@ int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch,
                        const float *mean, const float *variance,
                        const float *scales, const float *biases, int32_t act);
 
+/* ---- the element-wise methods of TNNCuda for the layers around the
+ *      convolution path (LRN, logistic / L2 cost, dropout, swish, a yolo
+ *      layer with scale_x_y != 1) ------------------------------------- */
+/* TNNCuda.subvv / mulvv (nncuda.pas:911, 924): dst = src1 - src2 / src1 * src2
+ * element by element, each with its offset and stride. */
+int32_t tnh_subvv(int64_t N, const float *src1, int64_t src1Offset,
+                  int64_t inca, const float *src2, int64_t src2Offset,
+                  int64_t incb, float *dst, int64_t dstOffset, int64_t incc);
+int32_t tnh_mulvv(int64_t N, const float *src1, int64_t src1Offset,
+                  int64_t inca, const float *src2, int64_t src2Offset,
+                  int64_t incb, float *dst, int64_t dstOffset, int64_t incc);
+/* TNNCuda.fmavv (nncuda.pas:937, an empty method in the reference): dst =
+ * src1 * src2 + src3, a multiply then an add. */
+int32_t tnh_fmavv(int64_t N, const float *src1, int64_t src1Offset,
+                  int64_t inca, const float *src2, int64_t src2Offset,
+                  int64_t incb, const float *src3, int64_t src3Offset,
+                  int64_t incc, float *dst, int64_t dstOffset, int64_t incd);
+/* TNNCuda.power (nncuda.pas:966): y = x^a, evaluated in double and stored as
+ * single (TTensor.power's Math.Power, ntensors.pas:8507). */
+int32_t tnh_power(int64_t N, const float *x, int64_t xOffset, int64_t incx,
+                  float a, float *y, int64_t yOffset, int64_t incy);
+/* TNNCuda.fmavss (nncuda.pas:1290; called by TYoloLayer.forwardGPU for
+ * scale_x_y != 1, nyololayer.pas:1099): dst[offset + i] = src[offset + i] *
+ * scalar + bias, a multiply then an add (sfmavss, ntensors.pas:3355). */
+int32_t tnh_fmavss(int64_t N, const float *src, int64_t offset, float scalar,
+                   float bias, float *dst);
+/* TNNCuda.crossEntropyLogistic (nncuda.pas:1005): error = -t log(max(p,eps))
+ * - (1-t) log(max(1-p,eps)), delta = t - p, in single precision. */
+int32_t tnh_cross_entropy_logistic(int64_t N, const float *pred,
+                                   const float *truth, float *delta,
+                                   float *error);
+/* TNNCuda.costL2 (nncuda.pas:1540): r = truth - pred, delta = r, error = r*r */
+int32_t tnh_cost_l2(int64_t N, const float *pred, const float *truth,
+                    float *delta, float *error);
+/* TNNCuda.inverseSqrt (nncuda.pas:1563): dst[i*stride + offset] =
+ * 1 / sqrt(max(src[i*stride + offset], 1e-6)); alpha is unused, as in
+ * TNNCuda's kernel. */
+int32_t tnh_inverse_sqrt(int64_t N, float alpha, const float *src, float *dst,
+                         int64_t stride, int64_t offset);
+/* TNNCuda.activateArraySWISH (nncuda.pas:544): s = 1/(1 + exp(-x)),
+ * outSigmoid = s, out = x*s (x, outSigmoid and out at + offset). */
+int32_t tnh_activate_swish(int64_t N, const float *x, int64_t offset,
+                           float *outSigmoid, float *out);
+/* TNNCuda.forwardDropout (nncuda.pas:1512): rnd[i] = a uniform [0, 1) draw,
+ * dst[i] = rnd[i] < probability ? 0 : src[i]*scale.  TNNCuda draws a seed
+ * on the host per call; here the caller passes it: element i takes the top
+ * 24 bits of splitmix64(seed + i), so a call is reproducible. */
+int32_t tnh_dropout_fwd(int64_t N, const float *src, float probability,
+                        float scale, int64_t seed, float *rnd, float *dst);
+/* TNNCuda.backwardDropout (nncuda.pas:1527): dst = rnd < probability ? 0 :
+ * src*scale, with the forward's rnd. */
+int32_t tnh_dropout_bwd(int64_t N, const float *src, float probability,
+                        float scale, const float *rnd, float *dst);
+
 /* ---- training direction (config-3 step: conv-BN-leaky, pooling,
  *      connected, softmax cross-entropy, SGD) --------------------------- */
 /* TNNCuda.meansAndVars (nncuda.pas:1308) with the CPU semantics of

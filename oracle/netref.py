@@ -4,7 +4,7 @@ INFRASTRUCTURE ONLY: parity tests and the cpu_baseline leg of bench.py).
 Runs the reference layer semantics one layer at a time: conv (Conv2D + bias +
 activation), shortcut (addvv + linear), route (per-image concat, or the
 reference's whole-tensor concat), upsample, maxpool, yolo (copy + logistic,
-exact reciprocal).  Returns every layer's output."""
+exact reciprocal, then scale_x_y's x*s + (1-s)/2 on x and y).  Returns every layer's output."""
 import numpy as np
 
 from oracle import refcpu as R
@@ -36,6 +36,10 @@ def forward(layers, weights, x, route_mode="image"):
             y, _ = R.maxpool_fwd(prev, L["size"], L["stride"], L["stride"], L["pad"], with_idx=False)
         elif t == "yolo":
             y = R.yolo_fwd(prev, L["n"], L["classes"], exact=True)
+            s = np.float32(L.get("scale_xy", 1.0))
+            if s != 1:  # output.FusedMultiplyAdd on x, y (nyololayer.pas:822-823)
+                v = y.reshape(B, L["n"], L["classes"] + 5, -1)
+                v[:, :, :2] = (v[:, :, :2] * s).astype(np.float32) + np.float32(0.5) * (np.float32(1) - s)
         else:
             raise ValueError(t)
         outs.append(y)

@@ -15,15 +15,10 @@ unit nnhip;
   one stream; readBuffer / writeBuffer block and finish() waits, as in
   TNNCuda.
 
-  Methods of TNNCuda that serve layers outside the convolution path
-  (dropout, swish, L2 / logistic costs, element-wise power, multiply and
-  fused multiply-add, separate means / variances) and its CUDA run-time
-  compilation (compileToCUBIN, loadCUBIN, compileFile, loadCUBinFile) raise
-  ETNHError: the kernels here are compiled ahead of time for gfx950 and
-  cover the convolution path (SGEMM, im2col / col2im, bias / batch-norm /
-  activation epilogues, pooling, upsample, route, YOLO head, the training
-  step's reductions and updates).  A layer needing one of those keeps its
-  CPU implementation. }
+  Every TNNCuda method has a kernel here except its CUDA run-time
+  compilation (compileToCUBIN, loadCUBIN, compileFile, loadCUBinFile),
+  which raises ETNHError: the kernels are compiled ahead of time for
+  gfx950, so there is no source to compile at run time. }
 
 {$mode delphi}{$Z4}{$H+}{$POINTERMATH ON}
 
@@ -181,6 +176,26 @@ function tnh_softmax_batch(N: Int64; input: PSingle; iOffset, batch, batchSize, 
   temp: Single; output: PSingle; oOffset: Int64): LongInt; cdecl; external libtnh;
 function tnh_cross_entropy_softmax(N: Int64; pred, truth, delta, error: PSingle): LongInt; cdecl; external libtnh;
 function tnh_clamp(N: Int64; alpha: Single; src, dst: PSingle; stride, offset: Int64): LongInt; cdecl;
+  external libtnh;
+function tnh_subvv(N: Int64; src1: PSingle; src1Offset, inca: Int64; src2: PSingle; src2Offset, incb: Int64;
+  dst: PSingle; dstOffset, incc: Int64): LongInt; cdecl; external libtnh;
+function tnh_mulvv(N: Int64; src1: PSingle; src1Offset, inca: Int64; src2: PSingle; src2Offset, incb: Int64;
+  dst: PSingle; dstOffset, incc: Int64): LongInt; cdecl; external libtnh;
+function tnh_fmavv(N: Int64; src1: PSingle; src1Offset, inca: Int64; src2: PSingle; src2Offset, incb: Int64;
+  src3: PSingle; src3Offset, incc: Int64; dst: PSingle; dstOffset, incd: Int64): LongInt; cdecl; external libtnh;
+function tnh_power(N: Int64; x: PSingle; xOffset, incx: Int64; a: Single; y: PSingle; yOffset, incy: Int64): LongInt;
+  cdecl; external libtnh;
+function tnh_fmavss(N: Int64; src: PSingle; offset: Int64; scalar, bias: Single; dst: PSingle): LongInt; cdecl;
+  external libtnh;
+function tnh_cross_entropy_logistic(N: Int64; pred, truth, delta, error: PSingle): LongInt; cdecl; external libtnh;
+function tnh_cost_l2(N: Int64; pred, truth, delta, error: PSingle): LongInt; cdecl; external libtnh;
+function tnh_inverse_sqrt(N: Int64; alpha: Single; src, dst: PSingle; stride, offset: Int64): LongInt; cdecl;
+  external libtnh;
+function tnh_activate_swish(N: Int64; x: PSingle; offset: Int64; outSigmoid, output: PSingle): LongInt; cdecl;
+  external libtnh;
+function tnh_dropout_fwd(N: Int64; src: PSingle; probability, scale: Single; seed: Int64; rnd, dst: PSingle): LongInt;
+  cdecl; external libtnh;
+function tnh_dropout_bwd(N: Int64; src: PSingle; probability, scale: Single; rnd, dst: PSingle): LongInt; cdecl;
   external libtnh;
 function tnh_avgpool_fwd(batch, c, h, w: Int64; input, output: PSingle): LongInt; cdecl; external libtnh;
 function tnh_avgpool_bwd(batch, c, h, w: Int64; delta, deltaIn: PSingle): LongInt; cdecl; external libtnh;
@@ -421,7 +436,7 @@ end;
 procedure TNNHip<T>.activateArraySWISH(const N: SizeInt; const x: TCUMem; const offset: SizeInt;
   const output_sigmoid, output: TCUMem);
 begin
-  unsupported('activateArraySWISH');
+  check(tnh_activate_swish(N, PSingle(x), offset, PSingle(output_sigmoid), PSingle(output)));
 end;
 
 procedure TNNHip<T>.DeriveArray(const N: SizeInt; const x: TCUMem; const offset: SizeInt; const activation: longint;
@@ -481,20 +496,23 @@ end;
 procedure TNNHip<T>.subvv(const N: SizeInt; const src1: TCUMem; const src1Offset, inca: SizeInt; const src2: TCUMem;
   const src2Offset, incb: SizeInt; dst: TCUMem; const dstOffset, incc: SizeInt);
 begin
-  unsupported('subvv');
+  check(tnh_subvv(N, PSingle(src1), src1Offset, inca, PSingle(src2), src2Offset, incb, PSingle(dst), dstOffset,
+    incc));
 end;
 
 procedure TNNHip<T>.mulvv(const N: SizeInt; const src1: TCUMem; const src1Offset, inca: SizeInt; const src2: TCUMem;
   const src2Offset, incb: SizeInt; dst: TCUMem; const dstOffset, incc: SizeInt);
 begin
-  unsupported('mulvv');
+  check(tnh_mulvv(N, PSingle(src1), src1Offset, inca, PSingle(src2), src2Offset, incb, PSingle(dst), dstOffset,
+    incc));
 end;
 
 procedure TNNHip<T>.fmavv(const N: SizeInt; const src1: TCUMem; const src1Offset, inca: SizeInt; const src2: TCUMem;
   const src2Offset, incb: SizeInt; const src3: TCUMem; const src3Offset, incc: SizeInt; dst: TCUMem;
   const dstOffset, incd: SizeInt);
 begin
-  unsupported('fmavv');
+  check(tnh_fmavv(N, PSingle(src1), src1Offset, inca, PSingle(src2), src2Offset, incb, PSingle(src3), src3Offset,
+    incc, PSingle(dst), dstOffset, incd));
 end;
 
 procedure TNNHip<T>.axpy(const N: SizeInt; const a: T; const x: TCUMem; const xOffset: SizeInt; const incx: SizeInt;
@@ -506,7 +524,7 @@ end;
 procedure TNNHip<T>.power(const N: SizeInt; const x: TCUMem; const xOffset: SizeInt; const incx: SizeInt;
   const a: T; const y: TCUMem; const yOffset: SizeInt; const incy: SizeInt);
 begin
-  unsupported('power');
+  check(tnh_power(N, PSingle(x), xOffset, incx, S(a), PSingle(y), yOffset, incy));
 end;
 
 procedure TNNHip<T>.scale(const N: SizeInt; const a: T; const x: TCUMem; const stride: SizeInt);
@@ -516,7 +534,7 @@ end;
 
 procedure TNNHip<T>.crossEntropyLogistic(const N: SizeInt; const pred, truth: TCUMem; delta, error: TCUMem);
 begin
-  unsupported('crossEntropyLogistic');
+  check(tnh_cross_entropy_logistic(N, PSingle(pred), PSingle(truth), PSingle(delta), PSingle(error)));
 end;
 
 procedure TNNHip<T>.fill(const N: SizeInt; const x: TCUMem; const offset: SizeInt; const val: T;
@@ -583,7 +601,7 @@ end;
 procedure TNNHip<T>.fmavss(const N: SizeInt; const src: TCUMem; const offset: SizeInt; const scalar, bias: T;
   dst: TCUMem);
 begin
-  unsupported('fmavss');
+  check(tnh_fmavss(N, PSingle(src), offset, S(scalar), S(bias), PSingle(dst)));
 end;
 
 procedure TNNHip<T>.meansAndVars(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
@@ -647,18 +665,19 @@ end;
 procedure TNNHip<T>.forwardDropout(const N: SizeInt; const src: TCUMem; const probability, scale: T; rnd: TCUMem;
   dst: TCUMem);
 begin
-  unsupported('forwardDropout');
+  // a fresh seed per call, drawn on the host as TNNCuda does (nncuda.pas:1521)
+  check(tnh_dropout_fwd(N, PSingle(src), S(probability), S(scale), random($10000000), PSingle(rnd), PSingle(dst)));
 end;
 
 procedure TNNHip<T>.backwardDropout(const N: SizeInt; const src: TCUMem; const probability, scale: T;
   const rnd: TCUMem; dst: TCUMem);
 begin
-  unsupported('backwardDropout');
+  check(tnh_dropout_bwd(N, PSingle(src), S(probability), S(scale), PSingle(rnd), PSingle(dst)));
 end;
 
 procedure TNNHip<T>.costL2(const N: SizeInt; const pred, truth, delta, error: TCUMem);
 begin
-  unsupported('costL2');
+  check(tnh_cost_l2(N, PSingle(pred), PSingle(truth), PSingle(delta), PSingle(error)));
 end;
 
 procedure TNNHip<T>.clamp(const N: SizeInt; const alpha: T; const src, dst: TCUMem; const stride: SizeInt;
@@ -670,7 +689,7 @@ end;
 procedure TNNHip<T>.inverseSqrt(const N: SizeInt; const alpha: T; const src, dst: TCUMem; const stride: SizeInt;
   offset: SizeInt);
 begin
-  unsupported('inverseSqrt');
+  check(tnh_inverse_sqrt(N, S(alpha), PSingle(src), PSingle(dst), stride, offset));
 end;
 
 procedure TNNHip<T>.finish();

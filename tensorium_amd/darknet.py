@@ -111,9 +111,10 @@ def parse_cfg(text, height=None, width=None):
             a = [float(v) for v in o["anchors"].split(",")] if "anchors" in o else [0.5] * (2 * (max(mask) + 1))
             if len(a) % 2 or max(mask) >= len(a) // 2:
                 raise ValueError(f"yolo {idx}: mask {mask} needs {max(mask) + 1} anchors, cfg has {len(a) // 2}")
-            if float(o.get("scale_x_y", 1)) != 1 or int(o.get("new_coords", 0)) != 0:
-                raise ValueError(f"yolo {idx}: scale_x_y != 1 / new_coords are not supported")
-            L.update(n=len(mask), classes=classes, mask=mask,
+            if int(o.get("new_coords", 0)) != 0:
+                raise ValueError(f"yolo {idx}: new_coords is not supported")
+            # scale_x_y (parseYolo, nparser.pas:554): x, y = x*s + (1-s)/2 after the logistic
+            L.update(n=len(mask), classes=classes, mask=mask, scale_xy=float(o.get("scale_x_y", 1)),
                      anchors=[(a[2 * m], a[2 * m + 1]) for m in mask], out=shape)
         else:
             raise ValueError(f"unsupported layer type [{name}]")
@@ -577,8 +578,23 @@ class Network:
                 C, h, ww = L["in"]
                 src, soff, spix = self.nhwc_store(i - 1)
                 hip.yoloForwardNHWC(B, L["n"], L["classes"], h, ww, src, soff, spix, self.out[i])
+            self._scale_xy(L, self.out[i])
             heads.append(self.out[i])
         return x
+
+    def _scale_xy(self, L, out):
+        """TYoloLayer.forwardGPU's scale_x_y step (nyololayer.pas:1098-1099):
+        per image and anchor, the 2*h*w x / y entries become v*s + (1-s)/2
+        (fmavss, a multiply then an add); nothing to do for s = 1."""
+        s = np.float32(L.get("scale_xy", 1.0))
+        if s == 1:
+            return
+        _, h, w = L["out"]
+        bias = float(np.float32(0.5) * (np.float32(1) - s))
+        per = (L["classes"] + 5) * h * w
+        for b in range(self.batch):
+            for a in range(L["n"]):
+                self.hip.fmavss(2 * h * w, out, (b * L["n"] + a) * per, float(s), bias, out)
 
     def _layer(self, L, prev, heads):
         if self.layout == "nhwc":
@@ -637,6 +653,7 @@ class Network:
         elif t == "yolo":
             C, h, ww = L["in"]
             hip.yoloForward(B, L["n"], L["classes"], h, ww, prev, self.out[i])
+            self._scale_xy(L, self.out[i])
             heads.append(self.out[i])
             prev = self.out[i]
         return prev

@@ -137,6 +137,17 @@ _PROTOS = {
     "tnh_softmax_batch": [i64, vp, i64, i64, i64, i64, i64, i64, f32, vp, i64],
     "tnh_cross_entropy_softmax": [i64, vp, vp, vp, vp],
     "tnh_clamp": [i64, f32, vp, vp, i64, i64],
+    "tnh_subvv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
+    "tnh_mulvv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
+    "tnh_fmavv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
+    "tnh_power": [i64, vp, i64, i64, f32, vp, i64, i64],
+    "tnh_fmavss": [i64, vp, i64, f32, f32, vp],
+    "tnh_cross_entropy_logistic": [i64, vp, vp, vp, vp],
+    "tnh_cost_l2": [i64, vp, vp, vp, vp],
+    "tnh_inverse_sqrt": [i64, f32, vp, vp, i64, i64],
+    "tnh_activate_swish": [i64, vp, i64, vp, vp],
+    "tnh_dropout_fwd": [i64, vp, f32, f32, i64, vp, vp],
+    "tnh_dropout_bwd": [i64, vp, f32, f32, vp, vp],
     "tnh_avgpool_fwd": [i64, i64, i64, i64, vp, vp],
     "tnh_avgpool_bwd": [i64, i64, i64, i64, vp, vp],
     "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
@@ -592,6 +603,49 @@ class TNNHip:
 
     def clamp(self, N, alpha, src, dst, stride=1, offset=0):
         call("tnh_clamp", N, alpha, addr(src), addr(dst), stride, offset)
+
+    def subvv(self, N, src1, src1Offset, inca, src2, src2Offset, incb, dst, dstOffset, incc):
+        call("tnh_subvv", N, addr(src1), src1Offset, inca, addr(src2), src2Offset, incb, addr(dst), dstOffset, incc)
+
+    def mulvv(self, N, src1, src1Offset, inca, src2, src2Offset, incb, dst, dstOffset, incc):
+        call("tnh_mulvv", N, addr(src1), src1Offset, inca, addr(src2), src2Offset, incb, addr(dst), dstOffset, incc)
+
+    def fmavv(self, N, src1, src1Offset, inca, src2, src2Offset, incb, src3, src3Offset, incc, dst, dstOffset,
+              incd):
+        call("tnh_fmavv", N, addr(src1), src1Offset, inca, addr(src2), src2Offset, incb, addr(src3), src3Offset,
+             incc, addr(dst), dstOffset, incd)
+
+    def power(self, N, x, xOffset, incx, a, y, yOffset, incy):
+        call("tnh_power", N, addr(x), xOffset, incx, a, addr(y), yOffset, incy)
+
+    def fmavss(self, N, src, offset, scalar, bias, dst):
+        call("tnh_fmavss", N, addr(src), offset, scalar, bias, addr(dst))
+
+    def crossEntropyLogistic(self, N, pred, truth, delta, error):
+        call("tnh_cross_entropy_logistic", N, addr(pred), addr(truth), addr(delta), addr(error))
+
+    def costL2(self, N, pred, truth, delta, error):
+        call("tnh_cost_l2", N, addr(pred), addr(truth), addr(delta), addr(error))
+
+    def inverseSqrt(self, N, alpha, src, dst, stride=1, offset=0):
+        call("tnh_inverse_sqrt", N, alpha, addr(src), addr(dst), stride, offset)
+
+    def activateArraySWISH(self, N, x, offset, output_sigmoid, output):
+        call("tnh_activate_swish", N, addr(x), offset, addr(output_sigmoid), addr(output))
+
+    def forwardDropout(self, N, src, probability, scale, rnd, dst, seed=None):
+        """rnd receives the per-element draws, dst the dropped/scaled values.
+        A fresh seed is drawn per call unless one is given, as TNNCuda
+        draws one on the host per call (nncuda.pas:1512)."""
+        if seed is None:
+            self._dropout_seed = getattr(self, "_dropout_seed", 0x9E3779B9) * 6364136223846793005 + 1442695040888963407
+            self._dropout_seed &= (1 << 63) - 1
+            seed = self._dropout_seed
+        call("tnh_dropout_fwd", N, addr(src), probability, scale, seed, addr(rnd), addr(dst))
+        return seed
+
+    def backwardDropout(self, N, src, probability, scale, rnd, dst):
+        call("tnh_dropout_bwd", N, addr(src), probability, scale, addr(rnd), addr(dst))
 
     def avgPoolForward(self, batch, c, h, w, input, output):
         call("tnh_avgpool_fwd", batch, c, h, w, addr(input), addr(output))

@@ -1,8 +1,12 @@
 """Host-side planning of darknet.Network (CPU): how a batch is split into
-passes so that no kernel call addresses more than 2 GiB."""
+passes so that no kernel call addresses more than 2 GiB; the cfg options
+the parser accepts."""
+import os
+
+import numpy as np
 import pytest
 
-from tensorium_amd import darknet
+from tensorium_amd import darknet, synth
 
 
 def test_pass_batch_yolov3():
@@ -30,3 +34,40 @@ def test_reference_route_mode_is_not_split():
     _, layers = darknet.load_cfg("yolov3.cfg", 64, 64)
     with pytest.raises(NotImplementedError, match="route_mode='reference'"):
         darknet.Network(None, layers, 4, {}, route_mode="reference", max_pass_batch=2)
+
+
+def _tiny_with(extra):
+    with open(os.path.join(darknet.CFG_DIR, "yolov3-tiny.cfg")) as f:
+        return f.read().replace("[yolo]", "[yolo]\n" + extra)
+
+
+def test_yolo_scale_xy_parsed_and_new_coords_refused():
+    """parseYolo's scale_x_y (nparser.pas:554, default 1) reaches each yolo
+    layer; new_coords (nparser.pas:556) changes the box decode and stays
+    refused."""
+    _, layers = darknet.load_cfg("yolov3-tiny.cfg")
+    assert [L["scale_xy"] for L in layers if L["type"] == "yolo"] == [1.0, 1.0]
+    _, layers = darknet.parse_cfg(_tiny_with("scale_x_y=1.05"))
+    assert [L["scale_xy"] for L in layers if L["type"] == "yolo"] == [1.05, 1.05]
+    with pytest.raises(ValueError, match="new_coords"):
+        darknet.parse_cfg(_tiny_with("new_coords=1"))
+
+
+def test_oracle_scale_xy_maps_the_logistic_range():
+    """The oracle's yolo output with scale_x_y = s: x, y in (0, 1) map to
+    (-(s-1)/2, (s+1)/2) (the grid-sensitivity stretch), exactly s*v + (1-s)/2
+    of the unscaled output at s = 2 (every step exact in fp32 for v = k/2^m),
+    and the w, h, objectness and class entries are unchanged."""
+    from oracle import netref
+    _, plain = darknet.parse_cfg(_tiny_with(""), 64, 64)
+    _, scaled = darknet.parse_cfg(_tiny_with("scale_x_y=2"), 64, 64)
+    W = darknet.synthetic_weights(plain)
+    x = synth.uniform(3, (1, 3, 64, 64))
+    a, b = netref.forward(plain, W, x), netref.forward(scaled, W, x)
+    for i in (16, 23):
+        L = plain[i]
+        va = a[i].reshape(1, L["n"], L["classes"] + 5, -1)
+        vb = b[i].reshape(1, L["n"], L["classes"] + 5, -1)
+        assert np.array_equal(vb[:, :, 2:], va[:, :, 2:])
+        assert np.array_equal(vb[:, :, :2], 2 * va[:, :, :2] - np.float32(0.5))
+        assert vb[:, :, :2].min() > -0.5 and vb[:, :, :2].max() < 1.5

@@ -487,3 +487,27 @@ def test_yolov3_tiny_vs_oracle(hip, layout):
             assert e <= TOL, (b, i, e)
         for h, i in zip(heads, (16, 23)):
             assert R.rel_err(h[b:b + 1].cpu().numpy(), ref[i]) <= TOL
+
+
+@pytest.mark.parametrize("layout", ["nchw", "nhwc"])
+def test_yolov3_tiny_scale_xy_vs_oracle(hip, layout):
+    """YOLOv3-tiny with scale_x_y = 1.05 on both yolo layers (the value
+    YOLOv4 cfgs use): the yolo outputs at batch 2 against the oracle run per
+    image, within the per-tensor bound; the fused conv + yolo head path
+    (channels-last) and the plain yolo kernel (NCHW) both take the step."""
+    print(f"[case] yolov3-tiny-256 scale_x_y=1.05 batch 2 {layout} vs oracle", flush=True)
+    import os
+    with open(os.path.join(darknet.CFG_DIR, "yolov3-tiny.cfg")) as f:
+        text = f.read().replace("[yolo]", "[yolo]\nscale_x_y=1.05")
+    _, layers = darknet.parse_cfg(text, 256, 256)
+    W = darknet.synthetic_weights(layers)
+    x = synth.uniform(6, (2, 3, 256, 256))
+    net = darknet.Network(hip, layers, 2, W, layout=layout)
+    heads = net.forward(torch.from_numpy(x).cuda())
+    hip.finish()
+    for b in range(2):
+        ref = netref.forward(layers, W, x[b:b + 1])
+        for h, i in zip(heads, (16, 23)):
+            e = R.rel_err(h[b:b + 1].cpu().numpy(), ref[i])
+            print(f"image {b} yolo {i}: {e:.3e}", flush=True)
+            assert e <= TOL, (b, i, e)
