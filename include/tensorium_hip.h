@@ -350,7 +350,9 @@ int32_t tnh_route(int64_t batch, int32_t n, const float *const *srcs,
 /* TNNCuda.forwardMaxPool (nncuda.pas:1088) with the CPU semantics of
  * TMaxPoolLayer.forwardMaxPool (nMaxPoolLayer.pas:363-455): window offset
  * -pad div 2, strict '>', -MaxSingle init, global int64 indices.
- * indexes may be NULL (inference). */
+ * indexes may be NULL (inference).  outC != c selects maxpool_depth
+ * (nMaxPoolLayer.pas:372-399; outH = h, outW = w required): output channel g
+ * is the max over input channels g, g + outC, ... < c. */
 int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH,
                         int64_t outW, const float *input, int64_t c,
                         int64_t h, int64_t w, int64_t strideX, int64_t strideY,

@@ -32,6 +32,8 @@ def forward(layers, weights, x, route_mode="image"):
                 y = np.concatenate([s.ravel() for s in srcs]).reshape((B,) + L["out"])
         elif t == "upsample":
             y = R.upsample_fwd(prev, L["stride"], L["scale"])
+        elif t == "maxpool" and L.get("depth"):
+            y, _ = R.maxpool_depth_fwd(prev, L["out"][0], with_idx=False)
         elif t == "maxpool":
             y, _ = R.maxpool_fwd(prev, L["size"], L["stride"], L["stride"], L["pad"], with_idx=False)
         elif t == "yolo":

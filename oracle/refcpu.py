@@ -172,6 +172,27 @@ def maxpool_fwd(x, size, strideX, strideY, pad, with_idx=True):
     return out, idx
 
 
+def maxpool_depth_fwd(x, outC, with_idx=True):
+    """maxpool_depth (TMaxPoolLayer.forwardMaxPool's first branch,
+    nMaxPoolLayer.pas:372-399): out[b, g, i, j] = max over input channels
+    k = g, g + outC, ... < c of x[b, k, i, j], scanned in ascending k with a
+    strict '>' from -MaxSingle; the index is the input's global offset
+    j + w*(i + h*(k + c*b)), -1 when nothing beats the start value."""
+    x = _f32(x)
+    B, Cc, H, W = x.shape
+    out = np.full((B, outC, H, W), -np.finfo(np.float32).max, np.float32)
+    idx = np.full((B, outC, H, W), -1, np.int64)
+    base = (np.arange(B, dtype=np.int64)[:, None, None] * Cc * H * W
+            + np.arange(H * W, dtype=np.int64).reshape(1, H, W))
+    for g in range(outC):
+        for k in range(g, Cc, outC):
+            v = x[:, k]
+            hit = v > out[:, g]
+            out[:, g] = np.where(hit, v, out[:, g])
+            idx[:, g] = np.where(hit, base + k * H * W, idx[:, g])
+    return out, (idx if with_idx else None)
+
+
 def maxpool_bwd(idx, dOut, dIn):
     assert dIn.dtype == np.float32 and dIn.flags.c_contiguous
     idx = np.ascontiguousarray(idx, np.int64)

@@ -35,6 +35,34 @@ struct PoolGeom {
   int64_t C, H, W, OH, OW, size, sX, sY, off;
 };
 
+// maxpool_depth (the CPU branch of TMaxPoolLayer.forwardMaxPool,
+// nMaxPoolLayer.pas:372-399): output channel g of pixel p is the max over
+// input channels g, g + outC, g + 2*outC, ... < c, strict '>', from
+// -MaxSingle, with the input's global index (-1 when nothing beats the
+// start value).
+__global__ __launch_bounds__(kThreads) void maxpool_depth_kernel(int64_t total, int64_t c, int64_t outC, int64_t hw,
+                                                                 const float* __restrict__ in,
+                                                                 float* __restrict__ out, int64_t* __restrict__ idx) {
+  GRID_STRIDE(o, total) {
+    const int64_t p = o % hw;
+    const int64_t t = o / hw;
+    const int64_t g = t % outC;
+    const int64_t b = t / outC;
+    float mx = -FLT_MAX;
+    int64_t mi = -1;
+    for (int64_t k = g; k < c; k += outC) {
+      const int64_t index = (b * c + k) * hw + p;
+      const float v = in[index];
+      if (v > mx) {
+        mi = index;
+        mx = v;
+      }
+    }
+    out[o] = mx;
+    if (idx) idx[o] = mi;
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(PoolGeom g, int64_t total, const float* __restrict__ in,
                                                                float* __restrict__ out, int64_t* __restrict__ idx) {
   GRID_STRIDE(o, total) {
@@ -357,12 +385,23 @@ extern "C" int32_t tnh_maxpool_fwd(int64_t batch, int64_t outC, int64_t outH, in
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(batch >= 0 && c > 0 && h > 0 && w > 0 && kernelSize > 0 && strideX > 0 && strideY > 0 && padding >= 0,
           "maxpool_fwd: bad geometry");
-  TNH_ARG(outC == c, "maxpool_fwd: outC %lld != c %lld (maxpool_depth is not supported)", (long long)outC,
-          (long long)c);
+  TNH_ARG(input && output, "maxpool_fwd: NULL buffer");
+  if (outC != c) {  // maxpool_depth: the output keeps the input's h x w (nMaxPoolLayer.pas:98-102)
+    TNH_ARG(outC > 0 && outH == h && outW == w, "maxpool_fwd: outC %lld != c %lld (maxpool_depth) needs outH = h "
+            "and outW = w", (long long)outC, (long long)c);
+    const int64_t total = batch * outC * h * w;
+    if (total == 0) return TNH_OK;
+    if (indexes) {  // every input element feeds at most one output: the backward scatters
+      std::lock_guard<std::mutex> lk(g_pool_mu);
+      g_pool_geom[indexes] = PoolRecord{PoolGeom{outC, h, w, h, w, 1, 1, 1, 0}, batch};
+    }
+    hipLaunchKernelGGL(maxpool_depth_kernel, dim3(grid_for(total)), dim3(kThreads), 0, cx->stream, total, c, outC,
+                       h * w, input, output, indexes);
+    return launch_status("maxpool_depth_kernel");
+  }
   TNH_ARG(outH == (h + padding - kernelSize) / strideY + 1 && outW == (w + padding - kernelSize) / strideX + 1,
           "maxpool_fwd: output dims do not match (h + pad - size)/stride + 1");
   TNH_ARG(outH > 0 && outW > 0, "maxpool_fwd: empty output");
-  TNH_ARG(input && output, "maxpool_fwd: NULL buffer");
   const int64_t total = batch * outC * outH * outW;
   if (total == 0) return TNH_OK;
   PoolGeom g{c, h, w, outH, outW, kernelSize, strideX, strideY, -padding / 2};

@@ -101,7 +101,11 @@ def parse_cfg(text, height=None, width=None):
             s = int(o.get("stride", 1))
             pad = int(o.get("padding", k - 1))  # parseMaxPool default (nparser.pas:257)
             C, h, w = shape
-            L.update(size=k, stride=s, pad=pad, out=(C, (h + pad - k) // s + 1, (w + pad - k) // s + 1))
+            depth = int(o.get("maxpool_depth", 0))  # nparser.pas:258-259
+            if depth:  # max over channel groups, the image size kept (nMaxPoolLayer.pas:98-102)
+                L.update(size=k, stride=s, pad=pad, depth=True, out=(int(o.get("out_channels", 1)), h, w))
+            else:
+                L.update(size=k, stride=s, pad=pad, out=(C, (h + pad - k) // s + 1, (w + pad - k) // s + 1))
         elif name == "yolo":
             mask = [int(v) for v in o.get("mask", "0").split(",")]
             classes = int(o.get("classes", 80))
@@ -329,6 +333,8 @@ class Network:
         L0 = layers[0]
         if L0["type"] != "convolutional" or L0["size"] != 3 or L0["in"][0] > 4:
             raise NotImplementedError("channels-last networks start with a 3x3 convolution on <= 4 channels")
+        if any(L.get("depth") for L in layers):
+            raise NotImplementedError("maxpool_depth needs layout='nchw'")
         self.store = {}
         self.copy_srcs = {}
         for L in layers:
@@ -646,8 +652,8 @@ class Network:
             prev = self.out[i]
         elif t == "maxpool":
             C, h, ww = L["in"]
-            _, oh, ow = L["out"]
-            hip.forwardMaxPool(B, C, oh, ow, prev, C, h, ww, L["stride"], L["stride"], L["pad"], L["size"],
+            oc, oh, ow = L["out"]
+            hip.forwardMaxPool(B, oc, oh, ow, prev, C, h, ww, L["stride"], L["stride"], L["pad"], L["size"],
                                None, self.out[i])
             prev = self.out[i]
         elif t == "yolo":

@@ -810,6 +810,34 @@ def test_maxpool_forward_backward_bit_exact(hip, size, stride, pad, shape):
         assert np.array_equal(H(ddIn, hip), ref)
 
 
+@pytest.mark.parametrize("c,outC", [(64, 4), (30, 7), (3, 5)])
+def test_maxpool_depth_bit_exact(hip, c, outC):
+    """maxpool_depth (outC != c, the image size kept): values and int64
+    indices against the oracle bit for bit (NaN, -inf and ties included;
+    outC > c leaves empty groups), and TNNCuda's 7-argument backward
+    scatters through them."""
+    case(f"maxpool_depth c{c} outC{outC}")
+    B, Hh, W = 2, 9, 13
+    x = synth.normal(65, (B, c, Hh, W))
+    x[0, :, 0, 0] = 1.0
+    x[1, :, 2, 3] = -np.inf
+    x[0, 0, 4, 4] = np.nan
+    out, idx = R.maxpool_depth_fwd(x, outC)
+    dout = torch.empty(out.shape, dtype=torch.float32, device="cuda")
+    didx = torch.empty(out.shape, dtype=torch.int64, device="cuda")
+    hip.forwardMaxPool(B, outC, Hh, W, D(x), c, Hh, W, 1, 1, 0, 1, didx, dout)
+    assert np.array_equal(H(dout, hip), out)
+    assert np.array_equal(H(didx, hip), idx)
+    delta = synth.normal(66, out.shape)
+    dIn0 = synth.normal(67, x.shape)
+    ref = R.maxpool_bwd(idx, delta, dIn0.copy())
+    ddIn = D(dIn0)
+    hip.backwardMaxPool(B, outC, Hh, W, ddIn, didx, D(delta))
+    assert np.array_equal(H(ddIn, hip), ref)
+    with pytest.raises(TNHError, match="maxpool_depth"):
+        hip.forwardMaxPool(B, outC, Hh - 1, W, D(x), c, Hh, W, 1, 1, 0, 1, didx, dout)
+
+
 def test_maxpool_inference_no_indexes(hip):
     case("maxpool without indexes")
     x = synth.normal(64, (2, 3, 8, 8))

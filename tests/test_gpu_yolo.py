@@ -511,3 +511,54 @@ def test_yolov3_tiny_scale_xy_vs_oracle(hip, layout):
             e = R.rel_err(h[b:b + 1].cpu().numpy(), ref[i])
             print(f"image {b} yolo {i}: {e:.3e}", flush=True)
             assert e <= TOL, (b, i, e)
+
+
+DEPTH_CFG = """[net]
+width=64
+height=64
+channels=3
+
+[convolutional]
+batch_normalize=1
+filters=32
+size=3
+stride=1
+pad=1
+activation=leaky
+
+[maxpool]
+maxpool_depth=1
+out_channels=8
+
+[convolutional]
+filters=18
+size=1
+stride=1
+pad=1
+activation=linear
+
+[yolo]
+mask=0,1,2
+anchors=10,13, 16,30, 33,23
+classes=1
+"""
+
+
+def test_maxpool_depth_network_vs_oracle(hip):
+    """A network with a maxpool_depth layer (32 channels -> 8 groups of 4):
+    the NCHW network's yolo output against the oracle within the per-tensor
+    bound, and the depth layer's output bit for bit; the channels-last planner
+    refuses it."""
+    print("[case] maxpool_depth network 64x64 batch 2", flush=True)
+    _, layers = darknet.parse_cfg(DEPTH_CFG)
+    assert layers[1]["out"] == (8, 64, 64)
+    W = darknet.synthetic_weights(layers)
+    x = synth.uniform(8, (2, 3, 64, 64))
+    net = darknet.Network(hip, layers, 2, W, layout="nchw")
+    heads = net.forward(torch.from_numpy(x).cuda())
+    hip.finish()
+    ref = netref.forward(layers, W, x)
+    assert np.array_equal(net.output(1).cpu().numpy(), R.maxpool_depth_fwd(net.output(0).cpu().numpy(), 8)[0])
+    assert R.rel_err(heads[0].cpu().numpy(), ref[3]) <= TOL
+    with pytest.raises(NotImplementedError, match="maxpool_depth"):
+        darknet.Network(hip, layers, 2, W, layout="nhwc")

@@ -291,6 +291,53 @@ def test_maxpool_backward_scatter():
     assert np.array_equal(dIn.ravel(), ref.astype(np.float32))
 
 
+def _maxpool_depth_brute(x, outC):
+    """nMaxPoolLayer.pas:372-399 as written: loops over b, i, j, g, then
+    k = g, g + outC, ... < c with a strict '>' from -MaxSingle."""
+    B, c, h, w = x.shape
+    flat = x.ravel()
+    out = np.zeros((B, outC, h, w), np.float32)
+    idx = np.zeros((B, outC, h, w), np.int64)
+    for b in range(B):
+        for i in range(h):
+            for j in range(w):
+                for g in range(outC):
+                    m, mi, k = -np.finfo(np.float32).max, -1, g
+                    while k < c:
+                        ii = j + w * (i + h * (k + c * b))
+                        if flat[ii] > m:
+                            m, mi = flat[ii], ii
+                        k += outC
+                    out[b, g, i, j], idx[b, g, i, j] = m, mi
+    return out, idx
+
+
+@pytest.mark.parametrize("c,outC", [(8, 1), (8, 3), (6, 2), (2, 4)])
+def test_maxpool_depth_vs_loops_and_torch(c, outC):
+    """maxpool_depth: against the layer's loops run literally on a small
+    input (ties from integer values keep the first channel; outC > c leaves
+    groups with no channel at -MaxSingle / -1), and, for outC dividing c,
+    the values against torch's max over the channel groups."""
+    rng = np.random.default_rng(c * 10 + outC)
+    x = rng.integers(-3, 4, (2, c, 3, 5)).astype(np.float32)
+    x[0, 0, 0, 0] = np.nan  # never beats anything ('>' is false)
+    out, idx = R.maxpool_depth_fwd(x, outC)
+    ref, ridx = _maxpool_depth_brute(x, outC)
+    assert np.array_equal(out, ref) and np.array_equal(idx, ridx)
+    if c % outC == 0:
+        t = torch.from_numpy(np.nan_to_num(x, nan=-np.inf)).reshape(2, c // outC, outC, 3, 5).amax(1)
+        assert np.array_equal(out, t.numpy())
+    # backward through the depth indices: every input receives at most one delta
+    d = rng.integers(-5, 6, idx.shape).astype(np.float32)
+    dIn = np.zeros(x.shape, np.float32)
+    R.maxpool_bwd(idx, d, dIn)
+    ref = np.zeros(x.size, np.float32)
+    for o, k in zip(range(idx.size), idx.ravel()):
+        if k >= 0:
+            ref[k] += d.ravel()[o]
+    assert np.array_equal(dIn.ravel(), ref)
+
+
 # ---------------------------------------------------------- upsample ------
 def test_upsample_vs_torch():
     rng = np.random.default_rng(12)
