@@ -261,12 +261,15 @@ int32_t tnh_conv2d_fwd_nhwc_yolo(int64_t batch, int64_t C, int64_t H,
  * it calls no hipMalloc / hipFree / allocating library routine:
  *  - the K pieces of tail-split or split-K tiles go to a fixed device array
  *    of tnh_conv2d_noalloc_scratch_bytes() bytes (64 MiB) that each device
- *    holds from tnh_init until the process ends; a call whose tiling needs
- *    more fails with TNH_ERR_INVALID_ARG and launches nothing;
+ *    holds from tnh_init until the process ends;
  *  - it never autotunes (a timing graph allocates): it runs the tiling forced
  *    by tnh_conv2d_set_autotune, else the one tnh_conv2d_fwd_nhwc tuned for
  *    the same call, else the cost model's choice, so after one tuning call of
- *    tnh_conv2d_fwd_nhwc its output equals that entry point's bit for bit.
+ *    tnh_conv2d_fwd_nhwc its output equals that entry point's bit for bit;
+ *  - a forced tiling whose pieces need more than the array fails with
+ *    TNH_ERR_INVALID_ARG and launches nothing; a tuned one falls back to the
+ *    cost model's choice (run whole-K if its pieces do not fit either), whose
+ *    sums may differ from the tuned tiling's in the last bits.
  * Every call on a device shares that device's array and the array keeps the
  * last call's contents (nothing in it needs to start at zero): calls that
  * overlap on one device (several streams or host threads) race. */

@@ -325,6 +325,16 @@ type
       const input: TCUMem; const inOffset, inPix: SizeInt; const weights, biases: TCUMem; const activation: longint;
       const residual: TCUMem; const resOffset, resPix: SizeInt; const output: TCUMem; const outOffset, outPix: SizeInt;
       const noAlloc: boolean = false);
+    // the convolution stores the upsampled image (tnh_upsample_nhwc) instead of its own output
+    procedure conv2dForwardNHWCUpsample(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY,
+      strideX: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const weights, biases: TCUMem;
+      const activation: longint; const upStride: SizeInt; const upScale: T; const output: TCUMem;
+      const outOffset, outPix: SizeInt);
+    // the convolution also writes the yolo head (tnh_yolo_fwd_nhwc) to the NCHW tensor yoloOut
+    procedure conv2dForwardNHWCYolo(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY,
+      strideX: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const weights, biases: TCUMem;
+      const activation: longint; const output: TCUMem; const outOffset, outPix: SizeInt; const n, classes: SizeInt;
+      const yoloOut: TCUMem);
     procedure packConvWeights(const filters, c, kernelH, kernelW: SizeInt; const src, dst: TCUMem);
     procedure route(const batch: SizeInt; const srcs: array of TCUMem; const sizes: array of Int64; const dst: TCUMem);
     procedure copyChannels(const pixels, channels: SizeInt; const src: TCUMem; const srcOffset, srcPix: SizeInt;
@@ -743,6 +753,26 @@ begin
     check(tnh_conv2d_fwd_nhwc(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
       PSingle(input), inOffset, inPix, PSingle(weights), 0, PSingle(biases), 0, activation, PSingle(residual),
       resOffset, resPix, PSingle(output), outOffset, outPix));
+end;
+
+procedure TNNHip<T>.conv2dForwardNHWCUpsample(const batch, c, h, w, filters, kernelH, kernelW, padH, padW,
+  strideY, strideX: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const weights, biases: TCUMem;
+  const activation: longint; const upStride: SizeInt; const upScale: T; const output: TCUMem;
+  const outOffset, outPix: SizeInt);
+begin
+  check(tnh_conv2d_fwd_nhwc_upsample(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
+    PSingle(input), inOffset, inPix, PSingle(weights), 0, PSingle(biases), 0, activation, upStride, S(upScale),
+    PSingle(output), outOffset, outPix));
+end;
+
+procedure TNNHip<T>.conv2dForwardNHWCYolo(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY,
+  strideX: SizeInt; const input: TCUMem; const inOffset, inPix: SizeInt; const weights, biases: TCUMem;
+  const activation: longint; const output: TCUMem; const outOffset, outPix: SizeInt; const n, classes: SizeInt;
+  const yoloOut: TCUMem);
+begin
+  check(tnh_conv2d_fwd_nhwc_yolo(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
+    PSingle(input), inOffset, inPix, PSingle(weights), 0, PSingle(biases), 0, activation, PSingle(output),
+    outOffset, outPix, n, classes, PSingle(yoloOut), 0));
 end;
 
 procedure TNNHip<T>.packConvWeights(const filters, c, kernelH, kernelW: SizeInt; const src, dst: TCUMem);

@@ -169,3 +169,39 @@ def test_unit_is_complete_text():
     raw = open(UNIT).read()
     assert "…" not in raw and "..." not in raw
     assert raw.rstrip().endswith("end.")
+
+
+PLAN_UNIT = os.path.join(ROOT, "pascal", "nnhipnet.pas")
+
+
+def test_plan_unit_calls_tnnhip_methods_with_their_arity():
+    """pascal/nnhipnet.pas (the channels-last TNNet forward) calls only
+    methods TNNHip<T> declares, each with at least its parameters without a
+    default and at most all of them."""
+    mine = {}
+    for m in tnnhip_methods():
+        mine.setdefault(m["name"].lower(), []).append(m)
+    text = strip_comments_pas(open(PLAN_UNIT).read())
+    impl = text[text.index("implementation"):]
+    calls = 0
+    for m in re.finditer(r"\bhip\.(\w+)\s*\(", impl):
+        start = m.end()
+        depth, i = 1, start
+        while depth:
+            depth += {"(": 1, ")": -1}.get(impl[i], 0)
+            i += 1
+        n = len(split_args(impl[start:i - 1]))
+        decls = mine.get(m.group(1).lower())
+        assert decls, "TNNHip has no method " + m.group(1)
+        assert any(sum(1 for p in d["params"] if not p[3]) <= n <= len(d["params"]) for d in decls), \
+            (m.group(1), n)
+        calls += 1
+    assert calls >= 12
+    for name in ("createDeviceBuffer", "freeDeviceBuffer"):
+        assert re.search(r"\bhip\.%s\b" % name, impl), name
+    assert text.rstrip().endswith("end.")
+
+
+def strip_comments_pas(text):
+    text = re.sub(r"\{[^}]*\}", "", text)
+    return re.sub(r"//[^\n]*", "", text)
