@@ -37,12 +37,12 @@ def layout_for(batch):
     return "nhwc"
 PEAK_HBM = 8.0e12
 # HBM bytes per launch of the dominant kernel family at batch 16 (tap-major
-# 3x3 conv, channels-last conv_nhwc_kernel, incl. its reductions) from two
+# 3x3 conv, channels-last conv_nhwc_kernel, incl. its in-kernel tail sums) from two
 # rocprofv3 --pmc runs of `bench.py --counter-pass` (FETCH_SIZE then
 # WRITE_SIZE, KiB per dispatch, scaled by a 64 MiB copy: read = 2.0 x
 # FETCH_SIZE, write = 1.0 x WRITE_SIZE); profiles/yolov3_416_b16_conv_nhwc_kernel.md
 # holds the figures and the commands.  Other layouts / batches: null.
-TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 66843.1 + 39756.1) * 1024}
+TRAFFIC_TAP3X3_B16 = {"conv_nhwc_kernel<tap3x3>": (2.0 * 93274.8 + 53472.5) * 1024}
 
 
 def log(*a):
