@@ -674,6 +674,26 @@ int32_t tnh_sgemm_nt_batch_reduce(int64_t M, int64_t N, int64_t L,
                                   int64_t bOff, int64_t ldb, int64_t strideB,
                                   float beta, float *C, int64_t cOff,
                                   int64_t ldc, int64_t batch);
+/* No reference counterpart: the weight-gradient step of
+ * TConvolutionalLayer.backwardGPU (nConvolutionLayer.pas:1203-1232: im2col of
+ * every image of the input, then gemmStridedBatched(NoTrans, Trans, F,
+ * C*kh*kw, OH*OW, 1, delta_b, col_b, beta = 1, dW) summed over the batch)
+ * in one call whose GEMM gathers the column matrix from the input:
+ *   dW = beta*dW + alpha * sum_b delta_b * im2col(x_b)^T,
+ * x_b = x + b*xBatchStride ([C][H][W]), delta_b = delta + b*deltaBatchStride
+ * ([F][OH*OW]), dW [F][C*kh*kw] in the reference weight order.  Geometry as
+ * tnh_im2col (padding, stride, dilation).  When OH*OW % 32 == 0, OW % 4 == 0
+ * and OW divides 32 or is a multiple of it, one launch (plus the split-K sum) does
+ * it, bit for bit equal to tnh_im2col_batched followed by
+ * tnh_sgemm_nt_batch_reduce; otherwise it runs im2col and the product image
+ * by image in the stream's workspace. */
+int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t W,
+                         int64_t F, int64_t kh, int64_t kw, int64_t padH,
+                         int64_t padW, int64_t strideY, int64_t strideX,
+                         int64_t dilY, int64_t dilX, const float *x,
+                         int64_t xBatchStride, const float *delta,
+                         int64_t deltaBatchStride, float alpha, float beta,
+                         float *dW);
 
 #ifdef __cplusplus
 }

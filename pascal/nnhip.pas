@@ -206,6 +206,9 @@ function tnh_param_update(N: Int64; learningRate: Single; batch: Int64; momentum
 function tnh_sgemm_nt_batch_reduce(M, N, L: Int64; alpha: Single; A: PSingle; aOff, lda, strideA: Int64;
   B: PSingle; bOff, ldb, strideB: Int64; beta: Single; C: PSingle; cOff, ldc, batch: Int64): LongInt; cdecl;
   external libtnh;
+function tnh_conv2d_wgrad(batch, C, H, W, F, kh, kw, padH, padW, strideY, strideX, dilY, dilX: Int64; x: PSingle;
+  xBatchStride: Int64; delta: PSingle; deltaBatchStride: Int64; alpha, beta: Single; dW: PSingle): LongInt; cdecl;
+  external libtnh;
 
 // --- the backend object -------------------------------------------------------
 type
@@ -371,6 +374,10 @@ type
     procedure gemmNTBatchReduce(const M, N, L: SizeInt; const ALPHA: T; const A: TCUMem;
       const aOffset, lda, strideA: SizeInt; const B: TCUMem; const bOffset, ldb, strideB: SizeInt; const BETA: T;
       const C: TCUMem; const cOffset, ldc, batch: SizeInt);
+    // backwardGPU's im2col + gemmStridedBatched weight gradient in one call (the im2col in the GEMM's loader)
+    procedure convWeightGradient(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
+      dilY, dilX: SizeInt; const input: TCUMem; const inBatchStride: SizeInt; const delta: TCUMem;
+      const deltaBatchStride: SizeInt; const ALPHA, BETA: T; const dW: TCUMem);
     procedure setDeterministic(const enable: boolean);
     procedure setConvAutotune(const enable: boolean; const forcedConfig: longint = -1);
     procedure setSgemmAutotune(const enable: boolean; const forcedConfig: longint = -1);
@@ -894,6 +901,14 @@ procedure TNNHip<T>.gemmNTBatchReduce(const M, N, L: SizeInt; const ALPHA: T; co
 begin
   check(tnh_sgemm_nt_batch_reduce(M, N, L, S(ALPHA), PSingle(A), aOffset, lda, strideA, PSingle(B), bOffset, ldb,
     strideB, S(BETA), PSingle(C), cOffset, ldc, batch));
+end;
+
+procedure TNNHip<T>.convWeightGradient(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY,
+  strideX, dilY, dilX: SizeInt; const input: TCUMem; const inBatchStride: SizeInt; const delta: TCUMem;
+  const deltaBatchStride: SizeInt; const ALPHA, BETA: T; const dW: TCUMem);
+begin
+  check(tnh_conv2d_wgrad(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY, dilX,
+    PSingle(input), inBatchStride, PSingle(delta), deltaBatchStride, S(ALPHA), S(BETA), PSingle(dW)));
 end;
 
 procedure TNNHip<T>.setDeterministic(const enable: boolean);

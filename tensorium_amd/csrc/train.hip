@@ -610,6 +610,116 @@ __global__ __launch_bounds__(Cfg::NT) void wgrad_kernel(WgradArgs a) {
   });
 }
 
+// The convolution weight gradient with the im2col in the B loader:
+// dW[f][n] = sum over (b, oy, ox) of delta_b[f][oy*OW + ox] * x_b[c][iy][ix],
+// n = (c*kh + ky)*kw + kx (the reference weight order), iy = oy*sY - pH +
+// ky*dY, ix = ox*sX - pW + kx*dX, 0 outside the image: the values im2col
+// writes (sim2Col, ntensors.pas:11415), read straight from the input.  The
+// reduction axis is wgrad_kernel's (image by image, L = OH*OW pixels each,
+// panels of BK pixels inside one image), so the sums equal im2col followed by
+// tnh_sgemm_nt_batch_reduce bit for bit.  A panel starts at a multiple of BK
+// pixels; with OW | BK or BK | OW the output row and column of a thread's
+// pixels are the panel's (uniform) plus a per-thread constant.
+struct ColGeom {
+  int64_t xBatchStride, xBytes;
+  int C, H, W, OW, L, kh, kw, sY, sX, pH, pW, dY, dX;
+};
+
+template <int ROWS, int BK, int NT>
+struct ColGatherLoader : DenseLoader<true, true, ROWS, BK, NT> {
+  // a thread's unit is 4 consecutive pixels of one row n: with OW % 4 == 0
+  // they lie in one output row, so one row test and one address serve all
+  // four (the input columns are sX apart); the four values go to LDS as one
+  // 16-byte store, like a dense 16-byte load's
+  using Base = DenseLoader<true, true, ROWS, BK, NT>;
+  static constexpr int PER = Base::PER;
+  ColGeom g;
+  int ky[PER], kx[PER], dy[PER], dx[PER];
+  int64_t cOff[PER];  // c*H*W of the unit's row
+  __device__ inline void init_col(const float* x, const ColGeom& geom, int64_t rows, int64_t Ktot, int64_t row0,
+                                  int tid) {
+    g = geom;
+    Base::rsrc = make_rsrc(x, geom.xBytes);
+    Base::K = static_cast<int>(Ktot);
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int idx = tid + v * NT;
+      int row, k;
+      Base::coords(idx, row, k);
+      const int64_t n = row0 + row;
+      Base::rowOk[v] = n < rows && (!Base::kPartial || idx < Base::UNITS);
+      Base::kIdx[v] = k;
+      const int64_t nn = Base::rowOk[v] ? n : 0;
+      const int64_t taps = static_cast<int64_t>(g.kh) * g.kw;
+      const int64_t c = nn / taps, t = nn - c * taps;
+      ky[v] = static_cast<int>(t / g.kw);
+      kx[v] = static_cast<int>(t - (t / g.kw) * g.kw);
+      cOff[v] = c * g.H * g.W;
+      dy[v] = g.OW >= BK ? 0 : k / g.OW;
+      dx[v] = g.OW >= BK ? k : k % g.OW;
+    }
+  }
+  __device__ inline void load(int64_t k0) {
+    const int64_t b = k0 / g.L;  // uniform: a panel lies inside one image
+    const int64_t l0 = k0 - b * g.L;
+    const int oy0 = static_cast<int>(l0 / g.OW);
+    const int ox0 = static_cast<int>(l0 - static_cast<int64_t>(oy0) * g.OW);
+    const int64_t base = b * g.xBatchStride;
+#pragma unroll
+    for (int v = 0; v < PER; ++v) {
+      const int iy = (oy0 + dy[v]) * g.sY - g.pH + ky[v] * g.dY;
+      const int ix = (ox0 + dx[v]) * g.sX - g.pW + kx[v] * g.dX;
+      const bool rowIn = Base::rowOk[v] && static_cast<unsigned>(iy) < static_cast<unsigned>(g.H);
+      const int64_t e = base + cOff[v] + static_cast<int64_t>(iy) * g.W + ix;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = rowIn && static_cast<unsigned>(ix + j * g.sX) < static_cast<unsigned>(g.W);
+        Base::reg[v][j] = buf_ld1(Base::rsrc, sel_off(ok, static_cast<uint32_t>((e + j * g.sX) * 4)));
+      }
+    }
+  }
+};
+
+template <class Cfg, bool VA>
+__global__ __launch_bounds__(Cfg::NT) void wgrad_col_kernel(WgradArgs a, ColGeom geom) {
+  using AL = SegLoader<VA, Cfg::BM, Cfg::BK, Cfg::NT>;
+  using BL = ColGatherLoader<Cfg::BN, Cfg::BK, Cfg::NT>;
+  using Main = GemmMainloop<Cfg, AL, BL>;
+  __shared__ __attribute__((aligned(16))) float smem[Main::LDS_FLOATS];
+  lds_t* lds = (lds_t*)smem;
+  int tm, tn;
+  tile_coords(blockIdx.x, a.tilesM, a.tilesN, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * Cfg::BM, n0 = static_cast<int64_t>(tn) * Cfg::BN;
+  const int64_t Ktot = a.batch * a.L;
+  AL al;
+  al.init(a.A, a.aBytes, a.lda, a.M, Ktot, m0, threadIdx.x);
+  al.segL = a.L;
+  al.segStride = a.strideA;
+  BL bl;
+  bl.init_col(a.B, geom, a.N, Ktot, n0, threadIdx.x);
+  f32x16 acc[Cfg::FM][Cfg::FN];
+  const int64_t kBegin = blockIdx.y * a.kChunk;
+  const int64_t kEnd = min(Ktot, kBegin + a.kChunk);
+  Main::exec(al, bl, kBegin, kEnd, lds, acc);
+  if (a.splits > 1) {
+    float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.M * a.N;
+    Main::for_each(acc, [&](int row, int col, float v) {
+      const int64_t gr = m0 + row, gc = n0 + col;
+      if (gr < a.M && gc < a.N) part[gr * a.N + gc] = v;
+    });
+    return;
+  }
+  Main::for_each(acc, [&](int row, int col, float v) {
+    const int64_t gr = m0 + row, gc = n0 + col;
+    if (gr < a.M && gc < a.N) {
+      float* p = a.C + gr * a.ldc + gc;
+      float out = a.alpha * v;
+      if (a.beta != 0.f) out = out + a.beta * *p;
+      *p = out;
+    }
+  });
+}
+
 // Sums the split partials of each output element: one wave per element, lane
 // l adds splits l, l + 64, ... in turn (their loads issued together), then a
 // fixed tree over the lanes; then alpha and beta.  Fixed order: the result
@@ -665,11 +775,25 @@ using WCfg = TileCfg<64, 64, 32, 2, 2, 2>;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+int launch_wgrad_reduce(const WgradArgs& a, hipStream_t s);
+
 template <bool VA, bool VB>
 int launch_wgrad(WgradArgs a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(a.tilesM * a.tilesN), static_cast<unsigned>(a.splits));
   hipLaunchKernelGGL((wgrad_kernel<WCfg, VA, VB>), grid, dim3(WCfg::NT), 0, s, a);
   if (int st = launch_status("wgrad_kernel")) return st;
+  return launch_wgrad_reduce(a, s);
+}
+
+template <bool VA>
+int launch_wgrad_col(WgradArgs a, const ColGeom& g, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(a.tilesM * a.tilesN), static_cast<unsigned>(a.splits));
+  hipLaunchKernelGGL((wgrad_col_kernel<WCfg, VA>), grid, dim3(WCfg::NT), 0, s, a, g);
+  if (int st = launch_status("wgrad_col_kernel")) return st;
+  return launch_wgrad_reduce(a, s);
+}
+
+int launch_wgrad_reduce(const WgradArgs& a, hipStream_t s) {
   if (a.splits > 1) {
     // few outputs: a wave per output element spreads the splits over its
     // lanes; many: a thread per element keeps the loads coalesced
@@ -902,6 +1026,39 @@ extern "C" int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch
   return launch_status("param_update_kernel");
 }
 
+namespace tnh {
+namespace {
+// Tiles and the split of the batch-folded K axis: about two workgroups per
+// CU over the weight tiles, at least four panels per split, the partials in
+// the stream's workspace (whole K when there is none, e.g. under capture
+// before any eager call).
+// measured on the config-3 step: 1 or 4 workgroups per CU, or at least 16
+// panels per split, were 1.5-3.5% slower per step
+constexpr int64_t kWgradWgPerCu = 2, kWgradMinPanels = 4;
+
+int wgrad_split(Context* cx, WgradArgs& a, const char* who) {
+  a.tilesM = static_cast<int>((a.M + WCfg::BM - 1) / WCfg::BM);
+  a.tilesN = static_cast<int>((a.N + WCfg::BN - 1) / WCfg::BN);
+  const int64_t tiles = static_cast<int64_t>(a.tilesM) * a.tilesN;
+  TNH_ARG(tiles < (int64_t(1) << 31), "%s: grid too large", who);
+  const int64_t Ktot = a.batch * a.L;
+  const int64_t panels = Ktot / WCfg::BK;
+  int64_t splits = (kWgradWgPerCu * cx->cu_count + tiles - 1) / tiles;
+  splits = std::max<int64_t>(1, std::min<int64_t>({splits, panels / kWgradMinPanels, 1024}));
+  a.kChunk = (panels + splits - 1) / splits * WCfg::BK;
+  a.splits = static_cast<int>((Ktot + a.kChunk - 1) / a.kChunk);
+  if (a.splits > 1) {
+    a.part = static_cast<float*>(workspace(cx, static_cast<size_t>(a.splits) * a.M * a.N * 4));
+    if (!a.part) {
+      a.splits = 1;
+      a.kChunk = Ktot;
+    }
+  }
+  return TNH_OK;
+}
+}  // namespace
+}  // namespace tnh
+
 extern "C" int32_t tnh_sgemm_nt_batch_reduce(int64_t M, int64_t N, int64_t L, float alpha, const float* A,
                                              int64_t aOff, int64_t lda, int64_t strideA, const float* B,
                                              int64_t bOff, int64_t ldb, int64_t strideB, float beta, float* C,
@@ -938,26 +1095,74 @@ extern "C" int32_t tnh_sgemm_nt_batch_reduce(int64_t M, int64_t N, int64_t L, fl
   a.bBytes = bElems * 4;
   a.alpha = alpha;
   a.beta = beta;
-  a.tilesM = static_cast<int>((M + WCfg::BM - 1) / WCfg::BM);
-  a.tilesN = static_cast<int>((N + WCfg::BN - 1) / WCfg::BN);
-  const int64_t tiles = static_cast<int64_t>(a.tilesM) * a.tilesN;
-  TNH_ARG(tiles < (int64_t(1) << 31), "sgemm_nt_batch_reduce: grid too large");
-  const int64_t panels = batch * L / WCfg::BK;
-  int64_t splits = (2 * cx->cu_count + tiles - 1) / tiles;
-  splits = std::max<int64_t>(1, std::min<int64_t>({splits, panels / 4, 1024}));
-  a.kChunk = (panels + splits - 1) / splits * WCfg::BK;
-  a.splits = static_cast<int>((batch * L + a.kChunk - 1) / a.kChunk);
-  if (a.splits > 1) {
-    a.part = static_cast<float*>(workspace(cx, static_cast<size_t>(a.splits) * M * N * 4));
-    if (!a.part) {  // no scratch (e.g. under graph capture without a prior eager call)
-      a.splits = 1;
-      a.kChunk = batch * L;
-    }
-  }
+  if (int st = wgrad_split(cx, a, "sgemm_nt_batch_reduce")) return st;
   const bool va = aligned16(a.A) && lda % 4 == 0 && strideA % 4 == 0 && L % 4 == 0;
   const bool vb = aligned16(a.B) && ldb % 4 == 0 && strideB % 4 == 0 && L % 4 == 0;
   if (va && vb) return launch_wgrad<true, true>(a, cx->stream);
   if (va) return launch_wgrad<true, false>(a, cx->stream);
   if (vb) return launch_wgrad<false, true>(a, cx->stream);
   return launch_wgrad<false, false>(a, cx->stream);
+}
+
+extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                    int64_t kw, int64_t padH, int64_t padW, int64_t strideY, int64_t strideX,
+                                    int64_t dilY, int64_t dilX, const float* x, int64_t xBatchStride,
+                                    const float* delta, int64_t deltaBatchStride, float alpha, float beta,
+                                    float* dW) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0 && kh > 0 && kw > 0 && padH >= 0 && padW >= 0 &&
+              strideY > 0 && strideX > 0 && dilY > 0 && dilX > 0,
+          "conv2d_wgrad: bad geometry");
+  TNH_ARG(x && delta && dW, "conv2d_wgrad: NULL buffer");
+  const int64_t OH = (H + 2 * padH - dilY * (kh - 1) - 1) / strideY + 1;
+  const int64_t OW = (W + 2 * padW - dilX * (kw - 1) - 1) / strideX + 1;
+  TNH_ARG(OH > 0 && OW > 0, "conv2d_wgrad: empty output");
+  const int64_t L = OH * OW, K = C * kh * kw;
+  TNH_ARG(xBatchStride >= C * H * W && deltaBatchStride >= F * L, "conv2d_wgrad: batch strides too small");
+  if (batch == 0) return tnh_sgemm(0, 1, F, K, 0, alpha, x, 0, 1, x, 0, 1, beta, dW, 0, K);
+  const int64_t xElems = (batch - 1) * xBatchStride + C * H * W;
+  const int64_t dElems = (batch - 1) * deltaBatchStride + F * L;
+  TNH_ARG(xElems * 4 <= kMaxBufBytes && dElems * 4 <= kMaxBufBytes && batch * L < (int64_t(1) << 31) &&
+              K * F < (int64_t(1) << 31),
+          "conv2d_wgrad: operands span more than 2 GiB (split the batch)");
+  constexpr int BK = WCfg::BK;
+  const bool fused = L % BK == 0 && OW % 4 == 0 && (OW % BK == 0 || BK % OW == 0);
+  if (!fused) {
+    // the gather's panel geometry does not hold: im2col image by image into
+    // the stream's workspace, then the NT product accumulated over images
+    float* col = static_cast<float*>(workspace(cx, static_cast<size_t>(K * L) * 4));
+    if (!col) return fail(TNH_ERR_OUT_OF_MEMORY, "conv2d_wgrad: no workspace for the column matrix");
+    for (int64_t b = 0; b < batch; ++b) {
+      if (int st = tnh_im2col(C, H, W, kh, kw, padH, padW, strideY, strideX, dilY, dilX, x, b * xBatchStride, col,
+                              0))
+        return st;
+      if (int st = tnh_sgemm(0, 1, F, K, L, alpha, delta, b * deltaBatchStride, L, col, 0, L, b == 0 ? beta : 1.0f,
+                             dW, 0, K))
+        return st;
+    }
+    return TNH_OK;
+  }
+  WgradArgs a{};
+  a.A = delta;
+  a.B = x;
+  a.C = dW;
+  a.M = F; a.N = K; a.L = L; a.lda = L; a.ldb = 0; a.ldc = K;
+  a.strideA = deltaBatchStride; a.strideB = xBatchStride; a.batch = batch;
+  a.aBytes = dElems * 4;
+  a.bBytes = xElems * 4;
+  a.alpha = alpha;
+  a.beta = beta;
+  if (int st = wgrad_split(cx, a, "conv2d_wgrad")) return st;
+  ColGeom g{};
+  g.xBatchStride = xBatchStride;
+  g.xBytes = xElems * 4;
+  g.C = static_cast<int>(C); g.H = static_cast<int>(H); g.W = static_cast<int>(W);
+  g.OW = static_cast<int>(OW); g.L = static_cast<int>(L);
+  g.kh = static_cast<int>(kh); g.kw = static_cast<int>(kw);
+  g.sY = static_cast<int>(strideY); g.sX = static_cast<int>(strideX);
+  g.pH = static_cast<int>(padH); g.pW = static_cast<int>(padW);
+  g.dY = static_cast<int>(dilY); g.dX = static_cast<int>(dilX);
+  const bool va = aligned16(delta) && L % 4 == 0 && deltaBatchStride % 4 == 0;
+  if (va) return launch_wgrad_col<true>(a, g, cx->stream);
+  return launch_wgrad_col<false>(a, g, cx->stream);
 }

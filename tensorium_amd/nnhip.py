@@ -152,6 +152,7 @@ _PROTOS = {
     "tnh_avgpool_bwd": [i64, i64, i64, i64, vp, vp],
     "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
     "tnh_param_update": [i64, f32, i64, f32, vp, vp],
+    "tnh_conv2d_wgrad": [i64] * 13 + [vp, i64, vp, i64, f32, f32, vp],
     "tnh_sgemm_nt_batch_reduce": [i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64, f32, vp, i64, i64,
                                   i64],
 }
@@ -658,6 +659,12 @@ class TNNHip:
 
     def paramUpdate(self, N, learningRate, batch, momentum, params, paramUpdates):
         call("tnh_param_update", N, learningRate, batch, momentum, addr(params), addr(paramUpdates))
+
+    def convWeightGradient(self, batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY, dilX,
+                           input, inBatchStride, delta, deltaBatchStride, alpha, beta, dW):
+        """dW = beta*dW + alpha * sum_b delta_b * im2col(input_b)^T (the im2col inside the GEMM)."""
+        call("tnh_conv2d_wgrad", batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY, dilX,
+             addr(input), inBatchStride, addr(delta), deltaBatchStride, alpha, beta, addr(dW))
 
     def gemmNTBatchReduce(self, M, N, L, ALPHA, A, aOffset, lda, strideA, B, bOffset, ldb, strideB, BETA, C_,
                           cOffset, ldc, batch):

@@ -66,10 +66,15 @@ class CifarTrainer:
     """One trainer per (batch, image size); `step(x, truth)` runs forward,
     backward and update on the device; `cost()` reads the loss back."""
 
-    def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1):
+    def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
+                 fused_wgrad=True):
+        """fused_wgrad: the conv weight gradients gather their column matrix
+        inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
+        im2col + NT product (the same bits)."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
+        self.fused_wgrad = fused_wgrad
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -205,11 +210,15 @@ class CifarTrainer:
             hip.bnBackwardScale(n, f, B, t[f"out{i}"], acLEAKY, t[f"xn{i}"], p[f"s{i}"], d, p[f"u_s{i}"])
             hip.meansAndVarsDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
             hip.normalizeDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
-            # conv weight gradient: im2col of the layer input, then sum_b delta_b * col_b^T
+            # conv weight gradient: sum_b delta_b * im2col(input_b)^T
             src = self.input if i == 0 else t[f"pool{i - 1}"]
             K, L = c * 9, hh * hh
-            hip.im2colStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, 0, col, K * L, 0, B)
-            hip.gemmNTBatchReduce(f, K, L, 1.0, d, 0, L, f * L, col, 0, L, K * L, 1.0, p[f"u_w{i}"], 0, K, B)
+            if self.fused_wgrad:
+                hip.convWeightGradient(B, c, hh, hh, f, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, d, f * L, 1.0, 1.0,
+                                       p[f"u_w{i}"])
+            else:
+                hip.im2colStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, 0, col, K * L, 0, B)
+                hip.gemmNTBatchReduce(f, K, L, 1.0, d, 0, L, f * L, col, 0, L, K * L, 1.0, p[f"u_w{i}"], 0, K, B)
             if i == 0:
                 break  # state.delta is nil for the first layer
             # input delta: col_b = W^T * delta_b, then col2im into a zeroed delta

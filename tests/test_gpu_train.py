@@ -415,3 +415,82 @@ def test_bn_backward_scale_equals_three_calls(hip, shape, off, act):
     hip.forwardScale(n, bv, 0, Cc, dg, 1, B)
     assert np.array_equal(H(da, hip), H(db, hip))
     assert np.array_equal(H(ua, hip), H(ub, hip))
+
+
+def _im2col_np(x, k, pad, stride, dil):
+    """im2col of a batch [B][C][H][W] -> [B][C*k*k][OH*OW] (sim2Col's order)."""
+    B, C, Hh, W = x.shape
+    OH = (Hh + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    OW = (W + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    xp = np.zeros((B, C, Hh + 2 * pad, W + 2 * pad), np.float32)
+    xp[:, :, pad:pad + Hh, pad:pad + W] = x
+    col = np.empty((B, C, k, k, OH, OW), np.float32)
+    for ky in range(k):
+        for kx in range(k):
+            col[:, :, ky, kx] = xp[:, :, ky * dil:ky * dil + stride * (OH - 1) + 1:stride,
+                                   kx * dil:kx * dil + stride * (OW - 1) + 1:stride]
+    return col.reshape(B, C * k * k, OH * OW), OH, OW
+
+
+@pytest.mark.parametrize("B,C,Hh,F,k,pad,stride,dil", [
+    (8, 3, 32, 32, 3, 1, 1, 1),     # config-3 conv1: OW 32, one output row per panel
+    (8, 32, 16, 64, 3, 1, 1, 1),    # conv2: two rows per panel
+    (8, 64, 8, 128, 3, 1, 1, 1),    # conv3: four rows per panel
+    (2, 16, 64, 24, 3, 1, 2, 1),    # stride 2 (OW 32)
+    (1, 8, 64, 16, 3, 1, 1, 1),     # OW 64: two panels per row
+    (4, 64, 16, 32, 1, 0, 1, 1),    # 1x1
+    (3, 8, 20, 16, 3, 2, 1, 2),     # dilation 2, OH*OW = 400: the image-by-image path
+    (2, 4, 12, 8, 5, 2, 1, 1),      # 5x5, OW 12: the image-by-image path
+])
+def test_conv_wgrad(hip, B, C, Hh, F, k, pad, stride, dil):
+    """tnh_conv2d_wgrad (the im2col inside the GEMM's loader): within 1e-5 of
+    float64 sum_b delta_b * im2col(x_b)^T with alpha 0.5 / beta 1; where it
+    runs fused, bit for bit equal to tnh_im2col_batched followed by
+    tnh_sgemm_nt_batch_reduce; on integer data exact."""
+    case(f"conv wgrad B{B} C{C} H{Hh} F{F} k{k} pad{pad} s{stride} d{dil}")
+    x = synth.normal(330, (B, C, Hh, Hh))
+    col, OH, OW = _im2col_np(x, k, pad, stride, dil)
+    L, K = OH * OW, C * k * k
+    delta = synth.normal(331, (B, F, L))
+    dW0 = synth.normal(332, (F, K))
+    ref = dW0.astype(np.float64) + 0.5 * np.einsum("bfl,bkl->fk", delta.astype(np.float64), col.astype(np.float64))
+    dW = D(dW0)
+    hip.convWeightGradient(B, C, Hh, Hh, F, k, k, pad, pad, stride, stride, dil, dil, D(x), C * Hh * Hh, D(delta),
+                           F * L, 0.5, 1.0, dW)
+    got = H(dW, hip)
+    assert R.rel_err(got, ref) <= TOL
+    fused = L % 32 == 0 and OW % 4 == 0 and (OW % 32 == 0 or 32 % OW == 0)
+    if fused:
+        dcol = torch.empty((B, K, L), dtype=torch.float32, device="cuda")
+        hip.im2colStridedBatched(C, Hh, Hh, k, k, pad, pad, stride, stride, dil, dil, D(x), C * Hh * Hh, 0, dcol, K * L,
+                                 0, B)
+        assert np.array_equal(H(dcol, hip), col)
+        dW2 = D(dW0)
+        hip.gemmNTBatchReduce(F, K, L, 0.5, D(delta), 0, L, F * L, dcol, 0, L, K * L, 1.0, dW2, 0, K, B)
+        assert np.array_equal(H(dW2, hip), got)
+    xi = np.floor(synth.uniform(333, x.shape, -4, 4)).astype(np.float32)
+    di = np.floor(synth.uniform(334, delta.shape, -4, 4)).astype(np.float32)
+    coli, _, _ = _im2col_np(xi, k, pad, stride, dil)
+    refi = np.einsum("bfl,bkl->fk", di.astype(np.float64), coli.astype(np.float64)).astype(np.float32)
+    dW = torch.zeros((F, K), dtype=torch.float32, device="cuda")
+    hip.convWeightGradient(B, C, Hh, Hh, F, k, k, pad, pad, stride, stride, dil, dil, D(xi), C * Hh * Hh, D(di), F * L,
+                           1.0, 0.0, dW)
+    assert np.array_equal(H(dW, hip), refi)
+
+
+def test_cifar_step_fused_wgrad_equals_im2col_path(hip):
+    """The training step with the fused weight gradients gives the same bits
+    as with the reference's im2col + NT product (every gradient and the
+    updated parameters)."""
+    case("cifar step fused wgrad vs im2col")
+    params = trainnet.init_params()
+    x, truth = _batch(321, 16)
+    out = []
+    for fused in (True, False):
+        gpu = trainnet.CifarTrainer(hip, params, 16, fused_wgrad=fused)
+        gpu.forward(D(x), D(truth))
+        gpu.backward()
+        gpu.update()
+        out.append({k: gpu.host(k).copy() for k in ("u_w0", "u_w1", "u_w2", "w0", "w1", "w2", "s0", "u_fw")})
+    for k in out[0]:
+        assert np.array_equal(out[0][k], out[1][k]), k
