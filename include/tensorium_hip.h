@@ -289,6 +289,16 @@ int32_t tnh_conv2d_noalloc_scratch_bytes(int64_t *bytes);
  * src[f][c][ky][kx] on the device; src and dst must not overlap. */
 int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int64_t kw,
                                 const float *src, float *dst);
+/* No reference counterpart (layout helper for the training step): from
+ * src [F][C][kh][kw], tapMajor[f][ky][kx][c] = src[f][c][ky][kx] (as
+ * tnh_conv2d_pack_weights; NULL to skip) and flipped[c][ky][kx][f] =
+ * src[f][c][kh-1-ky][kw-1-kx], in one pass.  With the flipped copy the input
+ * delta of a stride-1 convolution (backwardGPU's TN gemm + col2im,
+ * nConvolutionLayer.pas:1240-1290) is tnh_conv2d_fwd of the output delta: F
+ * input channels, C filters, padding kh-1-pad, tap-major weights. */
+int32_t tnh_conv2d_pack_weights_dgrad(int64_t F, int64_t C, int64_t kh,
+                                      int64_t kw, const float *src,
+                                      float *tapMajor, float *flipped);
 /* No reference counterpart: enable (1, default) or disable per-shape
  * autotuning of the conv tile shape; forcedConfig >= 0 pins one shape:
  * forcedConfig % 64 is the tile shape (0..5 LDS-staged, 11..19 lean

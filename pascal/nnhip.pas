@@ -105,6 +105,8 @@ function tnh_conv2d_fwd_nhwc_yolo(batch, C, H, W, F, kh, kw, pH, pW, sY, sX: Int
   external libtnh;
 function tnh_conv2d_noalloc_scratch_bytes(bytes: PInt64): LongInt; cdecl; external libtnh;
 function tnh_conv2d_pack_weights(F, C, kh, kw: Int64; src, dst: PSingle): LongInt; cdecl; external libtnh;
+function tnh_conv2d_pack_weights_dgrad(F, C, kh, kw: Int64; src, tapMajor, flipped: PSingle): LongInt; cdecl;
+  external libtnh;
 function tnh_conv2d_set_autotune(enable, forcedConfig: LongInt): LongInt; cdecl; external libtnh;
 function tnh_forward_bias(dstSize: Int64; dst: PSingle; offset, srcSize: Int64; src: PSingle;
   incb, batch: Int64): LongInt; cdecl; external libtnh;
@@ -339,6 +341,8 @@ type
       const activation: longint; const output: TCUMem; const outOffset, outPix: SizeInt; const n, classes: SizeInt;
       const yoloOut: TCUMem);
     procedure packConvWeights(const filters, c, kernelH, kernelW: SizeInt; const src, dst: TCUMem);
+    // the forward's tap-major copy (nil: skipped) and the data gradient's flipped [C][kh][kw][F] copy
+    procedure packConvWeightsDgrad(const filters, c, kernelH, kernelW: SizeInt; const src, tapMajor, flipped: TCUMem);
     procedure route(const batch: SizeInt; const srcs: array of TCUMem; const sizes: array of Int64; const dst: TCUMem);
     procedure copyChannels(const pixels, channels: SizeInt; const src: TCUMem; const srcOffset, srcPix: SizeInt;
       const dst: TCUMem; const dstOffset, dstPix: SizeInt);
@@ -785,6 +789,13 @@ end;
 procedure TNNHip<T>.packConvWeights(const filters, c, kernelH, kernelW: SizeInt; const src, dst: TCUMem);
 begin
   check(tnh_conv2d_pack_weights(filters, c, kernelH, kernelW, PSingle(src), PSingle(dst)));
+end;
+
+procedure TNNHip<T>.packConvWeightsDgrad(const filters, c, kernelH, kernelW: SizeInt;
+  const src, tapMajor, flipped: TCUMem);
+begin
+  check(tnh_conv2d_pack_weights_dgrad(filters, c, kernelH, kernelW, PSingle(src), PSingle(tapMajor),
+    PSingle(flipped)));
 end;
 
 procedure TNNHip<T>.route(const batch: SizeInt; const srcs: array of TCUMem; const sizes: array of Int64;

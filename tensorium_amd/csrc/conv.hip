@@ -752,6 +752,27 @@ __global__ void pack_weights_kernel(int64_t fc, int64_t C, int64_t taps, const f
   }
 }
 
+// Both weight copies a training step's convolution needs, from the
+// reference weights [F][C][kh][kw] in one pass (thread per (f, c), its taps
+// t = ky*kw + kx contiguous): the forward's tap-major [F][kh][kw][C] (when
+// tap is not null) and the data gradient's [C][kh][kw][F] with both kernel
+// axes flipped: flip[c][taps-1-t][f] = w[f][c][t].  With the flipped copy the
+// input delta of a stride-1 convolution is a convolution of the output delta
+// (F channels, C filters, padding kh-1-pad).
+__global__ void pack_weights_dgrad_kernel(int64_t F, int64_t C, int64_t taps, const float* __restrict__ src,
+                                          float* __restrict__ tap, float* __restrict__ flip) {
+  const int64_t fc = F * C;
+  for (int64_t q = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; q < fc; q += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t f = q / C, c = q - f * C;
+    const float* s = src + q * taps;
+    for (int64_t t = 0; t < taps; ++t) {
+      const float v = s[t];
+      if (tap) tap[(f * taps + t) * C + c] = v;
+      flip[(c * taps + (taps - 1 - t)) * F + f] = v;
+    }
+  }
+}
+
 struct Cand {
   int cfg, splits;
   int tail;   // tail-split pieces per remainder tile (lean configurations), 0: none
@@ -1214,6 +1235,18 @@ extern "C" int32_t tnh_conv2d_pack_weights(int64_t F, int64_t C, int64_t kh, int
   hipLaunchKernelGGL(pack_weights_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)), dim3(256), 0,
                      cx->stream, F * C, C, kh * kw, src, dst);
   return launch_status("pack_weights_kernel");
+}
+
+extern "C" int32_t tnh_conv2d_pack_weights_dgrad(int64_t F, int64_t C, int64_t kh, int64_t kw, const float* src,
+                                                 float* tapMajor, float* flipped) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(F > 0 && C > 0 && kh > 0 && kw > 0 && src && flipped && src != flipped && src != tapMajor &&
+              tapMajor != flipped,
+          "conv2d_pack_weights_dgrad: bad arguments");
+  const int64_t blocks = (F * C + 255) / 256;
+  hipLaunchKernelGGL(pack_weights_dgrad_kernel, dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
+                     dim3(256), 0, cx->stream, F, C, kh * kw, src, tapMajor, flipped);
+  return launch_status("pack_weights_dgrad_kernel");
 }
 
 extern "C" int32_t tnh_conv2d_fwd(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,

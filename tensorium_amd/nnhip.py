@@ -152,6 +152,7 @@ _PROTOS = {
     "tnh_avgpool_bwd": [i64, i64, i64, i64, vp, vp],
     "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
     "tnh_param_update": [i64, f32, i64, f32, vp, vp],
+    "tnh_conv2d_pack_weights_dgrad": [i64, i64, i64, i64, vp, vp, vp],
     "tnh_conv2d_wgrad": [i64] * 13 + [vp, i64, vp, i64, f32, f32, vp],
     "tnh_sgemm_nt_batch_reduce": [i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64, f32, vp, i64, i64,
                                   i64],
@@ -439,6 +440,12 @@ class TNNHip:
         """[F][C][kh][kw] -> tap-major [F][kh][kw][C] (device to device)."""
         call("tnh_conv2d_pack_weights", filters, c, kernelSize, kernelSize if kernelWidth is None else kernelWidth,
              addr(src), addr(dst))
+
+    def packConvWeightsDgrad(self, filters, c, kernelSize, src, tapMajor, flipped, kernelWidth=None):
+        """[F][C][kh][kw] -> tap-major [F][kh][kw][C] (tapMajor, may be None)
+        and the data gradient's flipped [C][kh][kw][F], one launch."""
+        call("tnh_conv2d_pack_weights_dgrad", filters, c, kernelSize, kernelSize if kernelWidth is None else kernelWidth,
+             addr(src), addr(tapMajor), addr(flipped))
 
     @staticmethod
     def setDeterministic(enable=True):

@@ -67,14 +67,17 @@ class CifarTrainer:
     backward and update on the device; `cost()` reads the loss back."""
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
-                 fused_wgrad=True):
+                 fused_wgrad=True, conv_dgrad=True):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
-        im2col + NT product (the same bits)."""
+        im2col + NT product (the same bits).  conv_dgrad: the conv input
+        deltas are one convolution of the output delta with the flipped
+        weights; False runs the reference's TN product + col2im (the same
+        sums in another order)."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
-        self.fused_wgrad = fused_wgrad
+        self.fused_wgrad, self.conv_dgrad = fused_wgrad, conv_dgrad
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -102,6 +105,7 @@ class CifarTrainer:
             if k not in self.p:  # rolling statistics
                 self.p[k] = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
         self.packed = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
+        self.flipped = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
         B = batch
         t = {}
         h = size
@@ -150,7 +154,10 @@ class CifarTrainer:
 
     def _pack(self):
         for i, (c, _, f) in enumerate(self.dims):
-            self.hip.packConvWeights(f, c, 3, self.p[f"w{i}"], self.packed[i])
+            if self.conv_dgrad and i > 0:  # the first layer computes no input delta
+                self.hip.packConvWeightsDgrad(f, c, 3, self.p[f"w{i}"], self.packed[i], self.flipped[i])
+            else:
+                self.hip.packConvWeights(f, c, 3, self.p[f"w{i}"], self.packed[i])
 
     # ------------------------------------------------------------- forward
     def forward(self, x, truth):
@@ -221,11 +228,17 @@ class CifarTrainer:
                 hip.gemmNTBatchReduce(f, K, L, 1.0, d, 0, L, f * L, col, 0, L, K * L, 1.0, p[f"u_w{i}"], 0, K, B)
             if i == 0:
                 break  # state.delta is nil for the first layer
-            # input delta: col_b = W^T * delta_b, then col2im into a zeroed delta
-            hip.gemmStridedBatched(True, False, K, L, f, 1.0, p[f"w{i}"], 0, K, 0, d, 0, L, f * L, 0.0, col, 0, L,
-                                   K * L, B)
             dx = t[f"dx{i}"]
-            hip.col2imStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx, c * hh * hh, 0, B)
+            if self.conv_dgrad:
+                # input delta: the output delta convolved with the flipped,
+                # transposed weights (f channels in, c filters out, pad 1)
+                hip.conv2dForward(B, f, hh, hh, c, 3, 1, 1, d, 0, self.flipped[i], None, acLINEAR, dx, 0,
+                                  weightLayout=WEIGHTS_TAP_MAJOR)
+            else:
+                # input delta: col_b = W^T * delta_b, then col2im into a zeroed delta
+                hip.gemmStridedBatched(True, False, K, L, f, 1.0, p[f"w{i}"], 0, K, 0, d, 0, L, f * L, 0.0, col, 0,
+                                       L, K * L, B)
+                hip.col2imStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx, c * hh * hh, 0, B)
             # maxpool backward into the previous block's zeroed delta
             pc, phh, pf = self.dims[i - 1]
             prev = t[f"delta{i - 1}"]

@@ -14,6 +14,7 @@ import torch
 from oracle import refcpu as R
 from oracle import trainref as T
 from tensorium_amd import synth, trainnet
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, acLINEAR
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -494,3 +495,46 @@ def test_cifar_step_fused_wgrad_equals_im2col_path(hip):
         out.append({k: gpu.host(k).copy() for k in ("u_w0", "u_w1", "u_w2", "w0", "w1", "w2", "s0", "u_fw")})
     for k in out[0]:
         assert np.array_equal(out[0][k], out[1][k]), k
+
+
+@pytest.mark.parametrize("F,C,k", [(64, 32, 3), (128, 64, 3), (5, 7, 3), (6, 4, 1), (3, 2, 5)])
+def test_pack_weights_dgrad(hip, F, C, k):
+    """The training step's dual repack: the tap-major copy equals
+    tnh_conv2d_pack_weights', the flipped one is w[f][c][k-1-ky][k-1-kx] at
+    [c][ky][kx][f], bit for bit; a NULL tap-major copy is skipped."""
+    case(f"pack_weights_dgrad F{F} C{C} k{k}")
+    w = synth.normal(340, (F, C, k, k))
+    tap = torch.empty(w.size, dtype=torch.float32, device="cuda")
+    flip = torch.empty(w.size, dtype=torch.float32, device="cuda")
+    hip.packConvWeightsDgrad(F, C, k, D(w), tap, flip)
+    assert np.array_equal(H(tap, hip).reshape(F, k, k, C), w.transpose(0, 2, 3, 1))
+    assert np.array_equal(H(flip, hip).reshape(C, k, k, F), w[:, :, ::-1, ::-1].transpose(1, 2, 3, 0))
+    flip2 = torch.empty(w.size, dtype=torch.float32, device="cuda")
+    hip.packConvWeightsDgrad(F, C, k, D(w), None, flip2)
+    assert np.array_equal(H(flip2, hip), H(flip, hip))
+
+
+@pytest.mark.parametrize("B,F,C,hh", [(128, 64, 32, 16), (128, 128, 64, 8), (3, 48, 16, 10)])
+def test_conv_input_delta_as_convolution(hip, B, F, C, hh):
+    """The conv input delta as tnh_conv2d_fwd of the output delta with the
+    flipped weights (3x3, stride 1, pad 1) against torch's transposed
+    convolution in float64 and against the reference sequence (TN product +
+    col2im) on the GPU, within 1e-5 per tensor."""
+    case(f"conv input delta B{B} F{F} C{C} {hh}x{hh}")
+    w = synth.normal(341, (F, C, 3, 3), 0.1)
+    d = synth.normal(342, (B, F, hh, hh))
+    ref = torch.nn.functional.conv_transpose2d(torch.from_numpy(d).double(), torch.from_numpy(w).double(),
+                                               padding=1).numpy()
+    flip = torch.empty(w.size, dtype=torch.float32, device="cuda")
+    hip.packConvWeightsDgrad(F, C, 3, D(w), None, flip)
+    dx = torch.empty((B, C, hh, hh), dtype=torch.float32, device="cuda")
+    hip.conv2dForward(B, F, hh, hh, C, 3, 1, 1, D(d), 0, flip, None, acLINEAR, dx, 0, weightLayout=WEIGHTS_TAP_MAJOR)
+    got = H(dx, hip)
+    assert R.rel_err(got, ref) <= TOL
+    K, L = C * 9, hh * hh
+    col = torch.empty((B, K, L), dtype=torch.float32, device="cuda")
+    hip.gemmStridedBatched(True, False, K, L, F, 1.0, D(w.reshape(F, K)), 0, K, 0, D(d), 0, L, F * L, 0.0, col, 0, L,
+                           K * L, B)
+    dx2 = torch.zeros((B, C, hh, hh), dtype=torch.float32, device="cuda")
+    hip.col2imStridedBatched(C, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx2, C * hh * hh, 0, B)
+    assert R.rel_err(got, H(dx2, hip)) <= TOL
