@@ -636,6 +636,19 @@ int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
                               const float *output, int32_t act,
                               const float *xNorm, const float *scales,
                               float *delta, float *scaleUpdates);
+/* No reference counterpart: batchNormBackGPU (nbaselayer.pas:662-712) with
+ * the layer's activation derivative before it, in four launches instead of
+ * six: tnh_bn_backward_scale's pass (delta *= act'(output), scaleUpdates +=
+ * sum x_norm*delta, delta *= scales), tnh_means_vars_delta's sums, the two
+ * final steps in one launch, then tnh_normalize_delta.  The same operations
+ * in the same order as those four calls, so the same bits; x is the
+ * pre-normalization output, mean / variance the forward's statistics. */
+int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
+                        const float *output, int32_t act, const float *xNorm,
+                        const float *x, const float *scales, const float *mean,
+                        const float *variance, float *delta,
+                        float *scaleUpdates, float *mean_delta,
+                        float *variance_delta);
 /* TNNCuda.softmaxBatch (nncuda.pas:1056) / softmax (nsoftmaxlayer.pas:81):
  * per (batch, group) row of N values (stride apart): e = exp((x-max)/temp),
  * out = e / sum(e). */

@@ -164,6 +164,8 @@ function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_backward_scale(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, scales, delta,
   scaleUpdates: PSingle): LongInt; cdecl; external libtnh;
+function tnh_bn_backward(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, x, scales, mean,
+  variance, delta, scaleUpdates, mean_delta, variance_delta: PSingle): LongInt; cdecl; external libtnh;
 function tnh_variances(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_statistics(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -369,6 +371,9 @@ type
     // DeriveArray + addDots + forwardScale of batchNormBack in one pass
     procedure bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
       const xNorm, scales, delta, scaleUpdates: TCUMem);
+    // batchNormBackGPU with the activation derivative before it, in four launches
+    procedure bnBackward(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
+      const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem);
     procedure avgPoolForward(const batch, c, h, w: SizeInt; const input, output: TCUMem);
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
@@ -875,6 +880,14 @@ procedure TNNHip<T>.bnStatistics(const srcSize, dstSize, groups: SizeInt; const 
 begin
   check(tnh_bn_statistics(srcSize, dstSize, groups, PSingle(src), offset, PSingle(means), PSingle(vars),
     PSingle(rollingMeans), PSingle(rollingVars), S(momentum)));
+end;
+
+procedure TNNHip<T>.bnBackward(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
+  const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem);
+begin
+  check(tnh_bn_backward(N, dstSize, groups, PSingle(output), activation, PSingle(xNorm), PSingle(x), PSingle(scales),
+    PSingle(mean), PSingle(variance), PSingle(delta), PSingle(scaleUpdates), PSingle(mean_delta),
+    PSingle(variance_delta)));
 end;
 
 procedure TNNHip<T>.bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem;

@@ -319,6 +319,20 @@ struct MvdFin {
   }
 };
 
+// The batch-norm backward's two final steps in one launch: the mean / variance
+// deltas (MvdFin) and dgamma += the BnBackOp partials' total (AddFin), each
+// from its own partials.
+struct BnBackFin {
+  MvdFin mvd;
+  const float* dotPart;
+  float* scaleUpdates;
+  __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
+    mvd.run(i, s, sh);
+    const float t = fixed_total(dotPart + i * s.P, s.P, sh);
+    if (threadIdx.x == 0) scaleUpdates[i] = scaleUpdates[i] + t;
+  }
+};
+
 // addDots (ntensors.pas:7783-7830): sum of a*b
 struct DotOp {
   const float* x;
@@ -495,14 +509,17 @@ __global__ void clamp_kernel(int64_t n, float alpha, const float* src, float* ds
 }
 
 // TAvgPoolLayer.forward (navgpoollayer.pas:60-84): one workgroup per (b, c).
-__global__ __launch_bounds__(kRed) void avgpool_fwd_kernel(const float* in, int64_t hw, float* out) {
-  __shared__ float sh[kRed];
-  const int64_t r = blockIdx.x;
+// One wave per (image, channel) row: lane l adds elements l, l + 64, ... in
+// turn, then a fixed shuffle tree over the lanes (the same order every run).
+__global__ __launch_bounds__(256) void avgpool_fwd_kernel(const float* in, int64_t rows, int64_t hw, float* out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // whole waves: no lane of a live wave leaves early
   const float* p = in + r * hw;
   float s = 0.f;
-  for (int64_t k = threadIdx.x; k < hw; k += kRed) s = s + p[k];
-  const float t = block_sum(s, sh);
-  if (threadIdx.x == 0) out[r] = t / static_cast<float>(hw);
+  for (int64_t k = lane; k < hw; k += 64) s = s + p[k];
+  for (int off = 32; off > 0; off >>= 1) s = s + __shfl_down(s, off, 64);
+  if (lane == 0) out[r] = s / static_cast<float>(hw);
 }
 
 // TAvgPoolLayer.backward (navgpoollayer.pas:86-100).
@@ -985,8 +1002,8 @@ extern "C" int32_t tnh_avgpool_fwd(int64_t batch, int64_t c, int64_t h, int64_t 
   if (batch == 0) return TNH_OK;
   TNH_ARG(input && output, "avgpool_fwd: NULL buffer");
   TNH_ARG(batch * c < (int64_t(1) << 31), "avgpool_fwd: too many planes");
-  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(static_cast<unsigned>(batch * c)), dim3(kRed), 0, cx->stream, input,
-                     h * w, output);
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(static_cast<unsigned>((batch * c + 3) / 4)), dim3(256), 0, cx->stream,
+                     input, batch * c, h * w, output);
   return launch_status("avgpool_fwd_kernel");
 }
 
@@ -1165,4 +1182,31 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
   const bool va = aligned16(delta) && L % 4 == 0 && deltaBatchStride % 4 == 0;
   if (va) return launch_wgrad_col<true>(a, g, cx->stream);
   return launch_wgrad_col<false>(a, g, cx->stream);
+}
+
+extern "C" int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups, const float* output, int32_t act,
+                                   const float* xNorm, const float* x, const float* scales, const float* mean,
+                                   const float* variance, float* delta, float* scaleUpdates, float* mean_delta,
+                                   float* variance_delta) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "bn_backward: bad sizes");
+  TNH_ARG(output && xNorm && x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
+          "bn_backward: NULL buffer");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_backward: activation %d", act);
+  const int64_t block = N / (dstSize * groups);
+  TNH_ARG(block * dstSize * groups == N, "bn_backward: sizes do not align");
+  ChanSplit s;
+  float* red = nullptr;
+  // three partials per workgroup slot: the dgamma dots after the two
+  // mean / variance delta sums
+  if (int st = chan_split(s, red, dstSize, block, groups, 3, cx)) return st;
+  float* dotPart = red + 2 * dstSize * s.P;
+  if (int st = launch_partial<1>(cx, BnBackOp{delta, output, xNorm, scales, act, 0.f}, s,
+                                 chan_vec(s, {delta, output, xNorm}), dotPart, "chan_partial_kernel<bn_back>"))
+    return st;
+  if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
+                                 "chan_partial_kernel<mean_var_delta>",
+                                 BnBackFin{MvdFin{red, variance, mean_delta, variance_delta}, dotPart, scaleUpdates}))
+    return st;
+  return tnh_normalize_delta(N, dstSize, groups, delta, x, 0, mean, variance, mean_delta, variance_delta);
 }

@@ -129,6 +129,7 @@ _PROTOS = {
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_means": [i64, i64, i64, vp, i64, vp],
     "tnh_bn_backward_scale": [i64, i64, i64, vp, i32, vp, vp, vp, vp],
+    "tnh_bn_backward": [i64, i64, i64, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "tnh_variances": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -581,6 +582,13 @@ class TNNHip:
     def variances(self, srcSize, dstSize, groups, src, offset, means, vars):
         """Unbiased variances about the given means (the CPU path's divisor)."""
         call("tnh_variances", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
+
+    def bnBackward(self, N, dstSize, groups, output, activation, xNorm, x, scales, mean, variance, delta,
+                   scaleUpdates, mean_delta, variance_delta):
+        """The batch-norm backward with the activation derivative before it:
+        bnBackwardScale, meansAndVarsDelta and normalizeDelta in four launches."""
+        call("tnh_bn_backward", N, dstSize, groups, addr(output), activation, addr(xNorm), addr(x), addr(scales),
+             addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta), addr(variance_delta))
 
     def bnBackwardScale(self, N, dstSize, groups, output, activation, xNorm, scales, delta, scaleUpdates):
         """DeriveArray + addDots + forwardScale of batchNormBack in one pass

@@ -212,11 +212,11 @@ class CifarTrainer:
             c, hh, f = self.dims[i]
             n = B * f * hh * hh
             d = t[f"delta{i}"]
-            # leaky gradient, then batchNormBack's dgamma (addDots) and
-            # delta *= gamma (forwardScale), in one pass
-            hip.bnBackwardScale(n, f, B, t[f"out{i}"], acLEAKY, t[f"xn{i}"], p[f"s{i}"], d, p[f"u_s{i}"])
-            hip.meansAndVarsDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
-            hip.normalizeDelta(n, f, B, d, t[f"x{i}"], 0, t[f"mean{i}"], t[f"var{i}"], t[f"md{i}"], t[f"vd{i}"])
+            # leaky gradient, batchNormBack's dgamma (addDots) and delta *=
+            # gamma (forwardScale) in one pass, then the mean / variance
+            # deltas and normalizeDelta (four launches)
+            hip.bnBackward(n, f, B, t[f"out{i}"], acLEAKY, t[f"xn{i}"], t[f"x{i}"], p[f"s{i}"], t[f"mean{i}"],
+                           t[f"var{i}"], d, p[f"u_s{i}"], t[f"md{i}"], t[f"vd{i}"])
             # conv weight gradient: sum_b delta_b * im2col(input_b)^T
             src = self.input if i == 0 else t[f"pool{i - 1}"]
             K, L = c * 9, hh * hh

@@ -14,7 +14,7 @@ import torch
 from oracle import refcpu as R
 from oracle import trainref as T
 from tensorium_amd import synth, trainnet
-from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, acLINEAR
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -538,3 +538,35 @@ def test_conv_input_delta_as_convolution(hip, B, F, C, hh):
     dx2 = torch.zeros((B, C, hh, hh), dtype=torch.float32, device="cuda")
     hip.col2imStridedBatched(C, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx2, C * hh * hh, 0, B)
     assert R.rel_err(got, H(dx2, hip)) <= TOL
+
+
+@pytest.mark.parametrize("shape,act", [((128, 32, 32, 32), acLEAKY), ((8, 64, 8, 8), acLEAKY), ((3, 5, 7, 9), acLINEAR)])
+def test_bn_backward_equals_the_sequence(hip, shape, act):
+    """tnh_bn_backward (four launches) against bnBackwardScale,
+    meansAndVarsDelta and normalizeDelta: delta, dgamma and the mean /
+    variance deltas bit for bit."""
+    case(f"bn_backward {shape} act{act}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    out = synth.normal(350, shape)
+    xn = synth.normal(351, shape)
+    x = synth.normal(352, shape)
+    gamma = synth.normal(353, (F,))
+    mean = synth.normal(354, (F,), 0.1)
+    var = np.abs(synth.normal(355, (F,))) + np.float32(0.5)
+    d0 = synth.normal(356, shape)
+    su0 = synth.normal(357, (F,))
+    res = []
+    for fused in (True, False):
+        d, su = D(d0), D(su0)
+        md = torch.empty(F, dtype=torch.float32, device="cuda")
+        vd = torch.empty(F, dtype=torch.float32, device="cuda")
+        if fused:
+            hip.bnBackward(n, F, B, D(out), act, D(xn), D(x), D(gamma), D(mean), D(var), d, su, md, vd)
+        else:
+            hip.bnBackwardScale(n, F, B, D(out), act, D(xn), D(gamma), d, su)
+            hip.meansAndVarsDelta(n, F, B, d, D(x), 0, D(mean), D(var), md, vd)
+            hip.normalizeDelta(n, F, B, d, D(x), 0, D(mean), D(var), md, vd)
+        res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
