@@ -681,6 +681,18 @@ int32_t tnh_avgpool_bwd(int64_t batch, int64_t c, int64_t h, int64_t w,
 int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch,
                        float momentum, float decay, float *weights,
                        float *weightUpdates);
+/* No reference counterpart: tnh_sgd_update (the same bits) whose pass also
+ * writes each updated weight of nPack <= 8 conv layers of the arena (layer l:
+ * [packF][packC][taps] at element packOffset[l]) to its tap-major copy
+ * packTap[l] and, when packFlip[l] is not NULL, its flipped copy, as
+ * tnh_conv2d_pack_weights_dgrad would after the update: a training step's
+ * repacks ride on the update's pass instead of a launch per layer. */
+int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch,
+                            float momentum, float decay, float *weights,
+                            float *weightUpdates, int32_t nPack,
+                            const int64_t *packOffset, const int64_t *packF,
+                            const int64_t *packC, const int64_t *packTaps,
+                            float *const *packTap, float *const *packFlip);
 /* bias / scale part of the same updates (nConvolutionLayer.pas:694-706):
  * params = fma(lr/batch, paramUpdates, params); paramUpdates *= momentum. */
 int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch,

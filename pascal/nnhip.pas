@@ -205,6 +205,9 @@ function tnh_avgpool_fwd(batch, c, h, w: Int64; input, output: PSingle): LongInt
 function tnh_avgpool_bwd(batch, c, h, w: Int64; delta, deltaIn: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgd_update(N: Int64; learningRate: Single; batch: Int64; momentum, decay: Single;
   weights, weightUpdates: PSingle): LongInt; cdecl; external libtnh;
+function tnh_sgd_update_pack(N: Int64; learningRate: Single; batch: Int64; momentum, decay: Single;
+  weights, weightUpdates: PSingle; nPack: LongInt; packOffset, packF, packC, packTaps: PInt64;
+  packTap, packFlip: PPSingle): LongInt; cdecl; external libtnh;
 function tnh_param_update(N: Int64; learningRate: Single; batch: Int64; momentum: Single;
   params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgemm_nt_batch_reduce(M, N, L: Int64; alpha: Single; A: PSingle; aOff, lda, strideA: Int64;
@@ -378,6 +381,10 @@ type
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
       weights, weightUpdates: TCUMem);
+    // sgdUpdate whose pass also refreshes the packed copies of conv layers in the arena (flip[l] may be nil)
+    procedure sgdUpdatePack(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
+      weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64; const tapMajor,
+      flipped: array of TCUMem);
     procedure paramUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum: T;
       params, paramUpdates: TCUMem);
     procedure gemmNTBatchReduce(const M, N, L: SizeInt; const ALPHA: T; const A: TCUMem;
@@ -911,6 +918,25 @@ procedure TNNHip<T>.sgdUpdate(const N: SizeInt; const learningRate: T; const bat
   const momentum, decay: T; weights, weightUpdates: TCUMem);
 begin
   check(tnh_sgd_update(N, S(learningRate), batch, S(momentum), S(decay), PSingle(weights), PSingle(weightUpdates)));
+end;
+
+procedure TNNHip<T>.sgdUpdatePack(const N: SizeInt; const learningRate: T; const batch: SizeInt;
+  const momentum, decay: T; weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64;
+  const tapMajor, flipped: array of TCUMem);
+var
+  tp, fl: array of PSingle;
+  i: SizeInt;
+begin
+  if Length(offsets) = 0 then begin
+    sgdUpdate(N, learningRate, batch, momentum, decay, weights, weightUpdates);
+    exit
+  end;
+  SetLength(tp, Length(tapMajor));
+  SetLength(fl, Length(flipped));
+  for i := 0 to High(tapMajor) do tp[i] := PSingle(tapMajor[i]);
+  for i := 0 to High(flipped) do fl[i] := PSingle(flipped[i]);
+  check(tnh_sgd_update_pack(N, S(learningRate), batch, S(momentum), S(decay), PSingle(weights),
+    PSingle(weightUpdates), Length(offsets), @offsets[0], @F[0], @C[0], @taps[0], @tp[0], @fl[0]));
 end;
 
 procedure TNNHip<T>.paramUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum: T;

@@ -537,6 +537,37 @@ __global__ void sgd_kernel(int64_t n, float aDecay, float aRate, float momentum,
   }
 }
 
+// The conv layers of a weight arena whose updated weights also go to their
+// tap-major (and, for the data gradient, flipped) copies.
+constexpr int kMaxPack = 8;
+struct PackSet {
+  int n;
+  int64_t off[kMaxPack], F[kMaxPack], C[kMaxPack], taps[kMaxPack];
+  float* tap[kMaxPack];
+  float* flip[kMaxPack];
+};
+
+// sgd_kernel, then each updated weight of a listed conv layer is also
+// written where tnh_conv2d_pack_weights_dgrad would put it.
+__global__ void sgd_pack_kernel(int64_t n, float aDecay, float aRate, float momentum, float* w, float* wu,
+                                PackSet ps) {
+  GRID_STRIDE(i, n) {
+    const float u = fmaf(aDecay, w[i], wu[i]);
+    const float v = fmaf(aRate, u, w[i]);
+    w[i] = v;
+    wu[i] = u * momentum;
+    for (int l = 0; l < ps.n; ++l) {
+      const int64_t j = i - ps.off[l];
+      const int64_t per = ps.C[l] * ps.taps[l];
+      if (j < 0 || j >= ps.F[l] * per) continue;
+      const int64_t f = j / per, r = j - f * per;
+      const int64_t c = r / ps.taps[l], t = r - c * ps.taps[l];
+      ps.tap[l][(f * ps.taps[l] + t) * ps.C[l] + c] = v;
+      if (ps.flip[l]) ps.flip[l][(c * ps.taps[l] + (ps.taps[l] - 1 - t)) * ps.F[l] + f] = v;
+    }
+  }
+}
+
 // p = fma(lr/batch, pu, p); pu *= momentum (biases / scales).
 __global__ void param_update_kernel(int64_t n, float aRate, float momentum, float* p, float* pu) {
   GRID_STRIDE(i, n) {
@@ -1029,6 +1060,38 @@ extern "C" int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch, 
   hipLaunchKernelGGL(sgd_kernel, dim3(grid_1d(N)), dim3(256), 0, cx->stream, N, aDecay, aRate, momentum, weights,
                      weightUpdates);
   return launch_status("sgd_kernel");
+}
+
+extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch, float momentum, float decay,
+                                       float* weights, float* weightUpdates, int32_t nPack, const int64_t* packOffset,
+                                       const int64_t* packF, const int64_t* packC, const int64_t* packTaps,
+                                       float* const* packTap, float* const* packFlip) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(N >= 0 && batch > 0, "sgd_update_pack: bad arguments");
+  TNH_ARG(nPack >= 0 && nPack <= kMaxPack, "sgd_update_pack: %d layers (at most %d)", nPack, kMaxPack);
+  if (N == 0) return TNH_OK;
+  TNH_ARG(weights && weightUpdates, "sgd_update_pack: NULL buffer");
+  TNH_ARG(nPack == 0 || (packOffset && packF && packC && packTaps && packTap && packFlip),
+          "sgd_update_pack: NULL layer table");
+  PackSet ps{};
+  ps.n = nPack;
+  for (int l = 0; l < nPack; ++l) {
+    TNH_ARG(packF[l] > 0 && packC[l] > 0 && packTaps[l] > 0 && packOffset[l] >= 0 &&
+                packOffset[l] + packF[l] * packC[l] * packTaps[l] <= N && packTap[l],
+            "sgd_update_pack: layer %d outside the arena", l);
+    TNH_ARG(packTap[l] != weights && packFlip[l] != weights, "sgd_update_pack: a copy aliases the weights");
+    ps.off[l] = packOffset[l];
+    ps.F[l] = packF[l];
+    ps.C[l] = packC[l];
+    ps.taps[l] = packTaps[l];
+    ps.tap[l] = packTap[l];
+    ps.flip[l] = packFlip[l];
+  }
+  const float aDecay = -decay * static_cast<float>(batch);
+  const float aRate = learningRate / static_cast<float>(batch);
+  hipLaunchKernelGGL(sgd_pack_kernel, dim3(grid_1d(N)), dim3(256), 0, cx->stream, N, aDecay, aRate, momentum, weights,
+                     weightUpdates, ps);
+  return launch_status("sgd_pack_kernel");
 }
 
 extern "C" int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch, float momentum, float* params,

@@ -152,6 +152,15 @@ class CifarTrainer:
         torch.cuda.synchronize()
         self._pack()
 
+    def _pack_layers(self):
+        w = self.arena["w"][0]
+        out = []
+        for i, (c, _, f) in enumerate(self.dims):
+            off = (self.p[f"w{i}"].data_ptr() - w.data_ptr()) // 4
+            flip = self.flipped[i] if (self.conv_dgrad and i > 0) else None
+            out.append((off, f, c, 9, self.packed[i], flip))
+        return out
+
     def _pack(self):
         for i, (c, _, f) in enumerate(self.dims):
             if self.conv_dgrad and i > 0:  # the first layer computes no input delta
@@ -252,10 +261,11 @@ class CifarTrainer:
         hip, B = self.hip, self.B
         lr, m, dec = self.lr, self.momentum, self.decay
         w, uw = self.arena["w"]
-        hip.sgdUpdate(w.numel(), lr, B, m, dec, w, uw)
+        # the update's pass also writes the conv weights' tap-major (and
+        # flipped) copies the next forward and backward read
+        hip.sgdUpdatePack(w.numel(), lr, B, m, dec, w, uw, self._pack_layers())
         q, uq = self.arena["p"]
         hip.paramUpdate(q.numel(), lr, B, m, q, uq)
-        self._pack()
 
     def step(self, x, truth):
         self.forward(x, truth)

@@ -570,3 +570,35 @@ def test_bn_backward_equals_the_sequence(hip, shape, act):
         res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
     for a, b in zip(*res):
         assert np.array_equal(a, b)
+
+
+def test_sgd_update_pack_equals_update_then_pack(hip):
+    """tnh_sgd_update_pack: the weights and momenta of tnh_sgd_update bit for
+    bit, and each listed layer's tap-major / flipped copies equal to
+    tnh_conv2d_pack_weights_dgrad of the updated weights; elements outside
+    the layers (a connected layer in the same arena) only updated."""
+    case("sgd_update_pack")
+    layers = [(32, 3, 9), (64, 32, 9), (10, 6, 1)]
+    sizes = [f * c * t for f, c, t in layers]
+    n = sum(sizes) + 1290
+    w0 = synth.normal(360, (n,))
+    u0 = synth.normal(361, (n,))
+    wa, ua = D(w0), D(u0)
+    hip.sgdUpdate(n, 1e-3, 128, 0.9, 1e-4, wa, ua)
+    wb, ub = D(w0), D(u0)
+    offs = np.concatenate([[0], np.cumsum(sizes)])[:-1] + 1290  # the connected layer first
+    taps = [torch.empty(sz, dtype=torch.float32, device="cuda") for sz in sizes]
+    flips = [torch.empty(sz, dtype=torch.float32, device="cuda") for sz in sizes]
+    hip.sgdUpdatePack(n, 1e-3, 128, 0.9, 1e-4, wb, ub,
+                      [(int(o), f, c, t, tp, fl if i > 0 else None)
+                       for i, ((f, c, t), o, tp, fl) in enumerate(zip(layers, offs, taps, flips))])
+    wref = H(wa, hip)
+    assert np.array_equal(H(wb, hip), wref) and np.array_equal(H(ub, hip), H(ua, hip))
+    for i, ((f, c, t), o) in enumerate(zip(layers, offs)):
+        k = int(round(t ** 0.5))
+        tp = torch.empty(f * c * t, dtype=torch.float32, device="cuda")
+        fl = torch.empty(f * c * t, dtype=torch.float32, device="cuda")
+        hip.packConvWeightsDgrad(f, c, k, wa[int(o):int(o) + f * c * t], tp, fl)
+        assert np.array_equal(H(taps[i], hip), H(tp, hip)), i
+        if i > 0:
+            assert np.array_equal(H(flips[i], hip), H(fl, hip)), i
