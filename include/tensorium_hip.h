@@ -517,6 +517,18 @@ int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch,
                        const float *x, float *xNorm, float *out,
                        const float *mean, const float *variance,
                        const float *scales, const float *biases, int32_t act);
+/* No reference counterpart: tnh_bn_forward over [batch][N][h][w] followed by
+ * tnh_maxpool_fwd of its output with size 2, stride 2, padding 0 (the
+ * config-3 blocks), in one pass and bit for bit: xNorm and out as
+ * tnh_bn_forward writes them, pooled [batch][N][h/2][w/2] and the int64
+ * indexes (may be NULL) as the maxpool writes them; tnh_maxpool_bwd then
+ * finds that geometry.  h even, w % 4 == 0, 16-byte aligned x, xNorm, out,
+ * indexes, 8-byte aligned pooled. */
+int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w,
+                               const float *x, float *xNorm, float *out,
+                               const float *mean, const float *variance,
+                               const float *scales, const float *biases,
+                               int32_t act, float *pooled, int64_t *indexes);
 
 /* ---- the element-wise methods of TNNCuda for the layers around the
  *      convolution path (LRN, logistic / L2 cost, dropout, swish, a yolo

@@ -158,6 +158,8 @@ function tnh_forward_scale_add(dstSize: Int64; dst: PSingle; offset, scaleSize: 
   incb, batch: Int64): LongInt; cdecl; external libtnh;
 function tnh_bn_forward(dstSize, N, batch: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
   act: LongInt): LongInt; cdecl; external libtnh;
+function tnh_bn_forward_maxpool(batch, N, h, w: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
+  act: LongInt; pooled: PSingle; indexes: PInt64): LongInt; cdecl; external libtnh;
 function tnh_means_vars(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -369,6 +371,9 @@ type
       const mean, variance: TCUMem; const batch: SizeInt);
     procedure bnForward(const dstSize, N, batch: SizeInt; const x, xNorm, output, mean, variance, scales,
       biases: TCUMem; const activation: longint);
+    // bnForward, then the 2x2 / stride 2 maxpool of its output, in one pass
+    procedure bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance, scales,
+      biases: TCUMem; const activation: longint; const pooled, indexes: TCUMem);
     procedure bnStatistics(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
       means, vars, rollingMeans, rollingVars: TCUMem; const momentum: T);
     // DeriveArray + addDots + forwardScale of batchNormBack in one pass
@@ -873,6 +878,13 @@ procedure TNNHip<T>.blockNormalize(const dstSize: SizeInt; const dst: TCUMem; co
   const mean, variance: TCUMem; const batch: SizeInt);
 begin
   check(tnh_bn_normalize(dstSize, PSingle(dst), offset, N, PSingle(mean), PSingle(variance), batch));
+end;
+
+procedure TNNHip<T>.bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance,
+  scales, biases: TCUMem; const activation: longint; const pooled, indexes: TCUMem);
+begin
+  check(tnh_bn_forward_maxpool(batch, N, h, w, PSingle(x), PSingle(xNorm), PSingle(output), PSingle(mean),
+    PSingle(variance), PSingle(scales), PSingle(biases), activation, PSingle(pooled), PInt64(indexes)));
 end;
 
 procedure TNNHip<T>.bnForward(const dstSize, N, batch: SizeInt; const x, xNorm, output, mean, variance, scales,

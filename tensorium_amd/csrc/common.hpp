@@ -95,6 +95,10 @@ int conv_scratch_setup(int device);
 // Forgets the maxpool forward geometry recorded for an indexes buffer at p
 // (pool.hip); tnh_free calls it for every buffer it releases.
 void pool_forget(const void* p);
+// records that `indexes` holds the int64 indices of a 2x2 / stride 2 /
+// padding 0 maxpool forward over [batch][C][h][w] (so tnh_maxpool_bwd finds
+// the geometry)
+void pool_remember_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t h, int64_t w);
 
 // Deterministic mode (tnh_set_deterministic): no timing-based tuning and no
 // split-K / tail-split tilings, so every process runs the same kernels and

@@ -3,6 +3,8 @@
 // element is produced by exactly the single fp32 operation the reference CPU
 // path applies (bit-exact).  Per-channel passes walk rows (rows.hpp);
 // flat passes use 16-byte accesses when the buffers allow.
+#include <cfloat>
+
 #include "common.hpp"
 #include "rows.hpp"
 #include "yolo_math.hpp"
@@ -144,6 +146,69 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_kernel(NormOp norm, ScaleAddO
         if (xNorm) xNorm[base + k] = n;
         out[base + k] = act_fwd(sa(cs, n), ACT);
       }
+    }
+  }
+}
+
+// bn_fwd_kernel followed by the 2x2 / stride 2 maxpool of its output in one
+// pass (the config-3 blocks: conv, batch norm, leaky, maxpool): a thread
+// takes two rows of four pixels of one plane, writes their x_norm and out as
+// bn_fwd_kernel does, then the two windows' max and global int64 index
+// exactly as the maxpool kernels scan them (rows, then columns, strict '>'
+// from -MaxSingle).  W % 4 == 0, H and W even, 16-byte aligned tensors.
+template <int ACT>
+__global__ __launch_bounds__(kThreads) void bn_fwd_pool2_kernel(NormOp norm, ScaleAddOp sa, int64_t total, int64_t C,
+                                                                int64_t H, int64_t W, const float* __restrict__ x,
+                                                                float* __restrict__ xNorm, float* __restrict__ out,
+                                                                float* __restrict__ pooled,
+                                                                int64_t* __restrict__ idx) {
+  const int64_t OH = H / 2, OW2 = W / 4;
+  for (int64_t t = blockIdx.x * int64_t(kThreads) + threadIdx.x; t < total; t += int64_t(gridDim.x) * kThreads) {
+    const int64_t jp = t % OW2, r = t / OW2;  // r = plane*OH + i
+    const int64_t i = r % OH, plane = r / OH;
+    const int64_t f = plane % C;
+    const NormOp::Ch cn = norm.chan(f);
+    const ScaleAddOp::Ch cs = sa.chan(f);
+    const int64_t x0 = 4 * jp;
+    const int64_t row0 = (plane * H + 2 * i) * W;
+    float a[8];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int64_t e = row0 + n * W + x0;
+      const float4 nv = map4(norm, cn, *reinterpret_cast<const float4*>(x + e));
+      if (xNorm) *reinterpret_cast<float4*>(xNorm + e) = nv;
+      const float4 o = map4(sa, cs, nv);
+      const float4 y = make_float4(act_fwd(o.x, ACT), act_fwd(o.y, ACT), act_fwd(o.z, ACT), act_fwd(o.w, ACT));
+      *reinterpret_cast<float4*>(out + e) = y;
+      a[4 * n] = y.x;
+      a[4 * n + 1] = y.y;
+      a[4 * n + 2] = y.z;
+      a[4 * n + 3] = y.w;
+    }
+    float m[2];
+    int64_t k[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float mx = -FLT_MAX;
+      int64_t mi = -1;
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float v = a[4 * n + 2 * h + c];
+          if (v > mx) {
+            mx = v;
+            mi = row0 + n * W + x0 + 2 * h + c;
+          }
+        }
+      m[h] = mx;
+      k[h] = mi;
+    }
+    const int64_t o = r * (2 * OW2) + 2 * jp;
+    *reinterpret_cast<float2*>(pooled + o) = make_float2(m[0], m[1]);
+    if (idx) {
+      idx[o] = k[0];
+      idx[o + 1] = k[1];
     }
   }
 }
@@ -578,4 +643,34 @@ extern "C" int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch, con
     if (act == TNH_AC_LEAKY) go(V1{}, L{}); else if (act == TNH_AC_LOGISTIC) go(V1{}, G{}); else go(V1{}, I{});
   }
   return launch_status("bn_fwd_kernel");
+}
+
+extern "C" int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,
+                                          float* xNorm, float* out, const float* mean, const float* variance,
+                                          const float* scales, const float* biases, int32_t act, float* pooled,
+                                          int64_t* indexes) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch > 0 && N > 0 && h > 0 && w > 0, "bn_forward_maxpool: bad sizes");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_forward_maxpool: activation %d",
+          act);
+  TNH_ARG(x && out && mean && variance && scales && biases && pooled, "bn_forward_maxpool: NULL buffer");
+  TNH_ARG(h % 2 == 0 && w % 4 == 0 && al16(x) && al16(out) && (!xNorm || al16(xNorm)) &&
+              (reinterpret_cast<uintptr_t>(pooled) & 7) == 0 && (!indexes || al16(indexes)),
+          "bn_forward_maxpool: needs even h, w %% 4 == 0 and aligned tensors");
+  const int64_t total = batch * N * (h / 2) * (w / 4);  // (plane, output row, pair of output columns)
+  const NormOp norm{mean, 1, variance, 1, h * w == 1};
+  const ScaleAddOp sa{scales, biases, 1};
+  const int64_t blocks = (total + kThreads - 1) / kThreads;
+  const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+  if (act == TNH_AC_LEAKY)
+    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LEAKY>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N, h,
+                       w, x, xNorm, out, pooled, indexes);
+  else if (act == TNH_AC_LOGISTIC)
+    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LOGISTIC>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N,
+                       h, w, x, xNorm, out, pooled, indexes);
+  else
+    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LINEAR>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N,
+                       h, w, x, xNorm, out, pooled, indexes);
+  if (indexes) pool_remember_2x2(indexes, batch, N, h, w);
+  return launch_status("bn_fwd_pool2_kernel");
 }

@@ -370,6 +370,11 @@ std::unordered_map<const int64_t*, PoolRecord> g_pool_geom;
 
 }  // namespace
 
+void pool_remember_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t h, int64_t w) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool_geom[indexes] = PoolRecord{PoolGeom{C, h, w, (h - 2) / 2 + 1, (w - 2) / 2 + 1, 2, 2, 2, 0}, batch};
+}
+
 void pool_forget(const void* p) {
   std::lock_guard<std::mutex> lk(g_pool_mu);
   g_pool_geom.erase(static_cast<const int64_t*>(p));

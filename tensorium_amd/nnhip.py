@@ -122,6 +122,7 @@ _PROTOS = {
     "tnh_normalize": [i64, i64, i64, vp, i64, vp, i64, vp, i64],
     "tnh_forward_scale_add": [i64, vp, i64, i64, vp, vp, i64, i64],
     "tnh_bn_forward": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32],
+    "tnh_bn_forward_maxpool": [i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
     "tnh_yolo_detections": [i64, i32, C.POINTER(vp), C.POINTER(i64), i64, i64, C.POINTER(f32), i64, i64, i64, i64,
                             f32, i32, i32, i64, vp, vp, vp, vp],
@@ -559,6 +560,12 @@ class TNNHip:
     def forwardScaleAdd(self, dstSize, dst, offset, scaleSize, scales, biases, incb, batch):
         """TNNCuda.forwardScaleAdd (nncuda.pas:1490): dst = fl(scale*dst) + bias."""
         call("tnh_forward_scale_add", dstSize, addr(dst), offset, scaleSize, addr(scales), addr(biases), incb, batch)
+
+    def bnForwardMaxPool(self, batch, N, h, w, x, xNorm, out, mean, variance, scales, biases, activation, pooled,
+                         indexes):
+        """bnForward then forwardMaxPool (2x2, stride 2) of its output, one pass."""
+        call("tnh_bn_forward_maxpool", batch, N, h, w, addr(x), addr(xNorm), addr(out), addr(mean), addr(variance),
+             addr(scales), addr(biases), activation, addr(pooled), addr(indexes))
 
     def bnForward(self, dstSize, N, batch, x, xNorm, out, mean, variance, scales, biases, activation):
         """Fused batch-norm forward + activation (tnh_bn_forward)."""

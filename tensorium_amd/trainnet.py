@@ -184,12 +184,13 @@ class CifarTrainer:
             xn, out = t[f"xn{i}"], t[f"out{i}"]
             # x (y) is kept as the layer's pre-normalization copy; one pass
             # writes x_norm and act(scale * x_norm + bias)
-            hip.bnForward(n, f, B, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"], acLEAKY)
             if i < len(self.dims) - 1:
-                ph = hh // 2
-                hip.forwardMaxPool(B, f, ph, ph, out, f, hh, hh, 2, 2, 0, 2, t[f"pidx{i}"], t[f"pool{i}"])
+                # ... and the 2x2 maxpool of out in the same pass
+                hip.bnForwardMaxPool(B, f, hh, hh, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"],
+                                     acLEAKY, t[f"pool{i}"], t[f"pidx{i}"])
                 h = t[f"pool{i}"]
             else:
+                hip.bnForward(n, f, B, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"], acLEAKY)
                 h = out
         F, hw = BLOCKS[-1][1], self.final_hw
         hip.avgPoolForward(B, F, hw, hw, h, t["avg"])

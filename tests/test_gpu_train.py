@@ -602,3 +602,45 @@ def test_sgd_update_pack_equals_update_then_pack(hip):
         assert np.array_equal(H(taps[i], hip), H(tp, hip)), i
         if i > 0:
             assert np.array_equal(H(flips[i], hip), H(fl, hip)), i
+
+
+@pytest.mark.parametrize("shape,act,idx", [((128, 32, 32, 32), acLEAKY, True), ((4, 3, 6, 8), acLINEAR, True),
+                                           ((2, 5, 4, 12), acLEAKY, False)])
+def test_bn_forward_maxpool_equals_the_two_calls(hip, shape, act, idx):
+    """tnh_bn_forward_maxpool against tnh_bn_forward then tnh_maxpool_fwd
+    (2x2, stride 2): x_norm, out, the pooled values and int64 indices bit
+    for bit (ties included); the 7-argument maxpool backward then finds the
+    geometry (the plain scatter, equal to the oracle's)."""
+    case(f"bn_forward_maxpool {shape} act{act} idx{idx}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    x = synth.normal(370, shape)
+    x[0, 0, 0, :4] = x[0, 0, 1, :4] = 0.25  # ties inside the first windows
+    mean, var = synth.normal(371, (F,), 0.1), np.abs(synth.normal(372, (F,))) + np.float32(0.5)
+    gamma, beta = synth.normal(373, (F,)), synth.normal(374, (F,))
+    res = []
+    for fused in (True, False):
+        xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        pool = torch.empty((B, F, h // 2, w // 2), dtype=torch.float32, device="cuda")
+        pidx = torch.empty((B, F, h // 2, w // 2), dtype=torch.int64, device="cuda") if idx else None
+        if fused:
+            hip.bnForwardMaxPool(B, F, h, w, D(x), xn, out, D(mean), D(var), D(gamma), D(beta), act, pool, pidx)
+        else:
+            hip.bnForward(n, F, B, D(x), xn, out, D(mean), D(var), D(gamma), D(beta), act)
+            hip.forwardMaxPool(B, F, h // 2, w // 2, out, F, h, w, 2, 2, 0, 2, pidx, pool)
+        res.append([H(t_, hip).copy() for t_ in (xn, out, pool) + ((pidx,) if idx else ())])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+    if idx:
+        delta = synth.normal(375, (B, F, h // 2, w // 2))
+        base = synth.normal(376, shape)
+        ref = R.maxpool_bwd(res[0][3], delta, base.copy())
+        xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        pool = torch.empty((B, F, h // 2, w // 2), dtype=torch.float32, device="cuda")
+        pidx = torch.empty((B, F, h // 2, w // 2), dtype=torch.int64, device="cuda")
+        hip.bnForwardMaxPool(B, F, h, w, D(x), xn, out, D(mean), D(var), D(gamma), D(beta), act, pool, pidx)
+        db = D(base)
+        hip.backwardMaxPool(B, F, h // 2, w // 2, db, pidx, D(delta))
+        assert np.array_equal(H(db, hip), ref)
