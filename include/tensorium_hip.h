@@ -674,6 +674,33 @@ int32_t tnh_softmax_batch(int64_t N, const float *input, int64_t iOffset,
 int32_t tnh_cross_entropy_softmax(int64_t N, const float *pred,
                                   const float *truth, float *delta,
                                   float *error);
+/* No reference counterpart: the tail of a classifier whose last conv block
+ * is followed by TAvgPoolLayer, TConnectedLayer and TSoftmaxLayer with
+ * cross-entropy (the config-3 network), forward in one launch (one
+ * workgroup per image): avg[b][f] = mean of x[b][f][0 .. hw) (the wave tree of
+ * tnh_avgpool_fwd), logits = 0 + sdot(avg_b, W_c) + bias[c] (gemm NT with
+ * beta 0 in sdot_avx2's 8-lane order, ntensors.pas:1233-1306, then
+ * forwardBias), prob = softmaxBatch of the logits (nsoftmaxlayer.pas:81-105),
+ * delta and error of softmaxCrossEntropy (nsoftmaxlayer.pas:123-137).
+ * weights [classes][F]; F <= 8192, classes <= 1024. */
+int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw,
+                                 int64_t classes, const float *x, float *avg,
+                                 const float *weights, const float *biases,
+                                 const float *truth, float *logits,
+                                 float *prob, float *delta, float *error);
+/* No reference counterpart: the backward of the same tail in one launch:
+ * delta = clamp(delta, -clampAlpha, clampAlpha) (TConnectedLayer.backward,
+ * nconnectedlayer.pas:255), biasUpdates += sum over images of delta
+ * (addSums), weightUpdates[c][f] = fma chain over the images of delta[b][c] *
+ * avg[b][f] (gemm TN, beta 1, saxpy_avx2's order), avgDelta[b][f] = fma chain
+ * over the classes from +0 (gemm NN), deltaIn[b][f][p] += avgDelta[b][f] / hw
+ * (TAvgPoolLayer.backward, navgpoollayer.pas:86-100). */
+int32_t tnh_softmax_head_backward(int64_t batch, int64_t F, int64_t hw,
+                                  int64_t classes, float clampAlpha,
+                                  float *delta, const float *avg,
+                                  const float *weights, float *weightUpdates,
+                                  float *biasUpdates, float *avgDelta,
+                                  float *deltaIn);
 /* TNNCuda.clamp (nncuda.pas:1551): dst = max(min(src, alpha), -alpha) at
  * offset + i*stride (TTensor.Clamp(-1, 1), nconnectedlayer.pas:255). */
 int32_t tnh_clamp(int64_t N, float alpha, const float *src, float *dst,

@@ -181,6 +181,10 @@ function tnh_add_dots(N, dstSize, groups: Int64; src1, src2: PSingle; srcOffset:
 function tnh_softmax_batch(N: Int64; input: PSingle; iOffset, batch, batchSize, groups, groupSize, stride: Int64;
   temp: Single; output: PSingle; oOffset: Int64): LongInt; cdecl; external libtnh;
 function tnh_cross_entropy_softmax(N: Int64; pred, truth, delta, error: PSingle): LongInt; cdecl; external libtnh;
+function tnh_softmax_head_forward(batch, F, hw, classes: Int64; x, avg, weights, biases, truth, logits, prob, delta,
+  error: PSingle): LongInt; cdecl; external libtnh;
+function tnh_softmax_head_backward(batch, F, hw, classes: Int64; clampAlpha: Single; delta, avg, weights,
+  weightUpdates, biasUpdates, avgDelta, deltaIn: PSingle): LongInt; cdecl; external libtnh;
 function tnh_clamp(N: Int64; alpha: Single; src, dst: PSingle; stride, offset: Int64): LongInt; cdecl;
   external libtnh;
 function tnh_subvv(N: Int64; src1: PSingle; src1Offset, inca: Int64; src2: PSingle; src2Offset, incb: Int64;
@@ -371,6 +375,11 @@ type
       const mean, variance: TCUMem; const batch: SizeInt);
     procedure bnForward(const dstSize, N, batch: SizeInt; const x, xNorm, output, mean, variance, scales,
       biases: TCUMem; const activation: longint);
+    // avgpool + connected + softmax cross-entropy, forward and backward, one launch each
+    procedure softmaxHeadForward(const batch, F, hw, classes: SizeInt; const x, avg, weights, biases, truth, logits,
+      prob, delta, error: TCUMem);
+    procedure softmaxHeadBackward(const batch, F, hw, classes: SizeInt; const clampAlpha: T; const delta, avg,
+      weights, weightUpdates, biasUpdates, avgDelta, deltaIn: TCUMem);
     // bnForward, then the 2x2 / stride 2 maxpool of its output, in one pass
     procedure bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance, scales,
       biases: TCUMem; const activation: longint; const pooled, indexes: TCUMem);
@@ -878,6 +887,20 @@ procedure TNNHip<T>.blockNormalize(const dstSize: SizeInt; const dst: TCUMem; co
   const mean, variance: TCUMem; const batch: SizeInt);
 begin
   check(tnh_bn_normalize(dstSize, PSingle(dst), offset, N, PSingle(mean), PSingle(variance), batch));
+end;
+
+procedure TNNHip<T>.softmaxHeadForward(const batch, F, hw, classes: SizeInt; const x, avg, weights, biases, truth,
+  logits, prob, delta, error: TCUMem);
+begin
+  check(tnh_softmax_head_forward(batch, F, hw, classes, PSingle(x), PSingle(avg), PSingle(weights), PSingle(biases),
+    PSingle(truth), PSingle(logits), PSingle(prob), PSingle(delta), PSingle(error)));
+end;
+
+procedure TNNHip<T>.softmaxHeadBackward(const batch, F, hw, classes: SizeInt; const clampAlpha: T; const delta, avg,
+  weights, weightUpdates, biasUpdates, avgDelta, deltaIn: TCUMem);
+begin
+  check(tnh_softmax_head_backward(batch, F, hw, classes, S(clampAlpha), PSingle(delta), PSingle(avg),
+    PSingle(weights), PSingle(weightUpdates), PSingle(biasUpdates), PSingle(avgDelta), PSingle(deltaIn)));
 end;
 
 procedure TNNHip<T>.bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance,

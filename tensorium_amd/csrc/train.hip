@@ -522,6 +522,155 @@ __global__ __launch_bounds__(256) void avgpool_fwd_kernel(const float* in, int64
   if (lane == 0) out[r] = s / static_cast<float>(hw);
 }
 
+// ---------------------------------------------------------------------------
+// The config-3 network's tail as two launches: the average pool, the
+// connected layer (logits = avg * W^T + bias), the softmax and the
+// cross-entropy forward in one, their backwards in the other.  Each value is
+// formed as the reference's CPU sequence forms it: the connected product's
+// 8-lane dot (sdot_avx2) for the logits, its saxpy FMA chains (saxpy_avx2)
+// for dW (over the batch) and the input delta (over the classes), the
+// softmax of softmaxBatch, the delta clamp of TConnectedLayer.backward.
+// ---------------------------------------------------------------------------
+
+// sdot_avx2's order (ntensors.pas:1233-1306): eight FMA chains over k = 8q +
+// l, masked tail lanes adding fma(0, 0, .), then (acc[l] + acc[l+4]) and two
+// pairwise adds.  a is in LDS, b in global memory.
+__device__ inline float sdot8_dev(int64_t n, const float* a, const float* b) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t j = 0;
+  for (; j + 8 <= n; j += 8)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = fmaf(a[j + l], b[j + l], acc[l]);
+  if (j < n) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const bool in = j + l < n;
+      acc[l] = fmaf(in ? a[j + l] : 0.f, in ? b[j + l] : 0.f, acc[l]);
+    }
+  }
+  const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
+  return (t0 + t1) + (t2 + t3);
+}
+
+// One workgroup per image b after the average pool's launch (dynamic LDS:
+// F + classes floats, and the weights when they fit).
+__global__ __launch_bounds__(256) void softmax_head_fwd_kernel(int64_t F, int64_t hw, int64_t classes, bool stageW,
+                                                               const float* __restrict__ avg,
+                                                               const float* __restrict__ W,
+                                                               const float* __restrict__ bias,
+                                                               const float* __restrict__ truth,
+                                                               float* __restrict__ logits, float* __restrict__ prob,
+                                                               float* __restrict__ delta, float* __restrict__ error) {
+  extern __shared__ float sm[];
+  float* sAvg = sm;
+  float* sLog = sm + F;
+  const int64_t b = blockIdx.x;
+  // the image's averages (written by avgpool_fwd_kernel just before) to LDS
+  for (int64_t f = threadIdx.x; f < F; f += blockDim.x) sAvg[f] = avg[b * F + f];
+  __syncthreads();
+  // the weights to LDS when they fit (read once per workgroup, coalesced)
+  const float* Wl = W;
+  if (stageW) {
+    float* sW = sm + F + classes;
+    for (int64_t e = threadIdx.x; e < classes * F; e += blockDim.x) sW[e] = W[e];
+    __syncthreads();
+    Wl = sW;
+  }
+  // logits = 0 + 1*sdot (gemm NT with beta 0, alpha 1), then + bias (forwardBias)
+  for (int64_t c = threadIdx.x; c < classes; c += blockDim.x) {
+    const float dot = 1.0f * sdot8_dev(F, sAvg, Wl + c * F);
+    const float l = (0.0f + dot) + bias[c];
+    sLog[c] = l;
+    logits[b * classes + c] = l;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // softmax_kernel's row (temperature 1), then the cross-entropy
+    const float* xl = sLog;
+    float largest = xl[0];
+    for (int64_t i = 1; i < classes; ++i)
+      if (xl[i] > largest) largest = xl[i];
+    float sum = 0.f;
+    for (int64_t i = 0; i < classes; ++i) {
+      const float e = static_cast<float>(exp(static_cast<double>((xl[i] - largest) / 1.0f)));
+      sum = sum + e;
+      sLog[i] = e;  // each logit is read before its slot is reused
+    }
+    for (int64_t i = 0; i < classes; ++i) {
+      const float pv = sLog[i] / sum;
+      const float t = truth[b * classes + i];
+      prob[b * classes + i] = pv;
+      error[b * classes + i] = t != 0.f ? static_cast<float>(-log(static_cast<double>(fmaxf(pv, kEps)))) : 0.f;
+      delta[b * classes + i] = t - pv;
+    }
+  }
+}
+
+// Workgroups [0, batch): image b's connected-layer input delta (a saxpy FMA
+// chain over the classes from +0, gemm NN) and its average-pool backward into
+// deltaIn; workgroups [batch, batch + classes): class c's weight gradient
+// (FMA chain over the images into dW, gemm TN with beta 1) and bias gradient
+// (the images' sum, then added: addSums).  Every workgroup reads the softmax
+// delta through the clamp, so none waits for another; the image workgroups
+// also store the clamped delta.
+__global__ __launch_bounds__(256) void softmax_head_bwd_kernel(int64_t batch, int64_t F, int64_t hw,
+                                                               int64_t classes, float alpha, float* __restrict__ delta,
+                                                               const float* __restrict__ avg,
+                                                               const float* __restrict__ W, float* __restrict__ dW,
+                                                               float* __restrict__ db, float* __restrict__ avgDelta,
+                                                               float* __restrict__ dIn) {
+  extern __shared__ float sm[];
+  auto clampv = [&](float v) { return fmaxf(fminf(v, alpha), -alpha); };
+  if (blockIdx.x < batch) {
+    const int64_t b = blockIdx.x;
+    float* sDel = sm;
+    float* sDA = sm + classes;
+    for (int64_t c = threadIdx.x; c < classes; c += blockDim.x) sDel[c] = clampv(delta[b * classes + c]);
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < classes; c += blockDim.x) delta[b * classes + c] = sDel[c];
+    for (int64_t f = threadIdx.x; f < F; f += blockDim.x) {
+      float acc = 0.f;
+      for (int64_t c = 0; c < classes; ++c) acc = fmaf(1.0f * sDel[c], W[c * F + f], acc);
+      sDA[f] = acc;
+      avgDelta[b * F + f] = acc;
+    }
+    __syncthreads();
+    float* d = dIn + b * F * hw;
+    for (int64_t e = threadIdx.x; e < F * hw; e += blockDim.x) d[e] = d[e] + sDA[e / hw] / static_cast<float>(hw);
+    return;
+  }
+  const int64_t c = blockIdx.x - batch;
+  // the class's clamped deltas to LDS (chunks of the dynamic LDS's F +
+  // classes floats), then 32 images' averages in flight per step of the chain
+  const int64_t chunk = F + classes;
+  float* sD = sm;
+  float s = 0.f;  // bias gradient: the images' sum in order (thread 0)
+  for (int64_t f0 = 0; f0 < F; f0 += blockDim.x) {
+    const int64_t f = f0 + threadIdx.x;
+    float acc = f < F ? dW[c * F + f] : 0.f;
+    for (int64_t b0 = 0; b0 < batch; b0 += chunk) {
+      const int64_t nb = min(chunk, batch - b0);
+      __syncthreads();
+      for (int64_t j = threadIdx.x; j < nb; j += blockDim.x) sD[j] = clampv(delta[(b0 + j) * classes + c]);
+      __syncthreads();
+      if (f0 == 0 && threadIdx.x == 0)
+        for (int64_t j = 0; j < nb; ++j) s = s + sD[j];
+      if (f < F) {
+        int64_t j = 0;
+        for (; j + 32 <= nb; j += 32) {
+          float av[32];
+#pragma unroll
+          for (int q = 0; q < 32; ++q) av[q] = avg[(b0 + j + q) * F + f];
+#pragma unroll
+          for (int q = 0; q < 32; ++q) acc = fmaf(1.0f * sD[j + q], av[q], acc);
+        }
+        for (; j < nb; ++j) acc = fmaf(1.0f * sD[j], avg[(b0 + j) * F + f], acc);
+      }
+    }
+    if (f < F) dW[c * F + f] = acc;
+  }
+  if (threadIdx.x == 0) db[c] = db[c] + s;
+}
+
 // TAvgPoolLayer.backward (navgpoollayer.pas:86-100).
 __global__ void avgpool_bwd_kernel(int64_t n, int64_t hw, const float* dOut, float* dIn) {
   GRID_STRIDE(e, n) dIn[e] = dIn[e] + dOut[e / hw] / static_cast<float>(hw);
@@ -1272,4 +1421,42 @@ extern "C" int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups, c
                                  BnBackFin{MvdFin{red, variance, mean_delta, variance_delta}, dotPart, scaleUpdates}))
     return st;
   return tnh_normalize_delta(N, dstSize, groups, delta, x, 0, mean, variance, mean_delta, variance_delta);
+}
+
+extern "C" int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw, int64_t classes, const float* x,
+                                            float* avg, const float* weights, const float* biases,
+                                            const float* truth, float* logits, float* prob, float* delta,
+                                            float* error) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch > 0 && F > 0 && hw > 0 && classes > 0 && F <= 8192 && classes <= 1024 && batch < (int64_t(1) << 31),
+          "softmax_head_forward: bad sizes");
+  TNH_ARG(x && avg && weights && biases && truth && logits && prob && delta && error,
+          "softmax_head_forward: NULL buffer");
+  // the average pool as tnh_avgpool_fwd runs it (a wave per plane: more
+  // parallel than a workgroup per image), then the rest per image
+  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(static_cast<unsigned>((batch * F + 3) / 4)), dim3(256), 0, cx->stream,
+                     x, batch * F, hw, avg);
+  if (int st = launch_status("avgpool_fwd_kernel")) return st;
+  const bool stageW = classes * F <= 8192;  // up to 32 KB of weights in LDS
+  const size_t lds = static_cast<size_t>(F + classes + (stageW ? classes * F : 0)) * 4;
+  hipLaunchKernelGGL(softmax_head_fwd_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), lds, cx->stream, F, hw,
+                     classes, stageW, avg, weights, biases, truth, logits, prob, delta, error);
+  return launch_status("softmax_head_fwd_kernel");
+}
+
+extern "C" int32_t tnh_softmax_head_backward(int64_t batch, int64_t F, int64_t hw, int64_t classes, float clampAlpha,
+                                             float* delta, const float* avg, const float* weights,
+                                             float* weightUpdates, float* biasUpdates, float* avgDelta,
+                                             float* deltaIn) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch > 0 && F > 0 && hw > 0 && classes > 0 && F <= 8192 && classes <= 1024 &&
+              batch + classes < (int64_t(1) << 31),
+          "softmax_head_backward: bad sizes");
+  TNH_ARG(delta && avg && weights && weightUpdates && biasUpdates && avgDelta && deltaIn,
+          "softmax_head_backward: NULL buffer");
+  const size_t lds = static_cast<size_t>(F + classes) * 4;
+  hipLaunchKernelGGL(softmax_head_bwd_kernel, dim3(static_cast<unsigned>(batch + classes)), dim3(256), lds,
+                     cx->stream, batch, F, hw, classes, clampAlpha, delta, avg, weights, weightUpdates, biasUpdates,
+                     avgDelta, deltaIn);
+  return launch_status("softmax_head_bwd_kernel");
 }

@@ -138,6 +138,8 @@ _PROTOS = {
     "tnh_add_dots": [i64, i64, i64, vp, vp, i64, vp],
     "tnh_softmax_batch": [i64, vp, i64, i64, i64, i64, i64, i64, f32, vp, i64],
     "tnh_cross_entropy_softmax": [i64, vp, vp, vp, vp],
+    "tnh_softmax_head_forward": [i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_softmax_head_backward": [i64, i64, i64, i64, f32, vp, vp, vp, vp, vp, vp, vp],
     "tnh_clamp": [i64, f32, vp, vp, i64, i64],
     "tnh_subvv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
     "tnh_mulvv": [i64, vp, i64, i64, vp, i64, i64, vp, i64, i64],
@@ -625,6 +627,18 @@ class TNNHip:
 
     def crossEntropySoftmax(self, N, pred, truth, delta, error):
         call("tnh_cross_entropy_softmax", N, addr(pred), addr(truth), addr(delta), addr(error))
+
+    def softmaxHeadForward(self, batch, F, hw, classes, x, avg, weights, biases, truth, logits, prob, delta,
+                           error):
+        """avgpool + connected + softmax + cross-entropy forward in one launch."""
+        call("tnh_softmax_head_forward", batch, F, hw, classes, addr(x), addr(avg), addr(weights), addr(biases),
+             addr(truth), addr(logits), addr(prob), addr(delta), addr(error))
+
+    def softmaxHeadBackward(self, batch, F, hw, classes, clampAlpha, delta, avg, weights, weightUpdates,
+                            biasUpdates, avgDelta, deltaIn):
+        """Their backward (clamp, bias / weight gradients, avgpool backward) in one launch."""
+        call("tnh_softmax_head_backward", batch, F, hw, classes, clampAlpha, addr(delta), addr(avg), addr(weights),
+             addr(weightUpdates), addr(biasUpdates), addr(avgDelta), addr(deltaIn))
 
     def clamp(self, N, alpha, src, dst, stride=1, offset=0):
         call("tnh_clamp", N, alpha, addr(src), addr(dst), stride, offset)

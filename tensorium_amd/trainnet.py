@@ -67,17 +67,19 @@ class CifarTrainer:
     backward and update on the device; `cost()` reads the loss back."""
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
-                 fused_wgrad=True, conv_dgrad=True):
+                 fused_wgrad=True, conv_dgrad=True, fused_head=True):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
         im2col + NT product (the same bits).  conv_dgrad: the conv input
         deltas are one convolution of the output delta with the flipped
         weights; False runs the reference's TN product + col2im (the same
-        sums in another order)."""
+        sums in another order).  fused_head: the average pool, the connected
+        layer, softmax and cross-entropy forward in one launch and their
+        backward in another; False runs them call by call."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
-        self.fused_wgrad, self.conv_dgrad = fused_wgrad, conv_dgrad
+        self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -193,13 +195,17 @@ class CifarTrainer:
                 hip.bnForward(n, f, B, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"], acLEAKY)
                 h = out
         F, hw = BLOCKS[-1][1], self.final_hw
+        self.truth = truth
+        # softmax backward: net.delta (zeroed each forward) += delta; t - p is
+        # never -0, so writing it straight into the zeroed delta is exact
+        if self.fused_head:
+            hip.softmaxHeadForward(B, F, hw * hw, CLASSES, h, t["avg"], p["fw"], p["fb"], truth, t["logits"],
+                                   t["prob"], t["fc_delta"], t["err"])
+            return
         hip.avgPoolForward(B, F, hw, hw, h, t["avg"])
         hip.gemm(False, True, B, CLASSES, F, 1.0, t["avg"], 0, F, p["fw"], 0, F, 0.0, t["logits"], 0, CLASSES)
         hip.forwardBias(B * CLASSES, t["logits"], 0, CLASSES, p["fb"], 1, B)
         hip.softmaxBatch(CLASSES, t["logits"], 0, B, CLASSES, 1, CLASSES, 1, 1.0, t["prob"], 0)
-        self.truth = truth
-        # softmax backward: net.delta (zeroed each forward) += delta; t - p is
-        # never -0, so writing it straight into the zeroed delta is exact
         hip.crossEntropySoftmax(B * CLASSES, t["prob"], truth, t["fc_delta"], t["err"])
 
     # ------------------------------------------------------------ backward
@@ -208,15 +214,20 @@ class CifarTrainer:
         F, hw = BLOCKS[-1][1], self.final_hw
         nfc = B * CLASSES
         hip.fill(self.zero_arena.numel(), self.zero_arena, 0, 0.0, 1)
-        # connected backward
-        hip.clamp(nfc, 1.0, t["fc_delta"], t["fc_delta"])
-        hip.backwardBias(CLASSES, p["u_fb"], nfc, t["fc_delta"], 0, 1, B)
-        hip.gemm(True, False, CLASSES, F, B, 1.0, t["fc_delta"], 0, CLASSES, t["avg"], 0, F, 1.0, p["u_fw"], 0, F)
-        hip.gemm(False, False, B, F, CLASSES, 1.0, t["fc_delta"], 0, CLASSES, p["fw"], 0, F, 0.0, t["avg_delta"], 0, F)
-        # avgpool backward into the last block's zeroed delta
         last = len(self.dims) - 1
         d = t[f"delta{last}"]
-        hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
+        if self.fused_head:
+            # connected backward and the avgpool backward into the last
+            # block's zeroed delta, one launch
+            hip.softmaxHeadBackward(B, F, hw * hw, CLASSES, 1.0, t["fc_delta"], t["avg"], p["fw"], p["u_fw"],
+                                    p["u_fb"], t["avg_delta"], d)
+        else:
+            hip.clamp(nfc, 1.0, t["fc_delta"], t["fc_delta"])
+            hip.backwardBias(CLASSES, p["u_fb"], nfc, t["fc_delta"], 0, 1, B)
+            hip.gemm(True, False, CLASSES, F, B, 1.0, t["fc_delta"], 0, CLASSES, t["avg"], 0, F, 1.0, p["u_fw"], 0, F)
+            hip.gemm(False, False, B, F, CLASSES, 1.0, t["fc_delta"], 0, CLASSES, p["fw"], 0, F, 0.0, t["avg_delta"],
+                     0, F)
+            hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
         col = t["col"]
         for i in range(last, -1, -1):
             c, hh, f = self.dims[i]

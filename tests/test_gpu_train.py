@@ -644,3 +644,69 @@ def test_bn_forward_maxpool_equals_the_two_calls(hip, shape, act, idx):
         db = D(base)
         hip.backwardMaxPool(B, F, h // 2, w // 2, db, pidx, D(delta))
         assert np.array_equal(H(db, hip), ref)
+
+
+@pytest.mark.parametrize("B,F,hw,classes", [(128, 128, 64, 10), (5, 37, 9, 3)])
+def test_softmax_head(hip, B, F, hw, classes):
+    """The fused tail against the oracle's sequence on the same inputs: the
+    averages within 1e-6 of float64; given the GPU's averages, the logits
+    (sdot_avx2 order + bias), the softmax, the cross-entropy delta, the
+    weight gradient (TN saxpy chains), the input delta (NN chains) and the
+    average-pool backward bit for bit; the error within 1e-6, the bias
+    gradient within 1e-6 (the oracle sums in float64)."""
+    case(f"softmax head B{B} F{F} hw{hw} classes{classes}")
+    x = synth.normal(380, (B, F, hw))
+    W = synth.normal(381, (classes, F), 0.2)
+    bias = synth.normal(382, (classes,), 0.1)
+    lab = (synth.splitmix64(383, B) % np.uint64(classes)).astype(np.int64)
+    truth = np.zeros((B, classes), np.float32)
+    truth[np.arange(B), lab] = 1
+    dev = lambda *sh: torch.empty(sh, dtype=torch.float32, device="cuda")  # noqa: E731
+    avg, logits, prob, delta, err = dev(B, F), dev(B, classes), dev(B, classes), dev(B, classes), dev(B, classes)
+    dW = D(W)
+    hip.softmaxHeadForward(B, F, hw, classes, D(x), avg, dW, D(bias), D(truth), logits, prob, delta, err)
+    a = H(avg, hip)
+    assert np.max(np.abs(a - x.astype(np.float64).mean(axis=2))) <= 1e-6 * max(1.0, np.abs(a).max())
+    ref = np.zeros((B, classes), np.float32)
+    R.sgemm(0, 1, B, classes, F, 1.0, a, F, W, F, 0.0, ref, classes)
+    ref = R.forward_bias(ref, bias, B)
+    assert np.array_equal(H(logits, hip), ref)
+    p_ref = R.softmax_rows(ref)
+    assert np.array_equal(H(prob, hip), p_ref)
+    d_ref, e_ref = T.cross_entropy(p_ref, truth)
+    assert np.array_equal(H(delta, hip), d_ref)
+    assert np.max(np.abs(H(err, hip) - e_ref)) <= 1e-6 * max(1.0, np.abs(e_ref).max())
+    # backward from a delta that the clamp cuts
+    dl = synth.normal(384, (B, classes), 1.5)
+    uw0, ub0 = synth.normal(385, (classes, F)), synth.normal(386, (classes,))
+    base = synth.normal(387, (B, F, hw))
+    duw, dub, dda, din, ddl = D(uw0), D(ub0), dev(B, F), D(base), D(dl)
+    hip.softmaxHeadBackward(B, F, hw, classes, 1.0, ddl, avg, dW, duw, dub, dda, din)
+    dc = T.clamp(dl, -1, 1)
+    assert np.array_equal(H(ddl, hip), dc)
+    uw = uw0.copy()
+    R.sgemm(1, 0, classes, F, B, 1.0, dc, classes, a, F, 1.0, uw, F)
+    assert np.array_equal(H(duw, hip), uw)
+    assert R.rel_err(H(dub, hip), T.add_sums(ub0, dc, B)) <= 1e-6  # a sequential fp32 sum against float64
+    dA = np.zeros((B, F), np.float32)
+    R.sgemm(0, 0, B, F, classes, 1.0, dc, classes, W, F, 1.0, dA, F)
+    assert np.array_equal(H(dda, hip), dA)
+    assert np.array_equal(H(din, hip), T.avgpool_bwd(base.reshape(B, F, hw, 1).copy(), dA).reshape(B, F, hw))
+
+
+def test_cifar_step_fused_head_matches_the_calls(hip):
+    """The training step with the fused tail against the call-by-call tail:
+    loss and every gradient within 1e-5 per tensor (the tails' sums run in
+    different orders)."""
+    case("cifar step fused head vs calls")
+    params = trainnet.init_params()
+    x, truth = _batch(322, 32)
+    out = []
+    for fused in (True, False):
+        gpu = trainnet.CifarTrainer(hip, params, 32, fused_head=fused)
+        gpu.forward(D(x), D(truth))
+        gpu.backward()
+        out.append((float(gpu.cost()), {k: gpu.host(k).copy() for k in ("u_fw", "u_fb", "u_w2", "u_s2", "u_w0")}))
+    assert abs(out[0][0] - out[1][0]) <= TOL * abs(out[1][0])
+    for k in out[0][1]:
+        assert R.rel_err(out[0][1][k], out[1][1][k]) <= TOL, k
