@@ -529,6 +529,15 @@ int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w,
                                const float *mean, const float *variance,
                                const float *scales, const float *biases,
                                int32_t act, float *pooled, int64_t *indexes);
+/* No reference counterpart: tnh_bn_forward over [batch][N][hw] (hw <= 64)
+ * followed by tnh_avgpool_fwd of its output, in one pass and bit for bit:
+ * xNorm (may be NULL) and out as tnh_bn_forward writes them, avg[b][n] the
+ * plane's mean as tnh_avgpool_fwd forms it. */
+int32_t tnh_bn_forward_avgpool(int64_t batch, int64_t N, int64_t hw,
+                               const float *x, float *xNorm, float *out,
+                               const float *mean, const float *variance,
+                               const float *scales, const float *biases,
+                               int32_t act, float *avg);
 
 /* ---- the element-wise methods of TNNCuda for the layers around the
  *      convolution path (LRN, logistic / L2 cost, dropout, swish, a yolo
@@ -661,6 +670,36 @@ int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
                         const float *variance, float *delta,
                         float *scaleUpdates, float *mean_delta,
                         float *variance_delta);
+/* No reference counterpart: TMaxPoolLayer.backward (2x2, stride 2) into the
+ * zeroed delta of the layer below it, then tnh_bn_backward, with the
+ * scatter formed inside tnh_bn_backward's first pass: the same bits as
+ * tnh_maxpool_bwd(poolDelta) into a zeroed delta followed by
+ * tnh_bn_backward.  delta [groups][dstSize][h][w] is written in full (its
+ * contents are not read); h and w even, N = groups*dstSize*h*w < 2^31;
+ * poolIndexes must be those that tnh_bn_forward_maxpool or tnh_maxpool_fwd
+ * (size 2, stride 2) last wrote over this geometry, else TNH_ERR_ARG. */
+int32_t tnh_bn_backward_maxpool(int64_t N, int64_t dstSize, int64_t groups,
+                                int64_t h, int64_t w,
+                                const int64_t *poolIndexes,
+                                const float *poolDelta, const float *output,
+                                int32_t act, const float *xNorm,
+                                const float *x, const float *scales,
+                                const float *mean, const float *variance,
+                                float *delta, float *scaleUpdates,
+                                float *mean_delta, float *variance_delta);
+/* No reference counterpart: TAvgPoolLayer.backward (deltaIn += avgDelta /
+ * hw, navgpoollayer.pas:86-100) into the zeroed delta of the layer below it,
+ * then tnh_bn_backward, the average pool's spread formed inside
+ * tnh_bn_backward's first pass: the same bits as the two calls.  avgDelta
+ * [groups][dstSize]; delta is written in full (its contents are not read);
+ * N < 2^31. */
+int32_t tnh_bn_backward_avgpool(int64_t N, int64_t dstSize, int64_t groups,
+                                const float *avgDelta, const float *output,
+                                int32_t act, const float *xNorm,
+                                const float *x, const float *scales,
+                                const float *mean, const float *variance,
+                                float *delta, float *scaleUpdates,
+                                float *mean_delta, float *variance_delta);
 /* TNNCuda.softmaxBatch (nncuda.pas:1056) / softmax (nsoftmaxlayer.pas:81):
  * per (batch, group) row of N values (stride apart): e = exp((x-max)/temp),
  * out = e / sum(e). */
@@ -682,7 +721,8 @@ int32_t tnh_cross_entropy_softmax(int64_t N, const float *pred,
  * beta 0 in sdot_avx2's 8-lane order, ntensors.pas:1233-1306, then
  * forwardBias), prob = softmaxBatch of the logits (nsoftmaxlayer.pas:81-105),
  * delta and error of softmaxCrossEntropy (nsoftmaxlayer.pas:123-137).
- * weights [classes][F]; F <= 8192, classes <= 1024. */
+ * weights [classes][F]; F <= 8192, classes <= 1024.  x NULL: avg holds the
+ * averages already (tnh_bn_forward_avgpool wrote them). */
 int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw,
                                  int64_t classes, const float *x, float *avg,
                                  const float *weights, const float *biases,
@@ -694,7 +734,8 @@ int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw,
  * (addSums), weightUpdates[c][f] = fma chain over the images of delta[b][c] *
  * avg[b][f] (gemm TN, beta 1, saxpy_avx2's order), avgDelta[b][f] = fma chain
  * over the classes from +0 (gemm NN), deltaIn[b][f][p] += avgDelta[b][f] / hw
- * (TAvgPoolLayer.backward, navgpoollayer.pas:86-100). */
+ * (TAvgPoolLayer.backward, navgpoollayer.pas:86-100).  deltaIn NULL: that
+ * last step is left out (tnh_bn_backward_avgpool takes avgDelta instead). */
 int32_t tnh_softmax_head_backward(int64_t batch, int64_t F, int64_t hw,
                                   int64_t classes, float clampAlpha,
                                   float *delta, const float *avg,

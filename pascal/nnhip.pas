@@ -160,6 +160,8 @@ function tnh_bn_forward(dstSize, N, batch: Int64; x, xNorm, output, mean, varian
   act: LongInt): LongInt; cdecl; external libtnh;
 function tnh_bn_forward_maxpool(batch, N, h, w: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
   act: LongInt; pooled: PSingle; indexes: PInt64): LongInt; cdecl; external libtnh;
+function tnh_bn_forward_avgpool(batch, N, hw: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
+  act: LongInt; avg: PSingle): LongInt; cdecl; external libtnh;
 function tnh_means_vars(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -168,6 +170,11 @@ function tnh_bn_backward_scale(N, dstSize, groups: Int64; output: PSingle; act: 
   scaleUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_backward(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, x, scales, mean,
   variance, delta, scaleUpdates, mean_delta, variance_delta: PSingle): LongInt; cdecl; external libtnh;
+function tnh_bn_backward_maxpool(N, dstSize, groups, h, w: Int64; poolIndexes: PInt64; poolDelta, output: PSingle;
+  act: LongInt; xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
+  variance_delta: PSingle): LongInt; cdecl; external libtnh;
+function tnh_bn_backward_avgpool(N, dstSize, groups: Int64; avgDelta, output: PSingle; act: LongInt; xNorm, x,
+  scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: PSingle): LongInt; cdecl; external libtnh;
 function tnh_variances(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_statistics(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -383,6 +390,9 @@ type
     // bnForward, then the 2x2 / stride 2 maxpool of its output, in one pass
     procedure bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance, scales,
       biases: TCUMem; const activation: longint; const pooled, indexes: TCUMem);
+    // bnForward, then the average of each output plane (hw <= 64), in one pass
+    procedure bnForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance, scales,
+      biases: TCUMem; const activation: longint; const avg: TCUMem);
     procedure bnStatistics(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
       means, vars, rollingMeans, rollingVars: TCUMem; const momentum: T);
     // DeriveArray + addDots + forwardScale of batchNormBack in one pass
@@ -391,6 +401,14 @@ type
     // batchNormBackGPU with the activation derivative before it, in four launches
     procedure bnBackward(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
       const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem);
+    // backwardMaxPool (2x2, stride 2) into a zeroed delta, then bnBackward; delta is written in full
+    procedure bnBackwardMaxPool(const N, dstSize, groups, h, w: SizeInt; const poolIndexes, poolDelta,
+      output: TCUMem; const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates,
+      mean_delta, variance_delta: TCUMem);
+    // avgPoolBackward into a zeroed delta, then bnBackward; delta is written in full
+    procedure bnBackwardAvgPool(const N, dstSize, groups: SizeInt; const avgDelta, output: TCUMem;
+      const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
+      variance_delta: TCUMem);
     procedure avgPoolForward(const batch, c, h, w: SizeInt; const input, output: TCUMem);
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
@@ -903,6 +921,13 @@ begin
     PSingle(weights), PSingle(weightUpdates), PSingle(biasUpdates), PSingle(avgDelta), PSingle(deltaIn)));
 end;
 
+procedure TNNHip<T>.bnForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance, scales,
+  biases: TCUMem; const activation: longint; const avg: TCUMem);
+begin
+  check(tnh_bn_forward_avgpool(batch, N, hw, PSingle(x), PSingle(xNorm), PSingle(output), PSingle(mean),
+    PSingle(variance), PSingle(scales), PSingle(biases), activation, PSingle(avg)));
+end;
+
 procedure TNNHip<T>.bnForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance,
   scales, biases: TCUMem; const activation: longint; const pooled, indexes: TCUMem);
 begin
@@ -930,6 +955,24 @@ begin
   check(tnh_bn_backward(N, dstSize, groups, PSingle(output), activation, PSingle(xNorm), PSingle(x), PSingle(scales),
     PSingle(mean), PSingle(variance), PSingle(delta), PSingle(scaleUpdates), PSingle(mean_delta),
     PSingle(variance_delta)));
+end;
+
+procedure TNNHip<T>.bnBackwardMaxPool(const N, dstSize, groups, h, w: SizeInt; const poolIndexes, poolDelta,
+  output: TCUMem; const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates,
+  mean_delta, variance_delta: TCUMem);
+begin
+  check(tnh_bn_backward_maxpool(N, dstSize, groups, h, w, PInt64(poolIndexes), PSingle(poolDelta), PSingle(output),
+    activation, PSingle(xNorm), PSingle(x), PSingle(scales), PSingle(mean), PSingle(variance), PSingle(delta),
+    PSingle(scaleUpdates), PSingle(mean_delta), PSingle(variance_delta)));
+end;
+
+procedure TNNHip<T>.bnBackwardAvgPool(const N, dstSize, groups: SizeInt; const avgDelta, output: TCUMem;
+  const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
+  variance_delta: TCUMem);
+begin
+  check(tnh_bn_backward_avgpool(N, dstSize, groups, PSingle(avgDelta), PSingle(output), activation, PSingle(xNorm),
+    PSingle(x), PSingle(scales), PSingle(mean), PSingle(variance), PSingle(delta), PSingle(scaleUpdates),
+    PSingle(mean_delta), PSingle(variance_delta)));
 end;
 
 procedure TNNHip<T>.bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem;

@@ -99,6 +99,9 @@ void pool_forget(const void* p);
 // padding 0 maxpool forward over [batch][C][h][w] (so tnh_maxpool_bwd finds
 // the geometry)
 void pool_remember_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t h, int64_t w);
+// True when the library recorded `indexes` as the indexes of a 2x2 stride-2
+// maxpool (no offset) over [batch][C][h][w].
+bool pool_is_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t h, int64_t w);
 
 // Deterministic mode (tnh_set_deterministic): no timing-based tuning and no
 // split-K / tail-split tilings, so every process runs the same kernels and

@@ -213,6 +213,35 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_pool2_kernel(NormOp norm, Sca
   }
 }
 
+// bn_fwd_kernel followed by the average of each output plane (the last
+// conv block of a classifier before its average pool): one wave per
+// (image, channel) plane of hw <= 64 elements, one element per lane, the
+// plane's x_norm and out written as bn_fwd_kernel writes them, then
+// avgpool_fwd_kernel's wave tree over the out values.
+template <int ACT>
+__global__ __launch_bounds__(kThreads) void bn_fwd_avg_kernel(NormOp norm, ScaleAddOp sa, int64_t planes, int64_t C,
+                                                              int64_t hw, const float* __restrict__ x,
+                                                              float* __restrict__ xNorm, float* __restrict__ out,
+                                                              float* __restrict__ avg) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= planes) return;  // whole waves
+  const int64_t f = r % C;
+  const NormOp::Ch cn = norm.chan(f);
+  const ScaleAddOp::Ch cs = sa.chan(f);
+  float s = 0.f;
+  if (lane < hw) {
+    const int64_t e = r * hw + lane;
+    const float n = norm(cn, x[e]);
+    if (xNorm) xNorm[e] = n;
+    const float o = act_fwd(sa(cs, n), ACT);
+    out[e] = o;
+    s = s + o;
+  }
+  for (int off = 32; off > 0; off >>= 1) s = s + __shfl_down(s, off, 64);
+  if (lane == 0) avg[r] = s / static_cast<float>(hw);
+}
+
 // Launches op over [groups][nb][block] at dst (n floats).
 template <class Op>
 int launch_rows(Op op, float* dst, int64_t n, int64_t block, int64_t nb, hipStream_t s, const char* name) {
@@ -673,4 +702,29 @@ extern "C" int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, i
                        h, w, x, xNorm, out, pooled, indexes);
   if (indexes) pool_remember_2x2(indexes, batch, N, h, w);
   return launch_status("bn_fwd_pool2_kernel");
+}
+
+extern "C" int32_t tnh_bn_forward_avgpool(int64_t batch, int64_t N, int64_t hw, const float* x, float* xNorm,
+                                          float* out, const float* mean, const float* variance, const float* scales,
+                                          const float* biases, int32_t act, float* avg) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(batch > 0 && N > 0 && hw > 0 && hw <= 64, "bn_forward_avgpool: bad sizes (hw <= 64)");
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_forward_avgpool: activation %d",
+          act);
+  TNH_ARG(x && out && mean && variance && scales && biases && avg, "bn_forward_avgpool: NULL buffer");
+  const int64_t planes = batch * N;
+  TNH_ARG(planes < (int64_t(1) << 31), "bn_forward_avgpool: too many planes");
+  const NormOp norm{mean, 1, variance, 1, hw == 1};
+  const ScaleAddOp sa{scales, biases, 1};
+  const dim3 grid(static_cast<unsigned>((planes + kThreads / 64 - 1) / (kThreads / 64)));
+  if (act == TNH_AC_LEAKY)
+    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LEAKY>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N, hw,
+                       x, xNorm, out, avg);
+  else if (act == TNH_AC_LOGISTIC)
+    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LOGISTIC>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N,
+                       hw, x, xNorm, out, avg);
+  else
+    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LINEAR>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N,
+                       hw, x, xNorm, out, avg);
+  return launch_status("bn_fwd_avg_kernel");
 }

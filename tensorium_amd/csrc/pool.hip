@@ -375,6 +375,16 @@ void pool_remember_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t
   g_pool_geom[indexes] = PoolRecord{PoolGeom{C, h, w, (h - 2) / 2 + 1, (w - 2) / 2 + 1, 2, 2, 2, 0}, batch};
 }
 
+bool pool_is_2x2(const int64_t* indexes, int64_t batch, int64_t C, int64_t h, int64_t w) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  const auto it = g_pool_geom.find(indexes);
+  if (it == g_pool_geom.end()) return false;
+  const PoolRecord& r = it->second;
+  const PoolGeom& g = r.g;
+  return r.batch == batch && g.C == C && g.H == h && g.W == w && g.OH == h / 2 && g.OW == w / 2 && g.size == 2 &&
+         g.sX == 2 && g.sY == 2 && g.off == 0;
+}
+
 void pool_forget(const void* p) {
   std::lock_guard<std::mutex> lk(g_pool_mu);
   g_pool_geom.erase(static_cast<const int64_t*>(p));

@@ -358,19 +358,66 @@ struct AddFin {
   }
 };
 
+// Where the layer's incoming delta comes from: the delta buffer itself, or
+// the backward of the pool layer above it, formed element by element as
+// that backward would leave it in the delta that TNNet zeroes before each
+// pass (nnet.pas:287-294), so the buffer need not be zeroed or written first:
+//   kFromMaxPool2: the 2x2 stride-2 maxpool scatter (TMaxPoolLayer.backward,
+//     delta[index] += poolDelta): 0 + poolDelta[o] at the element window o's
+//     index names, +0 at its other three elements;
+//   kFromAvgPool: TAvgPoolLayer.backward (navgpoollayer.pas:86-100), 0 +
+//     poolDelta[plane] / hw at every element of the plane.
+enum DeltaSrc { kFromDelta = 0, kFromMaxPool2 = 1, kFromAvgPool = 2 };
+
 // batchNormBack's first three steps (nbaselayer.pas:372-392) in one pass:
 // DeriveArray (delta *= act'(out)), addDots (dgamma += sum x_norm * delta)
 // and forwardScale (delta *= gamma), each element visited once with each
 // step's own operation, so the deltas and the dot equal the three separate
 // passes bit for bit.
-struct BnBackOp {
+template <int SRC>
+struct BnBackOpT {
   float* delta;
   const float* out;
   const float* xn;
   const float* gamma;
   int act;
   float g;
+  const int64_t* pidx = nullptr;  // kFromMaxPool2: the pool's indexes
+  const float* pdel = nullptr;    // the pool layer's delta
+  uint32_t block = 0, w = 0;      // plane size and row width (SRC != kFromDelta)
   __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) { g = gamma[i]; }
+  // 2x2 window of element e (planes of h x w, h and w even)
+  __device__ uint32_t win(uint32_t e) const {
+    const uint32_t plane = e / block, r = e - plane * block, y = r / w, x = r - y * w;
+    return plane * (block >> 2) + (y >> 1) * (w >> 1) + (x >> 1);
+  }
+  __device__ float src(int64_t e) const {
+    if constexpr (SRC == kFromDelta) {
+      return delta[e];
+    } else if constexpr (SRC == kFromAvgPool) {
+      return 0.f + pdel[static_cast<uint32_t>(e) / block] / static_cast<float>(block);
+    } else {
+      const uint32_t o = win(static_cast<uint32_t>(e));
+      return pidx[o] == e ? 0.f + pdel[o] : 0.f;
+    }
+  }
+  // four consecutive elements (e % 4 == 0; the 16-byte walk must be taken
+  // exactly when tnh_bn_backward takes it, which fixes the sums' order)
+  __device__ float4 src4(int64_t e) const {
+    if constexpr (SRC == kFromDelta) {
+      return ld4(delta + e);
+    } else if constexpr (SRC == kFromAvgPool) {
+      const float v = 0.f + pdel[static_cast<uint32_t>(e) / block] / static_cast<float>(block);
+      return make_float4(v, v, v, v);
+    } else {
+      if (w & 3) return make_float4(src(e), src(e + 1), src(e + 2), src(e + 3));
+      // one row, two windows
+      const uint32_t o = win(static_cast<uint32_t>(e));
+      const int64_t k0 = pidx[o], k1 = pidx[o + 1];
+      const float p0 = 0.f + pdel[o], p1 = 0.f + pdel[o + 1];
+      return make_float4(k0 == e ? p0 : 0.f, k0 == e + 1 ? p0 : 0.f, k1 == e + 2 ? p1 : 0.f, k1 == e + 3 ? p1 : 0.f);
+    }
+  }
   __device__ static float grad(float v, int act) {
     if (act == TNH_AC_LEAKY) return v > 0.f ? 1.f : 0.1f;
     if (act == TNH_AC_LOGISTIC) return (1.f - v) * v;
@@ -381,9 +428,9 @@ struct BnBackOp {
     a[0] = a[0] + x * d1;
     return g * d1;
   }
-  __device__ void add(float* a, int64_t e) const { delta[e] = one(a, delta[e], out[e], xn[e]); }
+  __device__ void add(float* a, int64_t e) const { delta[e] = one(a, src(e), out[e], xn[e]); }
   __device__ void add4(float* a, int64_t e) const {
-    const float4 d = ld4(delta + e), o = ld4(out + e), x = ld4(xn + e);
+    const float4 d = src4(e), o = ld4(out + e), x = ld4(xn + e);
     float4 r;
     r.x = one(a, d.x, o.x, x.x);
     r.y = one(a, d.y, o.y, x.y);
@@ -392,6 +439,7 @@ struct BnBackOp {
     *reinterpret_cast<float4*>(delta + e) = r;
   }
 };
+using BnBackOp = BnBackOpT<kFromDelta>;
 
 bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -634,8 +682,10 @@ __global__ __launch_bounds__(256) void softmax_head_bwd_kernel(int64_t batch, in
       avgDelta[b * F + f] = acc;
     }
     __syncthreads();
-    float* d = dIn + b * F * hw;
-    for (int64_t e = threadIdx.x; e < F * hw; e += blockDim.x) d[e] = d[e] + sDA[e / hw] / static_cast<float>(hw);
+    if (dIn) {
+      float* d = dIn + b * F * hw;
+      for (int64_t e = threadIdx.x; e < F * hw; e += blockDim.x) d[e] = d[e] + sDA[e / hw] / static_cast<float>(hw);
+    }
     return;
   }
   const int64_t c = blockIdx.x - batch;
@@ -1396,31 +1446,83 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
   return launch_wgrad_col<false>(a, g, cx->stream);
 }
 
-extern "C" int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups, const float* output, int32_t act,
-                                   const float* xNorm, const float* x, const float* scales, const float* mean,
-                                   const float* variance, float* delta, float* scaleUpdates, float* mean_delta,
-                                   float* variance_delta) {
+namespace {
+
+// tnh_bn_backward with the layer's incoming delta taken from SRC (see
+// BnBackOpT); w is the row width for kFromMaxPool2.
+template <int SRC>
+int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups, int64_t w, const int64_t* pidx,
+                     const float* pdel, const float* output, int32_t act, const float* xNorm, const float* x,
+                     const float* scales, const float* mean, const float* variance, float* delta,
+                     float* scaleUpdates, float* mean_delta, float* variance_delta) {
   TNH_REQUIRE_CTX(cx);
-  TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "bn_backward: bad sizes");
+  TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "%s: bad sizes", who);
   TNH_ARG(output && xNorm && x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
-          "bn_backward: NULL buffer");
-  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_backward: activation %d", act);
+          "%s: NULL buffer", who);
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "%s: activation %d", who, act);
   const int64_t block = N / (dstSize * groups);
-  TNH_ARG(block * dstSize * groups == N, "bn_backward: sizes do not align");
+  TNH_ARG(block * dstSize * groups == N, "%s: sizes do not align", who);
   ChanSplit s;
   float* red = nullptr;
   // three partials per workgroup slot: the dgamma dots after the two
   // mean / variance delta sums
   if (int st = chan_split(s, red, dstSize, block, groups, 3, cx)) return st;
   float* dotPart = red + 2 * dstSize * s.P;
-  if (int st = launch_partial<1>(cx, BnBackOp{delta, output, xNorm, scales, act, 0.f}, s,
-                                 chan_vec(s, {delta, output, xNorm}), dotPart, "chan_partial_kernel<bn_back>"))
+  BnBackOpT<SRC> op{delta, output, xNorm, scales, act, 0.f};
+  op.pidx = pidx;
+  op.pdel = pdel;
+  op.block = static_cast<uint32_t>(block);
+  op.w = static_cast<uint32_t>(w);
+  if (int st = launch_partial<1>(cx, op, s, chan_vec(s, {delta, output, xNorm}), dotPart,
+                                 "chan_partial_kernel<bn_back>"))
     return st;
   if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
                                  "chan_partial_kernel<mean_var_delta>",
                                  BnBackFin{MvdFin{red, variance, mean_delta, variance_delta}, dotPart, scaleUpdates}))
     return st;
   return tnh_normalize_delta(N, dstSize, groups, delta, x, 0, mean, variance, mean_delta, variance_delta);
+}
+
+}  // namespace
+
+extern "C" int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups, const float* output, int32_t act,
+                                   const float* xNorm, const float* x, const float* scales, const float* mean,
+                                   const float* variance, float* delta, float* scaleUpdates, float* mean_delta,
+                                   float* variance_delta) {
+  return bn_backward_impl<kFromDelta>("bn_backward", N, dstSize, groups, 0, nullptr, nullptr, output, act, xNorm, x,
+                                      scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta);
+}
+
+extern "C" int32_t tnh_bn_backward_maxpool(int64_t N, int64_t dstSize, int64_t groups, int64_t h, int64_t w,
+                                           const int64_t* poolIndexes, const float* poolDelta, const float* output,
+                                           int32_t act, const float* xNorm, const float* x, const float* scales,
+                                           const float* mean, const float* variance, float* delta,
+                                           float* scaleUpdates, float* mean_delta, float* variance_delta) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(h > 0 && w > 0 && h % 2 == 0 && w % 2 == 0 && groups > 0 && dstSize > 0 && N == groups * dstSize * h * w &&
+              N < (int64_t(1) << 31),
+          "bn_backward_maxpool: sizes (even h and w, N = groups * dstSize * h * w < 2^31)");
+  TNH_ARG(poolIndexes && poolDelta, "bn_backward_maxpool: NULL buffer");
+  // each index must name an element of its own window: only indexes that
+  // a 2x2 stride-2 pool over exactly this input wrote qualify
+  TNH_ARG(pool_is_2x2(poolIndexes, groups, dstSize, h, w),
+          "bn_backward_maxpool: the indexes were not written by a 2x2 stride-2 maxpool of this geometry");
+  return bn_backward_impl<kFromMaxPool2>("bn_backward_maxpool", N, dstSize, groups, w, poolIndexes, poolDelta, output,
+                                         act, xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
+                                         variance_delta);
+}
+
+extern "C" int32_t tnh_bn_backward_avgpool(int64_t N, int64_t dstSize, int64_t groups, const float* avgDelta,
+                                           const float* output, int32_t act, const float* xNorm, const float* x,
+                                           const float* scales, const float* mean, const float* variance,
+                                           float* delta, float* scaleUpdates, float* mean_delta,
+                                           float* variance_delta) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(N > 0 && N < (int64_t(1) << 31), "bn_backward_avgpool: 0 < N < 2^31");
+  TNH_ARG(avgDelta, "bn_backward_avgpool: NULL buffer");
+  return bn_backward_impl<kFromAvgPool>("bn_backward_avgpool", N, dstSize, groups, 0, nullptr, avgDelta, output, act,
+                                        xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
+                                        variance_delta);
 }
 
 extern "C" int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw, int64_t classes, const float* x,
@@ -1430,13 +1532,15 @@ extern "C" int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(batch > 0 && F > 0 && hw > 0 && classes > 0 && F <= 8192 && classes <= 1024 && batch < (int64_t(1) << 31),
           "softmax_head_forward: bad sizes");
-  TNH_ARG(x && avg && weights && biases && truth && logits && prob && delta && error,
-          "softmax_head_forward: NULL buffer");
+  TNH_ARG(avg && weights && biases && truth && logits && prob && delta && error, "softmax_head_forward: NULL buffer");
   // the average pool as tnh_avgpool_fwd runs it (a wave per plane: more
-  // parallel than a workgroup per image), then the rest per image
-  hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(static_cast<unsigned>((batch * F + 3) / 4)), dim3(256), 0, cx->stream,
-                     x, batch * F, hw, avg);
-  if (int st = launch_status("avgpool_fwd_kernel")) return st;
+  // parallel than a workgroup per image), then the rest per image; x NULL:
+  // avg holds the averages already (tnh_bn_forward_avgpool)
+  if (x) {
+    hipLaunchKernelGGL(avgpool_fwd_kernel, dim3(static_cast<unsigned>((batch * F + 3) / 4)), dim3(256), 0,
+                       cx->stream, x, batch * F, hw, avg);
+    if (int st = launch_status("avgpool_fwd_kernel")) return st;
+  }
   const bool stageW = classes * F <= 8192;  // up to 32 KB of weights in LDS
   const size_t lds = static_cast<size_t>(F + classes + (stageW ? classes * F : 0)) * 4;
   hipLaunchKernelGGL(softmax_head_fwd_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), lds, cx->stream, F, hw,
@@ -1452,8 +1556,7 @@ extern "C" int32_t tnh_softmax_head_backward(int64_t batch, int64_t F, int64_t h
   TNH_ARG(batch > 0 && F > 0 && hw > 0 && classes > 0 && F <= 8192 && classes <= 1024 &&
               batch + classes < (int64_t(1) << 31),
           "softmax_head_backward: bad sizes");
-  TNH_ARG(delta && avg && weights && weightUpdates && biasUpdates && avgDelta && deltaIn,
-          "softmax_head_backward: NULL buffer");
+  TNH_ARG(delta && avg && weights && weightUpdates && biasUpdates && avgDelta, "softmax_head_backward: NULL buffer");
   const size_t lds = static_cast<size_t>(F + classes) * 4;
   hipLaunchKernelGGL(softmax_head_bwd_kernel, dim3(static_cast<unsigned>(batch + classes)), dim3(256), lds,
                      cx->stream, batch, F, hw, classes, clampAlpha, delta, avg, weights, weightUpdates, biasUpdates,

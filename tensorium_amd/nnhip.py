@@ -123,6 +123,7 @@ _PROTOS = {
     "tnh_forward_scale_add": [i64, vp, i64, i64, vp, vp, i64, i64],
     "tnh_bn_forward": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32],
     "tnh_bn_forward_maxpool": [i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp],
+    "tnh_bn_forward_avgpool": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32, vp],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
     "tnh_yolo_detections": [i64, i32, C.POINTER(vp), C.POINTER(i64), i64, i64, C.POINTER(f32), i64, i64, i64, i64,
                             f32, i32, i32, i64, vp, vp, vp, vp],
@@ -131,6 +132,8 @@ _PROTOS = {
     "tnh_means": [i64, i64, i64, vp, i64, vp],
     "tnh_bn_backward_scale": [i64, i64, i64, vp, i32, vp, vp, vp, vp],
     "tnh_bn_backward": [i64, i64, i64, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_bn_backward_maxpool": [i64, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_bn_backward_avgpool": [i64, i64, i64, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "tnh_variances": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -563,6 +566,11 @@ class TNNHip:
         """TNNCuda.forwardScaleAdd (nncuda.pas:1490): dst = fl(scale*dst) + bias."""
         call("tnh_forward_scale_add", dstSize, addr(dst), offset, scaleSize, addr(scales), addr(biases), incb, batch)
 
+    def bnForwardAvgPool(self, batch, N, hw, x, xNorm, out, mean, variance, scales, biases, activation, avg):
+        """bnForward then avgPoolForward of its output (planes of hw <= 64), one pass."""
+        call("tnh_bn_forward_avgpool", batch, N, hw, addr(x), addr(xNorm), addr(out), addr(mean), addr(variance),
+             addr(scales), addr(biases), activation, addr(avg))
+
     def bnForwardMaxPool(self, batch, N, h, w, x, xNorm, out, mean, variance, scales, biases, activation, pooled,
                          indexes):
         """bnForward then forwardMaxPool (2x2, stride 2) of its output, one pass."""
@@ -601,6 +609,20 @@ class TNNHip:
         call("tnh_bn_backward", N, dstSize, groups, addr(output), activation, addr(xNorm), addr(x), addr(scales),
              addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta), addr(variance_delta))
 
+    def bnBackwardMaxPool(self, N, dstSize, groups, h, w, poolIndexes, poolDelta, output, activation, xNorm, x,
+                          scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta):
+        """backwardMaxPool (2x2, stride 2) into a zeroed delta, then bnBackward; delta is written in full."""
+        call("tnh_bn_backward_maxpool", N, dstSize, groups, h, w, addr(poolIndexes), addr(poolDelta), addr(output),
+             activation, addr(xNorm), addr(x), addr(scales), addr(mean), addr(variance), addr(delta),
+             addr(scaleUpdates), addr(mean_delta), addr(variance_delta))
+
+    def bnBackwardAvgPool(self, N, dstSize, groups, avgDelta, output, activation, xNorm, x, scales, mean, variance,
+                          delta, scaleUpdates, mean_delta, variance_delta):
+        """avgPoolBackward into a zeroed delta, then bnBackward; delta is written in full."""
+        call("tnh_bn_backward_avgpool", N, dstSize, groups, addr(avgDelta), addr(output), activation, addr(xNorm),
+             addr(x), addr(scales), addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta),
+             addr(variance_delta))
+
     def bnBackwardScale(self, N, dstSize, groups, output, activation, xNorm, scales, delta, scaleUpdates):
         """DeriveArray + addDots + forwardScale of batchNormBack in one pass
         (tnh_bn_backward_scale)."""
@@ -630,7 +652,7 @@ class TNNHip:
 
     def softmaxHeadForward(self, batch, F, hw, classes, x, avg, weights, biases, truth, logits, prob, delta,
                            error):
-        """avgpool + connected + softmax + cross-entropy forward in one launch."""
+        """avgpool + connected + softmax + cross-entropy forward in two launches (x None: avg is filled)."""
         call("tnh_softmax_head_forward", batch, F, hw, classes, addr(x), addr(avg), addr(weights), addr(biases),
              addr(truth), addr(logits), addr(prob), addr(delta), addr(error))
 

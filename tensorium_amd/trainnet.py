@@ -67,7 +67,7 @@ class CifarTrainer:
     backward and update on the device; `cost()` reads the loss back."""
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
-                 fused_wgrad=True, conv_dgrad=True, fused_head=True):
+                 fused_wgrad=True, conv_dgrad=True, fused_head=True, fused_pool_bwd=True):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
         im2col + NT product (the same bits).  conv_dgrad: the conv input
@@ -75,11 +75,15 @@ class CifarTrainer:
         weights; False runs the reference's TN product + col2im (the same
         sums in another order).  fused_head: the average pool, the connected
         layer, softmax and cross-entropy forward in one launch and their
-        backward in another; False runs them call by call."""
+        backward in another; False runs them call by call.  fused_pool_bwd:
+        the pool layers' backwards are formed inside the batch-norm backward
+        below them (no zeroed delta, no scatter launch; the same bits);
+        False runs backwardMaxPool / avgPoolBackward into zeroed deltas."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
         self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
+        self.fused_pool_bwd = fused_pool_bwd
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -191,6 +195,11 @@ class CifarTrainer:
                 hip.bnForwardMaxPool(B, f, hh, hh, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"],
                                      acLEAKY, t[f"pool{i}"], t[f"pidx{i}"])
                 h = t[f"pool{i}"]
+            elif self.fused_head and hh * hh <= 64:
+                # ... and the average of each plane (the head's average pool)
+                hip.bnForwardAvgPool(B, f, hh * hh, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"],
+                                     acLEAKY, t["avg"])
+                h = None
             else:
                 hip.bnForward(n, f, B, y, xn, out, t[f"mean{i}"], t[f"var{i}"], p[f"s{i}"], p[f"b{i}"], acLEAKY)
                 h = out
@@ -213,21 +222,27 @@ class CifarTrainer:
         hip, p, t, B = self.hip, self.p, self.t, self.B
         F, hw = BLOCKS[-1][1], self.final_hw
         nfc = B * CLASSES
-        hip.fill(self.zero_arena.numel(), self.zero_arena, 0, 0.0, 1)
+        # pool backwards and col2im accumulate into zeroed deltas; the conv
+        # input deltas and the pool backwards formed in the batch-norm
+        # backward write every element
+        if not (self.fused_pool_bwd and self.conv_dgrad):
+            hip.fill(self.zero_arena.numel(), self.zero_arena, 0, 0.0, 1)
         last = len(self.dims) - 1
         d = t[f"delta{last}"]
         if self.fused_head:
-            # connected backward and the avgpool backward into the last
-            # block's zeroed delta, one launch
+            # connected backward (and the avgpool backward into the last
+            # block's zeroed delta unless the batch-norm backward forms it),
+            # one launch
             hip.softmaxHeadBackward(B, F, hw * hw, CLASSES, 1.0, t["fc_delta"], t["avg"], p["fw"], p["u_fw"],
-                                    p["u_fb"], t["avg_delta"], d)
+                                    p["u_fb"], t["avg_delta"], None if self.fused_pool_bwd else d)
         else:
             hip.clamp(nfc, 1.0, t["fc_delta"], t["fc_delta"])
             hip.backwardBias(CLASSES, p["u_fb"], nfc, t["fc_delta"], 0, 1, B)
             hip.gemm(True, False, CLASSES, F, B, 1.0, t["fc_delta"], 0, CLASSES, t["avg"], 0, F, 1.0, p["u_fw"], 0, F)
             hip.gemm(False, False, B, F, CLASSES, 1.0, t["fc_delta"], 0, CLASSES, p["fw"], 0, F, 0.0, t["avg_delta"],
                      0, F)
-            hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
+            if not self.fused_pool_bwd:
+                hip.avgPoolBackward(B, F, hw, hw, t["avg_delta"], d)
         col = t["col"]
         for i in range(last, -1, -1):
             c, hh, f = self.dims[i]
@@ -236,8 +251,18 @@ class CifarTrainer:
             # leaky gradient, batchNormBack's dgamma (addDots) and delta *=
             # gamma (forwardScale) in one pass, then the mean / variance
             # deltas and normalizeDelta (four launches)
-            hip.bnBackward(n, f, B, t[f"out{i}"], acLEAKY, t[f"xn{i}"], t[f"x{i}"], p[f"s{i}"], t[f"mean{i}"],
-                           t[f"var{i}"], d, p[f"u_s{i}"], t[f"md{i}"], t[f"vd{i}"])
+            bn = (n, f, B)
+            rest = (t[f"out{i}"], acLEAKY, t[f"xn{i}"], t[f"x{i}"], p[f"s{i}"], t[f"mean{i}"], t[f"var{i}"], d,
+                    p[f"u_s{i}"], t[f"md{i}"], t[f"vd{i}"])
+            if not self.fused_pool_bwd:
+                hip.bnBackward(*bn, *rest)
+            elif i == last:
+                # ... the first pass forming the average pool's backward
+                hip.bnBackwardAvgPool(*bn, t["avg_delta"], *rest)
+            else:
+                # ... the first pass forming the 2x2 maxpool's backward of
+                # the next block's input delta
+                hip.bnBackwardMaxPool(*bn, hh, hh, t[f"pidx{i}"], t[f"dx{i + 1}"], *rest)
             # conv weight gradient: sum_b delta_b * im2col(input_b)^T
             src = self.input if i == 0 else t[f"pool{i - 1}"]
             K, L = c * 9, hh * hh
@@ -260,10 +285,11 @@ class CifarTrainer:
                 hip.gemmStridedBatched(True, False, K, L, f, 1.0, p[f"w{i}"], 0, K, 0, d, 0, L, f * L, 0.0, col, 0,
                                        L, K * L, B)
                 hip.col2imStridedBatched(c, hh, hh, 3, 3, 1, 1, 1, 1, 1, 1, col, K * L, 0, dx, c * hh * hh, 0, B)
-            # maxpool backward into the previous block's zeroed delta
-            pc, phh, pf = self.dims[i - 1]
-            prev = t[f"delta{i - 1}"]
-            hip.backwardMaxPool(B, pf, phh // 2, phh // 2, prev, t[f"pidx{i - 1}"], dx)
+            if not self.fused_pool_bwd:
+                # maxpool backward into the previous block's zeroed delta
+                pc, phh, pf = self.dims[i - 1]
+                prev = t[f"delta{i - 1}"]
+                hip.backwardMaxPool(B, pf, phh // 2, phh // 2, prev, t[f"pidx{i - 1}"], dx)
 
     # -------------------------------------------------------------- update
     def update(self):

@@ -14,7 +14,7 @@ import torch
 from oracle import refcpu as R
 from oracle import trainref as T
 from tensorium_amd import synth, trainnet
-from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -572,6 +572,108 @@ def test_bn_backward_equals_the_sequence(hip, shape, act):
         assert np.array_equal(a, b)
 
 
+def _bn_back_inputs(shape, seed):
+    B, F, h, w = shape
+    out = synth.normal(seed, shape)
+    xn = synth.normal(seed + 1, shape)
+    x = synth.normal(seed + 2, shape)
+    gamma = synth.normal(seed + 3, (F,))
+    mean = synth.normal(seed + 4, (F,), 0.1)
+    var = np.abs(synth.normal(seed + 5, (F,))) + np.float32(0.5)
+    return [D(a) for a in (out, xn, x, gamma, mean, var)], synth.normal(seed + 6, (F,))
+
+
+@pytest.mark.parametrize("shape,act", [((128, 32, 32, 32), acLEAKY), ((4, 3, 6, 6), acLINEAR),
+                                       ((2, 5, 4, 8), acLEAKY), ((3, 2, 2, 2), acLEAKY)])
+def test_bn_backward_maxpool_equals_the_calls(hip, shape, act):
+    """tnh_bn_backward_maxpool against tnh_maxpool_bwd into a zeroed delta
+    then tnh_bn_backward: delta, dgamma and the mean / variance deltas bit
+    for bit, with ties in the windows and +0 / -0 pool deltas; the fused
+    call does not read its delta (NaN before); indexes it did not see a
+    2x2 stride-2 pool write are refused."""
+    case(f"bn_backward_maxpool {shape} act{act}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    src = synth.normal(390, shape)
+    src[0, 0, 0, :2] = src[0, 0, 1, :2] = 0.25  # a tie inside the first window
+    pidx = torch.empty((B, F, h // 2, w // 2), dtype=torch.int64, device="cuda")
+    pooled = torch.empty((B, F, h // 2, w // 2), dtype=torch.float32, device="cuda")
+    hip.forwardMaxPool(B, F, h // 2, w // 2, D(src), F, h, w, 2, 2, 0, 2, pidx, pooled)
+    pdel = synth.normal(391, (B, F, h // 2, w // 2))
+    pdel.reshape(-1)[::7] = np.float32(-0.0)
+    pdel.reshape(-1)[3::11] = np.float32(0.0)
+    (out, xn, x, gamma, mean, var), su0 = _bn_back_inputs(shape, 392)
+    res = []
+    for fused in (True, False):
+        su = D(su0)
+        md = torch.empty(F, dtype=torch.float32, device="cuda")
+        vd = torch.empty(F, dtype=torch.float32, device="cuda")
+        if fused:
+            d = torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+            hip.bnBackwardMaxPool(n, F, B, h, w, pidx, D(pdel), out, act, xn, x, gamma, mean, var, d, su, md, vd)
+        else:
+            d = torch.zeros(shape, dtype=torch.float32, device="cuda")
+            hip.backwardMaxPool(B, F, h // 2, w // 2, d, pidx, D(pdel))
+            hip.bnBackward(n, F, B, out, act, xn, x, gamma, mean, var, d, su, md, vd)
+        res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
+    for a, b in zip(*res):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # an address no pool wrote (8 bytes past an allocation's start)
+    other = torch.zeros(pidx.numel() + 1, dtype=torch.int64, device="cuda")[1:]
+    with pytest.raises(TNHError, match="2x2"):
+        hip.bnBackwardMaxPool(n, F, B, h, w, other, D(pdel), out, act, xn, x, gamma, mean, var, d, su, md, vd)
+
+
+@pytest.mark.parametrize("shape,act", [((128, 128, 8, 8), acLEAKY), ((3, 5, 3, 3), acLINEAR),
+                                       ((2, 4, 1, 1), acLEAKY)])
+def test_bn_backward_avgpool_equals_the_calls(hip, shape, act):
+    """tnh_bn_backward_avgpool against tnh_avgpool_bwd into a zeroed delta
+    then tnh_bn_backward, bit for bit (-0 pool deltas included); the fused
+    call does not read its delta."""
+    case(f"bn_backward_avgpool {shape} act{act}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    adel = synth.normal(395, (B, F))
+    adel.reshape(-1)[::5] = np.float32(-0.0)
+    (out, xn, x, gamma, mean, var), su0 = _bn_back_inputs(shape, 396)
+    res = []
+    for fused in (True, False):
+        su = D(su0)
+        md = torch.empty(F, dtype=torch.float32, device="cuda")
+        vd = torch.empty(F, dtype=torch.float32, device="cuda")
+        if fused:
+            d = torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+            hip.bnBackwardAvgPool(n, F, B, D(adel), out, act, xn, x, gamma, mean, var, d, su, md, vd)
+        else:
+            d = torch.zeros(shape, dtype=torch.float32, device="cuda")
+            hip.avgPoolBackward(B, F, h, w, D(adel), d)
+            hip.bnBackward(n, F, B, out, act, xn, x, gamma, mean, var, d, su, md, vd)
+        res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
+    for a, b in zip(*res):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_cifar_step_fused_pool_bwd_equals_the_calls(hip):
+    """The training step with the pool backwards formed inside the
+    batch-norm backwards (no zeroed deltas) gives the same bits as with
+    backwardMaxPool / avgPoolBackward into zeroed deltas, with the fused
+    tail and with the call-by-call tail."""
+    case("cifar step fused pool backward vs calls")
+    params = trainnet.init_params()
+    x, truth = _batch(323, 16)
+    keys = ("u_w0", "u_w1", "u_w2", "u_s0", "u_s1", "u_s2", "w0", "w1", "w2", "u_fw", "u_fb")
+    for head in (True, False):
+        out = []
+        for fused in (True, False):
+            gpu = trainnet.CifarTrainer(hip, params, 16, fused_head=head, fused_pool_bwd=fused)
+            gpu.forward(D(x), D(truth))
+            gpu.backward()
+            gpu.update()
+            out.append({k: gpu.host(k).copy() for k in keys})
+        for k in keys:
+            assert np.array_equal(out[0][k], out[1][k]), (head, k)
+
+
 def test_sgd_update_pack_equals_update_then_pack(hip):
     """tnh_sgd_update_pack: the weights and momenta of tnh_sgd_update bit for
     bit, and each listed layer's tap-major / flipped copies equal to
@@ -644,6 +746,37 @@ def test_bn_forward_maxpool_equals_the_two_calls(hip, shape, act, idx):
         db = D(base)
         hip.backwardMaxPool(B, F, h // 2, w // 2, db, pidx, D(delta))
         assert np.array_equal(H(db, hip), ref)
+
+
+@pytest.mark.parametrize("shape", [(128, 128, 8, 8), (3, 5, 4, 4), (2, 7, 1, 1), (4, 3, 3, 5)])
+@pytest.mark.parametrize("act", [acLEAKY, acLINEAR])
+def test_bn_forward_avgpool_equals_the_two_calls(hip, shape, act):
+    """tnh_bn_forward_avgpool against tnh_bn_forward then tnh_avgpool_fwd:
+    x_norm, out and the plane averages bit for bit (planes of one element
+    take the other variance clamp, as tnh_bn_forward does)."""
+    case(f"bn_forward_avgpool {shape} act{act}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    x = synth.normal(380, shape)
+    mean, var = synth.normal(381, (F,), 0.1), np.abs(synth.normal(382, (F,))) + np.float32(0.5)
+    var[0] = np.float32(1e-13)  # below the clamps: the two forms differ here
+    gamma, beta = synth.normal(383, (F,)), synth.normal(384, (F,))
+    res = []
+    for fused in (True, False):
+        xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        avg = torch.empty((B, F), dtype=torch.float32, device="cuda")
+        if fused:
+            hip.bnForwardAvgPool(B, F, h * w, D(x), xn, out, D(mean), D(var), D(gamma), D(beta), act, avg)
+        else:
+            hip.bnForward(n, F, B, D(x), xn, out, D(mean), D(var), D(gamma), D(beta), act)
+            hip.avgPoolForward(B, F, h, w, out, avg)
+        res.append([H(t_, hip).copy() for t_ in (xn, out, avg)])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+    # the averages against a float64 mean, within rounding
+    ref = res[1][1].reshape(B * F, h * w).astype(np.float64).mean(axis=1).reshape(B, F)
+    assert np.abs(res[0][2] - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
 @pytest.mark.parametrize("B,F,hw,classes", [(128, 128, 64, 10), (5, 37, 9, 3)])
