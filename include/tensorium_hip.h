@@ -538,6 +538,26 @@ int32_t tnh_bn_forward_avgpool(int64_t batch, int64_t N, int64_t hw,
                                const float *mean, const float *variance,
                                const float *scales, const float *biases,
                                int32_t act, float *avg);
+/* No reference counterpart: tnh_bn_statistics (batch statistics and the
+ * rolling update) followed by tnh_bn_forward_maxpool, in three launches
+ * instead of four and bit for bit: the statistics' final step is taken by
+ * the normalize pass itself.  rollMean / rollVar may both be NULL. */
+int32_t tnh_bn_train_forward_maxpool(int64_t batch, int64_t N, int64_t h,
+                                     int64_t w, const float *x, float *xNorm,
+                                     float *out, float *mean, float *variance,
+                                     float *rollMean, float *rollVar,
+                                     float momentum, const float *scales,
+                                     const float *biases, int32_t act,
+                                     float *pooled, int64_t *indexes);
+/* No reference counterpart: tnh_bn_statistics followed by
+ * tnh_bn_forward_avgpool (hw <= 64), in three launches, bit for bit. */
+int32_t tnh_bn_train_forward_avgpool(int64_t batch, int64_t N, int64_t hw,
+                                     const float *x, float *xNorm, float *out,
+                                     float *mean, float *variance,
+                                     float *rollMean, float *rollVar,
+                                     float momentum, const float *scales,
+                                     const float *biases, int32_t act,
+                                     float *avg);
 
 /* ---- the element-wise methods of TNNCuda for the layers around the
  *      convolution path (LRN, logistic / L2 cost, dropout, swish, a yolo
@@ -658,12 +678,14 @@ int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
                               const float *xNorm, const float *scales,
                               float *delta, float *scaleUpdates);
 /* No reference counterpart: batchNormBackGPU (nbaselayer.pas:662-712) with
- * the layer's activation derivative before it, in four launches instead of
+ * the layer's activation derivative before it, in three launches instead of
  * six: tnh_bn_backward_scale's pass (delta *= act'(output), scaleUpdates +=
- * sum x_norm*delta, delta *= scales), tnh_means_vars_delta's sums, the two
- * final steps in one launch, then tnh_normalize_delta.  The same operations
- * in the same order as those four calls, so the same bits; x is the
- * pre-normalization output, mean / variance the forward's statistics. */
+ * sum x_norm*delta, delta *= scales), tnh_means_vars_delta's sums, then
+ * tnh_normalize_delta with the mean / variance deltas and the dgamma total
+ * formed inside it (four launches when a workgroup would hold more than 16
+ * channel rows).  The same operations in the same order as those calls, so
+ * the same bits; x is the pre-normalization output, mean / variance the
+ * forward's statistics. */
 int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
                         const float *output, int32_t act, const float *xNorm,
                         const float *x, const float *scales, const float *mean,

@@ -162,6 +162,12 @@ function tnh_bn_forward_maxpool(batch, N, h, w: Int64; x, xNorm, output, mean, v
   act: LongInt; pooled: PSingle; indexes: PInt64): LongInt; cdecl; external libtnh;
 function tnh_bn_forward_avgpool(batch, N, hw: Int64; x, xNorm, output, mean, variance, scales, biases: PSingle;
   act: LongInt; avg: PSingle): LongInt; cdecl; external libtnh;
+function tnh_bn_train_forward_maxpool(batch, N, h, w: Int64; x, xNorm, output, mean, variance, rollMean,
+  rollVar: PSingle; momentum: Single; scales, biases: PSingle; act: LongInt; pooled: PSingle;
+  indexes: PInt64): LongInt; cdecl; external libtnh;
+function tnh_bn_train_forward_avgpool(batch, N, hw: Int64; x, xNorm, output, mean, variance, rollMean,
+  rollVar: PSingle; momentum: Single; scales, biases: PSingle; act: LongInt; avg: PSingle): LongInt; cdecl;
+  external libtnh;
 function tnh_means_vars(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -393,6 +399,13 @@ type
     // bnForward, then the average of each output plane (hw <= 64), in one pass
     procedure bnForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance, scales,
       biases: TCUMem; const activation: longint; const avg: TCUMem);
+    // bnStatistics then bnForwardMaxPool / bnForwardAvgPool, three launches each
+    procedure bnTrainForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance, rollMean,
+      rollVar: TCUMem; const momentum: T; const scales, biases: TCUMem; const activation: longint;
+      const pooled, indexes: TCUMem);
+    procedure bnTrainForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance, rollMean,
+      rollVar: TCUMem; const momentum: T; const scales, biases: TCUMem; const activation: longint;
+      const avg: TCUMem);
     procedure bnStatistics(const srcSize, dstSize, groups: SizeInt; const src: TCUMem; const offset: SizeInt;
       means, vars, rollingMeans, rollingVars: TCUMem; const momentum: T);
     // DeriveArray + addDots + forwardScale of batchNormBack in one pass
@@ -919,6 +932,24 @@ procedure TNNHip<T>.softmaxHeadBackward(const batch, F, hw, classes: SizeInt; co
 begin
   check(tnh_softmax_head_backward(batch, F, hw, classes, S(clampAlpha), PSingle(delta), PSingle(avg),
     PSingle(weights), PSingle(weightUpdates), PSingle(biasUpdates), PSingle(avgDelta), PSingle(deltaIn)));
+end;
+
+procedure TNNHip<T>.bnTrainForwardMaxPool(const batch, N, h, w: SizeInt; const x, xNorm, output, mean, variance,
+  rollMean, rollVar: TCUMem; const momentum: T; const scales, biases: TCUMem; const activation: longint;
+  const pooled, indexes: TCUMem);
+begin
+  check(tnh_bn_train_forward_maxpool(batch, N, h, w, PSingle(x), PSingle(xNorm), PSingle(output), PSingle(mean),
+    PSingle(variance), PSingle(rollMean), PSingle(rollVar), momentum, PSingle(scales), PSingle(biases), activation,
+    PSingle(pooled), PInt64(indexes)));
+end;
+
+procedure TNNHip<T>.bnTrainForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance,
+  rollMean, rollVar: TCUMem; const momentum: T; const scales, biases: TCUMem; const activation: longint;
+  const avg: TCUMem);
+begin
+  check(tnh_bn_train_forward_avgpool(batch, N, hw, PSingle(x), PSingle(xNorm), PSingle(output), PSingle(mean),
+    PSingle(variance), PSingle(rollMean), PSingle(rollVar), momentum, PSingle(scales), PSingle(biases), activation,
+    PSingle(avg)));
 end;
 
 procedure TNNHip<T>.bnForwardAvgPool(const batch, N, hw: SizeInt; const x, xNorm, output, mean, variance, scales,

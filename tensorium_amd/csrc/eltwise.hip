@@ -5,6 +5,7 @@
 // flat passes use 16-byte accesses when the buffers allow.
 #include <cfloat>
 
+#include "chanstat.hpp"
 #include "common.hpp"
 #include "rows.hpp"
 #include "yolo_math.hpp"
@@ -93,8 +94,7 @@ struct NormOp {
   int64_t vs;
   int clampVar;
   struct Ch { float m, d; };
-  __device__ Ch chan(int64_t f) const {
-    const float var = v[f * vs];
+  __device__ Ch make(float mean, float var) const {
     float d;
     if (clampVar) {
       d = sqrtf(var > 1e-6f ? var : 1e-6f);
@@ -102,8 +102,9 @@ struct NormOp {
       d = sqrtf(var);
       d = d > 1e-6f ? d : 1e-6f;
     }
-    return {m[f * ms], d};
+    return {mean, d};
   }
+  __device__ Ch chan(int64_t f) const { return make(m[f * ms], v[f * vs]); }
   __device__ float operator()(const Ch& c, float x) const {
     const float t = x - c.m;
     return t / c.d;
@@ -156,18 +157,63 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_kernel(NormOp norm, ScaleAddO
 // bn_fwd_kernel does, then the two windows' max and global int64 index
 // exactly as the maxpool kernels scan them (rows, then columns, strict '>'
 // from -MaxSingle).  W % 4 == 0, H and W even, 16-byte aligned tensors.
-template <int ACT>
+// STATS: the batch statistics' final step is taken here (tnh_bn_statistics'
+// partials in sp, P <= 64): the workgroup forms the mean and variance of the
+// planes its threads touch (at most kStatPlanes; one unit per thread, grid
+// = total / kThreads), the one holding a channel's image-0 plane stores
+// them.
+constexpr int kStatPlanes = 64;
+template <int ACT, bool STATS>
 __global__ __launch_bounds__(kThreads) void bn_fwd_pool2_kernel(NormOp norm, ScaleAddOp sa, int64_t total, int64_t C,
                                                                 int64_t H, int64_t W, const float* __restrict__ x,
                                                                 float* __restrict__ xNorm, float* __restrict__ out,
                                                                 float* __restrict__ pooled,
-                                                                int64_t* __restrict__ idx) {
+                                                                int64_t* __restrict__ idx, StatParts sp) {
   const int64_t OH = H / 2, OW2 = W / 4;
+  __shared__ float sM[STATS ? kStatPlanes : 1], sV[STATS ? kStatPlanes : 1];
+  int64_t pA = 0;
+  if constexpr (STATS) {
+    const int64_t u0 = blockIdx.x * int64_t(kThreads);
+    const int64_t upp = OH * OW2;  // units per plane
+    const int64_t u1 = (u0 + kThreads < total ? u0 + kThreads : total) - 1;
+    pA = u0 / upp;
+    const int nP = static_cast<int>(u1 / upp - pA + 1);
+    // wave w takes planes w, w + 4, ...: the loads of up to four, then
+    // their arithmetic
+    constexpr int kW = kThreads / 64;
+    for (int k0 = threadIdx.x >> 6; k0 < nP; k0 += 4 * kW) {
+      float ts[4], tq[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ts[j] = tq[j] = 0.f;
+        const int k = k0 + j * kW;
+        if (k < nP) sp.lanes((pA + k) % C, ts[j], tq[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + j * kW;
+        if (k < nP) {
+          const int64_t plane = pA + k;
+          float m, v;
+          sp.finish_lanes(plane % C, plane < C, ts[j], tq[j], m, v);
+          if ((threadIdx.x & 63) == 0) {
+            sM[k] = m;
+            sV[k] = v;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
   for (int64_t t = blockIdx.x * int64_t(kThreads) + threadIdx.x; t < total; t += int64_t(gridDim.x) * kThreads) {
     const int64_t jp = t % OW2, r = t / OW2;  // r = plane*OH + i
     const int64_t i = r % OH, plane = r / OH;
     const int64_t f = plane % C;
-    const NormOp::Ch cn = norm.chan(f);
+    NormOp::Ch cn;
+    if constexpr (STATS)
+      cn = norm.make(sM[plane - pA], sV[plane - pA]);
+    else
+      cn = norm.chan(f);
     const ScaleAddOp::Ch cs = sa.chan(f);
     const int64_t x0 = 4 * jp;
     const int64_t row0 = (plane * H + 2 * i) * W;
@@ -217,22 +263,33 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_pool2_kernel(NormOp norm, Sca
 // conv block of a classifier before its average pool): one wave per
 // (image, channel) plane of hw <= 64 elements, one element per lane, the
 // plane's x_norm and out written as bn_fwd_kernel writes them, then
-// avgpool_fwd_kernel's wave tree over the out values.
-template <int ACT>
+// avgpool_fwd_kernel's wave tree over the out values.  STATS: each wave
+// forms its plane's mean and variance from the statistics' partials (the
+// final step, stored by the channel's image-0 plane).
+template <int ACT, bool STATS>
 __global__ __launch_bounds__(kThreads) void bn_fwd_avg_kernel(NormOp norm, ScaleAddOp sa, int64_t planes, int64_t C,
                                                               int64_t hw, const float* __restrict__ x,
                                                               float* __restrict__ xNorm, float* __restrict__ out,
-                                                              float* __restrict__ avg) {
+                                                              float* __restrict__ avg, StatParts sp) {
   const int lane = threadIdx.x & 63;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
   if (r >= planes) return;  // whole waves
   const int64_t f = r % C;
-  const NormOp::Ch cn = norm.chan(f);
+  const float xe = lane < hw ? x[r * hw + lane] : 0.f;
+  NormOp::Ch cn;
+  if constexpr (STATS) {  // P <= 64
+    float ts, tq, m, v;
+    sp.lanes(f, ts, tq);
+    sp.finish_lanes(f, r < C, ts, tq, m, v);
+    cn = norm.make(m, v);
+  } else {
+    cn = norm.chan(f);
+  }
   const ScaleAddOp::Ch cs = sa.chan(f);
   float s = 0.f;
   if (lane < hw) {
     const int64_t e = r * hw + lane;
-    const float n = norm(cn, x[e]);
+    const float n = norm(cn, xe);
     if (xNorm) xNorm[e] = n;
     const float o = act_fwd(sa(cs, n), ACT);
     out[e] = o;
@@ -674,57 +731,130 @@ extern "C" int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch, con
   return launch_status("bn_fwd_kernel");
 }
 
-extern "C" int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,
-                                          float* xNorm, float* out, const float* mean, const float* variance,
-                                          const float* scales, const float* biases, int32_t act, float* pooled,
-                                          int64_t* indexes) {
+namespace {
+
+// tnh_bn_forward_maxpool; sp non-NULL: the statistics' final step in the
+// same launch (the caller launched their partials)
+int bn_forward_maxpool_impl(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,
+                            float* xNorm, float* out, const float* mean, const float* variance, const float* scales,
+                            const float* biases, int32_t act, float* pooled, int64_t* indexes, const StatParts* sp) {
   TNH_REQUIRE_CTX(cx);
-  TNH_ARG(batch > 0 && N > 0 && h > 0 && w > 0, "bn_forward_maxpool: bad sizes");
-  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_forward_maxpool: activation %d",
-          act);
-  TNH_ARG(x && out && mean && variance && scales && biases && pooled, "bn_forward_maxpool: NULL buffer");
-  TNH_ARG(h % 2 == 0 && w % 4 == 0 && al16(x) && al16(out) && (!xNorm || al16(xNorm)) &&
-              (reinterpret_cast<uintptr_t>(pooled) & 7) == 0 && (!indexes || al16(indexes)),
-          "bn_forward_maxpool: needs even h, w %% 4 == 0 and aligned tensors");
   const int64_t total = batch * N * (h / 2) * (w / 4);  // (plane, output row, pair of output columns)
   const NormOp norm{mean, 1, variance, 1, h * w == 1};
   const ScaleAddOp sa{scales, biases, 1};
   const int64_t blocks = (total + kThreads - 1) / kThreads;
-  const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
-  if (act == TNH_AC_LEAKY)
-    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LEAKY>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N, h,
-                       w, x, xNorm, out, pooled, indexes);
-  else if (act == TNH_AC_LOGISTIC)
-    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LOGISTIC>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N,
-                       h, w, x, xNorm, out, pooled, indexes);
-  else
-    hipLaunchKernelGGL(bn_fwd_pool2_kernel<TNH_AC_LINEAR>, grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N,
-                       h, w, x, xNorm, out, pooled, indexes);
+  const dim3 grid(static_cast<unsigned>(sp ? blocks : (blocks < 65536 ? blocks : 65536)));
+  const StatParts none{};
+  auto go = [&](auto ac, auto st) {
+    constexpr int ACT = decltype(ac)::value;
+    constexpr bool ST = decltype(st)::value;
+    hipLaunchKernelGGL((bn_fwd_pool2_kernel<ACT, ST>), grid, dim3(kThreads), 0, cx->stream, norm, sa, total, N, h, w,
+                       x, xNorm, out, pooled, indexes, sp ? *sp : none);
+  };
+  using L = std::integral_constant<int, TNH_AC_LEAKY>;
+  using G = std::integral_constant<int, TNH_AC_LOGISTIC>;
+  using I = std::integral_constant<int, TNH_AC_LINEAR>;
+  using Y = std::true_type;
+  using Nn = std::false_type;
+  if (sp) {
+    if (act == TNH_AC_LEAKY) go(L{}, Y{}); else if (act == TNH_AC_LOGISTIC) go(G{}, Y{}); else go(I{}, Y{});
+  } else {
+    if (act == TNH_AC_LEAKY) go(L{}, Nn{}); else if (act == TNH_AC_LOGISTIC) go(G{}, Nn{}); else go(I{}, Nn{});
+  }
   if (indexes) pool_remember_2x2(indexes, batch, N, h, w);
   return launch_status("bn_fwd_pool2_kernel");
+}
+
+int bn_forward_avgpool_impl(int64_t batch, int64_t N, int64_t hw, const float* x, float* xNorm, float* out,
+                            const float* mean, const float* variance, const float* scales, const float* biases,
+                            int32_t act, float* avg, const StatParts* sp) {
+  TNH_REQUIRE_CTX(cx);
+  const int64_t planes = batch * N;
+  const NormOp norm{mean, 1, variance, 1, hw == 1};
+  const ScaleAddOp sa{scales, biases, 1};
+  const dim3 grid(static_cast<unsigned>((planes + kThreads / 64 - 1) / (kThreads / 64)));
+  const StatParts none{};
+  auto go = [&](auto ac, auto st) {
+    constexpr int ACT = decltype(ac)::value;
+    constexpr bool ST = decltype(st)::value;
+    hipLaunchKernelGGL((bn_fwd_avg_kernel<ACT, ST>), grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N, hw, x,
+                       xNorm, out, avg, sp ? *sp : none);
+  };
+  using L = std::integral_constant<int, TNH_AC_LEAKY>;
+  using G = std::integral_constant<int, TNH_AC_LOGISTIC>;
+  using I = std::integral_constant<int, TNH_AC_LINEAR>;
+  using Y = std::true_type;
+  using Nn = std::false_type;
+  if (sp) {
+    if (act == TNH_AC_LEAKY) go(L{}, Y{}); else if (act == TNH_AC_LOGISTIC) go(G{}, Y{}); else go(I{}, Y{});
+  } else {
+    if (act == TNH_AC_LEAKY) go(L{}, Nn{}); else if (act == TNH_AC_LOGISTIC) go(G{}, Nn{}); else go(I{}, Nn{});
+  }
+  return launch_status("bn_fwd_avg_kernel");
+}
+
+}  // namespace
+
+#define BN_POOL2_CHECKS(who)                                                                                         \
+  TNH_ARG(batch > 0 && N > 0 && h > 0 && w > 0, who ": bad sizes");                                                  \
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, who ": activation %d", act);        \
+  TNH_ARG(x && out && mean && variance && scales && biases && pooled, who ": NULL buffer");                          \
+  TNH_ARG(h % 2 == 0 && w % 4 == 0 && al16(x) && al16(out) && (!xNorm || al16(xNorm)) &&                             \
+              (reinterpret_cast<uintptr_t>(pooled) & 7) == 0 && (!indexes || al16(indexes)),                         \
+          who ": needs even h, w %% 4 == 0 and aligned tensors")
+
+#define BN_AVG_CHECKS(who)                                                                                           \
+  TNH_ARG(batch > 0 && N > 0 && hw > 0 && hw <= 64, who ": bad sizes (hw <= 64)");                                   \
+  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, who ": activation %d", act);        \
+  TNH_ARG(x && out && mean && variance && scales && biases && avg, who ": NULL buffer");                             \
+  TNH_ARG(batch * N < (int64_t(1) << 31), who ": too many planes")
+
+extern "C" int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,
+                                          float* xNorm, float* out, const float* mean, const float* variance,
+                                          const float* scales, const float* biases, int32_t act, float* pooled,
+                                          int64_t* indexes) {
+  BN_POOL2_CHECKS("bn_forward_maxpool");
+  return bn_forward_maxpool_impl(batch, N, h, w, x, xNorm, out, mean, variance, scales, biases,
+                                 act, pooled, indexes, nullptr);
 }
 
 extern "C" int32_t tnh_bn_forward_avgpool(int64_t batch, int64_t N, int64_t hw, const float* x, float* xNorm,
                                           float* out, const float* mean, const float* variance, const float* scales,
                                           const float* biases, int32_t act, float* avg) {
-  TNH_REQUIRE_CTX(cx);
-  TNH_ARG(batch > 0 && N > 0 && hw > 0 && hw <= 64, "bn_forward_avgpool: bad sizes (hw <= 64)");
-  TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "bn_forward_avgpool: activation %d",
-          act);
-  TNH_ARG(x && out && mean && variance && scales && biases && avg, "bn_forward_avgpool: NULL buffer");
-  const int64_t planes = batch * N;
-  TNH_ARG(planes < (int64_t(1) << 31), "bn_forward_avgpool: too many planes");
-  const NormOp norm{mean, 1, variance, 1, hw == 1};
-  const ScaleAddOp sa{scales, biases, 1};
-  const dim3 grid(static_cast<unsigned>((planes + kThreads / 64 - 1) / (kThreads / 64)));
-  if (act == TNH_AC_LEAKY)
-    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LEAKY>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N, hw,
-                       x, xNorm, out, avg);
-  else if (act == TNH_AC_LOGISTIC)
-    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LOGISTIC>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N,
-                       hw, x, xNorm, out, avg);
-  else
-    hipLaunchKernelGGL(bn_fwd_avg_kernel<TNH_AC_LINEAR>, grid, dim3(kThreads), 0, cx->stream, norm, sa, planes, N,
-                       hw, x, xNorm, out, avg);
-  return launch_status("bn_fwd_avg_kernel");
+  BN_AVG_CHECKS("bn_forward_avgpool");
+  return bn_forward_avgpool_impl(batch, N, hw, x, xNorm, out, mean, variance, scales, biases, act, avg, nullptr);
+}
+
+extern "C" int32_t tnh_bn_train_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,
+                                                float* xNorm, float* out, float* mean, float* variance,
+                                                float* rollMean, float* rollVar, float momentum, const float* scales,
+                                                const float* biases, int32_t act, float* pooled, int64_t* indexes) {
+  BN_POOL2_CHECKS("bn_train_forward_maxpool");
+  const int64_t upp = (h / 2) * (w / 4);
+  const int64_t blocks = (batch * N * upp + kThreads - 1) / kThreads;
+  StatParts sp;
+  if (int st = bn_stat_partials(N, h * w, batch, x, mean, variance, rollMean, rollVar, momentum, sp)) return st;
+  // the planes one workgroup touches must fit its table
+  if ((kThreads + upp - 1) / upp + 1 > kStatPlanes || sp.P > 64 || blocks >= (int64_t(1) << 31)) {
+    // ... else the final step in its own launch
+    if (int st = bn_stat_final(N, sp)) return st;
+    return bn_forward_maxpool_impl(batch, N, h, w, x, xNorm, out, mean, variance, scales,
+                                   biases, act, pooled, indexes, nullptr);
+  }
+  return bn_forward_maxpool_impl(batch, N, h, w, x, xNorm, out, mean, variance, scales,
+                                 biases, act, pooled, indexes, &sp);
+}
+
+extern "C" int32_t tnh_bn_train_forward_avgpool(int64_t batch, int64_t N, int64_t hw, const float* x, float* xNorm,
+                                                float* out, float* mean, float* variance, float* rollMean,
+                                                float* rollVar, float momentum, const float* scales,
+                                                const float* biases, int32_t act, float* avg) {
+  BN_AVG_CHECKS("bn_train_forward_avgpool");
+  StatParts sp;
+  if (int st = bn_stat_partials(N, hw, batch, x, mean, variance, rollMean, rollVar, momentum, sp)) return st;
+  if (sp.P > 64) {  // the final step in its own launch
+    if (int st = bn_stat_final(N, sp)) return st;
+    return bn_forward_avgpool_impl(batch, N, hw, x, xNorm, out, mean, variance, scales, biases, act, avg, nullptr);
+  }
+  return bn_forward_avgpool_impl(batch, N, hw, x, xNorm, out, mean, variance, scales, biases, act, avg, &sp);
 }

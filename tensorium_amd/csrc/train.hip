@@ -12,6 +12,7 @@
 #include <initializer_list>
 #include <type_traits>
 
+#include "chanstat.hpp"
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "rows.hpp"
@@ -326,6 +327,7 @@ struct BnBackFin {
   MvdFin mvd;
   const float* dotPart;
   float* scaleUpdates;
+  const double* vpow;  // normalize_delta_fin_kernel: BnBackOpT's Power term
   __device__ void run(int64_t i, const ChanSplit& s, float* sh) const {
     mvd.run(i, s, sh);
     const float t = fixed_total(dotPart + i * s.P, s.P, sh);
@@ -385,7 +387,16 @@ struct BnBackOpT {
   const int64_t* pidx = nullptr;  // kFromMaxPool2: the pool's indexes
   const float* pdel = nullptr;    // the pool layer's delta
   uint32_t block = 0, w = 0;      // plane size and row width (SRC != kFromDelta)
-  __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) { g = gamma[i]; }
+  // non-NULL: the first workgroup of channel i also stores
+  // Power(max(var[i], eps), -3/2) in double for the mean / variance delta
+  // step (the one term of it that does not wait for the delta sums)
+  const float* var = nullptr;
+  double* vpow = nullptr;
+  __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) {
+    g = gamma[i];
+    if (vpow && blockIdx.y == 0 && threadIdx.x == 0)
+      vpow[i] = pow(static_cast<double>(fmaxf(var[i], kEps)), -1.5);
+  }
   // 2x2 window of element e (planes of h x w, h and w even)
   __device__ uint32_t win(uint32_t e) const {
     const uint32_t plane = e / block, r = e - plane * block, y = r / w, x = r - y * w;
@@ -520,6 +531,104 @@ __global__ __launch_bounds__(kRowThreads) void normalize_delta_kernel(float* __r
       }
     }
   });
+}
+
+// The batch-norm backward's last two launches in one: each workgroup first
+// forms the mean / variance deltas of its rows' channels from the MvdOp
+// partials (MvdFin's arithmetic and wave_total's order = that of
+// fixed_total; P <= 64, one partial per lane); the workgroup holding a
+// channel's image-0 row also stores them and adds the channel's dgamma total
+// (BnBackFin).  Then its rows are normalized as normalize_delta_kernel does.
+// One row pass per workgroup (grid = rows / rpw), rpw <= kFinRows.  Each
+// thread loads its first chunk of delta and x before the final steps, so
+// their latency overlaps.
+constexpr int kFinRows = 16;
+template <int VW>
+__global__ __launch_bounds__(kRowThreads) void normalize_delta_fin_kernel(float* __restrict__ delta,
+                                                                          const float* __restrict__ x, Rows g,
+                                                                          float batchSize, const float* mean,
+                                                                          const float* variance, BnBackFin fin,
+                                                                          int P) {
+  using V = typename std::conditional<VW == 4, float4, float>::type;
+  __shared__ float sMd[kFinRows], sVd[kFinRows];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * g.rpw;
+  const int lr = threadIdx.x / g.cpt, lc = threadIdx.x - lr * g.cpt;
+  const bool live = lr < g.rpw && r0 + lr < g.rows;
+  V* dr = reinterpret_cast<V*>(delta + (r0 + lr) * g.block);
+  const V* xr = reinterpret_cast<const V*>(x + (r0 + lr) * g.block);
+  V d0{}, x0{};
+  if (live && lc < g.cpr) {
+    d0 = dr[lc];
+    x0 = xr[lc];
+  }
+  // the final steps: wave w takes rows w, w + 4, ... (at most kFinRows / 4)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int kPer = kFinRows / (kRowThreads / 64);
+  float pm[kPer], pv[kPer], pd[kPer], vc[kPer];
+  double pw[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int row = wv + j * (kRowThreads / 64);
+    const int64_t r = r0 + row;
+    pm[j] = pv[j] = pd[j] = 0.f;
+    vc[j] = 1.f;
+    pw[j] = 1.0;
+    if (row < g.rpw && r < g.rows) {
+      const int64_t i = r % g.nb;
+      if (lane < P) {
+        pm[j] = 0.f + fin.mvd.part[i * P + lane];
+        pv[j] = 0.f + fin.mvd.part[(g.nb + i) * P + lane];
+        if (r < g.nb) pd[j] = 0.f + fin.dotPart[i * P + lane];
+      }
+      vc[j] = fmaxf(variance[i], kEps);
+      pw[j] = fin.vpow[i];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int row = wv + j * (kRowThreads / 64);
+    const int64_t r = r0 + row;
+    if (row < g.rpw && r < g.rows) {  // wave-uniform
+      const int64_t i = r % g.nb;
+      const float m = lane_total(pm[j]);
+      const float v = lane_total(pv[j]);
+      const float md = m * (-1.0f / sqrtf(vc[j]));
+      // Power(max(var, eps), -3/2) in double, the product stored as single
+      const float vd = static_cast<float>(static_cast<double>(v) * -0.5 * pw[j]);
+      if (r < g.nb) {  // image 0's row of channel i: once per channel
+        const float t = lane_total(pd[j]);
+        if (lane == 0) {
+          fin.mvd.mean_delta[i] = md;
+          fin.mvd.variance_delta[i] = vd;
+          fin.scaleUpdates[i] = fin.scaleUpdates[i] + t;
+        }
+      }
+      if (lane == 0) {
+        sMd[row] = md;
+        sVd[row] = vd;
+      }
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  const int64_t i = (r0 + lr) % g.nb;
+  const float md = sMd[lr] / batchSize;
+  const float vd = (2.0f * sVd[lr]) / batchSize;
+  const float sd = sqrtf(fmaxf(variance[i], kEps));
+  const float mu = mean[i];
+  auto one = [&](float d, float xv) {
+    float t = (xv - mu) * vd;
+    t = t + md;
+    return d / sd + t;
+  };
+  auto put = [&](int64_t k, const V& d, const V& xv) {
+    if constexpr (VW == 4)
+      dr[k] = make_float4(one(d.x, xv.x), one(d.y, xv.y), one(d.z, xv.z), one(d.w, xv.w));
+    else
+      dr[k] = one(d, xv);
+  };
+  if (lc < g.cpr) put(lc, d0, x0);
+  for (int64_t k = lc + g.cpt; k < g.cpr; k += g.cpt) put(k, dr[k], xr[k]);
 }
 
 // softmax (nsoftmaxlayer.pas:81-105): one thread per (batch, group) row.
@@ -1056,6 +1165,38 @@ int launch_wgrad_reduce(const WgradArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+namespace {
+__global__ __launch_bounds__(256) void stat_final_kernel(StatParts sp, int64_t C) {
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (f >= C) return;  // whole waves
+  float m, v;
+  sp.finish(f, true, m, v);
+}
+}  // namespace
+
+int bn_stat_final(int64_t C, const StatParts& sp) {
+  TNH_REQUIRE_CTX(cx);
+  hipLaunchKernelGGL(stat_final_kernel, dim3(static_cast<unsigned>((C + 3) / 4)), dim3(256), 0, cx->stream, sp, C);
+  return launch_status("stat_final_kernel");
+}
+
+int bn_stat_partials(int64_t C, int64_t block, int64_t groups, const float* x, float* means, float* vars,
+                     float* rollMean, float* rollVar, float momentum, StatParts& sp) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(C > 0 && groups > 0 && block > 0 && groups * block > 1, "bn statistics: bad sizes");
+  TNH_ARG(x && means && vars, "bn statistics: NULL buffer");
+  TNH_ARG((rollMean == nullptr) == (rollVar == nullptr), "bn statistics: give both rolling buffers or none");
+  ChanSplit s;
+  float* red = nullptr;
+  if (int st = chan_split(s, red, C, block, groups, 2, cx)) return st;
+  const bool vec = chan_vec(s, {x});
+  const float S = static_cast<float>(groups * block);
+  sp = StatParts{red, red + C * s.P, s.P, S, means, vars, rollMean, rollVar, 1.0f - momentum, momentum};
+  if (int st = launch_partial<1>(cx, SumOp{x}, s, vec, red, "chan_partial_kernel<sum>")) return st;
+  return launch_partial<1>(cx, RssOp{x, red, S, 0.f}, s, vec, red + C * s.P, "chan_partial_kernel<rss>");
+}
+
 }  // namespace tnh
 
 using namespace tnh;
@@ -1465,22 +1606,45 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   ChanSplit s;
   float* red = nullptr;
   // three partials per workgroup slot: the dgamma dots after the two
-  // mean / variance delta sums
-  if (int st = chan_split(s, red, dstSize, block, groups, 3, cx)) return st;
+  // mean / variance delta sums; then (8-byte aligned) a double per channel
+  if (int st = chan_split(s, red, dstSize, block, groups, 6, cx)) return st;
   float* dotPart = red + 2 * dstSize * s.P;
+  double* vpow = reinterpret_cast<double*>(red + ((3 * dstSize * s.P + 1) & ~int64_t(1)));
+  const BnBackFin fin{MvdFin{red, variance, mean_delta, variance_delta}, dotPart, scaleUpdates, vpow};
+  const bool v4 = block % 4 == 0 && rows_al16(delta) && rows_al16(x);
+  const Rows g = make_rows(N, block, dstSize, v4 ? 4 : 1);
+  const int64_t wgs = (g.rows + g.rpw - 1) / g.rpw;
+  // many short rows (or P > 64): the finals in their own launch
+  const bool fused = g.rpw <= kFinRows && s.P <= 64 && wgs < (int64_t(1) << 31);
   BnBackOpT<SRC> op{delta, output, xNorm, scales, act, 0.f};
   op.pidx = pidx;
   op.pdel = pdel;
   op.block = static_cast<uint32_t>(block);
   op.w = static_cast<uint32_t>(w);
+  if (fused) {
+    op.var = variance;
+    op.vpow = vpow;
+  }
   if (int st = launch_partial<1>(cx, op, s, chan_vec(s, {delta, output, xNorm}), dotPart,
                                  "chan_partial_kernel<bn_back>"))
     return st;
+  if (!fused) {
+    if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
+                                   "chan_partial_kernel<mean_var_delta>", fin))
+      return st;
+    return tnh_normalize_delta(N, dstSize, groups, delta, x, 0, mean, variance, mean_delta, variance_delta);
+  }
   if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
-                                 "chan_partial_kernel<mean_var_delta>",
-                                 BnBackFin{MvdFin{red, variance, mean_delta, variance_delta}, dotPart, scaleUpdates}))
+                                 "chan_partial_kernel<mean_var_delta>"))
     return st;
-  return tnh_normalize_delta(N, dstSize, groups, delta, x, 0, mean, variance, mean_delta, variance_delta);
+  const float batchSize = static_cast<float>(block * groups);
+  if (v4)
+    hipLaunchKernelGGL(normalize_delta_fin_kernel<4>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
+                       cx->stream, delta, x, g, batchSize, mean, variance, fin, s.P);
+  else
+    hipLaunchKernelGGL(normalize_delta_fin_kernel<1>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
+                       cx->stream, delta, x, g, batchSize, mean, variance, fin, s.P);
+  return launch_status("normalize_delta_fin_kernel");
 }
 
 }  // namespace

@@ -124,6 +124,8 @@ _PROTOS = {
     "tnh_bn_forward": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32],
     "tnh_bn_forward_maxpool": [i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp],
     "tnh_bn_forward_avgpool": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, i32, vp],
+    "tnh_bn_train_forward_maxpool": [i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, vp, vp, i32, vp, vp],
+    "tnh_bn_train_forward_avgpool": [i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, f32, vp, vp, i32, vp],
     "tnh_yolo_fwd": [i64] * 5 + [vp, vp],
     "tnh_yolo_detections": [i64, i32, C.POINTER(vp), C.POINTER(i64), i64, i64, C.POINTER(f32), i64, i64, i64, i64,
                             f32, i32, i32, i64, vp, vp, vp, vp],
@@ -570,6 +572,20 @@ class TNNHip:
         """bnForward then avgPoolForward of its output (planes of hw <= 64), one pass."""
         call("tnh_bn_forward_avgpool", batch, N, hw, addr(x), addr(xNorm), addr(out), addr(mean), addr(variance),
              addr(scales), addr(biases), activation, addr(avg))
+
+    def bnTrainForwardMaxPool(self, batch, N, h, w, x, xNorm, out, mean, variance, rollMean, rollVar, momentum,
+                              scales, biases, activation, pooled, indexes):
+        """bnStatistics then bnForwardMaxPool, three launches (the statistics' final step in the last)."""
+        call("tnh_bn_train_forward_maxpool", batch, N, h, w, addr(x), addr(xNorm), addr(out), addr(mean),
+             addr(variance), addr(rollMean), addr(rollVar), momentum, addr(scales), addr(biases), activation,
+             addr(pooled), addr(indexes))
+
+    def bnTrainForwardAvgPool(self, batch, N, hw, x, xNorm, out, mean, variance, rollMean, rollVar, momentum, scales,
+                              biases, activation, avg):
+        """bnStatistics then bnForwardAvgPool, three launches."""
+        call("tnh_bn_train_forward_avgpool", batch, N, hw, addr(x), addr(xNorm), addr(out), addr(mean),
+             addr(variance), addr(rollMean), addr(rollVar), momentum, addr(scales), addr(biases), activation,
+             addr(avg))
 
     def bnForwardMaxPool(self, batch, N, h, w, x, xNorm, out, mean, variance, scales, biases, activation, pooled,
                          indexes):

@@ -67,7 +67,7 @@ class CifarTrainer:
     backward and update on the device; `cost()` reads the loss back."""
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
-                 fused_wgrad=True, conv_dgrad=True, fused_head=True, fused_pool_bwd=True):
+                 fused_wgrad=True, conv_dgrad=True, fused_head=True, fused_pool_bwd=True, fused_stats=True):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
         im2col + NT product (the same bits).  conv_dgrad: the conv input
@@ -78,12 +78,14 @@ class CifarTrainer:
         backward in another; False runs them call by call.  fused_pool_bwd:
         the pool layers' backwards are formed inside the batch-norm backward
         below them (no zeroed delta, no scatter launch; the same bits);
-        False runs backwardMaxPool / avgPoolBackward into zeroed deltas."""
+        False runs backwardMaxPool / avgPoolBackward into zeroed deltas.
+        fused_stats: the batch statistics' final step is taken by the
+        normalize pass (the same bits); False calls bnStatistics first."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
         self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
-        self.fused_pool_bwd = fused_pool_bwd
+        self.fused_pool_bwd, self.fused_stats = fused_pool_bwd, fused_stats
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -184,10 +186,24 @@ class CifarTrainer:
             y = t[f"x{i}"]
             hip.conv2dForward(B, c, hh, hh, f, 3, 1, 1, h, 0, self.packed[i], None, acLINEAR, y, 0,
                               weightLayout=WEIGHTS_TAP_MAJOR)
-            # MeansAndVars, then rolling = (1 - m) * rolling, rolling = axpy(m, stat)
-            hip.bnStatistics(n, f, B, y, 0, t[f"mean{i}"], t[f"var{i}"], p[f"rm{i}"], p[f"rv{i}"],
-                             float(np.float32(self.bnm)))
             xn, out = t[f"xn{i}"], t[f"out{i}"]
+            bnm = float(np.float32(self.bnm))
+            stats = (t[f"mean{i}"], t[f"var{i}"], p[f"rm{i}"], p[f"rv{i}"], bnm)
+            if self.fused_stats and self.fused_head and i == len(self.dims) - 1 and hh * hh <= 64:
+                # MeansAndVars (rolling = (1 - m) * rolling + m * stat), the
+                # normalize pass and the head's average pool: three launches
+                hip.bnTrainForwardAvgPool(B, f, hh * hh, y, xn, out, *stats, p[f"s{i}"], p[f"b{i}"], acLEAKY,
+                                          t["avg"])
+                h = None
+                continue
+            if self.fused_stats and i < len(self.dims) - 1:
+                # ... and the 2x2 maxpool
+                hip.bnTrainForwardMaxPool(B, f, hh, hh, y, xn, out, *stats, p[f"s{i}"], p[f"b{i}"], acLEAKY,
+                                          t[f"pool{i}"], t[f"pidx{i}"])
+                h = t[f"pool{i}"]
+                continue
+            # MeansAndVars, then rolling = (1 - m) * rolling, rolling = axpy(m, stat)
+            hip.bnStatistics(n, f, B, y, 0, *stats)
             # x (y) is kept as the layer's pre-normalization copy; one pass
             # writes x_norm and act(scale * x_norm + bias)
             if i < len(self.dims) - 1:

@@ -540,9 +540,11 @@ def test_conv_input_delta_as_convolution(hip, B, F, C, hh):
     assert R.rel_err(got, H(dx2, hip)) <= TOL
 
 
-@pytest.mark.parametrize("shape,act", [((128, 32, 32, 32), acLEAKY), ((8, 64, 8, 8), acLEAKY), ((3, 5, 7, 9), acLINEAR)])
+@pytest.mark.parametrize("shape,act", [((128, 32, 32, 32), acLEAKY), ((8, 64, 8, 8), acLEAKY), ((3, 5, 7, 9), acLINEAR),
+                                       ((4, 8, 2, 2), acLEAKY)])
 def test_bn_backward_equals_the_sequence(hip, shape, act):
-    """tnh_bn_backward (four launches) against bnBackwardScale,
+    """tnh_bn_backward (three launches; four for rows of 4 elements, whose
+    workgroups would hold 256 channel rows) against bnBackwardScale,
     meansAndVarsDelta and normalizeDelta: delta, dgamma and the mean /
     variance deltas bit for bit."""
     case(f"bn_backward {shape} act{act}")
@@ -651,6 +653,88 @@ def test_bn_backward_avgpool_equals_the_calls(hip, shape, act):
         res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
     for a, b in zip(*res):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape,rolling", [((128, 32, 32, 32), True), ((128, 64, 16, 16), True), ((4, 3, 6, 8), False),
+                                           ((8, 4, 2, 4), True)])
+def test_bn_train_forward_maxpool_equals_the_calls(hip, shape, rolling):
+    """tnh_bn_train_forward_maxpool against tnh_bn_statistics then
+    tnh_bn_forward_maxpool: mean, variance, the rolling statistics, x_norm,
+    out, the pooled values and indices bit for bit (planes of 2x4 take the
+    path with the final step in its own launch)."""
+    case(f"bn_train_forward_maxpool {shape} rolling{rolling}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    x = synth.normal(400, shape) * np.float32(1.7) + np.float32(0.3)
+    gamma, beta = synth.normal(401, (F,)), synth.normal(402, (F,))
+    rm0, rv0 = synth.normal(403, (F,)), np.abs(synth.normal(404, (F,)))
+    m = float(np.float32(0.1))
+    res = []
+    for fused in (True, False):
+        mean = torch.empty(F, dtype=torch.float32, device="cuda")
+        var = torch.empty(F, dtype=torch.float32, device="cuda")
+        rm, rv = (D(rm0), D(rv0)) if rolling else (None, None)
+        xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        pool = torch.empty((B, F, h // 2, w // 2), dtype=torch.float32, device="cuda")
+        pidx = torch.empty((B, F, h // 2, w // 2), dtype=torch.int64, device="cuda")
+        if fused:
+            hip.bnTrainForwardMaxPool(B, F, h, w, D(x), xn, out, mean, var, rm, rv, m, D(gamma), D(beta), acLEAKY,
+                                      pool, pidx)
+        else:
+            hip.bnStatistics(n, F, B, D(x), 0, mean, var, rm, rv, m)
+            hip.bnForwardMaxPool(B, F, h, w, D(x), xn, out, mean, var, D(gamma), D(beta), acLEAKY, pool, pidx)
+        res.append([H(t_, hip).copy() for t_ in (mean, var, xn, out, pool, pidx) + ((rm, rv) if rolling else ())])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("shape", [(128, 128, 8, 8), (3, 5, 3, 3), (6, 7, 1, 1)])
+def test_bn_train_forward_avgpool_equals_the_calls(hip, shape):
+    """tnh_bn_train_forward_avgpool against tnh_bn_statistics then
+    tnh_bn_forward_avgpool, bit for bit."""
+    case(f"bn_train_forward_avgpool {shape}")
+    B, F, h, w = shape
+    n = B * F * h * w
+    x = synth.normal(405, shape)
+    gamma, beta = synth.normal(406, (F,)), synth.normal(407, (F,))
+    rm0, rv0 = synth.normal(408, (F,)), np.abs(synth.normal(409, (F,)))
+    m = float(np.float32(0.1))
+    res = []
+    for fused in (True, False):
+        mean = torch.empty(F, dtype=torch.float32, device="cuda")
+        var = torch.empty(F, dtype=torch.float32, device="cuda")
+        rm, rv = D(rm0), D(rv0)
+        xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+        out = torch.empty(shape, dtype=torch.float32, device="cuda")
+        avg = torch.empty((B, F), dtype=torch.float32, device="cuda")
+        if fused:
+            hip.bnTrainForwardAvgPool(B, F, h * w, D(x), xn, out, mean, var, rm, rv, m, D(gamma), D(beta), acLEAKY,
+                                      avg)
+        else:
+            hip.bnStatistics(n, F, B, D(x), 0, mean, var, rm, rv, m)
+            hip.bnForwardAvgPool(B, F, h * w, D(x), xn, out, mean, var, D(gamma), D(beta), acLEAKY, avg)
+        res.append([H(t_, hip).copy() for t_ in (mean, var, rm, rv, xn, out, avg)])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+
+
+def test_cifar_step_fused_stats_equals_the_calls(hip):
+    """The training step with the statistics' final steps taken by the
+    normalize passes gives the same bits as with bnStatistics."""
+    case("cifar step fused statistics vs calls")
+    params = trainnet.init_params()
+    x, truth = _batch(324, 16)
+    keys = ("u_w0", "u_w1", "u_w2", "u_s0", "u_s1", "u_s2", "w0", "w1", "w2", "u_fw", "rm0", "rv1", "rm2")
+    out = []
+    for fused in (True, False):
+        gpu = trainnet.CifarTrainer(hip, params, 16, fused_stats=fused)
+        gpu.forward(D(x), D(truth))
+        gpu.backward()
+        gpu.update()
+        out.append({k: gpu.host(k).copy() for k in keys})
+    for k in keys:
+        assert np.array_equal(out[0][k], out[1][k]), k
 
 
 def test_cifar_step_fused_pool_bwd_equals_the_calls(hip):
