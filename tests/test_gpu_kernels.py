@@ -534,7 +534,7 @@ def test_conv_few_channels_bit_exact(hip, B, Cc, Hh, F, s, tap, act, resid):
     assert np.array_equal(H(dout, hip), ref)
 
 
-@pytest.mark.parametrize("cfg", [0, 6, 8, 11])
+@pytest.mark.parametrize("cfg", [0, 1, 11, 13])
 @pytest.mark.parametrize("splits", [2, 4, 16])
 @pytest.mark.parametrize("B,Cc,Hh,F,k,s", [(1, 512, 13, 1024, 3, 1), (1, 256, 13, 255, 1, 1), (2, 64, 9, 96, 3, 2)])
 def test_conv_splitk(hip, cfg, splits, B, Cc, Hh, F, k, s):
