@@ -1,0 +1,75 @@
+"""The library on its own device memory: buffers from tnh_malloc
+(TNNHip.createDeviceBuffer, TNNCuda.createDeviceBuffer nncuda.pas:488),
+uploads and downloads through tnh_h2d / tnh_d2h (writeBuffer / readBuffer,
+nncuda.pas:512, 499), no torch tensor anywhere: what a Pascal caller of
+pascal/nnhip.pas does.  Checked against the CPU oracle."""
+import numpy as np
+import pytest
+
+from oracle import refcpu as R
+from tensorium_amd import synth
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, DeviceBuffer, acLEAKY
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def up(hip, a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    buf = hip.createDeviceBuffer(a.size)
+    hip.writeBuffer(buf, a.nbytes, a)
+    return buf
+
+
+def down(hip, buf, shape):
+    out = np.empty(shape, np.float32)
+    hip.finish()
+    hip.readBuffer(buf, out.nbytes, out)
+    return out
+
+
+@pytest.mark.parametrize("B,C,H,F,k", [(2, 64, 26, 128, 3), (1, 32, 13, 64, 1)])
+def test_conv_on_library_buffers(hip, B, C, H, F, k):
+    """conv (reference-layout and packed weights) + bias + leaky on
+    tnh_malloc buffers only: within 1e-5 of the oracle."""
+    case(f"devmem conv B{B} C{C} H{H} F{F} k{k}")
+    p = k // 2
+    x = synth.uniform(501, (B, C, H, H))
+    Wt = synth.normal(502, (F, C * k * k), (2.0 / (C * k * k)) ** 0.5)
+    b = synth.normal(503, (F,), 0.1)
+    ref = R.conv_forward(x, Wt, b, k, 1, p, acLEAKY)
+    bufs = [up(hip, x), up(hip, Wt), up(hip, b)]
+    out = hip.createDeviceBuffer(ref.size)
+    packed = hip.createDeviceBuffer(Wt.size)
+    try:
+        assert all(isinstance(t, DeviceBuffer) for t in bufs + [out, packed])
+        hip.conv2dForward(B, C, H, H, F, k, 1, p, bufs[0], 0, bufs[1], bufs[2], acLEAKY, out, 0)
+        assert R.rel_err(down(hip, out, ref.shape), ref) <= 1e-5
+        hip.packConvWeights(F, C, k, bufs[1], packed)
+        hip.conv2dForward(B, C, H, H, F, k, 1, p, bufs[0], 0, packed, bufs[2], acLEAKY, out, 0,
+                          weightLayout=WEIGHTS_TAP_MAJOR)
+        assert R.rel_err(down(hip, out, ref.shape), ref) <= 1e-5
+    finally:
+        for t in bufs + [out, packed]:
+            hip.freeDeviceBuffer(t)
+
+
+def test_sgemm_on_library_buffers(hip):
+    """TNNHip.gemm on tnh_malloc buffers: integer-valued operands make the
+    product exact, so it must equal numpy's bit for bit."""
+    case("devmem sgemm 256x192x320")
+    M, N, K = 256, 192, 320
+    rng = np.random.default_rng(504)
+    A = rng.integers(-8, 9, (M, K)).astype(np.float32)
+    Bm = rng.integers(-8, 9, (K, N)).astype(np.float32)
+    a, bb = up(hip, A), up(hip, Bm)
+    c = hip.createDeviceBuffer(M * N)
+    try:
+        hip.gemm(False, False, M, N, K, 1.0, a, 0, K, bb, 0, N, 0.0, c, 0, N)
+        assert np.array_equal(down(hip, c, (M, N)), A @ Bm)
+    finally:
+        for t in (a, bb, c):
+            hip.freeDeviceBuffer(t)
