@@ -678,14 +678,15 @@ int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
                               const float *xNorm, const float *scales,
                               float *delta, float *scaleUpdates);
 /* No reference counterpart: batchNormBackGPU (nbaselayer.pas:662-712) with
- * the layer's activation derivative before it, in three launches instead of
- * six: tnh_bn_backward_scale's pass (delta *= act'(output), scaleUpdates +=
- * sum x_norm*delta, delta *= scales), tnh_means_vars_delta's sums, then
- * tnh_normalize_delta with the mean / variance deltas and the dgamma total
- * formed inside it (four launches when a workgroup would hold more than 16
- * channel rows).  The same operations in the same order as those calls, so
- * the same bits; x is the pre-normalization output, mean / variance the
- * forward's statistics. */
+ * the layer's activation derivative before it, in two launches instead of
+ * six: one pass doing tnh_bn_backward_scale's work (delta *= act'(output),
+ * scaleUpdates += sum x_norm*delta, delta *= scales) and taking
+ * tnh_means_vars_delta's sums of the new delta, then tnh_normalize_delta
+ * with the mean / variance deltas and the dgamma total formed inside it
+ * (four launches when a workgroup would hold more than 16 channel rows).
+ * The same operations in the same order as those calls, so the same bits; x
+ * is the pre-normalization output, mean / variance the forward's
+ * statistics. */
 int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
                         const float *output, int32_t act, const float *xNorm,
                         const float *x, const float *scales, const float *mean,

@@ -375,8 +375,11 @@ enum DeltaSrc { kFromDelta = 0, kFromMaxPool2 = 1, kFromAvgPool = 2 };
 // DeriveArray (delta *= act'(out)), addDots (dgamma += sum x_norm * delta)
 // and forwardScale (delta *= gamma), each element visited once with each
 // step's own operation, so the deltas and the dot equal the three separate
-// passes bit for bit.
-template <int SRC>
+// passes bit for bit.  MVD: the pass also takes MvdOp's two sums of the new
+// delta (a[0], a[1]; the dot in a[2]), element by element in the order
+// MvdOp's own pass over the same split adds them, so its partials are the
+// same bits and its pass over delta and x is saved.
+template <int SRC, bool MVD = false>
 struct BnBackOpT {
   float* delta;
   const float* out;
@@ -392,8 +395,12 @@ struct BnBackOpT {
   // step (the one term of it that does not wait for the delta sums)
   const float* var = nullptr;
   double* vpow = nullptr;
+  const float* x = nullptr;     // MVD: the pre-normalization input
+  const float* mean = nullptr;  // MVD: the forward's means
+  float mu = 0.f;
   __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) {
     g = gamma[i];
+    if constexpr (MVD) mu = mean[i];
     if (vpow && blockIdx.y == 0 && threadIdx.x == 0)
       vpow[i] = pow(static_cast<double>(fmaxf(var[i], kEps)), -1.5);
   }
@@ -434,19 +441,28 @@ struct BnBackOpT {
     if (act == TNH_AC_LOGISTIC) return (1.f - v) * v;
     return 1.f;
   }
-  __device__ float one(float* a, float d, float o, float x) const {
+  __device__ float one(float* a, float d, float o, float xnv, float xv) const {
     const float d1 = d * grad(o, act);
-    a[0] = a[0] + x * d1;
-    return g * d1;
+    constexpr int kDot = MVD ? 2 : 0;
+    a[kDot] = a[kDot] + xnv * d1;
+    const float r = g * d1;
+    if constexpr (MVD) {  // MvdOp::add on the new delta
+      a[0] = a[0] + r;
+      a[1] = a[1] + r * (xv - mu);
+    }
+    return r;
   }
-  __device__ void add(float* a, int64_t e) const { delta[e] = one(a, src(e), out[e], xn[e]); }
+  __device__ void add(float* a, int64_t e) const {
+    delta[e] = one(a, src(e), out[e], xn[e], MVD ? x[e] : 0.f);
+  }
   __device__ void add4(float* a, int64_t e) const {
-    const float4 d = src4(e), o = ld4(out + e), x = ld4(xn + e);
+    const float4 d = src4(e), o = ld4(out + e), xv = ld4(xn + e);
+    const float4 v = MVD ? ld4(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
     float4 r;
-    r.x = one(a, d.x, o.x, x.x);
-    r.y = one(a, d.y, o.y, x.y);
-    r.z = one(a, d.z, o.z, x.z);
-    r.w = one(a, d.w, o.w, x.w);
+    r.x = one(a, d.x, o.x, xv.x, v.x);
+    r.y = one(a, d.y, o.y, xv.y, v.y);
+    r.z = one(a, d.z, o.z, xv.z, v.z);
+    r.w = one(a, d.w, o.w, xv.w, v.w);
     *reinterpret_cast<float4*>(delta + e) = r;
   }
 };
@@ -1589,6 +1605,23 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
 
 namespace {
 
+// normalize_delta_fin_kernel over [groups][dstSize][block] (rows per
+// workgroup <= kFinRows, checked by the caller)
+int launch_normalize_fin(Context* cx, int64_t N, int64_t block, int64_t dstSize, int64_t groups, float* delta,
+                         const float* x, const float* mean, const float* variance, const BnBackFin& fin, int P) {
+  const bool v4 = block % 4 == 0 && rows_al16(delta) && rows_al16(x);
+  const Rows g = make_rows(N, block, dstSize, v4 ? 4 : 1);
+  const int64_t wgs = (g.rows + g.rpw - 1) / g.rpw;
+  const float batchSize = static_cast<float>(block * groups);
+  if (v4)
+    hipLaunchKernelGGL(normalize_delta_fin_kernel<4>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
+                       cx->stream, delta, x, g, batchSize, mean, variance, fin, P);
+  else
+    hipLaunchKernelGGL(normalize_delta_fin_kernel<1>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
+                       cx->stream, delta, x, g, batchSize, mean, variance, fin, P);
+  return launch_status("normalize_delta_fin_kernel");
+}
+
 // tnh_bn_backward with the layer's incoming delta taken from SRC (see
 // BnBackOpT); w is the row width for kFromMaxPool2.
 template <int SRC>
@@ -1616,6 +1649,22 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   const int64_t wgs = (g.rows + g.rpw - 1) / g.rpw;
   // many short rows (or P > 64): the finals in their own launch
   const bool fused = g.rpw <= kFinRows && s.P <= 64 && wgs < (int64_t(1) << 31);
+  const bool vec = chan_vec(s, {delta, output, xNorm});
+  if (fused && vec == chan_vec(s, {delta, x})) {
+    // one pass: the first pass's dot and MvdOp's two sums (the same walk as
+    // MvdOp's own pass, so the same partials), then the finals + normalize
+    BnBackOpT<SRC, true> op{delta, output, xNorm, scales, act, 0.f};
+    op.pidx = pidx;
+    op.pdel = pdel;
+    op.block = static_cast<uint32_t>(block);
+    op.w = static_cast<uint32_t>(w);
+    op.var = variance;
+    op.vpow = vpow;
+    op.x = x;
+    op.mean = mean;
+    if (int st = launch_partial<3>(cx, op, s, vec, red, "chan_partial_kernel<bn_back_mvd>")) return st;
+    return launch_normalize_fin(cx, N, block, dstSize, groups, delta, x, mean, variance, fin, s.P);
+  }
   BnBackOpT<SRC> op{delta, output, xNorm, scales, act, 0.f};
   op.pidx = pidx;
   op.pdel = pdel;
@@ -1625,9 +1674,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
     op.var = variance;
     op.vpow = vpow;
   }
-  if (int st = launch_partial<1>(cx, op, s, chan_vec(s, {delta, output, xNorm}), dotPart,
-                                 "chan_partial_kernel<bn_back>"))
-    return st;
+  if (int st = launch_partial<1>(cx, op, s, vec, dotPart, "chan_partial_kernel<bn_back>")) return st;
   if (!fused) {
     if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
                                    "chan_partial_kernel<mean_var_delta>", fin))
@@ -1637,14 +1684,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   if (int st = launch_partial<2>(cx, MvdOp{delta, x, mean, 0.f}, s, chan_vec(s, {delta, x}), red,
                                  "chan_partial_kernel<mean_var_delta>"))
     return st;
-  const float batchSize = static_cast<float>(block * groups);
-  if (v4)
-    hipLaunchKernelGGL(normalize_delta_fin_kernel<4>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
-                       cx->stream, delta, x, g, batchSize, mean, variance, fin, s.P);
-  else
-    hipLaunchKernelGGL(normalize_delta_fin_kernel<1>, dim3(static_cast<unsigned>(wgs)), dim3(kRowThreads), 0,
-                       cx->stream, delta, x, g, batchSize, mean, variance, fin, s.P);
-  return launch_status("normalize_delta_fin_kernel");
+  return launch_normalize_fin(cx, N, block, dstSize, groups, delta, x, mean, variance, fin, s.P);
 }
 
 }  // namespace
