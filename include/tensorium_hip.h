@@ -789,13 +789,17 @@ int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch,
  * [packF][packC][taps] at element packOffset[l]) to its tap-major copy
  * packTap[l] and, when packFlip[l] is not NULL, its flipped copy, as
  * tnh_conv2d_pack_weights_dgrad would after the update: a training step's
- * repacks ride on the update's pass instead of a launch per layer. */
+ * repacks ride on the update's pass instead of a launch per layer.  The same
+ * launch then runs tnh_param_update(nParams, learningRate, batch, momentum,
+ * params, paramUpdates) (the biases and scales; nParams 0: none). */
 int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch,
                             float momentum, float decay, float *weights,
                             float *weightUpdates, int32_t nPack,
                             const int64_t *packOffset, const int64_t *packF,
                             const int64_t *packC, const int64_t *packTaps,
-                            float *const *packTap, float *const *packFlip);
+                            float *const *packTap, float *const *packFlip,
+                            int64_t nParams, float *params,
+                            float *paramUpdates);
 /* bias / scale part of the same updates (nConvolutionLayer.pas:694-706):
  * params = fma(lr/batch, paramUpdates, params); paramUpdates *= momentum. */
 int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch,

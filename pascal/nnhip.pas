@@ -226,7 +226,7 @@ function tnh_sgd_update(N: Int64; learningRate: Single; batch: Int64; momentum, 
   weights, weightUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgd_update_pack(N: Int64; learningRate: Single; batch: Int64; momentum, decay: Single;
   weights, weightUpdates: PSingle; nPack: LongInt; packOffset, packF, packC, packTaps: PInt64;
-  packTap, packFlip: PPSingle): LongInt; cdecl; external libtnh;
+  packTap, packFlip: PPSingle; nParams: Int64; params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_param_update(N: Int64; learningRate: Single; batch: Int64; momentum: Single;
   params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgemm_nt_batch_reduce(M, N, L: Int64; alpha: Single; A: PSingle; aOff, lda, strideA: Int64;
@@ -426,10 +426,11 @@ type
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
       weights, weightUpdates: TCUMem);
-    // sgdUpdate whose pass also refreshes the packed copies of conv layers in the arena (flip[l] may be nil)
+    // sgdUpdate whose pass also refreshes the packed copies of conv layers in the arena (flip[l] may be nil),
+    // then paramUpdate of nParams biases / scales in the same launch
     procedure sgdUpdatePack(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
       weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64; const tapMajor,
-      flipped: array of TCUMem);
+      flipped: array of TCUMem; const nParams: SizeInt = 0; params: TCUMem = nil; paramUpdates: TCUMem = nil);
     procedure paramUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum: T;
       params, paramUpdates: TCUMem);
     procedure gemmNTBatchReduce(const M, N, L: SizeInt; const ALPHA: T; const A: TCUMem;
@@ -1031,13 +1032,14 @@ end;
 
 procedure TNNHip<T>.sgdUpdatePack(const N: SizeInt; const learningRate: T; const batch: SizeInt;
   const momentum, decay: T; weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64;
-  const tapMajor, flipped: array of TCUMem);
+  const tapMajor, flipped: array of TCUMem; const nParams: SizeInt; params: TCUMem; paramUpdates: TCUMem);
 var
   tp, fl: array of PSingle;
   i: SizeInt;
 begin
-  if Length(offsets) = 0 then begin
-    sgdUpdate(N, learningRate, batch, momentum, decay, weights, weightUpdates);
+  if Length(offsets) = 0 then begin  // no layer table: @offsets[0] would not exist
+    check(tnh_sgd_update_pack(N, S(learningRate), batch, S(momentum), S(decay), PSingle(weights),
+      PSingle(weightUpdates), 0, nil, nil, nil, nil, nil, nil, nParams, PSingle(params), PSingle(paramUpdates)));
     exit
   end;
   SetLength(tp, Length(tapMajor));
@@ -1045,7 +1047,8 @@ begin
   for i := 0 to High(tapMajor) do tp[i] := PSingle(tapMajor[i]);
   for i := 0 to High(flipped) do fl[i] := PSingle(flipped[i]);
   check(tnh_sgd_update_pack(N, S(learningRate), batch, S(momentum), S(decay), PSingle(weights),
-    PSingle(weightUpdates), Length(offsets), @offsets[0], @F[0], @C[0], @taps[0], @tp[0], @fl[0]));
+    PSingle(weightUpdates), Length(offsets), @offsets[0], @F[0], @C[0], @taps[0], @tp[0], @fl[0], nParams,
+    PSingle(params), PSingle(paramUpdates)));
 end;
 
 procedure TNNHip<T>.paramUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum: T;

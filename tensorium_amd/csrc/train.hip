@@ -872,10 +872,17 @@ struct PackSet {
 };
 
 // sgd_kernel, then each updated weight of a listed conv layer is also
-// written where tnh_conv2d_pack_weights_dgrad would put it.
+// written where tnh_conv2d_pack_weights_dgrad would put it; elements n ..
+// n + np - 1 of the grid run param_update_kernel's update on p / pu.
 __global__ void sgd_pack_kernel(int64_t n, float aDecay, float aRate, float momentum, float* w, float* wu,
-                                PackSet ps) {
-  GRID_STRIDE(i, n) {
+                                PackSet ps, int64_t np, float* p, float* pu) {
+  GRID_STRIDE(i, n + np) {
+    if (i >= n) {
+      const int64_t j = i - n;
+      p[j] = fmaf(aRate, pu[j], p[j]);
+      pu[j] = pu[j] * momentum;
+      continue;
+    }
     const float u = fmaf(aDecay, w[i], wu[i]);
     const float v = fmaf(aRate, u, w[i]);
     w[i] = v;
@@ -1421,12 +1428,14 @@ extern "C" int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch, 
 extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch, float momentum, float decay,
                                        float* weights, float* weightUpdates, int32_t nPack, const int64_t* packOffset,
                                        const int64_t* packF, const int64_t* packC, const int64_t* packTaps,
-                                       float* const* packTap, float* const* packFlip) {
+                                       float* const* packTap, float* const* packFlip, int64_t nParams, float* params,
+                                       float* paramUpdates) {
   TNH_REQUIRE_CTX(cx);
-  TNH_ARG(N >= 0 && batch > 0, "sgd_update_pack: bad arguments");
+  TNH_ARG(N >= 0 && batch > 0 && nParams >= 0, "sgd_update_pack: bad arguments");
   TNH_ARG(nPack >= 0 && nPack <= kMaxPack, "sgd_update_pack: %d layers (at most %d)", nPack, kMaxPack);
-  if (N == 0) return TNH_OK;
-  TNH_ARG(weights && weightUpdates, "sgd_update_pack: NULL buffer");
+  if (N + nParams == 0) return TNH_OK;
+  TNH_ARG(N == 0 || (weights && weightUpdates), "sgd_update_pack: NULL buffer");
+  TNH_ARG(nParams == 0 || (params && paramUpdates), "sgd_update_pack: NULL parameter buffer");
   TNH_ARG(nPack == 0 || (packOffset && packF && packC && packTaps && packTap && packFlip),
           "sgd_update_pack: NULL layer table");
   PackSet ps{};
@@ -1445,8 +1454,8 @@ extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t ba
   }
   const float aDecay = -decay * static_cast<float>(batch);
   const float aRate = learningRate / static_cast<float>(batch);
-  hipLaunchKernelGGL(sgd_pack_kernel, dim3(grid_1d(N)), dim3(256), 0, cx->stream, N, aDecay, aRate, momentum, weights,
-                     weightUpdates, ps);
+  hipLaunchKernelGGL(sgd_pack_kernel, dim3(grid_1d(N + nParams)), dim3(256), 0, cx->stream, N, aDecay, aRate, momentum,
+                     weights, weightUpdates, ps, nParams, params, paramUpdates);
   return launch_status("sgd_pack_kernel");
 }
 

@@ -161,7 +161,7 @@ _PROTOS = {
     "tnh_avgpool_bwd": [i64, i64, i64, i64, vp, vp],
     "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
     "tnh_sgd_update_pack": [i64, f32, i64, f32, f32, vp, vp, i32, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64),
-                            C.POINTER(i64), C.POINTER(vp), C.POINTER(vp)],
+                            C.POINTER(i64), C.POINTER(vp), C.POINTER(vp), i64, vp, vp],
     "tnh_param_update": [i64, f32, i64, f32, vp, vp],
     "tnh_conv2d_pack_weights_dgrad": [i64, i64, i64, i64, vp, vp, vp],
     "tnh_conv2d_wgrad": [i64] * 13 + [vp, i64, vp, i64, f32, f32, vp],
@@ -733,15 +733,17 @@ class TNNHip:
     def sgdUpdate(self, N, learningRate, batch, momentum, decay, weights, weightUpdates):
         call("tnh_sgd_update", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates))
 
-    def sgdUpdatePack(self, N, learningRate, batch, momentum, decay, weights, weightUpdates, layers):
+    def sgdUpdatePack(self, N, learningRate, batch, momentum, decay, weights, weightUpdates, layers, nParams=0,
+                      params=None, paramUpdates=None):
         """sgdUpdate whose pass also refreshes conv layers' packed copies;
-        layers: [(offset, F, C, taps, tapMajor, flipped or None), ...]."""
+        layers: [(offset, F, C, taps, tapMajor, flipped or None), ...]; then
+        paramUpdate(nParams, ..., params, paramUpdates) in the same launch."""
         n = len(layers)
         arr = lambda t, xs: (t * max(n, 1))(*xs)  # noqa: E731
         call("tnh_sgd_update_pack", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates), n,
              arr(i64, [l[0] for l in layers]), arr(i64, [l[1] for l in layers]), arr(i64, [l[2] for l in layers]),
              arr(i64, [l[3] for l in layers]), arr(vp, [addr(l[4]) for l in layers]),
-             arr(vp, [addr(l[5]) for l in layers]))
+             arr(vp, [addr(l[5]) for l in layers]), nParams, addr(params), addr(paramUpdates))
 
     def paramUpdate(self, N, learningRate, batch, momentum, params, paramUpdates):
         call("tnh_param_update", N, learningRate, batch, momentum, addr(params), addr(paramUpdates))

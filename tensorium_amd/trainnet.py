@@ -315,11 +315,11 @@ class CifarTrainer:
         hip, B = self.hip, self.B
         lr, m, dec = self.lr, self.momentum, self.decay
         w, uw = self.arena["w"]
-        # the update's pass also writes the conv weights' tap-major (and
-        # flipped) copies the next forward and backward read
-        hip.sgdUpdatePack(w.numel(), lr, B, m, dec, w, uw, self._pack_layers())
         q, uq = self.arena["p"]
-        hip.paramUpdate(q.numel(), lr, B, m, q, uq)
+        # the update's pass also writes the conv weights' tap-major (and
+        # flipped) copies the next forward and backward read, and updates the
+        # biases and scales
+        hip.sgdUpdatePack(w.numel(), lr, B, m, dec, w, uw, self._pack_layers(), q.numel(), q, uq)
 
     def step(self, x, truth):
         self.forward(x, truth)

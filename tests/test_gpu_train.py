@@ -762,7 +762,9 @@ def test_sgd_update_pack_equals_update_then_pack(hip):
     """tnh_sgd_update_pack: the weights and momenta of tnh_sgd_update bit for
     bit, and each listed layer's tap-major / flipped copies equal to
     tnh_conv2d_pack_weights_dgrad of the updated weights; elements outside
-    the layers (a connected layer in the same arena) only updated."""
+    the layers (a connected layer in the same arena) only updated; the
+    parameter arena updated as tnh_param_update does, in the same launch and
+    with no layer table too."""
     case("sgd_update_pack")
     layers = [(32, 3, 9), (64, 32, 9), (10, 6, 1)]
     sizes = [f * c * t for f, c, t in layers]
@@ -775,11 +777,22 @@ def test_sgd_update_pack_equals_update_then_pack(hip):
     offs = np.concatenate([[0], np.cumsum(sizes)])[:-1] + 1290  # the connected layer first
     taps = [torch.empty(sz, dtype=torch.float32, device="cuda") for sz in sizes]
     flips = [torch.empty(sz, dtype=torch.float32, device="cuda") for sz in sizes]
+    npar = 1234
+    p0, pu0 = synth.normal(362, (npar,)), synth.normal(363, (npar,))
+    pa, pua = D(p0), D(pu0)
+    hip.paramUpdate(npar, 1e-3, 128, 0.9, pa, pua)
+    pb, pub = D(p0), D(pu0)
     hip.sgdUpdatePack(n, 1e-3, 128, 0.9, 1e-4, wb, ub,
                       [(int(o), f, c, t, tp, fl if i > 0 else None)
-                       for i, ((f, c, t), o, tp, fl) in enumerate(zip(layers, offs, taps, flips))])
+                       for i, ((f, c, t), o, tp, fl) in enumerate(zip(layers, offs, taps, flips))], npar, pb, pub)
     wref = H(wa, hip)
     assert np.array_equal(H(wb, hip), wref) and np.array_equal(H(ub, hip), H(ua, hip))
+    assert np.array_equal(H(pb, hip), H(pa, hip)) and np.array_equal(H(pub, hip), H(pua, hip))
+    # no layer table: the plain update of both arenas
+    wc, uc, pc, puc = D(w0), D(u0), D(p0), D(pu0)
+    hip.sgdUpdatePack(n, 1e-3, 128, 0.9, 1e-4, wc, uc, [], npar, pc, puc)
+    assert np.array_equal(H(wc, hip), wref) and np.array_equal(H(uc, hip), H(ua, hip))
+    assert np.array_equal(H(pc, hip), H(pa, hip)) and np.array_equal(H(puc, hip), H(pua, hip))
     for i, ((f, c, t), o) in enumerate(zip(layers, offs)):
         k = int(round(t ** 0.5))
         tp = torch.empty(f * c * t, dtype=torch.float32, device="cuda")
