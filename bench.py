@@ -308,10 +308,24 @@ def extra_single_conv(hip, cpu_budget=0.0):
     ms = time_graph(hip, fn, 50)
     flop = 2.0 * 16 * 27 * 416 * 416
     byts = 4.0 * (3 * 416 * 416 + 16 * 416 * 416 + 16 * 27)
+    # floors at this size, timed the same way: writing the 11.1 MB output
+    # alone (a fill) and moving the layer's bytes as one copy of that size
+    nout = 16 * 416 * 416
+    fill_ms = time_graph(hip, lambda: hip.fill(nout, out, 0, 0.5, 1), 50)
+    half = int(byts / 8)  # floats read = floats written = the layer's bytes / 2
+    src = torch.empty(half, dtype=torch.float32, device="cuda")
+    dst = torch.empty(half, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    copy_ms = time_graph(hip, lambda: hip.copy(half, src, 0, 1, dst, 0, 1), 50)
     out = {"workload": "conv 3->16 3x3 s1 p1 + bias + leaky, 1x3x416x416", "launch": "hip_graph",
            "us": round(ms * 1e3, 2), "us_eager": round(eager * 1e3, 2),
            "gflops": round(flop / ms / 1e6, 1), "gb_s": round(byts / ms / 1e6, 1),
-           "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4)}
+           "hbm_frac": round(byts / ms * 1e3 / PEAK_HBM, 4),
+           "floor": {"fill_output_us": round(fill_ms * 1e3, 2), "copy_same_bytes_us": round(copy_ms * 1e3, 2),
+                     "conv_over_copy": round(ms / copy_ms, 3),
+                     "note": "one launch of this size, graph-timed like the conv: the output fill alone, and a "
+                             "device copy moving the layer's algorithmic bytes (half read, half written)"}}
+    del src, dst
     if cpu_budget > 0:
         from oracle import refcpu as R
         from tensorium_amd import synth as S
