@@ -223,7 +223,7 @@ def _batch(seed, B):
     return x, truth
 
 
-@pytest.mark.parametrize("B", [128, 8])
+@pytest.mark.parametrize("B", [128, 8, 3, 1])
 def test_cifar_train_step(hip, B):
     """One full trainEpoch iteration (forward, backward, update) on the device
     vs the oracle from identical parameters and inputs: loss, BN statistics,
