@@ -686,7 +686,9 @@ int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
  * (four launches when a workgroup would hold more than 16 channel rows).
  * The same operations in the same order as those calls, so the same bits; x
  * is the pre-normalization output, mean / variance the forward's
- * statistics. */
+ * statistics.  xNorm may be NULL (here and in the _maxpool / _avgpool
+ * forms): the first pass then forms x_norm from x, mean and variance as
+ * tnh_bn_forward forms it (the same bits; the forward need not store it). */
 int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
                         const float *output, int32_t act, const float *xNorm,
                         const float *x, const float *scales, const float *mean,

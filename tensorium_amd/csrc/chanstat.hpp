@@ -7,6 +7,22 @@
 
 namespace tnh {
 
+// The normalize step of the batch norm (TTensor.blockNormalize,
+// ntensors.pas:8693-8718, with IEEE division): d = max(sqrt(var), 1e-6) for
+// planes of more than one element (_snormblkvv, :4357), sqrt(max(var, 1e-6))
+// for one element per channel (_snormvv, :4338); x_norm = (x - mean) / d.
+// Shared by the forward pass and the backward passes that form x_norm again
+// instead of reading it, so both give the same bits.
+__device__ inline float bn_norm_d(float var, bool oneElem) {
+  if (oneElem) return sqrtf(var > 1e-6f ? var : 1e-6f);
+  const float d = sqrtf(var);
+  return d > 1e-6f ? d : 1e-6f;
+}
+__device__ inline float bn_norm(float x, float mean, float d) {
+  const float t = x - mean;
+  return t / d;
+}
+
 // The tree of the channel reductions' final step over one value per lane
 // (lane i adds lane i + w for w = 32, 16, ..., 1).  Called by a whole wave;
 // every lane gets lane 0's total.

@@ -94,21 +94,9 @@ struct NormOp {
   int64_t vs;
   int clampVar;
   struct Ch { float m, d; };
-  __device__ Ch make(float mean, float var) const {
-    float d;
-    if (clampVar) {
-      d = sqrtf(var > 1e-6f ? var : 1e-6f);
-    } else {
-      d = sqrtf(var);
-      d = d > 1e-6f ? d : 1e-6f;
-    }
-    return {mean, d};
-  }
+  __device__ Ch make(float mean, float var) const { return {mean, bn_norm_d(var, clampVar != 0)}; }
   __device__ Ch chan(int64_t f) const { return make(m[f * ms], v[f * vs]); }
-  __device__ float operator()(const Ch& c, float x) const {
-    const float t = x - c.m;
-    return t / c.d;
-  }
+  __device__ float operator()(const Ch& c, float x) const { return bn_norm(x, c.m, c.d); }
 };
 
 __device__ inline float act_fwd(float v, int act) {

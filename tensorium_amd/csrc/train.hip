@@ -395,12 +395,15 @@ struct BnBackOpT {
   // step (the one term of it that does not wait for the delta sums)
   const float* var = nullptr;
   double* vpow = nullptr;
-  const float* x = nullptr;     // MVD: the pre-normalization input
-  const float* mean = nullptr;  // MVD: the forward's means
-  float mu = 0.f;
+  const float* x = nullptr;     // MVD or xn NULL: the pre-normalization input
+  const float* mean = nullptr;  // MVD or xn NULL: the forward's means
+  const float* varN = nullptr;  // xn NULL: the forward's variances
+  bool oneElem = false;         // xn NULL: one element per channel and image
+  float mu = 0.f, nd = 1.f;
   __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) {
     g = gamma[i];
-    if constexpr (MVD) mu = mean[i];
+    if (MVD || !xn) mu = mean[i];
+    if (!xn) nd = bn_norm_d(varN[i], oneElem);  // x_norm formed as the forward formed it
     if (vpow && blockIdx.y == 0 && threadIdx.x == 0)
       vpow[i] = pow(static_cast<double>(fmaxf(var[i], kEps)), -1.5);
   }
@@ -453,11 +456,15 @@ struct BnBackOpT {
     return r;
   }
   __device__ void add(float* a, int64_t e) const {
-    delta[e] = one(a, src(e), out[e], xn[e], MVD ? x[e] : 0.f);
+    const float xv = (MVD || !xn) ? x[e] : 0.f;
+    delta[e] = one(a, src(e), out[e], xn ? xn[e] : bn_norm(xv, mu, nd), xv);
   }
   __device__ void add4(float* a, int64_t e) const {
-    const float4 d = src4(e), o = ld4(out + e), xv = ld4(xn + e);
-    const float4 v = MVD ? ld4(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 d = src4(e), o = ld4(out + e);
+    const float4 v = (MVD || !xn) ? ld4(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 xv = xn ? ld4(xn + e)
+                         : make_float4(bn_norm(v.x, mu, nd), bn_norm(v.y, mu, nd), bn_norm(v.z, mu, nd),
+                                       bn_norm(v.w, mu, nd));
     float4 r;
     r.x = one(a, d.x, o.x, xv.x, v.x);
     r.y = one(a, d.y, o.y, xv.y, v.y);
@@ -1640,7 +1647,8 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
                      float* scaleUpdates, float* mean_delta, float* variance_delta) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "%s: bad sizes", who);
-  TNH_ARG(output && xNorm && x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
+  // xNorm NULL: x_norm is formed from x, mean and variance in the first pass
+  TNH_ARG(output && x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
           "%s: NULL buffer", who);
   TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "%s: activation %d", who, act);
   const int64_t block = N / (dstSize * groups);
@@ -1658,7 +1666,13 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   const int64_t wgs = (g.rows + g.rpw - 1) / g.rpw;
   // many short rows (or P > 64): the finals in their own launch
   const bool fused = g.rpw <= kFinRows && s.P <= 64 && wgs < (int64_t(1) << 31);
-  const bool vec = chan_vec(s, {delta, output, xNorm});
+  const bool vec = chan_vec(s, {delta, output, xNorm ? xNorm : x});
+  auto norm_in_pass = [&](auto& o) {  // x_norm from x, mean and variance
+    o.x = x;
+    o.mean = mean;
+    o.varN = variance;
+    o.oneElem = block == 1;
+  };
   if (fused && vec == chan_vec(s, {delta, x})) {
     // one pass: the first pass's dot and MvdOp's two sums (the same walk as
     // MvdOp's own pass, so the same partials), then the finals + normalize
@@ -1671,6 +1685,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
     op.vpow = vpow;
     op.x = x;
     op.mean = mean;
+    if (!xNorm) norm_in_pass(op);
     if (int st = launch_partial<3>(cx, op, s, vec, red, "chan_partial_kernel<bn_back_mvd>")) return st;
     return launch_normalize_fin(cx, N, block, dstSize, groups, delta, x, mean, variance, fin, s.P);
   }
@@ -1679,6 +1694,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   op.pdel = pdel;
   op.block = static_cast<uint32_t>(block);
   op.w = static_cast<uint32_t>(w);
+  if (!xNorm) norm_in_pass(op);
   if (fused) {
     op.var = variance;
     op.vpow = vpow;

@@ -737,6 +737,73 @@ def test_cifar_step_fused_stats_equals_the_calls(hip):
         assert np.array_equal(out[0][k], out[1][k]), k
 
 
+XNORM_CASES = [(shape, form) for shape in [(16, 32, 32, 32), (8, 64, 8, 8), (3, 5, 6, 6), (6, 7, 1, 1)]
+               for form in ("plain", "maxpool", "avgpool") if not (form == "maxpool" and shape[2] == 1)]
+
+
+@pytest.mark.parametrize("shape,form", XNORM_CASES)
+def test_bn_backward_forms_xnorm(hip, shape, form):
+    """tnh_bn_backward (and its _maxpool / _avgpool forms) with xNorm NULL,
+    x_norm formed in the first pass from x, mean and variance, against the
+    same call given the x_norm that tnh_bn_forward stored: every output bit
+    for bit (planes of one element take the other variance clamp)."""
+    B, F, h, w = shape
+    case(f"bn_backward xNorm NULL {form} {shape}")
+    n = B * F * h * w
+    x = synth.normal(410, shape, 1.5)
+    mean = synth.normal(411, (F,), 0.1)
+    var = np.abs(synth.normal(412, (F,))) + np.float32(0.3)
+    var[0] = np.float32(1e-13)  # below both clamps
+    gamma, beta = synth.normal(413, (F,)), synth.normal(414, (F,))
+    dx, dm, dv, dg, db = D(x), D(mean), D(var), D(gamma), D(beta)
+    xn = torch.empty(shape, dtype=torch.float32, device="cuda")
+    out = torch.empty(shape, dtype=torch.float32, device="cuda")
+    hip.bnForward(n, F, B, dx, xn, out, dm, dv, dg, db, acLEAKY)
+    d0 = synth.normal(415, shape)
+    su0 = synth.normal(416, (F,))
+    extra = ()
+    if form == "maxpool":
+        pidx = torch.empty((B, F, h // 2, w // 2), dtype=torch.int64, device="cuda")
+        pooled = torch.empty((B, F, h // 2, w // 2), dtype=torch.float32, device="cuda")
+        hip.forwardMaxPool(B, F, h // 2, w // 2, out, F, h, w, 2, 2, 0, 2, pidx, pooled)
+        extra = (pidx, D(synth.normal(417, (B, F, h // 2, w // 2))))
+    elif form == "avgpool":
+        extra = (D(synth.normal(418, (B, F))),)
+    res = []
+    for given in (True, False):
+        d, su = D(d0), D(su0)
+        md = torch.empty(F, dtype=torch.float32, device="cuda")
+        vd = torch.empty(F, dtype=torch.float32, device="cuda")
+        rest = (out, acLEAKY, xn if given else None, dx, dg, dm, dv, d, su, md, vd)
+        if form == "plain":
+            hip.bnBackward(n, F, B, *rest)
+        elif form == "maxpool":
+            hip.bnBackwardMaxPool(n, F, B, h, w, *extra, *rest)
+        else:
+            hip.bnBackwardAvgPool(n, F, B, *extra, *rest)
+        res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
+    for a, b in zip(*res):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_cifar_step_formed_xnorm_equals_stored(hip):
+    """The training step with x_norm formed again in the backward gives the
+    same bits as with x_norm stored by the forward."""
+    case("cifar step x_norm formed vs stored")
+    params = trainnet.init_params()
+    x, truth = _batch(326, 16)
+    keys = ("u_w0", "u_w1", "u_w2", "u_s0", "u_s1", "u_s2", "w0", "w1", "w2", "u_fw", "s2")
+    out = []
+    for keep in (True, False):
+        gpu = trainnet.CifarTrainer(hip, params, 16, keep_xnorm=keep)
+        gpu.forward(D(x), D(truth))
+        gpu.backward()
+        gpu.update()
+        out.append({k: gpu.host(k).copy() for k in keys})
+    for k in keys:
+        assert np.array_equal(out[0][k], out[1][k]), k
+
+
 def test_cifar_step_fused_pool_bwd_equals_the_calls(hip):
     """The training step with the pool backwards formed inside the
     batch-norm backwards (no zeroed deltas) gives the same bits as with
