@@ -520,7 +520,8 @@ int32_t tnh_bn_forward(int64_t dstSize, int64_t N, int64_t batch,
 /* No reference counterpart: tnh_bn_forward over [batch][N][h][w] followed by
  * tnh_maxpool_fwd of its output with size 2, stride 2, padding 0 (the
  * config-3 blocks), in one pass and bit for bit: xNorm and out as
- * tnh_bn_forward writes them, pooled [batch][N][h/2][w/2] and the int64
+ * tnh_bn_forward writes them (either may be NULL: not stored; the batch-norm
+ * backward can form both again), pooled [batch][N][h/2][w/2] and the int64
  * indexes (may be NULL) as the maxpool writes them; tnh_maxpool_bwd then
  * finds that geometry.  h even, w % 4 == 0, 16-byte aligned x, xNorm, out,
  * indexes, 8-byte aligned pooled. */
@@ -531,8 +532,8 @@ int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w,
                                int32_t act, float *pooled, int64_t *indexes);
 /* No reference counterpart: tnh_bn_forward over [batch][N][hw] (hw <= 64)
  * followed by tnh_avgpool_fwd of its output, in one pass and bit for bit:
- * xNorm (may be NULL) and out as tnh_bn_forward writes them, avg[b][n] the
- * plane's mean as tnh_avgpool_fwd forms it. */
+ * xNorm and out as tnh_bn_forward writes them (either may be NULL: not
+ * stored), avg[b][n] the plane's mean as tnh_avgpool_fwd forms it. */
 int32_t tnh_bn_forward_avgpool(int64_t batch, int64_t N, int64_t hw,
                                const float *x, float *xNorm, float *out,
                                const float *mean, const float *variance,
@@ -688,13 +689,16 @@ int32_t tnh_bn_backward_scale(int64_t N, int64_t dstSize, int64_t groups,
  * is the pre-normalization output, mean / variance the forward's
  * statistics.  xNorm may be NULL (here and in the _maxpool / _avgpool
  * forms): the first pass then forms x_norm from x, mean and variance as
- * tnh_bn_forward forms it (the same bits; the forward need not store it). */
+ * tnh_bn_forward forms it (the same bits; the forward need not store it).
+ * output may be NULL too when biases is given: act(scales * x_norm +
+ * biases) is formed again in the same pass (biases is read only then). */
 int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups,
                         const float *output, int32_t act, const float *xNorm,
                         const float *x, const float *scales, const float *mean,
                         const float *variance, float *delta,
                         float *scaleUpdates, float *mean_delta,
-                        float *variance_delta);
+                        float *variance_delta,
+                        const float *biases);
 /* No reference counterpart: TMaxPoolLayer.backward (2x2, stride 2) into the
  * zeroed delta of the layer below it, then tnh_bn_backward, with the
  * scatter formed inside tnh_bn_backward's first pass: the same bits as
@@ -711,7 +715,8 @@ int32_t tnh_bn_backward_maxpool(int64_t N, int64_t dstSize, int64_t groups,
                                 const float *x, const float *scales,
                                 const float *mean, const float *variance,
                                 float *delta, float *scaleUpdates,
-                                float *mean_delta, float *variance_delta);
+                                float *mean_delta, float *variance_delta,
+                                const float *biases);
 /* No reference counterpart: TAvgPoolLayer.backward (deltaIn += avgDelta /
  * hw, navgpoollayer.pas:86-100) into the zeroed delta of the layer below it,
  * then tnh_bn_backward, the average pool's spread formed inside
@@ -724,7 +729,8 @@ int32_t tnh_bn_backward_avgpool(int64_t N, int64_t dstSize, int64_t groups,
                                 const float *x, const float *scales,
                                 const float *mean, const float *variance,
                                 float *delta, float *scaleUpdates,
-                                float *mean_delta, float *variance_delta);
+                                float *mean_delta, float *variance_delta,
+                                const float *biases);
 /* TNNCuda.softmaxBatch (nncuda.pas:1056) / softmax (nsoftmaxlayer.pas:81):
  * per (batch, group) row of N values (stride apart): e = exp((x-max)/temp),
  * out = e / sum(e). */

@@ -175,12 +175,13 @@ function tnh_means(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
 function tnh_bn_backward_scale(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, scales, delta,
   scaleUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_backward(N, dstSize, groups: Int64; output: PSingle; act: LongInt; xNorm, x, scales, mean,
-  variance, delta, scaleUpdates, mean_delta, variance_delta: PSingle): LongInt; cdecl; external libtnh;
+  variance, delta, scaleUpdates, mean_delta, variance_delta, biases: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_backward_maxpool(N, dstSize, groups, h, w: Int64; poolIndexes: PInt64; poolDelta, output: PSingle;
-  act: LongInt; xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
-  variance_delta: PSingle): LongInt; cdecl; external libtnh;
+  act: LongInt; xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta,
+  biases: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_backward_avgpool(N, dstSize, groups: Int64; avgDelta, output: PSingle; act: LongInt; xNorm, x,
-  scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: PSingle): LongInt; cdecl; external libtnh;
+  scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta, biases: PSingle): LongInt; cdecl;
+  external libtnh;
 function tnh_variances(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
   means, vars: PSingle): LongInt; cdecl; external libtnh;
 function tnh_bn_statistics(srcSize, dstSize, groups: Int64; src: PSingle; offset: Int64;
@@ -412,16 +413,18 @@ type
     procedure bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
       const xNorm, scales, delta, scaleUpdates: TCUMem);
     // batchNormBackGPU with the activation derivative before it, in four launches
+    // (xNorm nil: formed from x, mean, variance; output nil: formed from x_norm, scales and biases)
     procedure bnBackward(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
-      const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem);
+      const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem;
+      const biases: TCUMem = nil);
     // backwardMaxPool (2x2, stride 2) into a zeroed delta, then bnBackward; delta is written in full
     procedure bnBackwardMaxPool(const N, dstSize, groups, h, w: SizeInt; const poolIndexes, poolDelta,
       output: TCUMem; const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates,
-      mean_delta, variance_delta: TCUMem);
+      mean_delta, variance_delta: TCUMem; const biases: TCUMem = nil);
     // avgPoolBackward into a zeroed delta, then bnBackward; delta is written in full
     procedure bnBackwardAvgPool(const N, dstSize, groups: SizeInt; const avgDelta, output: TCUMem;
       const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
-      variance_delta: TCUMem);
+      variance_delta: TCUMem; const biases: TCUMem = nil);
     procedure avgPoolForward(const batch, c, h, w: SizeInt; const input, output: TCUMem);
     procedure avgPoolBackward(const batch, c, h, w: SizeInt; const delta, deltaIn: TCUMem);
     procedure sgdUpdate(const N: SizeInt; const learningRate: T; const batch: SizeInt; const momentum, decay: T;
@@ -982,29 +985,30 @@ begin
 end;
 
 procedure TNNHip<T>.bnBackward(const N, dstSize, groups: SizeInt; const output: TCUMem; const activation: longint;
-  const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem);
+  const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta: TCUMem;
+  const biases: TCUMem);
 begin
   check(tnh_bn_backward(N, dstSize, groups, PSingle(output), activation, PSingle(xNorm), PSingle(x), PSingle(scales),
     PSingle(mean), PSingle(variance), PSingle(delta), PSingle(scaleUpdates), PSingle(mean_delta),
-    PSingle(variance_delta)));
+    PSingle(variance_delta), PSingle(biases)));
 end;
 
 procedure TNNHip<T>.bnBackwardMaxPool(const N, dstSize, groups, h, w: SizeInt; const poolIndexes, poolDelta,
   output: TCUMem; const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates,
-  mean_delta, variance_delta: TCUMem);
+  mean_delta, variance_delta: TCUMem; const biases: TCUMem);
 begin
   check(tnh_bn_backward_maxpool(N, dstSize, groups, h, w, PInt64(poolIndexes), PSingle(poolDelta), PSingle(output),
     activation, PSingle(xNorm), PSingle(x), PSingle(scales), PSingle(mean), PSingle(variance), PSingle(delta),
-    PSingle(scaleUpdates), PSingle(mean_delta), PSingle(variance_delta)));
+    PSingle(scaleUpdates), PSingle(mean_delta), PSingle(variance_delta), PSingle(biases)));
 end;
 
 procedure TNNHip<T>.bnBackwardAvgPool(const N, dstSize, groups: SizeInt; const avgDelta, output: TCUMem;
   const activation: longint; const xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
-  variance_delta: TCUMem);
+  variance_delta: TCUMem; const biases: TCUMem);
 begin
   check(tnh_bn_backward_avgpool(N, dstSize, groups, PSingle(avgDelta), PSingle(output), activation, PSingle(xNorm),
     PSingle(x), PSingle(scales), PSingle(mean), PSingle(variance), PSingle(delta), PSingle(scaleUpdates),
-    PSingle(mean_delta), PSingle(variance_delta)));
+    PSingle(mean_delta), PSingle(variance_delta), PSingle(biases)));
 end;
 
 procedure TNNHip<T>.bnBackwardScale(const N, dstSize, groups: SizeInt; const output: TCUMem;

@@ -22,6 +22,17 @@ __device__ inline float bn_norm(float x, float mean, float d) {
   const float t = x - mean;
   return t / d;
 }
+// out = act(fl(scale * x_norm) + bias) (forwardScale, forwardBias, then the
+// activation: leaky_array, nactivation.pas:234-268, or the logistic)
+__device__ inline float bn_scale_add(float s, float b, float xn) {
+  const float u = s * xn;
+  return b + u;
+}
+__device__ inline float bn_act(float v, int act) {
+  if (act == TNH_AC_LEAKY) return 0.f > v ? 0.1f * v : v;
+  if (act == TNH_AC_LOGISTIC) return 1.f / (1.f + expf(-v));
+  return v;
+}
 
 // The tree of the channel reductions' final step over one value per lane
 // (lane i adds lane i + w for w = 32, 16, ..., 1).  Called by a whole wave;

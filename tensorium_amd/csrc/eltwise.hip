@@ -76,10 +76,7 @@ struct ScaleAddOp {
   int64_t inc;
   struct Ch { float s, b; };
   __device__ Ch chan(int64_t f) const { return {s[f * inc], b[f * inc]}; }
-  __device__ float operator()(const Ch& c, float x) const {
-    const float u = c.s * x;
-    return c.b + u;
-  }
+  __device__ float operator()(const Ch& c, float x) const { return bn_scale_add(c.s, c.b, x); }
 };
 
 // The CPU normalize of TTensor.blockNormalize (ntensors.pas:8693-8718) with
@@ -99,11 +96,7 @@ struct NormOp {
   __device__ float operator()(const Ch& c, float x) const { return bn_norm(x, c.m, c.d); }
 };
 
-__device__ inline float act_fwd(float v, int act) {
-  if (act == TNH_AC_LEAKY) return 0.f > v ? 0.1f * v : v;  // leaky_array (nactivation.pas:234-268)
-  if (act == TNH_AC_LOGISTIC) return 1.f / (1.f + expf(-v));
-  return v;
-}
+__device__ inline float act_fwd(float v, int act) { return bn_act(v, act); }
 
 
 // Batch norm forward of TBaseLayer.batchNorm (nbaselayer.pas:335-368) and
@@ -213,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_pool2_kernel(NormOp norm, Sca
       if (xNorm) *reinterpret_cast<float4*>(xNorm + e) = nv;
       const float4 o = map4(sa, cs, nv);
       const float4 y = make_float4(act_fwd(o.x, ACT), act_fwd(o.y, ACT), act_fwd(o.z, ACT), act_fwd(o.w, ACT));
-      *reinterpret_cast<float4*>(out + e) = y;
+      if (out) *reinterpret_cast<float4*>(out + e) = y;
       a[4 * n] = y.x;
       a[4 * n + 1] = y.y;
       a[4 * n + 2] = y.z;
@@ -280,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void bn_fwd_avg_kernel(NormOp norm, Scale
     const float n = norm(cn, xe);
     if (xNorm) xNorm[e] = n;
     const float o = act_fwd(sa(cs, n), ACT);
-    out[e] = o;
+    if (out) out[e] = o;
     s = s + o;
   }
   for (int off = 32; off > 0; off >>= 1) s = s + __shfl_down(s, off, 64);
@@ -786,15 +779,15 @@ int bn_forward_avgpool_impl(int64_t batch, int64_t N, int64_t hw, const float* x
 #define BN_POOL2_CHECKS(who)                                                                                         \
   TNH_ARG(batch > 0 && N > 0 && h > 0 && w > 0, who ": bad sizes");                                                  \
   TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, who ": activation %d", act);        \
-  TNH_ARG(x && out && mean && variance && scales && biases && pooled, who ": NULL buffer");                          \
-  TNH_ARG(h % 2 == 0 && w % 4 == 0 && al16(x) && al16(out) && (!xNorm || al16(xNorm)) &&                             \
+  TNH_ARG(x && mean && variance && scales && biases && pooled, who ": NULL buffer");                                 \
+  TNH_ARG(h % 2 == 0 && w % 4 == 0 && al16(x) && (!out || al16(out)) && (!xNorm || al16(xNorm)) &&                  \
               (reinterpret_cast<uintptr_t>(pooled) & 7) == 0 && (!indexes || al16(indexes)),                         \
           who ": needs even h, w %% 4 == 0 and aligned tensors")
 
 #define BN_AVG_CHECKS(who)                                                                                           \
   TNH_ARG(batch > 0 && N > 0 && hw > 0 && hw <= 64, who ": bad sizes (hw <= 64)");                                   \
   TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, who ": activation %d", act);        \
-  TNH_ARG(x && out && mean && variance && scales && biases && avg, who ": NULL buffer");                             \
+  TNH_ARG(x && mean && variance && scales && biases && avg, who ": NULL buffer");                                    \
   TNH_ARG(batch * N < (int64_t(1) << 31), who ": too many planes")
 
 extern "C" int32_t tnh_bn_forward_maxpool(int64_t batch, int64_t N, int64_t h, int64_t w, const float* x,

@@ -399,11 +399,13 @@ struct BnBackOpT {
   const float* mean = nullptr;  // MVD or xn NULL: the forward's means
   const float* varN = nullptr;  // xn NULL: the forward's variances
   bool oneElem = false;         // xn NULL: one element per channel and image
-  float mu = 0.f, nd = 1.f;
+  const float* beta = nullptr;  // out NULL: the biases (out formed from x_norm)
+  float mu = 0.f, nd = 1.f, bb = 0.f;
   __device__ void begin(int64_t i, const ChanSplit&, const float*, float*) {
     g = gamma[i];
     if (MVD || !xn) mu = mean[i];
     if (!xn) nd = bn_norm_d(varN[i], oneElem);  // x_norm formed as the forward formed it
+    if (!out) bb = beta[i];
     if (vpow && blockIdx.y == 0 && threadIdx.x == 0)
       vpow[i] = pow(static_cast<double>(fmaxf(var[i], kEps)), -1.5);
   }
@@ -455,16 +457,20 @@ struct BnBackOpT {
     }
     return r;
   }
+  // the forward's output formed again from x_norm (out NULL)
+  __device__ float outOf(float xnv) const { return bn_act(bn_scale_add(g, bb, xnv), act); }
   __device__ void add(float* a, int64_t e) const {
     const float xv = (MVD || !xn) ? x[e] : 0.f;
-    delta[e] = one(a, src(e), out[e], xn ? xn[e] : bn_norm(xv, mu, nd), xv);
+    const float xnv = xn ? xn[e] : bn_norm(xv, mu, nd);
+    delta[e] = one(a, src(e), out ? out[e] : outOf(xnv), xnv, xv);
   }
   __device__ void add4(float* a, int64_t e) const {
-    const float4 d = src4(e), o = ld4(out + e);
+    const float4 d = src4(e);
     const float4 v = (MVD || !xn) ? ld4(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 xv = xn ? ld4(xn + e)
                          : make_float4(bn_norm(v.x, mu, nd), bn_norm(v.y, mu, nd), bn_norm(v.z, mu, nd),
                                        bn_norm(v.w, mu, nd));
+    const float4 o = out ? ld4(out + e) : make_float4(outOf(xv.x), outOf(xv.y), outOf(xv.z), outOf(xv.w));
     float4 r;
     r.x = one(a, d.x, o.x, xv.x, v.x);
     r.y = one(a, d.y, o.y, xv.y, v.y);
@@ -1644,12 +1650,14 @@ template <int SRC>
 int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups, int64_t w, const int64_t* pidx,
                      const float* pdel, const float* output, int32_t act, const float* xNorm, const float* x,
                      const float* scales, const float* mean, const float* variance, float* delta,
-                     float* scaleUpdates, float* mean_delta, float* variance_delta) {
+                     float* scaleUpdates, float* mean_delta, float* variance_delta, const float* biases) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(N > 0 && dstSize > 0 && groups > 0, "%s: bad sizes", who);
-  // xNorm NULL: x_norm is formed from x, mean and variance in the first pass
-  TNH_ARG(output && x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
+  // xNorm NULL: x_norm is formed from x, mean and variance in the first
+  // pass; output NULL: the activation's output from x_norm, scales, biases
+  TNH_ARG(x && scales && mean && variance && delta && scaleUpdates && mean_delta && variance_delta,
           "%s: NULL buffer", who);
+  TNH_ARG(output || biases, "%s: give the output or the biases it is formed from", who);
   TNH_ARG(act == TNH_AC_LINEAR || act == TNH_AC_LEAKY || act == TNH_AC_LOGISTIC, "%s: activation %d", who, act);
   const int64_t block = N / (dstSize * groups);
   TNH_ARG(block * dstSize * groups == N, "%s: sizes do not align", who);
@@ -1666,12 +1674,15 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   const int64_t wgs = (g.rows + g.rpw - 1) / g.rpw;
   // many short rows (or P > 64): the finals in their own launch
   const bool fused = g.rpw <= kFinRows && s.P <= 64 && wgs < (int64_t(1) << 31);
-  const bool vec = chan_vec(s, {delta, output, xNorm ? xNorm : x});
-  auto norm_in_pass = [&](auto& o) {  // x_norm from x, mean and variance
-    o.x = x;
-    o.mean = mean;
-    o.varN = variance;
-    o.oneElem = block == 1;
+  const bool vec = chan_vec(s, {delta, output ? output : x, xNorm ? xNorm : x});
+  auto norm_in_pass = [&](auto& o) {  // x_norm from x, mean and variance; out from it
+    if (!xNorm) {
+      o.x = x;
+      o.mean = mean;
+      o.varN = variance;
+      o.oneElem = block == 1;
+    }
+    if (!output) o.beta = biases;
   };
   if (fused && vec == chan_vec(s, {delta, x})) {
     // one pass: the first pass's dot and MvdOp's two sums (the same walk as
@@ -1685,7 +1696,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
     op.vpow = vpow;
     op.x = x;
     op.mean = mean;
-    if (!xNorm) norm_in_pass(op);
+    norm_in_pass(op);
     if (int st = launch_partial<3>(cx, op, s, vec, red, "chan_partial_kernel<bn_back_mvd>")) return st;
     return launch_normalize_fin(cx, N, block, dstSize, groups, delta, x, mean, variance, fin, s.P);
   }
@@ -1694,7 +1705,7 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
   op.pdel = pdel;
   op.block = static_cast<uint32_t>(block);
   op.w = static_cast<uint32_t>(w);
-  if (!xNorm) norm_in_pass(op);
+  norm_in_pass(op);
   if (fused) {
     op.var = variance;
     op.vpow = vpow;
@@ -1717,16 +1728,18 @@ int bn_backward_impl(const char* who, int64_t N, int64_t dstSize, int64_t groups
 extern "C" int32_t tnh_bn_backward(int64_t N, int64_t dstSize, int64_t groups, const float* output, int32_t act,
                                    const float* xNorm, const float* x, const float* scales, const float* mean,
                                    const float* variance, float* delta, float* scaleUpdates, float* mean_delta,
-                                   float* variance_delta) {
+                                   float* variance_delta, const float* biases) {
   return bn_backward_impl<kFromDelta>("bn_backward", N, dstSize, groups, 0, nullptr, nullptr, output, act, xNorm, x,
-                                      scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta);
+                                      scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta,
+                                      biases);
 }
 
 extern "C" int32_t tnh_bn_backward_maxpool(int64_t N, int64_t dstSize, int64_t groups, int64_t h, int64_t w,
                                            const int64_t* poolIndexes, const float* poolDelta, const float* output,
                                            int32_t act, const float* xNorm, const float* x, const float* scales,
                                            const float* mean, const float* variance, float* delta,
-                                           float* scaleUpdates, float* mean_delta, float* variance_delta) {
+                                           float* scaleUpdates, float* mean_delta, float* variance_delta,
+                                           const float* biases) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(h > 0 && w > 0 && h % 2 == 0 && w % 2 == 0 && groups > 0 && dstSize > 0 && N == groups * dstSize * h * w &&
               N < (int64_t(1) << 31),
@@ -1738,20 +1751,20 @@ extern "C" int32_t tnh_bn_backward_maxpool(int64_t N, int64_t dstSize, int64_t g
           "bn_backward_maxpool: the indexes were not written by a 2x2 stride-2 maxpool of this geometry");
   return bn_backward_impl<kFromMaxPool2>("bn_backward_maxpool", N, dstSize, groups, w, poolIndexes, poolDelta, output,
                                          act, xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
-                                         variance_delta);
+                                         variance_delta, biases);
 }
 
 extern "C" int32_t tnh_bn_backward_avgpool(int64_t N, int64_t dstSize, int64_t groups, const float* avgDelta,
                                            const float* output, int32_t act, const float* xNorm, const float* x,
                                            const float* scales, const float* mean, const float* variance,
                                            float* delta, float* scaleUpdates, float* mean_delta,
-                                           float* variance_delta) {
+                                           float* variance_delta, const float* biases) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(N > 0 && N < (int64_t(1) << 31), "bn_backward_avgpool: 0 < N < 2^31");
   TNH_ARG(avgDelta, "bn_backward_avgpool: NULL buffer");
   return bn_backward_impl<kFromAvgPool>("bn_backward_avgpool", N, dstSize, groups, 0, nullptr, avgDelta, output, act,
                                         xNorm, x, scales, mean, variance, delta, scaleUpdates, mean_delta,
-                                        variance_delta);
+                                        variance_delta, biases);
 }
 
 extern "C" int32_t tnh_softmax_head_forward(int64_t batch, int64_t F, int64_t hw, int64_t classes, const float* x,

@@ -133,9 +133,9 @@ _PROTOS = {
     "tnh_means_vars": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_means": [i64, i64, i64, vp, i64, vp],
     "tnh_bn_backward_scale": [i64, i64, i64, vp, i32, vp, vp, vp, vp],
-    "tnh_bn_backward": [i64, i64, i64, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
-    "tnh_bn_backward_maxpool": [i64, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
-    "tnh_bn_backward_avgpool": [i64, i64, i64, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_bn_backward": [i64, i64, i64, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_bn_backward_maxpool": [i64, i64, i64, i64, i64, vp, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
+    "tnh_bn_backward_avgpool": [i64, i64, i64, vp, vp, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp],
     "tnh_variances": [i64, i64, i64, vp, i64, vp, vp],
     "tnh_bn_statistics": [i64, i64, i64, vp, i64, vp, vp, vp, vp, f32],
     "tnh_means_vars_delta": [i64, i64, i64, vp, vp, i64, vp, vp, vp, vp],
@@ -619,25 +619,26 @@ class TNNHip:
         call("tnh_variances", srcSize, dstSize, groups, addr(src), offset, addr(means), addr(vars))
 
     def bnBackward(self, N, dstSize, groups, output, activation, xNorm, x, scales, mean, variance, delta,
-                   scaleUpdates, mean_delta, variance_delta):
+                   scaleUpdates, mean_delta, variance_delta, biases=None):
         """The batch-norm backward with the activation derivative before it:
         bnBackwardScale, meansAndVarsDelta and normalizeDelta in four launches."""
         call("tnh_bn_backward", N, dstSize, groups, addr(output), activation, addr(xNorm), addr(x), addr(scales),
-             addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta), addr(variance_delta))
+             addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta), addr(variance_delta),
+             addr(biases))
 
     def bnBackwardMaxPool(self, N, dstSize, groups, h, w, poolIndexes, poolDelta, output, activation, xNorm, x,
-                          scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta):
+                          scales, mean, variance, delta, scaleUpdates, mean_delta, variance_delta, biases=None):
         """backwardMaxPool (2x2, stride 2) into a zeroed delta, then bnBackward; delta is written in full."""
         call("tnh_bn_backward_maxpool", N, dstSize, groups, h, w, addr(poolIndexes), addr(poolDelta), addr(output),
              activation, addr(xNorm), addr(x), addr(scales), addr(mean), addr(variance), addr(delta),
-             addr(scaleUpdates), addr(mean_delta), addr(variance_delta))
+             addr(scaleUpdates), addr(mean_delta), addr(variance_delta), addr(biases))
 
     def bnBackwardAvgPool(self, N, dstSize, groups, avgDelta, output, activation, xNorm, x, scales, mean, variance,
-                          delta, scaleUpdates, mean_delta, variance_delta):
+                          delta, scaleUpdates, mean_delta, variance_delta, biases=None):
         """avgPoolBackward into a zeroed delta, then bnBackward; delta is written in full."""
         call("tnh_bn_backward_avgpool", N, dstSize, groups, addr(avgDelta), addr(output), activation, addr(xNorm),
              addr(x), addr(scales), addr(mean), addr(variance), addr(delta), addr(scaleUpdates), addr(mean_delta),
-             addr(variance_delta))
+             addr(variance_delta), addr(biases))
 
     def bnBackwardScale(self, N, dstSize, groups, output, activation, xNorm, scales, delta, scaleUpdates):
         """DeriveArray + addDots + forwardScale of batchNormBack in one pass

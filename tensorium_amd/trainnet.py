@@ -68,7 +68,7 @@ class CifarTrainer:
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
                  fused_wgrad=True, conv_dgrad=True, fused_head=True, fused_pool_bwd=True, fused_stats=True,
-                 keep_xnorm=False):
+                 store_bn_outputs=False):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
         im2col + NT product (the same bits).  conv_dgrad: the conv input
@@ -82,16 +82,19 @@ class CifarTrainer:
         False runs backwardMaxPool / avgPoolBackward into zeroed deltas.
         fused_stats: the batch statistics' final step is taken by the
         normalize pass (the same bits); False calls bnStatistics first.
-        keep_xnorm: the forward stores x_norm for the backward, as the
-        reference's layer does; False: the backward's first pass forms it
-        again from x, mean and variance (the same bits, two fewer passes
-        over it)."""
+        store_bn_outputs: the forward stores x_norm and the activation's
+        output for the backward, as the reference's layer does; False: the
+        backward's first pass forms both again from x, the statistics, the
+        scales and the biases (the same bits, four fewer passes over a
+        layer's activations; out{i} is then stored only where a later layer
+        reads it)."""
         import torch
 
         self.hip, self.B, self.torch = hip, batch, torch
         self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
         self.fused_pool_bwd, self.fused_stats = fused_pool_bwd, fused_stats
-        self.keep_xnorm = keep_xnorm
+        self.store_bn_outputs = store_bn_outputs
+        self._out_stored = [True] * len(BLOCKS)
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
@@ -142,7 +145,7 @@ class CifarTrainer:
             off += n
         for i, (c, f) in enumerate(BLOCKS):
             self.dims.append((c, h, f))
-            for name in ("x", "xn", "out") if keep_xnorm else ("x", "out"):
+            for name in ("x", "xn", "out") if store_bn_outputs else ("x", "out"):
                 t[f"{name}{i}"] = torch.empty((B, f, h, h), dtype=torch.float32, device=dev)
             t[f"mean{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
             t[f"var{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
@@ -192,7 +195,13 @@ class CifarTrainer:
             y = t[f"x{i}"]
             hip.conv2dForward(B, c, hh, hh, f, 3, 1, 1, h, 0, self.packed[i], None, acLINEAR, y, 0,
                               weightLayout=WEIGHTS_TAP_MAJOR)
-            xn, out = (t[f"xn{i}"] if self.keep_xnorm else None), t[f"out{i}"]
+            last = i == len(self.dims) - 1
+            # the activation's output is stored where the backward cannot form
+            # it again or a later layer reads it (the unpooled last block)
+            pooled = not last or (self.fused_head and hh * hh <= 64)
+            self._out_stored[i] = self.store_bn_outputs or not pooled
+            xn = t[f"xn{i}"] if self.store_bn_outputs else None
+            out = t[f"out{i}"] if self._out_stored[i] else None
             bnm = float(np.float32(self.bnm))
             stats = (t[f"mean{i}"], t[f"var{i}"], p[f"rm{i}"], p[f"rv{i}"], bnm)
             if self.fused_stats and self.fused_head and i == len(self.dims) - 1 and hh * hh <= 64:
@@ -274,8 +283,10 @@ class CifarTrainer:
             # gamma (forwardScale) in one pass, then the mean / variance
             # deltas and normalizeDelta (four launches)
             bn = (n, f, B)
-            rest = (t[f"out{i}"], acLEAKY, t[f"xn{i}"] if self.keep_xnorm else None, t[f"x{i}"], p[f"s{i}"],
-                    t[f"mean{i}"], t[f"var{i}"], d, p[f"u_s{i}"], t[f"md{i}"], t[f"vd{i}"])
+            out_i = t[f"out{i}"] if self._out_stored[i] else None
+            xn_i = t[f"xn{i}"] if self.store_bn_outputs else None
+            rest = (out_i, acLEAKY, xn_i, t[f"x{i}"], p[f"s{i}"], t[f"mean{i}"], t[f"var{i}"], d, p[f"u_s{i}"],
+                    t[f"md{i}"], t[f"vd{i}"], p[f"b{i}"])
             if not self.fused_pool_bwd:
                 hip.bnBackward(*bn, *rest)
             elif i == last:

@@ -14,7 +14,7 @@ import torch
 from oracle import refcpu as R
 from oracle import trainref as T
 from tensorium_amd import synth, trainnet
-from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR
+from tensorium_amd.nnhip import WEIGHTS_TAP_MAJOR, TNHError, acLEAKY, acLINEAR, acLOGISTIC
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -235,7 +235,9 @@ def test_cifar_train_step(hip, B):
     ref = T.CifarStep(params)
     loss_ref = ref.forward(x, truth)
     ref.backward()
-    gpu = trainnet.CifarTrainer(hip, params, B)
+    # the activation outputs are stored so they can be compared (the default
+    # forms them again in the backward: the same bits, checked separately)
+    gpu = trainnet.CifarTrainer(hip, params, B, store_bn_outputs=True)
     dx, dt = D(x), D(truth)
     gpu.forward(dx, dt)
     gpu.backward()
@@ -737,18 +739,21 @@ def test_cifar_step_fused_stats_equals_the_calls(hip):
         assert np.array_equal(out[0][k], out[1][k]), k
 
 
-XNORM_CASES = [(shape, form) for shape in [(16, 32, 32, 32), (8, 64, 8, 8), (3, 5, 6, 6), (6, 7, 1, 1)]
+XNORM_CASES = [(shape, form, acLEAKY) for shape in [(16, 32, 32, 32), (8, 64, 8, 8), (3, 5, 6, 6), (6, 7, 1, 1)]
                for form in ("plain", "maxpool", "avgpool") if not (form == "maxpool" and shape[2] == 1)]
+XNORM_CASES += [((4, 6, 8, 8), "plain", acLOGISTIC), ((4, 6, 8, 8), "plain", acLINEAR)]
 
 
-@pytest.mark.parametrize("shape,form", XNORM_CASES)
-def test_bn_backward_forms_xnorm(hip, shape, form):
-    """tnh_bn_backward (and its _maxpool / _avgpool forms) with xNorm NULL,
-    x_norm formed in the first pass from x, mean and variance, against the
-    same call given the x_norm that tnh_bn_forward stored: every output bit
-    for bit (planes of one element take the other variance clamp)."""
+@pytest.mark.parametrize("shape,form,act", XNORM_CASES)
+def test_bn_backward_forms_xnorm(hip, shape, form, act):
+    """tnh_bn_backward (and its _maxpool / _avgpool forms) with xNorm NULL
+    (x_norm formed in the first pass from x, mean and variance) and with
+    output NULL too (the activation's output formed from x_norm, the scales
+    and the biases), against the same call given what tnh_bn_forward stored:
+    every output bit for bit (planes of one element take the other variance
+    clamp)."""
     B, F, h, w = shape
-    case(f"bn_backward xNorm NULL {form} {shape}")
+    case(f"bn_backward xNorm / output NULL {form} {shape} act{act}")
     n = B * F * h * w
     x = synth.normal(410, shape, 1.5)
     mean = synth.normal(411, (F,), 0.1)
@@ -758,7 +763,7 @@ def test_bn_backward_forms_xnorm(hip, shape, form):
     dx, dm, dv, dg, db = D(x), D(mean), D(var), D(gamma), D(beta)
     xn = torch.empty(shape, dtype=torch.float32, device="cuda")
     out = torch.empty(shape, dtype=torch.float32, device="cuda")
-    hip.bnForward(n, F, B, dx, xn, out, dm, dv, dg, db, acLEAKY)
+    hip.bnForward(n, F, B, dx, xn, out, dm, dv, dg, db, act)
     d0 = synth.normal(415, shape)
     su0 = synth.normal(416, (F,))
     extra = ()
@@ -770,11 +775,12 @@ def test_bn_backward_forms_xnorm(hip, shape, form):
     elif form == "avgpool":
         extra = (D(synth.normal(418, (B, F))),)
     res = []
-    for given in (True, False):
+    for given in ("both", "out", "none"):
         d, su = D(d0), D(su0)
         md = torch.empty(F, dtype=torch.float32, device="cuda")
         vd = torch.empty(F, dtype=torch.float32, device="cuda")
-        rest = (out, acLEAKY, xn if given else None, dx, dg, dm, dv, d, su, md, vd)
+        rest = (None if given == "none" else out, act, xn if given == "both" else None, dx, dg, dm, dv, d, su, md,
+                vd, db)
         if form == "plain":
             hip.bnBackward(n, F, B, *rest)
         elif form == "maxpool":
@@ -782,20 +788,22 @@ def test_bn_backward_forms_xnorm(hip, shape, form):
         else:
             hip.bnBackwardAvgPool(n, F, B, *extra, *rest)
         res.append([H(t_, hip).copy() for t_ in (d, su, md, vd)])
-    for a, b in zip(*res):
-        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for other in res[1:]:
+        for a, b in zip(res[0], other):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_cifar_step_formed_xnorm_equals_stored(hip):
-    """The training step with x_norm formed again in the backward gives the
-    same bits as with x_norm stored by the forward."""
+    """The training step with x_norm and the activation outputs formed
+    again in the backward gives the same bits as with both stored by the
+    forward."""
     case("cifar step x_norm formed vs stored")
     params = trainnet.init_params()
     x, truth = _batch(326, 16)
     keys = ("u_w0", "u_w1", "u_w2", "u_s0", "u_s1", "u_s2", "w0", "w1", "w2", "u_fw", "s2")
     out = []
     for keep in (True, False):
-        gpu = trainnet.CifarTrainer(hip, params, 16, keep_xnorm=keep)
+        gpu = trainnet.CifarTrainer(hip, params, 16, store_bn_outputs=keep)
         gpu.forward(D(x), D(truth))
         gpu.backward()
         gpu.update()
