@@ -1140,21 +1140,21 @@ __global__ __launch_bounds__(256) void wgrad_reduce_wave_kernel(WgradArgs a) {
 }
 
 // The same sums when there are many output elements: one thread per element
-// adds the splits in split order, eight loads issued together (coalesced
-// along the elements).
+// adds the splits in split order, kReduceLoads loads issued together
+// (coalesced along the elements), the last round's too.
+constexpr int kReduceLoads = 16;  // 8 and 32 were slower on the config-3 step
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradArgs a) {
   const int64_t total = a.M * a.N;
   GRID_STRIDE(e, total) {
     float v = 0.f;
-    int s = 0;
-    for (; s + 8 <= a.splits; s += 8) {
-      float t[8];
+    for (int s = 0; s < a.splits; s += kReduceLoads) {
+      float t[kReduceLoads];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[j] = a.part[(s + j) * total + e];
+      for (int j = 0; j < kReduceLoads; ++j) t[j] = s + j < a.splits ? a.part[(s + j) * total + e] : 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v = v + t[j];
+      for (int j = 0; j < kReduceLoads; ++j)
+        if (s + j < a.splits) v = v + t[j];  // only the pieces, in split order
     }
-    for (; s < a.splits; ++s) v = v + a.part[s * total + e];
     const int64_t r = e / a.N, c = e - r * a.N;
     float* p = a.C + r * a.ldc + c;
     float out = a.alpha * v;
