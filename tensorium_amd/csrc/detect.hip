@@ -365,7 +365,20 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_bits_kernel(int64_t capa
   for (int j = n + threadIdx.x; j < n + 64; j += kNmsThreads) idx[j] = idx[0];
   __syncthreads();
   const uint64_t* rows = bits + static_cast<int64_t>(b) * capacity * words;
+  constexpr int kPairs = 64 * (kNmsMax / 64) / kNmsThreads;  // (member, word) pairs per thread at most
   for (int c0 = 0; c0 < n; c0 += 64) {
+    // removed |= row of every kept member, over (member, word) pairs spread
+    // over the threads: the rows of all 64 members are loaded first, before
+    // the chunk is resolved (the loads depend only on the sorted order), so
+    // their latency passes while wave 0 resolves it; the kept ones are
+    // selected afterwards
+    uint64_t r[kPairs];
+#pragma unroll
+    for (int u = 0; u < kPairs; ++u) {
+      const int p = threadIdx.x + u * kNmsThreads;
+      const int l = p / W, w = p - (p / W) * W;
+      r[u] = rows[static_cast<int64_t>(idx[c0 + (l & 63)]) * words + w];
+    }
     if (wave == 0) {
       const int l = lane;
       const bool in = c0 + l < n;
@@ -373,19 +386,20 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_bits_kernel(int64_t capa
       const bool alive = in && !((removed[di >> 6] >> (di & 63)) & 1);
       // the later chunk members l suppresses: 64 independent loads with no
       // condition around them (a load inside a lane-dependent branch waits
-      // for every outstanding load at the branch's join), masked afterwards
+      // for every outstanding load at the branch's join), masked afterwards;
+      // each reads the 32-bit half of the word that holds the member's bit
       uint64_t mask = 0;
-      const uint64_t* row = rows + static_cast<int64_t>(idx[c0 + l]) * words;
+      const uint32_t* row = reinterpret_cast<const uint32_t*>(rows + static_cast<int64_t>(idx[c0 + l]) * words);
 #pragma unroll
       for (int g = 0; g < 64; g += 16) {  // 16 loads in flight, then their bits
         int dt[16];
-        uint64_t wv[16];
+        uint32_t wv[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) dt[u] = idx[c0 + g + u];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) wv[u] = row[dt[u] >> 6];
+        for (int u = 0; u < 16; ++u) wv[u] = row[dt[u] >> 5];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) mask |= ((wv[u] >> (dt[u] & 63)) & 1) << (g + u);
+        for (int u = 0; u < 16; ++u) mask |= static_cast<uint64_t>((wv[u] >> (dt[u] & 31)) & 1u) << (g + u);
       }
       const int rest = n - c0;  // chunk members present
       const uint64_t present = rest >= 64 ? ~uint64_t(0) : (uint64_t(1) << rest) - 1;
@@ -404,22 +418,13 @@ __global__ __launch_bounds__(kNmsThreads) void yolo_nms_bits_kernel(int64_t capa
     }
     __syncthreads();
     const uint64_t kept = keptBits;
-    // removed |= row of every kept member: (member, word) pairs spread over
-    // the threads, each thread's loads issued before its first LDS update
-    constexpr int kPairs = 64 * (kNmsMax / 64) / kNmsThreads;  // pairs per thread at most
-    uint64_t r[kPairs];
 #pragma unroll
     for (int u = 0; u < kPairs; ++u) {
       const int p = threadIdx.x + u * kNmsThreads;
-      const int l = p / W, w = p - (p / W) * W;
+      const int l = p / W;
       const bool use = p < 64 * W && ((kept >> l) & 1);  // kept members are < n
-      const uint64_t v = rows[static_cast<int64_t>(idx[c0 + (l & 63)]) * words + w];
-      r[u] = use ? v : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < kPairs; ++u) {
-      const int p = threadIdx.x + u * kNmsThreads;
-      if (r[u]) atomicOr(reinterpret_cast<unsigned long long*>(&removed[p % W]), static_cast<unsigned long long>(r[u]));
+      if (use && r[u])
+        atomicOr(reinterpret_cast<unsigned long long*>(&removed[p % W]), static_cast<unsigned long long>(r[u]));
     }
     __syncthreads();
   }
