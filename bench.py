@@ -429,9 +429,9 @@ def extra_train(hip, steps, warmup, cpu_steps):
     3x32x32 U[0,1) images with one-hot labels, batch 128, replayed from a HIP
     graph; the CPU oracle's step timed beside it."""
     import numpy as np
-    import torch
 
     from tensorium_amd import synth, trainnet
+    from tensorium_amd.nnhip import DeviceArray
 
     B = 128
     x = synth.uniform(21, (B, 3, 32, 32))
@@ -440,8 +440,8 @@ def extra_train(hip, steps, warmup, cpu_steps):
     truth[np.arange(B), lab] = 1
     params = trainnet.init_params()
     tr = trainnet.CifarTrainer(hip, params, B)
-    dx, dt = torch.from_numpy(x).cuda(), torch.from_numpy(truth).cuda()
-    torch.cuda.synchronize()
+    # the trainer and its inputs on the library's own memory (no torch)
+    dx, dt = DeviceArray.from_numpy(x), DeviceArray.from_numpy(truth)
     for _ in range(max(1, warmup)):
         tr.step(dx, dt)
     loss0 = float(tr.cost())

@@ -227,6 +227,77 @@ class DeviceBuffer:
         return self.ptr or 0
 
 
+def _free_device(ptr):
+    """Finalizer of a DeviceArray's allocation (the library may already be
+    gone at interpreter exit; then the process releases the memory)."""
+    if _lib is not None and ptr:
+        _lib.tnh_free(ptr)
+
+
+class DeviceArray:
+    """A shaped, typed device array in memory from tnh_malloc (the library's
+    own allocator, TNNCuda.createDeviceBuffer), for Python callers that use
+    no other GPU framework: flat slices and reshaped views share the memory,
+    uploads and downloads go through tnh_h2d / tnh_d2h, which are ordered on
+    the context stream.  Any entry point that takes a device buffer takes
+    it (data_ptr)."""
+
+    is_cuda = True
+
+    def __init__(self, shape, dtype=np.float32, _base=None, _ptr=None):
+        import weakref
+
+        self.shape = (int(shape),) if np.isscalar(shape) else tuple(int(d) for d in shape)
+        self.dtype = np.dtype(dtype)
+        self._base = _base  # keeps the owning allocation alive
+        if _ptr is not None:
+            self.ptr = _ptr
+            return
+        p = vp()
+        call("tnh_malloc", max(self.numel(), 1) * self.dtype.itemsize, C.byref(p))
+        self.ptr = p.value
+        weakref.finalize(self, _free_device, self.ptr)
+
+    @classmethod
+    def from_numpy(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        d.copy_from(a)
+        return d
+
+    def numel(self):
+        return int(np.prod(self.shape))
+
+    def data_ptr(self):
+        return self.ptr
+
+    def view(self, *shape):
+        """The same memory with another shape of as many elements."""
+        shape = tuple(shape[0]) if len(shape) == 1 and not np.isscalar(shape[0]) else shape
+        if int(np.prod(shape)) != self.numel():
+            raise ValueError(f"view {shape} of {self.shape}")
+        return DeviceArray(shape, self.dtype, self._base or self, self.ptr)
+
+    def __getitem__(self, sl):
+        """A flat slice a[lo:hi] of a one-dimensional array, sharing memory."""
+        if len(self.shape) != 1 or not isinstance(sl, slice) or sl.step not in (None, 1):
+            raise TypeError("DeviceArray supports contiguous slices of one-dimensional arrays only")
+        lo, hi, _ = sl.indices(self.shape[0])
+        hi = max(hi, lo)
+        return DeviceArray((hi - lo,), self.dtype, self._base or self, self.ptr + lo * self.dtype.itemsize)
+
+    def copy_from(self, a):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        if a.size != self.numel():
+            raise ValueError(f"copy of {a.size} elements into {self.numel()}")
+        call("tnh_h2d", self.ptr, a.ctypes.data, a.nbytes)
+
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        call("tnh_d2h", out.ctypes.data, self.ptr, out.nbytes)
+        return out
+
+
 def addr(buf):
     """Device address of a buffer argument (None -> NULL)."""
     if buf is None:

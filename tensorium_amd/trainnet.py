@@ -22,8 +22,10 @@ with the layer semantics of the reference CPU path:
     SGD with momentum and decay; BN biases receive no gradient (the
     reference's batchNormBack leaves bias_updates alone).
 
-Every operation is one C-ABI call on the library stream; buffers are device
-torch tensors (memory only).  Conv weights are kept in the reference layout
+Every operation is one C-ABI call on the library stream; buffers come from
+the library's own allocator (nnhip.DeviceArray over tnh_malloc), so the
+trainer needs no other GPU framework; its inputs may be any device buffer
+(a DeviceArray or a torch tensor).  Conv weights are kept in the reference layout
 [F][C*9] for the backward GEMMs and repacked tap-major for the forward.
 """
 from __future__ import annotations
@@ -32,7 +34,7 @@ import math
 
 import numpy as np
 
-from .nnhip import WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR
+from .nnhip import WEIGHTS_TAP_MAJOR, DeviceArray, acLEAKY, acLINEAR
 
 BLOCKS = ((3, 32), (32, 64), (64, 128))  # (C_in, F) of the conv-BN-leaky blocks
 CLASSES = 10
@@ -88,15 +90,12 @@ class CifarTrainer:
         scales and the biases (the same bits, four fewer passes over a
         layer's activations; out{i} is then stored only where a later layer
         reads it)."""
-        import torch
-
-        self.hip, self.B, self.torch = hip, batch, torch
+        self.hip, self.B = hip, batch
         self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
         self.fused_pool_bwd, self.fused_stats = fused_pool_bwd, fused_stats
         self.store_bn_outputs = store_bn_outputs
         self._out_stored = [True] * len(BLOCKS)
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
-        dev = "cuda"
         # Parameters live in two arenas (weights with decay; biases and
         # scales without), their momentum buffers in two more with the same
         # offsets, so each SGD step is two launches over all layers: the
@@ -107,22 +106,22 @@ class CifarTrainer:
         for group, keys in (("w", [k for k in params if k[0] == "w"] + ["fw"]),
                             ("p", [k for k in params if k[0] in "sb"] + ["fb"])):
             n = sum(params[k].size for k in keys)
-            flat = torch.empty(n, dtype=torch.float32, device=dev)
-            uflat = torch.empty(n, dtype=torch.float32, device=dev)
+            flat = DeviceArray(n)
+            uflat = DeviceArray(n)
             off = 0
             for k in keys:
                 v = np.ascontiguousarray(params[k])
-                flat[off:off + v.size].copy_(torch.from_numpy(v.ravel()))
-                uflat[off:off + v.size].copy_(torch.from_numpy(np.ascontiguousarray(params["u_" + k]).ravel()))
+                flat[off:off + v.size].copy_from(v.ravel())
+                uflat[off:off + v.size].copy_from(np.ascontiguousarray(params["u_" + k]).ravel())
                 self.p[k] = flat[off:off + v.size].view(v.shape)
                 self.p["u_" + k] = uflat[off:off + v.size].view(v.shape)
                 off += v.size
             self.arena[group] = (flat, uflat)
         for k, v in params.items():
             if k not in self.p:  # rolling statistics
-                self.p[k] = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
-        self.packed = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
-        self.flipped = [torch.empty_like(self.p[f"w{i}"]) for i in range(len(BLOCKS))]
+                self.p[k] = DeviceArray.from_numpy(np.ascontiguousarray(v, dtype=np.float32))
+        self.packed = [DeviceArray(self.p[f"w{i}"].shape) for i in range(len(BLOCKS))]
+        self.flipped = [DeviceArray(self.p[f"w{i}"].shape) for i in range(len(BLOCKS))]
         B = batch
         t = {}
         h = size
@@ -137,7 +136,7 @@ class CifarTrainer:
                 zsizes.append(("dx", i, (B, c, hh, hh)))
             if i < len(BLOCKS) - 1:
                 hh //= 2
-        self.zero_arena = torch.empty(sum(int(np.prod(sh)) for _, _, sh in zsizes), dtype=torch.float32, device=dev)
+        self.zero_arena = DeviceArray(sum(int(np.prod(sh)) for _, _, sh in zsizes))
         off = 0
         for name, i, sh in zsizes:
             n = int(np.prod(sh))
@@ -146,27 +145,26 @@ class CifarTrainer:
         for i, (c, f) in enumerate(BLOCKS):
             self.dims.append((c, h, f))
             for name in ("x", "xn", "out") if store_bn_outputs else ("x", "out"):
-                t[f"{name}{i}"] = torch.empty((B, f, h, h), dtype=torch.float32, device=dev)
-            t[f"mean{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
-            t[f"var{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
-            t[f"md{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
-            t[f"vd{i}"] = torch.empty(f, dtype=torch.float32, device=dev)
+                t[f"{name}{i}"] = DeviceArray((B, f, h, h))
+            t[f"mean{i}"] = DeviceArray(f)
+            t[f"var{i}"] = DeviceArray(f)
+            t[f"md{i}"] = DeviceArray(f)
+            t[f"vd{i}"] = DeviceArray(f)
             if i < len(BLOCKS) - 1:
-                t[f"pool{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.float32, device=dev)
-                t[f"pidx{i}"] = torch.empty((B, f, h // 2, h // 2), dtype=torch.int64, device=dev)
+                t[f"pool{i}"] = DeviceArray((B, f, h // 2, h // 2))
+                t[f"pidx{i}"] = DeviceArray((B, f, h // 2, h // 2), np.int64)
                 h //= 2
         self.final_hw = h
         F = BLOCKS[-1][1]
-        t["avg"] = torch.empty((B, F), dtype=torch.float32, device=dev)
-        t["avg_delta"] = torch.empty((B, F), dtype=torch.float32, device=dev)
-        t["logits"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
-        t["prob"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
-        t["fc_delta"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
-        t["err"] = torch.empty((B, CLASSES), dtype=torch.float32, device=dev)
+        t["avg"] = DeviceArray((B, F))
+        t["avg_delta"] = DeviceArray((B, F))
+        t["logits"] = DeviceArray((B, CLASSES))
+        t["prob"] = DeviceArray((B, CLASSES))
+        t["fc_delta"] = DeviceArray((B, CLASSES))
+        t["err"] = DeviceArray((B, CLASSES))
         colmax = max(c * 9 * (hh * hh) for (c, hh, f) in self.dims)
-        t["col"] = torch.empty(B * colmax, dtype=torch.float32, device=dev)
+        t["col"] = DeviceArray(B * colmax)
         self.t = t
-        torch.cuda.synchronize()
         self._pack()
 
     def _pack_layers(self):
@@ -353,7 +351,7 @@ class CifarTrainer:
         eager steps).  Each replay() then trains on the same buffers
         (contents may change)."""
         hip = self.hip
-        self.torch.cuda.synchronize()
+        hip.finish()
         hip.resetStream()
         self.step(x, truth)
         hip.finish()
@@ -375,10 +373,10 @@ class CifarTrainer:
         """Sum of the softmax cross-entropy errors of the last forward
         (TSoftmaxLayer cost[0] = loss.Sum(), read by TNNet.cost)."""
         self.hip.finish()
-        err = self.t["err"].cpu().numpy()
+        err = self.t["err"].numpy()
         return np.float32(err.astype(np.float64).sum())
 
     def host(self, name):
         self.hip.finish()
         src = self.p if name in self.p else self.t
-        return src[name].cpu().numpy()
+        return src[name].numpy()

@@ -61,3 +61,18 @@ def test_oracle_is_not_linked_into_the_product():
 
     data = open(nnhip.LIB_PATH, "rb").read()
     assert b"librefcpu" not in data and b"ref_sgemm" not in data
+
+
+def test_trainer_and_mirror_import_without_torch():
+    """The Python mirror and the config-3 trainer run on the library's own
+    memory: importing them loads no torch (the tests and bench.py use torch
+    only as plumbing around them)."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path.insert(0, %r); import tensorium_amd.nnhip, tensorium_amd.trainnet; "
+            "print('torch' in sys.modules)" % root)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-500:]
+    assert r.stdout.strip() == "False"

@@ -73,3 +73,33 @@ def test_sgemm_on_library_buffers(hip):
     finally:
         for t in (a, bb, c):
             hip.freeDeviceBuffer(t)
+
+
+def test_config3_trainer_on_library_memory(hip):
+    """The config-3 trainer allocates everything through tnh_malloc
+    (DeviceArray): one step on DeviceArray inputs, loss and updated weights
+    against the oracle's step within the per-tensor bound."""
+    from oracle import trainref as T
+    from tensorium_amd import trainnet
+    from tensorium_amd.nnhip import DeviceArray
+
+    case("devmem config-3 step B16")
+    B = 16
+    x = synth.uniform(505, (B, 3, 32, 32))
+    lab = (synth.splitmix64(506, B) % np.uint64(10)).astype(np.int64)
+    truth = np.zeros((B, 10), np.float32)
+    truth[np.arange(B), lab] = 1
+    params = trainnet.init_params()
+    ref = T.CifarStep(params)
+    loss_ref = ref.forward(x, truth)
+    ref.backward()
+    ref.update(B)
+    gpu = trainnet.CifarTrainer(hip, params, B)
+    assert all(isinstance(v, DeviceArray) for v in list(gpu.p.values()) + list(gpu.t.values()))
+    gpu.forward(DeviceArray.from_numpy(x), DeviceArray.from_numpy(truth))
+    gpu.backward()
+    loss = gpu.cost()
+    gpu.update()
+    assert abs(float(loss) - float(loss_ref)) <= 1e-5 * abs(float(loss_ref))
+    for k in ("w0", "w1", "w2", "fw", "s1"):
+        assert R.rel_err(gpu.host(k), ref.p[k]) <= 1e-5, k
