@@ -838,7 +838,7 @@ def main():
     import torch
 
     from tensorium_amd import darknet, synth
-    from tensorium_amd.nnhip import TNNHip
+    from tensorium_amd.nnhip import DeviceArray, TNNHip
 
     hip = TNNHip(0)
     hip.useTorchStream()  # one ordered stream for torch's buffers and the kernels
@@ -877,8 +877,7 @@ def main():
 
     def run(batch, steps, warmup):
         net = darknet.Network(hip, layers, batch, weights, layout=layout_for(batch))
-        x = torch.from_numpy(synth.uniform(7, (batch, 3, args.size, args.size))).cuda()
-        torch.cuda.synchronize()
+        x = DeviceArray.from_numpy(synth.uniform(7, (batch, 3, args.size, args.size)))
         ms, wall = time_forward(hip, net, x, steps, warmup, graph=not args.eager)
         return net, x, ms, wall
 
@@ -900,7 +899,7 @@ def main():
     conv_ms = sum(stats[k]["ms"] for k in conv_kinds)
     # image 0's head convolutions as the timed network computed them (the
     # profile pass above is one more eager forward of the same input)
-    gpu_heads = {i: net.output(i)[0:1].contiguous().cpu().numpy() for i in HEADS}
+    gpu_heads = {i: net.output(i)[0:1] for i in HEADS}
     del net, x
     torch.cuda.empty_cache()
 

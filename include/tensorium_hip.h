@@ -105,6 +105,12 @@ int32_t tnh_event_elapsed_ms(void *start, void *stop, float *ms);
  * from spares allocated by tnh_init (4 streams) or on a stream's first eager
  * reduction. */
 int32_t tnh_stream_wait_event(void *ev);
+/* No TNNCuda counterpart: a second stream (default priority, non-blocking)
+ * for tnh_set_stream, so a caller with no other GPU runtime can fork work as
+ * above.  tnh_stream_destroy waits for the stream's work, then destroys it;
+ * it refuses the context's own stream and the selected one. */
+int32_t tnh_stream_create(void **stream);
+int32_t tnh_stream_destroy(void *stream);
 
 /* ---- GEMM ------------------------------------------------------------- */
 /* TNNCuda.gemm (nncuda.pas:624) / cblas_sgemm (ntensors.pas:2231):

@@ -69,6 +69,8 @@ function tnh_event_create(ev: PPointer): LongInt; cdecl; external libtnh;
 function tnh_event_destroy(ev: Pointer): LongInt; cdecl; external libtnh;
 function tnh_event_record(ev: Pointer): LongInt; cdecl; external libtnh;
 function tnh_stream_wait_event(ev: Pointer): LongInt; cdecl; external libtnh;
+function tnh_stream_create(stream: PPointer): LongInt; cdecl; external libtnh;
+function tnh_stream_destroy(stream: Pointer): LongInt; cdecl; external libtnh;
 function tnh_event_elapsed_ms(start, stop: Pointer; ms: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgemm(transA, transB: LongInt; M, N, K: Int64; alpha: Single; A: PSingle; aOff, lda: Int64;
   B: PSingle; bOff, ldb: Int64; beta: Single; C: PSingle; cOff, ldc: Int64): LongInt; cdecl; external libtnh;

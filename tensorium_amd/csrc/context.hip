@@ -333,6 +333,27 @@ extern "C" int32_t tnh_event_record(void* ev) {
   return hip_status(hipEventRecord(static_cast<hipEvent_t>(ev), cx->stream), "hipEventRecord");
 }
 
+extern "C" int32_t tnh_stream_create(void** stream) {
+  TNH_REQUIRE_CTX(cx);
+  TNH_ARG(stream != nullptr, "stream_create: NULL");
+  hipStream_t s = nullptr;  // default priority, like the context's own stream
+  if (int st = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return st;
+  *stream = s;
+  return TNH_OK;
+}
+
+extern "C" int32_t tnh_stream_destroy(void* stream) {
+  TNH_REQUIRE_CTX(cx);
+  if (!stream) return TNH_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TNH_ARG(s != cx->own_stream && s != cx->tune_stream, "stream_destroy: the context's own stream");
+  TNH_ARG(s != cx->stream, "stream_destroy: the stream is selected (tnh_reset_stream first)");
+  // its work ends first: the scratch kept for this handle may go to a later
+  // stream that gets the same handle
+  if (int st = hip_status(hipStreamSynchronize(s), "hipStreamSynchronize")) return st;
+  return hip_status(hipStreamDestroy(s), "hipStreamDestroy");
+}
+
 extern "C" int32_t tnh_stream_wait_event(void* ev) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(ev != nullptr, "stream_wait_event: NULL");

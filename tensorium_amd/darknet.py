@@ -33,7 +33,7 @@ import os
 import numpy as np
 
 from . import synth
-from .nnhip import WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR, acLEAKY, acLINEAR, acLOGISTIC
+from .nnhip import WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR, DeviceArray, acLEAKY, acLINEAR, acLOGISTIC
 
 CFG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cfg")
 _ACT = {"leaky": acLEAKY, "linear": acLINEAR, "logistic": acLOGISTIC}
@@ -191,7 +191,10 @@ def pass_batch(layers, batch, max_pass_batch=None):
 
 
 class Network:
-    """Inference runner over the C ABI; buffers are device torch tensors.
+    """Inference runner over the C ABI.  Weights and activations live in
+    DeviceArrays (the library's own allocator, tnh_malloc); the input may be
+    any device buffer the entry points take (a DeviceArray or a torch tensor
+    on the device, ready before forward() is called).
 
     A batch whose activations would exceed the 2 GiB a kernel call addresses
     runs as consecutive passes of pass_batch() images over buffers sized for
@@ -200,8 +203,7 @@ class Network:
 
     def __init__(self, hip, layers, batch, weights, device="cuda", fuse=True, route_mode="image", pack=True,
                  layout="nchw", fuse_heads=True, max_pass_batch=None):
-        import torch
-
+        # `device` names the context's GPU, the one tnh_init selected
         if layout not in ("nchw", "nhwc"):
             raise ValueError(f"layout {layout!r}")
         if route_mode not in ("image", "reference"):
@@ -224,7 +226,6 @@ class Network:
         self.layout = layout
         if layout == "nhwc":
             pack = True  # the channels-last kernels read tap-major weights
-        self.torch = torch
         use = consumers(layers)
         self.fused = set()  # conv indices whose shortcut is fused
         if fuse:
@@ -238,15 +239,14 @@ class Network:
         self.w = {}
         for i, (w, b) in weights.items():
             L = layers[i]
-            dw = torch.from_numpy(np.ascontiguousarray(w)).to(device)
+            dw = DeviceArray.from_numpy(np.ascontiguousarray(w, dtype=np.float32))
             wl = WEIGHTS_REFERENCE
             if pack and L["size"] > 1:
-                packed = torch.empty_like(dw)
-                torch.cuda.synchronize()
+                packed = DeviceArray(dw.shape)
                 hip.packConvWeights(L["filters"], L["in"][0], L["size"], dw, packed)
                 hip.finish()
                 dw, wl = packed, WEIGHTS_TAP_MAJOR
-            self.w[i] = (dw, torch.from_numpy(np.ascontiguousarray(b)).to(device), wl)
+            self.w[i] = (dw, DeviceArray.from_numpy(np.ascontiguousarray(b, dtype=np.float32)), wl)
         self.out = [None] * len(layers)
         self.input_shape = (self.full_batch,) + layers[0]["in"]
         self.up_fused, self.yolo_fused = set(), set()
@@ -279,7 +279,7 @@ class Network:
             for L in layers:
                 if L["type"] == "route" and len(L["srcs"]) > 1:
                     C, h, w = L["out"]
-                    buf = torch.empty((1, C, h, w), dtype=torch.float32, device=device)
+                    buf = DeviceArray((1, C, h, w))
                     self.out[L["index"]] = buf
                     off, copies = 0, []
                     for s_ in L["srcs"]:
@@ -298,8 +298,7 @@ class Network:
             if i in self.fused or self.out[i] is not None:
                 continue  # writes into the shortcut's buffer / a route buffer
             C, h, w = L["out"]
-            self.out[i] = placed[i] if i in placed else torch.empty((batch, C, h, w), dtype=torch.float32,
-                                                                     device=device)
+            self.out[i] = placed[i] if i in placed else DeviceArray((batch, C, h, w))
         self._full_heads(device)
 
     def _full_heads(self, device):
@@ -309,8 +308,7 @@ class Network:
         if self.pass_batch < self.full_batch:
             for L in self.layers:
                 if L["type"] == "yolo":
-                    self.out[L["index"]] = self.torch.empty((self.full_batch,) + L["out"], dtype=self.torch.float32,
-                                                            device=device)
+                    self.out[L["index"]] = DeviceArray((self.full_batch,) + L["out"])
         self.batch = self.full_batch
 
     # -- channels-last storage plan --------------------------------------------
@@ -329,7 +327,7 @@ class Network:
         input owner that is a convolution, shortcut or upsample not placed
         elsewhere writes straight into its channel slice; other inputs are
         copied (tnh_copy_channels).  Yolo outputs are NCHW head tensors."""
-        torch, layers, B = self.torch, self.layers, self.batch
+        layers, B = self.layers, self.batch
         L0 = layers[0]
         if L0["type"] != "convolutional" or L0["size"] != 3 or L0["in"][0] > 4:
             raise NotImplementedError("channels-last networks start with a 3x3 convolution on <= 4 channels")
@@ -340,7 +338,7 @@ class Network:
         for L in layers:
             if L["type"] == "route" and len(L["srcs"]) > 1:
                 C, h, w = L["out"]
-                buf = torch.empty((B, h, w, C), dtype=torch.float32, device=device)
+                buf = DeviceArray((B, h, w, C))
                 self.store[L["index"]] = (buf, 0, C)
                 off, copies = 0, []
                 for s_ in L["srcs"]:
@@ -357,12 +355,12 @@ class Network:
             i, t = L["index"], L["type"]
             if t == "yolo":
                 C, h, w = L["out"]
-                self.out[i] = torch.empty((B, C, h, w), dtype=torch.float32, device=device)
+                self.out[i] = DeviceArray((B, C, h, w))
                 continue
             if (t == "route" and len(L["srcs"]) == 1) or i in self.fused or i in self.store or i in self.up_fused:
                 continue  # (an upsample-fused convolution stores only the upsample's output)
             C, h, w = L["out"]
-            self.store[i] = (torch.empty((B, h, w, C), dtype=torch.float32, device=device), 0, C)
+            self.store[i] = (DeviceArray((B, h, w, C)), 0, C)
         for L in layers:  # nothing may read a yolo head as an activation
             srcs = L.get("srcs", []) + ([L["src"]] if "src" in L else [])
             if L["index"] > 0 and L["type"] != "route":
@@ -398,20 +396,22 @@ class Network:
         return self.store[self._owner(i)]
 
     def output(self, i):
-        """Layer i's output as a [B, C, h, w] tensor (a view in NCHW mode, a
-        permuted view of the channel slice in NHWC mode)."""
+        """Layer i's output copied to the host as a [B, C, h, w] numpy array
+        (in NHWC mode: its channel slice of the channels-last storage,
+        transposed).  Waits for the context stream."""
         if self.layers[i]["type"] == "yolo":
-            return self.buffer(i)
+            return self.buffer(i).numpy()
         if self.pass_batch < self.full_batch:
             raise ValueError(f"the batch runs in passes of {self.pass_batch} images: only the yolo outputs "
                              "cover the whole batch")
         if self.layout == "nchw":
-            return self.buffer(i)
+            return self.buffer(i).numpy()
         if i in self.up_fused:
             raise ValueError(f"layer {i} stores only its upsampled output (layer {i + 1})")
         t, off, pix = self.nhwc_store(i)
         C = self.layers[i]["out"][0]
-        return t.view(self.batch, t.shape[1], t.shape[2], pix)[..., off:off + C].permute(0, 3, 1, 2)
+        a = t.numpy().reshape(self.batch, t.shape[1], t.shape[2], pix)
+        return np.ascontiguousarray(a[..., off:off + C].transpose(0, 3, 1, 2))
 
     def buffer(self, i):
         L = self.layers[i]
@@ -488,12 +488,12 @@ class Network:
         stream waits for it and runs the tail, and the main stream waits for
         every tail's end event after the last layer (also under graph
         capture, where the events become the graph's edges)."""
-        hip, torch = self.hip, self.torch
+        hip = self.hip
         if self._side is None:
-            self._side = torch.cuda.Stream()  # default priority
+            self._side = hip.streamCreate()  # default priority
             self._events = {s_: (hip.eventCreate(), hip.eventCreate()) for s_ in tails}
         main = hip.stream
-        side = self._side.cuda_stream
+        side = self._side
         heads, joins = [], []
         prev = x
         skip = -1
@@ -669,7 +669,6 @@ class Network:
         graph on the library's own stream (after an eager pass has tuned the
         kernels); replay() then launches the whole network at once."""
         hip = self.hip
-        self.torch.cuda.synchronize()
         hip.resetStream()
         if getattr(self, "_tuned", False):
             # one eager pass on the streams the capture uses: their split-K
@@ -701,7 +700,6 @@ class Network:
         (boxes [D, 4] in image pixels (or relative), objectness [D],
         prob [D, classes]) as numpy arrays: only the detection list leaves
         the GPU."""
-        torch = self.torch
         yl = [L for L in self.layers if L["type"] == "yolo"]
         if not yl:
             raise ValueError("network has no yolo layer")
@@ -713,11 +711,8 @@ class Network:
         B = self.batch
         key = (capacity, classes)
         if getattr(self, "_det_bufs", (None,))[0] != key:
-            dev = self.out[yl[0]["index"]].device
-            self._det_bufs = (key, torch.empty((B, capacity, 4), dtype=torch.float32, device=dev),
-                              torch.empty((B, capacity), dtype=torch.float32, device=dev),
-                              torch.empty((B, capacity, classes), dtype=torch.float32, device=dev),
-                              torch.empty(B, dtype=torch.int32, device=dev))
+            self._det_bufs = (key, DeviceArray((B, capacity, 4)), DeviceArray((B, capacity)),
+                              DeviceArray((B, capacity, classes)), DeviceArray(B, np.int32))
         _, boxes, obj, prob, counts = self._det_bufs
         self.hip.yoloDetections(B, [self.out[L["index"]] for L in yl], [L["out"][1:] for L in yl], n, classes,
                                 [L["anchors"] for L in yl], W, H, img_w, img_h, thresh, relative, letter, capacity,
@@ -725,11 +720,10 @@ class Network:
         if nms is not None:
             self.hip.yoloNmsSort(B, classes, capacity, boxes, prob, counts, nms)
         self.hip.finish()
-        cnt = counts.cpu().numpy()
+        cnt = counts.numpy()
         if (cnt > capacity).any():
             raise ValueError(f"{int(cnt.max())} detections exceed the capacity {capacity}")
-        return [(boxes[b, :c].cpu().numpy(), obj[b, :c].cpu().numpy(), prob[b, :c].cpu().numpy())
-                for b, c in enumerate(cnt)]
+        return [(boxes[b, :c].numpy(), obj[b, :c].numpy(), prob[b, :c].numpy()) for b, c in enumerate(cnt)]
 
     def head_convs(self):
         """Indices of the convolutions feeding the yolo layers (pre-logistic)."""

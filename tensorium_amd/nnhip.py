@@ -77,6 +77,8 @@ _PROTOS = {
     "tnh_event_destroy": [vp],
     "tnh_event_record": [vp],
     "tnh_stream_wait_event": [vp],
+    "tnh_stream_create": [C.POINTER(vp)],
+    "tnh_stream_destroy": [vp],
     "tnh_event_elapsed_ms": [vp, vp, C.POINTER(f32)],
     "tnh_sgemm": [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64],
     "tnh_sgemm_strided_batched": [i32, i32, i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64,
@@ -278,13 +280,35 @@ class DeviceArray:
             raise ValueError(f"view {shape} of {self.shape}")
         return DeviceArray(shape, self.dtype, self._base or self, self.ptr)
 
-    def __getitem__(self, sl):
-        """A flat slice a[lo:hi] of a one-dimensional array, sharing memory."""
-        if len(self.shape) != 1 or not isinstance(sl, slice) or sl.step not in (None, 1):
-            raise TypeError("DeviceArray supports contiguous slices of one-dimensional arrays only")
-        lo, hi, _ = sl.indices(self.shape[0])
-        hi = max(hi, lo)
-        return DeviceArray((hi - lo,), self.dtype, self._base or self, self.ptr + lo * self.dtype.itemsize)
+    def __getitem__(self, key):
+        """A contiguous block sharing the memory: integers on some axes, one
+        range on one axis, with every axis the block spans after it whole
+        (a[b], a[c0:c1], a[b, :n], a[:, lo:hi] of a batch of one)."""
+        key = key if isinstance(key, tuple) else (key,)
+        if len(key) > len(self.shape):
+            raise IndexError(f"{len(key)} indexes into {len(self.shape)} axes")
+        key = key + (slice(None),) * (len(self.shape) - len(key))
+        strides = [int(np.prod(self.shape[a + 1:])) for a in range(len(self.shape))]
+        off, shape, outer = 0, [], 1
+        for n, st, k in zip(self.shape, strides, key):
+            if isinstance(k, (int, np.integer)):
+                i = int(k) + n if k < 0 else int(k)
+                if not 0 <= i < n:
+                    raise IndexError(f"index {k} of an axis of {n}")
+                if outer > 1 and n > 1:
+                    raise TypeError("the selected block is not contiguous")
+                off += i * st
+            elif isinstance(k, slice) and k.step in (None, 1):
+                lo, hi, _ = k.indices(n)
+                m = max(hi - lo, 0)
+                if outer > 1 and m != n:
+                    raise TypeError("the selected block is not contiguous")
+                off += lo * st
+                shape.append(m)
+                outer *= m
+            else:
+                raise TypeError(f"unsupported index {k!r}")
+        return DeviceArray(tuple(shape), self.dtype, self._base or self, self.ptr + off * self.dtype.itemsize)
 
     def copy_from(self, a):
         a = np.ascontiguousarray(a, dtype=self.dtype)
@@ -852,3 +876,13 @@ class TNNHip:
 
     def eventDestroy(self, ev):
         call("tnh_event_destroy", ev)
+
+    def streamCreate(self):
+        """A second stream (default priority) to select with setStream."""
+        s = vp()
+        call("tnh_stream_create", C.byref(s))
+        return s.value
+
+    def streamDestroy(self, stream):
+        """Waits for the stream's work, then destroys it (not while selected)."""
+        call("tnh_stream_destroy", stream)

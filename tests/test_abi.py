@@ -63,15 +63,16 @@ def test_oracle_is_not_linked_into_the_product():
     assert b"librefcpu" not in data and b"ref_sgemm" not in data
 
 
-def test_trainer_and_mirror_import_without_torch():
-    """The Python mirror and the config-3 trainer run on the library's own
-    memory: importing them loads no torch (the tests and bench.py use torch
-    only as plumbing around them)."""
+def test_runners_and_mirror_import_without_torch():
+    """The Python mirror, the darknet network runner and the config-3 trainer
+    run on the library's own memory: importing them loads no torch (the tests
+    and bench.py use torch only as plumbing around them)."""
     import subprocess
     import sys
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    code = ("import sys; sys.path.insert(0, %r); import tensorium_amd.nnhip, tensorium_amd.trainnet; "
+    code = ("import sys; sys.path.insert(0, %r); "
+            "import tensorium_amd.nnhip, tensorium_amd.darknet, tensorium_amd.trainnet, tensorium_amd.weights; "
             "print('torch' in sys.modules)" % root)
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-500:]

@@ -113,7 +113,7 @@ def test_yolov3_detect_end_to_end(hip):
     net.forward(x)
     hip.finish()
     yl = [L for L in layers if L["type"] == "yolo"]
-    heads = [net.out[L["index"]].cpu().numpy().reshape((2, L["n"], L["classes"] + 5) + L["out"][1:]) for L in yl]
+    heads = [net.out[L["index"]].numpy().reshape((2, L["n"], L["classes"] + 5) + L["out"][1:]) for L in yl]
     anchors = [L["anchors"] for L in yl]
     dets = net.detect(thresh=0.995, nms=0.45, img_w=640, img_h=480)
     for b in range(2):

@@ -103,3 +103,37 @@ def test_config3_trainer_on_library_memory(hip):
     assert abs(float(loss) - float(loss_ref)) <= 1e-5 * abs(float(loss_ref))
     for k in ("w0", "w1", "w2", "fw", "s1"):
         assert R.rel_err(gpu.host(k), ref.p[k]) <= 1e-5, k
+
+
+def test_second_stream_from_the_library(hip):
+    """tnh_stream_create / tnh_stream_destroy: an SGEMM on a second stream,
+    joined through an event, equals the same SGEMM on the context stream;
+    destroying the selected stream or the context's own is refused."""
+    from tensorium_amd.nnhip import DeviceArray, TNHError
+
+    case("devmem second stream")
+    A = synth.uniform(520, (64, 96), -1, 1)
+    Bm = synth.uniform(521, (96, 80), -1, 1)
+    dA, dB = DeviceArray.from_numpy(A), DeviceArray.from_numpy(Bm)
+    c0, c1 = DeviceArray((64, 80)), DeviceArray((64, 80))
+    hip.resetStream()
+    main = hip.stream
+    hip.gemm(False, False, 64, 80, 96, 1.0, dA, 0, 96, dB, 0, 80, 0.0, c0, 0, 80)
+    side = hip.streamCreate()
+    ev = hip.eventCreate()
+    try:
+        hip.setStream(side)
+        with pytest.raises(TNHError, match="selected"):
+            hip.streamDestroy(side)
+        hip.gemm(False, False, 64, 80, 96, 1.0, dA, 0, 96, dB, 0, 80, 0.0, c1, 0, 80)
+        hip.eventRecord(ev)
+        hip.setStream(main)
+        hip.streamWaitEvent(ev)
+        with pytest.raises(TNHError, match="own stream"):
+            hip.streamDestroy(main)
+        assert np.array_equal(c0.numpy(), c1.numpy())
+    finally:
+        hip.resetStream()
+        hip.streamDestroy(side)
+        hip.eventDestroy(ev)
+        hip.useTorchStream()

@@ -84,4 +84,4 @@ def test_network_from_weights_file(hip, tmp_path):
     net.forward(dx)
     hip.finish()
     head = len(layers) - 2  # the linear 255-filter conv feeding the yolo layer
-    assert R.rel_err(net.out[head].cpu().numpy(), ref[head]) <= 1e-5
+    assert R.rel_err(net.out[head].numpy(), ref[head]) <= 1e-5

@@ -12,7 +12,7 @@ import torch
 from oracle import netref
 from oracle import refcpu as R
 from tensorium_amd import darknet, synth
-from tensorium_amd.nnhip import acLEAKY
+from tensorium_amd.nnhip import DeviceArray, acLEAKY
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -26,11 +26,10 @@ def yolo():
 
 def run_gpu(hip, layers, weights, x, fuse=True):
     n = darknet.Network(hip, layers, x.shape[0], weights, fuse=fuse)
-    dx = torch.from_numpy(x).cuda()
-    torch.cuda.synchronize()
+    dx = DeviceArray.from_numpy(x)  # the library's own memory (any device buffer is taken)
     heads = n.forward(dx)
     hip.finish()
-    return n, [h.cpu().numpy() for h in heads]
+    return n, [h.numpy() for h in heads]
 
 
 def test_yolov3_416_layerwise(hip, yolo):
@@ -73,7 +72,7 @@ def test_yolov3_416_batch1_heads(hip, yolo):
     for L in layers:
         i = L["index"]
         if L["type"] == "convolutional" and i not in n.fused:
-            errs[i] = R.rel_err(n.out[i].cpu().numpy(), ref[i])
+            errs[i] = R.rel_err(n.out[i].numpy(), ref[i])
     worst = max(errs, key=errs.get)
     print(f"worst intermediate conv error {errs[worst]:.3e} at layer {worst}", flush=True)
     for i in (81, 93, 105):
@@ -85,7 +84,7 @@ def test_yolov3_416_batch1_heads(hip, yolo):
         # relative difference moves logistic(x) near 0 by O(1): the parity
         # checkpoint is the pre-logistic conv above.  The yolo kernel itself
         # must be bit-exact on the GPU's own head-conv output.
-        own = R.yolo_fwd(n.out[i - 1].cpu().numpy(), 3, 80, exact=True)
+        own = R.yolo_fwd(n.out[i - 1].numpy(), 3, 80, exact=True)
         assert np.array_equal(h, own)
 
 
@@ -129,15 +128,15 @@ def test_yolov3_graph_replay(hip, yolo):
     n = darknet.Network(hip, layers, 2, W)
     dx = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
-    eager = [h.cpu().numpy() for h in n.forward(dx)]
+    eager = [h.numpy() for h in n.forward(dx)]
     hip.finish()
     try:
         n.capture(dx)
-        scratch = torch.zeros_like(n.out[0])
+        scratch = torch.zeros(n.out[0].shape, device="cuda")
         for rep in range(3):
             heads = n.replay()
             hip.finish()
-            got = [h.cpu().numpy() for h in heads]
+            got = [h.numpy() for h in heads]
             for u, v in zip(got, eager):
                 assert np.array_equal(u, v), rep
             # eager work between replays, on both streams
@@ -164,30 +163,30 @@ def test_yolov3_nhwc_heads(hip, yolo):
     n = darknet.Network(hip, layers, 1, W, layout="nhwc")
     dx = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
-    heads = [h.cpu().numpy() for h in n.forward(dx)]
+    heads = [h.numpy() for h in n.forward(dx)]
     hip.finish()
     errs = {}
     assert n.up_fused == {84, 96} and n.yolo_fused == {81, 93, 105}
     for L in layers:
         i = L["index"]
         if L["type"] == "convolutional" and i not in n.fused and i not in n.up_fused:
-            errs[i] = R.rel_err(n.output(i).cpu().numpy(), ref[i])
+            errs[i] = R.rel_err(n.output(i), ref[i])
         if L["type"] == "upsample":  # written by the convolution before it
-            errs[i] = R.rel_err(n.output(i).cpu().numpy(), ref[i])
+            errs[i] = R.rel_err(n.output(i), ref[i])
     worst = max(errs, key=errs.get)
     print(f"worst intermediate conv error {errs[worst]:.3e} at layer {worst}", flush=True)
     for i in (81, 93, 105):
         assert errs[i] <= TOL, (i, errs[i])
     assert max(errs.values()) <= 5 * TOL
     for h, i in zip(heads, (82, 94, 106)):
-        own = R.yolo_fwd(np.ascontiguousarray(n.output(i - 1).cpu().numpy()), 3, 80, exact=True)
+        own = R.yolo_fwd(n.output(i - 1), 3, 80, exact=True)
         assert np.array_equal(h, own)
     try:
         n.capture(dx)
         for rep in range(2):
             got = n.replay()
             hip.finish()
-            for u, v in zip([g.cpu().numpy() for g in got], heads):
+            for u, v in zip([g.numpy() for g in got], heads):
                 assert np.array_equal(u, v), rep
             torch.cuda.synchronize()
     finally:
@@ -210,10 +209,10 @@ def test_yolov3_nhwc_fusion_is_exact(hip, yolo, B):
     hip.setConvAutotune(False, -1)
     try:
         a = darknet.Network(hip, layers, B, W, layout="nhwc")
-        ha = [h.cpu().numpy() for h in a.forward(dx)]
+        ha = [h.numpy() for h in a.forward(dx)]
         hip.finish()
         b = darknet.Network(hip, layers, B, W, layout="nhwc", fuse_heads=False)
-        hb = [h.cpu().numpy() for h in b.forward(dx)]
+        hb = [h.numpy() for h in b.forward(dx)]
         hip.finish()
     finally:
         hip.setConvAutotune(True, -1)
@@ -221,7 +220,7 @@ def test_yolov3_nhwc_fusion_is_exact(hip, yolo, B):
     for u, v in zip(ha, hb):
         assert np.array_equal(u, v)
     for i in (85, 97, 81, 93, 105):
-        assert np.array_equal(a.output(i).cpu().numpy(), b.output(i).cpu().numpy()), i
+        assert np.array_equal(a.output(i), b.output(i)), i
 
 
 @pytest.mark.parametrize("B", [1, 4])
@@ -238,9 +237,9 @@ def test_yolov3_nhwc_branches(hip, yolo, B):
     torch.cuda.synchronize()
     n = darknet.Network(hip, layers, B, W, layout="nhwc")
     assert n.branches == {80: 82, 92: 94}
-    single = [h.cpu().numpy() for h in n.forward(dx, branches=False)]
+    single = [h.numpy() for h in n.forward(dx, branches=False)]
     hip.finish()
-    got = [h.cpu().numpy() for h in n.forward(dx, branches=True)]
+    got = [h.numpy() for h in n.forward(dx, branches=True)]
     hip.finish()
     for u, v in zip(got, single):
         assert np.array_equal(u, v)
@@ -250,7 +249,7 @@ def test_yolov3_nhwc_branches(hip, yolo, B):
         for rep in range(2):
             heads = n.replay()
             hip.finish()
-            for u, v in zip([h.cpu().numpy() for h in heads], single):
+            for u, v in zip([h.numpy() for h in heads], single):
                 assert np.array_equal(u, v), rep
             torch.cuda.synchronize()
     finally:
@@ -272,16 +271,16 @@ def test_yolov3_nhwc_matches_nchw_and_replays(hip, yolo):
     a.forward(dx)
     hip.finish()
     b = darknet.Network(hip, layers, 2, W, layout="nhwc")
-    eager = [h.cpu().numpy() for h in b.forward(dx)]
+    eager = [h.numpy() for h in b.forward(dx)]
     hip.finish()
     for i in (81, 93, 105, 86, 98):  # head convs and the two multi-input routes
-        assert R.rel_err(b.output(i).cpu().numpy(), a.output(i).cpu().numpy()) <= 2 * TOL, i
+        assert R.rel_err(b.output(i), a.output(i)) <= 2 * TOL, i
     try:
         b.capture(dx)
         for rep in range(3):
             heads = b.replay()
             hip.finish()
-            for u, v in zip([h.cpu().numpy() for h in heads], eager):
+            for u, v in zip([h.numpy() for h in heads], eager):
                 assert np.array_equal(u, v), rep
             torch.cuda.synchronize()
     finally:
@@ -303,9 +302,9 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
     dx = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
     big = darknet.Network(hip, layers, 16, W, layout="nhwc")
-    eager = [h.cpu().numpy() for h in big.forward(dx)]
+    eager = [h.numpy() for h in big.forward(dx)]
     hip.finish()
-    heads16 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
+    heads16 = {i: big.output(i) for i in (81, 93, 105)}
     for img in (0, 7, 15):
         print(f"[case] oracle and float64 forwards of image {img}", flush=True)
         xi = np.ascontiguousarray(x[img:img + 1])
@@ -324,7 +323,7 @@ def test_yolov3_416_b16_bench_config(hip, yolo):
         for rep in range(2):
             heads = big.replay()
             hip.finish()
-            for u, v in zip([h.cpu().numpy() for h in heads], eager):
+            for u, v in zip([h.numpy() for h in heads], eager):
                 assert np.array_equal(u, v), rep
             torch.cuda.synchronize()
     finally:
@@ -377,7 +376,7 @@ def test_yolov3_608_b32_bench_config(hip):
     big = darknet.Network(hip, layers, 32, W, layout="nhwc")
     big.forward(dx)
     hip.finish()
-    heads32 = {i: big.output(i).cpu().numpy() for i in (81, 93, 105)}
+    heads32 = {i: big.output(i) for i in (81, 93, 105)}
     del big
     for img in (0, 31):
         print(f"[case] oracle and float64 forwards of image {img} at 608", flush=True)
@@ -411,7 +410,7 @@ def test_yolov3_reference_route_mode(hip, yolo, B):
     n = darknet.Network(hip, layers, B, W, route_mode="reference")
     n.forward(dx)
     hip.finish()
-    got = {i: n.output(i).cpu().numpy() for i in (81, 93, 105)}
+    got = {i: n.output(i) for i in (81, 93, 105)}
     del n
     ref = netref.forward(layers, W, x, route_mode="reference")
     for i in (81, 93, 105):
@@ -421,7 +420,7 @@ def test_yolov3_reference_route_mode(hip, yolo, B):
     per_image = darknet.Network(hip, layers, B, W)
     per_image.forward(dx)
     hip.finish()
-    assert max(R.rel_err(per_image.output(i).cpu().numpy(), got[i]) for i in (93, 105)) > 10 * TOL
+    assert max(R.rel_err(per_image.output(i), got[i]) for i in (93, 105)) > 10 * TOL
 
 
 def test_nhwc_rejects_reference_route_mode(hip, yolo):
@@ -442,7 +441,7 @@ def test_yolov3_batch_in_passes(hip, layout):
     dx = torch.from_numpy(synth.uniform(11, (5, 3, 128, 128))).cuda()
     torch.cuda.synchronize()
     one = darknet.Network(hip, layers, 5, W, layout=layout)
-    ref = [h.cpu().numpy() for h in one.forward(dx)]
+    ref = [h.numpy() for h in one.forward(dx)]
     hip.finish()
     net = darknet.Network(hip, layers, 5, W, layout=layout, max_pass_batch=2)
     assert (net.pass_batch, net.batch) == (2, 5)
@@ -450,16 +449,16 @@ def test_yolov3_batch_in_passes(hip, layout):
     hip.finish()
     for h, r in zip(heads, ref):
         assert h.shape == r.shape
-        assert R.rel_err(h.cpu().numpy(), r) <= TOL
+        assert R.rel_err(h.numpy(), r) <= TOL
     heads = net.capture(dx)
     for _ in range(2):
         for h in heads:
-            h.zero_()
-        torch.cuda.synchronize()
+            hip.fill(h.numel(), h, 0, 0.0, 1)
+        hip.finish()
         net.replay()
         hip.finish()
         for h, r in zip(heads, ref):
-            assert R.rel_err(h.cpu().numpy(), r) <= TOL
+            assert R.rel_err(h.numpy(), r) <= TOL
     net.release_graph()
     with pytest.raises(ValueError, match="passes"):
         net.output(3)
@@ -481,12 +480,12 @@ def test_yolov3_tiny_vs_oracle(hip, layout):
     for b in range(2):
         ref = netref.forward(layers, W, x[b:b + 1])
         for i in (15, 22):
-            got = net.output(i)[b:b + 1].cpu().numpy()
+            got = net.output(i)[b:b + 1]
             e = R.rel_err(got, ref[i])
             print(f"image {b} head conv {i}: {e:.3e}", flush=True)
             assert e <= TOL, (b, i, e)
         for h, i in zip(heads, (16, 23)):
-            assert R.rel_err(h[b:b + 1].cpu().numpy(), ref[i]) <= TOL
+            assert R.rel_err(h[b:b + 1].numpy(), ref[i]) <= TOL
 
 
 @pytest.mark.parametrize("layout", ["nchw", "nhwc"])
@@ -508,7 +507,7 @@ def test_yolov3_tiny_scale_xy_vs_oracle(hip, layout):
     for b in range(2):
         ref = netref.forward(layers, W, x[b:b + 1])
         for h, i in zip(heads, (16, 23)):
-            e = R.rel_err(h[b:b + 1].cpu().numpy(), ref[i])
+            e = R.rel_err(h[b:b + 1].numpy(), ref[i])
             print(f"image {b} yolo {i}: {e:.3e}", flush=True)
             assert e <= TOL, (b, i, e)
 
@@ -558,7 +557,7 @@ def test_maxpool_depth_network_vs_oracle(hip):
     heads = net.forward(torch.from_numpy(x).cuda())
     hip.finish()
     ref = netref.forward(layers, W, x)
-    assert np.array_equal(net.output(1).cpu().numpy(), R.maxpool_depth_fwd(net.output(0).cpu().numpy(), 8)[0])
-    assert R.rel_err(heads[0].cpu().numpy(), ref[3]) <= TOL
+    assert np.array_equal(net.output(1), R.maxpool_depth_fwd(net.output(0), 8)[0])
+    assert R.rel_err(heads[0].numpy(), ref[3]) <= TOL
     with pytest.raises(NotImplementedError, match="maxpool_depth"):
         darknet.Network(hip, layers, 2, W, layout="nhwc")
