@@ -63,6 +63,8 @@ struct ConvArgs {
   // 16-byte vector there (OH*OW % 4 == 0, 16-byte aligned head)
   int64_t yoloBytes;
   int yoloVec;
+  // few-channel NCHW kernel: filters per grid.y group (a multiple of 4)
+  int64_t fGroup;
 };
 
 // K walk / B operand of a convolution kernel

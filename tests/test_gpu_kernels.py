@@ -510,11 +510,14 @@ def test_conv_nchw_wsplit_vs_oracle(hip, cfg, act):
                                                        (3, 4, 20, 7, 1, True, acLEAKY, False),
                                                        (2, 2, 15, 9, 2, True, acLINEAR, True),
                                                        (1, 3, 50, 12, 2, True, acLINEAR, True),
-                                                       (2, 3, 33, 64, 1, False, acLEAKY, False)])
+                                                       (2, 3, 33, 64, 1, False, acLEAKY, False),
+                                                       (1, 3, 24, 35, 1, True, acLINEAR, True)])
 def test_conv_few_channels_bit_exact(hip, B, Cc, Hh, F, s, tap, act, resid):
     """C <= 4 3x3 layers (the RGB input layer; config 1 at full size) run the
     per-pixel kernel, whose sequential FMA chain in the reference k order is
-    the reference CPU arithmetic: equal bit for bit to the oracle."""
+    the reference CPU arithmetic: equal bit for bit to the oracle.  32 and
+    more filters over few pixels split into filter groups (64: four groups
+    of 16; 35: groups of 20 and 15)."""
     case(f"conv few-channel B{B} C{Cc} H{Hh} F{F} s{s} tap{tap} act{act} res{resid}")
     x = synth.uniform(51, (B, Cc, Hh, Hh))
     Wt = synth.normal(52, (F, Cc * 9), 0.05)
