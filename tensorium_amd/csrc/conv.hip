@@ -885,10 +885,14 @@ int conv_dispatch(Context* cx, ConvArgs& a, int mode, bool va, bool vb, bool sma
       // whole tiles only; timed, never the cost model's pick, so absent from
       // the deterministic mode's choice; only for layers whose 64x64 tiles
       // leave the GPU under-filled (below two per CU), where they replace a
-      // K split and its reduction launch: on larger layers their 32-wide
-      // tiles read twice the L2 bytes per FLOP of the lean tiles
+      // K split and its reduction launch (on larger layers their 32-wide
+      // tiles read twice the L2 bytes per FLOP of the lean tiles), and for
+      // NCHW layers of at most 32 filters, which fill half of a lean tile's
+      // 64 filter rows (config 3's conv2 input delta: 0.3060-0.3074 against
+      // 0.3121-0.3138 ms per step)
       const int64_t tiles64 = ((N + 63) / 64) * ((F + 63) / 64);
-      if (!det && tiles64 < 2 * static_cast<int64_t>(cus)) cands.push_back({c, 1, 0, 0});
+      const bool narrow = !nhwc && F <= 32;
+      if (!det && (tiles64 < 2 * static_cast<int64_t>(cus) || narrow)) cands.push_back({c, 1, 0, 0});
       continue;
     }
     cands.push_back({c, 1, 0, 0});
