@@ -33,7 +33,7 @@ import os
 import numpy as np
 
 from . import synth
-from .nnhip import WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR, DeviceArray, acLEAKY, acLINEAR, acLOGISTIC
+from .nnhip import WEIGHTS_REFERENCE, WEIGHTS_TAP_MAJOR, DeviceArray, acLEAKY, acLINEAR, acLOGISTIC, release_stream
 
 CFG_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cfg")
 _ACT = {"leaky": acLEAKY, "linear": acLINEAR, "logistic": acLOGISTIC}
@@ -490,8 +490,11 @@ class Network:
         capture, where the events become the graph's edges)."""
         hip = self.hip
         if self._side is None:
+            import weakref
+
             self._side = hip.streamCreate()  # default priority
             self._events = {s_: (hip.eventCreate(), hip.eventCreate()) for s_ in tails}
+            weakref.finalize(self, release_stream, self._side, [e for pair in self._events.values() for e in pair])
         main = hip.stream
         side = self._side
         heads, joins = [], []

@@ -236,6 +236,18 @@ def _free_device(ptr):
         _lib.tnh_free(ptr)
 
 
+def release_stream(stream, events=()):
+    """Finalizer for a stream from streamCreate and events from eventCreate
+    (statuses ignored: at interpreter exit the context may already be gone,
+    and a stream still selected is refused and left to the process end)."""
+    if _lib is None:
+        return
+    for ev in events:
+        _lib.tnh_event_destroy(ev)
+    if stream:
+        _lib.tnh_stream_destroy(stream)
+
+
 class DeviceArray:
     """A shaped, typed device array in memory from tnh_malloc (the library's
     own allocator, TNNCuda.createDeviceBuffer), for Python callers that use
