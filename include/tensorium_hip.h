@@ -814,6 +814,23 @@ int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch,
                             float *const *packTap, float *const *packFlip,
                             int64_t nParams, float *params,
                             float *paramUpdates);
+/* No reference counterpart: tnh_sgd_update_pack whose layer l may also carry
+ * packNPieces[l] > 0 weight-gradient pieces from tnh_conv2d_wgrad_pieces at
+ * packPieces[l]: the pass first adds their sum to the layer's weight updates
+ * exactly as tnh_conv2d_wgrad with alpha = beta = 1 would have (the same
+ * bits), so a training step's weight-gradient reductions ride on the update's
+ * pass.  packPieces / packNPieces may be NULL (no pieces anywhere). */
+int32_t tnh_sgd_update_pack_pieces(int64_t N, float learningRate, int64_t batch,
+                                   float momentum, float decay, float *weights,
+                                   float *weightUpdates, int32_t nPack,
+                                   const int64_t *packOffset,
+                                   const int64_t *packF, const int64_t *packC,
+                                   const int64_t *packTaps,
+                                   float *const *packTap,
+                                   float *const *packFlip,
+                                   const float *const *packPieces,
+                                   const int32_t *packNPieces, int64_t nParams,
+                                   float *params, float *paramUpdates);
 /* bias / scale part of the same updates (nConvolutionLayer.pas:694-706):
  * params = fma(lr/batch, paramUpdates, params); paramUpdates *= momentum. */
 int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch,
@@ -850,6 +867,24 @@ int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t W,
                          int64_t xBatchStride, const float *delta,
                          int64_t deltaBatchStride, float alpha, float beta,
                          float *dW);
+/* No reference counterpart: tnh_conv2d_wgrad's product (one launch, the
+ * single-launch geometry only, else TNH_ERR_UNSUPPORTED) without its sum:
+ * the split's raw sums go to pieces ([*nPieces][F][C*kh*kw], piecesFloats
+ * floats available) for tnh_sgd_update_pack_pieces to add to dW with
+ * alpha = beta = 1.  pieces NULL: only *nPieces is set (the count depends
+ * on the geometry and the device's CU count, not on the data).  Refused
+ * (TNH_ERR_UNSUPPORTED) for fewer than 8192 weights cut into several pieces,
+ * which tnh_conv2d_wgrad sums a wave per weight in another order.  The pieces
+ * live in the caller's memory, so several layers' products can wait for one
+ * update. */
+int32_t tnh_conv2d_wgrad_pieces(int64_t batch, int64_t C, int64_t H, int64_t W,
+                                int64_t F, int64_t kh, int64_t kw,
+                                int64_t padH, int64_t padW, int64_t strideY,
+                                int64_t strideX, int64_t dilY, int64_t dilX,
+                                const float *x, int64_t xBatchStride,
+                                const float *delta, int64_t deltaBatchStride,
+                                float *pieces, int64_t piecesFloats,
+                                int32_t *nPieces);
 
 #ifdef __cplusplus
 }

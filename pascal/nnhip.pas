@@ -230,6 +230,10 @@ function tnh_sgd_update(N: Int64; learningRate: Single; batch: Int64; momentum, 
 function tnh_sgd_update_pack(N: Int64; learningRate: Single; batch: Int64; momentum, decay: Single;
   weights, weightUpdates: PSingle; nPack: LongInt; packOffset, packF, packC, packTaps: PInt64;
   packTap, packFlip: PPSingle; nParams: Int64; params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
+function tnh_sgd_update_pack_pieces(N: Int64; learningRate: Single; batch: Int64; momentum, decay: Single;
+  weights, weightUpdates: PSingle; nPack: LongInt; packOffset, packF, packC, packTaps: PInt64;
+  packTap, packFlip, packPieces: PPSingle; packNPieces: PLongInt; nParams: Int64;
+  params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_param_update(N: Int64; learningRate: Single; batch: Int64; momentum: Single;
   params, paramUpdates: PSingle): LongInt; cdecl; external libtnh;
 function tnh_sgemm_nt_batch_reduce(M, N, L: Int64; alpha: Single; A: PSingle; aOff, lda, strideA: Int64;
@@ -238,6 +242,9 @@ function tnh_sgemm_nt_batch_reduce(M, N, L: Int64; alpha: Single; A: PSingle; aO
 function tnh_conv2d_wgrad(batch, C, H, W, F, kh, kw, padH, padW, strideY, strideX, dilY, dilX: Int64; x: PSingle;
   xBatchStride: Int64; delta: PSingle; deltaBatchStride: Int64; alpha, beta: Single; dW: PSingle): LongInt; cdecl;
   external libtnh;
+function tnh_conv2d_wgrad_pieces(batch, C, H, W, F, kh, kw, padH, padW, strideY, strideX, dilY, dilX: Int64;
+  x: PSingle; xBatchStride: Int64; delta: PSingle; deltaBatchStride: Int64; pieces: PSingle; piecesFloats: Int64;
+  nPieces: PLongInt): LongInt; cdecl; external libtnh;
 
 // --- the backend object -------------------------------------------------------
 type
@@ -445,6 +452,15 @@ type
     procedure convWeightGradient(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
       dilY, dilX: SizeInt; const input: TCUMem; const inBatchStride: SizeInt; const delta: TCUMem;
       const deltaBatchStride: SizeInt; const ALPHA, BETA: T; const dW: TCUMem);
+    // the same product's split sums into pieces (nil: only counted); returns the number of pieces
+    function convWeightGradientPieces(const batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY,
+      strideX, dilY, dilX: SizeInt; const input: TCUMem; const inBatchStride: SizeInt; const delta: TCUMem;
+      const deltaBatchStride: SizeInt; const pieces: TCUMem = nil; const piecesFloats: SizeInt = 0): longint;
+    // sgdUpdatePack adding each layer's pieces (count 0: none) to its weight updates first
+    procedure sgdUpdatePackPieces(const N: SizeInt; const learningRate: T; const batch: SizeInt;
+      const momentum, decay: T; weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64;
+      const tapMajor, flipped, pieces: array of TCUMem; const nPieces: array of longint; const nParams: SizeInt;
+      params, paramUpdates: TCUMem);
     procedure setDeterministic(const enable: boolean);
     procedure setConvAutotune(const enable: boolean; const forcedConfig: longint = -1);
     procedure setSgemmAutotune(const enable: boolean; const forcedConfig: longint = -1);
@@ -1077,6 +1093,42 @@ procedure TNNHip<T>.convWeightGradient(const batch, c, h, w, filters, kernelH, k
 begin
   check(tnh_conv2d_wgrad(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY, dilX,
     PSingle(input), inBatchStride, PSingle(delta), deltaBatchStride, S(ALPHA), S(BETA), PSingle(dW)));
+end;
+
+function TNNHip<T>.convWeightGradientPieces(const batch, c, h, w, filters, kernelH, kernelW, padH, padW,
+  strideY, strideX, dilY, dilX: SizeInt; const input: TCUMem; const inBatchStride: SizeInt; const delta: TCUMem;
+  const deltaBatchStride: SizeInt; const pieces: TCUMem; const piecesFloats: SizeInt): longint;
+var
+  n: longint;
+begin
+  n := 0;
+  check(tnh_conv2d_wgrad_pieces(batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY,
+    dilX, PSingle(input), inBatchStride, PSingle(delta), deltaBatchStride, PSingle(pieces), piecesFloats, @n));
+  result := n;
+end;
+
+procedure TNNHip<T>.sgdUpdatePackPieces(const N: SizeInt; const learningRate: T; const batch: SizeInt;
+  const momentum, decay: T; weights, weightUpdates: TCUMem; const offsets, F, C, taps: array of Int64;
+  const tapMajor, flipped, pieces: array of TCUMem; const nPieces: array of longint; const nParams: SizeInt;
+  params, paramUpdates: TCUMem);
+var
+  tp, fl, pc: array of PSingle;
+  i: SizeInt;
+begin
+  if Length(offsets) = 0 then begin
+    sgdUpdatePack(N, learningRate, batch, momentum, decay, weights, weightUpdates, offsets, F, C, taps, tapMajor,
+      flipped, nParams, params, paramUpdates);
+    exit
+  end;
+  SetLength(tp, Length(tapMajor));
+  SetLength(fl, Length(flipped));
+  SetLength(pc, Length(pieces));
+  for i := 0 to High(tapMajor) do tp[i] := PSingle(tapMajor[i]);
+  for i := 0 to High(flipped) do fl[i] := PSingle(flipped[i]);
+  for i := 0 to High(pieces) do pc[i] := PSingle(pieces[i]);
+  check(tnh_sgd_update_pack_pieces(N, S(learningRate), batch, S(momentum), S(decay), PSingle(weights),
+    PSingle(weightUpdates), Length(offsets), @offsets[0], @F[0], @C[0], @taps[0], @tp[0], @fl[0], @pc[0],
+    @nPieces[0], nParams, PSingle(params), PSingle(paramUpdates)));
 end;
 
 procedure TNNHip<T>.setDeterministic(const enable: boolean);

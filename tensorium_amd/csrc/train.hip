@@ -882,7 +882,37 @@ struct PackSet {
   int64_t off[kMaxPack], F[kMaxPack], C[kMaxPack], taps[kMaxPack];
   float* tap[kMaxPack];
   float* flip[kMaxPack];
+  // weight-gradient pieces from tnh_conv2d_wgrad_pieces ([nPieces][F][C*taps],
+  // nPieces 0: none), added to the layer's weight updates before the step
+  const float* pieces[kMaxPack];
+  int nPieces[kMaxPack];
 };
+
+// weightUpdates[j] + the sum of layer l's pieces at j, with the arithmetic of
+// tnh_conv2d_wgrad (alpha = beta = 1): one piece is the accumulator itself;
+// several are summed from zero in piece order, kPieceLoads loads issued
+// together (wgrad_reduce_kernel's order), then the old value is added.
+constexpr int kPieceLoads = 16;
+__device__ inline float add_pieces(const PackSet& ps, int l, int64_t j, float wu) {
+  const int P = ps.nPieces[l];
+  const float* pc = ps.pieces[l];
+  const int64_t total = ps.F[l] * ps.C[l] * ps.taps[l];
+  float v;
+  if (P == 1) {
+    v = pc[j];
+  } else {
+    v = 0.f;
+    for (int s = 0; s < P; s += kPieceLoads) {
+      float t[kPieceLoads];
+#pragma unroll
+      for (int q = 0; q < kPieceLoads; ++q) t[q] = s + q < P ? pc[(s + q) * total + j] : 0.f;
+#pragma unroll
+      for (int q = 0; q < kPieceLoads; ++q)
+        if (s + q < P) v = v + t[q];
+    }
+  }
+  return v + wu;
+}
 
 // sgd_kernel, then each updated weight of a listed conv layer is also
 // written where tnh_conv2d_pack_weights_dgrad would put it; elements n ..
@@ -896,7 +926,12 @@ __global__ void sgd_pack_kernel(int64_t n, float aDecay, float aRate, float mome
       pu[j] = pu[j] * momentum;
       continue;
     }
-    const float u = fmaf(aDecay, w[i], wu[i]);
+    float g = wu[i];
+    for (int l = 0; l < ps.n; ++l) {
+      const int64_t j = i - ps.off[l];
+      if (ps.nPieces[l] > 0 && j >= 0 && j < ps.F[l] * ps.C[l] * ps.taps[l]) g = add_pieces(ps, l, j, g);
+    }
+    const float u = fmaf(aDecay, w[i], g);
     const float v = fmaf(aRate, u, w[i]);
     w[i] = v;
     wu[i] = u * momentum;
@@ -958,6 +993,7 @@ struct WgradArgs {
   int64_t aBytes, bBytes, kChunk;
   float alpha, beta;
   int tilesM, tilesN, splits;
+  int rawPieces;  // store every split's raw sums in part, no reduction (also one split)
 };
 
 template <class Cfg, bool VA, bool VB>
@@ -1093,7 +1129,7 @@ __global__ __launch_bounds__(Cfg::NT) void wgrad_col_kernel(WgradArgs a, ColGeom
   const int64_t kBegin = blockIdx.y * a.kChunk;
   const int64_t kEnd = min(Ktot, kBegin + a.kChunk);
   Main::exec(al, bl, kBegin, kEnd, lds, acc);
-  if (a.splits > 1) {
+  if (a.splits > 1 || a.rawPieces) {
     float* part = a.part + static_cast<int64_t>(blockIdx.y) * a.M * a.N;
     Main::for_each(acc, [&](int row, int col, float v) {
       const int64_t gr = m0 + row, gc = n0 + col;
@@ -1168,6 +1204,8 @@ using WCfg = TileCfg<64, 64, 32, 2, 2, 2>;
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 int launch_wgrad_reduce(const WgradArgs& a, hipStream_t s);
+// weight gradients of fewer elements sum their pieces a wave per element
+constexpr int64_t kWaveReduceBelow = 8192;
 
 template <bool VA, bool VB>
 int launch_wgrad(WgradArgs a, hipStream_t s) {
@@ -1186,10 +1224,10 @@ int launch_wgrad_col(WgradArgs a, const ColGeom& g, hipStream_t s) {
 }
 
 int launch_wgrad_reduce(const WgradArgs& a, hipStream_t s) {
-  if (a.splits > 1) {
+  if (a.splits > 1 && !a.rawPieces) {
     // few outputs: a wave per output element spreads the splits over its
     // lanes; many: a thread per element keeps the loads coalesced
-    if (a.M * a.N < 8192) {
+    if (a.M * a.N < kWaveReduceBelow) {
       hipLaunchKernelGGL(wgrad_reduce_wave_kernel, dim3(static_cast<unsigned>((a.M * a.N + 3) / 4)), dim3(256), 0, s,
                          a);
       return launch_status("wgrad_reduce_wave_kernel");
@@ -1438,11 +1476,12 @@ extern "C" int32_t tnh_sgd_update(int64_t N, float learningRate, int64_t batch, 
   return launch_status("sgd_kernel");
 }
 
-extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch, float momentum, float decay,
-                                       float* weights, float* weightUpdates, int32_t nPack, const int64_t* packOffset,
-                                       const int64_t* packF, const int64_t* packC, const int64_t* packTaps,
-                                       float* const* packTap, float* const* packFlip, int64_t nParams, float* params,
-                                       float* paramUpdates) {
+extern "C" int32_t tnh_sgd_update_pack_pieces(int64_t N, float learningRate, int64_t batch, float momentum,
+                                              float decay, float* weights, float* weightUpdates, int32_t nPack,
+                                              const int64_t* packOffset, const int64_t* packF, const int64_t* packC,
+                                              const int64_t* packTaps, float* const* packTap, float* const* packFlip,
+                                              const float* const* packPieces, const int32_t* packNPieces,
+                                              int64_t nParams, float* params, float* paramUpdates) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(N >= 0 && batch > 0 && nParams >= 0, "sgd_update_pack: bad arguments");
   TNH_ARG(nPack >= 0 && nPack <= kMaxPack, "sgd_update_pack: %d layers (at most %d)", nPack, kMaxPack);
@@ -1464,12 +1503,30 @@ extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t ba
     ps.taps[l] = packTaps[l];
     ps.tap[l] = packTap[l];
     ps.flip[l] = packFlip[l];
+    ps.pieces[l] = nullptr;
+    ps.nPieces[l] = 0;
+    if (packNPieces && packNPieces[l] != 0) {
+      TNH_ARG(packNPieces[l] > 0 && packPieces && packPieces[l], "sgd_update_pack: layer %d: bad pieces", l);
+      TNH_ARG(packPieces[l] != weights && packPieces[l] != weightUpdates, "sgd_update_pack: pieces alias the arena");
+      ps.pieces[l] = packPieces[l];
+      ps.nPieces[l] = packNPieces[l];
+    }
   }
   const float aDecay = -decay * static_cast<float>(batch);
   const float aRate = learningRate / static_cast<float>(batch);
   hipLaunchKernelGGL(sgd_pack_kernel, dim3(grid_1d(N + nParams)), dim3(256), 0, cx->stream, N, aDecay, aRate, momentum,
                      weights, weightUpdates, ps, nParams, params, paramUpdates);
   return launch_status("sgd_pack_kernel");
+}
+
+extern "C" int32_t tnh_sgd_update_pack(int64_t N, float learningRate, int64_t batch, float momentum, float decay,
+                                       float* weights, float* weightUpdates, int32_t nPack, const int64_t* packOffset,
+                                       const int64_t* packF, const int64_t* packC, const int64_t* packTaps,
+                                       float* const* packTap, float* const* packFlip, int64_t nParams, float* params,
+                                       float* paramUpdates) {
+  return tnh_sgd_update_pack_pieces(N, learningRate, batch, momentum, decay, weights, weightUpdates, nPack,
+                                    packOffset, packF, packC, packTaps, packTap, packFlip, nullptr, nullptr, nParams,
+                                    params, paramUpdates);
 }
 
 extern "C" int32_t tnh_param_update(int64_t N, float learningRate, int64_t batch, float momentum, float* params,
@@ -1494,6 +1551,8 @@ namespace {
 // panels per split, were 1.5-3.5% slower per step
 constexpr int64_t kWgradWgPerCu = 2, kWgradMinPanels = 4;
 
+// With rawPieces the caller's memory takes the pieces (a.part, set after the
+// split is known), so the split never falls back to whole K.
 int wgrad_split(Context* cx, WgradArgs& a, const char* who) {
   a.tilesM = static_cast<int>((a.M + WCfg::BM - 1) / WCfg::BM);
   a.tilesN = static_cast<int>((a.N + WCfg::BN - 1) / WCfg::BN);
@@ -1505,6 +1564,7 @@ int wgrad_split(Context* cx, WgradArgs& a, const char* who) {
   splits = std::max<int64_t>(1, std::min<int64_t>({splits, panels / kWgradMinPanels, 1024}));
   a.kChunk = (panels + splits - 1) / splits * WCfg::BK;
   a.splits = static_cast<int>((Ktot + a.kChunk - 1) / a.kChunk);
+  if (a.rawPieces) return TNH_OK;
   if (a.splits > 1) {
     a.part = static_cast<float*>(workspace(cx, static_cast<size_t>(a.splits) * a.M * a.N * 4));
     if (!a.part) {
@@ -1562,21 +1622,27 @@ extern "C" int32_t tnh_sgemm_nt_batch_reduce(int64_t M, int64_t N, int64_t L, fl
   return launch_wgrad<false, false>(a, cx->stream);
 }
 
-extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
-                                    int64_t kw, int64_t padH, int64_t padW, int64_t strideY, int64_t strideX,
-                                    int64_t dilY, int64_t dilX, const float* x, int64_t xBatchStride,
-                                    const float* delta, int64_t deltaBatchStride, float alpha, float beta,
-                                    float* dW) {
+namespace tnh {
+namespace {
+// tnh_conv2d_wgrad, or with pieces / nPieces (tnh_conv2d_wgrad_pieces) the
+// split's raw sums written to the caller's memory instead of reduced into dW.
+int32_t conv2d_wgrad_impl(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh, int64_t kw,
+                          int64_t padH, int64_t padW, int64_t strideY, int64_t strideX, int64_t dilY, int64_t dilX,
+                          const float* x, int64_t xBatchStride, const float* delta, int64_t deltaBatchStride,
+                          float alpha, float beta, float* dW, bool piecesMode, float* pieces, int64_t piecesFloats,
+                          int32_t* nPieces) {
   TNH_REQUIRE_CTX(cx);
   TNH_ARG(batch >= 0 && C > 0 && H > 0 && W > 0 && F > 0 && kh > 0 && kw > 0 && padH >= 0 && padW >= 0 &&
               strideY > 0 && strideX > 0 && dilY > 0 && dilX > 0,
           "conv2d_wgrad: bad geometry");
-  TNH_ARG(x && delta && dW, "conv2d_wgrad: NULL buffer");
+  TNH_ARG(x && delta && (piecesMode || dW), "conv2d_wgrad: NULL buffer");
+  TNH_ARG(!piecesMode || nPieces, "conv2d_wgrad_pieces: NULL nPieces");
   const int64_t OH = (H + 2 * padH - dilY * (kh - 1) - 1) / strideY + 1;
   const int64_t OW = (W + 2 * padW - dilX * (kw - 1) - 1) / strideX + 1;
   TNH_ARG(OH > 0 && OW > 0, "conv2d_wgrad: empty output");
   const int64_t L = OH * OW, K = C * kh * kw;
   TNH_ARG(xBatchStride >= C * H * W && deltaBatchStride >= F * L, "conv2d_wgrad: batch strides too small");
+  TNH_ARG(!piecesMode || batch > 0, "conv2d_wgrad_pieces: empty batch");
   if (batch == 0) return tnh_sgemm(0, 1, F, K, 0, alpha, x, 0, 1, x, 0, 1, beta, dW, 0, K);
   const int64_t xElems = (batch - 1) * xBatchStride + C * H * W;
   const int64_t dElems = (batch - 1) * deltaBatchStride + F * L;
@@ -1585,6 +1651,8 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
           "conv2d_wgrad: operands span more than 2 GiB (split the batch)");
   constexpr int BK = WCfg::BK;
   const bool fused = L % BK == 0 && OW % 4 == 0 && (OW % BK == 0 || BK % OW == 0);
+  if (!fused && piecesMode)
+    return fail(TNH_ERR_UNSUPPORTED, "conv2d_wgrad_pieces: needs OH*OW %% 32 == 0, OW %% 4 == 0 and OW | 32 or 32 | OW");
   if (!fused) {
     // the gather's panel geometry does not hold: im2col image by image into
     // the stream's workspace, then the NT product accumulated over images
@@ -1610,7 +1678,22 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
   a.bBytes = xElems * 4;
   a.alpha = alpha;
   a.beta = beta;
+  a.rawPieces = piecesMode ? 1 : 0;
   if (int st = wgrad_split(cx, a, "conv2d_wgrad")) return st;
+  if (piecesMode) {
+    // the update's pass sums a weight's pieces in one thread, in the order of
+    // the thread-per-element reduction; the wave-per-element order of small
+    // gradients is not reproduced there
+    if (a.splits > 1 && F * K < kWaveReduceBelow)
+      return fail(TNH_ERR_UNSUPPORTED, "conv2d_wgrad_pieces: %lld weights (below %lld) sum their pieces a wave each",
+                  static_cast<long long>(F * K), static_cast<long long>(kWaveReduceBelow));
+    *nPieces = a.splits;
+    if (!pieces) return TNH_OK;  // the query: the number of pieces only
+    TNH_ARG(piecesFloats >= static_cast<int64_t>(a.splits) * F * K,
+            "conv2d_wgrad_pieces: %lld floats hold fewer than %d pieces of %lld", static_cast<long long>(piecesFloats),
+            a.splits, static_cast<long long>(F * K));
+    a.part = pieces;
+  }
   ColGeom g{};
   g.xBatchStride = xBatchStride;
   g.xBytes = xElems * 4;
@@ -1623,6 +1706,26 @@ extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t
   const bool va = aligned16(delta) && L % 4 == 0 && deltaBatchStride % 4 == 0;
   if (va) return launch_wgrad_col<true>(a, g, cx->stream);
   return launch_wgrad_col<false>(a, g, cx->stream);
+}
+}  // namespace
+}  // namespace tnh
+
+extern "C" int32_t tnh_conv2d_wgrad(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                    int64_t kw, int64_t padH, int64_t padW, int64_t strideY, int64_t strideX,
+                                    int64_t dilY, int64_t dilX, const float* x, int64_t xBatchStride,
+                                    const float* delta, int64_t deltaBatchStride, float alpha, float beta,
+                                    float* dW) {
+  return tnh::conv2d_wgrad_impl(batch, C, H, W, F, kh, kw, padH, padW, strideY, strideX, dilY, dilX, x, xBatchStride,
+                                delta, deltaBatchStride, alpha, beta, dW, false, nullptr, 0, nullptr);
+}
+
+extern "C" int32_t tnh_conv2d_wgrad_pieces(int64_t batch, int64_t C, int64_t H, int64_t W, int64_t F, int64_t kh,
+                                           int64_t kw, int64_t padH, int64_t padW, int64_t strideY, int64_t strideX,
+                                           int64_t dilY, int64_t dilX, const float* x, int64_t xBatchStride,
+                                           const float* delta, int64_t deltaBatchStride, float* pieces,
+                                           int64_t piecesFloats, int32_t* nPieces) {
+  return tnh::conv2d_wgrad_impl(batch, C, H, W, F, kh, kw, padH, padW, strideY, strideX, dilY, dilX, x, xBatchStride,
+                                delta, deltaBatchStride, 1.0f, 1.0f, nullptr, true, pieces, piecesFloats, nPieces);
 }
 
 namespace {

@@ -164,9 +164,13 @@ _PROTOS = {
     "tnh_sgd_update": [i64, f32, i64, f32, f32, vp, vp],
     "tnh_sgd_update_pack": [i64, f32, i64, f32, f32, vp, vp, i32, C.POINTER(i64), C.POINTER(i64), C.POINTER(i64),
                             C.POINTER(i64), C.POINTER(vp), C.POINTER(vp), i64, vp, vp],
+    "tnh_sgd_update_pack_pieces": [i64, f32, i64, f32, f32, vp, vp, i32, C.POINTER(i64), C.POINTER(i64),
+                                   C.POINTER(i64), C.POINTER(i64), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
+                                   C.POINTER(i32), i64, vp, vp],
     "tnh_param_update": [i64, f32, i64, f32, vp, vp],
     "tnh_conv2d_pack_weights_dgrad": [i64, i64, i64, i64, vp, vp, vp],
     "tnh_conv2d_wgrad": [i64] * 13 + [vp, i64, vp, i64, f32, f32, vp],
+    "tnh_conv2d_wgrad_pieces": [i64] * 13 + [vp, i64, vp, i64, vp, i64, C.POINTER(i32)],
     "tnh_sgemm_nt_batch_reduce": [i64, i64, i64, f32, vp, i64, i64, i64, vp, i64, i64, i64, f32, vp, i64, i64,
                                   i64],
 }
@@ -842,16 +846,26 @@ class TNNHip:
         call("tnh_sgd_update", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates))
 
     def sgdUpdatePack(self, N, learningRate, batch, momentum, decay, weights, weightUpdates, layers, nParams=0,
-                      params=None, paramUpdates=None):
+                      params=None, paramUpdates=None, pieces=None):
         """sgdUpdate whose pass also refreshes conv layers' packed copies;
         layers: [(offset, F, C, taps, tapMajor, flipped or None), ...]; then
-        paramUpdate(nParams, ..., params, paramUpdates) in the same launch."""
+        paramUpdate(nParams, ..., params, paramUpdates) in the same launch.
+        pieces: per layer None or (buffer, count) from convWeightGradientPieces,
+        added to the layer's weight updates first (tnh_sgd_update_pack_pieces)."""
         n = len(layers)
         arr = lambda t, xs: (t * max(n, 1))(*xs)  # noqa: E731
-        call("tnh_sgd_update_pack", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates), n,
-             arr(i64, [l[0] for l in layers]), arr(i64, [l[1] for l in layers]), arr(i64, [l[2] for l in layers]),
-             arr(i64, [l[3] for l in layers]), arr(vp, [addr(l[4]) for l in layers]),
-             arr(vp, [addr(l[5]) for l in layers]), nParams, addr(params), addr(paramUpdates))
+        tables = (arr(i64, [l[0] for l in layers]), arr(i64, [l[1] for l in layers]),
+                  arr(i64, [l[2] for l in layers]), arr(i64, [l[3] for l in layers]),
+                  arr(vp, [addr(l[4]) for l in layers]), arr(vp, [addr(l[5]) for l in layers]))
+        if pieces is None:
+            call("tnh_sgd_update_pack", N, learningRate, batch, momentum, decay, addr(weights), addr(weightUpdates),
+                 n, *tables, nParams, addr(params), addr(paramUpdates))
+            return
+        if len(pieces) != n:
+            raise ValueError("one pieces entry per layer")
+        call("tnh_sgd_update_pack_pieces", N, learningRate, batch, momentum, decay, addr(weights),
+             addr(weightUpdates), n, *tables, arr(vp, [addr(q[0]) if q else None for q in pieces]),
+             arr(i32, [q[1] if q else 0 for q in pieces]), nParams, addr(params), addr(paramUpdates))
 
     def paramUpdate(self, N, learningRate, batch, momentum, params, paramUpdates):
         call("tnh_param_update", N, learningRate, batch, momentum, addr(params), addr(paramUpdates))
@@ -861,6 +875,17 @@ class TNNHip:
         """dW = beta*dW + alpha * sum_b delta_b * im2col(input_b)^T (the im2col inside the GEMM)."""
         call("tnh_conv2d_wgrad", batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY, dilX,
              addr(input), inBatchStride, addr(delta), deltaBatchStride, alpha, beta, addr(dW))
+
+    def convWeightGradientPieces(self, batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX,
+                                 dilY, dilX, input, inBatchStride, delta, deltaBatchStride, pieces=None,
+                                 piecesFloats=0):
+        """tnh_conv2d_wgrad_pieces: the weight-gradient product's split sums
+        into `pieces` (None: only count them); returns the number of pieces."""
+        n = i32(0)
+        call("tnh_conv2d_wgrad_pieces", batch, c, h, w, filters, kernelH, kernelW, padH, padW, strideY, strideX, dilY,
+             dilX, addr(input), inBatchStride, addr(delta), deltaBatchStride, addr(pieces), piecesFloats,
+             C.byref(n))
+        return n.value
 
     def gemmNTBatchReduce(self, M, N, L, ALPHA, A, aOffset, lda, strideA, B, bOffset, ldb, strideB, BETA, C_,
                           cOffset, ldc, batch):

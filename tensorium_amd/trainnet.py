@@ -70,7 +70,7 @@ class CifarTrainer:
 
     def __init__(self, hip, params, batch, size=32, lr=1e-3, momentum=0.9, decay=1e-4, bn_momentum=0.1,
                  fused_wgrad=True, conv_dgrad=True, fused_head=True, fused_pool_bwd=True, fused_stats=True,
-                 store_bn_outputs=False):
+                 store_bn_outputs=False, defer_wgrad_sum=True):
         """fused_wgrad: the conv weight gradients gather their column matrix
         inside the GEMM (tnh_conv2d_wgrad); False runs the reference's
         im2col + NT product (the same bits).  conv_dgrad: the conv input
@@ -89,11 +89,17 @@ class CifarTrainer:
         backward's first pass forms both again from x, the statistics, the
         scales and the biases (the same bits, four fewer passes over a
         layer's activations; out{i} is then stored only where a later layer
-        reads it)."""
+        reads it).  defer_wgrad_sum (with fused_wgrad): the weight gradients
+        of 8192 and more weights keep their split sums in the trainer's
+        memory (tnh_conv2d_wgrad_pieces) and the update's pass adds them to
+        the weight updates (tnh_sgd_update_pack_pieces; the same bits, one
+        reduction launch fewer per such layer); u_w{i} of those layers then
+        holds the new gradient only after update()."""
         self.hip, self.B = hip, batch
         self.fused_wgrad, self.conv_dgrad, self.fused_head = fused_wgrad, conv_dgrad, fused_head
         self.fused_pool_bwd, self.fused_stats = fused_pool_bwd, fused_stats
         self.store_bn_outputs = store_bn_outputs
+        self.defer_wgrad_sum = defer_wgrad_sum and fused_wgrad
         self._out_stored = [True] * len(BLOCKS)
         self.lr, self.momentum, self.decay, self.bnm = lr, momentum, decay, bn_momentum
         # Parameters live in two arenas (weights with decay; biases and
@@ -165,6 +171,15 @@ class CifarTrainer:
         colmax = max(c * 9 * (hh * hh) for (c, hh, f) in self.dims)
         t["col"] = DeviceArray(B * colmax)
         self.t = t
+        # split sums of the deferred weight gradients: [pieces][F][C*9] each
+        self.pieces = [None] * len(self.dims)
+        if self.defer_wgrad_sum:
+            for i, (c, hh, f) in enumerate(self.dims):
+                if i == 0 or f * c * 9 < 8192:
+                    continue  # conv1: 864 weights, summed a wave per weight by tnh_conv2d_wgrad
+                n = hip.convWeightGradientPieces(B, c, hh, hh, f, 3, 3, 1, 1, 1, 1, 1, 1, t[f"pool{i - 1}"],
+                                                 c * hh * hh, t[f"delta{i}"], f * hh * hh)
+                self.pieces[i] = (DeviceArray(n * f * c * 9), n)
         self._pack()
 
     def _pack_layers(self):
@@ -297,7 +312,11 @@ class CifarTrainer:
             # conv weight gradient: sum_b delta_b * im2col(input_b)^T
             src = self.input if i == 0 else t[f"pool{i - 1}"]
             K, L = c * 9, hh * hh
-            if self.fused_wgrad:
+            if self.pieces[i] is not None:
+                buf, _ = self.pieces[i]
+                hip.convWeightGradientPieces(B, c, hh, hh, f, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, d, f * L, buf,
+                                             buf.numel())
+            elif self.fused_wgrad:
                 hip.convWeightGradient(B, c, hh, hh, f, 3, 3, 1, 1, 1, 1, 1, 1, src, c * hh * hh, d, f * L, 1.0, 1.0,
                                        p[f"u_w{i}"])
             else:
@@ -334,7 +353,8 @@ class CifarTrainer:
         # the update's pass also writes the conv weights' tap-major (and
         # flipped) copies the next forward and backward read, and updates the
         # biases and scales
-        hip.sgdUpdatePack(w.numel(), lr, B, m, dec, w, uw, self._pack_layers(), q.numel(), q, uq)
+        hip.sgdUpdatePack(w.numel(), lr, B, m, dec, w, uw, self._pack_layers(), q.numel(), q, uq,
+                          pieces=self.pieces if self.defer_wgrad_sum else None)
 
     def step(self, x, truth):
         self.forward(x, truth)

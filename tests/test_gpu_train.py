@@ -237,7 +237,7 @@ def test_cifar_train_step(hip, B):
     ref.backward()
     # the activation outputs are stored so they can be compared (the default
     # forms them again in the backward: the same bits, checked separately)
-    gpu = trainnet.CifarTrainer(hip, params, B, store_bn_outputs=True)
+    gpu = trainnet.CifarTrainer(hip, params, B, store_bn_outputs=True, defer_wgrad_sum=False)
     dx, dt = D(x), D(truth)
     gpu.forward(dx, dt)
     gpu.backward()
@@ -1008,10 +1008,78 @@ def test_cifar_step_fused_head_matches_the_calls(hip):
     x, truth = _batch(322, 32)
     out = []
     for fused in (True, False):
-        gpu = trainnet.CifarTrainer(hip, params, 32, fused_head=fused)
+        gpu = trainnet.CifarTrainer(hip, params, 32, fused_head=fused, defer_wgrad_sum=False)
         gpu.forward(D(x), D(truth))
         gpu.backward()
         out.append((float(gpu.cost()), {k: gpu.host(k).copy() for k in ("u_fw", "u_fb", "u_w2", "u_s2", "u_w0")}))
     assert abs(out[0][0] - out[1][0]) <= TOL * abs(out[1][0])
     for k in out[0][1]:
         assert R.rel_err(out[0][1][k], out[1][1][k]) <= TOL, k
+
+
+def test_cifar_step_deferred_wgrad_sum_equals_the_calls(hip):
+    """Weight gradients kept as split sums (tnh_conv2d_wgrad_pieces) and added
+    by the update's pass (tnh_sgd_update_pack_pieces) against
+    tnh_conv2d_wgrad's own reduction: every weight, momentum buffer and the
+    packed copies equal bit for bit after two steps."""
+    case("cifar step deferred wgrad sums vs tnh_conv2d_wgrad")
+    params = trainnet.init_params()
+    x, truth = _batch(360, 64)
+    keys = ("w0", "w1", "w2", "u_w0", "u_w1", "u_w2", "s1", "u_s2", "fw", "u_fw")
+    out = []
+    for defer in (True, False):
+        gpu = trainnet.CifarTrainer(hip, params, 64, defer_wgrad_sum=defer)
+        if defer:
+            assert gpu.pieces[0] is None and gpu.pieces[1] is not None and gpu.pieces[2] is not None
+        dx, dt = D(x), D(truth)
+        for _ in range(2):
+            gpu.step(dx, dt)
+        hip.finish()
+        got = {k: gpu.host(k).copy() for k in keys}
+        got["packed2"] = gpu.packed[2].numpy()
+        got["flipped1"] = gpu.flipped[1].numpy()
+        out.append(got)
+    for k in out[0]:
+        assert np.array_equal(out[0][k], out[1][k]), k
+
+
+@pytest.mark.parametrize("B,C,H,F", [(4, 32, 16, 64), (1, 64, 8, 128), (2, 16, 32, 24)])
+def test_wgrad_pieces_through_the_update_equal_wgrad(hip, B, C, H, F):
+    """tnh_conv2d_wgrad_pieces + tnh_sgd_update_pack_pieces against
+    tnh_conv2d_wgrad (alpha = beta = 1) + tnh_sgd_update_pack on the same
+    data: updated weights, momentum buffer and tap-major copy equal bit for
+    bit (a single piece included: batch 1, 8x8); gradients of fewer than 8192
+    weights in several pieces are refused."""
+    case(f"wgrad pieces B{B} C{C} H{H} F{F}")
+    from tensorium_amd.nnhip import DeviceArray
+
+    K = C * 9
+    x = synth.uniform(370, (B, C, H, H), -1, 1)
+    d = synth.normal(371, (B, F, H, H), 1.0)
+    w0 = synth.normal(372, (F * K,), 0.05)
+    u0 = synth.normal(373, (F * K,), 0.01)
+    dx, dd = DeviceArray.from_numpy(x), DeviceArray.from_numpy(d)
+    if F * K < 8192:  # 16 pieces here: refused, the query included
+        with pytest.raises(TNHError, match="wave"):
+            hip.convWeightGradientPieces(B, C, H, H, F, 3, 3, 1, 1, 1, 1, 1, 1, dx, C * H * H, dd, F * H * H)
+        return
+    res = []
+    for deferred in (True, False):
+        w, u = DeviceArray.from_numpy(w0), DeviceArray.from_numpy(u0)
+        tap = DeviceArray(F * K)
+        layer = [(0, F, C, 9, tap, None)]
+        if deferred:
+            n = hip.convWeightGradientPieces(B, C, H, H, F, 3, 3, 1, 1, 1, 1, 1, 1, dx, C * H * H, dd, F * H * H)
+            pieces = DeviceArray(n * F * K)
+            with pytest.raises(TNHError, match="fewer than"):
+                hip.convWeightGradientPieces(B, C, H, H, F, 3, 3, 1, 1, 1, 1, 1, 1, dx, C * H * H, dd, F * H * H,
+                                             pieces, n * F * K - 1)
+            assert hip.convWeightGradientPieces(B, C, H, H, F, 3, 3, 1, 1, 1, 1, 1, 1, dx, C * H * H, dd,
+                                                F * H * H, pieces, n * F * K) == n
+            hip.sgdUpdatePack(F * K, 1e-3, B, 0.9, 1e-4, w, u, layer, pieces=[(pieces, n)])
+        else:
+            hip.convWeightGradient(B, C, H, H, F, 3, 3, 1, 1, 1, 1, 1, 1, dx, C * H * H, dd, F * H * H, 1.0, 1.0, u)
+            hip.sgdUpdatePack(F * K, 1e-3, B, 0.9, 1e-4, w, u, layer)
+        res.append((w.numpy(), u.numpy(), tap.numpy()))
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
